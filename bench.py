@@ -1,0 +1,199 @@
+"""Benchmark of the MI355X tiled Gaussian-splatting rasterizer (forward + backward).
+
+Headline workload: 1,000,000 Gaussians, SH degree 3,
+1920x1080, forward + L1 loss + backward to the five Gaussian parameter arrays, one
+frame per step, synthetic seeded scene (jax_gs_amd.scenes, seed 2), inputs resident
+in HBM before timing.
+
+Prints ONE JSON line (rank 0, N=1 only: this build runs on a single GPU).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+_ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(_ROOT, "jax-gs_amd"))
+sys.path.insert(0, _ROOT)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+FP32_PEAK_TFLOPS = 157.3  # MI355X FP32 (vector) peak
+COMPOSITE_FWD_FLOP_PER_PAIR = 22  # ~22 FLOP + 1 exp per evaluated pair
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-band", type=int, default=8, help="CPU sample = top 1/band of the image rows")
+    ap.add_argument("--stages", action="store_true", help="print per-stage timings to stderr")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build runs on one GPU only (the multi-GPU path is design-only); "
+                                   "run with --gpus 1"}))
+        sys.exit(2)
+    from jax_gs_amd import _lib, render, scenes
+    from jax_gs_amd.renderer import rasterizer
+    from jax_gs_amd.renderer.projection import preprocess
+    from jax_gs_amd.training.losses import l1_loss
+
+    dev = torch.device("cuda:0")
+    sc = scenes.make_scene(args.config)
+    g, cam, tgt, mask = scenes.to_torch(sc, dev)
+    if tgt is None:
+        tgt = torch.from_numpy(np.random.default_rng(99).uniform(0, 1, (cam.H, cam.W, 3)).astype(np.float32)).to(dev)
+    fields = ("means", "scales", "quaternions", "opacities", "sh_coeffs")
+    for f in fields:
+        getattr(g, f).requires_grad_(True)
+    D = sc["sh_degree"]
+    N = g.means.shape[0]
+
+    def step():
+        for f in fields:
+            getattr(g, f).grad = None
+        image, extras = render(g, cam, mask=mask, sh_degree=D)
+        loss = l1_loss(image, tgt)
+        loss.backward()
+        return extras
+
+    for _ in range(args.warmup):
+        extras = step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        extras = step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    n_int = int(extras["n_interactions"])
+
+    # ---- per-stage timing with HIP events on the launch stream (torch's current stream)
+    st = torch.cuda.current_stream(dev)
+    s_ = _lib.stream_handle(dev)
+    ev = {}
+
+    def mark(name):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record(st)
+        ev.setdefault(name, []).append(e)
+
+    reps = max(3, args.steps)
+    bg = torch.zeros(3, device=dev)
+    W, H = cam.W, cam.H
+    with torch.no_grad():
+        for _ in range(reps):
+            mark("t0")
+            pre = preprocess(g, cam, mask=mask, sh_degree=D)
+            mark("t1")
+            b = rasterizer.bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W,
+                                         want_tiles=False)
+            mark("t2")
+            image, fT, nc = rasterizer.composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg)
+            mark("t3")
+            loss = torch.empty((), device=dev)
+            gimg = torch.empty_like(image)
+            _lib.call("gs_l1_loss", s_, image.numel(), _lib.ptr(image), _lib.ptr(tgt), _lib.ptr(loss), _lib.ptr(gimg))
+            mark("t4")
+            grec = torch.empty((N, _lib.GS_REC_STRIDE), device=dev)
+            _lib.call("gs_composite_bwd", s_, N, _lib.ptr(pre["records"]), _lib.ptr(b["sorted_gids"]),
+                      b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), W, H, _lib.ptr(bg), _lib.ptr(gimg), _lib.ptr(fT), _lib.ptr(nc),
+                      _lib.ptr(grec), None)
+            mark("t5")
+            outs = [torch.empty_like(getattr(g, f)) for f in fields]
+            _lib.call("gs_preprocess_bwd", s_, N, g.sh_coeffs.shape[1], D, *[_lib.ptr(getattr(g, f).detach())
+                                                                             for f in fields],
+                      _lib.ptr(cam.W2C.contiguous()), W, H, float(cam.fx), float(cam.fy), float(cam.cx),
+                      float(cam.cy), _lib.ptr(grec), *[_lib.ptr(o) for o in outs])
+            mark("t6")
+    torch.cuda.synchronize()
+    names = ["preprocess_fwd", "binning", "composite_fwd", "l1_loss", "composite_bwd", "preprocess_bwd"]
+    stage_ms = {}
+    for i, nm in enumerate(names):
+        a, z = ev[f"t{i}"], ev[f"t{i + 1}"]
+        stage_ms[nm] = float(np.median([a[r].elapsed_time(z[r]) for r in range(reps)]))
+    K = g.sh_coeffs.shape[1]
+    nb = (D + 1) ** 2
+    pre_fwd_bytes = N * (44 + 12 * nb) + N * (8 + 16 + 4 + 1 + 4 + 12 + 48)
+    pre_bwd_bytes = N * (44 + 12 * nb) + N * 48 + N * (12 + 12 + 16 + 4 + 12 * K)
+    stage_gbs = {"preprocess_fwd": pre_fwd_bytes / (stage_ms["preprocess_fwd"] * 1e-3) / 1e9,
+                 "preprocess_bwd": pre_bwd_bytes / (stage_ms["preprocess_bwd"] * 1e-3) / 1e9}
+    dominant = max(stage_ms, key=stage_ms.get)
+    if args.stages:
+        print(json.dumps({"stage_ms": stage_ms, "stage_GBps": stage_gbs, "n_interactions": n_int}), file=sys.stderr)
+
+    # Roofline of the dominant kernel.  Compositing is VALU-bound: algorithmic work is
+    # pair evaluations (Σ over pixels of entries visited), ~22 FLOP each forward.
+    roofline = None
+    if dominant in ("preprocess_fwd", "preprocess_bwd"):
+        byt = pre_fwd_bytes if dominant == "preprocess_fwd" else pre_bwd_bytes
+        ach = byt / (stage_ms[dominant] * 1e-3) / 1e9
+        roofline = {"kernel": dominant, "bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": ach / HBM_PEAK_GBS, "traffic": None}
+    else:
+        nc_sum = int(nc.to(torch.int64).sum())
+        flop = nc_sum * COMPOSITE_FWD_FLOP_PER_PAIR
+        ach = flop / (stage_ms["composite_fwd"] * 1e-3) / 1e12
+        roofline = {"kernel": "composite_fwd", "bound": "valu", "achieved": ach, "peak": FP32_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": ach / FP32_PEAK_TFLOPS, "traffic": None,
+                    "pairs": nc_sum}
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(sc, args.cpu_band)
+
+    mpix = cam.W * cam.H / 1e6
+    out = {
+        "metric": "fwd+bwd ms/frame & Mpix/s at 1M Gaussians 1080p SH3; % HBM roofline",
+        "value": mpix / dt,
+        "unit": "Mpix/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dt * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded scene generator, configs[%d])" % args.config,
+        "config": {"workload": sc["name"] + " fwd+L1+bwd", "gaussians": N, "width": cam.W, "height": cam.H,
+                   "sh_degree": D, "n_interactions": n_int, "gaussians_per_s": N / dt},
+        "stage_ms": stage_ms,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+def cpu_baseline(sc, band):
+    """Oracle (C restatement of the reference path, 1 thread) fwd+bwd on a bounded sample:
+    all Gaussians, the top 1/band of the image rows (same camera, H reduced)."""
+    import oracle
+
+    cam = dict(sc["cam"])
+    cam["H"] = max(16, (cam["H"] // band) // 16 * 16)
+    t0 = time.perf_counter()
+    img, ex, res = oracle.render(sc["params"], cam, mask=sc["mask"], sh_degree=sc["sh_degree"])
+    tgt = np.random.default_rng(5).uniform(0, 1, img.shape).astype(np.float32)
+    _, seed = oracle.l1_loss_and_grad(img, tgt)
+    oracle.render_vjp(sc["params"], cam, res, seed, sh_degree=sc["sh_degree"])
+    t = time.perf_counter() - t0
+    px = cam["W"] * cam["H"]
+    return {"value": px / 1e6 / t, "unit": "Mpix/s", "cores": 1, "kind": "port",
+            "sample": f"all {sc['params']['means'].shape[0]} Gaussians, {cam['W']}x{cam['H']} top band of the "
+                      f"frame, fwd+L1+bwd, {t:.1f} s"}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,164 @@
+/*
+ * gs_raster.h -- C ABI of the MI355X (gfx950) tiled Gaussian-splatting rasterizer.
+ *
+ * Every entry point takes plain device pointers, sizes and scalars, launches on the
+ * HIP stream it is given (a hipStream_t passed as void*, NULL = default stream),
+ * performs no host synchronisation and no device allocation, and returns GS_OK or an
+ * error code; gs_last_error() then holds a message for the calling thread.
+ *
+ * Array layouts are the ones the reference's Python functions take and return
+ * (row-major, float32 unless stated):
+ *   means[N,3]  scales[N,3] (log)  quaternions[N,4] (w,x,y,z, unnormalised)
+ *   opacities[N,1] (logit)  sh_coeffs[N,K,3] (coefficient-major, channel-minor)
+ *   w2c[4,4] (device)  background[3] (device)  image[H,W,3]
+ * The reference is ghif/jax-gs (pure JAX; it has no FFI of its own).  Each entry
+ * point below names the reference function whose behaviour it reproduces; a jax.ffi
+ * custom call or the ctypes host module in this repository binds to them.
+ */
+#ifndef GS_RASTER_H
+#define GS_RASTER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GS_OK 0
+#define GS_ERR_INVALID 1  /* bad shape / size / argument */
+#define GS_ERR_HIP 2      /* a HIP runtime call or kernel launch failed */
+
+/* Constants of the reference rasterizer (jax_gs/renderer/rasterizer.py:6-10). */
+#define GS_TILE_SIZE 16
+#define GS_OFFSET_SIZE 16
+#define GS_BLOCK_SIZE 512
+#define GS_MAX_TILE_CHUNKS 8
+#define GS_MAX_TILE_INTERACTIONS 4096
+
+/* Per-Gaussian compositing record: 12 floats
+ *   [0]=mean2d.x [1]=mean2d.y [2]=-0.5*ic00 [3]=-0.5*(2*ic01) [4]=-0.5*ic11
+ *   [5]=sigmoid(opacity) [6..8]=colour rgb [9..11]=0
+ * (ic = inverse of cov2D with det clamped to 1e-6, rasterizer.py:147-156).
+ * The gradient record produced by gs_composite_bwd has the same layout and holds
+ * dL/d(record[0..8]). */
+#define GS_REC_STRIDE 12
+
+/* Layout of the int32 stats[] array filled by gs_bin (renderer.py:63-90 extras). */
+#define GS_STAT_N_INTERACTIONS 0
+#define GS_STAT_MAX_PER_TILE 1
+#define GS_STAT_OVERFLOW_TILES 2
+#define GS_STAT_OVERFLOW_INTERACTIONS 3
+#define GS_STAT_TRUNCATED_TILES 4
+#define GS_STAT_TRUNCATED_INTERACTIONS 5
+#define GS_STAT_RADIUS_CAP_VIOLATIONS 6
+#define GS_STAT_NEGATIVE_DEPTH 7   /* Gaussians whose depth has its sign bit set */
+#define GS_STAT_CAPACITY_EXCEEDED 8 /* 1 when n_interactions > capacity */
+#define GS_NUM_STATS 16
+
+const char* gs_last_error(void);
+int gs_abi_version(void);
+
+/* Projection + covariance + SH colour for every Gaussian.
+ * Replaces jax_gs/renderer/projection.py:6-79 (project_gaussians),
+ * jax_gs/core/gaussians.py:58-92 (get_covariance_3d), jax_gs/renderer/renderer.py:40-49
+ * with jax_gs/renderer/sh.py:25-74 (view directions, eval_sh, +0.5, clip) and the
+ * conic/sigmoid preparation of jax_gs/renderer/rasterizer.py:147-156.
+ * mask may be NULL (all active).  records may be NULL.
+ * Outputs: means2d[N,2] cov2d[N,2,2] radii[N] valid[N] (0/1) depths[N] colors[N,3]
+ * records[N,GS_REC_STRIDE]. */
+int gs_preprocess_fwd(void* stream, int64_t n, int sh_k, int sh_degree,
+                      const float* means, const float* scales, const float* quats,
+                      const float* opacities, const float* sh_coeffs, const uint8_t* mask,
+                      const float* w2c, int width, int height, float fx, float fy, float cx,
+                      float cy, float* means2d, float* cov2d, float* radii, uint8_t* valid,
+                      float* depths, float* colors, float* records);
+
+/* Builds compositing records from projected quantities.
+ * Replaces the prologue of jax_gs/renderer/rasterizer.py:119-156 (render_tiles):
+ * det clamp, inverse covariance, sigmoid(opacity). */
+int gs_composite_prep(void* stream, int64_t n, const float* means2d, const float* cov2d,
+                      const float* opacities, const float* colors, float* records);
+
+/* Workspace bytes gs_bin needs for n Gaussians, a width x height image and an
+ * interaction capacity (capacity <= 0 means the static bound 256*n). */
+size_t gs_bin_workspace_size(int64_t n, int width, int height, int64_t capacity);
+
+/* Tile binning: per-Gaussian tile rectangles, quantised 13-bit depth, stable sort
+ * by (tile, depth bucket, Gaussian id), tile ranges and the renderer's health stats.
+ * Replaces jax_gs/renderer/rasterizer.py:12-116 (get_tile_interactions) and the
+ * searchsorted tile ranges + extras of jax_gs/renderer/renderer.py:57-90.
+ * Outputs cover only the n_interactions valid entries, in the reference's order:
+ *   sorted_gids[capacity]   Gaussian id of entry i
+ *   sorted_tiles[capacity]  tile id of entry i (may be NULL)
+ *   ranges[T+1]             first entry of tile t (searchsorted-left), ranges[T]=n
+ *   stats[GS_NUM_STATS]     see GS_STAT_*
+ * With k Gaussians whose depth has its sign bit set, the reference's arrays carry
+ * 256*k extra entries in front (tile -1), so its boundaries equal ranges + 256*k.
+ * capacity <= 0 selects the static bound 256*n. */
+int gs_bin(void* stream, int64_t n, const float* means2d, const float* radii,
+           const uint8_t* valid, const float* depths, int width, int height,
+           int64_t capacity, void* workspace, size_t workspace_bytes, int32_t* sorted_gids,
+           int32_t* sorted_tiles, int32_t* ranges, int32_t* stats);
+
+/* Tile boundaries of an arbitrary sorted tile-id array (length L, entries in
+ * [-1, T]): ranges[t] = first index with tile >= t for t in 0..T.
+ * Replaces the searchsorted of jax_gs/renderer/renderer.py:57-61 and
+ * jax_gs/renderer/rasterizer.py:159-160 for callers that hold sorted ids. */
+int gs_tile_ranges(void* stream, const int32_t* sorted_tiles, int64_t length, int num_tiles,
+                   int32_t* ranges);
+
+/* Front-to-back compositing of every 16x16 tile.
+ * Replaces jax_gs/renderer/rasterizer.py:157-248 (render_tiles body; its equivalent
+ * jax_gs/renderer/rasterizer_tpu.py:13-135).  sorted_gids has n_entries elements and
+ * ranges[T+1] indexes into it (out-of-range ids clamp to [0, n-1] as XLA's gather
+ * does).  Per pixel it also writes the final
+ * transmittance final_T[H,W] and n_contrib[H,W] = number of leading entries blended
+ * while T > 1e-4 (residuals for gs_composite_bwd; either may be NULL). */
+int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
+                     int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
+                     float* image, float* final_T, int32_t* n_contrib);
+
+/* Vector-Jacobian product of gs_composite_fwd (JAX autodiff of render_tiles).
+ * grad_records[N,GS_REC_STRIDE] is overwritten with dL/d(record); grad_background[3]
+ * (may be NULL) with dL/d(background). */
+int gs_composite_bwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
+                     int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
+                     const float* grad_image, const float* final_T, const int32_t* n_contrib,
+                     float* grad_records, float* grad_background);
+
+/* Vector-Jacobian product of gs_preprocess_fwd's compositing records with respect to
+ * the five Gaussian parameter arrays (JAX autodiff of project_gaussians, eval_sh,
+ * get_covariance_3d and the conic/sigmoid prologue).  Outputs are overwritten:
+ * grad_means[N,3] grad_scales[N,3] grad_quats[N,4] grad_opacities[N,1]
+ * grad_sh[N,K,3] (coefficients >= (sh_degree+1)^2 get 0). */
+int gs_preprocess_bwd(void* stream, int64_t n, int sh_k, int sh_degree, const float* means,
+                      const float* scales, const float* quats, const float* opacities,
+                      const float* sh_coeffs, const float* w2c, int width, int height,
+                      float fx, float fy, float cx, float cy, const float* grad_records,
+                      float* grad_means, float* grad_scales, float* grad_quats,
+                      float* grad_opacities, float* grad_sh);
+
+/* mean(|pred - target|) into loss[0] and, when grad is not NULL, its gradient
+ * sign(pred - target) / count.  Replaces jax_gs/training/losses.py:4-8 (l1_loss)
+ * and its autodiff seed. */
+int gs_l1_loss(void* stream, int64_t count, const float* pred, const float* target,
+               float* loss, float* grad);
+
+/* Densification statistics of one training step, updated in place.
+ * Replaces jax_gs/training/trainer.py:278-294 (train_step, after value_and_grad):
+ *   grad_accum += (|grad_means| * (max(z_cam,0.01) / focal)) * pixel_scale
+ *   denom      += valid & active
+ *   max_radii   = valid ? max(max_radii, radii) : max_radii
+ * focal = float32((fx+fy)/2) and pixel_scale = float32(W*H*3), both formed in double
+ * precision by the caller exactly as the reference's Python does.
+ * active may be NULL (all active). */
+int gs_densify_accumulate(void* stream, int64_t n, const float* grad_means, const float* means,
+                          const float* w2c, float focal, float pixel_scale,
+                          const uint8_t* valid, const uint8_t* active, const float* radii,
+                          float* grad_accum, int32_t* denom, float* max_radii);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GS_RASTER_H */

@@ -1,0 +1,541 @@
+// Per-Gaussian preprocessing on gfx950: EWA projection, 3D/2D covariance, radius,
+// SH colour and compositing records (forward), and their vector-Jacobian product
+// (backward).  One thread per Gaussian; every input row is read once and every
+// output row written once, so both kernels are HBM-bound.
+//
+// Forward semantics follow, operation by operation and in float32:
+//   jax_gs/renderer/projection.py:26-77 (project_gaussians)
+//   jax_gs/core/gaussians.py:70-91     (get_covariance_3d)
+//   jax_gs/core/camera.py:15-21        (Camera.center)
+//   jax_gs/renderer/renderer.py:40-49 + jax_gs/renderer/sh.py:25-72 (colour)
+//   jax_gs/renderer/rasterizer.py:147-156 + 198 (conic, sigmoid, 2*ic01)
+// The backward is the reverse-mode derivative of that forward with JAX's
+// conventions: ties of maximum/minimum/clip split the cotangent 0.5/0.5, the
+// radius (ceil) and all masks carry no gradient, and cov2D[1,0] is unused.
+#include "gs_common.h"
+
+namespace gs {
+namespace {
+
+struct CamRows {
+  float w[16];
+};
+
+__device__ inline void load_w2c(const float* __restrict__ w2c, float* w) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k) w[k] = w2c[k];
+}
+
+// Quantities of the forward pass that the backward needs again.
+struct Proj {
+  float x, y, z;            // camera-space mean
+  float qn[4], qnorm;       // normalised quaternion (r,x,y,z) and |q|
+  float R[3][3], s[3];      // rotation, exp(scales)
+  float Mm[3][3];           // R * diag(s)
+  float Sig[3][3];          // Mm Mm^T
+  float zs, iz, iz2;        // max(z,.01), 1/zs, iz^2
+  float M2[2][3];           // J @ W_rot
+  float T1[2][3];           // M2 @ Sig
+  float c00, c01, c10, c11; // cov2D
+};
+
+__device__ inline void project(const float* w, float mx, float my, float mz, const float* q,
+                               const float* ls, float fx, float fy, Proj& p) {
+  // projection.py:26-29 -- [m,1] @ W2C^T, k ascending.
+  p.x = ((mx * w[0] + my * w[1]) + mz * w[2]) + w[3];
+  p.y = ((mx * w[4] + my * w[5]) + mz * w[6]) + w[7];
+  p.z = ((mx * w[8] + my * w[9]) + mz * w[10]) + w[11];
+  // gaussians.py:70-91
+  p.qnorm = sqrtf(((q[0] * q[0] + q[1] * q[1]) + q[2] * q[2]) + q[3] * q[3]);
+  const float r = q[0] / p.qnorm, x = q[1] / p.qnorm, y = q[2] / p.qnorm, z = q[3] / p.qnorm;
+  p.qn[0] = r; p.qn[1] = x; p.qn[2] = y; p.qn[3] = z;
+  p.R[0][0] = (1.0f - 2.0f * (y * y)) - 2.0f * (z * z);
+  p.R[0][1] = (2.0f * x) * y - (2.0f * r) * z;
+  p.R[0][2] = (2.0f * x) * z + (2.0f * r) * y;
+  p.R[1][0] = (2.0f * x) * y + (2.0f * r) * z;
+  p.R[1][1] = (1.0f - 2.0f * (x * x)) - 2.0f * (z * z);
+  p.R[1][2] = (2.0f * y) * z - (2.0f * r) * x;
+  p.R[2][0] = (2.0f * x) * z - (2.0f * r) * y;
+  p.R[2][1] = (2.0f * y) * z + (2.0f * r) * x;
+  p.R[2][2] = (1.0f - 2.0f * (x * x)) - 2.0f * (y * y);
+#pragma unroll
+  for (int j = 0; j < 3; ++j) p.s[j] = det_expf(ls[j]);
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) p.Mm[i][j] = p.R[i][j] * p.s[j];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      p.Sig[i][j] = (p.Mm[i][0] * p.Mm[j][0] + p.Mm[i][1] * p.Mm[j][1]) + p.Mm[i][2] * p.Mm[j][2];
+  // projection.py:43-62
+  p.zs = jmax(p.z, 0.01f);
+  p.iz = 1.0f / p.zs;
+  p.iz2 = p.iz * p.iz;
+  const float J[2][3] = {{fx * p.iz, 0.0f, ((-fx) * p.x) * p.iz2},
+                         {0.0f, fy * p.iz, ((-fy) * p.y) * p.iz2}};
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      p.M2[i][j] = (J[i][0] * w[0 * 4 + j] + J[i][1] * w[1 * 4 + j]) + J[i][2] * w[2 * 4 + j];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      p.T1[i][j] = (p.M2[i][0] * p.Sig[0][j] + p.M2[i][1] * p.Sig[1][j]) + p.M2[i][2] * p.Sig[2][j];
+  float c[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      c[i][j] = (p.T1[i][0] * p.M2[j][0] + p.T1[i][1] * p.M2[j][1]) + p.T1[i][2] * p.M2[j][2];
+  const float lp = 0.3f;  // 0.3 * eye(2)
+  p.c00 = c[0][0] + lp;
+  p.c01 = c[0][1] + 0.0f;
+  p.c10 = c[1][0] + 0.0f;
+  p.c11 = c[1][1] + lp;
+}
+
+// renderer.py:40-41 with camera.py:15-21: unit vector from the camera centre.
+__device__ inline void view_dir(const float* w, float mx, float my, float mz, float* v, float& nrm,
+                                float* d) {
+  float cen[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+    cen[i] = ((-w[0 * 4 + i]) * w[3] + (-w[1 * 4 + i]) * w[7]) + (-w[2 * 4 + i]) * w[11];
+  v[0] = mx - cen[0];
+  v[1] = my - cen[1];
+  v[2] = mz - cen[2];
+  nrm = sqrtf((v[0] * v[0] + v[1] * v[1]) + v[2] * v[2]);
+  d[0] = v[0] / nrm;
+  d[1] = v[1] / nrm;
+  d[2] = v[2] / nrm;
+}
+
+// sh.py:25-72 for one channel; sh points at coefficient 0 of that channel with a
+// stride of 3 floats between coefficients.
+__device__ inline float eval_sh_channel(int deg, const float* __restrict__ sh, const float* d) {
+  float res = SH_C0 * sh[0];
+  if (deg > 0) {
+    const float x = d[0], y = d[1], z = d[2];
+    res = ((res - (SH_C1 * y) * sh[3]) + (SH_C1 * z) * sh[6]) - (SH_C1 * x) * sh[9];
+    if (deg > 1) {
+      const float xx = x * x, yy = y * y, zz = z * z;
+      const float xy = x * y, yz = y * z, xz = x * z;
+      res = ((((res + (SH_C2_0 * xy) * sh[12]) + (SH_C2_1 * yz) * sh[15]) +
+              (SH_C2_2 * ((2.0f * zz - xx) - yy)) * sh[18]) +
+             (SH_C2_3 * xz) * sh[21]) +
+            (SH_C2_4 * (xx - yy)) * sh[24];
+      if (deg > 2) {
+        res = ((((((res + ((SH_C3_0 * y) * (3.0f * xx - yy)) * sh[27]) +
+                   ((SH_C3_1 * xy) * z) * sh[30]) +
+                  ((SH_C3_2 * y) * ((4.0f * zz - xx) - yy)) * sh[33]) +
+                 ((SH_C3_3 * z) * ((2.0f * zz - 3.0f * xx) - 3.0f * yy)) * sh[36]) +
+                ((SH_C3_4 * x) * ((4.0f * zz - xx) - yy)) * sh[39]) +
+               ((SH_C3_5 * z) * (xx - yy)) * sh[42]) +
+              ((SH_C3_6 * x) * (xx - 3.0f * yy)) * sh[45];
+      }
+    }
+  }
+  return res;
+}
+
+// rasterizer.py:147-156 and :198 -- record = (mean, -0.5*conic terms, sigmoid, colour).
+__device__ inline void write_record(float* __restrict__ rec, float m2x, float m2y, float c00,
+                                    float c01, float c11, float logit, const float* col) {
+  const float det = jmax(c00 * c11 - c01 * c01, 1e-6f);
+  const float ic00 = c11 / det;
+  const float ic01 = (-c01) / det;
+  const float ic11 = c00 / det;
+  float4* r4 = reinterpret_cast<float4*>(rec);
+  r4[0] = make_float4(m2x, m2y, -0.5f * ic00, -0.5f * (2.0f * ic01));
+  r4[1] = make_float4(-0.5f * ic11, det_sigmoidf(logit), col[0], col[1]);
+  r4[2] = make_float4(col[2], 0.0f, 0.0f, 0.0f);
+}
+
+__global__ __launch_bounds__(256) void preprocess_fwd_kernel(
+    int64_t n, int K, int deg, const float* __restrict__ means, const float* __restrict__ scales,
+    const float* __restrict__ quats, const float* __restrict__ opac, const float* __restrict__ sh,
+    const uint8_t* __restrict__ mask, const float* __restrict__ w2c, float fx, float fy, float cx,
+    float cy, float* __restrict__ means2d, float* __restrict__ cov2d, float* __restrict__ radii,
+    uint8_t* __restrict__ valid, float* __restrict__ depths, float* __restrict__ colors,
+    float* __restrict__ records) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float w[16];
+  load_w2c(w2c, w);
+  const float mx = means[3 * i], my = means[3 * i + 1], mz = means[3 * i + 2];
+  float q[4], ls[3];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) q[k] = quats[4 * i + k];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) ls[k] = scales[3 * i + k];
+  Proj p;
+  project(w, mx, my, mz, q, ls, fx, fy, p);
+  const bool v = (p.z > 0.01f) && (mask == nullptr || mask[i] != 0);
+  // projection.py:65-68 -- raw z here.
+  const float m2x = (fx * p.x) / p.z + cx;
+  const float m2y = (fy * p.y) / p.z + cy;
+  // projection.py:71-77
+  const float det = p.c00 * p.c11 - p.c01 * p.c01;
+  const float mid = (p.c00 + p.c11) / 2.0f;
+  const float term = sqrtf(jmax(mid * mid - det, 0.0f));
+  const float radius = ceilf(3.0f * sqrtf(mid + term));
+  // renderer.py:40-49
+  float vv[3], nrm, d[3];
+  view_dir(w, mx, my, mz, vv, nrm, d);
+  float col[3];
+  const float* shi = sh + (int64_t)i * K * 3;
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const float res = eval_sh_channel(deg, shi + c, d) + 0.5f;
+    col[c] = jmin(1.0f, jmax(0.0f, res));
+  }
+  means2d[2 * i] = m2x;
+  means2d[2 * i + 1] = m2y;
+  reinterpret_cast<float4*>(cov2d)[i] = make_float4(p.c00, p.c01, p.c10, p.c11);
+  radii[i] = radius;
+  valid[i] = v ? 1 : 0;
+  depths[i] = p.z;
+  colors[3 * i] = col[0];
+  colors[3 * i + 1] = col[1];
+  colors[3 * i + 2] = col[2];
+  if (records != nullptr) write_record(records + i * kRec, m2x, m2y, p.c00, p.c01, p.c11, opac[i], col);
+}
+
+__global__ __launch_bounds__(256) void composite_prep_kernel(int64_t n, const float* __restrict__ means2d,
+                                                             const float* __restrict__ cov2d,
+                                                             const float* __restrict__ opac,
+                                                             const float* __restrict__ colors,
+                                                             float* __restrict__ records) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float4 c = reinterpret_cast<const float4*>(cov2d)[i];
+  const float col[3] = {colors[3 * i], colors[3 * i + 1], colors[3 * i + 2]};
+  write_record(records + i * kRec, means2d[2 * i], means2d[2 * i + 1], c.x, c.y, c.w, opac[i], col);
+}
+
+// d basis_k / d(x,y,z) of the degree<=3 real SH basis used by eval_sh_channel.
+__device__ inline void sh_basis_and_grad(int deg, const float* d, float* B, float (*dB)[3]) {
+  const float x = d[0], y = d[1], z = d[2];
+  const float xx = x * x, yy = y * y, zz = z * z;
+  for (int k = 0; k < 16; ++k) {
+    B[k] = 0.0f;
+    dB[k][0] = dB[k][1] = dB[k][2] = 0.0f;
+  }
+  B[0] = SH_C0;
+  if (deg > 0) {
+    B[1] = -SH_C1 * y; dB[1][1] = -SH_C1;
+    B[2] = SH_C1 * z;  dB[2][2] = SH_C1;
+    B[3] = -SH_C1 * x; dB[3][0] = -SH_C1;
+  }
+  if (deg > 1) {
+    B[4] = SH_C2_0 * x * y; dB[4][0] = SH_C2_0 * y; dB[4][1] = SH_C2_0 * x;
+    B[5] = SH_C2_1 * y * z; dB[5][1] = SH_C2_1 * z; dB[5][2] = SH_C2_1 * y;
+    B[6] = SH_C2_2 * (2.0f * zz - xx - yy);
+    dB[6][0] = SH_C2_2 * (-2.0f * x); dB[6][1] = SH_C2_2 * (-2.0f * y); dB[6][2] = SH_C2_2 * (4.0f * z);
+    B[7] = SH_C2_3 * x * z; dB[7][0] = SH_C2_3 * z; dB[7][2] = SH_C2_3 * x;
+    B[8] = SH_C2_4 * (xx - yy); dB[8][0] = SH_C2_4 * (2.0f * x); dB[8][1] = SH_C2_4 * (-2.0f * y);
+  }
+  if (deg > 2) {
+    B[9] = SH_C3_0 * y * (3.0f * xx - yy);
+    dB[9][0] = SH_C3_0 * (6.0f * x * y); dB[9][1] = SH_C3_0 * (3.0f * xx - 3.0f * yy);
+    B[10] = SH_C3_1 * x * y * z;
+    dB[10][0] = SH_C3_1 * y * z; dB[10][1] = SH_C3_1 * x * z; dB[10][2] = SH_C3_1 * x * y;
+    B[11] = SH_C3_2 * y * (4.0f * zz - xx - yy);
+    dB[11][0] = SH_C3_2 * (-2.0f * x * y); dB[11][1] = SH_C3_2 * (4.0f * zz - xx - 3.0f * yy);
+    dB[11][2] = SH_C3_2 * (8.0f * y * z);
+    B[12] = SH_C3_3 * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
+    dB[12][0] = SH_C3_3 * (-6.0f * x * z); dB[12][1] = SH_C3_3 * (-6.0f * y * z);
+    dB[12][2] = SH_C3_3 * (6.0f * zz - 3.0f * xx - 3.0f * yy);
+    B[13] = SH_C3_4 * x * (4.0f * zz - xx - yy);
+    dB[13][0] = SH_C3_4 * (4.0f * zz - 3.0f * xx - yy); dB[13][1] = SH_C3_4 * (-2.0f * x * y);
+    dB[13][2] = SH_C3_4 * (8.0f * x * z);
+    B[14] = SH_C3_5 * z * (xx - yy);
+    dB[14][0] = SH_C3_5 * (2.0f * x * z); dB[14][1] = SH_C3_5 * (-2.0f * y * z); dB[14][2] = SH_C3_5 * (xx - yy);
+    B[15] = SH_C3_6 * x * (xx - 3.0f * yy);
+    dB[15][0] = SH_C3_6 * (3.0f * xx - 3.0f * yy); dB[15][1] = SH_C3_6 * (-6.0f * x * y);
+  }
+}
+
+__global__ __launch_bounds__(256) void preprocess_bwd_kernel(
+    int64_t n, int K, int deg, const float* __restrict__ means, const float* __restrict__ scales,
+    const float* __restrict__ quats, const float* __restrict__ opac, const float* __restrict__ sh,
+    const float* __restrict__ w2c, float fx, float fy, const float* __restrict__ grec,
+    float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_quats,
+    float* __restrict__ g_opac, float* __restrict__ g_sh) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float w[16];
+  load_w2c(w2c, w);
+  const float mx = means[3 * i], my = means[3 * i + 1], mz = means[3 * i + 2];
+  float q[4], ls[3];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) q[k] = quats[4 * i + k];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) ls[k] = scales[3 * i + k];
+  Proj p;
+  project(w, mx, my, mz, q, ls, fx, fy, p);
+
+  const float4 ga = reinterpret_cast<const float4*>(grec + i * kRec)[0];
+  const float4 gb = reinterpret_cast<const float4*>(grec + i * kRec)[1];
+  const float4 gc = reinterpret_cast<const float4*>(grec + i * kRec)[2];
+  const float g_m2x = ga.x, g_m2y = ga.y;
+  // record[2..4] = -0.5*ic00, -0.5*(2*ic01) = -ic01, -0.5*ic11
+  const float g_ic00 = -0.5f * ga.z;
+  const float g_ic01 = -ga.w;
+  const float g_ic11 = -0.5f * gb.x;
+  const float g_sig = gb.y;
+  const float g_col[3] = {gb.z, gb.w, gc.x};
+
+  // ---- opacity: sigmoid
+  const float sg = det_sigmoidf(opac[i]);
+  g_opac[i] = g_sig * sg * (1.0f - sg);
+
+  // ---- conic <- cov2D (rasterizer.py:147-153)
+  const float det_raw = p.c00 * p.c11 - p.c01 * p.c01;
+  const float det = jmax(det_raw, 1e-6f);
+  const float ic00 = p.c11 / det, ic01 = (-p.c01) / det, ic11 = p.c00 / det;
+  float g_c00 = g_ic11 / det;
+  float g_c11 = g_ic00 / det;
+  float g_c01 = -g_ic01 / det;
+  const float g_det = -((g_ic00 * ic00 + g_ic01 * ic01) + g_ic11 * ic11) / det * dmax_first(det_raw, 1e-6f);
+  g_c00 += g_det * p.c11;
+  g_c11 += g_det * p.c00;
+  g_c01 += -2.0f * p.c01 * g_det;
+  const float G[2][2] = {{g_c00, g_c01}, {0.0f, g_c11}};
+
+  // ---- cov2D = (M2 Sig) M2^T + 0.3 I
+  float g_T1[2][3], g_M2[2][3], g_Sig[3][3];
+#pragma unroll
+  for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      g_T1[i2][j] = G[i2][0] * p.M2[0][j] + G[i2][1] * p.M2[1][j];
+      g_M2[i2][j] = G[0][i2] * p.T1[0][j] + G[1][i2] * p.T1[1][j];
+    }
+#pragma unroll
+  for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      g_M2[i2][j] += (g_T1[i2][0] * p.Sig[j][0] + g_T1[i2][1] * p.Sig[j][1]) + g_T1[i2][2] * p.Sig[j][2];
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) g_Sig[k][j] = p.M2[0][k] * g_T1[0][j] + p.M2[1][k] * g_T1[1][j];
+
+  // ---- M2 = J W_rot
+  float g_J[2][3];
+#pragma unroll
+  for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      g_J[i2][k] = (g_M2[i2][0] * w[k * 4 + 0] + g_M2[i2][1] * w[k * 4 + 1]) + g_M2[i2][2] * w[k * 4 + 2];
+  float g_x = 0.0f, g_y = 0.0f, g_z = 0.0f;
+  float g_iz = fx * g_J[0][0] + fy * g_J[1][1];
+  const float g_iz2 = ((-fx) * p.x) * g_J[0][2] + ((-fy) * p.y) * g_J[1][2];
+  g_x += (-fx) * p.iz2 * g_J[0][2];
+  g_y += (-fy) * p.iz2 * g_J[1][2];
+  g_iz += 2.0f * p.iz * g_iz2;
+  const float g_zs = -g_iz * p.iz * p.iz;
+  g_z += g_zs * dmax_first(p.z, 0.01f);
+  // ---- means2D = f*x/z + c (raw z)
+  g_x += g_m2x * fx / p.z;
+  g_y += g_m2y * fy / p.z;
+  g_z += -(g_m2x * (fx * p.x) + g_m2y * (fy * p.y)) / (p.z * p.z);
+  // ---- camera-space mean <- world mean
+  float g_m[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) g_m[k] = (w[0 * 4 + k] * g_x + w[1 * 4 + k] * g_y) + w[2 * 4 + k] * g_z;
+
+  // ---- colour: clip(SH + 0.5, 0, 1)
+  float vv[3], nrm, d[3];
+  view_dir(w, mx, my, mz, vv, nrm, d);
+  const float* shi = sh + (int64_t)i * K * 3;
+  float g_pre[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const float pre = eval_sh_channel(deg, shi + c, d) + 0.5f;
+    const float lo = jmax(0.0f, pre);
+    g_pre[c] = g_col[c] * dmin_first(lo, 1.0f) * dmax_first(pre, 0.0f);
+  }
+  float B[16], dB[16][3];
+  sh_basis_and_grad(deg, d, B, dB);
+  const int nb = (deg + 1) * (deg + 1);
+  float g_d[3] = {0.0f, 0.0f, 0.0f};
+  float* gsh = g_sh + (int64_t)i * K * 3;
+  for (int k = 0; k < K; ++k) {
+    if (k < nb) {
+      const float s0 = shi[3 * k], s1 = shi[3 * k + 1], s2 = shi[3 * k + 2];
+      gsh[3 * k] = B[k] * g_pre[0];
+      gsh[3 * k + 1] = B[k] * g_pre[1];
+      gsh[3 * k + 2] = B[k] * g_pre[2];
+      const float sk = (s0 * g_pre[0] + s1 * g_pre[1]) + s2 * g_pre[2];
+      g_d[0] += sk * dB[k][0];
+      g_d[1] += sk * dB[k][1];
+      g_d[2] += sk * dB[k][2];
+    } else {
+      gsh[3 * k] = 0.0f;
+      gsh[3 * k + 1] = 0.0f;
+      gsh[3 * k + 2] = 0.0f;
+    }
+  }
+  if (deg > 0) {
+    const float dg = (d[0] * g_d[0] + d[1] * g_d[1]) + d[2] * g_d[2];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) g_m[k] += (g_d[k] - d[k] * dg) / nrm;
+  }
+  g_means[3 * i] = g_m[0];
+  g_means[3 * i + 1] = g_m[1];
+  g_means[3 * i + 2] = g_m[2];
+
+  // ---- Sig = Mm Mm^T, Mm = R diag(s), s = exp(ls)
+  float g_Mm[3][3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a)
+#pragma unroll
+    for (int b = 0; b < 3; ++b) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) acc += (g_Sig[a][k] + g_Sig[k][a]) * p.Mm[k][b];
+      g_Mm[a][b] = acc;
+    }
+  float g_R[3][3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    float gs = 0.0f;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      g_R[a][j] = g_Mm[a][j] * p.s[j];
+      gs += g_Mm[a][j] * p.R[a][j];
+    }
+    g_scales[3 * i + j] = gs * p.s[j];
+  }
+  // ---- R(qn)
+  const float r = p.qn[0], x = p.qn[1], y = p.qn[2], z = p.qn[3];
+  float gr = 0.0f, gx = 0.0f, gy = 0.0f, gz = 0.0f;
+  gy += -4.0f * y * g_R[0][0]; gz += -4.0f * z * g_R[0][0];
+  gx += 2.0f * y * g_R[0][1]; gy += 2.0f * x * g_R[0][1]; gr += -2.0f * z * g_R[0][1]; gz += -2.0f * r * g_R[0][1];
+  gx += 2.0f * z * g_R[0][2]; gz += 2.0f * x * g_R[0][2]; gr += 2.0f * y * g_R[0][2]; gy += 2.0f * r * g_R[0][2];
+  gx += 2.0f * y * g_R[1][0]; gy += 2.0f * x * g_R[1][0]; gr += 2.0f * z * g_R[1][0]; gz += 2.0f * r * g_R[1][0];
+  gx += -4.0f * x * g_R[1][1]; gz += -4.0f * z * g_R[1][1];
+  gy += 2.0f * z * g_R[1][2]; gz += 2.0f * y * g_R[1][2]; gr += -2.0f * x * g_R[1][2]; gx += -2.0f * r * g_R[1][2];
+  gx += 2.0f * z * g_R[2][0]; gz += 2.0f * x * g_R[2][0]; gr += -2.0f * y * g_R[2][0]; gy += -2.0f * r * g_R[2][0];
+  gy += 2.0f * z * g_R[2][1]; gz += 2.0f * y * g_R[2][1]; gr += 2.0f * x * g_R[2][1]; gx += 2.0f * r * g_R[2][1];
+  gx += -4.0f * x * g_R[2][2]; gy += -4.0f * y * g_R[2][2];
+  // ---- qn = q / |q|
+  const float gq[4] = {gr, gx, gy, gz};
+  const float qd = ((p.qn[0] * gq[0] + p.qn[1] * gq[1]) + p.qn[2] * gq[2]) + p.qn[3] * gq[3];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) g_quats[4 * i + k] = (gq[k] - p.qn[k] * qd) / p.qnorm;
+}
+
+__global__ __launch_bounds__(256) void densify_kernel(int64_t n, const float* __restrict__ g_means,
+                                                      const float* __restrict__ means,
+                                                      const float* __restrict__ w2c, float focal,
+                                                      float pixel_scale, const uint8_t* __restrict__ valid,
+                                                      const uint8_t* __restrict__ active,
+                                                      const float* __restrict__ radii,
+                                                      float* __restrict__ grad_accum,
+                                                      int32_t* __restrict__ denom,
+                                                      float* __restrict__ max_radii) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  // trainer.py:280-282
+  const float mx = means[3 * i], my = means[3 * i + 1], mz = means[3 * i + 2];
+  const float zc = ((mx * w2c[8] + my * w2c[9]) + mz * w2c[10]) + w2c[11];
+  const float z = jmax(zc, 0.01f);
+  // trainer.py:285
+  const float gx = g_means[3 * i], gy = g_means[3 * i + 1], gz = g_means[3 * i + 2];
+  const float gn = sqrtf((gx * gx + gy * gy) + gz * gz);
+  grad_accum[i] = grad_accum[i] + (gn * (z / focal)) * pixel_scale;
+  // trainer.py:288-294
+  const bool v = valid[i] != 0;
+  const bool act = (active == nullptr) || active[i] != 0;
+  denom[i] = denom[i] + ((v && act) ? 1 : 0);
+  if (v) max_radii[i] = jmax(max_radii[i], radii[i]);
+}
+
+}  // namespace
+}  // namespace gs
+
+using namespace gs;
+
+extern "C" int gs_preprocess_fwd(void* stream, int64_t n, int sh_k, int sh_degree, const float* means,
+                                 const float* scales, const float* quats, const float* opacities,
+                                 const float* sh_coeffs, const uint8_t* mask, const float* w2c,
+                                 int width, int height, float fx, float fy, float cx, float cy,
+                                 float* means2d, float* cov2d, float* radii, uint8_t* valid,
+                                 float* depths, float* colors, float* records) {
+  GS_REQUIRE(n >= 0, "gs_preprocess_fwd: n must be >= 0 (got %lld)", (long long)n);
+  GS_REQUIRE(sh_degree >= 0 && sh_degree <= 3, "gs_preprocess_fwd: sh_degree must be in 0..3 (got %d)", sh_degree);
+  GS_REQUIRE(sh_k >= (sh_degree + 1) * (sh_degree + 1),
+             "gs_preprocess_fwd: sh_coeffs has %d coefficients, degree %d needs %d", sh_k, sh_degree,
+             (sh_degree + 1) * (sh_degree + 1));
+  GS_REQUIRE(width > 0 && height > 0, "gs_preprocess_fwd: bad image size %dx%d", width, height);
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(means && scales && quats && opacities && sh_coeffs && w2c && means2d && cov2d && radii &&
+                 valid && depths && colors,
+             "gs_preprocess_fwd: NULL array argument");
+  (void)width;
+  (void)height;
+  hipLaunchKernelGGL(preprocess_fwd_kernel, dim3(div_up(n, 256)), dim3(256), 0, (hipStream_t)stream, n,
+                     sh_k, sh_degree, means, scales, quats, opacities, sh_coeffs, mask, w2c, fx, fy, cx,
+                     cy, means2d, cov2d, radii, valid, depths, colors, records);
+  GS_LAUNCH_CHECK("preprocess_fwd_kernel");
+  return GS_OK;
+}
+
+extern "C" int gs_composite_prep(void* stream, int64_t n, const float* means2d, const float* cov2d,
+                                 const float* opacities, const float* colors, float* records) {
+  GS_REQUIRE(n >= 0, "gs_composite_prep: n must be >= 0");
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(means2d && cov2d && opacities && colors && records, "gs_composite_prep: NULL array argument");
+  hipLaunchKernelGGL(composite_prep_kernel, dim3(div_up(n, 256)), dim3(256), 0, (hipStream_t)stream, n,
+                     means2d, cov2d, opacities, colors, records);
+  GS_LAUNCH_CHECK("composite_prep_kernel");
+  return GS_OK;
+}
+
+extern "C" int gs_preprocess_bwd(void* stream, int64_t n, int sh_k, int sh_degree, const float* means,
+                                 const float* scales, const float* quats, const float* opacities,
+                                 const float* sh_coeffs, const float* w2c, int width, int height,
+                                 float fx, float fy, float cx, float cy, const float* grad_records,
+                                 float* grad_means, float* grad_scales, float* grad_quats,
+                                 float* grad_opacities, float* grad_sh) {
+  GS_REQUIRE(n >= 0, "gs_preprocess_bwd: n must be >= 0");
+  GS_REQUIRE(sh_degree >= 0 && sh_degree <= 3, "gs_preprocess_bwd: sh_degree must be in 0..3 (got %d)", sh_degree);
+  GS_REQUIRE(sh_k >= (sh_degree + 1) * (sh_degree + 1) && sh_k <= 16,
+             "gs_preprocess_bwd: sh_coeffs has %d coefficients, degree %d needs %d (max 16)", sh_k,
+             sh_degree, (sh_degree + 1) * (sh_degree + 1));
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(means && scales && quats && opacities && sh_coeffs && w2c && grad_records && grad_means &&
+                 grad_scales && grad_quats && grad_opacities && grad_sh,
+             "gs_preprocess_bwd: NULL array argument");
+  (void)width;
+  (void)height;
+  (void)cx;
+  (void)cy;
+  hipLaunchKernelGGL(preprocess_bwd_kernel, dim3(div_up(n, 256)), dim3(256), 0, (hipStream_t)stream, n,
+                     sh_k, sh_degree, means, scales, quats, opacities, sh_coeffs, w2c, fx, fy,
+                     grad_records, grad_means, grad_scales, grad_quats, grad_opacities, grad_sh);
+  GS_LAUNCH_CHECK("preprocess_bwd_kernel");
+  return GS_OK;
+}
+
+extern "C" int gs_densify_accumulate(void* stream, int64_t n, const float* grad_means, const float* means,
+                                     const float* w2c, float focal, float pixel_scale,
+                                     const uint8_t* valid, const uint8_t* active, const float* radii,
+                                     float* grad_accum, int32_t* denom, float* max_radii) {
+  GS_REQUIRE(n >= 0, "gs_densify_accumulate: n must be >= 0");
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(grad_means && means && w2c && valid && radii && grad_accum && denom && max_radii,
+             "gs_densify_accumulate: NULL array argument");
+  hipLaunchKernelGGL(densify_kernel, dim3(div_up(n, 256)), dim3(256), 0, (hipStream_t)stream, n,
+                     grad_means, means, w2c, focal, pixel_scale, valid, active, radii, grad_accum, denom,
+                     max_radii);
+  GS_LAUNCH_CHECK("densify_kernel");
+  return GS_OK;
+}

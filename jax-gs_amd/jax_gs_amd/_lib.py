@@ -1,0 +1,93 @@
+"""ctypes binding of libgsraster.so, the gfx950 HIP kernels behind include/gs_raster.h.
+
+The library is built in-tree by ``jax_gs_amd._build.build_library()`` (called from
+``__graft_entry__.build()``).  Loading fails loudly when it is missing: the renderer
+has no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIBPATH = os.path.join(_HERE, "libgsraster.so")
+
+GS_OK = 0
+GS_REC_STRIDE = 12
+GS_NUM_STATS = 16
+STAT = dict(n_interactions=0, max_interactions_per_tile=1, overflow_tiles=2, overflow_interactions=3,
+            truncated_tiles=4, truncated_interactions=5, radius_cap_violations=6, negative_depth=7,
+            capacity_exceeded=8)
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> argtypes (all entry points return int status unless listed in _RESTYPE)
+_SIGS = {
+    "gs_last_error": [],
+    "gs_abi_version": [],
+    "gs_preprocess_fwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P,
+                          _P, _P],
+    "gs_composite_prep": [_P, _I64, _P, _P, _P, _P, _P],
+    "gs_bin_workspace_size": [_I64, _I, _I, _I64],
+    "gs_bin": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _SZ, _P, _P, _P, _P],
+    "gs_tile_ranges": [_P, _P, _I64, _I, _P],
+    "gs_composite_fwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P],
+    "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P],
+    "gs_preprocess_bwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P, _P],
+    "gs_l1_loss": [_P, _I64, _P, _P, _P, _P],
+    "gs_densify_accumulate": [_P, _I64, _P, _P, _P, _F, _F, _P, _P, _P, _P, _P, _P],
+}
+_RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ}
+
+_lib = None
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def lib():
+    """Load libgsraster.so (once).  Raises NativeLibraryMissing if it was not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBPATH):
+            raise NativeLibraryMissing(
+                f"{LIBPATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                "(hipcc --offload-arch=gfx950).  There is no CPU fallback.")
+        L = ctypes.CDLL(LIBPATH)
+        for name, args in _SIGS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPE.get(name, ctypes.c_int)
+        _lib = L
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call an int-returning entry point and raise on a non-zero status."""
+    rc = getattr(lib(), name)(*args)
+    if rc != GS_OK:
+        msg = lib().gs_last_error().decode("utf-8", "replace")
+        if rc == 1:
+            raise ValueError(f"{name}: {msg}")
+        raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+def ptr(t: torch.Tensor | None):
+    """Device pointer of a contiguous tensor (None -> NULL)."""
+    if t is None:
+        return None
+    if not t.is_contiguous():
+        raise ValueError("tensor must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream_handle(device: torch.device):
+    """The current torch stream of `device` as a hipStream_t."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)

@@ -1,0 +1,120 @@
+"""Tile binning and compositing on the GPU (jax_gs/renderer/rasterizer.py).
+
+Constants and function names follow the reference module so that callers (and the
+2DGS family's ``from ...rasterizer import get_tile_interactions, TILE_SIZE``) keep
+working.  Arrays are torch tensors on the GPU.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ._buffers import background_tensor, check_f32, num_tiles
+
+TILE_SIZE = 16  # rasterizer.py:6
+OFFSET_SIZE = 16  # rasterizer.py:7
+BLOCK_SIZE = 512  # rasterizer.py:8
+MAX_TILE_CHUNKS = 8  # rasterizer.py:9
+MAX_TILE_INTERACTIONS = BLOCK_SIZE * MAX_TILE_CHUNKS  # rasterizer.py:10
+
+
+class BinResult(dict):
+    """Outputs of the binning kernels (all device tensors).
+
+    sorted_gids / sorted_tiles: [capacity] int32, the first n entries valid;
+    ranges: [T+1] int32 (searchsorted-left boundaries); stats: [16] int32;
+    n_interactions: 0-d int32 view of stats."""
+
+
+def bin_gaussians(means2d: torch.Tensor, radii: torch.Tensor, valid: torch.Tensor, depths: torch.Tensor, H: int,
+                  W: int, capacity: int | None = None, want_tiles: bool = True) -> BinResult:
+    dev = means2d.device
+    n = means2d.shape[0]
+    means2d = check_f32("means2D", means2d, (n, 2), dev)
+    radii = check_f32("radii", radii.to(torch.float32), (n,), dev)
+    depths = check_f32("depths", depths, (n,), dev)
+    v = valid.to(device=dev, dtype=torch.uint8).contiguous()
+    cap = int(capacity) if capacity else max(256 * n, BLOCK_SIZE)
+    ws_bytes = _lib.lib().gs_bin_workspace_size(n, int(W), int(H), cap)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    _, _, T = num_tiles(W, H)
+    gids = torch.empty((cap,), dtype=torch.int32, device=dev)
+    tiles = torch.empty((cap,), dtype=torch.int32, device=dev) if want_tiles else None
+    ranges = torch.empty((T + 1,), dtype=torch.int32, device=dev)
+    stats = torch.empty((_lib.GS_NUM_STATS,), dtype=torch.int32, device=dev)
+    _lib.call("gs_bin", _lib.stream_handle(dev), n, _lib.ptr(means2d), _lib.ptr(radii), _lib.ptr(v), _lib.ptr(depths),
+              int(W), int(H), cap, _lib.ptr(ws), ws_bytes, _lib.ptr(gids), _lib.ptr(tiles), _lib.ptr(ranges),
+              _lib.ptr(stats))
+    return BinResult(sorted_gids=gids, sorted_tiles=tiles, ranges=ranges, stats=stats,
+                     n_interactions=stats[_lib.STAT["n_interactions"]], capacity=cap, num_tiles=T)
+
+
+def get_tile_interactions(means2D, radii, valid_mask, depths, H, W, tile_size: int = TILE_SIZE):
+    """rasterizer.py:12-116 -> (sorted_tile_ids, sorted_gaussian_ids, n_interactions).
+
+    The first n_interactions entries equal the reference's valid entries in the
+    reference's order (tile, 13-bit depth bucket, Gaussian id).  Positions >= n hold
+    tile T and id 0.  Difference: the reference keeps 256 slots of every Gaussian
+    whose depth has its sign bit set in front of that list (tile -1), and the ids of
+    invalid slots in its tail; no consumer of the arrays reads either."""
+    if tile_size != TILE_SIZE:
+        raise ValueError("only 16x16 tiles are supported (rasterizer.py:6)")
+    r = bin_gaussians(means2D, torch.as_tensor(radii, device=means2D.device), valid_mask, depths, H, W)
+    n = r["n_interactions"]
+    _, _, T = num_tiles(W, H)
+    idx = torch.arange(r["capacity"], device=means2D.device, dtype=torch.int32)
+    tail = idx >= n
+    tiles = torch.where(tail, torch.full_like(r["sorted_tiles"], T), r["sorted_tiles"])
+    gids = torch.where(tail, torch.zeros_like(r["sorted_gids"]), r["sorted_gids"])
+    return tiles, gids, n
+
+
+def tile_ranges(sorted_tile_ids: torch.Tensor, num_tiles_total: int) -> torch.Tensor:
+    """jnp.searchsorted(sorted_tile_ids, arange(T+1)) on the GPU (renderer.py:60)."""
+    st = sorted_tile_ids.to(torch.int32).contiguous()
+    out = torch.empty((num_tiles_total + 1,), dtype=torch.int32, device=st.device)
+    _lib.call("gs_tile_ranges", _lib.stream_handle(st.device), _lib.ptr(st), st.shape[0], int(num_tiles_total),
+              _lib.ptr(out))
+    return out
+
+
+def composite_records(means2D, cov2D, opacities, colors) -> torch.Tensor:
+    """Per-Gaussian compositing records (det clamp, inverse covariance, sigmoid)."""
+    dev = means2D.device
+    n = means2D.shape[0]
+    m = check_f32("means2D", means2D, (n, 2), dev)
+    c = check_f32("cov2D", cov2D, (n, 2, 2), dev)
+    o = check_f32("opacities", opacities, (n, 1), dev)
+    col = check_f32("colors", colors, (n, 3), dev)
+    rec = torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=dev)
+    _lib.call("gs_composite_prep", _lib.stream_handle(dev), n, _lib.ptr(m), _lib.ptr(c), _lib.ptr(o), _lib.ptr(col),
+              _lib.ptr(rec))
+    return rec
+
+
+def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Tensor, H: int, W: int,
+              background: torch.Tensor, residuals: bool = True):
+    """Front-to-back compositing; returns (image [H,W,3], final_T [H,W], n_contrib [H,W])."""
+    dev = records.device
+    image = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
+    fT = torch.empty((H, W), dtype=torch.float32, device=dev) if residuals else None
+    nc = torch.empty((H, W), dtype=torch.int32, device=dev) if residuals else None
+    _lib.call("gs_composite_fwd", _lib.stream_handle(dev), records.shape[0], _lib.ptr(records),
+              _lib.ptr(sorted_gids), sorted_gids.shape[0], _lib.ptr(ranges), int(W), int(H), _lib.ptr(background), _lib.ptr(image),
+              _lib.ptr(fT), _lib.ptr(nc))
+    return image, fT, nc
+
+
+def render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W,
+                 tile_size: int = TILE_SIZE, background=None):
+    """rasterizer.py:119-248 (forward).  Entries of tile t are the ones whose sorted
+    tile id equals t (searchsorted ranges), capped at 4096 per tile."""
+    if tile_size != TILE_SIZE:
+        raise ValueError("only 16x16 tiles are supported (rasterizer.py:6)")
+    dev = means2D.device
+    _, _, T = num_tiles(W, H)
+    rec = composite_records(means2D, cov2D, opacities, colors)
+    ranges = tile_ranges(sorted_tile_ids, T)
+    bg = background_tensor(background, dev)
+    image, _, _ = composite(rec, sorted_gaussian_ids.to(torch.int32).contiguous(), ranges, H, W, bg, residuals=False)
+    return image

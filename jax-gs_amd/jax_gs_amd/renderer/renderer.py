@@ -1,0 +1,111 @@
+"""render(): the drop-in for jax_gs/renderer/renderer.py:15-107.
+
+Same call signature and outputs: ``render(gaussians, camera, background=None,
+fast_tpu_rasterizer=False, mask=None, sh_degree=0) -> (image [H,W,3], extras)``.
+The reference differentiates render with JAX autodiff; here a
+``torch.autograd.Function`` plays the role of a ``jax.custom_vjp``: its forward runs
+the preprocessing, binning and compositing kernels and keeps the per-Gaussian
+records, the sorted entry list, the tile ranges and per-pixel (final T, entry count)
+as residuals; its backward runs the compositing VJP and the preprocessing VJP and
+returns cotangents of the five Gaussian arrays (equal to JAX autodiff of the
+reference forward, with its tie conventions) and of the background.  W2C gets no
+gradient (the reference's trainer never differentiates it) and mask gets None.
+``fast_tpu_rasterizer`` is accepted for signature parity: both reference
+rasterizers produce the same image and there is a single implementation here.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ..core.camera import Camera
+from ..core.gaussians import Gaussians
+from ._buffers import as_mask, background_tensor, check_f32, num_tiles
+from .projection import preprocess
+from .rasterizer import BLOCK_SIZE, bin_gaussians, composite
+
+
+class _Render(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, means, scales, quats, opac, sh, w2c, bg, mask, static):
+        W, H, fx, fy, cx, cy, sh_degree, capacity = static
+        g = Gaussians(means, scales, quats, opac, sh)
+        cam = Camera(W, H, fx, fy, cx, cy, w2c, None)
+        pre = preprocess(g, cam, mask=mask, sh_degree=sh_degree, records=True)
+        b = bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W, capacity=capacity,
+                          want_tiles=False)
+        image, fT, nc = composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg, residuals=True)
+        ctx.static = static
+        ctx.save_for_backward(means, scales, quats, opac, sh, w2c, bg, pre["records"], b["sorted_gids"], b["ranges"],
+                              fT, nc)
+        radii = pre["radii"]
+        valid = pre["valid"].bool()
+        stats = b["stats"]
+        ctx.mark_non_differentiable(radii, valid, stats)
+        return image, radii, valid, stats
+
+    @staticmethod
+    def backward(ctx, g_image, _g_radii, _g_valid, _g_stats):
+        W, H, fx, fy, cx, cy, sh_degree, _ = ctx.static
+        means, scales, quats, opac, sh, w2c, bg, rec, gids, ranges, fT, nc = ctx.saved_tensors
+        dev = means.device
+        n = means.shape[0]
+        s = _lib.stream_handle(dev)
+        g_image = g_image.contiguous()
+        grec = torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=dev)
+        gbg = torch.empty((3,), dtype=torch.float32, device=dev)
+        _lib.call("gs_composite_bwd", s, n, _lib.ptr(rec), _lib.ptr(gids), gids.shape[0], _lib.ptr(ranges), int(W), int(H),
+                  _lib.ptr(bg), _lib.ptr(g_image), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(grec), _lib.ptr(gbg))
+        gm = torch.empty_like(means)
+        gs_ = torch.empty_like(scales)
+        gq = torch.empty_like(quats)
+        go = torch.empty_like(opac)
+        gsh = torch.empty_like(sh)
+        _lib.call("gs_preprocess_bwd", s, n, sh.shape[1], int(sh_degree), _lib.ptr(means), _lib.ptr(scales),
+                  _lib.ptr(quats), _lib.ptr(opac), _lib.ptr(sh), _lib.ptr(w2c), int(W), int(H), float(fx), float(fy),
+                  float(cx), float(cy), _lib.ptr(grec), _lib.ptr(gm), _lib.ptr(gs_), _lib.ptr(gq), _lib.ptr(go),
+                  _lib.ptr(gsh))
+        return gm, gs_, gq, go, gsh, None, gbg, None, None
+
+
+def render(gaussians: Gaussians, camera: Camera, background=None, fast_tpu_rasterizer: bool = False, mask=None,
+           sh_degree: int = 0, capacity: int | None = None):
+    """Render one view; returns (image [H,W,3] float32, extras dict) like renderer.py:15-107.
+
+    capacity bounds the number of (Gaussian, tile) entries; the default is the
+    reference's static bound 256*N (every Gaussian may touch 16x16 tiles)."""
+    del fast_tpu_rasterizer  # single implementation (see module docstring)
+    means = gaussians.means
+    dev = means.device
+    n = means.shape[0]
+    means = check_f32("means", means, (n, 3), dev)
+    w2c = torch.as_tensor(camera.W2C, dtype=torch.float32, device=dev).contiguous()
+    bg = background_tensor(background, dev)
+    m = as_mask(mask, n, dev)
+    cap = int(capacity) if capacity else max(256 * n, BLOCK_SIZE)
+    static = (int(camera.W), int(camera.H), float(camera.fx), float(camera.fy), float(camera.cx), float(camera.cy),
+              int(sh_degree), cap)
+    image, radii, valid, stats = _Render.apply(means, gaussians.scales.contiguous(),
+                                               gaussians.quaternions.contiguous(), gaussians.opacities.contiguous(),
+                                               gaussians.sh_coeffs.contiguous(), w2c, bg, m, static)
+    _, _, T = num_tiles(camera.W, camera.H)
+    extras = extras_from_stats(stats, radii, valid, T)
+    return image, extras
+
+
+def extras_from_stats(stats: torch.Tensor, radii: torch.Tensor, valid: torch.Tensor, num_tiles_total: int) -> dict:
+    """renderer.py:79-90 from the binning kernel's stats (device tensors, no sync)."""
+    S = _lib.STAT
+    n = stats[S["n_interactions"]]
+    return {
+        "radii": radii,
+        "valid_mask": valid,
+        "n_interactions": n,
+        "mean_interactions_per_tile": n.to(torch.float32) / float(max(num_tiles_total, 1)),
+        "max_interactions_per_tile": stats[S["max_interactions_per_tile"]],
+        "overflow_tiles": stats[S["overflow_tiles"]],
+        "overflow_interactions": stats[S["overflow_interactions"]],
+        "truncated_tiles": stats[S["truncated_tiles"]],
+        "truncated_interactions": stats[S["truncated_interactions"]],
+        "radius_cap_violations": stats[S["radius_cap_violations"]],
+    }

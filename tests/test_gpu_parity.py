@@ -1,0 +1,140 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Bars:
+  * integer outputs bit-exact: per-Gaussian tile rectangles/counts (via the entry
+    list), the sorted entry list (tile, Gaussian id) and the tile ranges;
+  * image max-abs error <= 1e-4;
+  * gradients: relative L2 error <= 1e-3 per parameter tensor.
+The per-Gaussian preprocessing is compared bit-for-bit (same float32 operation
+order, no FMA contraction, same exp on both sides).
+
+Reference-order note: the reference's arrays carry 256 slots of every Gaussian whose
+depth has its sign bit set in front of the valid entries (tile -1); the GPU list
+holds only the valid entries, so its boundaries are compared after that shift and
+its entries against the reference's valid sub-list.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from jax_gs_amd import render, scenes
+from jax_gs_amd.renderer import rasterizer
+from jax_gs_amd.renderer.projection import preprocess
+
+pytestmark = pytest.mark.gpu
+
+IMG_TOL = 1e-4
+GRAD_TOL = 1e-3
+FIELDS = ("means", "scales", "quaternions", "opacities", "sh_coeffs")
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)
+
+
+def _ref_valid_sublist(st, sg, n_neg, n_int):
+    off = 256 * n_neg
+    return st[off:off + n_int], sg[off:off + n_int]
+
+
+def _check_preprocess(sc, cuda):
+    g, cam, _, m = scenes.to_torch(sc, cuda)
+    pre = preprocess(g, cam, mask=m, sh_degree=sc["sh_degree"])
+    c = sc["cam"]
+    f32 = np.float32
+    o = oracle.preprocess(sc["params"]["means"], sc["params"]["scales"], sc["params"]["quaternions"],
+                          sc["params"]["sh_coeffs"], c["W2C"], c["W"], c["H"], f32(c["fx"]), f32(c["fy"]),
+                          f32(c["cx"]), f32(c["cy"]), sc["sh_degree"], mask=sc["mask"])
+    for k in ("means2d", "cov2d", "radii", "depths", "colors"):
+        np.testing.assert_array_equal(_np(pre[k]), o[k], err_msg=k)
+    np.testing.assert_array_equal(_np(pre["valid"]).astype(bool), o["valid"])
+    return pre, o
+
+
+def _check_binning(sc, cuda, pre_gpu, pre_o):
+    c = sc["cam"]
+    W, H = c["W"], c["H"]
+    b = rasterizer.bin_gaussians(pre_gpu["means2d"], pre_gpu["radii"], pre_gpu["valid"], pre_gpu["depths"], H, W)
+    st, sg, n_int = oracle.tile_interactions(pre_o["means2d"], pre_o["radii"], pre_o["valid"], pre_o["depths"], H, W)
+    stats = _np(b["stats"])
+    n_neg = int((np.signbit(pre_o["depths"])).sum())
+    assert stats[7] == n_neg
+    assert stats[0] == n_int
+    assert stats[8] == 0
+    st_v, sg_v = _ref_valid_sublist(st, sg, n_neg, n_int)
+    np.testing.assert_array_equal(_np(b["sorted_tiles"])[:n_int], st_v)
+    np.testing.assert_array_equal(_np(b["sorted_gids"])[:n_int], sg_v)
+    T = ((W + 15) // 16) * ((H + 15) // 16)
+    b_ref = oracle.tile_boundaries(st, T)
+    np.testing.assert_array_equal(_np(b["ranges"]) + 256 * n_neg, b_ref)
+    ex = oracle.extras_from(pre_o, st, n_int, H, W)
+    for k, idx in (("max_interactions_per_tile", 1), ("overflow_tiles", 2), ("overflow_interactions", 3),
+                   ("truncated_tiles", 4), ("truncated_interactions", 5), ("radius_cap_violations", 6)):
+        assert stats[idx] == ex[k], k
+    return b, (st, sg, n_int)
+
+
+def _render_both(sc, cuda, seed_kind="l1"):
+    g, cam, tgt, m = scenes.to_torch(sc, cuda)
+    for f in FIELDS:
+        getattr(g, f).requires_grad_(True)
+    image, extras = render(g, cam, mask=m, sh_degree=sc["sh_degree"])
+    img_o, ex_o, res = oracle.render(sc["params"], sc["cam"], mask=sc["mask"], sh_degree=sc["sh_degree"])
+    if seed_kind == "l1":
+        target = sc["target"] if sc["target"] is not None else np.random.default_rng(7).uniform(
+            0, 1, img_o.shape).astype(np.float32)
+        # one seed for both sides (the L1 sign must not flip between them)
+        _, seed = oracle.l1_loss_and_grad(img_o, target)
+    else:
+        seed = np.random.default_rng(11).normal(0, 1, img_o.shape).astype(np.float32)
+    image.backward(torch.from_numpy(seed).to(cuda))
+    gr_o = oracle.render_vjp(sc["params"], sc["cam"], res, seed, sh_degree=sc["sh_degree"])
+    return image, extras, g, img_o, ex_o, gr_o
+
+
+@pytest.mark.parametrize("cfg,n,w,h", [(0, 3000, 128, 96), (1, 4000, 200, 150), (3, 6000, 160, 96),
+                                       (4, 5000, 160, 90)])
+def test_small_scene_parity(cuda, cfg, n, w, h):
+    sc = scenes.make_scene(cfg, n=n, width=w, height=h)
+    pre, pre_o = _check_preprocess(sc, cuda)
+    _check_binning(sc, cuda, pre, pre_o)
+    image, extras, g, img_o, ex_o, gr_o = _render_both(sc, cuda)
+    assert np.abs(_np(image) - img_o).max() <= IMG_TOL
+    assert int(extras["n_interactions"]) == ex_o["n_interactions"]
+    np.testing.assert_array_equal(_np(extras["radii"]), ex_o["radii"])
+    np.testing.assert_array_equal(_np(extras["valid_mask"]), ex_o["valid_mask"])
+    for f in FIELDS:
+        assert _rel(_np(getattr(g, f).grad), gr_o[f]) <= GRAD_TOL, f
+
+
+def test_cfg0_full_forward(cuda):
+    """Configuration 0 at full size: preprocessing + binning bit-exact, image <= 1e-4."""
+    sc = scenes.make_scene(0)
+    pre, pre_o = _check_preprocess(sc, cuda)
+    _check_binning(sc, cuda, pre, pre_o)
+    g, cam, _, _ = scenes.to_torch(sc, cuda)
+    image, extras = render(g, cam, sh_degree=0)
+    img_o, ex_o, _ = oracle.render(sc["params"], sc["cam"], sh_degree=0)
+    assert np.abs(_np(image) - img_o).max() <= IMG_TOL
+    for k in ("n_interactions", "max_interactions_per_tile", "overflow_tiles", "overflow_interactions",
+              "truncated_tiles", "truncated_interactions", "radius_cap_violations"):
+        assert int(extras[k]) == int(ex_o[k]), k
+    assert float(extras["mean_interactions_per_tile"]) == float(ex_o["mean_interactions_per_tile"])
+
+
+def test_cfg1_full_fwd_bwd(cuda):
+    """Configuration 1 at full size: 200k Gaussians, SH3, 504x378, L1 seed."""
+    sc = scenes.make_scene(1)
+    pre, pre_o = _check_preprocess(sc, cuda)
+    _check_binning(sc, cuda, pre, pre_o)
+    image, extras, g, img_o, ex_o, gr_o = _render_both(sc, cuda)
+    assert np.abs(_np(image) - img_o).max() <= IMG_TOL
+    for f in FIELDS:
+        assert _rel(_np(getattr(g, f).grad), gr_o[f]) <= GRAD_TOL, f

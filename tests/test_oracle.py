@@ -1,0 +1,401 @@
+"""Pins the CPU oracle against checks that do not restate its own formulas.
+
+Function of the oracle          pinned by
+------------------------------  -----------------------------------------------------
+gso_expf (float32 exp)          float64 exp, <= 1 ulp over the range the path uses
+preprocess: projection/cov/rad  known answers KA1, KA3 (closed form); float64 NumPy
+                                J W Sigma W^T J^T with Sigma from a rotation matrix
+                                built by scipy.spatial.transform; radius from
+                                numpy.linalg.eigvalsh; Sigma symmetric PSD
+preprocess: SH colour           scipy.special.sph_harm_y real harmonics (basis =
+                                (-1)^m x Condon-Shortley real SH), degrees 0..3
+tile_interactions               known answer KA2; pure-Python brute force over all
+                                256*N slots with Python's stable sorted(); invariants
+render_tiles                    KA4, KA5 closed forms (exactly 48 blends in KA5);
+                                float64 pure-Python per-pixel brute force; the two
+                                reference gathers agree when no clamp triggers
+extras                          scenes built to overflow 512 / truncate 4096 /
+                                exceed the 16-tile span, with counts known by
+                                construction
+render_tiles_bwd, preprocess_bwd central finite differences of the float64 oracle;
+                                KA3: d image / d opacity = 0 when the 0.99 cap binds;
+                                float32 backward within 1e-4 of float64 backward
+l1 seed                         closed form sign(d)/count
+"""
+import math
+
+import numpy as np
+import pytest
+from scipy.spatial.transform import Rotation
+
+import oracle
+
+F32 = np.float32
+C0 = 0.28209479177387814
+
+
+def _cam(W, H, f, c=None):
+    c = (W / 2.0, H / 2.0) if c is None else c
+    return dict(W=W, H=H, fx=f, fy=f, cx=c[0], cy=c[1], W2C=np.eye(4, dtype=F32))
+
+
+def _ulp_diff(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(a - b)
+
+
+# ---------------------------------------------------------------- exp
+def test_expf_within_one_ulp_of_float64():
+    xs = np.concatenate([np.linspace(-87.0, 88.0, 200001, dtype=F32),
+                         np.random.default_rng(0).normal(0, 3, 20000).astype(F32),
+                         np.linspace(-10.0, 0.0, 20001, dtype=F32)])
+    got = np.array([oracle.expf(float(x)) for x in xs[::7]], F32)
+    want = np.exp(xs[::7].astype(np.float64)).astype(F32)
+    assert _ulp_diff(got, want).max() <= 1
+    assert oracle.expf(0.0) == 1.0
+    assert oracle.expf(-200.0) == 0.0
+    assert math.isinf(oracle.expf(100.0))
+
+
+# ---------------------------------------------------------------- preprocess
+def _one(mean, ls, logit=0.0, rgb=(1.0, 1.0, 1.0), q=(1, 0, 0, 0)):
+    sh = np.zeros((1, 16, 3), F32)
+    sh[0, 0, :] = (np.asarray(rgb, F32) - F32(0.5)) / F32(C0)
+    return dict(means=np.array([mean], F32), scales=np.full((1, 3), ls, F32), quaternions=np.array([q], F32),
+                opacities=np.array([[logit]], F32), sh_coeffs=sh)
+
+
+def test_ka1_projection():
+    p = _one((0, 0, 5), -3.0)
+    pre = oracle.preprocess(p["means"], p["scales"], p["quaternions"], p["sh_coeffs"], np.eye(4), 100, 100, 50.0,
+                            50.0, 50.0, 50.0, 0)
+    np.testing.assert_array_equal(pre["means2d"][0], [50.0, 50.0])
+    assert pre["depths"][0] == 5.0 and pre["valid"][0]
+    # closed form: (f/z)^2 exp(-3)^2 + 0.3
+    c = (50.0 / 5.0) ** 2 * math.exp(-6.0) + 0.3
+    np.testing.assert_allclose(pre["cov2d"][0], [[c, 0], [0, c]], rtol=2e-6, atol=1e-7)
+    assert pre["radii"][0] == math.ceil(3 * math.sqrt(c)) == 3
+
+
+def test_projection_matches_float64_linear_algebra():
+    rng = np.random.default_rng(3)
+    n = 4000
+    means = np.stack([rng.uniform(-1, 1, n), rng.uniform(-1, 1, n), rng.uniform(1, 8, n)], 1).astype(F32)
+    scales = rng.normal(-3.0, 0.8, (n, 3)).astype(F32)
+    quats = rng.normal(0, 1, (n, 4)).astype(F32)
+    sh = np.zeros((n, 1, 3), F32)
+    fx, fy, cx, cy = 300.0, 280.0, 160.0, 120.0
+    pre = oracle.preprocess(means, scales, quats, sh, np.eye(4), 320, 240, F32(fx), F32(fy), F32(cx), F32(cy), 0)
+    q64 = quats.astype(np.float64)
+    R = Rotation.from_quat(np.concatenate([q64[:, 1:], q64[:, :1]], 1)).as_matrix()  # scipy: (x,y,z,w)
+    S = np.exp(scales.astype(np.float64))
+    A = R * S[:, None, :]
+    Sig = A @ A.transpose(0, 2, 1)
+    x, y, z = (means[:, k].astype(np.float64) for k in range(3))
+    J = np.zeros((n, 2, 3))
+    J[:, 0, 0] = fx / z
+    J[:, 0, 2] = -fx * x / z ** 2
+    J[:, 1, 1] = fy / z
+    J[:, 1, 2] = -fy * y / z ** 2
+    cov = J @ Sig @ J.transpose(0, 2, 1) + 0.3 * np.eye(2)
+    np.testing.assert_allclose(pre["cov2d"], cov, rtol=3e-4, atol=1e-5)
+    np.testing.assert_allclose(pre["means2d"][:, 0], fx * x / z + cx, rtol=1e-6, atol=1e-4)
+    np.testing.assert_allclose(pre["means2d"][:, 1], fy * y / z + cy, rtol=1e-6, atol=1e-4)
+    lam = np.linalg.eigvalsh(cov)[:, 1]
+    r64 = np.ceil(3 * np.sqrt(lam))
+    frac = 3 * np.sqrt(lam) - np.floor(3 * np.sqrt(lam))
+    safe = (frac > 1e-4) & (frac < 1 - 1e-4)
+    assert safe.mean() > 0.99
+    np.testing.assert_array_equal(pre["radii"][safe], r64[safe])
+    # Sigma from the float32 path is symmetric positive semi-definite
+    assert np.all(np.linalg.eigvalsh(Sig) > -1e-7)
+
+
+def _real_sh_no_cs(l, m, d):
+    from scipy.special import sph_harm_y
+
+    theta = np.arccos(np.clip(d[:, 2], -1, 1))
+    phi = np.arctan2(d[:, 1], d[:, 0])
+    if m < 0:
+        v = math.sqrt(2) * (-1) ** m * sph_harm_y(l, -m, theta, phi).imag
+    elif m == 0:
+        v = sph_harm_y(l, 0, theta, phi).real
+    else:
+        v = math.sqrt(2) * (-1) ** m * sph_harm_y(l, m, theta, phi).real
+    return (-1) ** m * v
+
+
+@pytest.mark.parametrize("deg", [0, 1, 2, 3])
+def test_sh_colour_matches_scipy_real_harmonics(deg):
+    rng = np.random.default_rng(10 + deg)
+    n = 300
+    means = rng.normal(0, 1, (n, 3)).astype(F32)
+    means[:, 2] += 4
+    K = 16
+    sh = rng.normal(0, 0.2, (n, K, 3)).astype(F32)
+    pre = oracle.preprocess(means, np.zeros((n, 3), F32), np.tile(np.array([[1, 0, 0, 0]], F32), (n, 1)), sh,
+                            np.eye(4), 64, 64, F32(50), F32(50), F32(32), F32(32), deg)
+    d = means.astype(np.float64) / np.linalg.norm(means.astype(np.float64), axis=1, keepdims=True)
+    res = np.zeros((n, 3))
+    k = 0
+    for l in range(deg + 1):
+        for m in range(-l, l + 1):
+            res += _real_sh_no_cs(l, m, d)[:, None] * sh[:, k, :].astype(np.float64)
+            k += 1
+    want = np.clip(res + 0.5, 0, 1)
+    np.testing.assert_allclose(pre["colors"], want, atol=2e-6)
+
+
+# ---------------------------------------------------------------- binning
+def test_ka2_tile_interactions():
+    st, sg, n = oracle.tile_interactions(np.array([[16, 16], [0, 0]], F32), np.array([4, 2], F32),
+                                         np.array([True, True]), np.array([5.0, 10.0], F32), 32, 32)
+    assert n == 5 and len(st) == 512
+    np.testing.assert_array_equal(st[:5], [0, 0, 1, 2, 3])
+    np.testing.assert_array_equal(sg[:5], [0, 1, 0, 0, 0])
+    assert np.all(st[5:] == 4)
+    np.testing.assert_array_equal(oracle.tile_boundaries(st, 4), [0, 2, 3, 4, 5])
+
+
+def _brute_bins(means2d, radii, valid, depths, H, W):
+    """Pure-Python enumeration of the 256 slots of every Gaussian + Python's stable sort."""
+    TX, TY = (W + 15) // 16, (H + 15) // 16
+    T = TX * TY
+    slots = []
+    for i in range(len(radii)):
+        mx, my, r = float(means2d[i, 0]), float(means2d[i, 1]), float(radii[i])
+        lo_x, hi_x = min(max(mx - r, 0.0), W - 1.0), min(max(mx + r, 0.0), W - 1.0)
+        lo_y, hi_y = min(max(my - r, 0.0), H - 1.0), min(max(my + r, 0.0), H - 1.0)
+        tx0, tx1, ty0, ty1 = int(lo_x // 16), int(hi_x // 16), int(lo_y // 16), int(hi_y // 16)
+        on = (mx + r > 0) and (mx - r < W) and (my + r > 0) and (my - r < H)
+        v = bool(valid[i]) and on and tx1 >= tx0 and ty1 >= ty0
+        zbits = int(np.array([depths[i]], F32).view(np.int32)[0])
+        dq = zbits >> 18
+        for oy in range(16):
+            for ox in range(16):
+                ax, ay = tx0 + ox, ty0 + oy
+                tile = ay * TX + ax if (v and ax <= tx1 and ay <= ty1) else T
+                key = ((tile << 13) | dq)
+                key = key - (1 << 32) if key >= (1 << 31) else key
+                slots.append((key, i))
+    order = sorted(range(len(slots)), key=lambda j: slots[j][0])  # stable
+    return [slots[j][0] >> 13 for j in order], [slots[j][1] for j in order]
+
+
+def test_tile_interactions_brute_force():
+    rng = np.random.default_rng(5)
+    n = 40
+    W, H = 70, 50
+    means2d = rng.uniform(-20, 90, (n, 2)).astype(F32)
+    radii = np.ceil(rng.uniform(0, 40, n)).astype(F32)
+    radii[:3] = 400  # spans wider than 16 tiles are truncated
+    valid = rng.uniform(0, 1, n) < 0.85
+    depths = rng.uniform(0.02, 9, n).astype(F32)
+    depths[5] = depths[6]  # equal depth bucket: ties resolve by Gaussian id
+    depths[7] = -1.0       # negative depth: its 256 slots sort first with tile -1
+    valid[7] = False
+    st, sg, cnt = oracle.tile_interactions(means2d, radii, valid, depths, H, W)
+    bt, bg = _brute_bins(means2d, radii, valid, depths, H, W)
+    np.testing.assert_array_equal(st, bt)
+    np.testing.assert_array_equal(sg, bg)
+    T = ((W + 15) // 16) * ((H + 15) // 16)
+    assert cnt == int(np.sum((np.asarray(bt) >= 0) & (np.asarray(bt) < T)))
+    assert np.sum(np.asarray(bt) == -1) == 256
+
+
+# ---------------------------------------------------------------- compositing
+def _brute_render(means2d, cov2d, opac, colors, st, sg, H, W, bg):
+    """float64, per pixel, straight from the definition (first min(count,4096) entries)."""
+    TX = (W + 15) // 16
+    T = TX * ((H + 15) // 16)
+    img = np.zeros((H, W, 3))
+    b = np.searchsorted(st, np.arange(T + 1), side="left")
+    for t in range(T):
+        ids = sg[b[t]:b[t + 1]][:4096]
+        tx, ty = t % TX, t // TX
+        for ly in range(16):
+            for lx in range(16):
+                X, Y = tx * 16 + lx, ty * 16 + ly
+                if X >= W or Y >= H:
+                    continue
+                if len(ids) == 0:
+                    img[Y, X] = bg
+                    continue
+                C = np.zeros(3)
+                Tr = 1.0
+                for g in ids:
+                    if Tr <= 1e-4:
+                        break
+                    c = cov2d[g].astype(np.float64)
+                    det = max(c[0, 0] * c[1, 1] - c[0, 1] ** 2, 1e-6)
+                    inv = np.array([[c[1, 1], -c[0, 1]], [-c[0, 1], c[0, 0]]]) / det
+                    d = np.array([X + 0.5, Y + 0.5]) - means2d[g]
+                    pw = -0.5 * d @ inv @ d
+                    if pw <= -10:
+                        continue
+                    a = min(0.99, math.exp(pw) / (1 + math.exp(-float(opac[g, 0]))))
+                    C += a * Tr * colors[g]
+                    Tr *= 1 - a
+                img[Y, X] = C + Tr * bg
+    return img
+
+
+def test_render_tiles_brute_force():
+    rng = np.random.default_rng(8)
+    n = 30
+    W, H = 40, 36
+    pre_m = rng.uniform(0, 40, (n, 2)).astype(F32)
+    A = rng.normal(0, 3, (n, 2, 2))
+    cov = (A @ A.transpose(0, 2, 1) + 0.3 * np.eye(2)).astype(F32)
+    opac = rng.normal(0, 2, (n, 1)).astype(F32)
+    col = rng.uniform(0, 1, (n, 3)).astype(F32)
+    radii = np.ceil(3 * np.sqrt(np.linalg.eigvalsh(cov.astype(np.float64))[:, 1])).astype(F32)
+    depths = rng.uniform(1, 5, n).astype(F32)
+    st, sg, _ = oracle.tile_interactions(pre_m, radii, np.ones(n, bool), depths, H, W)
+    bg = np.array([0.1, 0.2, 0.3], F32)
+    img, fT, nc = oracle.render_tiles(pre_m, cov, opac, col, st, sg, H, W, bg)
+    ref = _brute_render(pre_m, cov, opac, col, st, sg, H, W, bg.astype(np.float64))
+    np.testing.assert_allclose(img, ref, atol=2e-5)
+    img_tpu, _, _ = oracle.render_tiles(pre_m, cov, opac, col, st, sg, H, W, bg, tpu_gather=True)
+    np.testing.assert_allclose(img_tpu, img, atol=2e-6)
+    assert np.all(np.diff(fT.ravel()) == np.diff(fT.ravel()))  # finite
+    assert fT.min() > 0 and fT.max() <= 1
+
+
+def test_ka4_single_gaussian():
+    img, _, _ = oracle.render_tiles(np.array([[16, 16]], F32), np.array([[[10, 0], [0, 10]]], F32),
+                                    np.array([[10.0]], F32), np.array([[1, 0, 0]], F32),
+                                    np.array([0, 1, 2, 3], np.int32), np.zeros(4, np.int32), 32, 32)
+    want = math.exp(-0.5 * 0.5 / 10) * (1 / (1 + math.exp(-10)))
+    np.testing.assert_allclose(img[16, 16], [want, 0, 0], rtol=2e-6, atol=1e-7)
+
+
+def test_ka5_chunked_gated_composite():
+    N = 520
+    means2d = np.tile(np.array([[8, 8]], F32), (N, 1))
+    cov = np.tile(np.array([[[6, 0], [0, 6]]], F32), (N, 1, 1))
+    op = np.full((N, 1), -1.5, F32)
+    col = np.stack([np.linspace(0, 1, N, dtype=F32), np.linspace(1, 0, N, dtype=F32), np.zeros(N, F32)], -1)
+    img, fT, nc = oracle.render_tiles(means2d, cov, op, col, np.zeros(N, np.int32), np.arange(N, dtype=np.int32),
+                                      16, 16)
+    a = math.exp(-0.5 * 0.5 / 6) / (1 + math.exp(1.5))
+    assert abs(a - 0.17498064) < 1e-7
+    k = 0
+    Tr = 1.0
+    C = np.zeros(3)
+    while Tr > 1e-4:
+        C += a * Tr * col[k].astype(np.float64)
+        Tr *= 1 - a
+        k += 1
+    assert k == 48 and nc[8, 8] == 48
+    np.testing.assert_allclose(img[8, 8], C, atol=2e-6)
+    np.testing.assert_allclose(img[8, 8], [0.0090747, 0.9908275, 0.0], atol=1e-6)
+
+
+def test_extras_overflow_truncation_and_span_cap():
+    n = 4200
+    W = H = 64
+    means2d = np.tile(np.array([[8.0, 8.0]], F32), (n, 1))
+    radii = np.full(n, 2.0, F32)           # one tile each
+    radii[:2] = 600.0                      # spans over 16 tiles (image is 4x4 tiles: no cap)
+    depths = np.linspace(1, 3, n).astype(F32)
+    pre = dict(means2d=means2d, radii=radii, valid=np.ones(n, bool), depths=depths)
+    st, sg, cnt = oracle.tile_interactions(means2d, radii, pre["valid"], depths, H, W)
+    assert cnt == (n - 2) + 2 * 16
+    ex = oracle.extras_from(pre, st, cnt, H, W)
+    assert ex["max_interactions_per_tile"] == n
+    assert ex["truncated_tiles"] == 1 and ex["truncated_interactions"] == n - 4096
+    assert ex["overflow_tiles"] == 1 and ex["overflow_interactions"] == n - 512
+    assert ex["radius_cap_violations"] == 0
+    # a 30x30-tile image: the two wide Gaussians exceed the 16-tile span
+    st, sg, cnt = oracle.tile_interactions(means2d, radii, pre["valid"], depths, 480, 480)
+    assert cnt == (n - 2) + 2 * 16 * 16
+    ex = oracle.extras_from(pre, st, cnt, 480, 480)
+    assert ex["radius_cap_violations"] == 2
+
+
+# ---------------------------------------------------------------- backward
+def _tiny_scene(seed, n=12, W=40, H=32, deg=3):
+    rng = np.random.default_rng(seed)
+    means = np.stack([rng.uniform(-0.6, 0.6, n), rng.uniform(-0.5, 0.5, n), rng.uniform(2.5, 4, n)], 1)
+    sh = np.zeros((n, 16, 3))
+    sh[:, 0, :] = (rng.uniform(0.2, 0.8, (n, 3)) - 0.5) / C0
+    sh[:, 1:, :] = rng.normal(0, 0.05, (n, 15, 3))
+    params = dict(means=means, scales=rng.normal(-2.3, 0.2, (n, 3)), quaternions=rng.normal(0, 1, (n, 4)),
+                  opacities=rng.normal(0, 1, (n, 1)), sh_coeffs=sh)
+    return params, _cam(W, H, 30.0), deg
+
+
+def _fd_check(params, cam, deg, seed_img, dtype=np.float64, eps=1e-6, sample=8):
+    img, _, res = oracle.render(params, cam, sh_degree=deg, dtype=dtype)
+    g = oracle.render_vjp(params, cam, res, seed_img, sh_degree=deg, dtype=dtype)
+    rng = np.random.default_rng(1)
+
+    def loss(p):
+        im, _, _ = oracle.render(p, cam, sh_degree=deg, dtype=dtype)
+        return float((im * seed_img).sum())
+
+    for f in ("means", "scales", "quaternions", "opacities", "sh_coeffs"):
+        flat = params[f].reshape(-1)
+        idx = rng.choice(flat.size, size=min(sample, flat.size), replace=False)
+        if f == "sh_coeffs":
+            idx = np.concatenate([idx, [0, 3 * 5 + 1, 3 * 15 + 2]])
+        for i in idx:
+            pp = {k: v.copy() for k, v in params.items()}
+            pp[f].reshape(-1)[i] += eps
+            lp = loss(pp)
+            pp[f].reshape(-1)[i] -= 2 * eps
+            lm = loss(pp)
+            fd = (lp - lm) / (2 * eps)
+            an = g[f].reshape(-1)[i]
+            assert abs(fd - an) <= 1e-5 * max(1.0, abs(fd)) + 1e-7, (f, i, fd, an)
+    return g
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_backward_matches_finite_differences(seed):
+    params, cam, deg = _tiny_scene(seed)
+    rng = np.random.default_rng(100 + seed)
+    seed_img = rng.normal(0, 1, (cam["H"], cam["W"], 3))
+    _fd_check(params, cam, deg, seed_img)
+
+
+def test_float32_backward_close_to_float64():
+    params, cam, deg = _tiny_scene(4)
+    seed_img = np.random.default_rng(3).normal(0, 1, (cam["H"], cam["W"], 3))
+    p32 = {k: v.astype(F32) for k, v in params.items()}
+    p64 = {k: v.astype(F32).astype(np.float64) for k, v in params.items()}
+    _, _, r32 = oracle.render(p32, cam, sh_degree=deg)
+    g32 = oracle.render_vjp(p32, cam, r32, seed_img.astype(F32), sh_degree=deg)
+    _, _, r64 = oracle.render(p64, cam, sh_degree=deg, dtype=np.float64)
+    g64 = oracle.render_vjp(p64, cam, r64, seed_img, sh_degree=deg, dtype=np.float64)
+    for f in ("means", "scales", "quaternions", "opacities", "sh_coeffs"):
+        rel = np.linalg.norm(g32[f] - g64[f]) / np.linalg.norm(g64[f])
+        assert rel < 1e-4, (f, rel)
+
+
+def test_ka3_capped_alpha_has_zero_opacity_gradient():
+    p = _one((0, 0, 5), -1.0, logit=10.0, rgb=(1, 0, 0))
+    cam = _cam(64, 64, 100.0, (32.0, 32.0))
+    img, ex, res = oracle.render(p, cam)
+    c = (100.0 / 5.0) ** 2 * math.exp(-2.0) + 0.3
+    np.testing.assert_allclose(res["pre"]["cov2d"][0, 0, 0], c, rtol=2e-6)
+    assert res["pre"]["radii"][0] == 23
+    np.testing.assert_allclose(img[32, 32], [0.99, 0, 0], atol=1e-6)
+    g = np.zeros_like(img)
+    g[32, 32, 0] = 1
+    gr = oracle.render_vjp(p, cam, res, g)
+    assert gr["opacities"][0, 0] == 0.0
+    # one pixel off the centre the cap does not bind: gradient is positive
+    g2 = np.zeros_like(img)
+    g2[32, 40, 0] = 1
+    assert oracle.render_vjp(p, cam, res, g2)["opacities"][0, 0] > 0
+
+
+def test_l1_seed_closed_form():
+    a = np.array([[[0.5, 0.2, 0.7]]], F32)
+    b = np.array([[[0.5, 0.9, 0.1]]], F32)
+    loss, g = oracle.l1_loss_and_grad(a, b)
+    np.testing.assert_allclose(loss, (0 + 0.7 + 0.6) / 3, rtol=1e-6)
+    np.testing.assert_array_equal(g, np.array([[[0, -1, 1]]], F32) * F32(1 / 3))
