@@ -6,37 +6,62 @@
 // power > -10, with alpha = min(0.99, exp(power) * sigmoid(opacity)); the pixel is
 // C + T * background.  rasterizer_tpu.py computes the same image.
 //
-// Layout: one 256-thread workgroup (4 waves) per 16x16 tile, one pixel per thread.
-// Entries are staged through LDS in batches of 256 records (48 B each); the tile
-// stops as soon as every pixel has T <= 1e-4 (workgroup-wide vote).  The backward
-// replays each pixel back to front from its saved final T and entry count,
-// recovering T_k = T_{k+1} / (1 - alpha_k), reduces each entry's 9 gradient terms
-// across the wave, combines the 4 waves in LDS and issues one set of float atomics
-// per (tile, entry).
+// Work decomposition: every wave owns PPT*4 rows of one 16x16 tile; lane l holds the
+// PPT pixels (l % 16, row0 + l / 16 + 4 i), i < PPT, i.e. one column, so the x offset
+// to a Gaussian is shared by the lane's pixels.  Waves are independent (no LDS, no
+// barriers): a wave walks its tile's entry list in batches of 64, each lane loading
+// one record (12 floats) while the previous batch is being blended, and entry j of a
+// batch is broadcast to the whole wave with v_readlane (operands in SGPRs).  With
+// PPT = 4 a wave covers the whole tile (used for large images); PPT = 1 uses four
+// waves per tile for small images that would otherwise leave CUs idle.
+//
+// Forward: stops when every pixel of the wave has T <= 1e-4 (ballot), and writes per
+// pixel the final T and the number of leading entries consumed (n_contrib).
+// Backward: replays each pixel back to front from (final T, n_contrib), recovering
+// T_k = T_{k+1} / (1 - alpha_k) and the colour behind entry k,
+// R_{k-1} = alpha_k c_k + (1 - alpha_k) R_k.  The 9 gradient terms of an entry are
+// summed over the lane's pixels, reduced across the wave with DPP row shifts and row
+// broadcasts, and added to the Gaussian's gradient record with one atomic
+// instruction (9 lanes).  Gradients follow JAX autodiff of the reference: the cap
+// min(0.99, .) passes no gradient when it binds (half at a tie), gated entries pass
+// none.
 #include "gs_common.h"
 
 namespace gs {
 namespace {
 
-constexpr int kThreads = 256;
 constexpr float kTMin = 1e-4f;
+constexpr float kLog2e = 1.4426950408889634f;
 
-__device__ inline float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ inline float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 
-// power of rasterizer.py:210 with the -0.5 folded into the record (exact: a power
-// of two scaling), same association as the reference.
-__device__ inline float power_of(float dx, float dy, float4 a, float b_x) {
-  return ((dx * dx) * a.z + (dx * dy) * a.w) + (dy * dy) * b_x;
+__device__ inline float bcast(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ inline int bcast_i(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+
+__device__ inline float dpp_add(float x, int t) { return x + __int_as_float(t); }
+
+// Sum over the 64 lanes; the total is returned in every lane (through an SGPR).
+// Row reduction with row_shr 1,2,4,8 leaves each 16-lane row's sum in its lane 15;
+// row_bcast:15 and row_bcast:31 fold the rows into lane 63.
+__device__ inline float wave_sum(float v) {
+  float x = v;
+  x = dpp_add(x, __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xF, 0xF, false));
+  x = dpp_add(x, __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xF, 0xF, false));
+  x = dpp_add(x, __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xF, 0xF, false));
+  x = dpp_add(x, __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xF, 0xF, false));
+  x = dpp_add(x, __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xA, 0xF, false));
+  x = dpp_add(x, __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xC, 0xF, false));
+  return bcast(x, 63);
 }
 
 // XCD-aware tile order: consecutive workgroups go round-robin to the 8 XCDs, so
-// block b is given tile (b % 8) * per + b / 8 and each XCD's L2 sees a contiguous
+// workgroup b works on tile (b % 8) * per + b / 8 and each XCD's L2 sees a contiguous
 // band of tiles that share Gaussians.
 __device__ inline int tile_of_block(int b, int T) {
   const int per = (T + 7) >> 3;
-  const int xcd = b & 7, k = b >> 3;
-  const int t = xcd * per + k;
-  return t;
+  return (b & 7) * per + (b >> 3);
 }
 
 // Entries [start, start+n) of a tile, n capped at 4096; ranges are clamped to the
@@ -52,202 +77,254 @@ __device__ inline void tile_span(const int32_t* __restrict__ ranges, int tile, i
   n = num_g > 0 ? (int)c : 0;
 }
 
-__global__ __launch_bounds__(kThreads) void composite_fwd_kernel(
+struct Rec {
+  float mx, my, A, B, C, op, r, g, b;
+};
+
+__device__ inline Rec zero_rec() { return Rec{0, 0, 0, 0, 0, 0, 0, 0, 0}; }
+
+__device__ inline Rec load_rec(const float4* __restrict__ rec, int g) {
+  const float4 a = rec[(int64_t)g * 3];
+  const float4 b = rec[(int64_t)g * 3 + 1];
+  const float c = rec[(int64_t)g * 3 + 2].x;
+  return Rec{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c};
+}
+
+__device__ inline Rec bcast_rec(const Rec& r, int j) {
+  return Rec{bcast(r.mx, j), bcast(r.my, j), bcast(r.A, j), bcast(r.B, j), bcast(r.C, j),
+             bcast(r.op, j), bcast(r.r, j), bcast(r.g, j), bcast(r.b, j)};
+}
+
+// power = -0.5 * (ic00 dx^2 + 2 ic01 dx dy + ic11 dy^2) with the -0.5 folded into the
+// record (A, B, C); the forward and backward kernels share this exact expression.
+__device__ inline float power_of(float dy, float Adx2, float Bdx, float C) {
+  return fmaf(C * dy, dy, fmaf(Bdx, dy, Adx2));
+}
+
+template <int PPT>
+__global__ __launch_bounds__(64) void composite_fwd_kernel(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
-    float* __restrict__ img,
-    float* __restrict__ finalT, int32_t* __restrict__ ncontrib) {
-  const int tile = tile_of_block(blockIdx.x, T);
-  if (tile >= T) return;  // uniform per workgroup
+    float* __restrict__ img, float* __restrict__ finalT, int32_t* __restrict__ ncontrib) {
+  constexpr int WPT = 4 / PPT;  // waves per tile
+  const int b = blockIdx.x / WPT, part = blockIdx.x % WPT;
+  const int tile = tile_of_block(b, T);
+  if (tile >= T) return;
+  const int lane = threadIdx.x;
   const int tx = tile % TX, ty = tile / TX;
-  const int lx = threadIdx.x & 15, ly = threadIdx.x >> 4;
-  const int pix = tx * kTile + lx, piy = ty * kTile + ly;
-  const bool inside = pix < W && piy < H;
-  const float px = (float)(tx * kTile) + ((float)lx + 0.5f);
-  const float py = (float)(ty * kTile) + ((float)ly + 0.5f);
+  const int X = tx * kTile + (lane & 15);
+  const int Y0 = ty * kTile + part * 4 * PPT + (lane >> 4);
+  const float px = (float)(tx * kTile) + ((float)(lane & 15) + 0.5f);
+  float py[PPT];
+  bool done[PPT];
+  float Tr[PPT], c0[PPT], c1[PPT], c2[PPT];
+  int kstop[PPT];
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int yl = part * 4 * PPT + (lane >> 4) + 4 * i;
+    py[i] = (float)(ty * kTile) + ((float)yl + 0.5f);
+    done[i] = !(X < W && Y0 + 4 * i < H);
+    Tr[i] = 1.0f;
+    c0[i] = c1[i] = c2[i] = 0.0f;
+    kstop[i] = 0;
+  }
   int start, n;
   tile_span(ranges, tile, n_entries, num_g, start, n);
 
-  __shared__ float4 sA[kThreads], sB[kThreads];
-  __shared__ float sC[kThreads];
-  float T_ = 1.0f, c0 = 0.0f, c1 = 0.0f, c2 = 0.0f;
-  int kstop = 0;
-  bool done = !inside;
-  for (int b0 = 0; b0 < n; b0 += kThreads) {
-    if (__syncthreads_count(done) == kThreads) break;
-    const int k = b0 + threadIdx.x;
-    if (k < n) {
-      // out-of-range ids clamp, as XLA's gather does
-      const int g = min(max(gids[start + k], 0), num_g - 1);
-      const float4* r = rec + (int64_t)g * 3;
-      sA[threadIdx.x] = r[0];
-      sB[threadIdx.x] = r[1];
-      sC[threadIdx.x] = r[2].x;
-    }
-    __syncthreads();
-    if (!done) {
-      const int cnt = (n - b0) < kThreads ? (n - b0) : kThreads;
-      int j = 0;
-      for (; j < cnt; ++j) {
-        const float4 a = sA[j];
-        const float4 b = sB[j];
-        const float dx = px - a.x, dy = py - a.y;
-        const float pw = power_of(dx, dy, a, b.x);
-        if (pw > -10.0f) {
-          float al = fast_exp(pw) * b.y;
+  bool lane_done = true;
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) lane_done = lane_done && done[i];
+  Rec cur = zero_rec();
+  if (lane < n) cur = load_rec(rec, min(max(gids[start + lane], 0), num_g - 1));
+  for (int b0 = 0; b0 < n; b0 += 64) {
+    if (__ballot(!lane_done) == 0ull) break;
+    // prefetch the next batch while this one is blended
+    Rec nxt = zero_rec();
+    if (b0 + 64 + lane < n) nxt = load_rec(rec, min(max(gids[start + b0 + 64 + lane], 0), num_g - 1));
+    const int cnt = min(64, n - b0);
+    for (int j = 0; j < cnt; ++j) {
+      const Rec e = bcast_rec(cur, j);
+      const float dx = px - e.mx;
+      const float Adx2 = (e.A * dx) * dx, Bdx = e.B * dx;
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const float dy = py[i] - e.my;
+        const float pw = power_of(dy, Adx2, Bdx, e.C);
+        if (!done[i] && pw > -10.0f) {
+          float al = fast_exp(pw) * e.op;
           al = al < 0.99f ? al : 0.99f;
-          const float wgt = al * T_;
-          c0 = c0 + wgt * b.z;
-          c1 = c1 + wgt * b.w;
-          c2 = c2 + wgt * sC[j];
-          T_ = T_ * (1.0f - al);
-          if (T_ <= kTMin) {
-            done = true;
-            ++j;
-            break;
+          const float w = al * Tr[i];
+          c0[i] = fmaf(w, e.r, c0[i]);
+          c1[i] = fmaf(w, e.g, c1[i]);
+          c2[i] = fmaf(w, e.b, c2[i]);
+          Tr[i] = Tr[i] * (1.0f - al);
+          if (Tr[i] <= kTMin) {
+            done[i] = true;
+            kstop[i] = b0 + j + 1;
           }
         }
       }
-      kstop = b0 + j;
-    }
-  }
-  if (inside) {
-    const int64_t p = (int64_t)piy * W + pix;
-    img[3 * p] = c0 + T_ * bg[0];
-    img[3 * p + 1] = c1 + T_ * bg[1];
-    img[3 * p + 2] = c2 + T_ * bg[2];
-    if (finalT) finalT[p] = T_;
-    if (ncontrib) ncontrib[p] = kstop;
-  }
-}
-
-__device__ inline float wave_sum(float v) {
+      if ((j & 15) == 15) {
+        lane_done = true;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-__global__ __launch_bounds__(kThreads) void composite_bwd_kernel(
-    const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
-    const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
-    const float* __restrict__ gimg,
-    const float* __restrict__ finalT, const int32_t* __restrict__ ncontrib, float* __restrict__ grec,
-    float* __restrict__ gbg) {
-  const int tile = tile_of_block(blockIdx.x, T);
-  if (tile >= T) return;
-  const int tx = tile % TX, ty = tile / TX;
-  const int lx = threadIdx.x & 15, ly = threadIdx.x >> 4;
-  const int pix = tx * kTile + lx, piy = ty * kTile + ly;
-  const bool inside = pix < W && piy < H;
-  const float px = (float)(tx * kTile) + ((float)lx + 0.5f);
-  const float py = (float)(ty * kTile) + ((float)ly + 0.5f);
-  int start, n;
-  tile_span(ranges, tile, n_entries, num_g, start, n);
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-
-  float T_ = 1.0f, g0 = 0.0f, g1 = 0.0f, g2 = 0.0f;
-  int kp = 0;
-  if (inside) {
-    const int64_t p = (int64_t)piy * W + pix;
-    T_ = finalT[p];
-    kp = ncontrib[p];
-    kp = kp < 0 ? 0 : (kp > n ? n : kp);  // entries beyond the tile's list never load
-    g0 = gimg[3 * p];
-    g1 = gimg[3 * p + 1];
-    g2 = gimg[3 * p + 2];
+        for (int i = 0; i < PPT; ++i) lane_done = lane_done && done[i];
+        if (__ballot(!lane_done) == 0ull) break;
+      }
+    }
+    lane_done = true;
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) lane_done = lane_done && done[i];
+    cur = nxt;
   }
   const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];
-  // dL/dbackground = sum_p T_final(p) * g(p)
-  if (gbg != nullptr) {
-    float t0 = wave_sum(T_ * g0), t1 = wave_sum(T_ * g1), t2 = wave_sum(T_ * g2);
-    if (lane == 0) {
-      atomicAdd(&gbg[0], t0);
-      atomicAdd(&gbg[1], t1);
-      atomicAdd(&gbg[2], t2);
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int Y = Y0 + 4 * i;
+    if (X < W && Y < H) {
+      const int64_t p = (int64_t)Y * W + X;
+      img[3 * p] = c0[i] + Tr[i] * bg0;
+      img[3 * p + 1] = c1[i] + Tr[i] * bg1;
+      img[3 * p + 2] = c2[i] + Tr[i] * bg2;
+      if (finalT) finalT[p] = Tr[i];
+      if (ncontrib) ncontrib[p] = done[i] ? kstop[i] : n;
     }
   }
-  float R0 = bg0, R1 = bg1, R2 = bg2;  // colour behind the current entry, per unit T
+}
 
-  __shared__ int skmax[4];
-  int km = kp;
+template <int PPT>
+__global__ __launch_bounds__(64) void composite_bwd_kernel(
+    const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
+    const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
+    const float* __restrict__ gimg, const float* __restrict__ finalT, const int32_t* __restrict__ ncontrib,
+    float* __restrict__ grec, float* __restrict__ gbg) {
+  constexpr int WPT = 4 / PPT;
+  const int b = blockIdx.x / WPT, part = blockIdx.x % WPT;
+  const int tile = tile_of_block(b, T);
+  if (tile >= T) return;
+  const int lane = threadIdx.x;
+  const int tx = tile % TX, ty = tile / TX;
+  const int X = tx * kTile + (lane & 15);
+  const int Y0 = ty * kTile + part * 4 * PPT + (lane >> 4);
+  const float px = (float)(tx * kTile) + ((float)(lane & 15) + 0.5f);
+  int start, n;
+  tile_span(ranges, tile, n_entries, num_g, start, n);
+  const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];
+
+  float py[PPT], Tr[PPT], g0[PPT], g1[PPT], g2[PPT], R0[PPT], R1[PPT], R2[PPT];
+  int kp[PPT];
+  int kmax = 0;
+  float tb0 = 0.0f, tb1 = 0.0f, tb2 = 0.0f;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) km = max(km, __shfl_xor(km, o, 64));
-  if (lane == 0) skmax[wid] = km;
-  __syncthreads();
-  const int kmax = max(max(skmax[0], skmax[1]), max(skmax[2], skmax[3]));
-
-  __shared__ float4 sA[kThreads], sB[kThreads];
-  __shared__ float sC[kThreads];
-  __shared__ int sG[kThreads];
-  __shared__ float sgrad[9][kThreads];
-  for (int b1 = kmax; b1 > 0; b1 -= kThreads) {
-    const int b0 = b1 > kThreads ? b1 - kThreads : 0;
-    const int cnt = b1 - b0;
-    if ((int)threadIdx.x < cnt) {
-      const int g = min(max(gids[start + b0 + threadIdx.x], 0), num_g - 1);
-      const float4* r = rec + (int64_t)g * 3;
-      sG[threadIdx.x] = g;
-      sA[threadIdx.x] = r[0];
-      sB[threadIdx.x] = r[1];
-      sC[threadIdx.x] = r[2].x;
+  for (int i = 0; i < PPT; ++i) {
+    const int yl = part * 4 * PPT + (lane >> 4) + 4 * i;
+    py[i] = (float)(ty * kTile) + ((float)yl + 0.5f);
+    Tr[i] = 1.0f;
+    g0[i] = g1[i] = g2[i] = 0.0f;
+    kp[i] = 0;
+    const int Y = Y0 + 4 * i;
+    if (X < W && Y < H) {
+      const int64_t p = (int64_t)Y * W + X;
+      Tr[i] = finalT[p];
+      const int k = ncontrib[p];
+      kp[i] = k < 0 ? 0 : (k > n ? n : k);  // entries beyond the tile's list never load
+      g0[i] = gimg[3 * p];
+      g1[i] = gimg[3 * p + 1];
+      g2[i] = gimg[3 * p + 2];
     }
+    R0[i] = bg0;
+    R1[i] = bg1;
+    R2[i] = bg2;
+    kmax = max(kmax, kp[i]);
+    // dL/dbackground = sum over pixels of T_final * g
+    tb0 = fmaf(Tr[i], g0[i], tb0);
+    tb1 = fmaf(Tr[i], g1[i], tb1);
+    tb2 = fmaf(Tr[i], g2[i], tb2);
+  }
+  if (gbg != nullptr) {
+    const float s0 = wave_sum(tb0), s1 = wave_sum(tb1), s2 = wave_sum(tb2);
+    if (lane < 3) atomicAdd(&gbg[lane], lane == 0 ? s0 : (lane == 1 ? s1 : s2));
+  }
+  // wave-wide maximum entry count (uniform loop bound)
 #pragma unroll
-    for (int c = 0; c < 9; ++c) sgrad[c][threadIdx.x] = 0.0f;
-    __syncthreads();
-    for (int j = cnt - 1; j >= 0; --j) {
+  for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, __shfl_xor(kmax, o, 64));
+  kmax = bcast_i(kmax, 0);
+
+  int b1 = kmax;
+  Rec cur = zero_rec();
+  int gcur = 0;
+  if (b1 > 0) {
+    const int b0 = b1 > 64 ? b1 - 64 : 0;
+    if (b0 + lane < b1) {
+      gcur = min(max(gids[start + b0 + lane], 0), num_g - 1);
+      cur = load_rec(rec, gcur);
+    }
+  }
+  while (b1 > 0) {
+    const int b0 = b1 > 64 ? b1 - 64 : 0;
+    // prefetch the batch in front of this one
+    Rec nxt = zero_rec();
+    int gnxt = 0;
+    const int pb0 = b0 > 64 ? b0 - 64 : 0;
+    if (pb0 + lane < b0) {
+      gnxt = min(max(gids[start + pb0 + lane], 0), num_g - 1);
+      nxt = load_rec(rec, gnxt);
+    }
+    for (int j = b1 - b0 - 1; j >= 0; --j) {
       const int k = b0 + j;
+      const Rec e = bcast_rec(cur, j);
+      const float dx = px - e.mx;
+      const float Adx2 = (e.A * dx) * dx, Bdx = e.B * dx;
       float v[9];
 #pragma unroll
       for (int c = 0; c < 9; ++c) v[c] = 0.0f;
-      bool contrib = false;
-      if (k < kp) {
-        const float4 a = sA[j];
-        const float4 b = sB[j];
-        const float cb = sC[j];
-        const float dx = px - a.x, dy = py - a.y;
-        const float pw = power_of(dx, dy, a, b.x);
-        if (pw > -10.0f) {
-          contrib = true;
-          const float e = fast_exp(pw);
-          const float araw = e * b.y;
+      bool any = false;
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const float dy = py[i] - e.my;
+        const float pw = power_of(dy, Adx2, Bdx, e.C);
+        if (k < kp[i] && pw > -10.0f) {
+          any = true;
+          const float ex = fast_exp(pw);
+          const float araw = ex * e.op;
           const float al = araw < 0.99f ? araw : 0.99f;
           const float capf = araw < 0.99f ? 1.0f : (araw == 0.99f ? 0.5f : 0.0f);
           const float om = 1.0f - al;
-          const float Tk = T_ / om;
-          const float wgt = al * Tk;
-          v[6] = wgt * g0;
-          v[7] = wgt * g1;
-          v[8] = wgt * g2;
-          const float dal = Tk * (((b.z - R0) * g0 + (b.w - R1) * g1) + (cb - R2) * g2);
-          R0 = al * b.z + om * R0;
-          R1 = al * b.w + om * R1;
-          R2 = al * cb + om * R2;
-          T_ = Tk;
-          const float dpw = dal * araw * capf;
-          v[5] = dal * e * capf;
-          v[2] = dpw * dx * dx;
-          v[3] = dpw * dx * dy;
-          v[4] = dpw * dy * dy;
-          v[0] = -dpw * (2.0f * a.z * dx + a.w * dy);
-          v[1] = -dpw * (a.w * dx + 2.0f * b.x * dy);
+          const float Tk = Tr[i] * __builtin_amdgcn_rcpf(om);
+          const float w = al * Tk;
+          v[6] = fmaf(w, g0[i], v[6]);
+          v[7] = fmaf(w, g1[i], v[7]);
+          v[8] = fmaf(w, g2[i], v[8]);
+          const float dal = Tk * fmaf(e.b - R2[i], g2[i], fmaf(e.g - R1[i], g1[i], (e.r - R0[i]) * g0[i]));
+          R0[i] = fmaf(al, e.r, om * R0[i]);
+          R1[i] = fmaf(al, e.g, om * R1[i]);
+          R2[i] = fmaf(al, e.b, om * R2[i]);
+          Tr[i] = Tk;
+          const float dae = dal * capf;
+          const float dpw = dae * araw;
+          v[5] = fmaf(dae, ex, v[5]);
+          const float dpx = dpw * dx, dpy = dpw * dy;
+          v[2] = fmaf(dpx, dx, v[2]);
+          v[3] = fmaf(dpx, dy, v[3]);
+          v[4] = fmaf(dpy, dy, v[4]);
+          // d power / d mean = -(2 A dx + B dy, B dx + 2 C dy)
+          v[0] = fmaf(-dpw, fmaf(2.0f * e.A, dx, e.B * dy), v[0]);
+          v[1] = fmaf(-dpw, fmaf(e.B, dx, 2.0f * e.C * dy), v[1]);
         }
       }
-      if (__ballot(contrib) != 0ull) {
+      if (__ballot(any) != 0ull) {
+        float s[9];
 #pragma unroll
-        for (int c = 0; c < 9; ++c) v[c] = wave_sum(v[c]);
-        if (lane == 0) {
+        for (int c = 0; c < 9; ++c) s[c] = wave_sum(v[c]);
+        float mine = s[0];
 #pragma unroll
-          for (int c = 0; c < 9; ++c) atomicAdd(&sgrad[c][j], v[c]);
-        }
+        for (int c = 1; c < 9; ++c) mine = lane == c ? s[c] : mine;
+        const int g = bcast_i(gcur, j);
+        if (lane < 9 && mine != 0.0f) atomicAdd(&grec[(int64_t)g * kRec + lane], mine);
       }
     }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < 9 * cnt; idx += kThreads) {
-      const int j = idx / 9, c = idx - 9 * j;
-      const float val = sgrad[c][j];
-      if (val != 0.0f) atomicAdd(&grec[(int64_t)sG[j] * kRec + c], val);
-    }
-    __syncthreads();
+    cur = nxt;
+    gcur = gnxt;
+    b1 = b0;
   }
 }
 
@@ -256,14 +333,8 @@ __global__ void zero_f32_kernel(float* __restrict__ p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0.0f;
 }
 
-__global__ void fill_bg_kernel(const float* __restrict__ bg, float* __restrict__ img, int64_t npix) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < npix; i += stride) {
-    img[3 * i] = bg[0];
-    img[3 * i + 1] = bg[1];
-    img[3 * i + 2] = bg[2];
-  }
-}
+// Large images have enough tiles to fill the GPU with one wave per tile.
+inline int pick_ppt(int T) { return T >= 2048 ? 4 : 1; }
 
 }  // namespace
 }  // namespace gs
@@ -271,30 +342,38 @@ __global__ void fill_bg_kernel(const float* __restrict__ bg, float* __restrict__
 using namespace gs;
 
 extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
-                                int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
-                                float* image, float* final_T, int32_t* n_contrib) {
-  GS_REQUIRE(n >= 0, "gs_composite_fwd: n must be >= 0");
+                                int64_t n_entries, const int32_t* ranges, int width, int height,
+                                const float* background, float* image, float* final_T, int32_t* n_contrib) {
+  GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "gs_composite_fwd: n out of range");
+  GS_REQUIRE(n_entries >= 0, "gs_composite_fwd: n_entries must be >= 0");
   GS_REQUIRE(width > 0 && height > 0, "gs_composite_fwd: bad image size %dx%d", width, height);
   GS_REQUIRE(ranges && background && image, "gs_composite_fwd: NULL argument");
-  GS_REQUIRE(n == 0 || (records && sorted_gids), "gs_composite_fwd: NULL records/gids");
+  GS_REQUIRE(n == 0 || n_entries == 0 || (records && sorted_gids), "gs_composite_fwd: NULL records/gids");
   const int TX = (width + kTile - 1) / kTile, TY = (height + kTile - 1) / kTile;
   const int T = TX * TY;
   const int nblk = ((T + 7) / 8) * 8;
-  hipLaunchKernelGGL(composite_fwd_kernel, dim3(nblk), dim3(kThreads), 0, (hipStream_t)stream,
-                     (const float4*)records, (int)n, sorted_gids, n_entries, ranges, width, height, TX, T,
-                     background, image, final_T, n_contrib);
+  hipStream_t s = (hipStream_t)stream;
+  if (pick_ppt(T) == 4) {
+    hipLaunchKernelGGL(composite_fwd_kernel<4>, dim3(nblk), dim3(64), 0, s, (const float4*)records, (int)n,
+                       sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib);
+  } else {
+    hipLaunchKernelGGL(composite_fwd_kernel<1>, dim3(nblk * 4), dim3(64), 0, s, (const float4*)records, (int)n,
+                       sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib);
+  }
   GS_LAUNCH_CHECK("composite_fwd_kernel");
   return GS_OK;
 }
 
 extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
-                                int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
-                                const float* grad_image, const float* final_T, const int32_t* n_contrib,
-                                float* grad_records, float* grad_background) {
-  GS_REQUIRE(n >= 0, "gs_composite_bwd: n must be >= 0");
+                                int64_t n_entries, const int32_t* ranges, int width, int height,
+                                const float* background, const float* grad_image, const float* final_T,
+                                const int32_t* n_contrib, float* grad_records, float* grad_background) {
+  GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "gs_composite_bwd: n out of range");
+  GS_REQUIRE(n_entries >= 0, "gs_composite_bwd: n_entries must be >= 0");
   GS_REQUIRE(width > 0 && height > 0, "gs_composite_bwd: bad image size %dx%d", width, height);
   GS_REQUIRE(ranges && background && grad_image && final_T && n_contrib, "gs_composite_bwd: NULL argument");
-  GS_REQUIRE(n == 0 || (records && sorted_gids && grad_records), "gs_composite_bwd: NULL records/gids");
+  GS_REQUIRE(n == 0 || n_entries == 0 || (records && sorted_gids && grad_records),
+             "gs_composite_bwd: NULL records/gids");
   hipStream_t s = (hipStream_t)stream;
   if (n > 0) {
     hipLaunchKernelGGL(zero_f32_kernel, dim3(1024), dim3(256), 0, s, grad_records, n * kRec);
@@ -307,9 +386,15 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
   const int TX = (width + kTile - 1) / kTile, TY = (height + kTile - 1) / kTile;
   const int T = TX * TY;
   const int nblk = ((T + 7) / 8) * 8;
-  hipLaunchKernelGGL(composite_bwd_kernel, dim3(nblk), dim3(kThreads), 0, s, (const float4*)records, (int)n,
-                     sorted_gids, n_entries, ranges, width, height, TX, T, background, grad_image, final_T, n_contrib, grad_records,
-                     grad_background);
+  if (pick_ppt(T) == 4) {
+    hipLaunchKernelGGL(composite_bwd_kernel<4>, dim3(nblk), dim3(64), 0, s, (const float4*)records, (int)n,
+                       sorted_gids, n_entries, ranges, width, height, TX, T, background, grad_image, final_T,
+                       n_contrib, grad_records, grad_background);
+  } else {
+    hipLaunchKernelGGL(composite_bwd_kernel<1>, dim3(nblk * 4), dim3(64), 0, s, (const float4*)records, (int)n,
+                       sorted_gids, n_entries, ranges, width, height, TX, T, background, grad_image, final_T,
+                       n_contrib, grad_records, grad_background);
+  }
   GS_LAUNCH_CHECK("composite_bwd_kernel");
   return GS_OK;
 }

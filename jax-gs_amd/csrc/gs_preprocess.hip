@@ -114,28 +114,49 @@ __device__ inline void view_dir(const float* w, float mx, float my, float mz, fl
   d[2] = v[2] / nrm;
 }
 
-// sh.py:25-72 for one channel; sh points at coefficient 0 of that channel with a
-// stride of 3 floats between coefficients.
-__device__ inline float eval_sh_channel(int deg, const float* __restrict__ sh, const float* d) {
-  float res = SH_C0 * sh[0];
-  if (deg > 0) {
+// Loads the first NB coefficient triples of one Gaussian's sh row (K triples) into
+// registers: float4 loads when the row is 16-byte aligned (K % 4 == 0), else dwords.
+template <int NB>
+__device__ inline void load_sh(const float* __restrict__ row, int K, float* v) {
+  if ((K & 3) == 0) {
+    constexpr int NQ = (3 * NB + 3) / 4;
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const float4 t = r4[q];
+      if (4 * q + 0 < 3 * NB) v[4 * q + 0] = t.x;
+      if (4 * q + 1 < 3 * NB) v[4 * q + 1] = t.y;
+      if (4 * q + 2 < 3 * NB) v[4 * q + 2] = t.z;
+      if (4 * q + 3 < 3 * NB) v[4 * q + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 3 * NB; ++q) v[q] = row[q];
+  }
+}
+
+// sh.py:25-72 for channel c; sh holds coefficient triples (k, channel) at 3k + c.
+template <int DEG>
+__device__ inline float eval_sh_channel(const float* sh, int c, const float* d) {
+  float res = SH_C0 * sh[c];
+  if (DEG > 0) {
     const float x = d[0], y = d[1], z = d[2];
-    res = ((res - (SH_C1 * y) * sh[3]) + (SH_C1 * z) * sh[6]) - (SH_C1 * x) * sh[9];
-    if (deg > 1) {
+    res = ((res - (SH_C1 * y) * sh[3 + c]) + (SH_C1 * z) * sh[6 + c]) - (SH_C1 * x) * sh[9 + c];
+    if (DEG > 1) {
       const float xx = x * x, yy = y * y, zz = z * z;
       const float xy = x * y, yz = y * z, xz = x * z;
-      res = ((((res + (SH_C2_0 * xy) * sh[12]) + (SH_C2_1 * yz) * sh[15]) +
-              (SH_C2_2 * ((2.0f * zz - xx) - yy)) * sh[18]) +
-             (SH_C2_3 * xz) * sh[21]) +
-            (SH_C2_4 * (xx - yy)) * sh[24];
-      if (deg > 2) {
-        res = ((((((res + ((SH_C3_0 * y) * (3.0f * xx - yy)) * sh[27]) +
-                   ((SH_C3_1 * xy) * z) * sh[30]) +
-                  ((SH_C3_2 * y) * ((4.0f * zz - xx) - yy)) * sh[33]) +
-                 ((SH_C3_3 * z) * ((2.0f * zz - 3.0f * xx) - 3.0f * yy)) * sh[36]) +
-                ((SH_C3_4 * x) * ((4.0f * zz - xx) - yy)) * sh[39]) +
-               ((SH_C3_5 * z) * (xx - yy)) * sh[42]) +
-              ((SH_C3_6 * x) * (xx - 3.0f * yy)) * sh[45];
+      res = ((((res + (SH_C2_0 * xy) * sh[12 + c]) + (SH_C2_1 * yz) * sh[15 + c]) +
+              (SH_C2_2 * ((2.0f * zz - xx) - yy)) * sh[18 + c]) +
+             (SH_C2_3 * xz) * sh[21 + c]) +
+            (SH_C2_4 * (xx - yy)) * sh[24 + c];
+      if (DEG > 2) {
+        res = ((((((res + ((SH_C3_0 * y) * (3.0f * xx - yy)) * sh[27 + c]) +
+                   ((SH_C3_1 * xy) * z) * sh[30 + c]) +
+                  ((SH_C3_2 * y) * ((4.0f * zz - xx) - yy)) * sh[33 + c]) +
+                 ((SH_C3_3 * z) * ((2.0f * zz - 3.0f * xx) - 3.0f * yy)) * sh[36 + c]) +
+                ((SH_C3_4 * x) * ((4.0f * zz - xx) - yy)) * sh[39 + c]) +
+               ((SH_C3_5 * z) * (xx - yy)) * sh[42 + c]) +
+              ((SH_C3_6 * x) * (xx - 3.0f * yy)) * sh[45 + c];
       }
     }
   }
@@ -155,8 +176,9 @@ __device__ inline void write_record(float* __restrict__ rec, float m2x, float m2
   r4[2] = make_float4(col[2], 0.0f, 0.0f, 0.0f);
 }
 
+template <int DEG>
 __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
-    int64_t n, int K, int deg, const float* __restrict__ means, const float* __restrict__ scales,
+    int64_t n, int K, const float* __restrict__ means, const float* __restrict__ scales,
     const float* __restrict__ quats, const float* __restrict__ opac, const float* __restrict__ sh,
     const uint8_t* __restrict__ mask, const float* __restrict__ w2c, float fx, float fy, float cx,
     float cy, float* __restrict__ means2d, float* __restrict__ cov2d, float* __restrict__ radii,
@@ -186,11 +208,13 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
   // renderer.py:40-49
   float vv[3], nrm, d[3];
   view_dir(w, mx, my, mz, vv, nrm, d);
+  constexpr int NB = (DEG + 1) * (DEG + 1);
+  float shv[3 * NB];
+  load_sh<NB>(sh + (int64_t)i * K * 3, K, shv);
   float col[3];
-  const float* shi = sh + (int64_t)i * K * 3;
 #pragma unroll
   for (int c = 0; c < 3; ++c) {
-    const float res = eval_sh_channel(deg, shi + c, d) + 0.5f;
+    const float res = eval_sh_channel<DEG>(shv, c, d) + 0.5f;
     col[c] = jmin(1.0f, jmax(0.0f, res));
   }
   means2d[2 * i] = m2x;
@@ -217,10 +241,13 @@ __global__ __launch_bounds__(256) void composite_prep_kernel(int64_t n, const fl
   write_record(records + i * kRec, means2d[2 * i], means2d[2 * i + 1], c.x, c.y, c.w, opac[i], col);
 }
 
-// d basis_k / d(x,y,z) of the degree<=3 real SH basis used by eval_sh_channel.
-__device__ inline void sh_basis_and_grad(int deg, const float* d, float* B, float (*dB)[3]) {
+// basis_k and d basis_k / d(x,y,z) of the degree<=3 real SH basis of eval_sh_channel.
+template <int DEG>
+__device__ inline void sh_basis_and_grad(const float* d, float* B, float (*dB)[3]) {
+  constexpr int deg = DEG;
   const float x = d[0], y = d[1], z = d[2];
   const float xx = x * x, yy = y * y, zz = z * z;
+#pragma unroll
   for (int k = 0; k < 16; ++k) {
     B[k] = 0.0f;
     dB[k][0] = dB[k][1] = dB[k][2] = 0.0f;
@@ -260,8 +287,9 @@ __device__ inline void sh_basis_and_grad(int deg, const float* d, float* B, floa
   }
 }
 
+template <int DEG>
 __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
-    int64_t n, int K, int deg, const float* __restrict__ means, const float* __restrict__ scales,
+    int64_t n, int K, const float* __restrict__ means, const float* __restrict__ scales,
     const float* __restrict__ quats, const float* __restrict__ opac, const float* __restrict__ sh,
     const float* __restrict__ w2c, float fx, float fy, const float* __restrict__ grec,
     float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_quats,
@@ -353,36 +381,48 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
   // ---- colour: clip(SH + 0.5, 0, 1)
   float vv[3], nrm, d[3];
   view_dir(w, mx, my, mz, vv, nrm, d);
-  const float* shi = sh + (int64_t)i * K * 3;
+  constexpr int NB = (DEG + 1) * (DEG + 1);
+  float shv[3 * NB];
+  load_sh<NB>(sh + (int64_t)i * K * 3, K, shv);
   float g_pre[3];
 #pragma unroll
   for (int c = 0; c < 3; ++c) {
-    const float pre = eval_sh_channel(deg, shi + c, d) + 0.5f;
+    const float pre = eval_sh_channel<DEG>(shv, c, d) + 0.5f;
     const float lo = jmax(0.0f, pre);
     g_pre[c] = g_col[c] * dmin_first(lo, 1.0f) * dmax_first(pre, 0.0f);
   }
   float B[16], dB[16][3];
-  sh_basis_and_grad(deg, d, B, dB);
-  const int nb = (deg + 1) * (deg + 1);
+  sh_basis_and_grad<DEG>(d, B, dB);
   float g_d[3] = {0.0f, 0.0f, 0.0f};
-  float* gsh = g_sh + (int64_t)i * K * 3;
-  for (int k = 0; k < K; ++k) {
-    if (k < nb) {
-      const float s0 = shi[3 * k], s1 = shi[3 * k + 1], s2 = shi[3 * k + 2];
-      gsh[3 * k] = B[k] * g_pre[0];
-      gsh[3 * k + 1] = B[k] * g_pre[1];
-      gsh[3 * k + 2] = B[k] * g_pre[2];
-      const float sk = (s0 * g_pre[0] + s1 * g_pre[1]) + s2 * g_pre[2];
+  float gshv[48];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    if (k < NB) {
+      gshv[3 * k] = B[k] * g_pre[0];
+      gshv[3 * k + 1] = B[k] * g_pre[1];
+      gshv[3 * k + 2] = B[k] * g_pre[2];
+      const float sk = (shv[3 * k] * g_pre[0] + shv[3 * k + 1] * g_pre[1]) + shv[3 * k + 2] * g_pre[2];
       g_d[0] += sk * dB[k][0];
       g_d[1] += sk * dB[k][1];
       g_d[2] += sk * dB[k][2];
     } else {
-      gsh[3 * k] = 0.0f;
-      gsh[3 * k + 1] = 0.0f;
-      gsh[3 * k + 2] = 0.0f;
+      gshv[3 * k] = gshv[3 * k + 1] = gshv[3 * k + 2] = 0.0f;
     }
   }
-  if (deg > 0) {
+  // the whole row of K triples is written (coefficients >= NB get 0)
+  float* gsh = g_sh + (int64_t)i * K * 3;
+  if ((K & 3) == 0) {
+    float4* g4 = reinterpret_cast<float4*>(gsh);
+    const int nq = 3 * K / 4;
+#pragma unroll
+    for (int q = 0; q < 12; ++q)
+      if (q < nq) g4[q] = make_float4(gshv[4 * q], gshv[4 * q + 1], gshv[4 * q + 2], gshv[4 * q + 3]);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 48; ++q)
+      if (q < 3 * K) gsh[q] = gshv[q];
+  }
+  if (DEG > 0) {
     const float dg = (d[0] * g_d[0] + d[1] * g_d[1]) + d[2] * g_d[2];
 #pragma unroll
     for (int k = 0; k < 3; ++k) g_m[k] += (g_d[k] - d[k] * dg) / nrm;
@@ -481,9 +521,17 @@ extern "C" int gs_preprocess_fwd(void* stream, int64_t n, int sh_k, int sh_degre
              "gs_preprocess_fwd: NULL array argument");
   (void)width;
   (void)height;
-  hipLaunchKernelGGL(preprocess_fwd_kernel, dim3(div_up(n, 256)), dim3(256), 0, (hipStream_t)stream, n,
-                     sh_k, sh_degree, means, scales, quats, opacities, sh_coeffs, mask, w2c, fx, fy, cx,
-                     cy, means2d, cov2d, radii, valid, depths, colors, records);
+#define GS_PRE_FWD(D)                                                                                          \
+  hipLaunchKernelGGL(preprocess_fwd_kernel<D>, dim3(div_up(n, 256)), dim3(256), 0, (hipStream_t)stream, n, sh_k,  \
+                     means, scales, quats, opacities, sh_coeffs, mask, w2c, fx, fy, cx, cy, means2d, cov2d, radii, \
+                     valid, depths, colors, records)
+  switch (sh_degree) {
+    case 0: GS_PRE_FWD(0); break;
+    case 1: GS_PRE_FWD(1); break;
+    case 2: GS_PRE_FWD(2); break;
+    default: GS_PRE_FWD(3); break;
+  }
+#undef GS_PRE_FWD
   GS_LAUNCH_CHECK("preprocess_fwd_kernel");
   return GS_OK;
 }
@@ -518,9 +566,17 @@ extern "C" int gs_preprocess_bwd(void* stream, int64_t n, int sh_k, int sh_degre
   (void)height;
   (void)cx;
   (void)cy;
-  hipLaunchKernelGGL(preprocess_bwd_kernel, dim3(div_up(n, 256)), dim3(256), 0, (hipStream_t)stream, n,
-                     sh_k, sh_degree, means, scales, quats, opacities, sh_coeffs, w2c, fx, fy,
-                     grad_records, grad_means, grad_scales, grad_quats, grad_opacities, grad_sh);
+#define GS_PRE_BWD(D)                                                                                          \
+  hipLaunchKernelGGL(preprocess_bwd_kernel<D>, dim3(div_up(n, 256)), dim3(256), 0, (hipStream_t)stream, n, sh_k,  \
+                     means, scales, quats, opacities, sh_coeffs, w2c, fx, fy, grad_records, grad_means, grad_scales, \
+                     grad_quats, grad_opacities, grad_sh)
+  switch (sh_degree) {
+    case 0: GS_PRE_BWD(0); break;
+    case 1: GS_PRE_BWD(1); break;
+    case 2: GS_PRE_BWD(2); break;
+    default: GS_PRE_BWD(3); break;
+  }
+#undef GS_PRE_BWD
   GS_LAUNCH_CHECK("preprocess_bwd_kernel");
   return GS_OK;
 }
