@@ -20,9 +20,10 @@
 // Backward: replays each pixel back to front from (final T, n_contrib), recovering
 // T_k = T_{k+1} / (1 - alpha_k) and the colour behind entry k,
 // R_{k-1} = alpha_k c_k + (1 - alpha_k) R_k.  The 9 gradient terms of an entry are
-// summed over the lane's pixels, reduced across the wave with DPP row shifts and row
-// broadcasts, and added to the Gaussian's gradient record with one atomic
-// instruction (9 lanes).  Gradients follow JAX autodiff of the reference: the cap
+// summed over the lane's pixels, reduce-scattered across the wave (recursive halving,
+// so lane c ends with the total of term c) and added to the Gaussian's gradient
+// record with one atomic instruction (9 lanes).  Gradients follow JAX autodiff of the
+// reference: the cap
 // min(0.99, .) passes no gradient when it binds (half at a tie), gated entries pass
 // none.
 #include "gs_common.h"
@@ -54,6 +55,59 @@ __device__ inline float wave_sum(float v) {
   x = dpp_add(x, __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xA, 0xF, false));
   x = dpp_add(x, __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xC, 0xF, false));
   return bcast(x, 63);
+}
+
+// Reduce-scatter of 9 per-lane values over the wave by recursive halving: at level
+// k a lane keeps the half of its values whose index bit k equals its own lane bit k
+// and adds the partner's copy of them (partner = lane ^ 2^k: DPP quad_perm for
+// 1 and 2, ds_swizzle for 4, 8, 16, ds_bpermute for 32).  Afterwards lane L holds
+// the wave total of value L % 16 (values 9..15 are zero padding).
+__device__ inline float swz_xor(float v, int pattern_xor) {
+  // ds_swizzle bit mode: and_mask 0x1F, or_mask 0, xor_mask in bits 14:10
+  switch (pattern_xor) {
+    case 4: return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (4 << 10) | 0x1F));
+    case 8: return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (8 << 10) | 0x1F));
+    default: return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (16 << 10) | 0x1F));
+  }
+}
+
+__device__ inline float reduce_scatter9(const float* v, int lane) {
+  const bool b0 = lane & 1, b1 = lane & 2, b2 = lane & 4, b3 = lane & 8;
+  float y[5], z[3], r[2];
+  // level 0: xor 1 (quad_perm [1,0,3,2])
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    const float lo = v[2 * k];
+    const float hi = (2 * k + 1 < 9) ? v[2 * k + 1] : 0.0f;
+    const float keep = b0 ? hi : lo, send = b0 ? lo : hi;
+    y[k] = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0xB1, 0xF, 0xF, false));
+  }
+  // level 1: xor 2 (quad_perm [2,3,0,1])
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    const float lo = y[2 * m];
+    const float hi = (2 * m + 1 < 5) ? y[2 * m + 1] : 0.0f;
+    const float keep = b1 ? hi : lo, send = b1 ? lo : hi;
+    z[m] = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x4E, 0xF, 0xF, false));
+  }
+  // level 2: xor 4
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const float lo = z[2 * q];
+    const float hi = (2 * q + 1 < 3) ? z[2 * q + 1] : 0.0f;
+    const float keep = b2 ? hi : lo, send = b2 ? lo : hi;
+    r[q] = keep + swz_xor(send, 4);
+  }
+  // level 3: xor 8
+  float t;
+  {
+    const float keep = b3 ? r[1] : r[0], send = b3 ? r[0] : r[1];
+    t = keep + swz_xor(send, 8);
+  }
+  // levels 4, 5: full sums across the 16-lane rows
+  t = t + swz_xor(t, 16);
+  t = t + __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __float_as_int(t)));
+  return t;
 }
 
 // XCD-aware tile order: consecutive workgroups go round-robin to the 8 XCDs, so
@@ -312,12 +366,7 @@ __global__ __launch_bounds__(64) void composite_bwd_kernel(
         }
       }
       if (__ballot(any) != 0ull) {
-        float s[9];
-#pragma unroll
-        for (int c = 0; c < 9; ++c) s[c] = wave_sum(v[c]);
-        float mine = s[0];
-#pragma unroll
-        for (int c = 1; c < 9; ++c) mine = lane == c ? s[c] : mine;
+        const float mine = reduce_scatter9(v, lane);
         const int g = bcast_i(gcur, j);
         if (lane < 9 && mine != 0.0f) atomicAdd(&grec[(int64_t)g * kRec + lane], mine);
       }
