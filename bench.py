@@ -24,7 +24,9 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 FP32_PEAK_TFLOPS = 157.3  # MI355X FP32 (vector) peak
-COMPOSITE_FWD_FLOP_PER_PAIR = 22  # ~22 FLOP + 1 exp per evaluated pair
+COMPOSITE_FWD_FLOP_PER_PAIR = 22  # ~22 FLOP + 1 exp per evaluated (pixel, entry) pair
+COMPOSITE_BWD_FLOP_PER_PAIR = 55  # ~2.5x the forward per pair
+TRAFFIC_FILE = os.path.join(_ROOT, "profiles", "hbm_traffic_cfg2.md")
 
 
 def parse():
@@ -36,6 +38,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-band", type=int, default=8, help="CPU sample = top 1/band of the image rows")
     ap.add_argument("--stages", action="store_true", help="print per-stage timings to stderr")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="finish with a plain 256 MiB device copy (PMC byte-counter calibration)")
     return ap.parse_args()
 
 
@@ -125,29 +129,42 @@ def main():
         stage_ms[nm] = float(np.median([a[r].elapsed_time(z[r]) for r in range(reps)]))
     K = g.sh_coeffs.shape[1]
     nb = (D + 1) ** 2
+    # Algorithmic bytes per launch (what each stage must move at minimum):
+    #   preprocess fwd: read means 12 + scales 12 + quats 16 + opacity 4 + (D+1)^2 SH triples
+    #                   12 each; write means2d 8, cov2d 16, radius 4, valid 1, depth 4,
+    #                   colour 12, compositing record 48.
+    #   preprocess bwd: the same inputs + gradient record 48; write 5 gradient arrays
+    #                   (12 + 12 + 16 + 4 + 12 K).
     pre_fwd_bytes = N * (44 + 12 * nb) + N * (8 + 16 + 4 + 1 + 4 + 12 + 48)
     pre_bwd_bytes = N * (44 + 12 * nb) + N * 48 + N * (12 + 12 + 16 + 4 + 12 * K)
     stage_gbs = {"preprocess_fwd": pre_fwd_bytes / (stage_ms["preprocess_fwd"] * 1e-3) / 1e9,
                  "preprocess_bwd": pre_bwd_bytes / (stage_ms["preprocess_bwd"] * 1e-3) / 1e9}
+    # Compositing is VALU-bound; its unit of work is an evaluated (pixel, entry) pair,
+    # i.e. sum over pixels of n_contrib, at ~22 FLOP forward and ~55 FLOP backward.
+    pairs = int(nc.to(torch.int64).sum())
+    stage_tflops = {"composite_fwd": pairs * COMPOSITE_FWD_FLOP_PER_PAIR / (stage_ms["composite_fwd"] * 1e-3) / 1e12,
+                    "composite_bwd": pairs * COMPOSITE_BWD_FLOP_PER_PAIR / (stage_ms["composite_bwd"] * 1e-3) / 1e12}
     dominant = max(stage_ms, key=stage_ms.get)
     if args.stages:
-        print(json.dumps({"stage_ms": stage_ms, "stage_GBps": stage_gbs, "n_interactions": n_int}), file=sys.stderr)
+        print(json.dumps({"stage_ms": stage_ms, "stage_GBps": stage_gbs, "stage_TFLOPs": stage_tflops,
+                          "n_interactions": n_int, "pairs": pairs}), file=sys.stderr)
 
-    # Roofline of the dominant kernel.  Compositing is VALU-bound: algorithmic work is
-    # pair evaluations (Σ over pixels of entries visited), ~22 FLOP each forward.
-    roofline = None
-    if dominant in ("preprocess_fwd", "preprocess_bwd"):
-        byt = pre_fwd_bytes if dominant == "preprocess_fwd" else pre_bwd_bytes
-        ach = byt / (stage_ms[dominant] * 1e-3) / 1e9
+    if dominant in stage_gbs:
+        ach = stage_gbs[dominant]
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": ach / HBM_PEAK_GBS, "traffic": None}
+                    "frac": ach / HBM_PEAK_GBS, "traffic": measured_traffic(dominant)}
     else:
-        nc_sum = int(nc.to(torch.int64).sum())
-        flop = nc_sum * COMPOSITE_FWD_FLOP_PER_PAIR
-        ach = flop / (stage_ms["composite_fwd"] * 1e-3) / 1e12
-        roofline = {"kernel": "composite_fwd", "bound": "valu", "achieved": ach, "peak": FP32_PEAK_TFLOPS,
-                    "unit": "TFLOP/s", "frac": ach / FP32_PEAK_TFLOPS, "traffic": None,
-                    "pairs": nc_sum}
+        ach = stage_tflops.get(dominant, 0.0)
+        roofline = {"kernel": dominant, "bound": "valu", "achieved": ach, "peak": FP32_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": ach / FP32_PEAK_TFLOPS, "traffic": measured_traffic(dominant),
+                    "pairs": pairs}
+
+    if args.copy_calibration:
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
 
     cpu = None
     if not args.no_cpu:
@@ -170,10 +187,26 @@ def main():
         "config": {"workload": sc["name"] + " fwd+L1+bwd", "gaussians": N, "width": cam.W, "height": cam.H,
                    "sh_degree": D, "n_interactions": n_int, "gaussians_per_s": N / dt},
         "stage_ms": stage_ms,
+        "stage_GBps": stage_gbs,
+        "stage_TFLOPs": stage_tflops,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE scaled by the copy-kernel calibration), else None."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        if line.startswith("| " + kernel + " |"):
+            try:
+                return float(line.split("|")[-2].strip())
+            except ValueError:
+                return None
+    return None
 
 
 def cpu_baseline(sc, band):

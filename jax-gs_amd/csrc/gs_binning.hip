@@ -8,26 +8,30 @@
 // order without sorting the entries themselves:
 //
 //   1. bin_prep        per Gaussian: tile rectangle (clipped to 16x16 tiles) and depth
-//                      bucket; per-block counts of radius-cap violations and negative
-//                      depths (no same-address atomics).
-//   2. depth sort      stable LSD radix sort of the N Gaussian ids by depth bucket
-//                      (two 7-bit passes)            -> Gaussians in (bucket, id) order.
+//                      bucket, packed with the id into one 64-bit word; per-block
+//                      counts of radius-cap violations and negative depths; histogram
+//                      of the first radix digit of the bucket.
+//   2. depth sort      stable LSD radix sort of the packed words by depth bucket (two
+//                      7-bit passes)  -> Gaussians in (bucket, id) order.
 //   3. superblocks     every Gaussian meets at most 5x5 "superblocks" of 4x4 tiles;
-//                      its (superblock, id) pairs are written in depth order and
-//                      stably sorted by superblock (two 7-bit passes) -> per superblock
-//                      the list of Gaussians touching it, in (bucket, id) order.
+//                      its (superblock, packed word) pairs are written in depth order
+//                      and stably sorted by superblock (two 7-bit passes) -> per
+//                      superblock the list of Gaussians touching it, in (bucket, id)
+//                      order.  Carrying the rectangle in the sorted word keeps every
+//                      later read coalesced.
 //   4. tile pass       a superblock's list is cut into chunks of 256 Gaussians; a wave
-//                      takes a chunk 64 Gaussians at a time, forms 4 column and 4 row
-//                      lane masks with ballots, and so knows for each of the 16 tiles
-//                      which lanes hit it.  A counting sweep gives per (chunk, tile)
-//                      counts, a scan over tiles gives the tile ranges and per-chunk
-//                      offsets, and a writing sweep stores each entry's Gaussian id at
-//                      offset + popcount(mask & lanes-below) -- stable by construction.
-//   5. stats           the renderer's health extras from the ranges.
+//                      takes a chunk 64 Gaussians at a time and forms 4 column and 4
+//                      row lane masks with ballots, so for each of the 16 tiles it
+//                      knows which lanes hit it.  A counting sweep gives per (chunk,
+//                      tile) counts and tile totals, one scan gives the tile ranges,
+//                      and a writing sweep stores each entry's id at
+//                      range + counts of earlier chunks + popcount(mask & lanes-below)
+//                      -- stable by construction.
+//   5. stats           the renderer's health extras, computed with the range scan.
 //
-// Radix passes use one wave per workgroup and a fixed grid of G workgroups that each
-// own a contiguous key range, so stability only needs an in-wave rank: lanes with
-// equal digits are found with ballots ("match any") and ranked by lane order.
+// Radix passes use one wave per workgroup over a contiguous key range (in-wave rank
+// with ballot "match any"), a per-digit spine scan across workgroups, and no
+// inter-workgroup waiting.  There are no same-address atomics.
 #include "gs_common.h"
 
 #include <algorithm>
@@ -45,73 +49,97 @@ constexpr int kSB = 4;                              // superblock = 4x4 tiles
 constexpr int kSBMax = 5 * 5;                       // superblocks one Gaussian can meet
 constexpr int kChunk = 256;                         // Gaussians per chunk of the tile pass
 constexpr int kPrepBlock = 256;
+constexpr int kPrepPer = 4;                         // Gaussians per bin_prep thread
+constexpr int kPrepSpan = kPrepBlock * kPrepPer;    // = depth-sort workgroup range
+constexpr int kBig = 1024;                          // single-block scan kernels
 
 __device__ inline uint64_t lanemask_lt() {
   const unsigned lane = threadIdx.x & 63;
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
-// rect.x = tminx | tminy << 16, rect.y = w | h << 8 (w, h <= 16; 0 when invalid)
-__device__ inline void unpack_rect(uint2 rc, int& x0, int& y0, int& w, int& h) {
-  x0 = rc.x & 0xFFFF;
-  y0 = rc.x >> 16;
-  w = rc.y & 0xFF;
-  h = (rc.y >> 8) & 0xFF;
+// Packed Gaussian word: id (26 bits) | tminx (12) | tminy (12) | w-1 (4) | h-1 (4) |
+// has-entries (1).
+struct Packed {
+  uint32_t gid;
+  int x0, y0, w, h;  // w = h = 0 when the Gaussian meets no tile
+};
+__device__ inline uint64_t pack(uint32_t gid, int x0, int y0, int w, int h) {
+  uint64_t v = gid;
+  if (w > 0 && h > 0)
+    v |= ((uint64_t)x0 << 26) | ((uint64_t)y0 << 38) | ((uint64_t)(w - 1) << 50) | ((uint64_t)(h - 1) << 54) |
+         (1ull << 58);
+  return v;
 }
-
-__device__ inline uint32_t sb_count(uint2 rc) {
-  int x0, y0, w, h;
-  unpack_rect(rc, x0, y0, w, h);
-  if (w == 0 || h == 0) return 0u;
-  const int nx = ((x0 + w - 1) >> 2) - (x0 >> 2) + 1;
-  const int ny = ((y0 + h - 1) >> 2) - (y0 >> 2) + 1;
+__device__ inline Packed unpack(uint64_t v) {
+  Packed p;
+  p.gid = (uint32_t)(v & 0x3FFFFFFull);
+  const bool has = (v >> 58) & 1;
+  p.x0 = (int)((v >> 26) & 0xFFF);
+  p.y0 = (int)((v >> 38) & 0xFFF);
+  p.w = has ? (int)((v >> 50) & 0xF) + 1 : 0;
+  p.h = has ? (int)((v >> 54) & 0xF) + 1 : 0;
+  return p;
+}
+__device__ inline uint32_t sb_count(const Packed& p) {
+  if (p.w == 0) return 0u;
+  const int nx = ((p.x0 + p.w - 1) >> 2) - (p.x0 >> 2) + 1;
+  const int ny = ((p.y0 + p.h - 1) >> 2) - (p.y0 >> 2) + 1;
   return (uint32_t)(nx * ny);
 }
 
 // ---------------------------------------------------------------------------------
 // 1. per-Gaussian rectangle and depth bucket (rasterizer.py:36-51, 84-94;
-//    renderer.py:63-75 for the radius-cap statistic).
+//    renderer.py:63-75 for the radius-cap statistic).  Block b handles Gaussians
+//    [b*1024, b*1024+1024), the same range as depth-sort workgroup b, and writes that
+//    workgroup's histogram of the first radix digit.
 __global__ __launch_bounds__(kPrepBlock) void bin_prep_kernel(int64_t n, const float* __restrict__ means2d,
                                                               const float* __restrict__ radii,
                                                               const uint8_t* __restrict__ valid,
-                                                              const float* __restrict__ depths, int W, int H,
-                                                              uint32_t* __restrict__ dkey, uint2* __restrict__ rect,
+                                                              const float* __restrict__ depths, int W, int H, int G,
+                                                              uint32_t* __restrict__ dkey, uint64_t* __restrict__ word,
+                                                              uint32_t* __restrict__ table,
                                                               uint32_t* __restrict__ blkstat) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  bool cap_violation = false, negative = false;
-  if (i < n) {
-    const float mx = means2d[2 * i], my = means2d[2 * i + 1], r = radii[i];
-    const float wm1 = (float)(W - 1), hm1 = (float)(H - 1);
-    const float minx = jmin(jmax(mx - r, 0.0f), wm1);
-    const float maxx = jmin(jmax(mx + r, 0.0f), wm1);
-    const float miny = jmin(jmax(my - r, 0.0f), hm1);
-    const float maxy = jmin(jmax(my + r, 0.0f), hm1);
-    // floor(x/16) of values in [0, W-1] (NaN only for Gaussians that are invalid).
-    const int tminx = (int)floorf(minx / 16.0f), tmaxx = (int)floorf(maxx / 16.0f);
-    const int tminy = (int)floorf(miny / 16.0f), tmaxy = (int)floorf(maxy / 16.0f);
-    const bool on_screen = (mx + r > 0.0f) && (mx - r < (float)W) && (my + r > 0.0f) && (my - r < (float)H);
-    const bool proj_valid = valid[i] != 0;
-    const bool v = proj_valid && on_screen && (tmaxx >= tminx) && (tmaxy >= tminy);
-    const int spanx = tmaxx - tminx + 1, spany = tmaxy - tminy + 1;
-    cap_violation = proj_valid && on_screen && (spanx > kOffset || spany > kOffset);
-    const uint32_t zb = float_to_bits(depths[i]);
-    negative = (zb >> 31) != 0;
-    uint32_t key = kDepthBinEmpty;
-    uint2 rc = make_uint2(0u, 0u);
-    if (v) {
-      const int w = spanx < kOffset ? spanx : kOffset;
-      const int h = spany < kOffset ? spany : kOffset;
-      // v implies depth > 0.01, so the 13-bit bucket is in [3848, 8191].
-      key = (zb >> (31 - kDepthBits)) - kDepthBucketLo;
-      rc.x = (uint32_t)tminx | ((uint32_t)tminy << 16);
-      rc.y = (uint32_t)w | ((uint32_t)h << 8);
-    }
-    dkey[i] = key;
-    rect[i] = rc;
-  }
+  __shared__ uint32_t hist[kRadixBins];
   __shared__ uint32_t wcnt[2][kPrepBlock / 64];
-  const uint32_t capc = (uint32_t)__popcll(__ballot(cap_violation));
-  const uint32_t negc = (uint32_t)__popcll(__ballot(negative));
+  for (int d = threadIdx.x; d < kRadixBins; d += kPrepBlock) hist[d] = 0;
+  __syncthreads();
+  uint32_t capc = 0, negc = 0;
+  for (int r = 0; r < kPrepPer; ++r) {
+    const int64_t i = (int64_t)blockIdx.x * kPrepSpan + r * kPrepBlock + threadIdx.x;
+    bool cap_violation = false, negative = false;
+    if (i < n) {
+      const float mx = means2d[2 * i], my = means2d[2 * i + 1], rr = radii[i];
+      const float wm1 = (float)(W - 1), hm1 = (float)(H - 1);
+      const float minx = jmin(jmax(mx - rr, 0.0f), wm1);
+      const float maxx = jmin(jmax(mx + rr, 0.0f), wm1);
+      const float miny = jmin(jmax(my - rr, 0.0f), hm1);
+      const float maxy = jmin(jmax(my + rr, 0.0f), hm1);
+      // floor(x/16) of values in [0, W-1] (NaN only for Gaussians that are invalid).
+      const int tminx = (int)floorf(minx / 16.0f), tmaxx = (int)floorf(maxx / 16.0f);
+      const int tminy = (int)floorf(miny / 16.0f), tmaxy = (int)floorf(maxy / 16.0f);
+      const bool on_screen = (mx + rr > 0.0f) && (mx - rr < (float)W) && (my + rr > 0.0f) && (my - rr < (float)H);
+      const bool proj_valid = valid[i] != 0;
+      const bool v = proj_valid && on_screen && (tmaxx >= tminx) && (tmaxy >= tminy);
+      const int spanx = tmaxx - tminx + 1, spany = tmaxy - tminy + 1;
+      cap_violation = proj_valid && on_screen && (spanx > kOffset || spany > kOffset);
+      const uint32_t zb = float_to_bits(depths[i]);
+      negative = (zb >> 31) != 0;
+      uint32_t key = kDepthBinEmpty;
+      int w = 0, h = 0;
+      if (v) {
+        w = spanx < kOffset ? spanx : kOffset;
+        h = spany < kOffset ? spany : kOffset;
+        // v implies depth > 0.01, so the 13-bit bucket is in [3848, 8191].
+        key = (zb >> (31 - kDepthBits)) - kDepthBucketLo;
+      }
+      dkey[i] = key;
+      word[i] = pack((uint32_t)i, v ? tminx : 0, v ? tminy : 0, w, h);
+      atomicAdd(&hist[key & (kRadixBins - 1)], 1u);
+    }
+    capc += (uint32_t)__popcll(__ballot(cap_violation));
+    negc += (uint32_t)__popcll(__ballot(negative));
+  }
   if ((threadIdx.x & 63) == 0) {
     wcnt[0][threadIdx.x >> 6] = capc;
     wcnt[1][threadIdx.x >> 6] = negc;
@@ -122,6 +150,7 @@ __global__ __launch_bounds__(kPrepBlock) void bin_prep_kernel(int64_t n, const f
     for (int k = 0; k < kPrepBlock / 64; ++k) s += wcnt[threadIdx.x][k];
     blkstat[2 * (int64_t)blockIdx.x + threadIdx.x] = s;
   }
+  for (int d = threadIdx.x; d < kRadixBins; d += kPrepBlock) table[(int64_t)d * G + blockIdx.x] = hist[d];
 }
 
 // ---------------------------------------------------------------------------------
@@ -132,22 +161,8 @@ struct LoadPlain {
 };
 // Number of superblocks met by the Gaussian at depth-sorted position i.
 struct LoadSortedSB {
-  const uint32_t* order;
-  const uint2* rect;
-  int64_t n;
-  __device__ uint32_t operator()(int64_t i) const {
-    const uint32_t g = order[i];
-    if ((int64_t)g >= n) return 0u;  // unreachable for a permutation; keeps reads in bounds
-    return sb_count(rect[g]);
-  }
-};
-// Number of chunks of superblock i's list.
-struct LoadChunks {
-  const int32_t* sb_ranges;
-  __device__ uint32_t operator()(int64_t i) const {
-    const int len = sb_ranges[i + 1] - sb_ranges[i];
-    return (uint32_t)((len + kChunk - 1) / kChunk);
-  }
+  const uint64_t* word;
+  __device__ uint32_t operator()(int64_t i) const { return sb_count(unpack(word[i])); }
 };
 
 __device__ inline uint32_t wave_incl_scan(uint32_t v) {
@@ -160,17 +175,19 @@ __device__ inline uint32_t wave_incl_scan(uint32_t v) {
   return v;
 }
 
-// Exclusive scan of one value per thread over a 256-thread block; the block total
+// Exclusive scan of one value per thread over a block of NT threads; the block total
 // is returned through *total.
+template <int NT>
 __device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t* total) {
-  __shared__ uint32_t wsum[4];
+  constexpr int NW = NT / 64;
+  __shared__ uint32_t wsum[NW];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const uint32_t inc = wave_incl_scan(v);
   if (lane == 63) wsum[wid] = inc;
   __syncthreads();
   uint32_t wbase = 0, tot = 0;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < NW; ++k) {
     if (k < wid) wbase += wsum[k];
     tot += wsum[k];
   }
@@ -190,7 +207,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_reduce_kernel(Load load, int6
     if (i < n) s += load(i);
   }
   uint32_t tot;
-  block_excl_scan(s, &tot);
+  block_excl_scan<kScanBlock>(s, &tot);
   if (threadIdx.x == 0) partial[blockIdx.x] = tot;
 }
 
@@ -204,7 +221,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_partials_kernel(uint32_t* __r
     const int i = b0 + threadIdx.x;
     const uint32_t v = i < nb ? partial[i] : 0u;
     uint32_t tot;
-    const uint32_t ex = block_excl_scan(v, &tot);
+    const uint32_t ex = block_excl_scan<kScanBlock>(v, &tot);
     const uint32_t c = carry;
     if (i < nb) partial[i] = c + ex;
     __syncthreads();
@@ -216,10 +233,11 @@ __global__ __launch_bounds__(kScanBlock) void scan_partials_kernel(uint32_t* __r
 
 // Blocked layout: thread t owns elements [t*16, t*16+16) of the block's tile, so the
 // per-thread sums compose into an exclusive scan in element order.  out[n] receives
-// the grand total when write_total is set (out has n+1 elements then).
-template <class Load, class Out>
+// the grand total when total is given (out has n+1 elements then).
+template <class Load>
 __global__ __launch_bounds__(kScanBlock) void scan_down_kernel(Load load, int64_t n,
-                                                               const uint32_t* __restrict__ partial, Out* out,
+                                                               const uint32_t* __restrict__ partial,
+                                                               uint32_t* __restrict__ out,
                                                                const uint32_t* __restrict__ total) {
   const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
   uint32_t v[kScanItems];
@@ -231,29 +249,32 @@ __global__ __launch_bounds__(kScanBlock) void scan_down_kernel(Load load, int64_
     s += v[k];
   }
   uint32_t tot;
-  uint32_t run = partial[blockIdx.x] + block_excl_scan(s, &tot);
+  uint32_t run = partial[blockIdx.x] + block_excl_scan<kScanBlock>(s, &tot);
 #pragma unroll
   for (int k = 0; k < kScanItems; ++k) {
     const int64_t i = base + k;
-    if (i < n) out[i] = (Out)run;
+    if (i < n) out[i] = run;
     run += v[k];
   }
-  if (total != nullptr && blockIdx.x == 0 && threadIdx.x == 0) out[n] = (Out)(*total);
+  if (total != nullptr && blockIdx.x == 0 && threadIdx.x == 0) out[n] = *total;
 }
 
 // ---------------------------------------------------------------------------------
-// Stable LSD radix pass on a 7-bit digit at `shift`.  Grid = G single-wave
-// workgroups; workgroup g owns keys [g*chunk, min(n,(g+1)*chunk)).  n is
-// min(*n_dev, cap) when n_dev is given (device-resident count), else n_static.
-__device__ inline void pass_range(const uint32_t* n_dev, int64_t n_static, int64_t cap, int G,
+// Stable LSD radix pass on a 7-bit digit at `shift`, keys u32 + values u64.
+// Workgroup g (one wave) owns keys [g*chunk, min(n,(g+1)*chunk)); chunk is fixed when
+// given, else derived from G.  n is min(*n_dev, cap) when n_dev is given.
+__device__ inline void pass_range(const uint32_t* n_dev, int64_t n_static, int64_t cap, int G, int fixed_chunk,
                                   int64_t& begin, int64_t& end, int64_t* n_out = nullptr) {
   int64_t n = n_static;
   if (n_dev != nullptr) {
     n = (int64_t)(*n_dev);
     if (n > cap) n = cap;
   }
-  int64_t chunk = (n + G - 1) / G;
-  chunk = (chunk + 63) & ~(int64_t)63;
+  int64_t chunk = fixed_chunk;
+  if (chunk == 0) {
+    chunk = (n + G - 1) / G;
+    chunk = (chunk + 63) & ~(int64_t)63;
+  }
   begin = (int64_t)blockIdx.x * chunk;
   end = begin + chunk;
   if (end > n) end = n;
@@ -262,40 +283,70 @@ __device__ inline void pass_range(const uint32_t* n_dev, int64_t n_static, int64
 
 __global__ __launch_bounds__(64) void radix_upsweep_kernel(const uint32_t* __restrict__ keys,
                                                            const uint32_t* __restrict__ n_dev,
-                                                           int64_t n_static, int64_t cap, int shift,
-                                                           int G, uint32_t* __restrict__ table) {
+                                                           int64_t n_static, int64_t cap, int shift, int G,
+                                                           int fixed_chunk, uint32_t* __restrict__ table) {
   __shared__ uint32_t hist[kRadixBins];
   const int lane = threadIdx.x;
   for (int d = lane; d < kRadixBins; d += 64) hist[d] = 0;
   __syncthreads();
   int64_t begin, end;
-  pass_range(n_dev, n_static, cap, G, begin, end);
+  pass_range(n_dev, n_static, cap, G, fixed_chunk, begin, end);
   for (int64_t i = begin + lane; i < end; i += 64) atomicAdd(&hist[(keys[i] >> shift) & (kRadixBins - 1)], 1u);
   __syncthreads();
   for (int d = lane; d < kRadixBins; d += 64) table[(int64_t)d * G + blockIdx.x] = hist[d];
 }
 
+// One block per digit: exclusive scan of that digit's row of the table (over the G
+// workgroups) in place, and the digit's total.
+__global__ __launch_bounds__(kScanBlock) void radix_spine_kernel(uint32_t* __restrict__ table, int G,
+                                                                 uint32_t* __restrict__ digit_tot) {
+  const int d = blockIdx.x;
+  uint32_t* row = table + (int64_t)d * G;
+  const int per = (G + kScanBlock - 1) / kScanBlock;
+  const int b0 = threadIdx.x * per;
+  uint32_t s = 0;
+  for (int k = 0; k < per; ++k)
+    if (b0 + k < G) s += row[b0 + k];
+  uint32_t tot;
+  uint32_t run = block_excl_scan<kScanBlock>(s, &tot);
+  for (int k = 0; k < per; ++k)
+    if (b0 + k < G) {
+      const uint32_t v = row[b0 + k];
+      row[b0 + k] = run;
+      run += v;
+    }
+  if (threadIdx.x == 0) digit_tot[d] = tot;
+}
+
 constexpr int kUnroll = 4;
 
 __global__ __launch_bounds__(64) void radix_downsweep_kernel(
-    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
-    const uint32_t* __restrict__ n_dev, int64_t n_static, int64_t cap, int shift, int G,
-    const uint32_t* __restrict__ table, uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out) {
+    const uint32_t* __restrict__ keys_in, const uint64_t* __restrict__ vals_in, const uint32_t* __restrict__ n_dev,
+    int64_t n_static, int64_t cap, int shift, int G, int fixed_chunk, const uint32_t* __restrict__ table,
+    const uint32_t* __restrict__ digit_tot, uint32_t* __restrict__ keys_out, uint64_t* __restrict__ vals_out) {
   __shared__ uint32_t cnt[kRadixBins];
   const int lane = threadIdx.x;
-  for (int d = lane; d < kRadixBins; d += 64) cnt[d] = table[(int64_t)d * G + blockIdx.x];
+  {
+    // digit bases: exclusive scan of the digit totals (2 digits per lane)
+    const uint32_t a = digit_tot[2 * lane], b = digit_tot[2 * lane + 1];
+    const uint32_t inc = wave_incl_scan(a + b);
+    const uint32_t base = inc - (a + b);
+    cnt[2 * lane] = base + table[(int64_t)(2 * lane) * G + blockIdx.x];
+    cnt[2 * lane + 1] = base + a + table[(int64_t)(2 * lane + 1) * G + blockIdx.x];
+  }
   __syncthreads();
   int64_t begin, end, n_pass;
-  pass_range(n_dev, n_static, cap, G, begin, end, &n_pass);
+  pass_range(n_dev, n_static, cap, G, fixed_chunk, begin, end, &n_pass);
   const uint64_t lt = lanemask_lt();
   for (int64_t base = begin; base < end; base += 64 * kUnroll) {
-    uint32_t k[kUnroll], v[kUnroll];
+    uint32_t k[kUnroll];
+    uint64_t v[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int64_t i = base + u * 64 + lane;
       const bool a = i < end;
       k[u] = a ? keys_in[i] : 0u;
-      v[u] = a ? (vals_in ? vals_in[i] : (uint32_t)i) : 0u;
+      v[u] = a ? vals_in[i] : 0ull;
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -304,10 +355,10 @@ __global__ __launch_bounds__(64) void radix_downsweep_kernel(
       const uint32_t d = (k[u] >> shift) & (kRadixBins - 1);
       uint64_t m = __ballot(a);
 #pragma unroll
-      for (int b = 0; b < kRadixBits; ++b) {
-        const bool bit = (d >> b) & 1u;
-        const uint64_t bb = __ballot(bit);
-        m &= bit ? bb : ~bb;
+      for (int bb = 0; bb < kRadixBits; ++bb) {
+        const bool bit = (d >> bb) & 1u;
+        const uint64_t bm = __ballot(bit);
+        m &= bit ? bm : ~bm;
       }
       uint32_t dst = 0;
       if (a) {
@@ -319,7 +370,7 @@ __global__ __launch_bounds__(64) void radix_downsweep_kernel(
         if (before == 0) cnt[d] = base_d + (uint32_t)__popcll(m);
       }
       if (a && dst < (uint32_t)n_pass) {  // always true for a consistent table
-        if (keys_out) keys_out[dst] = k[u];
+        keys_out[dst] = k[u];
         vals_out[dst] = v[u];
       }
     }
@@ -327,24 +378,21 @@ __global__ __launch_bounds__(64) void radix_downsweep_kernel(
 }
 
 // ---------------------------------------------------------------------------------
-// 3. (superblock, id) pairs of the Gaussian at depth-sorted position p, at off[p].
-__global__ __launch_bounds__(256) void sb_pairs_kernel(int64_t n, const uint32_t* __restrict__ order,
-                                                       const uint2* __restrict__ rect,
+// 3. (superblock, word) pairs of the Gaussian at depth-sorted position p, at off[p].
+__global__ __launch_bounds__(256) void sb_pairs_kernel(int64_t n, const uint64_t* __restrict__ word,
                                                        const uint32_t* __restrict__ off, int64_t pcap, int SX,
-                                                       uint32_t* __restrict__ pkey, uint32_t* __restrict__ pval) {
+                                                       uint32_t* __restrict__ pkey, uint64_t* __restrict__ pval) {
   const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= n) return;
-  const uint32_t g = order[p];
-  if ((int64_t)g >= n) return;
-  int x0, y0, w, h;
-  unpack_rect(rect[g], x0, y0, w, h);
-  if (w == 0 || h == 0) return;
+  const uint64_t wv = word[p];
+  const Packed g = unpack(wv);
+  if (g.w == 0) return;
   int64_t o = off[p];
-  for (int sy = y0 >> 2; sy <= (y0 + h - 1) >> 2; ++sy)
-    for (int sx = x0 >> 2; sx <= (x0 + w - 1) >> 2; ++sx, ++o)
+  for (int sy = g.y0 >> 2; sy <= (g.y0 + g.h - 1) >> 2; ++sy)
+    for (int sx = g.x0 >> 2; sx <= (g.x0 + g.w - 1) >> 2; ++sx, ++o)
       if (o < pcap) {
         pkey[o] = (uint32_t)(sy * SX + sx);
-        pval[o] = g;
+        pval[o] = wv;
       }
 }
 
@@ -365,33 +413,57 @@ __global__ __launch_bounds__(256) void ranges_kernel(const uint32_t* __restrict_
   }
 }
 
-// chunk c of superblock s covers its list positions [c*256, c*256+256).
-__global__ __launch_bounds__(256) void chunk_map_kernel(int S, const uint32_t* __restrict__ chunk_base,
-                                                        int64_t cmax, uint32_t* __restrict__ chunk_sb) {
-  const int s = blockIdx.x * blockDim.x + threadIdx.x;
-  if (s >= S) return;
-  for (uint32_t c = chunk_base[s]; c < chunk_base[s + 1] && c < (uint64_t)cmax; ++c) chunk_sb[c] = (uint32_t)s;
+// One block: chunk count per superblock -> exclusive scan -> chunk_base[S+1] and
+// the chunk -> superblock map; also clears the tile totals.
+__global__ __launch_bounds__(kBig) void chunks_kernel(int S, const int32_t* __restrict__ sb_ranges, int64_t cmax,
+                                                      uint32_t* __restrict__ chunk_base,
+                                                      uint32_t* __restrict__ chunk_sb, uint32_t* __restrict__ n_chunks,
+                                                      int T, uint32_t* __restrict__ tot) {
+  for (int t = threadIdx.x; t < T; t += kBig) tot[t] = 0;
+  __shared__ uint32_t carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (int s0 = 0; s0 < S; s0 += kBig) {
+    const int s = s0 + threadIdx.x;
+    uint32_t nc = 0;
+    if (s < S) nc = (uint32_t)((sb_ranges[s + 1] - sb_ranges[s] + kChunk - 1) / kChunk);
+    uint32_t sum;
+    const uint32_t ex = block_excl_scan<kBig>(nc, &sum);
+    const uint32_t c0 = carry + ex;
+    if (s < S) {
+      chunk_base[s] = c0;
+      for (uint32_t c = c0; c < c0 + nc && (int64_t)c < cmax; ++c) chunk_sb[c] = (uint32_t)s;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) carry += sum;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    chunk_base[S] = carry;
+    *n_chunks = carry;
+  }
 }
 
-// One wave's view of a 64-Gaussian step of a chunk: lane masks of the 4 tile
-// columns and 4 tile rows of the superblock met by each lane's rectangle.
+// One wave's view of a 64-Gaussian step of a chunk: lane masks of the 4 tile columns
+// and 4 tile rows of the superblock met by each lane's rectangle.
 struct StepMasks {
   uint64_t col[kSB], row[kSB];
 };
 
-__device__ inline StepMasks step_masks(bool act, int x0, int y0, int w, int h, int sx, int sy) {
+__device__ inline StepMasks step_masks(bool act, const Packed& g, int sx, int sy) {
   StepMasks m;
 #pragma unroll
   for (int k = 0; k < kSB; ++k) {
     const int tx = sx * kSB + k, ty = sy * kSB + k;
-    m.col[k] = __ballot(act && x0 <= tx && tx < x0 + w);
-    m.row[k] = __ballot(act && y0 <= ty && ty < y0 + h);
+    m.col[k] = __ballot(act && g.x0 <= tx && tx < g.x0 + g.w);
+    m.row[k] = __ballot(act && g.y0 <= ty && ty < g.y0 + g.h);
   }
   return m;
 }
 
 struct ChunkSpan {
   int s, sx, sy;
+  uint32_t first;      // first chunk of the superblock
   int64_t begin, end;  // positions in the superblock-sorted pair list
 };
 
@@ -402,20 +474,34 @@ __device__ inline ChunkSpan chunk_span(uint32_t c, const uint32_t* __restrict__ 
   cs.s = min((int)chunk_sb[c], S - 1);
   cs.sx = cs.s % SX;
   cs.sy = cs.s / SX;
+  cs.first = chunk_base[cs.s];
   const int64_t lo = sb_ranges[cs.s], hi = sb_ranges[cs.s + 1];
-  cs.begin = lo + (int64_t)(c - chunk_base[cs.s]) * kChunk;
+  cs.begin = lo + (int64_t)(c - cs.first) * kChunk;
   cs.end = cs.begin + kChunk < hi ? cs.begin + kChunk : hi;
   return cs;
 }
 
-// 4a. counts per (chunk, tile of its superblock): cnt[c*16 + u], u = 4*(ty%4) + tx%4.
+// tile u of superblock (sx, sy), u = 4*(ty%4) + tx%4, or -1 outside the image
+__device__ inline int tile_of(int sx, int sy, int u, int TX, int TY) {
+  const int tx = sx * kSB + (u & 3), ty = sy * kSB + (u >> 2);
+  return (tx < TX && ty < TY) ? ty * TX + tx : -1;
+}
+
+__device__ inline uint64_t lane_tile_mask(const StepMasks& m, int lane) {
+  uint64_t mine = 0;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) mine = (lane == u) ? (m.col[u & 3] & m.row[u >> 2]) : mine;
+  return mine;
+}
+
+// 4a. counts per (chunk, tile of its superblock) -> cnt[c*16 + u]; tile totals by
+// atomics (one per chunk and tile, distinct chunks rarely share a tile).
 __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restrict__ n_chunks, int64_t cmax,
                                                          const uint32_t* __restrict__ chunk_sb,
                                                          const uint32_t* __restrict__ chunk_base,
                                                          const int32_t* __restrict__ sb_ranges, int S,
-                                                         const uint32_t* __restrict__ pval,
-                                                         const uint2* __restrict__ rect, uint32_t n_gauss,
-                                                         int SX, uint32_t* __restrict__ cnt) {
+                                                         const uint64_t* __restrict__ pval, int SX, int TX, int TY,
+                                                         uint32_t* __restrict__ cnt, uint32_t* __restrict__ tot) {
   const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
   const uint32_t C = (uint32_t)min<int64_t>((int64_t)*n_chunks, cmax);
@@ -424,64 +510,90 @@ __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restr
     uint32_t mycount = 0;  // lane u < 16 accumulates tile u
     for (int64_t base = cs.begin; base < cs.end; base += 64) {
       const int64_t q = base + lane;
-      bool act = q < cs.end;
-      int x0 = 0, y0 = 0, w = 0, h = 0;
-      const uint32_t g = act ? pval[q] : 0u;
-      act = act && g < n_gauss;  // ids are < n by construction; keeps reads in bounds
-      if (act) unpack_rect(rect[g], x0, y0, w, h);
-      const StepMasks m = step_masks(act, x0, y0, w, h, cs.sx, cs.sy);
-      uint64_t mine = 0;
-#pragma unroll
-      for (int u = 0; u < 16; ++u) mine = (lane == u) ? (m.col[u & 3] & m.row[u >> 2]) : mine;
-      mycount += (uint32_t)__popcll(mine);
+      const bool act = q < cs.end;
+      const Packed g = unpack(act ? pval[q] : 0ull);
+      const StepMasks m = step_masks(act, g, cs.sx, cs.sy);
+      mycount += (uint32_t)__popcll(lane_tile_mask(m, lane));
     }
-    if (lane < 16) cnt[(int64_t)c * 16 + lane] = mycount;
+    if (lane < 16) {
+      cnt[(int64_t)c * 16 + lane] = mycount;
+      const int t = tile_of(cs.sx, cs.sy, lane, TX, TY);
+      if (t >= 0 && mycount) atomicAdd(&tot[t], mycount);
+    }
   }
 }
 
-// 4b. per tile: total over the chunks of its superblock.
-__global__ __launch_bounds__(256) void tile_total_kernel(int T, int TX, int SX, int64_t cmax,
-                                                         const uint32_t* __restrict__ chunk_base,
-                                                         const uint32_t* __restrict__ cnt,
-                                                         uint32_t* __restrict__ tot) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= T) return;
-  const int tx = t % TX, ty = t / TX;
-  const int s = (ty >> 2) * SX + (tx >> 2), u = (ty & 3) * 4 + (tx & 3);
-  uint32_t acc = 0;
-  const uint32_t ce = (uint32_t)min<int64_t>(chunk_base[s + 1], cmax);
-  for (uint32_t c = chunk_base[s]; c < ce; ++c) acc += cnt[(int64_t)c * 16 + u];
-  tot[t] = acc;
-}
-
-// 4c. per tile: starting offset of each chunk's entries, in place of the counts.
-__global__ __launch_bounds__(256) void tile_offsets_kernel(int T, int TX, int SX, int64_t cmax,
-                                                           const uint32_t* __restrict__ chunk_base,
-                                                           const int32_t* __restrict__ ranges,
-                                                           uint32_t* __restrict__ cnt) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= T) return;
-  const int tx = t % TX, ty = t / TX;
-  const int s = (ty >> 2) * SX + (tx >> 2), u = (ty & 3) * 4 + (tx & 3);
-  uint32_t run = (uint32_t)ranges[t];
-  const uint32_t ce = (uint32_t)min<int64_t>(chunk_base[s + 1], cmax);
-  for (uint32_t c = chunk_base[s]; c < ce; ++c) {
-    const uint32_t k = cnt[(int64_t)c * 16 + u];
-    cnt[(int64_t)c * 16 + u] = run;
-    run += k;
+// 4b + 5. One block: ranges = exclusive scan of the tile totals, and the stats.
+__global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* __restrict__ tot, int T,
+                                                               const uint32_t* __restrict__ blkstat, int nblk,
+                                                               int64_t cap, int32_t* __restrict__ ranges,
+                                                               int32_t* __restrict__ stats) {
+  __shared__ uint32_t carry;
+  __shared__ int64_t red[7][kBig / 64];
+  if (threadIdx.x == 0) carry = 0;
+  int64_t acc[7] = {0, 0, 0, 0, 0, 0, 0};  // max, ovf tiles, ovf inter, trunc tiles, trunc inter, cap, neg
+  __syncthreads();
+  for (int t0 = 0; t0 < T; t0 += kBig) {
+    const int t = t0 + threadIdx.x;
+    const uint32_t c = t < T ? tot[t] : 0u;
+    uint32_t sum;
+    const uint32_t ex = block_excl_scan<kBig>(c, &sum);
+    if (t < T) ranges[t] = (int32_t)(carry + ex);
+    acc[0] = acc[0] > (int64_t)c ? acc[0] : (int64_t)c;
+    acc[1] += c > (uint32_t)kBlock;
+    acc[2] += c > (uint32_t)kBlock ? c - kBlock : 0;
+    acc[3] += c > (uint32_t)kMaxTileEntries;
+    acc[4] += c > (uint32_t)kMaxTileEntries ? c - kMaxTileEntries : 0;
+    __syncthreads();
+    if (threadIdx.x == 0) carry += sum;
+    __syncthreads();
+  }
+  for (int b = threadIdx.x; b < nblk; b += kBig) {
+    acc[5] += blkstat[2 * b];
+    acc[6] += blkstat[2 * b + 1];
+  }
+  // reduce the 7 accumulators over the block
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < 7; ++k) {
+    int64_t v = acc[k];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const int64_t w = __shfl_xor(v, o, 64);
+      v = k == 0 ? (v > w ? v : w) : v + w;
+    }
+    if (lane == 0) red[k][wid] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t r[7] = {0, 0, 0, 0, 0, 0, 0};
+    for (int w = 0; w < kBig / 64; ++w)
+      for (int k = 0; k < 7; ++k) r[k] = k == 0 ? (r[0] > red[0][w] ? r[0] : red[0][w]) : r[k] + red[k][w];
+    const int64_t m = carry;
+    ranges[T] = (int32_t)m;
+    for (int k = 0; k < GS_NUM_STATS; ++k) stats[k] = 0;
+    stats[GS_STAT_N_INTERACTIONS] = (int32_t)m;
+    stats[GS_STAT_MAX_PER_TILE] = (int32_t)r[0];
+    stats[GS_STAT_OVERFLOW_TILES] = (int32_t)r[1];
+    stats[GS_STAT_OVERFLOW_INTERACTIONS] = (int32_t)r[2];
+    stats[GS_STAT_TRUNCATED_TILES] = (int32_t)r[3];
+    stats[GS_STAT_TRUNCATED_INTERACTIONS] = (int32_t)r[4];
+    stats[GS_STAT_RADIUS_CAP_VIOLATIONS] = (int32_t)r[5];
+    stats[GS_STAT_NEGATIVE_DEPTH] = (int32_t)r[6];
+    stats[GS_STAT_CAPACITY_EXCEEDED] = m > cap ? 1 : 0;
   }
 }
 
-// 4d. write every entry: tile t's entries from chunk c start at off[c*16+u]; within a
-// step, lane L's entry in tile u is preceded by popcount(mask_u & lanes-below-L).
+// 4c. write every entry: tile t's entries from chunk c start at ranges[t] plus the
+// counts of the superblock's earlier chunks; within a step, lane L's entry in tile u
+// is preceded by popcount(mask_u & lanes-below-L).
 __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restrict__ n_chunks, int64_t cmax,
                                                          const uint32_t* __restrict__ chunk_sb,
                                                          const uint32_t* __restrict__ chunk_base,
                                                          const int32_t* __restrict__ sb_ranges, int S,
-                                                         const uint32_t* __restrict__ pval,
-                                                         const uint2* __restrict__ rect, uint32_t n_gauss,
-                                                         int SX, int TX, const uint32_t* __restrict__ off,
-                                                         int64_t cap,
+                                                         const uint64_t* __restrict__ pval, uint32_t n_gauss, int SX,
+                                                         int TX, int TY, const uint32_t* __restrict__ cnt,
+                                                         const int32_t* __restrict__ ranges, int64_t cap,
                                                          int32_t* __restrict__ out_gid,
                                                          int32_t* __restrict__ out_tile) {
   __shared__ uint64_t smask[4][16];
@@ -492,31 +604,32 @@ __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restr
   const uint64_t lt = lanemask_lt();
   for (uint32_t c = blockIdx.x * (blockDim.x / 64) + wid; c < C; c += nwaves) {
     const ChunkSpan cs = chunk_span(c, chunk_sb, chunk_base, sb_ranges, S, SX);
-    if (lane < 16) sbase[wid][lane] = off[(int64_t)c * 16 + lane];
+    if (lane < 16) {
+      const int t = tile_of(cs.sx, cs.sy, lane, TX, TY);
+      uint32_t b = t >= 0 ? (uint32_t)ranges[t] : 0u;
+      for (uint32_t c2 = cs.first; c2 < c; ++c2) b += cnt[(int64_t)c2 * 16 + lane];
+      sbase[wid][lane] = b;
+    }
     for (int64_t base = cs.begin; base < cs.end; base += 64) {
       const int64_t q = base + lane;
       bool act = q < cs.end;
-      int x0 = 0, y0 = 0, w = 0, h = 0;
-      const uint32_t g = act ? pval[q] : 0u;
-      act = act && g < n_gauss;  // ids are < n by construction; keeps reads in bounds
-      if (act) unpack_rect(rect[g], x0, y0, w, h);
-      const StepMasks m = step_masks(act, x0, y0, w, h, cs.sx, cs.sy);
-      uint64_t mine = 0;
-#pragma unroll
-      for (int u = 0; u < 16; ++u) mine = (lane == u) ? (m.col[u & 3] & m.row[u >> 2]) : mine;
+      const Packed g = unpack(act ? pval[q] : 0ull);
+      act = act && g.gid < n_gauss;  // ids are < n by construction
+      const StepMasks m = step_masks(act, g, cs.sx, cs.sy);
+      const uint64_t mine = lane_tile_mask(m, lane);
       if (lane < 16) smask[wid][lane] = mine;
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       if (act) {
-        const int ux0 = max(x0, cs.sx * kSB), ux1 = min(x0 + w, cs.sx * kSB + kSB);
-        const int uy0 = max(y0, cs.sy * kSB), uy1 = min(y0 + h, cs.sy * kSB + kSB);
+        const int ux0 = max(g.x0, cs.sx * kSB), ux1 = min(g.x0 + g.w, cs.sx * kSB + kSB);
+        const int uy0 = max(g.y0, cs.sy * kSB), uy1 = min(g.y0 + g.h, cs.sy * kSB + kSB);
         for (int ty = uy0; ty < uy1; ++ty)
           for (int tx = ux0; tx < ux1; ++tx) {
             const int u = (ty - cs.sy * kSB) * kSB + (tx - cs.sx * kSB);
             const int64_t dst = (int64_t)sbase[wid][u] + __popcll(smask[wid][u] & lt);
             if (dst < cap) {
-              out_gid[dst] = (int32_t)g;
+              out_gid[dst] = (int32_t)g.gid;
               if (out_tile) out_tile[dst] = ty * TX + tx;
             }
           }
@@ -527,56 +640,6 @@ __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restr
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-  }
-}
-
-// 5. renderer.py:76-89 from the tile ranges, plus the per-block prep counts.
-__global__ __launch_bounds__(256) void stats_kernel(const int32_t* __restrict__ ranges, int T,
-                                                    const uint32_t* __restrict__ blkstat, int nblk, int64_t cap,
-                                                    int32_t* __restrict__ stats) {
-  int mx = 0;
-  int64_t ot = 0, oi = 0, tt = 0, ti = 0, cv = 0, ng = 0;
-  for (int t = threadIdx.x; t < T; t += blockDim.x) {
-    const int c = ranges[t + 1] - ranges[t];
-    mx = max(mx, c);
-    ot += c > kBlock;
-    oi += c > kBlock ? c - kBlock : 0;
-    tt += c > kMaxTileEntries;
-    ti += c > kMaxTileEntries ? c - kMaxTileEntries : 0;
-  }
-  for (int b = threadIdx.x; b < nblk; b += blockDim.x) {
-    cv += blkstat[2 * b];
-    ng += blkstat[2 * b + 1];
-  }
-  __shared__ int64_t red[6][256];
-  __shared__ int rmax[256];
-  rmax[threadIdx.x] = mx;
-  red[0][threadIdx.x] = ot;
-  red[1][threadIdx.x] = oi;
-  red[2][threadIdx.x] = tt;
-  red[3][threadIdx.x] = ti;
-  red[4][threadIdx.x] = cv;
-  red[5][threadIdx.x] = ng;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if ((int)threadIdx.x < o) {
-      rmax[threadIdx.x] = max(rmax[threadIdx.x], rmax[threadIdx.x + o]);
-      for (int k = 0; k < 6; ++k) red[k][threadIdx.x] += red[k][threadIdx.x + o];
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    for (int k = 0; k < GS_NUM_STATS; ++k) stats[k] = 0;
-    const int64_t m = ranges[T];
-    stats[GS_STAT_N_INTERACTIONS] = (int32_t)m;
-    stats[GS_STAT_MAX_PER_TILE] = rmax[0];
-    stats[GS_STAT_OVERFLOW_TILES] = (int32_t)red[0][0];
-    stats[GS_STAT_OVERFLOW_INTERACTIONS] = (int32_t)red[1][0];
-    stats[GS_STAT_TRUNCATED_TILES] = (int32_t)red[2][0];
-    stats[GS_STAT_TRUNCATED_INTERACTIONS] = (int32_t)red[3][0];
-    stats[GS_STAT_RADIUS_CAP_VIOLATIONS] = (int32_t)red[4][0];
-    stats[GS_STAT_NEGATIVE_DEPTH] = (int32_t)red[5][0];
-    stats[GS_STAT_CAPACITY_EXCEEDED] = m > cap ? 1 : 0;
   }
 }
 
@@ -591,9 +654,8 @@ struct BinPlan {
   int T, TX, TY, SX, SY, S;
   int G_d, G_p;  // radix grids for the depth sort and the superblock sort
   int sb_passes;
-  int nblk_prep;
-  size_t o_dkey, o_rect, o_ka, o_va, o_kb, o_vb, o_off, o_part, o_table, o_scal, o_pk0, o_pv0, o_pk1, o_pv1,
-      o_sbr, o_cbase, o_csb, o_cnt, o_tot, o_blk, total;
+  size_t o_dkey, o_word, o_ka, o_wa, o_kb, o_wb, o_off, o_part, o_table, o_dtot, o_scal, o_pk0, o_pv0, o_pk1,
+      o_pv1, o_sbr, o_cbase, o_csb, o_cnt, o_tot, o_blk, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -614,11 +676,9 @@ BinPlan make_plan(int64_t n, int width, int height, int64_t capacity) {
   const int64_t nn = std::max<int64_t>(n, 1);
   P.pcap = kSBMax * nn;
   P.cmax = (P.pcap + kChunk - 1) / kChunk + P.S;
-  P.G_d = (int)std::min<int64_t>(4096, std::max<int64_t>(1, (nn + 1023) / 1024));
-  P.G_p = (int)std::min<int64_t>(4096, std::max<int64_t>(1, (2 * nn + 1023) / 1024));
-  P.nblk_prep = div_up(nn, kPrepBlock);
+  P.G_d = (int)((nn + kPrepSpan - 1) / kPrepSpan);
+  P.G_p = (int)std::min<int64_t>(8192, std::max<int64_t>(1, (2 * nn + 1023) / 1024));
   const int64_t tbl = (int64_t)kRadixBins * std::max(P.G_d, P.G_p);
-  const int64_t scan_max = std::max<int64_t>({nn, tbl, (int64_t)P.T, (int64_t)P.S});
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -626,31 +686,32 @@ BinPlan make_plan(int64_t n, int width, int height, int64_t capacity) {
     return at;
   };
   P.o_dkey = take(nn * 4);
-  P.o_rect = take(nn * 8);
+  P.o_word = take(nn * 8);
   P.o_ka = take(nn * 4);
-  P.o_va = take(nn * 4);
+  P.o_wa = take(nn * 8);
   P.o_kb = take(nn * 4);
-  P.o_vb = take(nn * 4);
+  P.o_wb = take(nn * 8);
   P.o_off = take((nn + 1) * 4);
-  P.o_part = take((size_t)div_up(scan_max, kScanTile) * 4 + 64);
+  P.o_part = take((size_t)div_up(nn, kScanTile) * 4 + 64);
   P.o_table = take((size_t)tbl * 4);
+  P.o_dtot = take(kRadixBins * 4);
   P.o_scal = take(256);  // device scalars: [0] pairs, [1] chunks
   P.o_pk0 = take((size_t)P.pcap * 4);
-  P.o_pv0 = take((size_t)P.pcap * 4);
+  P.o_pv0 = take((size_t)P.pcap * 8);
   P.o_pk1 = take((size_t)P.pcap * 4);
-  P.o_pv1 = take((size_t)P.pcap * 4);
+  P.o_pv1 = take((size_t)P.pcap * 8);
   P.o_sbr = take(((size_t)P.S + 1) * 4);
   P.o_cbase = take(((size_t)P.S + 1) * 4);
   P.o_csb = take((size_t)P.cmax * 4);
   P.o_cnt = take((size_t)P.cmax * 16 * 4);
   P.o_tot = take((size_t)P.T * 4);
-  P.o_blk = take((size_t)P.nblk_prep * 2 * 4);
+  P.o_blk = take((size_t)P.G_d * 2 * 4);
   P.total = o;
   return P;
 }
 
-template <class Load, class Out>
-int run_scan(hipStream_t s, Load load, int64_t n, uint32_t* partial, Out* out, uint32_t* total) {
+template <class Load>
+int run_scan(hipStream_t s, Load load, int64_t n, uint32_t* partial, uint32_t* out, uint32_t* total) {
   const int nb = div_up(std::max<int64_t>(n, 1), kScanTile);
   if (nb > kMaxScanPartials) {
     set_error("gs_bin: scan of %lld elements exceeds the supported size", (long long)n);
@@ -660,22 +721,26 @@ int run_scan(hipStream_t s, Load load, int64_t n, uint32_t* partial, Out* out, u
   GS_LAUNCH_CHECK("scan_reduce_kernel");
   hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanBlock), 0, s, partial, nb, total);
   GS_LAUNCH_CHECK("scan_partials_kernel");
-  hipLaunchKernelGGL((scan_down_kernel<Load, Out>), dim3(nb), dim3(kScanBlock), 0, s, load, n, partial, out,
+  hipLaunchKernelGGL(scan_down_kernel<Load>, dim3(nb), dim3(kScanBlock), 0, s, load, n, partial, out,
                      (const uint32_t*)total);
   GS_LAUNCH_CHECK("scan_down_kernel");
   return GS_OK;
 }
 
 // One stable radix pass: keys_in/vals_in -> keys_out/vals_out on digit `shift`.
-int radix_pass(hipStream_t s, const uint32_t* kin, const uint32_t* vin, uint32_t* kout, uint32_t* vout,
-               const uint32_t* n_dev, int64_t n_static, int64_t cap, int shift, int G, uint32_t* table,
-               uint32_t* partial) {
-  hipLaunchKernelGGL(radix_upsweep_kernel, dim3(G), dim3(64), 0, s, kin, n_dev, n_static, cap, shift, G, table);
-  GS_LAUNCH_CHECK("radix_upsweep_kernel");
-  int rc = run_scan(s, LoadPlain{table}, (int64_t)kRadixBins * G, partial, table, (uint32_t*)nullptr);
-  if (rc != GS_OK) return rc;
+// The upsweep is skipped when the table was already filled (first depth pass).
+int radix_pass(hipStream_t s, bool upsweep, const uint32_t* kin, const uint64_t* vin, uint32_t* kout, uint64_t* vout,
+               const uint32_t* n_dev, int64_t n_static, int64_t cap, int shift, int G, int fixed_chunk,
+               uint32_t* table, uint32_t* dtot) {
+  if (upsweep) {
+    hipLaunchKernelGGL(radix_upsweep_kernel, dim3(G), dim3(64), 0, s, kin, n_dev, n_static, cap, shift, G,
+                       fixed_chunk, table);
+    GS_LAUNCH_CHECK("radix_upsweep_kernel");
+  }
+  hipLaunchKernelGGL(radix_spine_kernel, dim3(kRadixBins), dim3(kScanBlock), 0, s, table, G, dtot);
+  GS_LAUNCH_CHECK("radix_spine_kernel");
   hipLaunchKernelGGL(radix_downsweep_kernel, dim3(G), dim3(64), 0, s, kin, vin, n_dev, n_static, cap, shift, G,
-                     table, kout, vout);
+                     fixed_chunk, table, dtot, kout, vout);
   GS_LAUNCH_CHECK("radix_downsweep_kernel");
   return GS_OK;
 }
@@ -695,8 +760,8 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
                       size_t workspace_bytes, int32_t* sorted_gids, int32_t* sorted_tiles, int32_t* ranges,
                       int32_t* stats) {
   GS_REQUIRE(n >= 0 && n <= ((int64_t)1 << 26), "gs_bin: n must be in [0, 2^26] (got %lld)", (long long)n);
-  GS_REQUIRE(width > 0 && height > 0 && width <= 65535 * kTile && height <= 65535 * kTile,
-             "gs_bin: bad image size %dx%d", width, height);
+  GS_REQUIRE(width > 0 && height > 0 && width <= 4096 * kTile && height <= 4096 * kTile,
+             "gs_bin: bad image size %dx%d (each side at most 65536)", width, height);
   const BinPlan P = make_plan(n, width, height, capacity);
   GS_REQUIRE(P.cap < ((int64_t)1 << 31), "gs_bin: capacity %lld too large", (long long)P.cap);
   GS_REQUIRE(P.sb_passes <= 2, "gs_bin: %d tiles exceed the supported 16384 superblocks", P.T);
@@ -707,19 +772,20 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
   uint32_t* dkey = (uint32_t*)(ws + P.o_dkey);
-  uint2* rect = (uint2*)(ws + P.o_rect);
+  uint64_t* word = (uint64_t*)(ws + P.o_word);
   uint32_t* ka = (uint32_t*)(ws + P.o_ka);
-  uint32_t* va = (uint32_t*)(ws + P.o_va);
+  uint64_t* wa = (uint64_t*)(ws + P.o_wa);
   uint32_t* kb = (uint32_t*)(ws + P.o_kb);
-  uint32_t* vb = (uint32_t*)(ws + P.o_vb);
+  uint64_t* wb = (uint64_t*)(ws + P.o_wb);
   uint32_t* off = (uint32_t*)(ws + P.o_off);
   uint32_t* part = (uint32_t*)(ws + P.o_part);
   uint32_t* table = (uint32_t*)(ws + P.o_table);
+  uint32_t* dtot = (uint32_t*)(ws + P.o_dtot);
   uint32_t* scal = (uint32_t*)(ws + P.o_scal);
   uint32_t* pk0 = (uint32_t*)(ws + P.o_pk0);
-  uint32_t* pv0 = (uint32_t*)(ws + P.o_pv0);
+  uint64_t* pv0 = (uint64_t*)(ws + P.o_pv0);
   uint32_t* pk1 = (uint32_t*)(ws + P.o_pk1);
-  uint32_t* pv1 = (uint32_t*)(ws + P.o_pv1);
+  uint64_t* pv1 = (uint64_t*)(ws + P.o_pv1);
   int32_t* sbr = (int32_t*)(ws + P.o_sbr);
   uint32_t* cbase = (uint32_t*)(ws + P.o_cbase);
   uint32_t* csb = (uint32_t*)(ws + P.o_csb);
@@ -736,32 +802,32 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
     GS_LAUNCH_CHECK("fill_i32_kernel");
     return GS_OK;
   }
-  // 1. prep
-  hipLaunchKernelGGL(bin_prep_kernel, dim3(P.nblk_prep), dim3(kPrepBlock), 0, s, n, means2d, radii, valid, depths,
-                     width, height, dkey, rect, blk);
+  // 1. prep (+ histogram of the first depth digit)
+  hipLaunchKernelGGL(bin_prep_kernel, dim3(P.G_d), dim3(kPrepBlock), 0, s, n, means2d, radii, valid, depths, width,
+                     height, P.G_d, dkey, word, table, blk);
   GS_LAUNCH_CHECK("bin_prep_kernel");
-  // 2. stable depth sort of Gaussian ids (13-bit bucket: 7 + 6 bits)
-  int rc = radix_pass(s, dkey, nullptr, kb, vb, nullptr, n, n, 0, P.G_d, table, part);
+  // 2. stable depth sort of the packed words (13-bit bucket: 7 + 6 bits)
+  int rc = radix_pass(s, false, dkey, word, kb, wb, nullptr, n, n, 0, P.G_d, kPrepSpan, table, dtot);
   if (rc != GS_OK) return rc;
-  rc = radix_pass(s, kb, vb, ka, va, nullptr, n, n, kRadixBits, P.G_d, table, part);
+  rc = radix_pass(s, true, kb, wb, ka, wa, nullptr, n, n, kRadixBits, P.G_d, kPrepSpan, table, dtot);
   if (rc != GS_OK) return rc;
-  const uint32_t* order = va;
+  const uint64_t* sorted_word = wa;
   // 3. superblock pairs in depth order, stably sorted by superblock
-  rc = run_scan(s, LoadSortedSB{order, rect, n}, n, part, off, n_pairs);
+  rc = run_scan(s, LoadSortedSB{sorted_word}, n, part, off, n_pairs);
   if (rc != GS_OK) return rc;
-  hipLaunchKernelGGL(sb_pairs_kernel, dim3(div_up(n, 256)), dim3(256), 0, s, n, order, rect, off, P.pcap, P.SX, pk0,
+  hipLaunchKernelGGL(sb_pairs_kernel, dim3(div_up(n, 256)), dim3(256), 0, s, n, sorted_word, off, P.pcap, P.SX, pk0,
                      pv0);
   GS_LAUNCH_CHECK("sb_pairs_kernel");
   uint32_t* sbkey = pk0;
-  uint32_t* sbval = pv0;
+  uint64_t* sbval = pv0;
   if (P.sb_passes >= 1) {
-    rc = radix_pass(s, pk0, pv0, pk1, pv1, n_pairs, 0, P.pcap, 0, P.G_p, table, part);
+    rc = radix_pass(s, true, pk0, pv0, pk1, pv1, n_pairs, 0, P.pcap, 0, P.G_p, 0, table, dtot);
     if (rc != GS_OK) return rc;
     sbkey = pk1;
     sbval = pv1;
   }
   if (P.sb_passes == 2) {
-    rc = radix_pass(s, pk1, pv1, pk0, pv0, n_pairs, 0, P.pcap, kRadixBits, P.G_p, table, part);
+    rc = radix_pass(s, true, pk1, pv1, pk0, pv0, n_pairs, 0, P.pcap, kRadixBits, P.G_p, 0, table, dtot);
     if (rc != GS_OK) return rc;
     sbkey = pk0;
     sbval = pv0;
@@ -770,28 +836,17 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
                      P.pcap, P.S, sbr);
   GS_LAUNCH_CHECK("ranges_kernel");
   // 4. tile pass
-  rc = run_scan(s, LoadChunks{sbr}, P.S, part, cbase, n_chunks);
-  if (rc != GS_OK) return rc;
-  hipLaunchKernelGGL(chunk_map_kernel, dim3(div_up(P.S, 256)), dim3(256), 0, s, P.S, cbase, P.cmax, csb);
-  GS_LAUNCH_CHECK("chunk_map_kernel");
+  hipLaunchKernelGGL(chunks_kernel, dim3(1), dim3(kBig), 0, s, P.S, sbr, P.cmax, cbase, csb, n_chunks, P.T, tot);
+  GS_LAUNCH_CHECK("chunks_kernel");
   const int pass_blocks = 2048;
   hipLaunchKernelGGL(tile_count_kernel, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, csb, cbase, sbr, P.S,
-                     sbval, rect, (uint32_t)n, P.SX, cnt);
+                     sbval, P.SX, P.TX, P.TY, cnt, tot);
   GS_LAUNCH_CHECK("tile_count_kernel");
-  hipLaunchKernelGGL(tile_total_kernel, dim3(div_up(P.T, 256)), dim3(256), 0, s, P.T, P.TX, P.SX, P.cmax, cbase, cnt,
-                     tot);
-  GS_LAUNCH_CHECK("tile_total_kernel");
-  rc = run_scan(s, LoadPlain{tot}, P.T, part, ranges, part + div_up(P.T, kScanTile));
-  if (rc != GS_OK) return rc;
-  hipLaunchKernelGGL(tile_offsets_kernel, dim3(div_up(P.T, 256)), dim3(256), 0, s, P.T, P.TX, P.SX, P.cmax, cbase,
-                     ranges, cnt);
-  GS_LAUNCH_CHECK("tile_offsets_kernel");
+  hipLaunchKernelGGL(tile_scan_stats_kernel, dim3(1), dim3(kBig), 0, s, tot, P.T, blk, P.G_d, P.cap, ranges, stats);
+  GS_LAUNCH_CHECK("tile_scan_stats_kernel");
   hipLaunchKernelGGL(tile_write_kernel, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, csb, cbase, sbr, P.S,
-                     sbval, rect, (uint32_t)n, P.SX, P.TX, cnt, P.cap, sorted_gids, sorted_tiles);
+                     sbval, (uint32_t)n, P.SX, P.TX, P.TY, cnt, ranges, P.cap, sorted_gids, sorted_tiles);
   GS_LAUNCH_CHECK("tile_write_kernel");
-  // 5. stats
-  hipLaunchKernelGGL(stats_kernel, dim3(1), dim3(256), 0, s, ranges, P.T, blk, P.nblk_prep, P.cap, stats);
-  GS_LAUNCH_CHECK("stats_kernel");
   return GS_OK;
 }
 

@@ -9,14 +9,16 @@
 // Work decomposition: every wave owns PPT*4 rows of one 16x16 tile; lane l holds the
 // PPT pixels (l % 16, row0 + l / 16 + 4 i), i < PPT, i.e. one column, so the x offset
 // to a Gaussian is shared by the lane's pixels.  Waves are independent (no LDS, no
-// barriers): a wave walks its tile's entry list in batches of 64, each lane loading
-// one record (12 floats) while the previous batch is being blended, and entry j of a
-// batch is broadcast to the whole wave with v_readlane (operands in SGPRs).  With
-// PPT = 4 a wave covers the whole tile (used for large images); PPT = 1 uses four
-// waves per tile for small images that would otherwise leave CUs idle.
+// barriers).  The entry a wave works on is the same for all its lanes, so its id and
+// its 48-byte record come in through scalar loads straight into SGPRs (prefetched one
+// and two entries ahead) and feed the vector math as scalar operands.  With PPT = 4 a
+// wave covers the whole tile (used for large images); PPT = 1 uses four waves per
+// tile for small images that would otherwise leave CUs idle.
 //
-// Forward: stops when every pixel of the wave has T <= 1e-4 (ballot), and writes per
-// pixel the final T and the number of leading entries consumed (n_contrib).
+// Forward: branch-free per pixel (an entry blends iff T > 1e-4 before it and its
+// power > -10); the wave stops when every pixel has T <= 1e-4 (ballot every 8
+// entries).  Per pixel it writes the final T and n_contrib, the number of leading
+// entries met while T > 1e-4.
 // Backward: replays each pixel back to front from (final T, n_contrib), recovering
 // T_k = T_{k+1} / (1 - alpha_k) and the colour behind entry k,
 // R_{k-1} = alpha_k c_k + (1 - alpha_k) R_k.  The 9 gradient terms of an entry are
@@ -144,16 +146,16 @@ __device__ inline Rec load_rec(const float4* __restrict__ rec, int g) {
   return Rec{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c};
 }
 
-__device__ inline Rec bcast_rec(const Rec& r, int j) {
-  return Rec{bcast(r.mx, j), bcast(r.my, j), bcast(r.A, j), bcast(r.B, j), bcast(r.C, j),
-             bcast(r.op, j), bcast(r.r, j), bcast(r.g, j), bcast(r.b, j)};
-}
-
 // power = -0.5 * (ic00 dx^2 + 2 ic01 dx dy + ic11 dy^2) with the -0.5 folded into the
 // record (A, B, C); the forward and backward kernels share this exact expression.
 __device__ inline float power_of(float dy, float Adx2, float Bdx, float C) {
   return fmaf(C * dy, dy, fmaf(Bdx, dy, Adx2));
 }
+
+// Gaussian id of entry k of the tile (uniform: scalar load).  Ids are clamped like
+// XLA's gather only where they are used, so that the load is not waited for early.
+__device__ inline int entry_gid(const int32_t* __restrict__ gids, int start, int k) { return gids[start + k]; }
+__device__ inline int clamp_gid(int g, int num_g) { return min(max(g, 0), num_g - 1); }
 
 template <int PPT>
 __global__ __launch_bounds__(64) void composite_fwd_kernel(
@@ -169,66 +171,53 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
   const int X = tx * kTile + (lane & 15);
   const int Y0 = ty * kTile + part * 4 * PPT + (lane >> 4);
   const float px = (float)(tx * kTile) + ((float)(lane & 15) + 0.5f);
-  float py[PPT];
-  bool done[PPT];
-  float Tr[PPT], c0[PPT], c1[PPT], c2[PPT];
-  int kstop[PPT];
+  float py[PPT], Tr[PPT], c0[PPT], c1[PPT], c2[PPT];
+  int cnt[PPT];
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
     const int yl = part * 4 * PPT + (lane >> 4) + 4 * i;
     py[i] = (float)(ty * kTile) + ((float)yl + 0.5f);
-    done[i] = !(X < W && Y0 + 4 * i < H);
-    Tr[i] = 1.0f;
+    // pixels outside the image start "finished" so they never hold the wave
+    Tr[i] = (X < W && Y0 + 4 * i < H) ? 1.0f : 0.0f;
     c0[i] = c1[i] = c2[i] = 0.0f;
-    kstop[i] = 0;
+    cnt[i] = 0;
   }
   int start, n;
   tile_span(ranges, tile, n_entries, num_g, start, n);
 
-  bool lane_done = true;
+  // Entry k's id and record are wave-uniform: scalar loads, the record fetched one
+  // entry ahead and the id two entries ahead so neither load stalls the wave.
+  Rec nxt = zero_rec();
+  int gnext = 0;
+  if (n > 0) nxt = load_rec(rec, clamp_gid(entry_gid(gids, start, 0), num_g));
+  if (n > 1) gnext = entry_gid(gids, start, 1);
+  for (int k = 0; k < n; ++k) {
+    const Rec e = nxt;
+    if (k + 1 < n) nxt = load_rec(rec, clamp_gid(gnext, num_g));
+    if (k + 2 < n) gnext = entry_gid(gids, start, k + 2);
+    const float dx = px - e.mx;
+    const float Adx2 = (e.A * dx) * dx, Bdx = e.B * dx;
 #pragma unroll
-  for (int i = 0; i < PPT; ++i) lane_done = lane_done && done[i];
-  Rec cur = zero_rec();
-  if (lane < n) cur = load_rec(rec, min(max(gids[start + lane], 0), num_g - 1));
-  for (int b0 = 0; b0 < n; b0 += 64) {
-    if (__ballot(!lane_done) == 0ull) break;
-    // prefetch the next batch while this one is blended
-    Rec nxt = zero_rec();
-    if (b0 + 64 + lane < n) nxt = load_rec(rec, min(max(gids[start + b0 + 64 + lane], 0), num_g - 1));
-    const int cnt = min(64, n - b0);
-    for (int j = 0; j < cnt; ++j) {
-      const Rec e = bcast_rec(cur, j);
-      const float dx = px - e.mx;
-      const float Adx2 = (e.A * dx) * dx, Bdx = e.B * dx;
-#pragma unroll
-      for (int i = 0; i < PPT; ++i) {
-        const float dy = py[i] - e.my;
-        const float pw = power_of(dy, Adx2, Bdx, e.C);
-        if (!done[i] && pw > -10.0f) {
-          float al = fast_exp(pw) * e.op;
-          al = al < 0.99f ? al : 0.99f;
-          const float w = al * Tr[i];
-          c0[i] = fmaf(w, e.r, c0[i]);
-          c1[i] = fmaf(w, e.g, c1[i]);
-          c2[i] = fmaf(w, e.b, c2[i]);
-          Tr[i] = Tr[i] * (1.0f - al);
-          if (Tr[i] <= kTMin) {
-            done[i] = true;
-            kstop[i] = b0 + j + 1;
-          }
-        }
-      }
-      if ((j & 15) == 15) {
-        lane_done = true;
-#pragma unroll
-        for (int i = 0; i < PPT; ++i) lane_done = lane_done && done[i];
-        if (__ballot(!lane_done) == 0ull) break;
-      }
+    for (int i = 0; i < PPT; ++i) {
+      const float dy = py[i] - e.my;
+      const float pw = power_of(dy, Adx2, Bdx, e.C);
+      const bool act = Tr[i] > kTMin;  // rasterizer.py:206
+      float al = fast_exp(pw) * e.op;
+      al = al < 0.99f ? al : 0.99f;
+      al = (act && pw > -10.0f) ? al : 0.0f;  // rasterizer.py:212
+      const float w = al * Tr[i];
+      c0[i] = fmaf(w, e.r, c0[i]);
+      c1[i] = fmaf(w, e.g, c1[i]);
+      c2[i] = fmaf(w, e.b, c2[i]);
+      Tr[i] = Tr[i] * (1.0f - al);
+      cnt[i] += act ? 1 : 0;
     }
-    lane_done = true;
+    if ((k & 7) == 7) {
+      bool live = false;
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) lane_done = lane_done && done[i];
-    cur = nxt;
+      for (int i = 0; i < PPT; ++i) live = live || Tr[i] > kTMin;
+      if (__ballot(live) == 0ull) break;
+    }
   }
   const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];
 #pragma unroll
@@ -240,7 +229,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
       img[3 * p + 1] = c1[i] + Tr[i] * bg1;
       img[3 * p + 2] = c2[i] + Tr[i] * bg2;
       if (finalT) finalT[p] = Tr[i];
-      if (ncontrib) ncontrib[p] = done[i] ? kstop[i] : n;
+      if (ncontrib) ncontrib[p] = cnt[i];
     }
   }
 }
@@ -303,77 +292,65 @@ __global__ __launch_bounds__(64) void composite_bwd_kernel(
   for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, __shfl_xor(kmax, o, 64));
   kmax = bcast_i(kmax, 0);
 
-  int b1 = kmax;
-  Rec cur = zero_rec();
-  int gcur = 0;
-  if (b1 > 0) {
-    const int b0 = b1 > 64 ? b1 - 64 : 0;
-    if (b0 + lane < b1) {
-      gcur = min(max(gids[start + b0 + lane], 0), num_g - 1);
-      cur = load_rec(rec, gcur);
-    }
+  // entries kmax-1 .. 0, ids and records by scalar loads (uniform), prefetched
+  Rec nxt = zero_rec();
+  int gcur = 0, gnext = 0;
+  if (kmax > 0) {
+    gcur = clamp_gid(entry_gid(gids, start, kmax - 1), num_g);
+    nxt = load_rec(rec, gcur);
   }
-  while (b1 > 0) {
-    const int b0 = b1 > 64 ? b1 - 64 : 0;
-    // prefetch the batch in front of this one
-    Rec nxt = zero_rec();
-    int gnxt = 0;
-    const int pb0 = b0 > 64 ? b0 - 64 : 0;
-    if (pb0 + lane < b0) {
-      gnxt = min(max(gids[start + pb0 + lane], 0), num_g - 1);
-      nxt = load_rec(rec, gnxt);
+  if (kmax > 1) gnext = entry_gid(gids, start, kmax - 2);
+  for (int k = kmax - 1; k >= 0; --k) {
+    const Rec e = nxt;
+    const int g = gcur;
+    if (k >= 1) {
+      gcur = clamp_gid(gnext, num_g);
+      nxt = load_rec(rec, gcur);
     }
-    for (int j = b1 - b0 - 1; j >= 0; --j) {
-      const int k = b0 + j;
-      const Rec e = bcast_rec(cur, j);
-      const float dx = px - e.mx;
-      const float Adx2 = (e.A * dx) * dx, Bdx = e.B * dx;
-      float v[9];
+    if (k >= 2) gnext = entry_gid(gids, start, k - 2);
+    const float dx = px - e.mx;
+    const float Adx2 = (e.A * dx) * dx, Bdx = e.B * dx;
+    float v[9];
 #pragma unroll
-      for (int c = 0; c < 9; ++c) v[c] = 0.0f;
-      bool any = false;
+    for (int c = 0; c < 9; ++c) v[c] = 0.0f;
+    bool any = false;
 #pragma unroll
-      for (int i = 0; i < PPT; ++i) {
-        const float dy = py[i] - e.my;
-        const float pw = power_of(dy, Adx2, Bdx, e.C);
-        if (k < kp[i] && pw > -10.0f) {
-          any = true;
-          const float ex = fast_exp(pw);
-          const float araw = ex * e.op;
-          const float al = araw < 0.99f ? araw : 0.99f;
-          const float capf = araw < 0.99f ? 1.0f : (araw == 0.99f ? 0.5f : 0.0f);
-          const float om = 1.0f - al;
-          const float Tk = Tr[i] * __builtin_amdgcn_rcpf(om);
-          const float w = al * Tk;
-          v[6] = fmaf(w, g0[i], v[6]);
-          v[7] = fmaf(w, g1[i], v[7]);
-          v[8] = fmaf(w, g2[i], v[8]);
-          const float dal = Tk * fmaf(e.b - R2[i], g2[i], fmaf(e.g - R1[i], g1[i], (e.r - R0[i]) * g0[i]));
-          R0[i] = fmaf(al, e.r, om * R0[i]);
-          R1[i] = fmaf(al, e.g, om * R1[i]);
-          R2[i] = fmaf(al, e.b, om * R2[i]);
-          Tr[i] = Tk;
-          const float dae = dal * capf;
-          const float dpw = dae * araw;
-          v[5] = fmaf(dae, ex, v[5]);
-          const float dpx = dpw * dx, dpy = dpw * dy;
-          v[2] = fmaf(dpx, dx, v[2]);
-          v[3] = fmaf(dpx, dy, v[3]);
-          v[4] = fmaf(dpy, dy, v[4]);
-          // d power / d mean = -(2 A dx + B dy, B dx + 2 C dy)
-          v[0] = fmaf(-dpw, fmaf(2.0f * e.A, dx, e.B * dy), v[0]);
-          v[1] = fmaf(-dpw, fmaf(e.B, dx, 2.0f * e.C * dy), v[1]);
-        }
-      }
-      if (__ballot(any) != 0ull) {
-        const float mine = reduce_scatter9(v, lane);
-        const int g = bcast_i(gcur, j);
-        if (lane < 9 && mine != 0.0f) atomicAdd(&grec[(int64_t)g * kRec + lane], mine);
+    for (int i = 0; i < PPT; ++i) {
+      const float dy = py[i] - e.my;
+      const float pw = power_of(dy, Adx2, Bdx, e.C);
+      if (k < kp[i] && pw > -10.0f) {
+        any = true;
+        const float ex = fast_exp(pw);
+        const float araw = ex * e.op;
+        const float al = araw < 0.99f ? araw : 0.99f;
+        const float capf = araw < 0.99f ? 1.0f : (araw == 0.99f ? 0.5f : 0.0f);
+        const float om = 1.0f - al;
+        const float Tk = Tr[i] * __builtin_amdgcn_rcpf(om);
+        const float w = al * Tk;
+        v[6] = fmaf(w, g0[i], v[6]);
+        v[7] = fmaf(w, g1[i], v[7]);
+        v[8] = fmaf(w, g2[i], v[8]);
+        const float dal = Tk * fmaf(e.b - R2[i], g2[i], fmaf(e.g - R1[i], g1[i], (e.r - R0[i]) * g0[i]));
+        R0[i] = fmaf(al, e.r, om * R0[i]);
+        R1[i] = fmaf(al, e.g, om * R1[i]);
+        R2[i] = fmaf(al, e.b, om * R2[i]);
+        Tr[i] = Tk;
+        const float dae = dal * capf;
+        const float dpw = dae * araw;
+        v[5] = fmaf(dae, ex, v[5]);
+        const float dpx = dpw * dx, dpy = dpw * dy;
+        v[2] = fmaf(dpx, dx, v[2]);
+        v[3] = fmaf(dpx, dy, v[3]);
+        v[4] = fmaf(dpy, dy, v[4]);
+        // d power / d mean = -(2 A dx + B dy, B dx + 2 C dy)
+        v[0] = fmaf(-dpw, fmaf(2.0f * e.A, dx, e.B * dy), v[0]);
+        v[1] = fmaf(-dpw, fmaf(e.B, dx, 2.0f * e.C * dy), v[1]);
       }
     }
-    cur = nxt;
-    gcur = gnxt;
-    b1 = b0;
+    if (__ballot(any) != 0ull) {
+      const float mine = reduce_scatter9(v, lane);
+      if (lane < 9 && mine != 0.0f) atomicAdd(&grec[(int64_t)g * kRec + lane], mine);
+    }
   }
 }
 
