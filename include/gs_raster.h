@@ -36,12 +36,18 @@ extern "C" {
 #define GS_MAX_TILE_CHUNKS 8
 #define GS_MAX_TILE_INTERACTIONS 4096
 
-/* Per-Gaussian compositing record: 12 floats
- *   [0]=mean2d.x [1]=mean2d.y [2]=-0.5*ic00 [3]=-0.5*(2*ic01) [4]=-0.5*ic11
- *   [5]=sigmoid(opacity) [6..8]=colour rgb [9..11]=0
- * (ic = inverse of cov2D with det clamped to 1e-6, rasterizer.py:147-156).
- * The gradient record produced by gs_composite_bwd has the same layout and holds
- * dL/d(record[0..8]). */
+/* Per-Gaussian compositing record: 12 floats, L = log2(e)
+ *   [0]=mean2d.x [1]=mean2d.y [2]=-0.5*ic00*L [3]=-ic01*L [4]=-0.5*ic11*L
+ *   [5]=log2(op) [6..8]=colour rgb [9]=op [10]=log2(op) - 10*L [11]=0
+ * where op = sigmoid(opacity) and ic = inverse of cov2D with det clamped to 1e-6
+ * (rasterizer.py:147-156), so that alpha = exp2([2]dx^2 + [3]dx dy + [4]dy^2 + [5])
+ * and the gate power > -10 is exponent > [10].
+ * The gradient record produced by gs_composite_bwd holds, with dP = dL/dpower of one
+ * (pixel, entry) pair, dx = pixel.x - mean2d.x, dy = pixel.y - mean2d.y, summed over
+ * the Gaussian's pairs:
+ *   [0]=sum dP dx [1]=sum dP dy [2]=sum dP dx^2 [3]=sum dP dx dy [4]=sum dP dy^2
+ *   [5]=sum dP (= op * dL/dop) [6..8]=dL/dcolour [9..11]=0
+ * (gs_preprocess_bwd turns these into dL/dmean2d, dL/dic and dL/dopacity). */
 #define GS_REC_STRIDE 12
 
 /* Layout of the int32 stats[] array filled by gs_bin (renderer.py:63-90 extras). */
@@ -120,8 +126,8 @@ int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_
                      float* image, float* final_T, int32_t* n_contrib);
 
 /* Vector-Jacobian product of gs_composite_fwd (JAX autodiff of render_tiles).
- * grad_records[N,GS_REC_STRIDE] is overwritten with dL/d(record); grad_background[3]
- * (may be NULL) with dL/d(background). */
+ * grad_records[N,GS_REC_STRIDE] is overwritten with the gradient record (layout
+ * above); grad_background[3] (may be NULL) with dL/d(background). */
 int gs_composite_bwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                      int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
                      const float* grad_image, const float* final_T, const int32_t* n_contrib,

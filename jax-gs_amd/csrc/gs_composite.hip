@@ -6,26 +6,40 @@
 // power > -10, with alpha = min(0.99, exp(power) * sigmoid(opacity)); the pixel is
 // C + T * background.  rasterizer_tpu.py computes the same image.
 //
+// Records hold the conic pre-scaled by log2(e) and log2(sigmoid(opacity)), so one
+// exp2 of  q = log2(e) * power + log2(opacity)  gives the unclipped alpha, and the
+// gate power > -10 reads  q > log2(opacity) - 10 log2(e)  (a per-entry threshold
+// kept in the record).
+//
 // Work decomposition: every wave owns PPT*4 rows of one 16x16 tile; lane l holds the
 // PPT pixels (l % 16, row0 + l / 16 + 4 i), i < PPT, i.e. one column, so the x offset
 // to a Gaussian is shared by the lane's pixels.  Waves are independent (no LDS, no
-// barriers).  The entry a wave works on is the same for all its lanes, so its id and
-// its 48-byte record come in through scalar loads straight into SGPRs (prefetched one
-// and two entries ahead) and feed the vector math as scalar operands.  With PPT = 4 a
-// wave covers the whole tile (used for large images); PPT = 1 uses four waves per
-// tile for small images that would otherwise leave CUs idle.
+// barriers).  With PPT = 4 a wave covers the whole tile (used for large images);
+// PPT = 1 uses four waves per tile for small images that would otherwise leave CUs
+// idle.
 //
-// Forward: branch-free per pixel (an entry blends iff T > 1e-4 before it and its
-// power > -10); the wave stops when every pixel has T <= 1e-4 (ballot every 8
-// entries).  Per pixel it writes the final T and n_contrib, the number of leading
-// entries met while T > 1e-4.
+// Culling: a Gaussian is binned to every tile its square 3-sigma box touches, but its
+// "power > -10" region is an ellipse, and for about a third of the (tile, entry) pairs
+// of a dense scene that ellipse reaches no pixel centre of the tile.  Such entries
+// change nothing (every pixel gates them out), so a wave first tests 64 entries at a
+// time, one per lane, against the rectangle spanned by its pixel centres (exact
+// minimum of the convex quadratic form over the rectangle, with a rounding margin,
+// so an entry is dropped only if no pixel could pass the gate), and then walks the
+// surviving entries.  The walked entry is wave-uniform: its id comes from the
+// testing lane and its 48-byte record through scalar loads into SGPRs, prefetched
+// one surviving entry ahead.
+//
+// Forward: branch-free per pixel; the wave stops when every pixel has T <= 1e-4
+// (ballot every 8 walked entries).  Per pixel it writes the final T and n_contrib,
+// the number of leading entries met while T > 1e-4 (culled entries included).
 // Backward: replays each pixel back to front from (final T, n_contrib), recovering
-// T_k = T_{k+1} / (1 - alpha_k) and the colour behind entry k,
-// R_{k-1} = alpha_k c_k + (1 - alpha_k) R_k.  The 9 gradient terms of an entry are
-// summed over the lane's pixels, reduce-scattered across the wave (recursive halving,
-// so lane c ends with the total of term c) and added to the Gaussian's gradient
-// record with one atomic instruction (9 lanes).  Gradients follow JAX autodiff of the
-// reference: the cap
+// T_k = T_{k+1} / (1 - alpha_k) and the colour behind entry k projected on the
+// pixel's image cotangent g, Rg_{k-1} = alpha_k (c_k . g) + (1 - alpha_k) Rg_k, so
+// dL/dalpha_k = T_k (c_k . g - Rg_k).  Per lane the entry's power cotangents are kept
+// as sums that the lane's pixels (one column, one dx) share; the 9 sums of an entry
+// are reduce-scattered across the wave (recursive halving, so lane c ends with the
+// total of sum c) and added to the Gaussian's gradient record with one atomic
+// instruction (9 lanes).  Gradients follow JAX autodiff of the reference: the cap
 // min(0.99, .) passes no gradient when it binds (half at a tie), gated entries pass
 // none.
 #include "gs_common.h"
@@ -34,9 +48,6 @@ namespace gs {
 namespace {
 
 constexpr float kTMin = 1e-4f;
-constexpr float kLog2e = 1.4426950408889634f;
-
-__device__ inline float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 
 __device__ inline float bcast(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
@@ -133,29 +144,77 @@ __device__ inline void tile_span(const int32_t* __restrict__ ranges, int tile, i
   n = num_g > 0 ? (int)c : 0;
 }
 
+// One compositing record (layout of GS_REC_STRIDE floats in gs_raster.h).
 struct Rec {
-  float mx, my, A, B, C, op, r, g, b;
+  float mx, my, A, B, C, lop, r, g, b, op, thr;
 };
 
-__device__ inline Rec zero_rec() { return Rec{0, 0, 0, 0, 0, 0, 0, 0, 0}; }
+__device__ inline Rec zero_rec() { return Rec{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}; }
 
 __device__ inline Rec load_rec(const float4* __restrict__ rec, int g) {
   const float4 a = rec[(int64_t)g * 3];
   const float4 b = rec[(int64_t)g * 3 + 1];
-  const float c = rec[(int64_t)g * 3 + 2].x;
-  return Rec{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c};
+  const float4 c = rec[(int64_t)g * 3 + 2];
+  return Rec{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z};
 }
 
-// power = -0.5 * (ic00 dx^2 + 2 ic01 dx dy + ic11 dy^2) with the -0.5 folded into the
-// record (A, B, C); the forward and backward kernels share this exact expression.
-__device__ inline float power_of(float dy, float Adx2, float Bdx, float C) {
-  return fmaf(C * dy, dy, fmaf(Bdx, dy, Adx2));
+// q = log2(e) * power + log2(opacity) with (A, B, C) = log2(e) * (-ic00/2, -ic01,
+// -ic11/2); Adx2l = A dx^2 + log2(opacity) is shared by a lane's pixels.  The forward
+// and backward kernels share this exact expression.
+__device__ inline float q_of(float dy, float Adx2l, float Bdx, float C) {
+  return fmaf(C * dy, dy, fmaf(Bdx, dy, Adx2l));
 }
 
-// Gaussian id of entry k of the tile (uniform: scalar load).  Ids are clamped like
-// XLA's gather only where they are used, so that the load is not waited for early.
-__device__ inline int entry_gid(const int32_t* __restrict__ gids, int start, int k) { return gids[start + k]; }
+// Ids are clamped like XLA's gather.
 __device__ inline int clamp_gid(int g, int num_g) { return min(max(g, 0), num_g - 1); }
+
+// True when no point of the rectangle [x0,x1] x [y0,y1] can pass the gate
+// power > -10 for the entry (mx, my, A, B, C), where A dx^2 + B dx dy + C dy^2 =
+// log2(e) * power.  f = -(A dx^2 + B dx dy + C dy^2) is a convex quadratic when A < 0,
+// C < 0 and B^2 < 4AC (anything else, NaN included, is kept); its minimum over the
+// rectangle is 0 when the centre lies inside, else it lies on an edge, where it is
+// the 1-D minimum at the clamped stationary point.  The threshold exceeds
+// 10 log2(e) by an allowance for the rounding of both this minimum and the per-pixel
+// exponent (a few ulp of the largest term), so a dropped entry fails the gate at
+// every pixel centre of the rectangle as the compositing loops compute it.
+__host__ __device__ inline bool entry_misses_rect(float mx, float my, float A, float B, float C, float x0,
+                                                  float x1, float y0, float y1) {
+  const float a = -A, b = -B, c = -C;
+  if (!(a > 0.0f && c > 0.0f && b * b < 4.0f * a * c)) return false;
+  const float dx0 = x0 - mx, dx1 = x1 - mx, dy0 = y0 - my, dy1 = y1 - my;
+  if (dx0 <= 0.0f && dx1 >= 0.0f && dy0 <= 0.0f && dy1 >= 0.0f) return false;
+  const float sx = -0.5f * b / a, sy = -0.5f * b / c;  // stationary points: dx* = sx dy, dy* = sy dx
+  auto on_x_edge = [&](float dx) {
+    const float dy = fminf(fmaxf(sy * dx, dy0), dy1);
+    return (a * dx) * dx + (b * dx) * dy + (c * dy) * dy;
+  };
+  auto on_y_edge = [&](float dy) {
+    const float dx = fminf(fmaxf(sx * dy, dx0), dx1);
+    return (a * dx) * dx + (b * dx) * dy + (c * dy) * dy;
+  };
+  const float fmin = fminf(fminf(on_x_edge(dx0), on_x_edge(dx1)), fminf(on_y_edge(dy0), on_y_edge(dy1)));
+  const float ex = fmaxf(dx0 * dx0, dx1 * dx1), ey = fmaxf(dy0 * dy0, dy1 * dy1);
+  const float scale = a * ex + fabsf(b) * sqrtf(ex * ey) + c * ey;
+  return fmin >= 10.25f * 1.4426950408889634f + 1e-5f * scale;
+}
+
+// Test entries [b0, b0+64) of a tile against a wave's pixel rectangle, one per lane:
+// returns the ballot of surviving entries; *gl receives the lane's (clamped) id.
+__device__ inline uint64_t test_batch(const float4* __restrict__ rec, const int32_t* __restrict__ gids, int start,
+                                      int b0, int n, int num_g, float x0, float x1, float y0, float y1, int lane,
+                                      int* gl) {
+  const int k = b0 + lane;
+  bool keep = false;
+  int g = 0;
+  if (k < n) {
+    g = clamp_gid(gids[start + k], num_g);
+    const float4 a = rec[(int64_t)g * 3];
+    const float c = rec[(int64_t)g * 3 + 1].x;
+    keep = !entry_misses_rect(a.x, a.y, a.z, a.w, c, x0, x1, y0, y1);
+  }
+  *gl = g;
+  return __ballot(keep);
+}
 
 template <int PPT>
 __global__ __launch_bounds__(64) void composite_fwd_kernel(
@@ -184,39 +243,53 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
   }
   int start, n;
   tile_span(ranges, tile, n_entries, num_g, start, n);
+  const float rx0 = (float)(tx * kTile) + 0.5f, rx1 = rx0 + (float)(kTile - 1);
+  const float ry0 = (float)(ty * kTile + part * 4 * PPT) + 0.5f, ry1 = ry0 + (float)(4 * PPT - 1);
 
-  // Entry k's id and record are wave-uniform: scalar loads, the record fetched one
-  // entry ahead and the id two entries ahead so neither load stalls the wave.
-  Rec nxt = zero_rec();
-  int gnext = 0;
-  if (n > 0) nxt = load_rec(rec, clamp_gid(entry_gid(gids, start, 0), num_g));
-  if (n > 1) gnext = entry_gid(gids, start, 1);
-  for (int k = 0; k < n; ++k) {
-    const Rec e = nxt;
-    if (k + 1 < n) nxt = load_rec(rec, clamp_gid(gnext, num_g));
-    if (k + 2 < n) gnext = entry_gid(gids, start, k + 2);
-    const float dx = px - e.mx;
-    const float Adx2 = (e.A * dx) * dx, Bdx = e.B * dx;
-#pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const float dy = py[i] - e.my;
-      const float pw = power_of(dy, Adx2, Bdx, e.C);
-      const bool act = Tr[i] > kTMin;  // rasterizer.py:206
-      float al = fast_exp(pw) * e.op;
-      al = al < 0.99f ? al : 0.99f;
-      al = (act && pw > -10.0f) ? al : 0.0f;  // rasterizer.py:212
-      const float w = al * Tr[i];
-      c0[i] = fmaf(w, e.r, c0[i]);
-      c1[i] = fmaf(w, e.g, c1[i]);
-      c2[i] = fmaf(w, e.b, c2[i]);
-      Tr[i] = Tr[i] * (1.0f - al);
-      cnt[i] += act ? 1 : 0;
+  bool done = false;
+  int walked = 0;
+  for (int b0 = 0; b0 < n && !done; b0 += 64) {
+    int gl;
+    uint64_t m = test_batch(rec, gids, start, b0, n, num_g, rx0, rx1, ry0, ry1, lane, &gl);
+    Rec nxt = zero_rec();
+    int jn = 0;
+    if (m != 0ull) {
+      jn = __builtin_ctzll(m);
+      nxt = load_rec(rec, bcast_i(gl, jn));
     }
-    if ((k & 7) == 7) {
-      bool live = false;
+    while (m != 0ull) {
+      const Rec e = nxt;
+      const int kk = b0 + jn + 1;  // entries met so far, this one included
+      m &= m - 1ull;
+      if (m != 0ull) {
+        jn = __builtin_ctzll(m);
+        nxt = load_rec(rec, bcast_i(gl, jn));
+      }
+      const float dx = px - e.mx;
+      const float Adx2l = fmaf(e.A * dx, dx, e.lop), Bdx = e.B * dx;
 #pragma unroll
-      for (int i = 0; i < PPT; ++i) live = live || Tr[i] > kTMin;
-      if (__ballot(live) == 0ull) break;
+      for (int i = 0; i < PPT; ++i) {
+        const float q = q_of(py[i] - e.my, Adx2l, Bdx, e.C);
+        const bool act = Tr[i] > kTMin;  // rasterizer.py:206
+        float al = __builtin_amdgcn_exp2f(q);
+        al = al < 0.99f ? al : 0.99f;
+        al = (act && q > e.thr) ? al : 0.0f;  // rasterizer.py:212
+        const float w = al * Tr[i];
+        c0[i] = fmaf(w, e.r, c0[i]);
+        c1[i] = fmaf(w, e.g, c1[i]);
+        c2[i] = fmaf(w, e.b, c2[i]);
+        Tr[i] = Tr[i] * (1.0f - al);
+        cnt[i] = act ? kk : cnt[i];
+      }
+      if ((++walked & 7) == 0) {
+        bool live = false;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) live = live || Tr[i] > kTMin;
+        if (__ballot(live) == 0ull) {
+          done = true;
+          break;
+        }
+      }
     }
   }
   const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];
@@ -229,7 +302,8 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
       img[3 * p + 1] = c1[i] + Tr[i] * bg1;
       img[3 * p + 2] = c2[i] + Tr[i] * bg2;
       if (finalT) finalT[p] = Tr[i];
-      if (ncontrib) ncontrib[p] = cnt[i];
+      // a pixel still open met every entry of the tile, culled ones included
+      if (ncontrib) ncontrib[p] = Tr[i] > kTMin ? n : cnt[i];
     }
   }
 }
@@ -253,7 +327,7 @@ __global__ __launch_bounds__(64) void composite_bwd_kernel(
   tile_span(ranges, tile, n_entries, num_g, start, n);
   const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];
 
-  float py[PPT], Tr[PPT], g0[PPT], g1[PPT], g2[PPT], R0[PPT], R1[PPT], R2[PPT];
+  float py[PPT], Tr[PPT], g0[PPT], g1[PPT], g2[PPT], Rg[PPT];
   int kp[PPT];
   int kmax = 0;
   float tb0 = 0.0f, tb1 = 0.0f, tb2 = 0.0f;
@@ -274,9 +348,8 @@ __global__ __launch_bounds__(64) void composite_bwd_kernel(
       g1[i] = gimg[3 * p + 1];
       g2[i] = gimg[3 * p + 2];
     }
-    R0[i] = bg0;
-    R1[i] = bg1;
-    R2[i] = bg2;
+    // colour behind the last entry is the background
+    Rg[i] = fmaf(bg2, g2[i], fmaf(bg1, g1[i], bg0 * g0[i]));
     kmax = max(kmax, kp[i]);
     // dL/dbackground = sum over pixels of T_final * g
     tb0 = fmaf(Tr[i], g0[i], tb0);
@@ -292,64 +365,72 @@ __global__ __launch_bounds__(64) void composite_bwd_kernel(
   for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, __shfl_xor(kmax, o, 64));
   kmax = bcast_i(kmax, 0);
 
-  // entries kmax-1 .. 0, ids and records by scalar loads (uniform), prefetched
-  Rec nxt = zero_rec();
-  int gcur = 0, gnext = 0;
-  if (kmax > 0) {
-    gcur = clamp_gid(entry_gid(gids, start, kmax - 1), num_g);
-    nxt = load_rec(rec, gcur);
-  }
-  if (kmax > 1) gnext = entry_gid(gids, start, kmax - 2);
-  for (int k = kmax - 1; k >= 0; --k) {
-    const Rec e = nxt;
-    const int g = gcur;
-    if (k >= 1) {
-      gcur = clamp_gid(gnext, num_g);
-      nxt = load_rec(rec, gcur);
+  // entries kmax-1 .. 0 in batches of 64 from the top; surviving entries walked from
+  // the highest down, ids from the testing lane, records by scalar loads, prefetched
+  const float rx0 = (float)(tx * kTile) + 0.5f, rx1 = rx0 + (float)(kTile - 1);
+  const float ry0 = (float)(ty * kTile + part * 4 * PPT) + 0.5f, ry1 = ry0 + (float)(4 * PPT - 1);
+  for (int b0 = (kmax - 1) & ~63; b0 >= 0; b0 -= 64) {
+    int gl;
+    uint64_t m = test_batch(rec, gids, start, b0, kmax, num_g, rx0, rx1, ry0, ry1, lane, &gl);
+    Rec nxt = zero_rec();
+    int jn = 0, gn = 0;
+    if (m != 0ull) {
+      jn = 63 - __builtin_clzll(m);
+      gn = bcast_i(gl, jn);
+      nxt = load_rec(rec, gn);
     }
-    if (k >= 2) gnext = entry_gid(gids, start, k - 2);
-    const float dx = px - e.mx;
-    const float Adx2 = (e.A * dx) * dx, Bdx = e.B * dx;
-    float v[9];
-#pragma unroll
-    for (int c = 0; c < 9; ++c) v[c] = 0.0f;
-    bool any = false;
-#pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const float dy = py[i] - e.my;
-      const float pw = power_of(dy, Adx2, Bdx, e.C);
-      if (k < kp[i] && pw > -10.0f) {
-        any = true;
-        const float ex = fast_exp(pw);
-        const float araw = ex * e.op;
-        const float al = araw < 0.99f ? araw : 0.99f;
-        const float capf = araw < 0.99f ? 1.0f : (araw == 0.99f ? 0.5f : 0.0f);
-        const float om = 1.0f - al;
-        const float Tk = Tr[i] * __builtin_amdgcn_rcpf(om);
-        const float w = al * Tk;
-        v[6] = fmaf(w, g0[i], v[6]);
-        v[7] = fmaf(w, g1[i], v[7]);
-        v[8] = fmaf(w, g2[i], v[8]);
-        const float dal = Tk * fmaf(e.b - R2[i], g2[i], fmaf(e.g - R1[i], g1[i], (e.r - R0[i]) * g0[i]));
-        R0[i] = fmaf(al, e.r, om * R0[i]);
-        R1[i] = fmaf(al, e.g, om * R1[i]);
-        R2[i] = fmaf(al, e.b, om * R2[i]);
-        Tr[i] = Tk;
-        const float dae = dal * capf;
-        const float dpw = dae * araw;
-        v[5] = fmaf(dae, ex, v[5]);
-        const float dpx = dpw * dx, dpy = dpw * dy;
-        v[2] = fmaf(dpx, dx, v[2]);
-        v[3] = fmaf(dpx, dy, v[3]);
-        v[4] = fmaf(dpy, dy, v[4]);
-        // d power / d mean = -(2 A dx + B dy, B dx + 2 C dy)
-        v[0] = fmaf(-dpw, fmaf(2.0f * e.A, dx, e.B * dy), v[0]);
-        v[1] = fmaf(-dpw, fmaf(e.B, dx, 2.0f * e.C * dy), v[1]);
+    while (m != 0ull) {
+      const Rec e = nxt;
+      const int g = gn;
+      const int k = b0 + jn;
+      m &= ~(1ull << jn);
+      if (m != 0ull) {
+        jn = 63 - __builtin_clzll(m);
+        gn = bcast_i(gl, jn);
+        nxt = load_rec(rec, gn);
       }
-    }
-    if (__ballot(any) != 0ull) {
-      const float mine = reduce_scatter9(v, lane);
-      if (lane < 9 && mine != 0.0f) atomicAdd(&grec[(int64_t)g * kRec + lane], mine);
+      const float dx = px - e.mx;
+      const float Adx2l = fmaf(e.A * dx, dx, e.lop), Bdx = e.B * dx;
+      // per-lane sums over the lane's pixels: P = sum dpower, Q = sum dpower*dy,
+      // V = sum dpower*dy^2, colour cotangents
+      float P = 0.0f, Q = 0.0f, V = 0.0f, gc0 = 0.0f, gc1 = 0.0f, gc2 = 0.0f;
+      bool any = false;
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const float dy = py[i] - e.my;
+        const float q = q_of(dy, Adx2l, Bdx, e.C);
+        if (k < kp[i] && q > e.thr) {
+          any = true;
+          const float araw = __builtin_amdgcn_exp2f(q);
+          const float al = araw < 0.99f ? araw : 0.99f;
+          const float om = 1.0f - al;
+          const float Tk = Tr[i] * __builtin_amdgcn_rcpf(om);
+          const float w = al * Tk;
+          gc0 = fmaf(w, g0[i], gc0);
+          gc1 = fmaf(w, g1[i], gc1);
+          gc2 = fmaf(w, g2[i], gc2);
+          const float cg = fmaf(e.b, g2[i], fmaf(e.g, g1[i], e.r * g0[i]));
+          const float dal = Tk * (cg - Rg[i]);
+          Rg[i] = fmaf(al, cg, om * Rg[i]);
+          Tr[i] = Tk;
+          // min(araw, 0.99): the cotangent passes below the cap, half of it at a tie
+          float dae = araw < 0.99f ? dal : 0.0f;
+          if (araw == 0.99f) dae = 0.5f * dal;
+          const float dpw = dae * araw;  // d/d power (natural units)
+          P += dpw;
+          const float dpy = dpw * dy;
+          Q += dpy;
+          V = fmaf(dpy, dy, V);
+        }
+      }
+      if (__ballot(any) != 0ull) {
+        // gradient record sums: [0] dpw dx, [1] dpw dy, [2] dpw dx^2, [3] dpw dx dy,
+        // [4] dpw dy^2, [5] dpw, [6..8] colour
+        const float Sx = P * dx;
+        float v[9] = {Sx, Q, Sx * dx, Q * dx, V, P, gc0, gc1, gc2};
+        const float mine = reduce_scatter9(v, lane);
+        if (lane < 9 && mine != 0.0f) atomicAdd(&grec[(int64_t)g * kRec + lane], mine);
+      }
     }
   }
 }

@@ -170,10 +170,13 @@ __device__ inline void write_record(float* __restrict__ rec, float m2x, float m2
   const float ic00 = c11 / det;
   const float ic01 = (-c01) / det;
   const float ic11 = c00 / det;
+  constexpr float kL2E = 1.4426950408889634f;
+  const float op = det_sigmoidf(logit);
+  const float lop = log2f(op);
   float4* r4 = reinterpret_cast<float4*>(rec);
-  r4[0] = make_float4(m2x, m2y, -0.5f * ic00, -0.5f * (2.0f * ic01));
-  r4[1] = make_float4(-0.5f * ic11, det_sigmoidf(logit), col[0], col[1]);
-  r4[2] = make_float4(col[2], 0.0f, 0.0f, 0.0f);
+  r4[0] = make_float4(m2x, m2y, (-0.5f * ic00) * kL2E, (-ic01) * kL2E);
+  r4[1] = make_float4((-0.5f * ic11) * kL2E, lop, col[0], col[1]);
+  r4[2] = make_float4(col[2], op, lop - 10.0f * kL2E, 0.0f);
 }
 
 template <int DEG>
@@ -310,22 +313,25 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
   const float4 ga = reinterpret_cast<const float4*>(grec + i * kRec)[0];
   const float4 gb = reinterpret_cast<const float4*>(grec + i * kRec)[1];
   const float4 gc = reinterpret_cast<const float4*>(grec + i * kRec)[2];
-  const float g_m2x = ga.x, g_m2y = ga.y;
-  // record[2..4] = -0.5*ic00, -0.5*(2*ic01) = -ic01, -0.5*ic11
+  // gradient record (sums over the Gaussian's pixels of dL/dpower times):
+  // [0] dx, [1] dy, [2] dx^2, [3] dx dy, [4] dy^2, [5] 1; [6..8] dL/dcolour
+  // power = -0.5 (ic00 dx^2 + 2 ic01 dx dy + ic11 dy^2), dx = px - mean2d.x
   const float g_ic00 = -0.5f * ga.z;
   const float g_ic01 = -ga.w;
   const float g_ic11 = -0.5f * gb.x;
-  const float g_sig = gb.y;
   const float g_col[3] = {gb.z, gb.w, gc.x};
 
-  // ---- opacity: sigmoid
+  // ---- opacity: alpha = exp(power) * sigmoid(logit); sum dL/dpower = sigmoid * dL/dsigmoid
   const float sg = det_sigmoidf(opac[i]);
-  g_opac[i] = g_sig * sg * (1.0f - sg);
+  g_opac[i] = gb.y * (1.0f - sg);
 
   // ---- conic <- cov2D (rasterizer.py:147-153)
   const float det_raw = p.c00 * p.c11 - p.c01 * p.c01;
   const float det = jmax(det_raw, 1e-6f);
   const float ic00 = p.c11 / det, ic01 = (-p.c01) / det, ic11 = p.c00 / det;
+  // ---- d power / d mean2d = (ic00 dx + ic01 dy, ic01 dx + ic11 dy)
+  const float g_m2x = ic00 * ga.x + ic01 * ga.y;
+  const float g_m2y = ic01 * ga.x + ic11 * ga.y;
   float g_c00 = g_ic11 / det;
   float g_c11 = g_ic00 / det;
   float g_c01 = -g_ic01 / det;
