@@ -1,7 +1,9 @@
 // Per-Gaussian preprocessing on gfx950: EWA projection, 3D/2D covariance, radius,
 // SH colour and compositing records (forward), and their vector-Jacobian product
-// (backward).  One thread per Gaussian; every input row is read once and every
-// output row written once, so both kernels are HBM-bound.
+// (backward).  One thread per Gaussian, one wave per 64 Gaussians; every input row
+// is read once and every output row written once, so both kernels are HBM-bound.
+// The SH rows (192 bytes per Gaussian at degree 3) move between HBM and LDS with
+// coalesced accesses.
 //
 // Forward semantics follow, operation by operation and in float32:
 //   jax_gs/renderer/projection.py:26-77 (project_gaussians)
@@ -114,27 +116,6 @@ __device__ inline void view_dir(const float* w, float mx, float my, float mz, fl
   d[2] = v[2] / nrm;
 }
 
-// Loads the first NB coefficient triples of one Gaussian's sh row (K triples) into
-// registers: float4 loads when the row is 16-byte aligned (K % 4 == 0), else dwords.
-template <int NB>
-__device__ inline void load_sh(const float* __restrict__ row, int K, float* v) {
-  if ((K & 3) == 0) {
-    constexpr int NQ = (3 * NB + 3) / 4;
-    const float4* r4 = reinterpret_cast<const float4*>(row);
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      const float4 t = r4[q];
-      if (4 * q + 0 < 3 * NB) v[4 * q + 0] = t.x;
-      if (4 * q + 1 < 3 * NB) v[4 * q + 1] = t.y;
-      if (4 * q + 2 < 3 * NB) v[4 * q + 2] = t.z;
-      if (4 * q + 3 < 3 * NB) v[4 * q + 3] = t.w;
-    }
-  } else {
-#pragma unroll
-    for (int q = 0; q < 3 * NB; ++q) v[q] = row[q];
-  }
-}
-
 // sh.py:25-72 for channel c; sh holds coefficient triples (k, channel) at 3k + c.
 template <int DEG>
 __device__ inline float eval_sh_channel(const float* sh, int c, const float* d) {
@@ -179,24 +160,75 @@ __device__ inline void write_record(float* __restrict__ rec, float m2x, float m2
   r4[2] = make_float4(col[2], op, lop - 10.0f * kL2E, 0.0f);
 }
 
+// Copies the first COLS floats of rows [g0, g0+64) of a row-major array (row
+// stride `stride` floats) into LDS rows of stride `ls`, consecutive lanes reading
+// consecutive addresses (16-byte vectors when rows are 16-byte aligned); every load
+// is issued before the first LDS write.  Rows beyond n repeat row n-1 (never used).
+template <int COLS>
+__device__ inline void stage_rows(const float* __restrict__ src, int64_t g0, int64_t n, int64_t stride,
+                                  float* __restrict__ lds, int ls, int lane) {
+  constexpr int C4 = COLS / 4 > 0 ? COLS / 4 : 1;
+  const float* __restrict__ base = src + g0 * stride;
+  const int rmax = (int)(n - 1 - g0 < 63 ? n - 1 - g0 : 63);
+  const uint32_t st = (uint32_t)stride;
+  if ((COLS & 3) == 0 && (stride & 3) == 0) {
+    float4 v[C4];
+#pragma unroll
+    for (int t = 0; t < C4; ++t) {
+      const int e = lane + 64 * t, r = e / C4, c = e - r * C4;
+      const uint32_t off = (uint32_t)min(r, rmax) * st + 4u * (uint32_t)c;
+      v[t] = *reinterpret_cast<const float4*>(base + off);
+    }
+#pragma unroll
+    for (int t = 0; t < C4; ++t) {
+      const int e = lane + 64 * t, r = e / C4, c = e - r * C4;
+      float* d = lds + r * ls + 4 * c;
+      d[0] = v[t].x;
+      d[1] = v[t].y;
+      d[2] = v[t].z;
+      d[3] = v[t].w;
+    }
+  } else {
+#pragma unroll 8
+    for (int t = 0; t < COLS; ++t) {
+      const int e = lane + 64 * t, r = e / COLS, c = e - r * COLS;
+      lds[r * ls + c] = base[(uint32_t)min(r, rmax) * st + (uint32_t)c];
+    }
+  }
+}
+
+// One wave per 64 Gaussians.  The SH rows (the largest input, 3 (D+1)^2 floats per
+// Gaussian) are staged through LDS so that the global loads are coalesced; the
+// per-Gaussian work reads its row from LDS (odd row stride: no bank conflicts).
 template <int DEG>
-__global__ __launch_bounds__(256) void preprocess_fwd_kernel(
+__global__ __launch_bounds__(64) void preprocess_fwd_kernel(
     int64_t n, int K, const float* __restrict__ means, const float* __restrict__ scales,
     const float* __restrict__ quats, const float* __restrict__ opac, const float* __restrict__ sh,
     const uint8_t* __restrict__ mask, const float* __restrict__ w2c, float fx, float fy, float cx,
     float cy, float* __restrict__ means2d, float* __restrict__ cov2d, float* __restrict__ radii,
     uint8_t* __restrict__ valid, float* __restrict__ depths, float* __restrict__ colors,
     float* __restrict__ records) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  constexpr int NB = (DEG + 1) * (DEG + 1);
+  constexpr int LS = (3 * NB) | 1;
+  __shared__ float shs[64 * LS];
+  const int lane = threadIdx.x;
+  const int64_t g0 = (int64_t)blockIdx.x * 64;
+  const int64_t i = g0 + lane;
+  // per-Gaussian inputs first (clamped index), so that their loads are in flight
+  // together with the SH staging
+  const int64_t ic = i < n ? i : n - 1;
+  const float mx = means[3 * ic], my = means[3 * ic + 1], mz = means[3 * ic + 2];
+  float q[4], ls[3];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) q[k] = quats[4 * ic + k];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) ls[k] = scales[3 * ic + k];
+  const float logit = opac[ic];
+  stage_rows<3 * NB>(sh, g0, n, (int64_t)3 * K, shs, LS, lane);
+  __syncthreads();
   if (i >= n) return;
   float w[16];
   load_w2c(w2c, w);
-  const float mx = means[3 * i], my = means[3 * i + 1], mz = means[3 * i + 2];
-  float q[4], ls[3];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) q[k] = quats[4 * i + k];
-#pragma unroll
-  for (int k = 0; k < 3; ++k) ls[k] = scales[3 * i + k];
   Proj p;
   project(w, mx, my, mz, q, ls, fx, fy, p);
   const bool v = (p.z > 0.01f) && (mask == nullptr || mask[i] != 0);
@@ -211,9 +243,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
   // renderer.py:40-49
   float vv[3], nrm, d[3];
   view_dir(w, mx, my, mz, vv, nrm, d);
-  constexpr int NB = (DEG + 1) * (DEG + 1);
-  float shv[3 * NB];
-  load_sh<NB>(sh + (int64_t)i * K * 3, K, shv);
+  const float* shv = shs + lane * LS;
   float col[3];
 #pragma unroll
   for (int c = 0; c < 3; ++c) {
@@ -229,7 +259,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
   colors[3 * i] = col[0];
   colors[3 * i + 1] = col[1];
   colors[3 * i + 2] = col[2];
-  if (records != nullptr) write_record(records + i * kRec, m2x, m2y, p.c00, p.c01, p.c11, opac[i], col);
+  if (records != nullptr) write_record(records + i * kRec, m2x, m2y, p.c00, p.c01, p.c11, logit, col);
 }
 
 __global__ __launch_bounds__(256) void composite_prep_kernel(int64_t n, const float* __restrict__ means2d,
@@ -290,29 +320,46 @@ __device__ inline void sh_basis_and_grad(const float* d, float* B, float (*dB)[3
   }
 }
 
+struct GaussIn {
+  float mx, my, mz, q[4], ls[3], logit;
+};
+
+__device__ inline GaussIn load_gauss(const float* __restrict__ means, const float* __restrict__ scales,
+                                     const float* __restrict__ quats, const float* __restrict__ opac, int64_t i) {
+  GaussIn a;
+  a.mx = means[3 * i];
+  a.my = means[3 * i + 1];
+  a.mz = means[3 * i + 2];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) a.q[k] = quats[4 * i + k];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) a.ls[k] = scales[3 * i + k];
+  a.logit = opac[i];
+  return a;
+}
+
+// Backward of one Gaussian.  shv: its SH row in LDS, overwritten with the SH
+// cotangent row (K triples, coefficients >= (D+1)^2 get 0); grow: its gradient record
+// in LDS.
 template <int DEG>
-__global__ __launch_bounds__(256) void preprocess_bwd_kernel(
-    int64_t n, int K, const float* __restrict__ means, const float* __restrict__ scales,
-    const float* __restrict__ quats, const float* __restrict__ opac, const float* __restrict__ sh,
-    const float* __restrict__ w2c, float fx, float fy, const float* __restrict__ grec,
-    float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_quats,
-    float* __restrict__ g_opac, float* __restrict__ g_sh) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
+__device__ inline void preprocess_bwd_one(int64_t i, int K, const GaussIn& in, const float* __restrict__ w2c,
+                                          float fx, float fy, const float* grow, float* shv,
+                                          float* __restrict__ g_means, float* __restrict__ g_scales,
+                                          float* __restrict__ g_quats, float* __restrict__ g_opac) {
   float w[16];
   load_w2c(w2c, w);
-  const float mx = means[3 * i], my = means[3 * i + 1], mz = means[3 * i + 2];
+  const float mx = in.mx, my = in.my, mz = in.mz;
   float q[4], ls[3];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) q[k] = quats[4 * i + k];
+  for (int k = 0; k < 4; ++k) q[k] = in.q[k];
 #pragma unroll
-  for (int k = 0; k < 3; ++k) ls[k] = scales[3 * i + k];
+  for (int k = 0; k < 3; ++k) ls[k] = in.ls[k];
   Proj p;
   project(w, mx, my, mz, q, ls, fx, fy, p);
 
-  const float4 ga = reinterpret_cast<const float4*>(grec + i * kRec)[0];
-  const float4 gb = reinterpret_cast<const float4*>(grec + i * kRec)[1];
-  const float4 gc = reinterpret_cast<const float4*>(grec + i * kRec)[2];
+  const float4 ga = make_float4(grow[0], grow[1], grow[2], grow[3]);
+  const float4 gb = make_float4(grow[4], grow[5], grow[6], grow[7]);
+  const float4 gc = make_float4(grow[8], grow[9], grow[10], grow[11]);
   // gradient record (sums over the Gaussian's pixels of dL/dpower times):
   // [0] dx, [1] dy, [2] dx^2, [3] dx dy, [4] dy^2, [5] 1; [6..8] dL/dcolour
   // power = -0.5 (ic00 dx^2 + 2 ic01 dx dy + ic11 dy^2), dx = px - mean2d.x
@@ -322,7 +369,7 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
   const float g_col[3] = {gb.z, gb.w, gc.x};
 
   // ---- opacity: alpha = exp(power) * sigmoid(logit); sum dL/dpower = sigmoid * dL/dsigmoid
-  const float sg = det_sigmoidf(opac[i]);
+  const float sg = det_sigmoidf(in.logit);
   g_opac[i] = gb.y * (1.0f - sg);
 
   // ---- conic <- cov2D (rasterizer.py:147-153)
@@ -388,8 +435,6 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
   float vv[3], nrm, d[3];
   view_dir(w, mx, my, mz, vv, nrm, d);
   constexpr int NB = (DEG + 1) * (DEG + 1);
-  float shv[3 * NB];
-  load_sh<NB>(sh + (int64_t)i * K * 3, K, shv);
   float g_pre[3];
 #pragma unroll
   for (int c = 0; c < 3; ++c) {
@@ -400,34 +445,17 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
   float B[16], dB[16][3];
   sh_basis_and_grad<DEG>(d, B, dB);
   float g_d[3] = {0.0f, 0.0f, 0.0f};
-  float gshv[48];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    if (k < NB) {
-      gshv[3 * k] = B[k] * g_pre[0];
-      gshv[3 * k + 1] = B[k] * g_pre[1];
-      gshv[3 * k + 2] = B[k] * g_pre[2];
-      const float sk = (shv[3 * k] * g_pre[0] + shv[3 * k + 1] * g_pre[1]) + shv[3 * k + 2] * g_pre[2];
-      g_d[0] += sk * dB[k][0];
-      g_d[1] += sk * dB[k][1];
-      g_d[2] += sk * dB[k][2];
-    } else {
-      gshv[3 * k] = gshv[3 * k + 1] = gshv[3 * k + 2] = 0.0f;
-    }
+  for (int k = 0; k < NB; ++k) {
+    const float sk = (shv[3 * k] * g_pre[0] + shv[3 * k + 1] * g_pre[1]) + shv[3 * k + 2] * g_pre[2];
+    g_d[0] += sk * dB[k][0];
+    g_d[1] += sk * dB[k][1];
+    g_d[2] += sk * dB[k][2];
+    shv[3 * k] = B[k] * g_pre[0];
+    shv[3 * k + 1] = B[k] * g_pre[1];
+    shv[3 * k + 2] = B[k] * g_pre[2];
   }
-  // the whole row of K triples is written (coefficients >= NB get 0)
-  float* gsh = g_sh + (int64_t)i * K * 3;
-  if ((K & 3) == 0) {
-    float4* g4 = reinterpret_cast<float4*>(gsh);
-    const int nq = 3 * K / 4;
-#pragma unroll
-    for (int q = 0; q < 12; ++q)
-      if (q < nq) g4[q] = make_float4(gshv[4 * q], gshv[4 * q + 1], gshv[4 * q + 2], gshv[4 * q + 3]);
-  } else {
-#pragma unroll
-    for (int q = 0; q < 48; ++q)
-      if (q < 3 * K) gsh[q] = gshv[q];
-  }
+  for (int q = 3 * NB; q < 3 * K; ++q) shv[q] = 0.0f;
   if (DEG > 0) {
     const float dg = (d[0] * g_d[0] + d[1] * g_d[1]) + d[2] * g_d[2];
 #pragma unroll
@@ -476,6 +504,46 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
   const float qd = ((p.qn[0] * gq[0] + p.qn[1] * gq[1]) + p.qn[2] * gq[2]) + p.qn[3] * gq[3];
 #pragma unroll
   for (int k = 0; k < 4; ++k) g_quats[4 * i + k] = (gq[k] - p.qn[k] * qd) / p.qnorm;
+}
+
+// One wave per 64 Gaussians: the SH rows and gradient records are staged into LDS
+// with coalesced loads, and the SH cotangent rows leave through the same LDS rows
+// with coalesced stores (rows of K <= 16 triples, odd row stride 49).
+template <int DEG>
+__global__ __launch_bounds__(64) void preprocess_bwd_kernel(
+    int64_t n, int K, const float* __restrict__ means, const float* __restrict__ scales,
+    const float* __restrict__ quats, const float* __restrict__ opac, const float* __restrict__ sh,
+    const float* __restrict__ w2c, float fx, float fy, const float* __restrict__ grec,
+    float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_quats,
+    float* __restrict__ g_opac, float* __restrict__ g_sh) {
+  constexpr int NB = (DEG + 1) * (DEG + 1);
+  constexpr int LS = 49, LG = 13;
+  __shared__ float shs[64 * LS];
+  __shared__ float grs[64 * LG];
+  const int lane = threadIdx.x;
+  const int64_t g0 = (int64_t)blockIdx.x * 64;
+  const int KC = 3 * K;
+  const int64_t i = g0 + lane;
+  // per-Gaussian inputs first (clamped index) so that their loads overlap the staging
+  const GaussIn in = load_gauss(means, scales, quats, opac, i < n ? i : n - 1);
+  stage_rows<3 * NB>(sh, g0, n, (int64_t)KC, shs, LS, lane);
+  stage_rows<kRec>(grec, g0, n, (int64_t)kRec, grs, LG, lane);
+  __syncthreads();
+  if (i < n)
+    preprocess_bwd_one<DEG>(i, K, in, w2c, fx, fy, grs + lane * LG, shs + lane * LS, g_means, g_scales, g_quats,
+                            g_opac);
+  __syncthreads();
+  // rows g0.. are contiguous in g_sh: consecutive lanes store consecutive floats.
+  // Row of element e: e / KC computed as floor((e + 0.5) / KC) in float, exact since
+  // (e + 0.5) / KC is at least 0.5 / KC away from an integer and e < 3072.
+  const float inv = 1.0f / (float)KC;
+  const int64_t rows = n - g0 < 64 ? n - g0 : 64;
+  const int total = (int)rows * KC;
+  float* dst = g_sh + g0 * KC;
+  for (int e = lane; e < total; e += 64) {
+    const int r = (int)(((float)e + 0.5f) * inv);
+    dst[e] = shs[r * LS + (e - r * KC)];
+  }
 }
 
 __global__ __launch_bounds__(256) void densify_kernel(int64_t n, const float* __restrict__ g_means,
@@ -528,7 +596,7 @@ extern "C" int gs_preprocess_fwd(void* stream, int64_t n, int sh_k, int sh_degre
   (void)width;
   (void)height;
 #define GS_PRE_FWD(D)                                                                                          \
-  hipLaunchKernelGGL(preprocess_fwd_kernel<D>, dim3(div_up(n, 256)), dim3(256), 0, (hipStream_t)stream, n, sh_k,  \
+  hipLaunchKernelGGL(preprocess_fwd_kernel<D>, dim3(div_up(n, 64)), dim3(64), 0, (hipStream_t)stream, n, sh_k,    \
                      means, scales, quats, opacities, sh_coeffs, mask, w2c, fx, fy, cx, cy, means2d, cov2d, radii, \
                      valid, depths, colors, records)
   switch (sh_degree) {
@@ -573,7 +641,7 @@ extern "C" int gs_preprocess_bwd(void* stream, int64_t n, int sh_k, int sh_degre
   (void)cx;
   (void)cy;
 #define GS_PRE_BWD(D)                                                                                          \
-  hipLaunchKernelGGL(preprocess_bwd_kernel<D>, dim3(div_up(n, 256)), dim3(256), 0, (hipStream_t)stream, n, sh_k,  \
+  hipLaunchKernelGGL(preprocess_bwd_kernel<D>, dim3(div_up(n, 64)), dim3(64), 0, (hipStream_t)stream, n, sh_k,    \
                      means, scales, quats, opacities, sh_coeffs, w2c, fx, fy, grad_records, grad_means, grad_scales, \
                      grad_quats, grad_opacities, grad_sh)
   switch (sh_degree) {
