@@ -13,25 +13,31 @@
 //                      of the first radix digit of the bucket.
 //   2. depth sort      stable LSD radix sort of the packed words by depth bucket (two
 //                      7-bit passes)  -> Gaussians in (bucket, id) order.
-//   3. superblocks     every Gaussian meets at most 5x5 "superblocks" of 4x4 tiles;
-//                      its (superblock, packed word) pairs are written in depth order
-//                      and stably sorted by superblock (two 7-bit passes) -> per
-//                      superblock the list of Gaussians touching it, in (bucket, id)
-//                      order.  Carrying the rectangle in the sorted word keeps every
-//                      later read coalesced.
+//   3. superblocks     a superblock is 8x8 tiles; a Gaussian (at most 16 tiles a side)
+//                      meets at most 3x3 of them.  Its (superblock, word) pairs are
+//                      generated on the fly from the depth-sorted words and counting-
+//                      sorted by superblock in one 8-bit radix pass (two when the image
+//                      has more than 256 superblocks) -> per superblock the list of
+//                      Gaussians touching it, in (bucket, id) order.  A Gaussian's pair
+//                      for superblock (sx, sy) is produced in slot (sx % 3, sy % 3), so
+//                      all pairs of one superblock come from the same slot and are
+//                      ranked in Gaussian order.
 //   4. tile pass       a superblock's list is cut into chunks of 256 Gaussians; a wave
-//                      takes a chunk 64 Gaussians at a time and forms 4 column and 4
-//                      row lane masks with ballots, so for each of the 16 tiles it
-//                      knows which lanes hit it.  A counting sweep gives per (chunk,
-//                      tile) counts and tile totals, one scan gives the tile ranges,
-//                      and a writing sweep stores each entry's id at
-//                      range + counts of earlier chunks + popcount(mask & lanes-below)
-//                      -- stable by construction.
+//                      takes a chunk 64 Gaussians at a time and forms 8 column and 8
+//                      row lane masks with ballots; lane u owns tile u of the
+//                      superblock and its mask (column & row) says which Gaussians of
+//                      the step hit it.  A counting sweep gives per (chunk, tile) counts,
+//                      a per-superblock scan turns them into chunk offsets and tile
+//                      totals, one scan gives the tile ranges, and a writing
+//                      sweep stores, tile by tile, the ids of the lanes in the tile's
+//                      mask at range + counts of earlier chunks + popcount(mask &
+//                      lanes-below): stable by construction, one contiguous run per
+//                      store instruction.
 //   5. stats           the renderer's health extras, computed with the range scan.
 //
-// Radix passes use one wave per workgroup over a contiguous key range (in-wave rank
-// with ballot "match any"), a per-digit spine scan across workgroups, and no
-// inter-workgroup waiting.  There are no same-address atomics.
+// Radix passes use one wave per workgroup over a contiguous range (in-wave rank with
+// ballot "match any"), a per-digit spine scan across workgroups, and no
+// inter-workgroup waiting.  There are no same-address global atomics.
 #include "gs_common.h"
 
 #include <algorithm>
@@ -39,19 +45,16 @@
 namespace gs {
 namespace {
 
-constexpr int kRadixBits = 7;
-constexpr int kRadixBins = 1 << kRadixBits;
 constexpr int kScanBlock = 256;
-constexpr int kScanItems = 16;
-constexpr int kScanTile = kScanBlock * kScanItems;  // 4096 elements per scan block
-constexpr int kMaxScanPartials = 1024 * 64;         // single-block scan of partials
-constexpr int kSB = 4;                              // superblock = 4x4 tiles
-constexpr int kSBMax = 5 * 5;                       // superblocks one Gaussian can meet
-constexpr int kChunk = 256;                         // Gaussians per chunk of the tile pass
+constexpr int kSB = 8;                            // superblock = 8x8 tiles
+constexpr int kSBSpan = 3;                        // superblocks a Gaussian meets per axis
+constexpr int kChunk = 256;                       // Gaussians per chunk of the tile pass
 constexpr int kPrepBlock = 256;
-constexpr int kPrepPer = 4;                         // Gaussians per bin_prep thread
-constexpr int kPrepSpan = kPrepBlock * kPrepPer;    // = depth-sort workgroup range
-constexpr int kBig = 1024;                          // single-block scan kernels
+constexpr int kPrepPer = 4;                       // Gaussians per bin_prep thread
+constexpr int kSpan = kPrepBlock * kPrepPer;      // Gaussians per sort workgroup
+constexpr int kBig = 1024;                        // single-block kernels
+constexpr int kDepthRB = 7;                       // depth buckets: two 7-bit digits
+constexpr int kPairRB = 8;                        // superblock ids: 8-bit digits
 
 __device__ inline uint64_t lanemask_lt() {
   const unsigned lane = threadIdx.x & 63;
@@ -81,89 +84,41 @@ __device__ inline Packed unpack(uint64_t v) {
   p.h = has ? (int)((v >> 54) & 0xF) + 1 : 0;
   return p;
 }
-__device__ inline uint32_t sb_count(const Packed& p) {
-  if (p.w == 0) return 0u;
-  const int nx = ((p.x0 + p.w - 1) >> 2) - (p.x0 >> 2) + 1;
-  const int ny = ((p.y0 + p.h - 1) >> 2) - (p.y0 >> 2) + 1;
-  return (uint32_t)(nx * ny);
+
+// Superblock rectangle [sx0, sx1] x [sy0, sy1] of a Gaussian (empty when w == 0).
+struct SBRect {
+  int sx0, sx1, sy0, sy1;
+  bool has;
+};
+__device__ inline SBRect sb_rect(const Packed& p) {
+  SBRect r;
+  r.has = p.w > 0;
+  r.sx0 = p.x0 / kSB;
+  r.sx1 = (p.x0 + p.w - 1) / kSB;
+  r.sy0 = p.y0 / kSB;
+  r.sy1 = (p.y0 + p.h - 1) / kSB;
+  return r;
 }
 
-// ---------------------------------------------------------------------------------
-// 1. per-Gaussian rectangle and depth bucket (rasterizer.py:36-51, 84-94;
-//    renderer.py:63-75 for the radius-cap statistic).  Block b handles Gaussians
-//    [b*1024, b*1024+1024), the same range as depth-sort workgroup b, and writes that
-//    workgroup's histogram of the first radix digit.
-__global__ __launch_bounds__(kPrepBlock) void bin_prep_kernel(int64_t n, const float* __restrict__ means2d,
-                                                              const float* __restrict__ radii,
-                                                              const uint8_t* __restrict__ valid,
-                                                              const float* __restrict__ depths, int W, int H, int G,
-                                                              uint32_t* __restrict__ dkey, uint64_t* __restrict__ word,
-                                                              uint32_t* __restrict__ table,
-                                                              uint32_t* __restrict__ blkstat) {
-  __shared__ uint32_t hist[kRadixBins];
-  __shared__ uint32_t wcnt[2][kPrepBlock / 64];
-  for (int d = threadIdx.x; d < kRadixBins; d += kPrepBlock) hist[d] = 0;
-  __syncthreads();
-  uint32_t capc = 0, negc = 0;
-  for (int r = 0; r < kPrepPer; ++r) {
-    const int64_t i = (int64_t)blockIdx.x * kPrepSpan + r * kPrepBlock + threadIdx.x;
-    bool cap_violation = false, negative = false;
-    if (i < n) {
-      const float mx = means2d[2 * i], my = means2d[2 * i + 1], rr = radii[i];
-      const float wm1 = (float)(W - 1), hm1 = (float)(H - 1);
-      const float minx = jmin(jmax(mx - rr, 0.0f), wm1);
-      const float maxx = jmin(jmax(mx + rr, 0.0f), wm1);
-      const float miny = jmin(jmax(my - rr, 0.0f), hm1);
-      const float maxy = jmin(jmax(my + rr, 0.0f), hm1);
-      // floor(x/16) of values in [0, W-1] (NaN only for Gaussians that are invalid).
-      const int tminx = (int)floorf(minx / 16.0f), tmaxx = (int)floorf(maxx / 16.0f);
-      const int tminy = (int)floorf(miny / 16.0f), tmaxy = (int)floorf(maxy / 16.0f);
-      const bool on_screen = (mx + rr > 0.0f) && (mx - rr < (float)W) && (my + rr > 0.0f) && (my - rr < (float)H);
-      const bool proj_valid = valid[i] != 0;
-      const bool v = proj_valid && on_screen && (tmaxx >= tminx) && (tmaxy >= tminy);
-      const int spanx = tmaxx - tminx + 1, spany = tmaxy - tminy + 1;
-      cap_violation = proj_valid && on_screen && (spanx > kOffset || spany > kOffset);
-      const uint32_t zb = float_to_bits(depths[i]);
-      negative = (zb >> 31) != 0;
-      uint32_t key = kDepthBinEmpty;
-      int w = 0, h = 0;
-      if (v) {
-        w = spanx < kOffset ? spanx : kOffset;
-        h = spany < kOffset ? spany : kOffset;
-        // v implies depth > 0.01, so the 13-bit bucket is in [3848, 8191].
-        key = (zb >> (31 - kDepthBits)) - kDepthBucketLo;
-      }
-      dkey[i] = key;
-      word[i] = pack((uint32_t)i, v ? tminx : 0, v ? tminy : 0, w, h);
-      atomicAdd(&hist[key & (kRadixBins - 1)], 1u);
-    }
-    capc += (uint32_t)__popcll(__ballot(cap_violation));
-    negc += (uint32_t)__popcll(__ballot(negative));
-  }
-  if ((threadIdx.x & 63) == 0) {
-    wcnt[0][threadIdx.x >> 6] = capc;
-    wcnt[1][threadIdx.x >> 6] = negc;
-  }
-  __syncthreads();
-  if (threadIdx.x < 2) {
-    uint32_t s = 0;
-    for (int k = 0; k < kPrepBlock / 64; ++k) s += wcnt[threadIdx.x][k];
-    blkstat[2 * (int64_t)blockIdx.x + threadIdx.x] = s;
-  }
-  for (int d = threadIdx.x; d < kRadixBins; d += kPrepBlock) table[(int64_t)d * G + blockIdx.x] = hist[d];
+// The superblock coordinate in [c0, c1] congruent to j mod 3 (at most one exists,
+// since c1 - c0 < 3); returns c1 + 1 when there is none.
+__device__ inline int slot_coord(int c0, int c1, int j) {
+  const int c = c0 + (j - c0 % kSBSpan + kSBSpan) % kSBSpan;
+  return c <= c1 ? c : c1 + 1;
 }
 
-// ---------------------------------------------------------------------------------
-// Device-wide exclusive scan of uint32 (3 phases, no inter-block waiting).
-struct LoadPlain {
-  const uint32_t* p;
-  __device__ uint32_t operator()(int64_t i) const { return p[i]; }
-};
-// Number of superblocks met by the Gaussian at depth-sorted position i.
-struct LoadSortedSB {
-  const uint64_t* word;
-  __device__ uint32_t operator()(int64_t i) const { return sb_count(unpack(word[i])); }
-};
+// Lanes (among `act` lanes) whose value d (RB bits) equals this lane's.
+template <int RB>
+__device__ inline uint64_t match_any(uint32_t d, bool act) {
+  uint64_t m = __ballot(act);
+#pragma unroll
+  for (int bb = 0; bb < RB; ++bb) {
+    const bool bit = (d >> bb) & 1u;
+    const uint64_t bm = __ballot(bit);
+    m &= bit ? bm : ~bm;
+  }
+  return m;
+}
 
 __device__ inline uint32_t wave_incl_scan(uint32_t v) {
   const int lane = threadIdx.x & 63;
@@ -196,71 +151,74 @@ __device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t* total) {
   return wbase + inc - v;
 }
 
-template <class Load>
-__global__ __launch_bounds__(kScanBlock) void scan_reduce_kernel(Load load, int64_t n,
-                                                                 uint32_t* __restrict__ partial) {
-  const int64_t base = (int64_t)blockIdx.x * kScanTile + threadIdx.x;
-  uint32_t s = 0;
-#pragma unroll
-  for (int k = 0; k < kScanItems; ++k) {
-    const int64_t i = base + (int64_t)k * kScanBlock;
-    if (i < n) s += load(i);
-  }
-  uint32_t tot;
-  block_excl_scan<kScanBlock>(s, &tot);
-  if (threadIdx.x == 0) partial[blockIdx.x] = tot;
-}
-
-// Single block: exclusive scan of nb partials in place; grand total to *total.
-__global__ __launch_bounds__(kScanBlock) void scan_partials_kernel(uint32_t* __restrict__ partial, int nb,
-                                                                   uint32_t* __restrict__ total) {
-  __shared__ uint32_t carry;
-  if (threadIdx.x == 0) carry = 0;
+// ---------------------------------------------------------------------------------
+// 1. per-Gaussian rectangle and depth bucket (rasterizer.py:36-51, 84-94;
+//    renderer.py:63-75 for the radius-cap statistic).  Block b handles Gaussians
+//    [b*1024, b*1024+1024), the range of depth-sort workgroup b, and writes that
+//    workgroup's histogram of the first radix digit.
+__global__ __launch_bounds__(kPrepBlock) void bin_prep_kernel(int64_t n, const float* __restrict__ means2d,
+                                                              const float* __restrict__ radii,
+                                                              const uint8_t* __restrict__ valid,
+                                                              const float* __restrict__ depths, int W, int H, int G,
+                                                              uint32_t* __restrict__ dkey, uint64_t* __restrict__ word,
+                                                              uint32_t* __restrict__ table,
+                                                              uint32_t* __restrict__ blkstat) {
+  constexpr int NB = 1 << kDepthRB;
+  __shared__ uint32_t hist[NB];
+  __shared__ uint32_t wcnt[2][kPrepBlock / 64];
+  for (int d = threadIdx.x; d < NB; d += kPrepBlock) hist[d] = 0;
   __syncthreads();
-  for (int b0 = 0; b0 < nb; b0 += kScanBlock) {
-    const int i = b0 + threadIdx.x;
-    const uint32_t v = i < nb ? partial[i] : 0u;
-    uint32_t tot;
-    const uint32_t ex = block_excl_scan<kScanBlock>(v, &tot);
-    const uint32_t c = carry;
-    if (i < nb) partial[i] = c + ex;
-    __syncthreads();
-    if (threadIdx.x == 0) carry = c + tot;
-    __syncthreads();
+  uint32_t capc = 0, negc = 0;
+  for (int r = 0; r < kPrepPer; ++r) {
+    const int64_t i = (int64_t)blockIdx.x * kSpan + r * kPrepBlock + threadIdx.x;
+    bool cap_violation = false, negative = false;
+    if (i < n) {
+      const float mx = means2d[2 * i], my = means2d[2 * i + 1], rr = radii[i];
+      const float wm1 = (float)(W - 1), hm1 = (float)(H - 1);
+      const float minx = jmin(jmax(mx - rr, 0.0f), wm1);
+      const float maxx = jmin(jmax(mx + rr, 0.0f), wm1);
+      const float miny = jmin(jmax(my - rr, 0.0f), hm1);
+      const float maxy = jmin(jmax(my + rr, 0.0f), hm1);
+      // floor(x/16) of values in [0, W-1] (NaN only for Gaussians that are invalid).
+      const int tminx = (int)floorf(minx / 16.0f), tmaxx = (int)floorf(maxx / 16.0f);
+      const int tminy = (int)floorf(miny / 16.0f), tmaxy = (int)floorf(maxy / 16.0f);
+      const bool on_screen = (mx + rr > 0.0f) && (mx - rr < (float)W) && (my + rr > 0.0f) && (my - rr < (float)H);
+      const bool proj_valid = valid[i] != 0;
+      const bool v = proj_valid && on_screen && (tmaxx >= tminx) && (tmaxy >= tminy);
+      const int spanx = tmaxx - tminx + 1, spany = tmaxy - tminy + 1;
+      cap_violation = proj_valid && on_screen && (spanx > kOffset || spany > kOffset);
+      const uint32_t zb = float_to_bits(depths[i]);
+      negative = (zb >> 31) != 0;
+      uint32_t key = kDepthBinEmpty;
+      int w = 0, h = 0;
+      if (v) {
+        w = spanx < kOffset ? spanx : kOffset;
+        h = spany < kOffset ? spany : kOffset;
+        // v implies depth > 0.01, so the 13-bit bucket is in [3848, 8191].
+        key = (zb >> (31 - kDepthBits)) - kDepthBucketLo;
+      }
+      dkey[i] = key;
+      word[i] = pack((uint32_t)i, v ? tminx : 0, v ? tminy : 0, w, h);
+      atomicAdd(&hist[key & (NB - 1)], 1u);
+    }
+    capc += (uint32_t)__popcll(__ballot(cap_violation));
+    negc += (uint32_t)__popcll(__ballot(negative));
   }
-  if (threadIdx.x == 0 && total != nullptr) *total = carry;
-}
-
-// Blocked layout: thread t owns elements [t*16, t*16+16) of the block's tile, so the
-// per-thread sums compose into an exclusive scan in element order.  out[n] receives
-// the grand total when total is given (out has n+1 elements then).
-template <class Load>
-__global__ __launch_bounds__(kScanBlock) void scan_down_kernel(Load load, int64_t n,
-                                                               const uint32_t* __restrict__ partial,
-                                                               uint32_t* __restrict__ out,
-                                                               const uint32_t* __restrict__ total) {
-  const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
-  uint32_t v[kScanItems];
-  uint32_t s = 0;
-#pragma unroll
-  for (int k = 0; k < kScanItems; ++k) {
-    const int64_t i = base + k;
-    v[k] = i < n ? load(i) : 0u;
-    s += v[k];
+  if ((threadIdx.x & 63) == 0) {
+    wcnt[0][threadIdx.x >> 6] = capc;
+    wcnt[1][threadIdx.x >> 6] = negc;
   }
-  uint32_t tot;
-  uint32_t run = partial[blockIdx.x] + block_excl_scan<kScanBlock>(s, &tot);
-#pragma unroll
-  for (int k = 0; k < kScanItems; ++k) {
-    const int64_t i = base + k;
-    if (i < n) out[i] = run;
-    run += v[k];
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    uint32_t s = 0;
+    for (int k = 0; k < kPrepBlock / 64; ++k) s += wcnt[threadIdx.x][k];
+    blkstat[2 * (int64_t)blockIdx.x + threadIdx.x] = s;
   }
-  if (total != nullptr && blockIdx.x == 0 && threadIdx.x == 0) out[n] = *total;
+  for (int d = threadIdx.x; d < NB; d += kPrepBlock) table[(int64_t)d * G + blockIdx.x] = hist[d];
 }
 
 // ---------------------------------------------------------------------------------
-// Stable LSD radix pass on a 7-bit digit at `shift`, keys u32 + values u64.
+// Stable LSD radix pass on an RB-bit digit at `shift`, keys u32 + values u64.
 // Workgroup g (one wave) owns keys [g*chunk, min(n,(g+1)*chunk)); chunk is fixed when
 // given, else derived from G.  n is min(*n_dev, cap) when n_dev is given.
 __device__ inline void pass_range(const uint32_t* n_dev, int64_t n_static, int64_t cap, int G, int fixed_chunk,
@@ -281,19 +239,21 @@ __device__ inline void pass_range(const uint32_t* n_dev, int64_t n_static, int64
   if (n_out) *n_out = n;
 }
 
+template <int RB>
 __global__ __launch_bounds__(64) void radix_upsweep_kernel(const uint32_t* __restrict__ keys,
                                                            const uint32_t* __restrict__ n_dev,
                                                            int64_t n_static, int64_t cap, int shift, int G,
                                                            int fixed_chunk, uint32_t* __restrict__ table) {
-  __shared__ uint32_t hist[kRadixBins];
+  constexpr int NB = 1 << RB;
+  __shared__ uint32_t hist[NB];
   const int lane = threadIdx.x;
-  for (int d = lane; d < kRadixBins; d += 64) hist[d] = 0;
+  for (int d = lane; d < NB; d += 64) hist[d] = 0;
   __syncthreads();
   int64_t begin, end;
   pass_range(n_dev, n_static, cap, G, fixed_chunk, begin, end);
-  for (int64_t i = begin + lane; i < end; i += 64) atomicAdd(&hist[(keys[i] >> shift) & (kRadixBins - 1)], 1u);
+  for (int64_t i = begin + lane; i < end; i += 64) atomicAdd(&hist[(keys[i] >> shift) & (NB - 1)], 1u);
   __syncthreads();
-  for (int d = lane; d < kRadixBins; d += 64) table[(int64_t)d * G + blockIdx.x] = hist[d];
+  for (int d = lane; d < NB; d += 64) table[(int64_t)d * G + blockIdx.x] = hist[d];
 }
 
 // One block per digit: exclusive scan of that digit's row of the table (over the G
@@ -318,22 +278,39 @@ __global__ __launch_bounds__(kScanBlock) void radix_spine_kernel(uint32_t* __res
   if (threadIdx.x == 0) digit_tot[d] = tot;
 }
 
+// Per-lane digit counters of workgroup g: base of each digit (exclusive scan of the
+// digit totals) plus the workgroup's offset within the digit.  Returns the total.
+template <int RB>
+__device__ inline uint32_t init_digit_counters(uint32_t* cnt, const uint32_t* __restrict__ table,
+                                               const uint32_t* __restrict__ digit_tot, int G, int g, int lane) {
+  constexpr int DPL = (1 << RB) / 64;  // digits per lane
+  uint32_t a[DPL], sum = 0;
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) {
+    a[k] = digit_tot[DPL * lane + k];
+    sum += a[k];
+  }
+  const uint32_t inc = wave_incl_scan(sum);
+  uint32_t base = inc - sum;
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) {
+    cnt[DPL * lane + k] = base + table[(int64_t)(DPL * lane + k) * G + g];
+    base += a[k];
+  }
+  return __shfl(inc, 63, 64);
+}
+
 constexpr int kUnroll = 4;
 
+template <int RB>
 __global__ __launch_bounds__(64) void radix_downsweep_kernel(
     const uint32_t* __restrict__ keys_in, const uint64_t* __restrict__ vals_in, const uint32_t* __restrict__ n_dev,
     int64_t n_static, int64_t cap, int shift, int G, int fixed_chunk, const uint32_t* __restrict__ table,
     const uint32_t* __restrict__ digit_tot, uint32_t* __restrict__ keys_out, uint64_t* __restrict__ vals_out) {
-  __shared__ uint32_t cnt[kRadixBins];
+  constexpr int NB = 1 << RB;
+  __shared__ uint32_t cnt[NB];
   const int lane = threadIdx.x;
-  {
-    // digit bases: exclusive scan of the digit totals (2 digits per lane)
-    const uint32_t a = digit_tot[2 * lane], b = digit_tot[2 * lane + 1];
-    const uint32_t inc = wave_incl_scan(a + b);
-    const uint32_t base = inc - (a + b);
-    cnt[2 * lane] = base + table[(int64_t)(2 * lane) * G + blockIdx.x];
-    cnt[2 * lane + 1] = base + a + table[(int64_t)(2 * lane + 1) * G + blockIdx.x];
-  }
+  init_digit_counters<RB>(cnt, table, digit_tot, G, blockIdx.x, lane);
   __syncthreads();
   int64_t begin, end, n_pass;
   pass_range(n_dev, n_static, cap, G, fixed_chunk, begin, end, &n_pass);
@@ -352,14 +329,8 @@ __global__ __launch_bounds__(64) void radix_downsweep_kernel(
     for (int u = 0; u < kUnroll; ++u) {
       const int64_t i = base + u * 64 + lane;
       const bool a = i < end;
-      const uint32_t d = (k[u] >> shift) & (kRadixBins - 1);
-      uint64_t m = __ballot(a);
-#pragma unroll
-      for (int bb = 0; bb < kRadixBits; ++bb) {
-        const bool bit = (d >> bb) & 1u;
-        const uint64_t bm = __ballot(bit);
-        m &= bit ? bm : ~bm;
-      }
+      const uint32_t d = (k[u] >> shift) & (NB - 1);
+      const uint64_t m = match_any<RB>(d, a);
       uint32_t dst = 0;
       if (a) {
         const uint64_t before = m & lt;
@@ -378,22 +349,72 @@ __global__ __launch_bounds__(64) void radix_downsweep_kernel(
 }
 
 // ---------------------------------------------------------------------------------
-// 3. (superblock, word) pairs of the Gaussian at depth-sorted position p, at off[p].
-__global__ __launch_bounds__(256) void sb_pairs_kernel(int64_t n, const uint64_t* __restrict__ word,
-                                                       const uint32_t* __restrict__ off, int64_t pcap, int SX,
-                                                       uint32_t* __restrict__ pkey, uint64_t* __restrict__ pval) {
-  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (p >= n) return;
-  const uint64_t wv = word[p];
-  const Packed g = unpack(wv);
-  if (g.w == 0) return;
-  int64_t o = off[p];
-  for (int sy = g.y0 >> 2; sy <= (g.y0 + g.h - 1) >> 2; ++sy)
-    for (int sx = g.x0 >> 2; sx <= (g.x0 + g.w - 1) >> 2; ++sx, ++o)
-      if (o < pcap) {
-        pkey[o] = (uint32_t)(sy * SX + sx);
-        pval[o] = wv;
+// 3. Superblock pairs, generated from the depth-sorted words.  Workgroup g covers
+// Gaussians [g*1024, (g+1)*1024) (depth-sorted positions); the pass sorts on the
+// low 8 bits of the superblock id.
+__global__ __launch_bounds__(256) void pair_upsweep_kernel(const uint64_t* __restrict__ words, int64_t n, int SX,
+                                                           int G, uint32_t* __restrict__ table) {
+  constexpr int NB = 1 << kPairRB;
+  __shared__ uint32_t hist[NB];
+  hist[threadIdx.x] = 0;
+  __syncthreads();
+  for (int r = 0; r < kPrepPer; ++r) {
+    const int64_t i = (int64_t)blockIdx.x * kSpan + r * 256 + threadIdx.x;
+    if (i >= n) break;
+    const SBRect b = sb_rect(unpack(words[i]));
+    if (!b.has) continue;
+    for (int sy = b.sy0; sy <= b.sy1; ++sy)
+      for (int sx = b.sx0; sx <= b.sx1; ++sx) atomicAdd(&hist[(uint32_t)(sy * SX + sx) & (NB - 1)], 1u);
+  }
+  __syncthreads();
+  table[(int64_t)threadIdx.x * G + blockIdx.x] = hist[threadIdx.x];
+}
+
+template <bool WITH_KEYS>
+__global__ __launch_bounds__(64) void pair_downsweep_kernel(const uint64_t* __restrict__ words, int64_t n, int SX,
+                                                            int G, const uint32_t* __restrict__ table,
+                                                            const uint32_t* __restrict__ digit_tot,
+                                                            uint32_t* __restrict__ keys_out,
+                                                            uint64_t* __restrict__ vals_out,
+                                                            uint32_t* __restrict__ n_pairs) {
+  constexpr int NB = 1 << kPairRB;
+  __shared__ uint32_t cnt[NB];
+  const int lane = threadIdx.x;
+  const uint32_t total = init_digit_counters<kPairRB>(cnt, table, digit_tot, G, blockIdx.x, lane);
+  if (blockIdx.x == 0 && lane == 0) *n_pairs = total;
+  __syncthreads();
+  const int64_t begin = (int64_t)blockIdx.x * kSpan;
+  const int64_t end = begin + kSpan < n ? begin + kSpan : n;
+  const uint64_t lt = lanemask_lt();
+  for (int64_t base = begin; base < end; base += 64) {
+    const int64_t i = base + lane;
+    const bool in = i < end;
+    const uint64_t wv = in ? words[i] : 0ull;
+    const SBRect b = sb_rect(unpack(wv));
+    const bool has = in && b.has;
+#pragma unroll
+    for (int jy = 0; jy < kSBSpan; ++jy) {
+      const int sy = slot_coord(b.sy0, b.sy1, jy);
+#pragma unroll
+      for (int jx = 0; jx < kSBSpan; ++jx) {
+        const int sx = slot_coord(b.sx0, b.sx1, jx);
+        const bool act = has && sx <= b.sx1 && sy <= b.sy1;
+        const uint32_t s = (uint32_t)(sy * SX + sx);
+        const uint32_t d = s & (NB - 1);
+        const uint64_t m = match_any<kPairRB>(d, act);
+        if (act) {
+          const uint64_t before = m & lt;
+          const uint32_t base_d = cnt[d];
+          const uint32_t dst = base_d + (uint32_t)__popcll(before);
+          if (before == 0) cnt[d] = base_d + (uint32_t)__popcll(m);
+          if (dst < total) {  // always true for a consistent table
+            vals_out[dst] = wv;
+            if (WITH_KEYS) keys_out[dst] = s;
+          }
+        }
       }
+    }
+  }
 }
 
 // ranges[t] = first index with key >= t (searchsorted-left), ranges[T] = count.
@@ -413,13 +434,23 @@ __global__ __launch_bounds__(256) void ranges_kernel(const uint32_t* __restrict_
   }
 }
 
-// One block: chunk count per superblock -> exclusive scan -> chunk_base[S+1] and
-// the chunk -> superblock map; also clears the tile totals.
-__global__ __launch_bounds__(kBig) void chunks_kernel(int S, const int32_t* __restrict__ sb_ranges, int64_t cmax,
+// One block: superblock ranges (from the digit totals when the pair sort had one
+// pass, digit = superblock id), chunk count per superblock -> exclusive scan ->
+// chunk_base[S+1] and the chunk -> superblock map.
+__global__ __launch_bounds__(kBig) void chunks_kernel(int S, bool from_digits, const uint32_t* __restrict__ digit_tot,
+                                                      int32_t* __restrict__ sb_ranges, int64_t cmax,
                                                       uint32_t* __restrict__ chunk_base,
-                                                      uint32_t* __restrict__ chunk_sb, uint32_t* __restrict__ n_chunks,
-                                                      int T, uint32_t* __restrict__ tot) {
-  for (int t = threadIdx.x; t < T; t += kBig) tot[t] = 0;
+                                                      uint32_t* __restrict__ chunk_sb,
+                                                      uint32_t* __restrict__ n_chunks) {
+  if (from_digits) {  // S <= 256 <= kBig
+    const int s = threadIdx.x;
+    const uint32_t c = s < S ? digit_tot[s] : 0u;
+    uint32_t sum;
+    const uint32_t ex = block_excl_scan<kBig>(c, &sum);
+    if (s < S) sb_ranges[s] = (int32_t)ex;
+    if (s == 0) sb_ranges[S] = (int32_t)sum;
+    __syncthreads();
+  }
   __shared__ uint32_t carry;
   if (threadIdx.x == 0) carry = 0;
   __syncthreads();
@@ -444,23 +475,6 @@ __global__ __launch_bounds__(kBig) void chunks_kernel(int S, const int32_t* __re
   }
 }
 
-// One wave's view of a 64-Gaussian step of a chunk: lane masks of the 4 tile columns
-// and 4 tile rows of the superblock met by each lane's rectangle.
-struct StepMasks {
-  uint64_t col[kSB], row[kSB];
-};
-
-__device__ inline StepMasks step_masks(bool act, const Packed& g, int sx, int sy) {
-  StepMasks m;
-#pragma unroll
-  for (int k = 0; k < kSB; ++k) {
-    const int tx = sx * kSB + k, ty = sy * kSB + k;
-    m.col[k] = __ballot(act && g.x0 <= tx && tx < g.x0 + g.w);
-    m.row[k] = __ballot(act && g.y0 <= ty && ty < g.y0 + g.h);
-  }
-  return m;
-}
-
 struct ChunkSpan {
   int s, sx, sy;
   uint32_t first;      // first chunk of the superblock
@@ -481,72 +495,120 @@ __device__ inline ChunkSpan chunk_span(uint32_t c, const uint32_t* __restrict__ 
   return cs;
 }
 
-// tile u of superblock (sx, sy), u = 4*(ty%4) + tx%4, or -1 outside the image
-__device__ inline int tile_of(int sx, int sy, int u, int TX, int TY) {
-  const int tx = sx * kSB + (u & 3), ty = sy * kSB + (u >> 2);
+// Lane u owns tile u of superblock (sx, sy): column u % 8, row u / 8.  Returns the
+// lanes (Gaussians of the step) whose rectangle contains that tile: 8 column and 8
+// row ballots, and each lane picks its column's and row's mask.
+__device__ inline uint64_t tile_lane_mask(bool act, const Packed& g, int sx, int sy, int lane) {
+  uint64_t cm = 0, rm = 0;
+  const int ux = lane & 7, uy = lane >> 3;
+#pragma unroll
+  for (int k = 0; k < kSB; ++k) {
+    const int tx = sx * kSB + k, ty = sy * kSB + k;
+    const uint64_t c = __ballot(act && g.x0 <= tx && tx < g.x0 + g.w);
+    const uint64_t r = __ballot(act && g.y0 <= ty && ty < g.y0 + g.h);
+    cm = ux == k ? c : cm;
+    rm = uy == k ? r : rm;
+  }
+  return cm & rm;
+}
+
+// tile of lane u of superblock (sx, sy), or -1 outside the image
+__device__ inline int tile_of(int sx, int sy, int lane, int TX, int TY) {
+  const int tx = sx * kSB + (lane & 7), ty = sy * kSB + (lane >> 3);
   return (tx < TX && ty < TY) ? ty * TX + tx : -1;
 }
 
-__device__ inline uint64_t lane_tile_mask(const StepMasks& m, int lane) {
-  uint64_t mine = 0;
-#pragma unroll
-  for (int u = 0; u < 16; ++u) mine = (lane == u) ? (m.col[u & 3] & m.row[u >> 2]) : mine;
-  return mine;
-}
-
-// 4a. counts per (chunk, tile of its superblock) -> cnt[c*16 + u]; tile totals by
-// atomics (one per chunk and tile, distinct chunks rarely share a tile).
+// 4a. counts per (chunk, tile of its superblock) -> cnt[c*64 + u].
 __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restrict__ n_chunks, int64_t cmax,
                                                          const uint32_t* __restrict__ chunk_sb,
                                                          const uint32_t* __restrict__ chunk_base,
                                                          const int32_t* __restrict__ sb_ranges, int S,
-                                                         const uint64_t* __restrict__ pval, int SX, int TX, int TY,
-                                                         uint32_t* __restrict__ cnt, uint32_t* __restrict__ tot) {
+                                                         const uint64_t* __restrict__ pval, int SX,
+                                                         uint32_t* __restrict__ cnt) {
   const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
   const uint32_t C = (uint32_t)min<int64_t>((int64_t)*n_chunks, cmax);
   for (uint32_t c = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); c < C; c += nwaves) {
     const ChunkSpan cs = chunk_span(c, chunk_sb, chunk_base, sb_ranges, S, SX);
-    uint32_t mycount = 0;  // lane u < 16 accumulates tile u
+    uint32_t mycount = 0;  // lane u counts tile u
     for (int64_t base = cs.begin; base < cs.end; base += 64) {
       const int64_t q = base + lane;
       const bool act = q < cs.end;
       const Packed g = unpack(act ? pval[q] : 0ull);
-      const StepMasks m = step_masks(act, g, cs.sx, cs.sy);
-      mycount += (uint32_t)__popcll(lane_tile_mask(m, lane));
+      mycount += (uint32_t)__popcll(tile_lane_mask(act, g, cs.sx, cs.sy, lane));
     }
-    if (lane < 16) {
-      cnt[(int64_t)c * 16 + lane] = mycount;
-      const int t = tile_of(cs.sx, cs.sy, lane, TX, TY);
-      if (t >= 0 && mycount) atomicAdd(&tot[t], mycount);
-    }
+    cnt[(int64_t)c * 64 + lane] = mycount;
   }
 }
 
-// 4b + 5. One block: ranges = exclusive scan of the tile totals, and the stats.
+// 4b. One block per superblock: per tile (lane), exclusive prefix of the counts over
+// the superblock's chunks, in place, and the tile's total.  16 waves split the
+// chunks into contiguous runs: run sums, a scan over the 16 runs, then a second walk
+// writes the prefixes.
+__global__ __launch_bounds__(kBig) void chunk_scan_kernel(const uint32_t* __restrict__ chunk_base, int SX, int TX,
+                                                          int TY, uint32_t* __restrict__ cnt,
+                                                          uint32_t* __restrict__ tot) {
+  constexpr int NW = kBig / 64;
+  __shared__ uint32_t part[NW][64];
+  const int sb = blockIdx.x;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const uint32_t c0 = chunk_base[sb], c1 = chunk_base[sb + 1];
+  const uint32_t per = (c1 - c0 + NW - 1) / NW;
+  const uint32_t a = c0 + wid * per;
+  const uint32_t b = a + per < c1 ? a + per : c1;
+  uint32_t sum = 0;
+#pragma unroll 8
+  for (uint32_t c = a; c < b; ++c) sum += cnt[(int64_t)c * 64 + lane];
+  part[wid][lane] = sum;
+  __syncthreads();
+  if (wid == 0) {
+    uint32_t run = 0;
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t v = part[w][lane];
+      part[w][lane] = run;
+      run += v;
+    }
+    const int t = tile_of(sb % SX, sb / SX, lane, TX, TY);
+    if (t >= 0) tot[t] = run;
+  }
+  __syncthreads();
+  uint32_t run = part[wid][lane];
+  for (uint32_t c = a; c < b; ++c) {
+    const uint32_t v = cnt[(int64_t)c * 64 + lane];
+    cnt[(int64_t)c * 64 + lane] = run;
+    run += v;
+  }
+}
+
+// 4c + 5. One block: ranges = exclusive scan of the tile totals (each thread a
+// contiguous run of tiles), and the stats.
 __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* __restrict__ tot, int T,
                                                                const uint32_t* __restrict__ blkstat, int nblk,
                                                                int64_t cap, int32_t* __restrict__ ranges,
                                                                int32_t* __restrict__ stats) {
-  __shared__ uint32_t carry;
   __shared__ int64_t red[7][kBig / 64];
-  if (threadIdx.x == 0) carry = 0;
   int64_t acc[7] = {0, 0, 0, 0, 0, 0, 0};  // max, ovf tiles, ovf inter, trunc tiles, trunc inter, cap, neg
-  __syncthreads();
-  for (int t0 = 0; t0 < T; t0 += kBig) {
-    const int t = t0 + threadIdx.x;
+  const int per = (T + kBig - 1) / kBig;
+  const int t0 = threadIdx.x * per;
+  uint32_t run = 0;
+  for (int k = 0; k < per; ++k) {
+    const int t = t0 + k;
     const uint32_t c = t < T ? tot[t] : 0u;
-    uint32_t sum;
-    const uint32_t ex = block_excl_scan<kBig>(c, &sum);
-    if (t < T) ranges[t] = (int32_t)(carry + ex);
+    run += c;
     acc[0] = acc[0] > (int64_t)c ? acc[0] : (int64_t)c;
     acc[1] += c > (uint32_t)kBlock;
     acc[2] += c > (uint32_t)kBlock ? c - kBlock : 0;
     acc[3] += c > (uint32_t)kMaxTileEntries;
     acc[4] += c > (uint32_t)kMaxTileEntries ? c - kMaxTileEntries : 0;
-    __syncthreads();
-    if (threadIdx.x == 0) carry += sum;
-    __syncthreads();
+  }
+  uint32_t total;
+  uint32_t pos = block_excl_scan<kBig>(run, &total);
+  for (int k = 0; k < per; ++k) {
+    const int t = t0 + k;
+    if (t < T) {
+      ranges[t] = (int32_t)pos;
+      pos += tot[t];
+    }
   }
   for (int b = threadIdx.x; b < nblk; b += kBig) {
     acc[5] += blkstat[2 * b];
@@ -569,7 +631,7 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
     int64_t r[7] = {0, 0, 0, 0, 0, 0, 0};
     for (int w = 0; w < kBig / 64; ++w)
       for (int k = 0; k < 7; ++k) r[k] = k == 0 ? (r[0] > red[0][w] ? r[0] : red[0][w]) : r[k] + red[k][w];
-    const int64_t m = carry;
+    const int64_t m = total;
     ranges[T] = (int32_t)m;
     for (int k = 0; k < GS_NUM_STATS; ++k) stats[k] = 0;
     stats[GS_STAT_N_INTERACTIONS] = (int32_t)m;
@@ -584,9 +646,10 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
   }
 }
 
-// 4c. write every entry: tile t's entries from chunk c start at ranges[t] plus the
-// counts of the superblock's earlier chunks; within a step, lane L's entry in tile u
-// is preceded by popcount(mask_u & lanes-below-L).
+// 4d. write every entry: tile t's entries from chunk c start at ranges[t] plus the
+// counts of the superblock's earlier chunks; within a step the tiles hit by any lane
+// are visited in turn, and the lanes in a tile's mask store their ids at
+// base + popcount(mask & lanes-below): one contiguous run per store.
 __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restrict__ n_chunks, int64_t cmax,
                                                          const uint32_t* __restrict__ chunk_sb,
                                                          const uint32_t* __restrict__ chunk_base,
@@ -596,49 +659,36 @@ __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restr
                                                          const int32_t* __restrict__ ranges, int64_t cap,
                                                          int32_t* __restrict__ out_gid,
                                                          int32_t* __restrict__ out_tile) {
-  __shared__ uint64_t smask[4][16];
-  __shared__ uint32_t sbase[4][16];
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
   const uint32_t C = (uint32_t)min<int64_t>((int64_t)*n_chunks, cmax);
-  const uint64_t lt = lanemask_lt();
-  for (uint32_t c = blockIdx.x * (blockDim.x / 64) + wid; c < C; c += nwaves) {
+  for (uint32_t c = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); c < C; c += nwaves) {
     const ChunkSpan cs = chunk_span(c, chunk_sb, chunk_base, sb_ranges, S, SX);
-    if (lane < 16) {
-      const int t = tile_of(cs.sx, cs.sy, lane, TX, TY);
-      uint32_t b = t >= 0 ? (uint32_t)ranges[t] : 0u;
-      for (uint32_t c2 = cs.first; c2 < c; ++c2) b += cnt[(int64_t)c2 * 16 + lane];
-      sbase[wid][lane] = b;
-    }
-    for (int64_t base = cs.begin; base < cs.end; base += 64) {
-      const int64_t q = base + lane;
+    const int t = tile_of(cs.sx, cs.sy, lane, TX, TY);
+    // lane u: next slot of tile u
+    uint32_t base = (t >= 0 ? (uint32_t)ranges[t] : 0u) + cnt[(int64_t)c * 64 + lane];
+    for (int64_t b0 = cs.begin; b0 < cs.end; b0 += 64) {
+      const int64_t q = b0 + lane;
       bool act = q < cs.end;
       const Packed g = unpack(act ? pval[q] : 0ull);
       act = act && g.gid < n_gauss;  // ids are < n by construction
-      const StepMasks m = step_masks(act, g, cs.sx, cs.sy);
-      const uint64_t mine = lane_tile_mask(m, lane);
-      if (lane < 16) smask[wid][lane] = mine;
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (act) {
-        const int ux0 = max(g.x0, cs.sx * kSB), ux1 = min(g.x0 + g.w, cs.sx * kSB + kSB);
-        const int uy0 = max(g.y0, cs.sy * kSB), uy1 = min(g.y0 + g.h, cs.sy * kSB + kSB);
-        for (int ty = uy0; ty < uy1; ++ty)
-          for (int tx = ux0; tx < ux1; ++tx) {
-            const int u = (ty - cs.sy * kSB) * kSB + (tx - cs.sx * kSB);
-            const int64_t dst = (int64_t)sbase[wid][u] + __popcll(smask[wid][u] & lt);
-            if (dst < cap) {
-              out_gid[dst] = (int32_t)g.gid;
-              if (out_tile) out_tile[dst] = ty * TX + tx;
-            }
+      const uint64_t mine = tile_lane_mask(act, g, cs.sx, cs.sy, lane);
+      uint64_t tiles = __ballot(mine != 0ull && t >= 0);
+      while (tiles != 0ull) {
+        const int u = __builtin_ctzll(tiles);
+        tiles &= tiles - 1ull;
+        const uint64_t m = ((uint64_t)__builtin_amdgcn_readlane((uint32_t)(mine >> 32), u) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane((uint32_t)mine, u);
+        const uint32_t b = __builtin_amdgcn_readlane(base, u);
+        if ((m >> lane) & 1ull) {
+          const int64_t dst = (int64_t)b + __popcll(m & lanemask_lt());
+          if (dst < cap) {
+            out_gid[dst] = (int32_t)g.gid;
+            if (out_tile) out_tile[dst] = (cs.sy * kSB + (u >> 3)) * TX + cs.sx * kSB + (u & 7);
           }
+        }
       }
-      __builtin_amdgcn_wave_barrier();
-      if (lane < 16) sbase[wid][lane] += (uint32_t)__popcll(mine);
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      base += (uint32_t)__popcll(mine);
     }
   }
 }
@@ -652,10 +702,11 @@ __global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
 struct BinPlan {
   int64_t n, cap, pcap, cmax;
   int T, TX, TY, SX, SY, S;
-  int G_d, G_p;  // radix grids for the depth sort and the superblock sort
-  int sb_passes;
-  size_t o_dkey, o_word, o_ka, o_wa, o_kb, o_wb, o_off, o_part, o_table, o_dtot, o_scal, o_pk0, o_pv0, o_pk1,
-      o_pv1, o_sbr, o_cbase, o_csb, o_cnt, o_tot, o_blk, total;
+  int G_d;        // sort workgroups over Gaussians (depth passes and the first pair pass)
+  int G_p;        // workgroups of the second pair pass
+  int sb_passes;  // 1 when S <= 256, else 2
+  size_t o_dkey, o_word, o_ka, o_wa, o_kb, o_wb, o_table, o_dtot, o_scal, o_pk0, o_pv0, o_pk1, o_pv1, o_sbr,
+      o_cbase, o_csb, o_cnt, o_tot, o_blk, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -670,15 +721,14 @@ BinPlan make_plan(int64_t n, int width, int height, int64_t capacity) {
   P.SX = (P.TX + kSB - 1) / kSB;
   P.SY = (P.TY + kSB - 1) / kSB;
   P.S = P.SX * P.SY;
-  int bits = 1;
-  while ((1 << bits) < P.S) ++bits;
-  P.sb_passes = (bits + kRadixBits - 1) / kRadixBits;
+  P.sb_passes = P.S <= (1 << kPairRB) ? 1 : 2;
   const int64_t nn = std::max<int64_t>(n, 1);
-  P.pcap = kSBMax * nn;
+  P.pcap = (int64_t)kSBSpan * kSBSpan * nn;
   P.cmax = (P.pcap + kChunk - 1) / kChunk + P.S;
-  P.G_d = (int)((nn + kPrepSpan - 1) / kPrepSpan);
+  P.G_d = (int)((nn + kSpan - 1) / kSpan);
   P.G_p = (int)std::min<int64_t>(8192, std::max<int64_t>(1, (2 * nn + 1023) / 1024));
-  const int64_t tbl = (int64_t)kRadixBins * std::max(P.G_d, P.G_p);
+  const int64_t tbl = (int64_t)(1 << kPairRB) * std::max(P.G_d, P.G_p);
+  const bool two = P.sb_passes == 2;
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -691,55 +741,37 @@ BinPlan make_plan(int64_t n, int width, int height, int64_t capacity) {
   P.o_wa = take(nn * 8);
   P.o_kb = take(nn * 4);
   P.o_wb = take(nn * 8);
-  P.o_off = take((nn + 1) * 4);
-  P.o_part = take((size_t)div_up(nn, kScanTile) * 4 + 64);
   P.o_table = take((size_t)tbl * 4);
-  P.o_dtot = take(kRadixBins * 4);
+  P.o_dtot = take((1 << kPairRB) * 4);
   P.o_scal = take(256);  // device scalars: [0] pairs, [1] chunks
-  P.o_pk0 = take((size_t)P.pcap * 4);
+  P.o_pk0 = take(two ? (size_t)P.pcap * 4 : 0);
   P.o_pv0 = take((size_t)P.pcap * 8);
-  P.o_pk1 = take((size_t)P.pcap * 4);
-  P.o_pv1 = take((size_t)P.pcap * 8);
+  P.o_pk1 = take(two ? (size_t)P.pcap * 4 : 0);
+  P.o_pv1 = take(two ? (size_t)P.pcap * 8 : 0);
   P.o_sbr = take(((size_t)P.S + 1) * 4);
   P.o_cbase = take(((size_t)P.S + 1) * 4);
   P.o_csb = take((size_t)P.cmax * 4);
-  P.o_cnt = take((size_t)P.cmax * 16 * 4);
+  P.o_cnt = take((size_t)P.cmax * 64 * 4);
   P.o_tot = take((size_t)P.T * 4);
   P.o_blk = take((size_t)P.G_d * 2 * 4);
   P.total = o;
   return P;
 }
 
-template <class Load>
-int run_scan(hipStream_t s, Load load, int64_t n, uint32_t* partial, uint32_t* out, uint32_t* total) {
-  const int nb = div_up(std::max<int64_t>(n, 1), kScanTile);
-  if (nb > kMaxScanPartials) {
-    set_error("gs_bin: scan of %lld elements exceeds the supported size", (long long)n);
-    return GS_ERR_INVALID;
-  }
-  hipLaunchKernelGGL(scan_reduce_kernel<Load>, dim3(nb), dim3(kScanBlock), 0, s, load, n, partial);
-  GS_LAUNCH_CHECK("scan_reduce_kernel");
-  hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanBlock), 0, s, partial, nb, total);
-  GS_LAUNCH_CHECK("scan_partials_kernel");
-  hipLaunchKernelGGL(scan_down_kernel<Load>, dim3(nb), dim3(kScanBlock), 0, s, load, n, partial, out,
-                     (const uint32_t*)total);
-  GS_LAUNCH_CHECK("scan_down_kernel");
-  return GS_OK;
-}
-
 // One stable radix pass: keys_in/vals_in -> keys_out/vals_out on digit `shift`.
-// The upsweep is skipped when the table was already filled (first depth pass).
+// The upsweep is skipped when the table was already filled.
+template <int RB>
 int radix_pass(hipStream_t s, bool upsweep, const uint32_t* kin, const uint64_t* vin, uint32_t* kout, uint64_t* vout,
                const uint32_t* n_dev, int64_t n_static, int64_t cap, int shift, int G, int fixed_chunk,
                uint32_t* table, uint32_t* dtot) {
   if (upsweep) {
-    hipLaunchKernelGGL(radix_upsweep_kernel, dim3(G), dim3(64), 0, s, kin, n_dev, n_static, cap, shift, G,
+    hipLaunchKernelGGL(radix_upsweep_kernel<RB>, dim3(G), dim3(64), 0, s, kin, n_dev, n_static, cap, shift, G,
                        fixed_chunk, table);
     GS_LAUNCH_CHECK("radix_upsweep_kernel");
   }
-  hipLaunchKernelGGL(radix_spine_kernel, dim3(kRadixBins), dim3(kScanBlock), 0, s, table, G, dtot);
+  hipLaunchKernelGGL(radix_spine_kernel, dim3(1 << RB), dim3(kScanBlock), 0, s, table, G, dtot);
   GS_LAUNCH_CHECK("radix_spine_kernel");
-  hipLaunchKernelGGL(radix_downsweep_kernel, dim3(G), dim3(64), 0, s, kin, vin, n_dev, n_static, cap, shift, G,
+  hipLaunchKernelGGL(radix_downsweep_kernel<RB>, dim3(G), dim3(64), 0, s, kin, vin, n_dev, n_static, cap, shift, G,
                      fixed_chunk, table, dtot, kout, vout);
   GS_LAUNCH_CHECK("radix_downsweep_kernel");
   return GS_OK;
@@ -764,7 +796,8 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
              "gs_bin: bad image size %dx%d (each side at most 65536)", width, height);
   const BinPlan P = make_plan(n, width, height, capacity);
   GS_REQUIRE(P.cap < ((int64_t)1 << 31), "gs_bin: capacity %lld too large", (long long)P.cap);
-  GS_REQUIRE(P.sb_passes <= 2, "gs_bin: %d tiles exceed the supported 16384 superblocks", P.T);
+  GS_REQUIRE(P.S <= (1 << (2 * kPairRB)), "gs_bin: %d tiles exceed the supported 65536 superblocks of 8x8 tiles",
+             P.T);
   GS_REQUIRE(workspace != nullptr && workspace_bytes >= P.total,
              "gs_bin: workspace of %zu bytes is smaller than the %zu required", workspace_bytes, P.total);
   GS_REQUIRE(sorted_gids && ranges && stats, "gs_bin: NULL output");
@@ -777,8 +810,6 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   uint64_t* wa = (uint64_t*)(ws + P.o_wa);
   uint32_t* kb = (uint32_t*)(ws + P.o_kb);
   uint64_t* wb = (uint64_t*)(ws + P.o_wb);
-  uint32_t* off = (uint32_t*)(ws + P.o_off);
-  uint32_t* part = (uint32_t*)(ws + P.o_part);
   uint32_t* table = (uint32_t*)(ws + P.o_table);
   uint32_t* dtot = (uint32_t*)(ws + P.o_dtot);
   uint32_t* scal = (uint32_t*)(ws + P.o_scal);
@@ -807,41 +838,42 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
                      height, P.G_d, dkey, word, table, blk);
   GS_LAUNCH_CHECK("bin_prep_kernel");
   // 2. stable depth sort of the packed words (13-bit bucket: 7 + 6 bits)
-  int rc = radix_pass(s, false, dkey, word, kb, wb, nullptr, n, n, 0, P.G_d, kPrepSpan, table, dtot);
+  int rc = radix_pass<kDepthRB>(s, false, dkey, word, kb, wb, nullptr, n, n, 0, P.G_d, kSpan, table, dtot);
   if (rc != GS_OK) return rc;
-  rc = radix_pass(s, true, kb, wb, ka, wa, nullptr, n, n, kRadixBits, P.G_d, kPrepSpan, table, dtot);
+  rc = radix_pass<kDepthRB>(s, true, kb, wb, ka, wa, nullptr, n, n, kDepthRB, P.G_d, kSpan, table, dtot);
   if (rc != GS_OK) return rc;
   const uint64_t* sorted_word = wa;
-  // 3. superblock pairs in depth order, stably sorted by superblock
-  rc = run_scan(s, LoadSortedSB{sorted_word}, n, part, off, n_pairs);
-  if (rc != GS_OK) return rc;
-  hipLaunchKernelGGL(sb_pairs_kernel, dim3(div_up(n, 256)), dim3(256), 0, s, n, sorted_word, off, P.pcap, P.SX, pk0,
-                     pv0);
-  GS_LAUNCH_CHECK("sb_pairs_kernel");
-  uint32_t* sbkey = pk0;
-  uint64_t* sbval = pv0;
-  if (P.sb_passes >= 1) {
-    rc = radix_pass(s, true, pk0, pv0, pk1, pv1, n_pairs, 0, P.pcap, 0, P.G_p, 0, table, dtot);
+  // 3. superblock pairs generated from the depth order, sorted by superblock
+  hipLaunchKernelGGL(pair_upsweep_kernel, dim3(P.G_d), dim3(256), 0, s, sorted_word, n, P.SX, P.G_d, table);
+  GS_LAUNCH_CHECK("pair_upsweep_kernel");
+  hipLaunchKernelGGL(radix_spine_kernel, dim3(1 << kPairRB), dim3(kScanBlock), 0, s, table, P.G_d, dtot);
+  GS_LAUNCH_CHECK("radix_spine_kernel");
+  const uint64_t* sbval = pv0;
+  if (P.sb_passes == 1) {
+    hipLaunchKernelGGL(pair_downsweep_kernel<false>, dim3(P.G_d), dim3(64), 0, s, sorted_word, n, P.SX, P.G_d, table,
+                       dtot, nullptr, pv0, n_pairs);
+    GS_LAUNCH_CHECK("pair_downsweep_kernel");
+  } else {
+    hipLaunchKernelGGL(pair_downsweep_kernel<true>, dim3(P.G_d), dim3(64), 0, s, sorted_word, n, P.SX, P.G_d, table,
+                       dtot, pk0, pv0, n_pairs);
+    GS_LAUNCH_CHECK("pair_downsweep_kernel");
+    rc = radix_pass<kPairRB>(s, true, pk0, pv0, pk1, pv1, n_pairs, 0, P.pcap, kPairRB, P.G_p, 0, table, dtot);
     if (rc != GS_OK) return rc;
-    sbkey = pk1;
     sbval = pv1;
+    hipLaunchKernelGGL(ranges_kernel, dim3(std::min(2048, div_up(P.pcap + 1, 256))), dim3(256), 0, s, pk1, n_pairs,
+                       P.pcap, P.S, sbr);
+    GS_LAUNCH_CHECK("ranges_kernel");
   }
-  if (P.sb_passes == 2) {
-    rc = radix_pass(s, true, pk1, pv1, pk0, pv0, n_pairs, 0, P.pcap, kRadixBits, P.G_p, 0, table, dtot);
-    if (rc != GS_OK) return rc;
-    sbkey = pk0;
-    sbval = pv0;
-  }
-  hipLaunchKernelGGL(ranges_kernel, dim3(std::min(2048, div_up(P.pcap + 1, 256))), dim3(256), 0, s, sbkey, n_pairs,
-                     P.pcap, P.S, sbr);
-  GS_LAUNCH_CHECK("ranges_kernel");
   // 4. tile pass
-  hipLaunchKernelGGL(chunks_kernel, dim3(1), dim3(kBig), 0, s, P.S, sbr, P.cmax, cbase, csb, n_chunks, P.T, tot);
+  hipLaunchKernelGGL(chunks_kernel, dim3(1), dim3(kBig), 0, s, P.S, P.sb_passes == 1, dtot, sbr, P.cmax, cbase, csb,
+                     n_chunks);
   GS_LAUNCH_CHECK("chunks_kernel");
   const int pass_blocks = 2048;
   hipLaunchKernelGGL(tile_count_kernel, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, csb, cbase, sbr, P.S,
-                     sbval, P.SX, P.TX, P.TY, cnt, tot);
+                     sbval, P.SX, cnt);
   GS_LAUNCH_CHECK("tile_count_kernel");
+  hipLaunchKernelGGL(chunk_scan_kernel, dim3(P.S), dim3(kBig), 0, s, cbase, P.SX, P.TX, P.TY, cnt, tot);
+  GS_LAUNCH_CHECK("chunk_scan_kernel");
   hipLaunchKernelGGL(tile_scan_stats_kernel, dim3(1), dim3(kBig), 0, s, tot, P.T, blk, P.G_d, P.cap, ranges, stats);
   GS_LAUNCH_CHECK("tile_scan_stats_kernel");
   hipLaunchKernelGGL(tile_write_kernel, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, csb, cbase, sbr, P.S,

@@ -138,3 +138,47 @@ def test_cfg1_full_fwd_bwd(cuda):
     assert np.abs(_np(image) - img_o).max() <= IMG_TOL
     for f in FIELDS:
         assert _rel(_np(getattr(g, f).grad), gr_o[f]) <= GRAD_TOL, f
+
+
+@pytest.mark.parametrize("cfg,n,w,h", [(1, 20000, 4400, 2600), (3, 30000, 2100, 2100)])
+def test_binning_large_image(cuda, cfg, n, w, h):
+    """Images with more than 256 superblocks of 8x8 tiles (two-pass superblock sort)."""
+    sc = scenes.make_scene(cfg, n=n, width=w, height=h)
+    pre, pre_o = _check_preprocess(sc, cuda)
+    b, _ = _check_binning(sc, cuda, pre, pre_o)
+    S = (((w + 15) // 16 + 7) // 8) * (((h + 15) // 16 + 7) // 8)
+    assert S > 256
+
+
+def test_cfg3_truncated_tiles(cuda):
+    """Clustered scene whose densest tiles exceed the 4096-entry compositing cap."""
+    sc = scenes.make_scene(3, n=60000, width=320, height=180)
+    pre, pre_o = _check_preprocess(sc, cuda)
+    b, _ = _check_binning(sc, cuda, pre, pre_o)
+    assert int(_np(b["stats"])[4]) > 0  # truncated tiles present
+    image, extras, g, img_o, ex_o, gr_o = _render_both(sc, cuda)
+    assert np.abs(_np(image) - img_o).max() <= IMG_TOL
+    for f in FIELDS:
+        assert _rel(_np(getattr(g, f).grad), gr_o[f]) <= GRAD_TOL, f
+
+
+def test_cfg2_binning_full(cuda):
+    """Headline configuration (1M Gaussians, 1920x1080): preprocessing and the whole
+    entry list bit-exact against the oracle."""
+    sc = scenes.make_scene(2)
+    pre, pre_o = _check_preprocess(sc, cuda)
+    _check_binning(sc, cuda, pre, pre_o)
+
+
+def test_cfg2_band_fwd_bwd(cuda):
+    """All 1M Gaussians of the headline scene rendered into the top 1920x128 band of
+    its camera: image and gradients against the oracle."""
+    sc = scenes.make_scene(2)
+    sc["cam"] = dict(sc["cam"])
+    sc["cam"]["H"] = 128
+    sc["target"] = sc["target"][:128]
+    image, extras, g, img_o, ex_o, gr_o = _render_both(sc, cuda)
+    assert np.abs(_np(image) - img_o).max() <= IMG_TOL
+    assert int(extras["n_interactions"]) == ex_o["n_interactions"]
+    for f in FIELDS:
+        assert _rel(_np(getattr(g, f).grad), gr_o[f]) <= GRAD_TOL, f
