@@ -60,6 +60,7 @@ extern "C" {
 #define GS_STAT_RADIUS_CAP_VIOLATIONS 6
 #define GS_STAT_NEGATIVE_DEPTH 7   /* Gaussians whose depth has its sign bit set */
 #define GS_STAT_CAPACITY_EXCEEDED 8 /* 1 when n_interactions > capacity */
+#define GS_STAT_MEAN_PER_TILE 9     /* float32 bits of float(n_interactions) / num_tiles */
 #define GS_NUM_STATS 16
 
 const char* gs_last_error(void);

@@ -643,6 +643,8 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
     stats[GS_STAT_RADIUS_CAP_VIOLATIONS] = (int32_t)r[5];
     stats[GS_STAT_NEGATIVE_DEPTH] = (int32_t)r[6];
     stats[GS_STAT_CAPACITY_EXCEEDED] = m > cap ? 1 : 0;
+    // renderer.py:81: float32(n_interactions) / num_tiles
+    stats[GS_STAT_MEAN_PER_TILE] = (int32_t)float_to_bits((float)(int32_t)m / (float)T);
   }
 }
 

@@ -19,7 +19,7 @@ GS_REC_STRIDE = 12
 GS_NUM_STATS = 16
 STAT = dict(n_interactions=0, max_interactions_per_tile=1, overflow_tiles=2, overflow_interactions=3,
             truncated_tiles=4, truncated_interactions=5, radius_cap_violations=6, negative_depth=7,
-            capacity_exceeded=8)
+            capacity_exceeded=8, mean_per_tile=9)
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64

@@ -27,9 +27,16 @@ def as_mask(mask, n: int, device) -> torch.Tensor | None:
     return m.to(torch.uint8).contiguous()
 
 
+_BLACK: dict = {}
+
+
 def background_tensor(background, device) -> torch.Tensor:
     if background is None:
-        return torch.zeros(3, dtype=torch.float32, device=device)
+        # one read-only black background per device (no fill kernel per call)
+        key = str(torch.device(device))
+        if key not in _BLACK:
+            _BLACK[key] = torch.zeros(3, dtype=torch.float32, device=device)
+        return _BLACK[key]
     b = torch.as_tensor(background, dtype=torch.float32, device=device).reshape(3)
     return b.contiguous()
 

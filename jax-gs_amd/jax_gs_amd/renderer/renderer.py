@@ -36,10 +36,12 @@ class _Render(torch.autograd.Function):
                           want_tiles=False)
         image, fT, nc = composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg, residuals=True)
         ctx.static = static
+        # radii, valid and stats carry no gradient: no zero cotangents for them
+        ctx.set_materialize_grads(False)
         ctx.save_for_backward(means, scales, quats, opac, sh, w2c, bg, pre["records"], b["sorted_gids"], b["ranges"],
                               fT, nc)
         radii = pre["radii"]
-        valid = pre["valid"].bool()
+        valid = pre["valid"].view(torch.bool)  # the kernel writes 0/1 bytes
         stats = b["stats"]
         ctx.mark_non_differentiable(radii, valid, stats)
         return image, radii, valid, stats
@@ -47,6 +49,8 @@ class _Render(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g_image, _g_radii, _g_valid, _g_stats):
         W, H, fx, fy, cx, cy, sh_degree, _ = ctx.static
+        if g_image is None:
+            return None, None, None, None, None, None, None, None, None
         means, scales, quats, opac, sh, w2c, bg, rec, gids, ranges, fT, nc = ctx.saved_tensors
         dev = means.device
         n = means.shape[0]
@@ -101,7 +105,8 @@ def extras_from_stats(stats: torch.Tensor, radii: torch.Tensor, valid: torch.Ten
         "radii": radii,
         "valid_mask": valid,
         "n_interactions": n,
-        "mean_interactions_per_tile": n.to(torch.float32) / float(max(num_tiles_total, 1)),
+        # float32(n) / num_tiles, computed by the binning kernel (stats holds its bits)
+        "mean_interactions_per_tile": stats.view(torch.float32)[S["mean_per_tile"]],
         "max_interactions_per_tile": stats[S["max_interactions_per_tile"]],
         "overflow_tiles": stats[S["overflow_tiles"]],
         "overflow_interactions": stats[S["overflow_interactions"]],

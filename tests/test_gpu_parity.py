@@ -182,3 +182,24 @@ def test_cfg2_band_fwd_bwd(cuda):
     assert int(extras["n_interactions"]) == ex_o["n_interactions"]
     for f in FIELDS:
         assert _rel(_np(getattr(g, f).grad), gr_o[f]) <= GRAD_TOL, f
+
+
+@pytest.mark.parametrize("shape,offset", [((96, 128, 3), 0), ((37, 41, 3), 0), ((37, 41, 3), 1)])
+def test_l1_loss(cuda, shape, offset):
+    """losses.py:4-8: loss and its gradient seed against the oracle (vector path, odd
+    sizes, and a misaligned view that takes the scalar path)."""
+    from jax_gs_amd.training.losses import l1_loss
+
+    rng = np.random.default_rng(3)
+    count = int(np.prod(shape))
+    pred_np = rng.uniform(0, 1, count + offset).astype(np.float32)
+    tgt_np = rng.uniform(0, 1, count + offset).astype(np.float32)
+    tgt_np[offset + 5] = pred_np[offset + 5]  # a zero difference: sign 0
+    pred = torch.from_numpy(pred_np).to(cuda)[offset:].view(shape).requires_grad_(True)
+    tgt = torch.from_numpy(tgt_np).to(cuda)[offset:].view(shape)
+    loss = l1_loss(pred, tgt)
+    loss.backward()
+    want, seed = oracle.l1_loss_and_grad(pred_np[offset:].reshape(shape), tgt_np[offset:].reshape(shape))
+    got = float(loss.detach())
+    assert abs(got - float(want)) <= 1e-6 * max(1.0, abs(float(want)))
+    np.testing.assert_array_equal(_np(pred.grad), seed)
