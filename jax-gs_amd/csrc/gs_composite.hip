@@ -44,6 +44,8 @@
 // none.
 #include "gs_common.h"
 
+#include <algorithm>
+
 namespace gs {
 namespace {
 
@@ -313,7 +315,7 @@ __global__ __launch_bounds__(64) void composite_bwd_kernel(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
     const float* __restrict__ gimg, const float* __restrict__ finalT, const int32_t* __restrict__ ncontrib,
-    float* __restrict__ grec, float* __restrict__ gbg) {
+    float* __restrict__ grec) {
   constexpr int WPT = 4 / PPT;
   const int b = blockIdx.x / WPT, part = blockIdx.x % WPT;
   const int tile = tile_of_block(b, T);
@@ -330,7 +332,6 @@ __global__ __launch_bounds__(64) void composite_bwd_kernel(
   float py[PPT], Tr[PPT], g0[PPT], g1[PPT], g2[PPT], Rg[PPT];
   int kp[PPT];
   int kmax = 0;
-  float tb0 = 0.0f, tb1 = 0.0f, tb2 = 0.0f;
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
     const int yl = part * 4 * PPT + (lane >> 4) + 4 * i;
@@ -351,14 +352,6 @@ __global__ __launch_bounds__(64) void composite_bwd_kernel(
     // colour behind the last entry is the background
     Rg[i] = fmaf(bg2, g2[i], fmaf(bg1, g1[i], bg0 * g0[i]));
     kmax = max(kmax, kp[i]);
-    // dL/dbackground = sum over pixels of T_final * g
-    tb0 = fmaf(Tr[i], g0[i], tb0);
-    tb1 = fmaf(Tr[i], g1[i], tb1);
-    tb2 = fmaf(Tr[i], g2[i], tb2);
-  }
-  if (gbg != nullptr) {
-    const float s0 = wave_sum(tb0), s1 = wave_sum(tb1), s2 = wave_sum(tb2);
-    if (lane < 3) atomicAdd(&gbg[lane], lane == 0 ? s0 : (lane == 1 ? s1 : s2));
   }
   // wave-wide maximum entry count (uniform loop bound)
 #pragma unroll
@@ -435,9 +428,40 @@ __global__ __launch_bounds__(64) void composite_bwd_kernel(
   }
 }
 
-__global__ void zero_f32_kernel(float* __restrict__ p, int64_t n) {
+// Clears the gradient records (and the 3 background cotangents when given).
+__global__ void zero_grads_kernel(float4* __restrict__ p, int64_t n4, float* __restrict__ gbg) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0.0f;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int64_t i = tid; i < n4; i += stride) p[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (gbg != nullptr && tid < 3) gbg[tid] = 0.0f;
+}
+
+// dL/dbackground = sum over pixels of T_final * g (rasterizer.py:244): grid-stride
+// partial sums, a block reduction and 3 atomics per block.
+__global__ __launch_bounds__(256) void background_grad_kernel(int64_t npix, const float* __restrict__ finalT,
+                                                              const float* __restrict__ gimg,
+                                                              float* __restrict__ gbg) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f;
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < npix; p += stride) {
+    const float t = finalT[p];
+    a0 = fmaf(t, gimg[3 * p], a0);
+    a1 = fmaf(t, gimg[3 * p + 1], a1);
+    a2 = fmaf(t, gimg[3 * p + 2], a2);
+  }
+  a0 = wave_sum(a0);
+  a1 = wave_sum(a1);
+  a2 = wave_sum(a2);
+  __shared__ float ws[4][3];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) {
+    ws[wid][0] = a0;
+    ws[wid][1] = a1;
+    ws[wid][2] = a2;
+  }
+  __syncthreads();
+  if (threadIdx.x < 3)
+    atomicAdd(&gbg[threadIdx.x], (ws[0][threadIdx.x] + ws[1][threadIdx.x]) + (ws[2][threadIdx.x] + ws[3][threadIdx.x]));
 }
 
 // Large images have enough tiles to fill the GPU with one wave per tile.
@@ -482,13 +506,16 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
   GS_REQUIRE(n == 0 || n_entries == 0 || (records && sorted_gids && grad_records),
              "gs_composite_bwd: NULL records/gids");
   hipStream_t s = (hipStream_t)stream;
-  if (n > 0) {
-    hipLaunchKernelGGL(zero_f32_kernel, dim3(1024), dim3(256), 0, s, grad_records, n * kRec);
-    GS_LAUNCH_CHECK("zero_f32_kernel");
+  if (n > 0 || grad_background) {
+    hipLaunchKernelGGL(zero_grads_kernel, dim3(1024), dim3(256), 0, s, (float4*)grad_records, n * kRec / 4,
+                       grad_background);
+    GS_LAUNCH_CHECK("zero_grads_kernel");
   }
   if (grad_background) {
-    hipLaunchKernelGGL(zero_f32_kernel, dim3(1), dim3(64), 0, s, grad_background, (int64_t)3);
-    GS_LAUNCH_CHECK("zero_f32_kernel");
+    const int64_t npix = (int64_t)width * height;
+    hipLaunchKernelGGL(background_grad_kernel, dim3(std::min<int64_t>(256, div_up(npix, 256))), dim3(256), 0, s,
+                       npix, final_T, grad_image, grad_background);
+    GS_LAUNCH_CHECK("background_grad_kernel");
   }
   const int TX = (width + kTile - 1) / kTile, TY = (height + kTile - 1) / kTile;
   const int T = TX * TY;
@@ -496,11 +523,11 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
   if (pick_ppt(T) == 4) {
     hipLaunchKernelGGL(composite_bwd_kernel<4>, dim3(nblk), dim3(64), 0, s, (const float4*)records, (int)n,
                        sorted_gids, n_entries, ranges, width, height, TX, T, background, grad_image, final_T,
-                       n_contrib, grad_records, grad_background);
+                       n_contrib, grad_records);
   } else {
     hipLaunchKernelGGL(composite_bwd_kernel<1>, dim3(nblk * 4), dim3(64), 0, s, (const float4*)records, (int)n,
                        sorted_gids, n_entries, ranges, width, height, TX, T, background, grad_image, final_T,
-                       n_contrib, grad_records, grad_background);
+                       n_contrib, grad_records);
   }
   GS_LAUNCH_CHECK("composite_bwd_kernel");
   return GS_OK;

@@ -203,3 +203,22 @@ def test_l1_loss(cuda, shape, offset):
     got = float(loss.detach())
     assert abs(got - float(want)) <= 1e-6 * max(1.0, abs(float(want)))
     np.testing.assert_array_equal(_np(pred.grad), seed)
+
+
+def test_background_forward_and_grad(cuda):
+    """A coloured background (rasterizer.py:244, C + T * bg) and its cotangent."""
+    sc = scenes.make_scene(1, n=4000, width=200, height=150)
+    bg_np = np.array([0.2, 0.5, 0.9], np.float32)
+    g, cam, _, _ = scenes.to_torch(sc, cuda)
+    for f in FIELDS:
+        getattr(g, f).requires_grad_(True)
+    bg = torch.from_numpy(bg_np).to(cuda).requires_grad_(True)
+    image, _ = render(g, cam, background=bg, sh_degree=sc["sh_degree"])
+    img_o, _, res = oracle.render(sc["params"], sc["cam"], background=bg_np, sh_degree=sc["sh_degree"])
+    assert np.abs(_np(image) - img_o).max() <= IMG_TOL
+    seed = np.random.default_rng(5).normal(0, 1, img_o.shape).astype(np.float32)
+    image.backward(torch.from_numpy(seed).to(cuda))
+    gr_o = oracle.render_vjp(sc["params"], sc["cam"], res, seed, sh_degree=sc["sh_degree"])
+    assert _rel(_np(bg.grad), gr_o["background"]) <= GRAD_TOL
+    for f in FIELDS:
+        assert _rel(_np(getattr(g, f).grad), gr_o[f]) <= GRAD_TOL, f
