@@ -51,7 +51,8 @@ constexpr int kSBSpan = 3;                        // superblocks a Gaussian meet
 constexpr int kChunk = 256;                       // Gaussians per chunk of the tile pass
 constexpr int kPrepBlock = 256;
 constexpr int kPrepPer = 4;                       // Gaussians per bin_prep thread
-constexpr int kSpan = kPrepBlock * kPrepPer;      // Gaussians per sort workgroup
+constexpr int kSpan = kPrepBlock * kPrepPer;      // Gaussians per depth-sort workgroup
+constexpr int kPairSpan = 256;                    // Gaussians per superblock-sort workgroup
 constexpr int kBig = 1024;                        // single-block kernels
 constexpr int kDepthRB = 7;                       // depth buckets: two 7-bit digits
 constexpr int kPairRB = 8;                        // superblock ids: 8-bit digits
@@ -257,24 +258,37 @@ __global__ __launch_bounds__(64) void radix_upsweep_kernel(const uint32_t* __res
 }
 
 // One block per digit: exclusive scan of that digit's row of the table (over the G
-// workgroups) in place, and the digit's total.
+// workgroups) in place, and the digit's total.  Rows of up to kSpineMax entries move
+// through LDS with coalesced loads and stores; each thread scans a contiguous run.
+constexpr int kSpineMax = 8192;
 __global__ __launch_bounds__(kScanBlock) void radix_spine_kernel(uint32_t* __restrict__ table, int G,
                                                                  uint32_t* __restrict__ digit_tot) {
+  __shared__ uint32_t row_s[kSpineMax];
   const int d = blockIdx.x;
   uint32_t* row = table + (int64_t)d * G;
+  const bool staged = G <= kSpineMax;
+  uint32_t* r = staged ? row_s : row;
+  if (staged) {
+    for (int k = threadIdx.x; k < G; k += kScanBlock) row_s[k] = row[k];
+    __syncthreads();
+  }
   const int per = (G + kScanBlock - 1) / kScanBlock;
   const int b0 = threadIdx.x * per;
   uint32_t s = 0;
   for (int k = 0; k < per; ++k)
-    if (b0 + k < G) s += row[b0 + k];
+    if (b0 + k < G) s += r[b0 + k];
   uint32_t tot;
   uint32_t run = block_excl_scan<kScanBlock>(s, &tot);
   for (int k = 0; k < per; ++k)
     if (b0 + k < G) {
-      const uint32_t v = row[b0 + k];
-      row[b0 + k] = run;
+      const uint32_t v = r[b0 + k];
+      r[b0 + k] = run;
       run += v;
     }
+  if (staged) {
+    __syncthreads();
+    for (int k = threadIdx.x; k < G; k += kScanBlock) row[k] = row_s[k];
+  }
   if (threadIdx.x == 0) digit_tot[d] = tot;
 }
 
@@ -350,21 +364,21 @@ __global__ __launch_bounds__(64) void radix_downsweep_kernel(
 
 // ---------------------------------------------------------------------------------
 // 3. Superblock pairs, generated from the depth-sorted words.  Workgroup g covers
-// Gaussians [g*1024, (g+1)*1024) (depth-sorted positions); the pass sorts on the
-// low 8 bits of the superblock id.
+// Gaussians [g*256, (g+1)*256) (depth-sorted positions); the pass sorts on the low
+// 8 bits of the superblock id.
 __global__ __launch_bounds__(256) void pair_upsweep_kernel(const uint64_t* __restrict__ words, int64_t n, int SX,
                                                            int G, uint32_t* __restrict__ table) {
   constexpr int NB = 1 << kPairRB;
   __shared__ uint32_t hist[NB];
   hist[threadIdx.x] = 0;
   __syncthreads();
-  for (int r = 0; r < kPrepPer; ++r) {
-    const int64_t i = (int64_t)blockIdx.x * kSpan + r * 256 + threadIdx.x;
-    if (i >= n) break;
+  static_assert(kPairSpan == 256, "one Gaussian per thread");
+  const int64_t i = (int64_t)blockIdx.x * kPairSpan + threadIdx.x;
+  if (i < n) {
     const SBRect b = sb_rect(unpack(words[i]));
-    if (!b.has) continue;
-    for (int sy = b.sy0; sy <= b.sy1; ++sy)
-      for (int sx = b.sx0; sx <= b.sx1; ++sx) atomicAdd(&hist[(uint32_t)(sy * SX + sx) & (NB - 1)], 1u);
+    if (b.has)
+      for (int sy = b.sy0; sy <= b.sy1; ++sy)
+        for (int sx = b.sx0; sx <= b.sx1; ++sx) atomicAdd(&hist[(uint32_t)(sy * SX + sx) & (NB - 1)], 1u);
   }
   __syncthreads();
   table[(int64_t)threadIdx.x * G + blockIdx.x] = hist[threadIdx.x];
@@ -383,8 +397,8 @@ __global__ __launch_bounds__(64) void pair_downsweep_kernel(const uint64_t* __re
   const uint32_t total = init_digit_counters<kPairRB>(cnt, table, digit_tot, G, blockIdx.x, lane);
   if (blockIdx.x == 0 && lane == 0) *n_pairs = total;
   __syncthreads();
-  const int64_t begin = (int64_t)blockIdx.x * kSpan;
-  const int64_t end = begin + kSpan < n ? begin + kSpan : n;
+  const int64_t begin = (int64_t)blockIdx.x * kPairSpan;
+  const int64_t end = begin + kPairSpan < n ? begin + kPairSpan : n;
   const uint64_t lt = lanemask_lt();
   for (int64_t base = begin; base < end; base += 64) {
     const int64_t i = base + lane;
@@ -440,38 +454,61 @@ __global__ __launch_bounds__(256) void ranges_kernel(const uint32_t* __restrict_
 __global__ __launch_bounds__(kBig) void chunks_kernel(int S, bool from_digits, const uint32_t* __restrict__ digit_tot,
                                                       int32_t* __restrict__ sb_ranges, int64_t cmax,
                                                       uint32_t* __restrict__ chunk_base,
-                                                      uint32_t* __restrict__ chunk_sb,
-                                                      uint32_t* __restrict__ n_chunks) {
-  if (from_digits) {  // S <= 256 <= kBig
-    const int s = threadIdx.x;
-    const uint32_t c = s < S ? digit_tot[s] : 0u;
-    uint32_t sum;
-    const uint32_t ex = block_excl_scan<kBig>(c, &sum);
-    if (s < S) sb_ranges[s] = (int32_t)ex;
-    if (s == 0) sb_ranges[S] = (int32_t)sum;
-    __syncthreads();
+                                                      uint32_t* __restrict__ chunk_sb, uint32_t* __restrict__ n_chunks) {
+  __shared__ uint32_t cb[kBig + 1];  // chunk bases, when S <= kBig
+  __shared__ uint32_t carry_p, carry_c;
+  if (threadIdx.x == 0) {
+    carry_p = 0;
+    carry_c = 0;
   }
-  __shared__ uint32_t carry;
-  if (threadIdx.x == 0) carry = 0;
   __syncthreads();
   for (int s0 = 0; s0 < S; s0 += kBig) {
-    const int s = s0 + threadIdx.x;
-    uint32_t nc = 0;
-    if (s < S) nc = (uint32_t)((sb_ranges[s + 1] - sb_ranges[s] + kChunk - 1) / kChunk);
+    const int sb = s0 + threadIdx.x;
+    uint32_t lo = 0, hi = 0;
+    if (from_digits) {  // S <= 256: one iteration
+      const uint32_t c = sb < S ? digit_tot[sb] : 0u;
+      uint32_t sum;
+      lo = carry_p + block_excl_scan<kBig>(c, &sum);
+      hi = lo + c;
+      if (sb < S) sb_ranges[sb] = (int32_t)lo;
+      if (sb == S - 1) sb_ranges[S] = (int32_t)hi;
+    } else if (sb < S) {
+      lo = (uint32_t)sb_ranges[sb];
+      hi = (uint32_t)sb_ranges[sb + 1];
+    }
+    const uint32_t nc = sb < S ? (hi - lo + kChunk - 1) / kChunk : 0u;
     uint32_t sum;
-    const uint32_t ex = block_excl_scan<kBig>(nc, &sum);
-    const uint32_t c0 = carry + ex;
-    if (s < S) {
-      chunk_base[s] = c0;
-      for (uint32_t c = c0; c < c0 + nc && (int64_t)c < cmax; ++c) chunk_sb[c] = (uint32_t)s;
+    const uint32_t c0 = carry_c + block_excl_scan<kBig>(nc, &sum);
+    if (sb < S) {
+      chunk_base[sb] = c0;
+      if (S <= kBig) {
+        cb[sb] = c0;
+      } else {
+        for (uint32_t c = c0; c < c0 + nc && (int64_t)c < cmax; ++c) chunk_sb[c] = (uint32_t)sb;
+      }
     }
     __syncthreads();
-    if (threadIdx.x == 0) carry += sum;
+    if (threadIdx.x == 0) carry_c += sum;
     __syncthreads();
   }
+  const uint32_t total = carry_c;
   if (threadIdx.x == 0) {
-    chunk_base[S] = carry;
-    *n_chunks = carry;
+    chunk_base[S] = total;
+    *n_chunks = total;
+  }
+  if (S <= kBig) {
+    if (threadIdx.x == 0) cb[S] = total;
+    __syncthreads();
+    // chunk j belongs to the last superblock whose base is <= j
+    const uint32_t lim = (int64_t)total < cmax ? total : (uint32_t)cmax;
+    for (uint32_t j = threadIdx.x; j < lim; j += kBig) {
+      int lo = 0, hi = S;  // invariant: cb[lo] <= j < cb[hi]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (cb[mid] <= j) lo = mid; else hi = mid;
+      }
+      chunk_sb[j] = (uint32_t)lo;
+    }
   }
 }
 
@@ -538,45 +575,6 @@ __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restr
       mycount += (uint32_t)__popcll(tile_lane_mask(act, g, cs.sx, cs.sy, lane));
     }
     cnt[(int64_t)c * 64 + lane] = mycount;
-  }
-}
-
-// 4b. One block per superblock: per tile (lane), exclusive prefix of the counts over
-// the superblock's chunks, in place, and the tile's total.  16 waves split the
-// chunks into contiguous runs: run sums, a scan over the 16 runs, then a second walk
-// writes the prefixes.
-__global__ __launch_bounds__(kBig) void chunk_scan_kernel(const uint32_t* __restrict__ chunk_base, int SX, int TX,
-                                                          int TY, uint32_t* __restrict__ cnt,
-                                                          uint32_t* __restrict__ tot) {
-  constexpr int NW = kBig / 64;
-  __shared__ uint32_t part[NW][64];
-  const int sb = blockIdx.x;
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const uint32_t c0 = chunk_base[sb], c1 = chunk_base[sb + 1];
-  const uint32_t per = (c1 - c0 + NW - 1) / NW;
-  const uint32_t a = c0 + wid * per;
-  const uint32_t b = a + per < c1 ? a + per : c1;
-  uint32_t sum = 0;
-#pragma unroll 8
-  for (uint32_t c = a; c < b; ++c) sum += cnt[(int64_t)c * 64 + lane];
-  part[wid][lane] = sum;
-  __syncthreads();
-  if (wid == 0) {
-    uint32_t run = 0;
-    for (int w = 0; w < NW; ++w) {
-      const uint32_t v = part[w][lane];
-      part[w][lane] = run;
-      run += v;
-    }
-    const int t = tile_of(sb % SX, sb / SX, lane, TX, TY);
-    if (t >= 0) tot[t] = run;
-  }
-  __syncthreads();
-  uint32_t run = part[wid][lane];
-  for (uint32_t c = a; c < b; ++c) {
-    const uint32_t v = cnt[(int64_t)c * 64 + lane];
-    cnt[(int64_t)c * 64 + lane] = run;
-    run += v;
   }
 }
 
@@ -648,6 +646,45 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
   }
 }
 
+// 4b. One block per superblock: per tile (lane), exclusive prefix of the counts over
+// the superblock's chunks, in place, and the tile's total.  16 waves split the
+// chunks into contiguous runs: run sums, a scan over the 16 runs, then a second walk
+// writes the prefixes.
+__global__ __launch_bounds__(kBig) void chunk_scan_kernel(const uint32_t* __restrict__ chunk_base, int SX, int TX,
+                                                          int TY, uint32_t* __restrict__ cnt,
+                                                          uint32_t* __restrict__ tot) {
+  constexpr int NW = kBig / 64;
+  __shared__ uint32_t part[NW][64];
+  const int sb = blockIdx.x;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const uint32_t c0 = chunk_base[sb], c1 = chunk_base[sb + 1];
+  const uint32_t per = (c1 - c0 + NW - 1) / NW;
+  const uint32_t a = c0 + wid * per;
+  const uint32_t b = a + per < c1 ? a + per : c1;
+  uint32_t sum = 0;
+#pragma unroll 8
+  for (uint32_t c = a; c < b; ++c) sum += cnt[(int64_t)c * 64 + lane];
+  part[wid][lane] = sum;
+  __syncthreads();
+  if (wid == 0) {
+    uint32_t run = 0;
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t v = part[w][lane];
+      part[w][lane] = run;
+      run += v;
+    }
+    const int t = tile_of(sb % SX, sb / SX, lane, TX, TY);
+    if (t >= 0) tot[t] = run;
+  }
+  __syncthreads();
+  uint32_t run = part[wid][lane];
+  for (uint32_t c = a; c < b; ++c) {
+    const uint32_t v = cnt[(int64_t)c * 64 + lane];
+    cnt[(int64_t)c * 64 + lane] = run;
+    run += v;
+  }
+}
+
 // 4d. write every entry: tile t's entries from chunk c start at ranges[t] plus the
 // counts of the superblock's earlier chunks; within a step the tiles hit by any lane
 // are visited in turn, and the lanes in a tile's mask store their ids at
@@ -704,7 +741,8 @@ __global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
 struct BinPlan {
   int64_t n, cap, pcap, cmax;
   int T, TX, TY, SX, SY, S;
-  int G_d;        // sort workgroups over Gaussians (depth passes and the first pair pass)
+  int G_d;        // depth-sort workgroups (= bin_prep blocks)
+  int G_q;        // workgroups of the first superblock pass
   int G_p;        // workgroups of the second pair pass
   int sb_passes;  // 1 when S <= 256, else 2
   size_t o_dkey, o_word, o_ka, o_wa, o_kb, o_wb, o_table, o_dtot, o_scal, o_pk0, o_pv0, o_pk1, o_pv1, o_sbr,
@@ -728,8 +766,9 @@ BinPlan make_plan(int64_t n, int width, int height, int64_t capacity) {
   P.pcap = (int64_t)kSBSpan * kSBSpan * nn;
   P.cmax = (P.pcap + kChunk - 1) / kChunk + P.S;
   P.G_d = (int)((nn + kSpan - 1) / kSpan);
+  P.G_q = (int)((nn + kPairSpan - 1) / kPairSpan);
   P.G_p = (int)std::min<int64_t>(8192, std::max<int64_t>(1, (2 * nn + 1023) / 1024));
-  const int64_t tbl = (int64_t)(1 << kPairRB) * std::max(P.G_d, P.G_p);
+  const int64_t tbl = (int64_t)(1 << kPairRB) * std::max(P.G_q, P.G_p);
   const bool two = P.sb_passes == 2;
   size_t o = 0;
   auto take = [&](size_t bytes) {
@@ -836,8 +875,8 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
     return GS_OK;
   }
   // 1. prep (+ histogram of the first depth digit)
-  hipLaunchKernelGGL(bin_prep_kernel, dim3(P.G_d), dim3(kPrepBlock), 0, s, n, means2d, radii, valid, depths, width,
-                     height, P.G_d, dkey, word, table, blk);
+  hipLaunchKernelGGL(bin_prep_kernel, dim3(P.G_d), dim3(kPrepBlock), 0, s, n, means2d, radii, valid, depths,
+                     width, height, P.G_d, dkey, word, table, blk);
   GS_LAUNCH_CHECK("bin_prep_kernel");
   // 2. stable depth sort of the packed words (13-bit bucket: 7 + 6 bits)
   int rc = radix_pass<kDepthRB>(s, false, dkey, word, kb, wb, nullptr, n, n, 0, P.G_d, kSpan, table, dtot);
@@ -846,17 +885,17 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   if (rc != GS_OK) return rc;
   const uint64_t* sorted_word = wa;
   // 3. superblock pairs generated from the depth order, sorted by superblock
-  hipLaunchKernelGGL(pair_upsweep_kernel, dim3(P.G_d), dim3(256), 0, s, sorted_word, n, P.SX, P.G_d, table);
+  hipLaunchKernelGGL(pair_upsweep_kernel, dim3(P.G_q), dim3(256), 0, s, sorted_word, n, P.SX, P.G_q, table);
   GS_LAUNCH_CHECK("pair_upsweep_kernel");
-  hipLaunchKernelGGL(radix_spine_kernel, dim3(1 << kPairRB), dim3(kScanBlock), 0, s, table, P.G_d, dtot);
+  hipLaunchKernelGGL(radix_spine_kernel, dim3(1 << kPairRB), dim3(kScanBlock), 0, s, table, P.G_q, dtot);
   GS_LAUNCH_CHECK("radix_spine_kernel");
   const uint64_t* sbval = pv0;
   if (P.sb_passes == 1) {
-    hipLaunchKernelGGL(pair_downsweep_kernel<false>, dim3(P.G_d), dim3(64), 0, s, sorted_word, n, P.SX, P.G_d, table,
+    hipLaunchKernelGGL(pair_downsweep_kernel<false>, dim3(P.G_q), dim3(64), 0, s, sorted_word, n, P.SX, P.G_q, table,
                        dtot, nullptr, pv0, n_pairs);
     GS_LAUNCH_CHECK("pair_downsweep_kernel");
   } else {
-    hipLaunchKernelGGL(pair_downsweep_kernel<true>, dim3(P.G_d), dim3(64), 0, s, sorted_word, n, P.SX, P.G_d, table,
+    hipLaunchKernelGGL(pair_downsweep_kernel<true>, dim3(P.G_q), dim3(64), 0, s, sorted_word, n, P.SX, P.G_q, table,
                        dtot, pk0, pv0, n_pairs);
     GS_LAUNCH_CHECK("pair_downsweep_kernel");
     rc = radix_pass<kPairRB>(s, true, pk0, pv0, pk1, pv1, n_pairs, 0, P.pcap, kPairRB, P.G_p, 0, table, dtot);

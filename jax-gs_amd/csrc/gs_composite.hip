@@ -513,7 +513,7 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
   }
   if (grad_background) {
     const int64_t npix = (int64_t)width * height;
-    hipLaunchKernelGGL(background_grad_kernel, dim3(std::min<int64_t>(256, div_up(npix, 256))), dim3(256), 0, s,
+    hipLaunchKernelGGL(background_grad_kernel, dim3(std::min<int64_t>(1024, div_up(npix, 256))), dim3(256), 0, s,
                        npix, final_T, grad_image, grad_background);
     GS_LAUNCH_CHECK("background_grad_kernel");
   }
