@@ -260,6 +260,17 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
       nxt = load_rec(rec, bcast_i(gl, jn));
     }
     while (m != 0ull) {
+      // every 8 walked entries: stop when no pixel of the wave is still open
+      if (walked != 0 && (walked & 7) == 0) {
+        bool live = false;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) live = live || Tr[i] > kTMin;
+        if (__ballot(live) == 0ull) {
+          done = true;
+          break;
+        }
+      }
+      ++walked;
       const Rec e = nxt;
       const int kk = b0 + jn + 1;  // entries met so far, this one included
       m &= m - 1ull;
@@ -282,15 +293,6 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
         c2[i] = fmaf(w, e.b, c2[i]);
         Tr[i] = Tr[i] * (1.0f - al);
         cnt[i] = act ? kk : cnt[i];
-      }
-      if ((++walked & 7) == 0) {
-        bool live = false;
-#pragma unroll
-        for (int i = 0; i < PPT; ++i) live = live || Tr[i] > kTMin;
-        if (__ballot(live) == 0ull) {
-          done = true;
-          break;
-        }
       }
     }
   }
@@ -403,12 +405,13 @@ __global__ __launch_bounds__(64) void composite_bwd_kernel(
           gc1 = fmaf(w, g1[i], gc1);
           gc2 = fmaf(w, g2[i], gc2);
           const float cg = fmaf(e.b, g2[i], fmaf(e.g, g1[i], e.r * g0[i]));
-          const float dal = Tk * (cg - Rg[i]);
-          Rg[i] = fmaf(al, cg, om * Rg[i]);
+          const float dR = cg - Rg[i];
+          const float dal = Tk * dR;
+          Rg[i] = fmaf(al, dR, Rg[i]);  // alpha c.g + (1 - alpha) Rg
           Tr[i] = Tk;
           // min(araw, 0.99): the cotangent passes below the cap, half of it at a tie
           float dae = araw < 0.99f ? dal : 0.0f;
-          if (araw == 0.99f) dae = 0.5f * dal;
+          if (__builtin_expect(araw == 0.99f, 0)) dae = 0.5f * dal;
           const float dpw = dae * araw;  // d/d power (natural units)
           P += dpw;
           const float dpy = dpw * dy;
