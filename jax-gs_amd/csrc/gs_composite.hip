@@ -36,10 +36,10 @@
 // T_k = T_{k+1} / (1 - alpha_k) and the colour behind entry k projected on the
 // pixel's image cotangent g, Rg_{k-1} = alpha_k (c_k . g) + (1 - alpha_k) Rg_k, so
 // dL/dalpha_k = T_k (c_k . g - Rg_k).  Per lane the entry's power cotangents are kept
-// as sums that the lane's pixels (one column, one dx) share; the 9 sums of an entry
-// are reduce-scattered across the wave (recursive halving, so lane c ends with the
-// total of sum c) and added to the Gaussian's gradient record with one atomic
-// instruction (9 lanes).  Gradients follow JAX autodiff of the reference: the cap
+// as sums that the lane's pixels (one column, one dx) share; the 9 sums of two
+// contributing entries are reduce-scattered across the wave together (recursive
+// halving, so lane c ends with the total of sum c) and added to the Gaussians'
+// gradient records with one atomic instruction (18 lanes).  Gradients follow JAX autodiff of the reference: the cap
 // min(0.99, .) passes no gradient when it binds (half at a tie), gated entries pass
 // none.
 #include "gs_common.h"
@@ -72,11 +72,10 @@ __device__ inline float wave_sum(float v) {
   return bcast(x, 63);
 }
 
-// Reduce-scatter of 9 per-lane values over the wave by recursive halving: at level
-// k a lane keeps the half of its values whose index bit k equals its own lane bit k
-// and adds the partner's copy of them (partner = lane ^ 2^k: DPP quad_perm for
-// 1 and 2, ds_swizzle for 4, 8, 16, ds_bpermute for 32).  Afterwards lane L holds
-// the wave total of value L % 16 (values 9..15 are zero padding).
+// Reduce-scatter of per-lane values over the wave by recursive halving: at level k a
+// lane keeps the half of its values whose index bit k equals its own lane bit k and
+// adds the partner's copy of them (partner = lane ^ 2^k: DPP quad_perm for 1 and 2,
+// ds_swizzle for 4, 8, 16), then the two 32-lane halves are summed (ds_bpermute).
 __device__ inline float swz_xor(float v, int pattern_xor) {
   // ds_swizzle bit mode: and_mask 0x1F, or_mask 0, xor_mask in bits 14:10
   switch (pattern_xor) {
@@ -86,41 +85,42 @@ __device__ inline float swz_xor(float v, int pattern_xor) {
   }
 }
 
-__device__ inline float reduce_scatter9(const float* v, int lane) {
-  const bool b0 = lane & 1, b1 = lane & 2, b2 = lane & 4, b3 = lane & 8;
-  float y[5], z[3], r[2];
-  // level 0: xor 1 (quad_perm [1,0,3,2])
+// Value of the lane's partner at lane distance 2^l (l = 0..4).
+template <int L>
+__device__ inline float xor_lane(float v) {
+  if (L == 0) return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  if (L == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  return swz_xor(v, 1 << L);
+}
+
+// One halving level: pairs (2k, 2k+1) of the n values; the lane keeps the member
+// selected by its bit L and adds the partner's copy of it.
+template <int L, int N>
+__device__ inline void halve(float* cur, int lane) {
+  const bool bit = (lane >> L) & 1;
 #pragma unroll
-  for (int k = 0; k < 5; ++k) {
-    const float lo = v[2 * k];
-    const float hi = (2 * k + 1 < 9) ? v[2 * k + 1] : 0.0f;
-    const float keep = b0 ? hi : lo, send = b0 ? lo : hi;
-    y[k] = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0xB1, 0xF, 0xF, false));
+  for (int k = 0; k < (N + 1) / 2; ++k) {
+    const float lo = cur[2 * k];
+    const float hi = (2 * k + 1 < N) ? cur[2 * k + 1] : 0.0f;
+    const float keep = bit ? hi : lo, send = bit ? lo : hi;
+    cur[k] = keep + xor_lane<L>(send);
   }
-  // level 1: xor 2 (quad_perm [2,3,0,1])
+}
+
+// Reduce-scatter of NV <= 32 per-lane values: afterwards lane L holds the wave total
+// of value L % 32 (0 for L % 32 >= NV).
+template <int NV>
+__device__ inline float reduce_scatter(const float* v, int lane) {
+  float cur[NV];
 #pragma unroll
-  for (int m = 0; m < 3; ++m) {
-    const float lo = y[2 * m];
-    const float hi = (2 * m + 1 < 5) ? y[2 * m + 1] : 0.0f;
-    const float keep = b1 ? hi : lo, send = b1 ? lo : hi;
-    z[m] = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x4E, 0xF, 0xF, false));
-  }
-  // level 2: xor 4
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const float lo = z[2 * q];
-    const float hi = (2 * q + 1 < 3) ? z[2 * q + 1] : 0.0f;
-    const float keep = b2 ? hi : lo, send = b2 ? lo : hi;
-    r[q] = keep + swz_xor(send, 4);
-  }
-  // level 3: xor 8
-  float t;
-  {
-    const float keep = b3 ? r[1] : r[0], send = b3 ? r[0] : r[1];
-    t = keep + swz_xor(send, 8);
-  }
-  // levels 4, 5: full sums across the 16-lane rows
-  t = t + swz_xor(t, 16);
+  for (int k = 0; k < NV; ++k) cur[k] = v[k];
+  constexpr int N1 = (NV + 1) / 2, N2 = (N1 + 1) / 2, N3 = (N2 + 1) / 2, N4 = (N3 + 1) / 2;
+  halve<0, NV>(cur, lane);
+  halve<1, N1>(cur, lane);
+  halve<2, N2>(cur, lane);
+  halve<3, N3>(cur, lane);
+  halve<4, N4>(cur, lane);
+  float t = cur[0];
   t = t + __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __float_as_int(t)));
   return t;
 }
@@ -161,10 +161,11 @@ __device__ inline Rec load_rec(const float4* __restrict__ rec, int g) {
 }
 
 // q = log2(e) * power + log2(opacity) with (A, B, C) = log2(e) * (-ic00/2, -ic01,
-// -ic11/2); Adx2l = A dx^2 + log2(opacity) is shared by a lane's pixels.  The forward
-// and backward kernels share this exact expression.
+// -ic11/2), evaluated as (C dy + B dx) dy + (A dx^2 + log2(opacity)); the last term
+// and B dx are shared by a lane's pixels.  The forward and backward kernels share
+// this exact expression, so they gate the same (pixel, entry) pairs.
 __device__ inline float q_of(float dy, float Adx2l, float Bdx, float C) {
-  return fmaf(C * dy, dy, fmaf(Bdx, dy, Adx2l));
+  return fmaf(fmaf(C, dy, Bdx), dy, Adx2l);
 }
 
 // Ids are clamped like XLA's gather.
@@ -364,6 +365,8 @@ __global__ __launch_bounds__(64) void composite_bwd_kernel(
   // the highest down, ids from the testing lane, records by scalar loads, prefetched
   const float rx0 = (float)(tx * kTile) + 0.5f, rx1 = rx0 + (float)(kTile - 1);
   const float ry0 = (float)(ty * kTile + part * 4 * PPT) + 0.5f, ry1 = ry0 + (float)(4 * PPT - 1);
+  // survivors are walked two at a time and their 9 + 9 sums reduced together (one
+  // 18-value reduce-scatter costs fewer cross-lane steps than two 9-value ones)
   for (int b0 = (kmax - 1) & ~63; b0 >= 0; b0 -= 64) {
     int gl;
     uint64_t m = test_batch(rec, gids, start, b0, kmax, num_g, rx0, rx1, ry0, ry1, lane, &gl);
@@ -375,57 +378,76 @@ __global__ __launch_bounds__(64) void composite_bwd_kernel(
       nxt = load_rec(rec, gn);
     }
     while (m != 0ull) {
-      const Rec e = nxt;
-      const int g = gn;
-      const int k = b0 + jn;
-      m &= ~(1ull << jn);
-      if (m != 0ull) {
-        jn = 63 - __builtin_clzll(m);
-        gn = bcast_i(gl, jn);
-        nxt = load_rec(rec, gn);
-      }
-      const float dx = px - e.mx;
-      const float Adx2l = fmaf(e.A * dx, dx, e.lop), Bdx = e.B * dx;
-      // per-lane sums over the lane's pixels: P = sum dpower, Q = sum dpower*dy,
-      // V = sum dpower*dy^2, colour cotangents
-      float P = 0.0f, Q = 0.0f, V = 0.0f, gc0 = 0.0f, gc1 = 0.0f, gc2 = 0.0f;
+      float v[18];
       bool any = false;
+      int ga = 0, gb = 0;
 #pragma unroll
-      for (int i = 0; i < PPT; ++i) {
-        const float dy = py[i] - e.my;
-        const float q = q_of(dy, Adx2l, Bdx, e.C);
-        if (k < kp[i] && q > e.thr) {
-          any = true;
-          const float araw = __builtin_amdgcn_exp2f(q);
-          const float al = araw < 0.99f ? araw : 0.99f;
-          const float om = 1.0f - al;
-          const float Tk = Tr[i] * __builtin_amdgcn_rcpf(om);
-          const float w = al * Tk;
-          gc0 = fmaf(w, g0[i], gc0);
-          gc1 = fmaf(w, g1[i], gc1);
-          gc2 = fmaf(w, g2[i], gc2);
-          const float cg = fmaf(e.b, g2[i], fmaf(e.g, g1[i], e.r * g0[i]));
-          const float dR = cg - Rg[i];
-          const float dal = Tk * dR;
-          Rg[i] = fmaf(al, dR, Rg[i]);  // alpha c.g + (1 - alpha) Rg
-          Tr[i] = Tk;
-          // min(araw, 0.99): the cotangent passes below the cap, half of it at a tie
-          float dae = araw < 0.99f ? dal : 0.0f;
-          if (__builtin_expect(araw == 0.99f, 0)) dae = 0.5f * dal;
-          const float dpw = dae * araw;  // d/d power (natural units)
-          P += dpw;
-          const float dpy = dpw * dy;
-          Q += dpy;
-          V = fmaf(dpy, dy, V);
+      for (int h = 0; h < 2; ++h) {
+        // h = 1 with no survivor left: an empty second half (all sums 0)
+        const bool live = m != 0ull;
+        const Rec e = nxt;
+        const int g = gn;
+        const int k = live ? b0 + jn : -1;
+        if (live) {
+          m &= ~(1ull << jn);
+          if (m != 0ull) {
+            jn = 63 - __builtin_clzll(m);
+            gn = bcast_i(gl, jn);
+            nxt = load_rec(rec, gn);
+          }
         }
-      }
-      if (__ballot(any) != 0ull) {
+        if (h == 0) ga = g; else gb = live ? g : ga;
+        const float dx = px - e.mx;
+        const float Adx2l = fmaf(e.A * dx, dx, e.lop), Bdx = e.B * dx;
+        // per-lane sums over the lane's pixels: P = sum dpower, Q = sum dpower*dy,
+        // V = sum dpower*dy^2, colour cotangents
+        float P = 0.0f, Q = 0.0f, V = 0.0f, gc0 = 0.0f, gc1 = 0.0f, gc2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+          const float dy = py[i] - e.my;
+          const float q = q_of(dy, Adx2l, Bdx, e.C);
+          if (k >= 0 && k < kp[i] && q > e.thr) {
+            any = true;
+            const float araw = __builtin_amdgcn_exp2f(q);
+            const float al = araw < 0.99f ? araw : 0.99f;
+            const float om = 1.0f - al;
+            const float Tk = Tr[i] * __builtin_amdgcn_rcpf(om);
+            const float w = al * Tk;
+            gc0 = fmaf(w, g0[i], gc0);
+            gc1 = fmaf(w, g1[i], gc1);
+            gc2 = fmaf(w, g2[i], gc2);
+            const float cg = fmaf(e.b, g2[i], fmaf(e.g, g1[i], e.r * g0[i]));
+            const float dR = cg - Rg[i];
+            const float dal = Tk * dR;
+            Rg[i] = fmaf(al, dR, Rg[i]);  // alpha c.g + (1 - alpha) Rg
+            Tr[i] = Tk;
+            // min(araw, 0.99): the cotangent passes below the cap, half of it at a tie
+            float dae = araw < 0.99f ? dal : 0.0f;
+            if (__builtin_expect(araw == 0.99f, 0)) dae = 0.5f * dal;
+            const float dpw = dae * araw;  // d/d power (natural units)
+            P += dpw;
+            const float dpy = dpw * dy;
+            Q += dpy;
+            V = fmaf(dpy, dy, V);
+          }
+        }
         // gradient record sums: [0] dpw dx, [1] dpw dy, [2] dpw dx^2, [3] dpw dx dy,
         // [4] dpw dy^2, [5] dpw, [6..8] colour
         const float Sx = P * dx;
-        float v[9] = {Sx, Q, Sx * dx, Q * dx, V, P, gc0, gc1, gc2};
-        const float mine = reduce_scatter9(v, lane);
-        if (lane < 9 && mine != 0.0f) atomicAdd(&grec[(int64_t)g * kRec + lane], mine);
+        v[9 * h + 0] = Sx;
+        v[9 * h + 1] = Q;
+        v[9 * h + 2] = Sx * dx;
+        v[9 * h + 3] = Q * dx;
+        v[9 * h + 4] = V;
+        v[9 * h + 5] = P;
+        v[9 * h + 6] = gc0;
+        v[9 * h + 7] = gc1;
+        v[9 * h + 8] = gc2;
+      }
+      if (__ballot(any) != 0ull) {
+        const float mine = reduce_scatter<18>(v, lane);
+        if (lane < 18 && mine != 0.0f)
+          atomicAdd(&grec[(int64_t)(lane < 9 ? ga : gb) * kRec + (lane < 9 ? lane : lane - 9)], mine);
       }
     }
   }
