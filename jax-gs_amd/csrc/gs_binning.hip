@@ -686,9 +686,12 @@ __global__ __launch_bounds__(kBig) void chunk_scan_kernel(const uint32_t* __rest
 }
 
 // 4d. write every entry: tile t's entries from chunk c start at ranges[t] plus the
-// counts of the superblock's earlier chunks; within a step the tiles hit by any lane
-// are visited in turn, and the lanes in a tile's mask store their ids at
-// base + popcount(mask & lanes-below): one contiguous run per store.
+// counts of the superblock's earlier chunks; within a step the 64 tiles are visited
+// in an unrolled loop with wave-uniform masks (column & row ballots), and the lanes
+// of a tile's mask store their ids at base + popcount(mask & lanes-below): one
+// contiguous run per store.  Lane u holds tile u's next slot (read with v_readlane,
+// advanced once per step).
+template <bool WITH_TILES>
 __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restrict__ n_chunks, int64_t cmax,
                                                          const uint32_t* __restrict__ chunk_sb,
                                                          const uint32_t* __restrict__ chunk_base,
@@ -701,33 +704,53 @@ __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restr
   const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
   const uint32_t C = (uint32_t)min<int64_t>((int64_t)*n_chunks, cmax);
+  const uint32_t cap32 = (uint32_t)cap;  // gs_bin checks cap < 2^31
   for (uint32_t c = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); c < C; c += nwaves) {
     const ChunkSpan cs = chunk_span(c, chunk_sb, chunk_base, sb_ranges, S, SX);
     const int t = tile_of(cs.sx, cs.sy, lane, TX, TY);
-    // lane u: next slot of tile u
+    // lane u: next slot of tile u (tiles outside the image never get entries)
     uint32_t base = (t >= 0 ? (uint32_t)ranges[t] : 0u) + cnt[(int64_t)c * 64 + lane];
     for (int64_t b0 = cs.begin; b0 < cs.end; b0 += 64) {
       const int64_t q = b0 + lane;
       bool act = q < cs.end;
       const Packed g = unpack(act ? pval[q] : 0ull);
       act = act && g.gid < n_gauss;  // ids are < n by construction
-      const uint64_t mine = tile_lane_mask(act, g, cs.sx, cs.sy, lane);
-      uint64_t tiles = __ballot(mine != 0ull && t >= 0);
-      while (tiles != 0ull) {
-        const int u = __builtin_ctzll(tiles);
-        tiles &= tiles - 1ull;
-        const uint64_t m = ((uint64_t)__builtin_amdgcn_readlane((uint32_t)(mine >> 32), u) << 32) |
-                           (uint32_t)__builtin_amdgcn_readlane((uint32_t)mine, u);
-        const uint32_t b = __builtin_amdgcn_readlane(base, u);
-        if ((m >> lane) & 1ull) {
-          const int64_t dst = (int64_t)b + __popcll(m & lanemask_lt());
-          if (dst < cap) {
-            out_gid[dst] = (int32_t)g.gid;
-            if (out_tile) out_tile[dst] = (cs.sy * kSB + (u >> 3)) * TX + cs.sx * kSB + (u & 7);
+      // column and row masks are wave-uniform; tile (ux, uy)'s mask is their AND
+      uint64_t cm[kSB], rm[kSB];
+#pragma unroll
+      for (int k = 0; k < kSB; ++k) {
+        const int tx = cs.sx * kSB + k, ty = cs.sy * kSB + k;
+        cm[k] = __ballot(act && g.x0 <= tx && tx < g.x0 + g.w);
+        rm[k] = __ballot(act && g.y0 <= ty && ty < g.y0 + g.h);
+      }
+#pragma unroll
+      for (int uy = 0; uy < kSB; ++uy) {
+        if (rm[uy] == 0ull) continue;
+#pragma unroll
+        for (int ux = 0; ux < kSB; ++ux) {
+          const uint64_t m = cm[ux] & rm[uy];
+          if (m == 0ull) continue;
+          const uint32_t b = __builtin_amdgcn_readlane(base, uy * kSB + ux);
+          if (__builtin_amdgcn_inverse_ballot_w64(m)) {
+            // lanes of m store their ids at b + (lanes of m below them): one run
+            const uint32_t dst = b + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            if (dst < cap32) {
+              out_gid[dst] = (int32_t)g.gid;
+              if (WITH_TILES) out_tile[dst] = (cs.sy * kSB + uy) * TX + cs.sx * kSB + ux;
+            }
           }
         }
       }
-      base += (uint32_t)__popcll(mine);
+      // lane u advances tile u's slot by its count in this step
+      uint64_t mine = 0;
+      const int ux = lane & 7, uy = lane >> 3;
+#pragma unroll
+      for (int k = 0; k < kSB; ++k) mine = ux == k ? cm[k] : mine;
+      uint64_t rmine = 0;
+#pragma unroll
+      for (int k = 0; k < kSB; ++k) rmine = uy == k ? rm[k] : rmine;
+      base += (uint32_t)__popcll(mine & rmine);
     }
   }
 }
@@ -917,8 +940,12 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   GS_LAUNCH_CHECK("chunk_scan_kernel");
   hipLaunchKernelGGL(tile_scan_stats_kernel, dim3(1), dim3(kBig), 0, s, tot, P.T, blk, P.G_d, P.cap, ranges, stats);
   GS_LAUNCH_CHECK("tile_scan_stats_kernel");
-  hipLaunchKernelGGL(tile_write_kernel, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, csb, cbase, sbr, P.S,
-                     sbval, (uint32_t)n, P.SX, P.TX, P.TY, cnt, ranges, P.cap, sorted_gids, sorted_tiles);
+  if (sorted_tiles != nullptr)
+    hipLaunchKernelGGL(tile_write_kernel<true>, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, csb, cbase, sbr,
+                       P.S, sbval, (uint32_t)n, P.SX, P.TX, P.TY, cnt, ranges, P.cap, sorted_gids, sorted_tiles);
+  else
+    hipLaunchKernelGGL(tile_write_kernel<false>, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, csb, cbase, sbr,
+                       P.S, sbval, (uint32_t)n, P.SX, P.TX, P.TY, cnt, ranges, P.cap, sorted_gids, sorted_tiles);
   GS_LAUNCH_CHECK("tile_write_kernel");
   return GS_OK;
 }
