@@ -201,22 +201,35 @@ __host__ __device__ inline bool entry_misses_rect(float mx, float my, float A, f
   return fmin >= 10.25f * 1.4426950408889634f + 1e-5f * scale;
 }
 
-// Test entries [b0, b0+64) of a tile against a wave's pixel rectangle, one per lane:
-// returns the ballot of surviving entries; *gl receives the lane's (clamped) id.
-__device__ inline uint64_t test_batch(const float4* __restrict__ rec, const int32_t* __restrict__ gids, int start,
-                                      int b0, int n, int num_g, float x0, float x1, float y0, float y1, int lane,
-                                      int* gl) {
-  const int k = b0 + lane;
-  bool keep = false;
-  int g = 0;
-  if (k < n) {
-    g = clamp_gid(gids[start + k], num_g);
+// What a lane fetches to test one entry of a batch against the wave's pixel
+// rectangle: the (clamped) id, or -1 past the tile's list, and the record's centre
+// and conic.  Batches are software-pipelined: the ids of batch b+2 and the records of
+// batch b+1 are in flight while batch b is walked.
+struct Probe {
+  int g;
+  float mx, my, A, B, C;
+};
+
+__device__ inline int probe_gid(const int32_t* __restrict__ gids, int start, int k, int n, int num_g) {
+  return (k >= 0 && k < n) ? clamp_gid(gids[start + k], num_g) : -1;
+}
+
+__device__ inline Probe probe_load(const float4* __restrict__ rec, int g) {
+  Probe p{g, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  if (g >= 0) {
     const float4 a = rec[(int64_t)g * 3];
-    const float c = rec[(int64_t)g * 3 + 1].x;
-    keep = !entry_misses_rect(a.x, a.y, a.z, a.w, c, x0, x1, y0, y1);
+    p.mx = a.x;
+    p.my = a.y;
+    p.A = a.z;
+    p.B = a.w;
+    p.C = rec[(int64_t)g * 3 + 1].x;
   }
-  *gl = g;
-  return __ballot(keep);
+  return p;
+}
+
+// Ballot of the entries of a batch that survive the rectangle test.
+__device__ inline uint64_t probe_test(const Probe& p, float x0, float x1, float y0, float y1) {
+  return __ballot(p.g >= 0 && !entry_misses_rect(p.mx, p.my, p.A, p.B, p.C, x0, x1, y0, y1));
 }
 
 template <int PPT>
@@ -251,9 +264,14 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
 
   bool done = false;
   int walked = 0;
+  int g_ahead = probe_gid(gids, start, 64 + lane, n, num_g);
+  Probe p_next = probe_load(rec, probe_gid(gids, start, lane, n, num_g));
   for (int b0 = 0; b0 < n && !done; b0 += 64) {
-    int gl;
-    uint64_t m = test_batch(rec, gids, start, b0, n, num_g, rx0, rx1, ry0, ry1, lane, &gl);
+    const Probe pr = p_next;
+    p_next = probe_load(rec, g_ahead);
+    g_ahead = probe_gid(gids, start, b0 + 128 + lane, n, num_g);
+    const int gl = pr.g;
+    uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
     Rec nxt = zero_rec();
     int jn = 0;
     if (m != 0ull) {
@@ -314,7 +332,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
 }
 
 template <int PPT>
-__global__ __launch_bounds__(64) void composite_bwd_kernel(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void composite_bwd_kernel(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
     const float* __restrict__ gimg, const float* __restrict__ finalT, const int32_t* __restrict__ ncontrib,
@@ -367,9 +385,15 @@ __global__ __launch_bounds__(64) void composite_bwd_kernel(
   const float ry0 = (float)(ty * kTile + part * 4 * PPT) + 0.5f, ry1 = ry0 + (float)(4 * PPT - 1);
   // survivors are walked two at a time and their 9 + 9 sums reduced together (one
   // 18-value reduce-scatter costs fewer cross-lane steps than two 9-value ones)
-  for (int b0 = (kmax - 1) & ~63; b0 >= 0; b0 -= 64) {
-    int gl;
-    uint64_t m = test_batch(rec, gids, start, b0, kmax, num_g, rx0, rx1, ry0, ry1, lane, &gl);
+  const int btop = (kmax - 1) & ~63;
+  int g_ahead = probe_gid(gids, start, btop - 64 + lane, kmax, num_g);
+  Probe p_next = probe_load(rec, probe_gid(gids, start, btop + lane, kmax, num_g));
+  for (int b0 = btop; b0 >= 0; b0 -= 64) {
+    const Probe pr = p_next;
+    p_next = probe_load(rec, g_ahead);
+    g_ahead = probe_gid(gids, start, b0 - 128 + lane, kmax, num_g);
+    const int gl = pr.g;
+    uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
     Rec nxt = zero_rec();
     int jn = 0, gn = 0;
     if (m != 0ull) {
