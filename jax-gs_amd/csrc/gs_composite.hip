@@ -310,7 +310,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
         c0[i] = fmaf(w, e.r, c0[i]);
         c1[i] = fmaf(w, e.g, c1[i]);
         c2[i] = fmaf(w, e.b, c2[i]);
-        Tr[i] = Tr[i] * (1.0f - al);
+        Tr[i] = Tr[i] - w;  // T (1 - alpha)
         cnt[i] = act ? kk : cnt[i];
       }
     }
