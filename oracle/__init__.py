@@ -228,6 +228,27 @@ def render_vjp(params, cam, res, g_image, sh_degree=0, tpu_gather=False, dtype=n
                 sh_coeffs=gp["sh_coeffs"], background=gt["background"])
 
 
+def densify(g_means, means, w2c, fx, fy, W, H, valid, radii, grad_accum, denom, max_radii, active=None,
+            dtype=np.float32):
+    """trainer.py:143-159: returns updated (grad_accum, denom, max_radii) (inputs untouched).
+
+    focal = (fx + fy) / 2 and the scale W*H*3 enter as the float32 scalars JAX's weak
+    typing makes of the Python floats."""
+    f = np.dtype(dtype).type
+    g_means, means, w2c, radii = (_c(a, dtype) for a in (g_means, means, w2c, radii))
+    ga = _c(grad_accum, dtype).copy()
+    de = _c(denom, np.int32).copy()
+    mr = _c(max_radii, dtype).copy()
+    v = _c(valid, np.uint8)
+    a = None if active is None else _c(active, np.uint8)
+    fn = getattr(lib(), "gso_densify_" + _sfx(dtype))
+    R = _real(dtype)
+    rc = fn(ctypes.c_int64(means.shape[0]), _p(g_means), _p(means), _p(w2c.reshape(16)), R(f((fx + fy) / 2.0)),
+            R(f(float(W) * float(H) * 3.0)), _p(v), _p(a), _p(radii), _p(ga), _p(de), _p(mr))
+    assert rc == 0
+    return ga, de, mr
+
+
 def l1_loss_and_grad(image, target):
     """losses.py:4-8: mean(|pred - target|) and its seed sign(d) * (1/count)."""
     d = image.astype(np.float32) - target.astype(np.float32)

@@ -22,6 +22,7 @@
  *                       of T propagated backwards, gathers transposed to scatter-adds
  *   preprocess_bwd_*    reverse-mode derivative of preprocess_* (JAX conventions:
  *                       min/max/clip ties split 0.5/0.5, ceil has zero derivative)
+ *   densify_*           jax_gs/training/trainer.py:143-159 (densification statistics)
  */
 
 #define CAT2(a, b) a##_##b
@@ -649,6 +650,31 @@ int FN(gso_preprocess_bwd)(int64_t n, int K, int deg, const REAL* means, const R
     }
     qd = ((p.qn[0] * gq[0] + p.qn[1] * gq[1]) + p.qn[2] * gq[2]) + p.qn[3] * gq[3];
     for (k = 0; k < 4; ++k) g_quats[4 * i + k] = (gq[k] - p.qn[k] * qd) / p.qnorm;
+  }
+  return 0;
+}
+
+/* jax_gs/training/trainer.py:143-159, the densification statistics of one step:
+ * means_cam = [m, 1] @ W2C^T (:145-146), z = max(z_cam, 0.01) (:147),
+ * grad_2d_mag = ||dL/dmeans|| * (z / focal) * (W*H*3) (:148-150), focal = (fx+fy)/2,
+ * grad_accum += grad_2d_mag (:152), denom += valid & active (:153-154),
+ * max_radii = where(valid, max(max_radii, radii), max_radii) (:157-159).
+ * active may be NULL (all active). */
+int FN(gso_densify)(int64_t n, const REAL* g_means, const REAL* means, const REAL* w2c, REAL focal,
+                    REAL pixel_scale, const uint8_t* valid, const uint8_t* active, const REAL* radii,
+                    REAL* grad_accum, int32_t* denom, REAL* max_radii) {
+  int64_t i;
+  for (i = 0; i < n; ++i) {
+    const REAL* m = means + 3 * i;
+    const REAL* g = g_means + 3 * i;
+    const REAL zc = ((m[0] * w2c[8] + m[1] * w2c[9]) + m[2] * w2c[10]) + w2c[11];
+    const REAL z = FN(r_max)(zc, (REAL)0.01);
+    const REAL nrm = SQRT((g[0] * g[0] + g[1] * g[1]) + g[2] * g[2]);
+    const int v = valid[i] != 0;
+    const int act = active == NULL || active[i] != 0;
+    grad_accum[i] = grad_accum[i] + (nrm * (z / focal)) * pixel_scale;
+    denom[i] = denom[i] + ((v && act) ? 1 : 0);
+    if (v) max_radii[i] = FN(r_max)(max_radii[i], radii[i]);
   }
   return 0;
 }

@@ -222,3 +222,25 @@ def test_background_forward_and_grad(cuda):
     assert _rel(_np(bg.grad), gr_o["background"]) <= GRAD_TOL
     for f in FIELDS:
         assert _rel(_np(getattr(g, f).grad), gr_o[f]) <= GRAD_TOL, f
+
+
+def test_cfg4_masked_step_with_densify_accumulators(cuda):
+    """Configuration 4's step on a small scene: masked render, backward, then the
+    densification statistics (trainer.py:143-159) against the oracle's."""
+    from jax_gs_amd.training.trainer import accumulate_from_extras
+
+    sc = scenes.make_scene(4, n=6000, width=160, height=96)
+    image, extras, g, img_o, ex_o, gr_o = _render_both(sc, cuda)
+    assert np.abs(_np(image) - img_o).max() <= IMG_TOL
+    n = sc["params"]["means"].shape[0]
+    state = {"grad_accum": torch.full((n,), 0.25, device=cuda), "denom": torch.ones(n, dtype=torch.int32, device=cuda),
+             "max_radii": torch.full((n,), 2.0, device=cuda)}
+    _, cam, _, m = scenes.to_torch(sc, cuda)
+    accumulate_from_extras(state, g.means.grad, g.means.detach(), cam, extras, active=m)
+    c = sc["cam"]
+    ga, de, mr = oracle.densify(gr_o["means"], sc["params"]["means"], c["W2C"], c["fx"], c["fy"], c["W"], c["H"],
+                                ex_o["valid_mask"], ex_o["radii"], np.full(n, 0.25, np.float32),
+                                np.ones(n, np.int32), np.full(n, 2.0, np.float32), active=sc["mask"])
+    np.testing.assert_array_equal(_np(state["denom"]), de)
+    np.testing.assert_array_equal(_np(state["max_radii"]), mr)
+    assert _rel(_np(state["grad_accum"]), ga) <= GRAD_TOL

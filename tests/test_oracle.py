@@ -399,3 +399,43 @@ def test_l1_seed_closed_form():
     loss, g = oracle.l1_loss_and_grad(a, b)
     np.testing.assert_allclose(loss, (0 + 0.7 + 0.6) / 3, rtol=1e-6)
     np.testing.assert_array_equal(g, np.array([[[0, -1, 1]]], F32) * F32(1 / 3))
+
+
+def test_densify_closed_form():
+    """trainer.py:143-159 on hand-computable cases: z/focal = 1/64, |g| = 5, W*H*3 = 192
+    give exactly 15; a Gaussian behind the camera uses z = 0.01; denom counts valid and
+    active only; max_radii moves only for valid Gaussians."""
+    w2c = np.eye(4, dtype=np.float32)
+    w2c[2, 3] = 1.0  # z_cam = z + 1
+    means = np.array([[0.5, -2.0, 3.0], [1.0, 1.0, -4.0], [0.0, 0.0, 3.0], [2.0, 2.0, 3.0]], np.float32)
+    g = np.array([[3.0, 4.0, 0.0], [0.0, 0.0, 5.0], [0.0, 0.0, 0.0], [4.0, 0.0, 3.0]], np.float32)
+    valid = np.array([1, 1, 0, 1], np.uint8)
+    active = np.array([1, 1, 1, 0], np.uint8)
+    radii = np.array([7.0, 2.0, 50.0, 9.0], np.float32)
+    ga0 = np.array([1.0, 0.0, 0.5, 0.0], np.float32)
+    de0 = np.array([2, 0, 1, 3], np.int32)
+    mr0 = np.array([3.0, 4.0, 5.0, 6.0], np.float32)
+    ga, de, mr = oracle.densify(g, means, w2c, 200.0, 312.0, 8, 8, valid, radii, ga0, de0, mr0, active=active)
+    assert ga[0] == 1.0 + 15.0 and ga[3] == 15.0  # z = 4, focal = 256
+    assert abs(ga[1] - 5.0 * (0.01 / 256.0) * 192.0) <= 1e-7  # z_cam = -3 -> 0.01
+    assert ga[2] == 0.5
+    np.testing.assert_array_equal(de, [3, 1, 1, 3])
+    np.testing.assert_array_equal(mr, [7.0, 4.0, 5.0, 9.0])
+
+
+def test_densify_float32_matches_float64():
+    rng = np.random.default_rng(4)
+    n = 500
+    means = rng.normal(0, 2, (n, 3)).astype(np.float32)
+    g = rng.normal(0, 1e-3, (n, 3)).astype(np.float32)
+    w2c = np.eye(4, dtype=np.float32)
+    w2c[:3, 3] = [0.1, -0.2, 4.0]
+    valid = (rng.uniform(size=n) < 0.8).astype(np.uint8)
+    radii = np.ceil(rng.uniform(0, 30, n)).astype(np.float32)
+    z = np.zeros(n, np.float32)
+    out32 = oracle.densify(g, means, w2c, 500.0, 510.0, 64, 48, valid, radii, z, np.zeros(n, np.int32), z)
+    out64 = oracle.densify(g, means, w2c, 500.0, 510.0, 64, 48, valid, radii, z, np.zeros(n, np.int32), z,
+                           dtype=np.float64)
+    np.testing.assert_allclose(out32[0], out64[0], rtol=1e-5)
+    np.testing.assert_array_equal(out32[1], out64[1])
+    np.testing.assert_array_equal(out32[2], out64[2])
