@@ -64,6 +64,7 @@ extern "C" {
 #define GS_NUM_STATS 16
 
 const char* gs_last_error(void);
+/* 2: gs_composite_fwd/bwd take the tile order. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -121,18 +122,21 @@ int gs_tile_ranges(void* stream, const int32_t* sorted_tiles, int64_t length, in
  * ranges[T+1] indexes into it (out-of-range ids clamp to [0, n-1] as XLA's gather
  * does).  Per pixel it also writes the final
  * transmittance final_T[H,W] and n_contrib[H,W] = number of leading entries blended
- * while T > 1e-4 (residuals for gs_composite_bwd; either may be NULL). */
+ * while T > 1e-4, and tile_order[T] = the tiles sorted by decreasing walk length, the
+ * launch order of gs_composite_bwd (residuals for gs_composite_bwd; each may be NULL). */
 int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                      int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
-                     float* image, float* final_T, int32_t* n_contrib);
+                     float* image, float* final_T, int32_t* n_contrib, int32_t* tile_order);
 
 /* Vector-Jacobian product of gs_composite_fwd (JAX autodiff of render_tiles).
- * grad_records[N,GS_REC_STRIDE] is overwritten with the gradient record (layout
- * above); grad_background[3] (may be NULL) with dL/d(background). */
+ * tile_order is the forward's (NULL: a fixed order; results agree up to the order of
+ * floating-point additions).  grad_records[N,GS_REC_STRIDE] is overwritten with the
+ * gradient record (layout above); grad_background[3] (may be NULL) with
+ * dL/d(background). */
 int gs_composite_bwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                      int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
                      const float* grad_image, const float* final_T, const int32_t* n_contrib,
-                     float* grad_records, float* grad_background);
+                     const int32_t* tile_order, float* grad_records, float* grad_background);
 
 /* Vector-Jacobian product of gs_preprocess_fwd's compositing records with respect to
  * the five Gaussian parameter arrays (JAX autodiff of project_gaussians, eval_sh,

@@ -236,7 +236,8 @@ template <int PPT>
 __global__ __launch_bounds__(64) void composite_fwd_kernel(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
-    float* __restrict__ img, float* __restrict__ finalT, int32_t* __restrict__ ncontrib) {
+    float* __restrict__ img, float* __restrict__ finalT, int32_t* __restrict__ ncontrib,
+    int32_t* __restrict__ tile_cost) {
   constexpr int WPT = 4 / PPT;  // waves per tile
   const int b = blockIdx.x / WPT, part = blockIdx.x % WPT;
   const int tile = tile_of_block(b, T);
@@ -329,6 +330,8 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
       if (ncontrib) ncontrib[p] = Tr[i] > kTMin ? n : cnt[i];
     }
   }
+  // walk length of the tile (first wave of the tile): the backward's cost estimate
+  if (tile_cost && part == 0 && lane == 0) tile_cost[tile] = walked;
 }
 
 template <int PPT>
@@ -336,10 +339,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
     const float* __restrict__ gimg, const float* __restrict__ finalT, const int32_t* __restrict__ ncontrib,
-    float* __restrict__ grec) {
+    float* __restrict__ grec, const int32_t* __restrict__ order) {
   constexpr int WPT = 4 / PPT;
   const int b = blockIdx.x / WPT, part = blockIdx.x % WPT;
-  const int tile = tile_of_block(b, T);
+  const int tile = order ? (b < T ? order[b] : T) : tile_of_block(b, T);
+  if (tile < 0) return;
   if (tile >= T) return;
   const int lane = threadIdx.x;
   const int tx = tile % TX, ty = tile / TX;
@@ -513,6 +517,55 @@ __global__ __launch_bounds__(256) void background_grad_kernel(int64_t npix, cons
     atomicAdd(&gbg[threadIdx.x], (ws[0][threadIdx.x] + ws[1][threadIdx.x]) + (ws[2][threadIdx.x] + ws[3][threadIdx.x]));
 }
 
+// Backward schedule.  Every wave of a compositing launch is resident from the start
+// (one wave per tile, 8 per SIMD), so a launch lasts as long as its most loaded SIMD;
+// tiles differ in walk length by an order of magnitude, and in tile order a SIMD's
+// 8 tiles can all be long.  Handing the tiles out longest first (blocks are dispatched
+// in index order, round-robin over the XCDs and SIMDs) spreads the long walks over
+// all SIMDs, each next to short ones.  The forward pass measures the walk length of
+// every tile; the backward walks the same entries (up to the last contributing one),
+// so that length is its cost.  tile_order_kernel turns the lengths (written into the
+// order array itself) into the permutation, longest first: a counting sort over
+// buckets of 8 entries in one workgroup, with the lengths held in LDS.  Beyond
+// kOrderMaxTiles tiles the order is the identity.
+constexpr int kOrderMaxTiles = 65536;
+constexpr int kOrderBuckets = 1024;  // walk lengths <= 4096 -> buckets <= 512
+
+__global__ __launch_bounds__(1024) void tile_order_kernel(int32_t* __restrict__ order, int T) {
+  __shared__ uint16_t bucket[kOrderMaxTiles];
+  __shared__ int start[kOrderBuckets];
+  __shared__ int wsum[16];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  if (T > kOrderMaxTiles) {
+    for (int t = tid; t < T; t += 1024) order[t] = t;
+    return;
+  }
+  start[tid] = 0;
+  __syncthreads();
+  for (int t = tid; t < T; t += 1024) {
+    const int c = order[t];
+    const int bk = min(max(c, 0) >> 3, kOrderBuckets - 1);
+    bucket[t] = (uint16_t)bk;
+    atomicAdd(&start[bk], 1);
+  }
+  __syncthreads();
+  // exclusive scan over buckets in descending order: thread j owns bucket 1023 - j
+  const int own = start[kOrderBuckets - 1 - tid];
+  int x = own;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[wid] = x;
+  __syncthreads();
+  int before = 0;
+  for (int w = 0; w < wid; ++w) before += wsum[w];
+  start[kOrderBuckets - 1 - tid] = before + x - own;
+  __syncthreads();
+  for (int t = tid; t < T; t += 1024) order[atomicAdd(&start[bucket[t]], 1)] = t;
+}
+
 // Large images have enough tiles to fill the GPU with one wave per tile.
 inline int pick_ppt(int T) { return T >= 2048 ? 4 : 1; }
 
@@ -523,7 +576,8 @@ using namespace gs;
 
 extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                                 int64_t n_entries, const int32_t* ranges, int width, int height,
-                                const float* background, float* image, float* final_T, int32_t* n_contrib) {
+                                const float* background, float* image, float* final_T, int32_t* n_contrib,
+                                int32_t* tile_order) {
   GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "gs_composite_fwd: n out of range");
   GS_REQUIRE(n_entries >= 0, "gs_composite_fwd: n_entries must be >= 0");
   GS_REQUIRE(width > 0 && height > 0, "gs_composite_fwd: bad image size %dx%d", width, height);
@@ -535,19 +589,26 @@ extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, c
   hipStream_t s = (hipStream_t)stream;
   if (pick_ppt(T) == 4) {
     hipLaunchKernelGGL(composite_fwd_kernel<4>, dim3(nblk), dim3(64), 0, s, (const float4*)records, (int)n,
-                       sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib);
+                       sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib,
+                       tile_order);
   } else {
     hipLaunchKernelGGL(composite_fwd_kernel<1>, dim3(nblk * 4), dim3(64), 0, s, (const float4*)records, (int)n,
-                       sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib);
+                       sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib,
+                       tile_order);
   }
   GS_LAUNCH_CHECK("composite_fwd_kernel");
+  if (tile_order) {
+    hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(1024), 0, s, tile_order, T);
+    GS_LAUNCH_CHECK("tile_order_kernel");
+  }
   return GS_OK;
 }
 
 extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                                 int64_t n_entries, const int32_t* ranges, int width, int height,
                                 const float* background, const float* grad_image, const float* final_T,
-                                const int32_t* n_contrib, float* grad_records, float* grad_background) {
+                                const int32_t* n_contrib, const int32_t* tile_order, float* grad_records,
+                                float* grad_background) {
   GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "gs_composite_bwd: n out of range");
   GS_REQUIRE(n_entries >= 0, "gs_composite_bwd: n_entries must be >= 0");
   GS_REQUIRE(width > 0 && height > 0, "gs_composite_bwd: bad image size %dx%d", width, height);
@@ -572,11 +633,11 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
   if (pick_ppt(T) == 4) {
     hipLaunchKernelGGL(composite_bwd_kernel<4>, dim3(nblk), dim3(64), 0, s, (const float4*)records, (int)n,
                        sorted_gids, n_entries, ranges, width, height, TX, T, background, grad_image, final_T,
-                       n_contrib, grad_records);
+                       n_contrib, grad_records, tile_order);
   } else {
     hipLaunchKernelGGL(composite_bwd_kernel<1>, dim3(nblk * 4), dim3(64), 0, s, (const float4*)records, (int)n,
                        sorted_gids, n_entries, ranges, width, height, TX, T, background, grad_image, final_T,
-                       n_contrib, grad_records);
+                       n_contrib, grad_records, tile_order);
   }
   GS_LAUNCH_CHECK("composite_bwd_kernel");
   return GS_OK;

@@ -37,8 +37,8 @@ _SIGS = {
     "gs_bin_workspace_size": [_I64, _I, _I, _I64],
     "gs_bin": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _SZ, _P, _P, _P, _P],
     "gs_tile_ranges": [_P, _P, _I64, _I, _P],
-    "gs_composite_fwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P],
-    "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P],
+    "gs_composite_fwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P],
+    "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "gs_preprocess_bwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P, _P],
     "gs_l1_loss": [_P, _I64, _P, _P, _P, _P],
     "gs_densify_accumulate": [_P, _I64, _P, _P, _P, _F, _F, _P, _P, _P, _P, _P, _P],
@@ -46,6 +46,9 @@ _SIGS = {
 _RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ}
 
 _lib = None
+
+
+ABI_VERSION = 2  # gs_abi_version() of the signatures bound below
 
 
 class NativeLibraryMissing(RuntimeError):
@@ -65,6 +68,9 @@ def lib():
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = _RESTYPE.get(name, ctypes.c_int)
+        if L.gs_abi_version() != ABI_VERSION:
+            raise NativeLibraryMissing(f"{LIBPATH} implements ABI {L.gs_abi_version()}, this module binds ABI "
+                                       f"{ABI_VERSION}: rebuild it")
         _lib = L
     return _lib
 

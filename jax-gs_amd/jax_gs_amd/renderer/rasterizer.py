@@ -94,15 +94,19 @@ def composite_records(means2D, cov2D, opacities, colors) -> torch.Tensor:
 
 def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Tensor, H: int, W: int,
               background: torch.Tensor, residuals: bool = True):
-    """Front-to-back compositing; returns (image [H,W,3], final_T [H,W], n_contrib [H,W])."""
+    """Front-to-back compositing; returns (image [H,W,3], final_T [H,W], n_contrib [H,W],
+    tile_order [T]), the last three the backward's residuals (None unless residuals):
+    tile_order lists the tiles longest walk first, the backward's launch order."""
     dev = records.device
+    _, _, T = num_tiles(W, H)
     image = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
     fT = torch.empty((H, W), dtype=torch.float32, device=dev) if residuals else None
     nc = torch.empty((H, W), dtype=torch.int32, device=dev) if residuals else None
+    order = torch.empty((T,), dtype=torch.int32, device=dev) if residuals else None
     _lib.call("gs_composite_fwd", _lib.stream_handle(dev), records.shape[0], _lib.ptr(records),
               _lib.ptr(sorted_gids), sorted_gids.shape[0], _lib.ptr(ranges), int(W), int(H), _lib.ptr(background), _lib.ptr(image),
-              _lib.ptr(fT), _lib.ptr(nc))
-    return image, fT, nc
+              _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order))
+    return image, fT, nc, order
 
 
 def render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W,
@@ -116,5 +120,5 @@ def render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaus
     rec = composite_records(means2D, cov2D, opacities, colors)
     ranges = tile_ranges(sorted_tile_ids, T)
     bg = background_tensor(background, dev)
-    image, _, _ = composite(rec, sorted_gaussian_ids.to(torch.int32).contiguous(), ranges, H, W, bg, residuals=False)
+    image, _, _, _ = composite(rec, sorted_gaussian_ids.to(torch.int32).contiguous(), ranges, H, W, bg, residuals=False)
     return image

@@ -5,8 +5,8 @@ fast_tpu_rasterizer=False, mask=None, sh_degree=0) -> (image [H,W,3], extras)``.
 The reference differentiates render with JAX autodiff; here a
 ``torch.autograd.Function`` plays the role of a ``jax.custom_vjp``: its forward runs
 the preprocessing, binning and compositing kernels and keeps the per-Gaussian
-records, the sorted entry list, the tile ranges and per-pixel (final T, entry count)
-as residuals; its backward runs the compositing VJP and the preprocessing VJP and
+records, the sorted entry list, the tile ranges, per-pixel (final T, entry count)
+and the backward's tile order as residuals; its backward runs the compositing VJP and the preprocessing VJP and
 returns cotangents of the five Gaussian arrays (equal to JAX autodiff of the
 reference forward, with its tie conventions) and of the background.  W2C gets no
 gradient (the reference's trainer never differentiates it) and mask gets None.
@@ -34,12 +34,12 @@ class _Render(torch.autograd.Function):
         pre = preprocess(g, cam, mask=mask, sh_degree=sh_degree, records=True)
         b = bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W, capacity=capacity,
                           want_tiles=False)
-        image, fT, nc = composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg, residuals=True)
+        image, fT, nc, order = composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg, residuals=True)
         ctx.static = static
         # radii, valid and stats carry no gradient: no zero cotangents for them
         ctx.set_materialize_grads(False)
         ctx.save_for_backward(means, scales, quats, opac, sh, w2c, bg, pre["records"], b["sorted_gids"], b["ranges"],
-                              fT, nc)
+                              fT, nc, order)
         radii = pre["radii"]
         valid = pre["valid"].view(torch.bool)  # the kernel writes 0/1 bytes
         stats = b["stats"]
@@ -51,7 +51,7 @@ class _Render(torch.autograd.Function):
         W, H, fx, fy, cx, cy, sh_degree, _ = ctx.static
         if g_image is None:
             return None, None, None, None, None, None, None, None, None
-        means, scales, quats, opac, sh, w2c, bg, rec, gids, ranges, fT, nc = ctx.saved_tensors
+        means, scales, quats, opac, sh, w2c, bg, rec, gids, ranges, fT, nc, order = ctx.saved_tensors
         dev = means.device
         n = means.shape[0]
         s = _lib.stream_handle(dev)
@@ -59,7 +59,8 @@ class _Render(torch.autograd.Function):
         grec = torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=dev)
         gbg = torch.empty((3,), dtype=torch.float32, device=dev)
         _lib.call("gs_composite_bwd", s, n, _lib.ptr(rec), _lib.ptr(gids), gids.shape[0], _lib.ptr(ranges), int(W), int(H),
-                  _lib.ptr(bg), _lib.ptr(g_image), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(grec), _lib.ptr(gbg))
+                  _lib.ptr(bg), _lib.ptr(g_image), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec),
+                  _lib.ptr(gbg))
         gm = torch.empty_like(means)
         gs_ = torch.empty_like(scales)
         gq = torch.empty_like(quats)

@@ -244,3 +244,37 @@ def test_cfg4_masked_step_with_densify_accumulators(cuda):
     np.testing.assert_array_equal(_np(state["denom"]), de)
     np.testing.assert_array_equal(_np(state["max_radii"]), mr)
     assert _rel(_np(state["grad_accum"]), ga) <= GRAD_TOL
+
+
+@pytest.mark.parametrize("cfg", [1, 2])
+def test_backward_tile_order(cuda, cfg):
+    """The forward's tile order (tiles by decreasing walk length) is a permutation of
+    the tiles, and the backward launched in that order equals the backward in the fixed
+    order up to the order of the gradient additions (one and four waves per tile)."""
+    from jax_gs_amd import _lib
+    from jax_gs_amd.renderer._buffers import num_tiles
+
+    sc = scenes.make_scene(cfg)
+    g, cam, _, mask = scenes.to_torch(sc, cuda)
+    W, H = cam.W, cam.H
+    with torch.no_grad():
+        pre = preprocess(g, cam, mask=mask, sh_degree=sc["sh_degree"])
+        b = rasterizer.bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W,
+                                     want_tiles=False)
+        bg = torch.zeros(3, device=cuda)
+        image, fT, nc, order = rasterizer.composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg)
+        _, _, T = num_tiles(W, H)
+        assert order.shape == (T,)
+        assert np.array_equal(np.sort(_np(order)), np.arange(T))
+        gimg = torch.from_numpy(np.random.default_rng(7).normal(0, 1, (H, W, 3)).astype(np.float32)).to(cuda)
+        n = pre["records"].shape[0]
+        out = []
+        for o in (order, None):
+            grec = torch.empty((n, _lib.GS_REC_STRIDE), device=cuda)
+            gbg = torch.empty(3, device=cuda)
+            _lib.call("gs_composite_bwd", _lib.stream_handle(cuda), n, _lib.ptr(pre["records"]),
+                      _lib.ptr(b["sorted_gids"]), b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), W, H, _lib.ptr(bg),
+                      _lib.ptr(gimg), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(o), _lib.ptr(grec), _lib.ptr(gbg))
+            out.append((_np(grec), _np(gbg)))
+    assert _rel(out[0][0], out[1][0]) <= 1e-5
+    assert _rel(out[0][1], out[1][1]) <= 1e-5
