@@ -137,7 +137,12 @@ def main():
     #                   (12 + 12 + 16 + 4 + 12 K).
     pre_fwd_bytes = N * (44 + 12 * nb) + N * (8 + 16 + 4 + 1 + 4 + 12 + 48)
     pre_bwd_bytes = N * (44 + 12 * nb) + N * 48 + N * (12 + 12 + 16 + 4 + 12 * K)
+    #   binning: read means2d 8 + radius 4 + valid 1 + depth 4 per Gaussian; write the entry
+    #            list (4 B per entry) and the tile ranges (4 B per tile).
+    T = b["ranges"].shape[0] - 1
+    bin_bytes = N * 17 + 4 * n_int + 4 * (T + 1)
     stage_gbs = {"preprocess_fwd": pre_fwd_bytes / (stage_ms["preprocess_fwd"] * 1e-3) / 1e9,
+                 "binning": bin_bytes / (stage_ms["binning"] * 1e-3) / 1e9,
                  "preprocess_bwd": pre_bwd_bytes / (stage_ms["preprocess_bwd"] * 1e-3) / 1e9}
     # Compositing is VALU-bound; its unit of work is an evaluated (pixel, entry) pair,
     # i.e. sum over pixels of n_contrib, at ~22 FLOP forward and ~55 FLOP backward.
@@ -179,6 +184,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": dt * 1e3,
+        "fwd_ms": stage_ms["preprocess_fwd"] + stage_ms["binning"] + stage_ms["composite_fwd"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
