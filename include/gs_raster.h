@@ -64,7 +64,7 @@ extern "C" {
 #define GS_NUM_STATS 16
 
 const char* gs_last_error(void);
-/* 2: gs_composite_fwd/bwd take the tile order. */
+/* 2: gs_composite_fwd/bwd take the tile order; losses gs_mse_loss, gs_l1_ssim. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -155,6 +155,31 @@ int gs_preprocess_bwd(void* stream, int64_t n, int sh_k, int sh_degree, const fl
  * and its autodiff seed. */
 int gs_l1_loss(void* stream, int64_t count, const float* pred, const float* target,
                float* loss, float* grad);
+
+/* mean((pred - target)^2) into loss[0] and, when grad is not NULL, its gradient
+ * 2 (pred - target) / count.  Replaces jax_gs/training/losses.py:10-14 (mse_loss). */
+int gs_mse_loss(void* stream, int64_t count, const float* pred, const float* target,
+                float* loss, float* grad);
+
+/* Workspace bytes of gs_l1_ssim / gs_l1_ssim_bwd for an image of height x width x
+ * channels (0 for a bad shape). */
+size_t gs_l1_ssim_workspace_size(int height, int width, int channels);
+
+/* L1 and SSIM of pred against target [H,W,C] in one pass: out[0] = mean |pred - target|,
+ * out[1] = mean SSIM.  Replaces jax_gs/training/losses.py:4-8 (l1_loss) and :16-68
+ * (ssim: 11-tap Gaussian window, sigma 1.5, 'SAME' zero padding, C1 = 0.01^2,
+ * C2 = 0.03^2, map clipped to [-1, 1]), the two terms of trainer.py:18-26.  With
+ * with_grad != 0 the workspace also keeps what gs_l1_ssim_bwd needs. */
+int gs_l1_ssim(void* stream, int height, int width, int channels, const float* pred,
+               const float* target, float* out, int with_grad, void* workspace,
+               size_t workspace_bytes);
+
+/* grad_pred = grad_out[0] * d out[0] / d pred + grad_out[1] * d out[1] / d pred, with
+ * grad_out[2] on the device (JAX autodiff of l1_loss and ssim; ties of max and clip pass
+ * half).  Needs the workspace of a gs_l1_ssim call with_grad on the same images. */
+int gs_l1_ssim_bwd(void* stream, int height, int width, int channels, const float* pred,
+                   const float* target, const float* grad_out, const void* workspace,
+                   size_t workspace_bytes, float* grad_pred);
 
 /* Densification statistics of one training step, updated in place.
  * Replaces jax_gs/training/trainer.py:278-294 (train_step, after value_and_grad):

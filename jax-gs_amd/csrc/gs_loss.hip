@@ -1,6 +1,7 @@
-// L1 photometric loss and its gradient seed on gfx950.
-// Reference: jax_gs/training/losses.py:4-8, l1_loss(pred, target) = mean(|pred - target|);
-// its reverse-mode seed is sign(pred - target) * (1 / count) with sign(0) = 0.
+// L1 and MSE photometric losses and their gradient seeds on gfx950.
+// Reference: jax_gs/training/losses.py:4-8, l1_loss(pred, target) = mean(|pred - target|),
+// whose reverse-mode seed is sign(pred - target) * (1 / count) with sign(0) = 0, and
+// losses.py:10-14, mse_loss = mean((pred - target)^2), seed 2 (pred - target) / count.
 #include "gs_common.h"
 
 namespace gs {
@@ -10,9 +11,17 @@ __global__ void zero_loss_kernel(float* __restrict__ loss) { loss[0] = 0.0f; }
 
 __device__ inline float sgn(float d) { return d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f); }
 
+// Per-value loss term and gradient seed (before the 1 / count): |d| and sign(d), or
+// d^2 and 2 d.
+template <bool SQ>
+__device__ inline float term(float d) { return SQ ? d * d : fabsf(d); }
+template <bool SQ>
+__device__ inline float seed(float d) { return SQ ? 2.0f * d : sgn(d); }
+
 // 16-byte loads and stores over the first count/4 quads (when all three arrays are
 // 16-byte aligned), scalars for the rest.
-__global__ __launch_bounds__(256) void l1_kernel(int64_t count, bool vec, const float* __restrict__ pred,
+template <bool SQ>
+__global__ __launch_bounds__(256) void loss_kernel(int64_t count, bool vec, const float* __restrict__ pred,
                                                  const float* __restrict__ target, float inv_count,
                                                  float* __restrict__ loss, float* __restrict__ grad) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -26,14 +35,15 @@ __global__ __launch_bounds__(256) void l1_kernel(int64_t count, bool vec, const 
   for (int64_t q = tid; q < nq; q += stride) {
     const float4 a = p4[q], b = t4[q];
     const float d0 = a.x - b.x, d1 = a.y - b.y, d2 = a.z - b.z, d3 = a.w - b.w;
-    acc += (fabsf(d0) + fabsf(d1)) + (fabsf(d2) + fabsf(d3));
+    acc += (term<SQ>(d0) + term<SQ>(d1)) + (term<SQ>(d2) + term<SQ>(d3));
     if (grad != nullptr)
-      g4[q] = make_float4(sgn(d0) * inv_count, sgn(d1) * inv_count, sgn(d2) * inv_count, sgn(d3) * inv_count);
+      g4[q] = make_float4(seed<SQ>(d0) * inv_count, seed<SQ>(d1) * inv_count, seed<SQ>(d2) * inv_count,
+                          seed<SQ>(d3) * inv_count);
   }
   for (int64_t i = 4 * nq + tid; i < count; i += stride) {
     const float d = pred[i] - target[i];
-    acc += fabsf(d);
-    if (grad != nullptr) grad[i] = sgn(d) * inv_count;
+    acc += term<SQ>(d);
+    if (grad != nullptr) grad[i] = seed<SQ>(d) * inv_count;
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
@@ -48,10 +58,12 @@ __global__ __launch_bounds__(256) void l1_kernel(int64_t count, bool vec, const 
 
 using namespace gs;
 
-extern "C" int gs_l1_loss(void* stream, int64_t count, const float* pred, const float* target, float* loss,
-                          float* grad) {
-  GS_REQUIRE(count > 0, "gs_l1_loss: count must be > 0");
-  GS_REQUIRE(pred && target && loss, "gs_l1_loss: NULL argument");
+namespace {
+template <bool SQ>
+int mean_loss(const char* name, void* stream, int64_t count, const float* pred, const float* target, float* loss,
+              float* grad) {
+  GS_REQUIRE(count > 0, "%s: count must be > 0", name);
+  GS_REQUIRE(pred && target && loss, "%s: NULL argument", name);
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(zero_loss_kernel, dim3(1), dim3(1), 0, s, loss);
   GS_LAUNCH_CHECK("zero_loss_kernel");
@@ -60,7 +72,18 @@ extern "C" int gs_l1_loss(void* stream, int64_t count, const float* pred, const 
   // few blocks: each adds its partial sum to loss[0] with one atomic
   int blocks = div_up(count, 256 * 16);
   if (blocks > 512) blocks = 512;
-  hipLaunchKernelGGL(l1_kernel, dim3(blocks), dim3(256), 0, s, count, vec, pred, target, inv, loss, grad);
-  GS_LAUNCH_CHECK("l1_kernel");
+  hipLaunchKernelGGL(loss_kernel<SQ>, dim3(blocks), dim3(256), 0, s, count, vec, pred, target, inv, loss, grad);
+  GS_LAUNCH_CHECK("loss_kernel");
   return GS_OK;
+}
+}  // namespace
+
+extern "C" int gs_l1_loss(void* stream, int64_t count, const float* pred, const float* target, float* loss,
+                          float* grad) {
+  return mean_loss<false>("gs_l1_loss", stream, count, pred, target, loss, grad);
+}
+
+extern "C" int gs_mse_loss(void* stream, int64_t count, const float* pred, const float* target, float* loss,
+                           float* grad) {
+  return mean_loss<true>("gs_mse_loss", stream, count, pred, target, loss, grad);
 }

@@ -1,0 +1,337 @@
+// L1 and SSIM photometric losses of a rendered image, and their gradient, on gfx950.
+//
+// Reference: jax_gs/training/losses.py:4-8 (l1_loss) and :16-75 (ssim, d_ssim_loss),
+// combined by jax_gs/training/trainer.py:18-26 as (1 - 0.2) l1 + 0.2 d_ssim.
+//   taps    w_k = exp(-k^2 / 4.5) / sum, k = -5..5 (window 11, sigma 1.5)
+//   blur    correlation with w along H, then along W, 'SAME' zero padding
+//   mu1 = blur(x), mu2 = blur(y), s11 = max(0, blur(x^2) - mu1^2),
+//   s22 = max(0, blur(y^2) - mu2^2), s12 = blur(x y) - mu1 mu2
+//   map = (2 mu1 mu2 + C1)(2 s12 + C2) / ((mu1^2 + mu2^2 + C1)(s11 + s22 + C2)),
+//   C1 = 0.01^2, C2 = 0.03^2, clipped to [-1, 1]; ssim = mean over H x W x C.
+//
+// Forward (one launch + a final sum): a workgroup owns 16 x 54 outputs of every channel.
+// The vertical pass runs over 64 columns (54 + 2 x 5 halo): each thread takes one
+// column and 4 output rows, reads the 14 input rows it needs once and keeps the five
+// blurred products (x, y, x^2, y^2, x y) in registers; they meet in LDS, where the
+// horizontal pass (each thread 4 adjacent outputs of one row, 128-bit LDS reads of
+// its 14-column window) completes the blur.  Per output the map, |x - y| and, when a
+// gradient is wanted, the map's derivatives with respect to (mu1, blur(x^2),
+// blur(x y)) -- divided by the count and gated by the clip -- are formed; the
+// derivatives go to three planes of the workspace.
+// Backward: dL/dx = blur(d/dmu1) + 2 x blur(d/dblur(x^2)) + y blur(d/dblur(x y)) (the
+// blur is a correlation with a symmetric kernel and zero padding, so it is its own
+// adjoint), scaled by the cotangent of the mean SSIM, plus the L1 cotangent times
+// sign(x - y) / count.  Same tiling over the three planes.
+// Ties follow JAX: max(0, .) and the clip pass half the cotangent at equality.
+#include "gs_common.h"
+
+namespace gs {
+namespace {
+
+constexpr int kSR = 5;                   // window radius
+constexpr int kSTaps = 2 * kSR + 1;      // 11 taps
+constexpr int kSTH = 16;                 // output rows per workgroup
+constexpr int kSCols = 64;               // columns of the vertical pass
+constexpr int kSTW = kSCols - 2 * kSR;   // 54 output columns per workgroup
+constexpr int kSPad = kSCols + 4;        // LDS row (the last window reads 2 columns past 64)
+constexpr float kC1 = 0.01f * 0.01f;
+constexpr float kC2 = 0.03f * 0.03f;
+
+struct Taps {
+  float w[kSTaps];
+};
+
+__device__ inline float tie_step(float z) { return z > 0.0f ? 1.0f : (z == 0.0f ? 0.5f : 0.0f); }
+
+// Vertical pass of NM maps for image column col: acc[m][o] = sum_k w_k v_m(row0 + o + k),
+// o < 4, where v_m(r) = load(m, r) inside the image and 0 outside.
+template <int NM, typename Load>
+__device__ inline void vertical4(const Taps& t, int row0, int H, bool col_in, Load load, float (&acc)[NM][4]) {
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int o = 0; o < 4; ++o) acc[m][o] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4 + 2 * kSR; ++i) {
+    const int r = row0 + i;
+    float v[NM];
+    load(col_in && r >= 0 && r < H, r, v);
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+      const int k = i - o;
+      if (k >= 0 && k < kSTaps) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m) acc[m][o] = fmaf(t.w[k], v[m], acc[m][o]);
+      }
+    }
+  }
+}
+
+// Horizontal pass from LDS row `row` of NM maps: out[m][o] = sum_k w_k V[m][row][c0 + o + k].
+template <int NM>
+__device__ inline void horizontal4(const Taps& t, const float (*V)[kSTH][kSPad], int row, int c0, float (&out)[NM][4]) {
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    float win[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 f = *reinterpret_cast<const float4*>(&V[m][row][c0 + 4 * q]);
+      win[4 * q] = f.x;
+      win[4 * q + 1] = f.y;
+      win[4 * q + 2] = f.z;
+      win[4 * q + 3] = f.w;
+    }
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+      float a = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kSTaps; ++k) a = fmaf(t.w[k], win[o + k], a);
+      out[m][o] = a;
+    }
+  }
+}
+
+__device__ inline float block_sum256(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__global__ __launch_bounds__(256) void l1_ssim_fwd_kernel(int H, int W, int C, const float* __restrict__ x,
+                                                          const float* __restrict__ y, Taps taps, float inv_count,
+                                                          float* __restrict__ gmap, float2* __restrict__ partial) {
+  __shared__ __align__(16) float V[5][kSTH][kSPad];
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int ox = blockIdx.x * kSTW;  // first output column
+  const int r0 = blockIdx.y * kSTH;  // first output row
+  // columns 64..67 of every LDS row feed only outputs past the tile: keep them finite
+  for (int i = tid; i < 5 * kSTH * 4; i += 256) V[i / (kSTH * 4)][(i / 4) % kSTH][kSCols + (i & 3)] = 0.0f;
+  const int vj = tid & 63, vq = tid >> 6;  // vertical pass: column, group of 4 rows
+  const int vcol = ox - kSR + vj;
+  const bool vcol_in = vcol >= 0 && vcol < W;
+  const int hr = tid >> 4, hs = tid & 15;  // horizontal pass: row, group of 4 columns
+  const bool h_on = 4 * hs < kSTW;
+  const int64_t plane = (int64_t)H * W * C;
+  float l1_acc = 0.0f, ss_acc = 0.0f;
+  for (int ch = 0; ch < C; ++ch) {
+    float a[5][4];
+    vertical4<5>(taps, r0 + 4 * vq - kSR, H, vcol_in,
+                 [&](bool in, int r, float* v) {
+                   float xv = 0.0f, yv = 0.0f;
+                   if (in) {
+                     const int64_t o = ((int64_t)r * W + vcol) * C + ch;
+                     xv = x[o];
+                     yv = y[o];
+                   }
+                   v[0] = xv;
+                   v[1] = yv;
+                   v[2] = xv * xv;
+                   v[3] = yv * yv;
+                   v[4] = xv * yv;
+                 },
+                 a);
+    __syncthreads();  // the previous channel's horizontal pass is done with V
+#pragma unroll
+    for (int m = 0; m < 5; ++m)
+#pragma unroll
+      for (int o = 0; o < 4; ++o) V[m][4 * vq + o][vj] = a[m][o];
+    __syncthreads();
+    if (!h_on) continue;
+    float b[5][4];
+    horizontal4<5>(taps, V, hr, 4 * hs, b);
+    const int orow = r0 + hr;
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+      const int ocol = ox + 4 * hs + o;
+      if (4 * hs + o >= kSTW || ocol >= W || orow >= H) continue;
+      const float mu1 = b[0][o], mu2 = b[1][o];
+      const float m11 = mu1 * mu1, m22 = mu2 * mu2, m12 = mu1 * mu2;
+      const float d11 = b[2][o] - m11;
+      const float s11 = fmaxf(0.0f, d11), s22 = fmaxf(0.0f, b[3][o] - m22);
+      const float s12 = b[4][o] - m12;
+      const float A = 2.0f * m12 + kC1, B = 2.0f * s12 + kC2;
+      const float Cc = (m11 + m22) + kC1, D = (s11 + s22) + kC2;
+      const float num = A * B, den = Cc * D;
+      const float raw = num / den;
+      ss_acc += fminf(1.0f, fmaxf(-1.0f, raw));
+      const int64_t p = ((int64_t)orow * W + ocol) * C + ch;
+      l1_acc += fabsf(x[p] - y[p]);
+      if (gmap != nullptr) {
+        // d map / d(mu1, blur(x^2), blur(x y)), times the clip gate and 1 / count
+        const float G = inv_count * (tie_step(raw + 1.0f) * tie_step(1.0f - raw));
+        const float dnum = G / den, dden = -(G * raw) / den;
+        const float dA = dnum * B, dB = dnum * A, dCc = dden * D, dD = dden * Cc;
+        const float de12 = 2.0f * dB;
+        const float dm12 = 2.0f * dA - de12;
+        const float de11 = dD * tie_step(d11);
+        const float dm11 = dCc - de11;
+        gmap[p] = 2.0f * mu1 * dm11 + mu2 * dm12;
+        gmap[plane + p] = de11;
+        gmap[2 * plane + p] = de12;
+      }
+    }
+  }
+  const float l1s = block_sum256(l1_acc, red);
+  const float sss = block_sum256(ss_acc, red);
+  if (tid == 0) partial[blockIdx.y * gridDim.x + blockIdx.x] = make_float2(l1s, sss);
+}
+
+// out[0] = sum of |x - y| / count, out[1] = sum of the clipped map / count.
+__global__ __launch_bounds__(1024) void l1_ssim_sum_kernel(const float2* __restrict__ partial, int nb,
+                                                           float inv_count, float* __restrict__ out) {
+  __shared__ float red[2][16];
+  float a = 0.0f, b = 0.0f;
+  for (int i = threadIdx.x; i < nb; i += 1024) {
+    const float2 v = partial[i];
+    a += v.x;
+    b += v.y;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    a += __shfl_xor(a, o, 64);
+    b += __shfl_xor(b, o, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    red[0][threadIdx.x >> 6] = a;
+    red[1][threadIdx.x >> 6] = b;
+  }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    float s = 0.0f;
+    for (int w = 0; w < 16; ++w) s += red[threadIdx.x][w];
+    out[threadIdx.x] = s * inv_count;
+  }
+}
+
+__global__ __launch_bounds__(256) void l1_ssim_bwd_kernel(int H, int W, int C, const float* __restrict__ x,
+                                                          const float* __restrict__ y, Taps taps, float inv_count,
+                                                          const float* __restrict__ gmap,
+                                                          const float* __restrict__ grad_out,
+                                                          float* __restrict__ grad) {
+  __shared__ __align__(16) float V[3][kSTH][kSPad];
+  const int tid = threadIdx.x;
+  const int ox = blockIdx.x * kSTW, r0 = blockIdx.y * kSTH;
+  for (int i = tid; i < 3 * kSTH * 4; i += 256) V[i / (kSTH * 4)][(i / 4) % kSTH][kSCols + (i & 3)] = 0.0f;
+  const int vj = tid & 63, vq = tid >> 6;
+  const int vcol = ox - kSR + vj;
+  const bool vcol_in = vcol >= 0 && vcol < W;
+  const int hr = tid >> 4, hs = tid & 15;
+  const bool h_on = 4 * hs < kSTW;
+  const int64_t plane = (int64_t)H * W * C;
+  const float g_l1 = grad_out[0] * inv_count, g_ss = grad_out[1];
+  for (int ch = 0; ch < C; ++ch) {
+    float a[3][4];
+    vertical4<3>(taps, r0 + 4 * vq - kSR, H, vcol_in,
+                 [&](bool in, int r, float* v) {
+                   v[0] = v[1] = v[2] = 0.0f;
+                   if (in) {
+                     const int64_t o = ((int64_t)r * W + vcol) * C + ch;
+                     v[0] = gmap[o];
+                     v[1] = gmap[plane + o];
+                     v[2] = gmap[2 * plane + o];
+                   }
+                 },
+                 a);
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < 3; ++m)
+#pragma unroll
+      for (int o = 0; o < 4; ++o) V[m][4 * vq + o][vj] = a[m][o];
+    __syncthreads();
+    if (!h_on) continue;
+    float b[3][4];
+    horizontal4<3>(taps, V, hr, 4 * hs, b);
+    const int orow = r0 + hr;
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+      const int ocol = ox + 4 * hs + o;
+      if (4 * hs + o >= kSTW || ocol >= W || orow >= H) continue;
+      const int64_t p = ((int64_t)orow * W + ocol) * C + ch;
+      const float xv = x[p], yv = y[p], d = xv - yv;
+      const float sg = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f);
+      const float gs = b[0][o] + 2.0f * xv * b[1][o] + yv * b[2][o];
+      grad[p] = g_ss * gs + g_l1 * sg;
+    }
+  }
+}
+
+Taps make_taps() {
+  Taps t;
+  double s = 0.0, e[kSTaps];
+  for (int k = 0; k < kSTaps; ++k) {
+    const double d = (double)(k - kSR);
+    e[k] = std::exp(-d * d / (2.0 * 1.5 * 1.5));
+    s += e[k];
+  }
+  for (int k = 0; k < kSTaps; ++k) t.w[k] = (float)(e[k] / s);
+  return t;
+}
+
+struct SsimLayout {
+  int64_t count;
+  dim3 grid;
+  size_t gmap_off, part_off, total;
+};
+
+SsimLayout ssim_layout(int H, int W, int C) {
+  SsimLayout L;
+  L.count = (int64_t)H * W * C;
+  L.grid = dim3((unsigned)div_up(W, kSTW), (unsigned)div_up(H, kSTH));
+  L.gmap_off = 0;
+  L.part_off = ((size_t)3 * L.count * sizeof(float) + 255) & ~(size_t)255;
+  L.total = L.part_off + (size_t)L.grid.x * L.grid.y * sizeof(float2);
+  return L;
+}
+
+}  // namespace
+}  // namespace gs
+
+using namespace gs;
+
+extern "C" size_t gs_l1_ssim_workspace_size(int height, int width, int channels) {
+  if (height <= 0 || width <= 0 || channels <= 0) return 0;
+  return ssim_layout(height, width, channels).total;
+}
+
+extern "C" int gs_l1_ssim(void* stream, int height, int width, int channels, const float* pred,
+                          const float* target, float* out, int with_grad, void* workspace, size_t workspace_bytes) {
+  GS_REQUIRE(height > 0 && width > 0 && channels > 0, "gs_l1_ssim: bad image shape %dx%dx%d", height, width,
+             channels);
+  GS_REQUIRE(pred && target && out && workspace, "gs_l1_ssim: NULL argument");
+  GS_REQUIRE(height <= 65535 * kSTH, "gs_l1_ssim: height %d too large", height);
+  const SsimLayout L = ssim_layout(height, width, channels);
+  GS_REQUIRE(workspace_bytes >= L.total, "gs_l1_ssim: workspace of %zu bytes, %zu needed", workspace_bytes, L.total);
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  const float inv = (float)(1.0 / (double)L.count);
+  float2* part = (float2*)(ws + L.part_off);
+  hipLaunchKernelGGL(l1_ssim_fwd_kernel, L.grid, dim3(256), 0, s, height, width, channels, pred, target, make_taps(),
+                     inv, with_grad ? (float*)(ws + L.gmap_off) : nullptr, part);
+  GS_LAUNCH_CHECK("l1_ssim_fwd_kernel");
+  hipLaunchKernelGGL(l1_ssim_sum_kernel, dim3(1), dim3(1024), 0, s, (const float2*)part, (int)(L.grid.x * L.grid.y),
+                     inv, out);
+  GS_LAUNCH_CHECK("l1_ssim_sum_kernel");
+  return GS_OK;
+}
+
+extern "C" int gs_l1_ssim_bwd(void* stream, int height, int width, int channels, const float* pred,
+                              const float* target, const float* grad_out, const void* workspace,
+                              size_t workspace_bytes, float* grad_pred) {
+  GS_REQUIRE(height > 0 && width > 0 && channels > 0, "gs_l1_ssim_bwd: bad image shape %dx%dx%d", height, width,
+             channels);
+  GS_REQUIRE(pred && target && grad_out && workspace && grad_pred, "gs_l1_ssim_bwd: NULL argument");
+  GS_REQUIRE(height <= 65535 * kSTH, "gs_l1_ssim_bwd: height %d too large", height);
+  const SsimLayout L = ssim_layout(height, width, channels);
+  GS_REQUIRE(workspace_bytes >= L.total, "gs_l1_ssim_bwd: workspace of %zu bytes, %zu needed", workspace_bytes,
+             L.total);
+  hipStream_t s = (hipStream_t)stream;
+  const float inv = (float)(1.0 / (double)L.count);
+  hipLaunchKernelGGL(l1_ssim_bwd_kernel, L.grid, dim3(256), 0, s, height, width, channels, pred, target, make_taps(),
+                     inv, (const float*)((const char*)workspace + L.gmap_off), grad_out, grad_pred);
+  GS_LAUNCH_CHECK("l1_ssim_bwd_kernel");
+  return GS_OK;
+}

@@ -41,9 +41,13 @@ _SIGS = {
     "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "gs_preprocess_bwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P, _P],
     "gs_l1_loss": [_P, _I64, _P, _P, _P, _P],
+    "gs_mse_loss": [_P, _I64, _P, _P, _P, _P],
+    "gs_l1_ssim_workspace_size": [_I, _I, _I],
+    "gs_l1_ssim": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _SZ],
+    "gs_l1_ssim_bwd": [_P, _I, _I, _I, _P, _P, _P, _P, _SZ, _P],
     "gs_densify_accumulate": [_P, _I64, _P, _P, _P, _F, _F, _P, _P, _P, _P, _P, _P],
 }
-_RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ}
+_RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_l1_ssim_workspace_size": _SZ}
 
 _lib = None
 

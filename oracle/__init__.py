@@ -8,7 +8,8 @@ It wraps ``libgsoracle.so`` (``gs_oracle.c`` / ``gs_oracle_impl.h``), a C restat
 of the reference ghif/jax-gs in float32 (``dtype=np.float32``) and float64
 (``dtype=np.float64``), and restates in NumPy the host-side glue of
 ``jax_gs/renderer/renderer.py:15-107`` (view-independent plumbing, tile ranges and
-the ``extras`` dict).
+the ``extras`` dict) and the losses of ``jax_gs/training/losses.py:4-75`` (L1, MSE,
+SSIM with its VJP written out by hand).
 
 Pinning (what checks this oracle independently of its own formulas) is listed in
 ``tests/test_oracle.py``; every function below is pinned there.
@@ -254,3 +255,107 @@ def l1_loss_and_grad(image, target):
     d = image.astype(np.float32) - target.astype(np.float32)
     cnt = np.float32(d.size)
     return np.float32(np.abs(d).astype(np.float64).mean()), (np.sign(d) * (np.float32(1) / cnt)).astype(np.float32)
+
+
+def mse_loss_and_grad(image, target):
+    """losses.py:10-14: mean((pred - target)^2) and its seed 2 d * (1/count)."""
+    d = image.astype(np.float32) - target.astype(np.float32)
+    cnt = np.float32(d.size)
+    return np.float32((d.astype(np.float64) ** 2).mean()), (np.float32(2) * d * (np.float32(1) / cnt)).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------------------
+# SSIM (losses.py:16-75): separable Gaussian window, 'SAME' zero padding, clipped map.
+SSIM_C1 = 0.01 ** 2
+SSIM_C2 = 0.03 ** 2
+
+
+def ssim_window(size=11, sigma=1.5, dtype=np.float32):
+    """losses.py:24-29: taps exp(-x^2 / (2 sigma^2)) for x = -(size//2)..size//2, normalised."""
+    x = (np.arange(size) - size // 2).astype(dtype)
+    k = np.exp(-(x * x) / dtype(2.0 * sigma * sigma)).astype(dtype)
+    return (k / k.sum(dtype=dtype)).astype(dtype)
+
+
+def ssim_blur(img, w):
+    """losses.py:35-47: depthwise correlation with w along H, then along W, each with
+    'SAME' zero padding (len(w)//2 on both sides).  img is [H, W, C]."""
+    H, W = img.shape[:2]
+    r = len(w) // 2
+    dt = img.dtype
+    p = np.zeros((H + 2 * r,) + img.shape[1:], dt)
+    p[r:r + H] = img
+    v = np.zeros_like(img)
+    for k in range(len(w)):
+        v = v + w[k] * p[k:k + H]
+    p = np.zeros((H, W + 2 * r) + img.shape[2:], dt)
+    p[:, r:r + W] = v
+    out = np.zeros_like(img)
+    for k in range(len(w)):
+        out = out + w[k] * p[:, k:k + W]
+    return out
+
+
+def _ssim_parts(img1, img2, dtype):
+    w = ssim_window(dtype=dtype)
+    x = np.asarray(img1, dtype)
+    y = np.asarray(img2, dtype)
+    mu1, mu2 = ssim_blur(x, w), ssim_blur(y, w)
+    m11, m22, m12 = mu1 * mu1, mu2 * mu2, mu1 * mu2
+    d11 = ssim_blur(x * x, w) - m11
+    d22 = ssim_blur(y * y, w) - m22
+    s11, s22 = np.maximum(dtype(0), d11), np.maximum(dtype(0), d22)
+    s12 = ssim_blur(x * y, w) - m12
+    c1, c2 = dtype(SSIM_C1), dtype(SSIM_C2)
+    A, B = dtype(2) * m12 + c1, dtype(2) * s12 + c2
+    Cc, D = m11 + m22 + c1, s11 + s22 + c2
+    raw = (A * B) / (Cc * D)
+    return dict(w=w, x=x, y=y, mu1=mu1, mu2=mu2, d11=d11, A=A, B=B, Cc=Cc, D=D, raw=raw)
+
+
+def ssim_map(img1, img2, dtype=np.float64):
+    """losses.py:49-64: the clipped per-value SSIM map [H, W, C]."""
+    return np.clip(_ssim_parts(img1, img2, dtype)["raw"], -1.0, 1.0)
+
+
+def ssim(img1, img2, dtype=np.float64):
+    """losses.py:16-68 (size_average): mean of the clipped SSIM map."""
+    return ssim_map(img1, img2, dtype).astype(np.float64).mean()
+
+
+def d_ssim_loss(pred, target, dtype=np.float64):
+    """losses.py:70-75: max(0, (1 - ssim) / 2)."""
+    return max(0.0, (1.0 - ssim(pred, target, dtype)) / 2.0)
+
+
+def _tie_grad(z):
+    """d max(0, z)/dz with JAX's balanced tie: 1 above, 1/2 at 0, 0 below."""
+    return np.where(z > 0, 1.0, np.where(z == 0, 0.5, 0.0))
+
+
+def ssim_vjp(img1, img2, g_ssim, dtype=np.float64):
+    """Cotangent of img1 for the mean SSIM given its cotangent g_ssim: reverse-mode AD
+    of losses.py:49-68 written out by hand.  Ties of max/clip pass half the cotangent
+    (lax.max/min).  The blur is a correlation with a symmetric kernel and zero
+    padding, so its adjoint is the same blur."""
+    P = _ssim_parts(img1, img2, dtype)
+    raw, A, B, Cc, D = P["raw"], P["A"], P["B"], P["Cc"], P["D"]
+    # clip(raw, -1, 1) = minimum(1, maximum(-1, raw))
+    clip_d = _tie_grad(raw + 1.0) * _tie_grad(1.0 - raw)
+    G = dtype(g_ssim) / dtype(raw.size) * clip_d.astype(dtype)
+    num, den = A * B, Cc * D
+    dnum, dden = G / den, -G * num / (den * den)
+    dA, dB, dCc, dD = dnum * B, dnum * A, dden * D, dden * Cc
+    de12 = dtype(2) * dB                                   # s12 = e12 - m12
+    dm12 = dtype(2) * dA - de12
+    de11 = dD * _tie_grad(P["d11"]).astype(dtype)          # s11 = max(0, e11 - m11)
+    dm11 = dCc - de11
+    dmu1 = dtype(2) * P["mu1"] * dm11 + P["mu2"] * dm12    # m11 = mu1^2, m12 = mu1 mu2
+    w = P["w"]
+    return ssim_blur(dmu1, w) + dtype(2) * P["x"] * ssim_blur(de11, w) + P["y"] * ssim_blur(de12, w)
+
+
+def d_ssim_vjp(pred, target, g, dtype=np.float64):
+    """Cotangent of pred for d_ssim_loss = max(0, (1 - ssim) / 2) with cotangent g."""
+    s = ssim(pred, target, dtype)
+    return ssim_vjp(pred, target, -0.5 * g * float(_tie_grad(np.float64((1.0 - s) / 2.0))), dtype)

@@ -278,3 +278,80 @@ def test_backward_tile_order(cuda, cfg):
             out.append((_np(grec), _np(gbg)))
     assert _rel(out[0][0], out[1][0]) <= 1e-5
     assert _rel(out[0][1], out[1][1]) <= 1e-5
+
+
+def _l1_ssim_gpu(cuda, pred_np, tgt_np, gout):
+    from jax_gs_amd import _lib
+
+    H, W, C = pred_np.shape
+    pred = torch.from_numpy(pred_np).to(cuda)
+    tgt = torch.from_numpy(tgt_np).to(cuda)
+    nb = _lib.lib().gs_l1_ssim_workspace_size(H, W, C)
+    ws = torch.empty((nb,), dtype=torch.uint8, device=cuda)
+    out = torch.empty((2,), device=cuda)
+    s = _lib.stream_handle(cuda)
+    _lib.call("gs_l1_ssim", s, H, W, C, _lib.ptr(pred), _lib.ptr(tgt), _lib.ptr(out), 1, _lib.ptr(ws), nb)
+    g = torch.tensor(gout, dtype=torch.float32, device=cuda)
+    grad = torch.empty_like(pred)
+    _lib.call("gs_l1_ssim_bwd", s, H, W, C, _lib.ptr(pred), _lib.ptr(tgt), _lib.ptr(g), _lib.ptr(ws), nb,
+              _lib.ptr(grad))
+    return _np(out), _np(grad)
+
+
+@pytest.mark.parametrize("shape", [(32, 32, 3), (37, 41, 3), (70, 55, 1), (378, 504, 3), (1080, 1920, 3)])
+def test_l1_ssim_parity(cuda, shape):
+    """losses.py:4-8 and :16-68 in one kernel pair: the L1 and SSIM means against the
+    float64 oracle, and the image gradient of a * l1 + b * ssim against the oracle's
+    L1 seed and hand-written SSIM VJP (shapes: the reference's test image, odd sizes
+    that end inside a tile, one channel, cfg1's and cfg2's frames)."""
+    rng = np.random.default_rng(sum(shape))
+    tgt = rng.uniform(0, 1, shape).astype(np.float32)
+    pred = np.clip(tgt + rng.normal(0, 0.2, shape), 0, 1).astype(np.float32)
+    a, b = 0.8, -0.1  # trainer.py:26 weights of l1 and d_ssim = (1 - ssim) / 2
+    out, grad = _l1_ssim_gpu(cuda, pred, tgt, [a, b])
+    want_l1, seed = oracle.l1_loss_and_grad(pred, tgt)
+    want_s = oracle.ssim(pred, tgt)
+    assert abs(out[0] - want_l1) <= 1e-6 * want_l1
+    assert abs(out[1] - want_s) <= 1e-5
+    want_g = a * seed.astype(np.float64) + oracle.ssim_vjp(pred, tgt, b)
+    assert _rel(grad, want_g) <= 1e-4
+    assert np.abs(grad - want_g).max() <= 1e-3 * np.abs(want_g).max()
+
+
+def test_ssim_identical_images_and_losses_module(cuda):
+    """test_training.py:21-38 through the host module: ssim(t, t) = 1, d_ssim(t, t) = 0,
+    bounds, d_ssim = (1 - ssim) / 2, and l1_ssim_loss's total and gradient."""
+    from jax_gs_amd.training import losses
+
+    rng = np.random.default_rng(0)
+    t_np = rng.uniform(0, 1, (32, 32, 3)).astype(np.float32)
+    p_np = (t_np + 0.1 * rng.uniform(0, 1, t_np.shape)).astype(np.float32)
+    t = torch.from_numpy(t_np).to(cuda)
+    assert abs(float(losses.ssim(t, t)) - 1.0) <= 1e-6
+    assert abs(float(losses.d_ssim_loss(t, t))) <= 1e-6
+    p = torch.from_numpy(p_np).to(cuda).requires_grad_(True)
+    s = float(losses.ssim(p, t).detach())
+    d = float(losses.d_ssim_loss(p, t).detach())
+    assert 0.0 <= s <= 1.0 and 0.0 <= d <= 1.0 and abs(d - (1.0 - s) / 2.0) <= 1e-7
+    total, l1, dss = losses.l1_ssim_loss(p, t, 0.2)
+    total.backward()
+    want_l1, seed = oracle.l1_loss_and_grad(p_np, t_np)
+    want_total = 0.8 * want_l1 + 0.2 * oracle.d_ssim_loss(p_np, t_np)
+    assert abs(float(total) - want_total) <= 1e-6
+    want_g = 0.8 * seed.astype(np.float64) + 0.2 * oracle.d_ssim_vjp(p_np, t_np, 1.0)
+    assert _rel(_np(p.grad), want_g) <= 1e-4
+
+
+def test_mse_loss(cuda):
+    """losses.py:10-14 and its seed, through the host module."""
+    from jax_gs_amd.training import losses
+
+    rng = np.random.default_rng(4)
+    p_np = rng.uniform(0, 1, (37, 41, 3)).astype(np.float32)
+    t_np = rng.uniform(0, 1, p_np.shape).astype(np.float32)
+    p = torch.from_numpy(p_np).to(cuda).requires_grad_(True)
+    loss = losses.mse_loss(p, torch.from_numpy(t_np).to(cuda))
+    loss.backward()
+    want, seed = oracle.mse_loss_and_grad(p_np, t_np)
+    assert abs(float(loss.detach()) - float(want)) <= 1e-6 * float(want)
+    np.testing.assert_allclose(_np(p.grad), seed, rtol=1e-6, atol=1e-12)

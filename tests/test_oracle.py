@@ -439,3 +439,91 @@ def test_densify_float32_matches_float64():
     np.testing.assert_allclose(out32[0], out64[0], rtol=1e-5)
     np.testing.assert_array_equal(out32[1], out64[1])
     np.testing.assert_array_equal(out32[2], out64[2])
+
+
+# ---------------------------------------------------------------------------------------
+# SSIM restatement (losses.py:16-75)
+def test_ssim_window_is_the_normalised_gaussian():
+    from scipy.signal.windows import gaussian
+
+    w = oracle.ssim_window(dtype=np.float64)
+    g = gaussian(11, std=1.5)
+    np.testing.assert_allclose(w, g / g.sum(), rtol=1e-14)
+
+
+def test_ssim_blur_matches_scipy():
+    """Separable 'SAME' zero-padded correlation = scipy's correlate1d twice = a 2-D
+    convolution with the outer product of the taps."""
+    from scipy.ndimage import correlate1d
+    from scipy.signal import convolve2d
+
+    rng = np.random.default_rng(1)
+    img = rng.normal(size=(12, 17, 3))
+    w = oracle.ssim_window(dtype=np.float64)
+    got = oracle.ssim_blur(img, w)
+    want = correlate1d(correlate1d(img, w, axis=0, mode="constant"), w, axis=1, mode="constant")
+    np.testing.assert_allclose(got, want, atol=1e-13)
+    for c in range(3):
+        np.testing.assert_allclose(got[..., c], convolve2d(img[..., c], np.outer(w, w), mode="same"), atol=1e-13)
+
+
+def test_ssim_reference_fixture():
+    """test_training.py:21-38: bounds, d_ssim = (1 - ssim) / 2, perfect match."""
+    rng = np.random.default_rng(0)
+    target = rng.uniform(0, 1, (32, 32, 3))
+    pred = target + 0.1 * rng.uniform(0, 1, target.shape)
+    s = oracle.ssim(pred, target)
+    assert 0.0 <= s <= 1.0
+    assert 0.0 <= oracle.d_ssim_loss(pred, target) <= 1.0
+    assert np.isclose(oracle.d_ssim_loss(pred, target), (1.0 - s) / 2.0)
+    assert np.isclose(oracle.ssim(target, target), 1.0)
+    assert np.isclose(oracle.d_ssim_loss(target, target), 0.0)
+
+
+def test_ssim_constant_images_closed_form():
+    """Constant images a and b: away from the zero-padded border (>= 5 pixels) the means
+    are a and b and the variances 0, so the map is (2ab + C1) / (a^2 + b^2 + C1)."""
+    a, b = 0.3, 0.7
+    x = np.full((24, 26, 2), a)
+    y = np.full((24, 26, 2), b)
+    m = oracle.ssim_map(x, y)
+    want = (2 * a * b + oracle.SSIM_C1) / (a * a + b * b + oracle.SSIM_C1)
+    np.testing.assert_allclose(m[5:-5, 5:-5], want, rtol=1e-12)
+    assert np.all(m[:5] != want)  # the border sees the zero padding
+
+
+def test_ssim_vjp_matches_finite_differences():
+    rng = np.random.default_rng(2)
+    x = rng.uniform(0, 1, (9, 13, 2))
+    y = rng.uniform(0, 1, (9, 13, 2))
+    g = oracle.ssim_vjp(x, y, 1.0)
+    num = np.zeros_like(x)
+    eps = 1e-6
+    for idx in np.ndindex(x.shape):
+        xp, xm = x.copy(), x.copy()
+        xp[idx] += eps
+        xm[idx] -= eps
+        num[idx] = (oracle.ssim(xp, y) - oracle.ssim(xm, y)) / (2 * eps)
+    assert np.linalg.norm(num - g) / np.linalg.norm(num) < 1e-6
+    # the cotangent scales the result; d_ssim's cotangent is -1/2 of ssim's
+    np.testing.assert_allclose(oracle.ssim_vjp(x, y, 3.0), 3.0 * g, rtol=1e-12)
+    np.testing.assert_allclose(oracle.d_ssim_vjp(x, y, 1.0), -0.5 * g, rtol=1e-12)
+
+
+def test_ssim_float32_matches_float64():
+    rng = np.random.default_rng(3)
+    x = rng.uniform(0, 1, (40, 50, 3)).astype(np.float32)
+    y = rng.uniform(0, 1, (40, 50, 3)).astype(np.float32)
+    assert abs(oracle.ssim(x, y, np.float32) - oracle.ssim(x, y, np.float64)) < 1e-6
+    g32 = oracle.ssim_vjp(x, y, 1.0, np.float32)
+    g64 = oracle.ssim_vjp(x, y, 1.0, np.float64)
+    assert np.linalg.norm(g32 - g64) / np.linalg.norm(g64) < 1e-4
+
+
+def test_mse_closed_form():
+    """test_training.py:9-19: mean of (0.1^2, 0.1^2, 0) = 0.00666..."""
+    pred = np.array([1.0, 2.0, 3.0], np.float32)
+    target = np.array([1.1, 1.9, 3.0], np.float32)
+    loss, seed = oracle.mse_loss_and_grad(pred, target)
+    assert np.isclose(loss, 0.00666667, atol=1e-7)
+    np.testing.assert_allclose(seed, 2 * (pred - target) / 3, rtol=1e-6)
