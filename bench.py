@@ -121,7 +121,25 @@ def main():
                       _lib.ptr(cam.W2C.contiguous()), W, H, float(cam.fx), float(cam.fy), float(cam.cx),
                       float(cam.cy), _lib.ptr(grec), *[_lib.ptr(o) for o in outs])
             mark("t6")
+        # the trainer's other loss term (trainer.py:18-26): L1 + SSIM forward and VJP of
+        # the same frame, timed beside the step (the headline step seeds L1 only)
+        Hc, Wc, Cc = image.shape
+        ws_bytes = _lib.lib().gs_l1_ssim_workspace_size(Hc, Wc, Cc)
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+        lo = torch.empty((2,), device=dev)
+        gout = torch.tensor([0.8, -0.1], device=dev)
+        gss = torch.empty_like(image)
+        for _ in range(reps):
+            mark("s0")
+            _lib.call("gs_l1_ssim", s_, Hc, Wc, Cc, _lib.ptr(image), _lib.ptr(tgt), _lib.ptr(lo), 1, _lib.ptr(ws),
+                      ws_bytes)
+            mark("s1")
+            _lib.call("gs_l1_ssim_bwd", s_, Hc, Wc, Cc, _lib.ptr(image), _lib.ptr(tgt), _lib.ptr(gout), _lib.ptr(ws),
+                      ws_bytes, _lib.ptr(gss))
+            mark("s2")
     torch.cuda.synchronize()
+    loss_ms = {nm: float(np.median([ev[a][r].elapsed_time(ev[z][r]) for r in range(reps)]))
+               for nm, a, z in (("l1_ssim_fwd", "s0", "s1"), ("l1_ssim_bwd", "s1", "s2"))}
     names = ["preprocess_fwd", "binning", "composite_fwd", "l1_loss", "composite_bwd", "preprocess_bwd"]
     stage_ms = {}
     for i, nm in enumerate(names):
@@ -195,6 +213,7 @@ def main():
         "stage_ms": stage_ms,
         "stage_GBps": stage_gbs,
         "stage_TFLOPs": stage_tflops,
+        "loss_ms": loss_ms,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

@@ -88,6 +88,7 @@ __device__ inline void horizontal4(const Taps& t, const float (*V)[kSTH][kSPad],
       for (int k = 0; k < kSTaps; ++k) a = fmaf(t.w[k], win[o + k], a);
       out[m][o] = a;
     }
+    __asm__ volatile("" ::: "memory");  // one map's window in registers at a time
   }
 }
 
@@ -100,14 +101,25 @@ __device__ inline float block_sum256(float v, float* red) {
   return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-__global__ __launch_bounds__(256) void l1_ssim_fwd_kernel(int H, int W, int C, const float* __restrict__ x,
-                                                          const float* __restrict__ y, Taps taps, float inv_count,
-                                                          float* __restrict__ gmap, float2* __restrict__ partial) {
+// XCD-aware tile order: consecutive workgroups go round-robin to the 8 XCDs; workgroup
+// b takes tile (b % 8) * per + b / 8, so each XCD's L2 holds a band of tile rows and
+// the halo rows two vertically adjacent tiles share are fetched once.
+__device__ inline int ssim_tile_of_block(int b, int T) { return (b & 7) * ((T + 7) >> 3) + (b >> 3); }
+
+// Forward, CC channels (1..4), one channel at a time (the next channel's loads hit the
+// cache).  The gradient maps of a channel are staged in LDS and leave as whole rows.
+template <int CC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void l1_ssim_fwd_kernel(
+    int H, int W, int TX, int T, const float* __restrict__ x, const float* __restrict__ y, Taps taps,
+    float inv_count, float* __restrict__ gmap, float2* __restrict__ partial) {
   __shared__ __align__(16) float V[5][kSTH][kSPad];
+  __shared__ float Gs[3][kSTH][kSTW];
   __shared__ float red[4];
+  const int tile = ssim_tile_of_block(blockIdx.x, T);
+  if (tile >= T) return;
   const int tid = threadIdx.x;
-  const int ox = blockIdx.x * kSTW;  // first output column
-  const int r0 = blockIdx.y * kSTH;  // first output row
+  const int ox = (tile % TX) * kSTW;  // first output column
+  const int r0 = (tile / TX) * kSTH;  // first output row
   // columns 64..67 of every LDS row feed only outputs past the tile: keep them finite
   for (int i = tid; i < 5 * kSTH * 4; i += 256) V[i / (kSTH * 4)][(i / 4) % kSTH][kSCols + (i & 3)] = 0.0f;
   const int vj = tid & 63, vq = tid >> 6;  // vertical pass: column, group of 4 rows
@@ -115,18 +127,15 @@ __global__ __launch_bounds__(256) void l1_ssim_fwd_kernel(int H, int W, int C, c
   const bool vcol_in = vcol >= 0 && vcol < W;
   const int hr = tid >> 4, hs = tid & 15;  // horizontal pass: row, group of 4 columns
   const bool h_on = 4 * hs < kSTW;
-  const int64_t plane = (int64_t)H * W * C;
+  const int plane = H * W * CC;  // one gradient map, channel-planar [CC][H][W]
   float l1_acc = 0.0f, ss_acc = 0.0f;
-  for (int ch = 0; ch < C; ++ch) {
+#pragma unroll 1
+  for (int ch = 0; ch < CC; ++ch) {
     float a[5][4];
     vertical4<5>(taps, r0 + 4 * vq - kSR, H, vcol_in,
                  [&](bool in, int r, float* v) {
-                   float xv = 0.0f, yv = 0.0f;
-                   if (in) {
-                     const int64_t o = ((int64_t)r * W + vcol) * C + ch;
-                     xv = x[o];
-                     yv = y[o];
-                   }
+                   const int o = (r * W + vcol) * CC + ch;  // 3 * count < 2^31 (checked by the host)
+                   const float xv = in ? x[o] : 0.0f, yv = in ? y[o] : 0.0f;
                    v[0] = xv;
                    v[1] = yv;
                    v[2] = xv * xv;
@@ -134,50 +143,61 @@ __global__ __launch_bounds__(256) void l1_ssim_fwd_kernel(int H, int W, int C, c
                    v[4] = xv * yv;
                  },
                  a);
-    __syncthreads();  // the previous channel's horizontal pass is done with V
+    if (ch > 0) __syncthreads();  // the previous channel is done with V and Gs
 #pragma unroll
     for (int m = 0; m < 5; ++m)
 #pragma unroll
       for (int o = 0; o < 4; ++o) V[m][4 * vq + o][vj] = a[m][o];
     __syncthreads();
-    if (!h_on) continue;
-    float b[5][4];
-    horizontal4<5>(taps, V, hr, 4 * hs, b);
-    const int orow = r0 + hr;
+    if (h_on) {
+      float b[5][4];
+      horizontal4<5>(taps, V, hr, 4 * hs, b);
+      const int orow = r0 + hr;
 #pragma unroll
-    for (int o = 0; o < 4; ++o) {
-      const int ocol = ox + 4 * hs + o;
-      if (4 * hs + o >= kSTW || ocol >= W || orow >= H) continue;
-      const float mu1 = b[0][o], mu2 = b[1][o];
-      const float m11 = mu1 * mu1, m22 = mu2 * mu2, m12 = mu1 * mu2;
-      const float d11 = b[2][o] - m11;
-      const float s11 = fmaxf(0.0f, d11), s22 = fmaxf(0.0f, b[3][o] - m22);
-      const float s12 = b[4][o] - m12;
-      const float A = 2.0f * m12 + kC1, B = 2.0f * s12 + kC2;
-      const float Cc = (m11 + m22) + kC1, D = (s11 + s22) + kC2;
-      const float num = A * B, den = Cc * D;
-      const float raw = num / den;
-      ss_acc += fminf(1.0f, fmaxf(-1.0f, raw));
-      const int64_t p = ((int64_t)orow * W + ocol) * C + ch;
-      l1_acc += fabsf(x[p] - y[p]);
-      if (gmap != nullptr) {
+      for (int o = 0; o < 4; ++o) {
+        const int tc = 4 * hs + o, ocol = ox + tc;
+        if (tc >= kSTW || ocol >= W || orow >= H) continue;
+        const float mu1 = b[0][o], mu2 = b[1][o];
+        const float m11 = mu1 * mu1, m22 = mu2 * mu2, m12 = mu1 * mu2;
+        const float d11 = b[2][o] - m11;
+        const float s11 = fmaxf(0.0f, d11), s22 = fmaxf(0.0f, b[3][o] - m22);
+        const float s12 = b[4][o] - m12;
+        const float A = 2.0f * m12 + kC1, B = 2.0f * s12 + kC2;
+        const float Cc = (m11 + m22) + kC1, D = (s11 + s22) + kC2;
+        const float num = A * B, den = Cc * D;
+        // one reciprocal for the three quotients (den >= C1 C2 > 0; ~1 ulp)
+        const float rden = __builtin_amdgcn_rcpf(den);
+        const float raw = num * rden;
+        ss_acc += fminf(1.0f, fmaxf(-1.0f, raw));
+        const int p = (orow * W + ocol) * CC + ch;
+        l1_acc += fabsf(x[p] - y[p]);
         // d map / d(mu1, blur(x^2), blur(x y)), times the clip gate and 1 / count
         const float G = inv_count * (tie_step(raw + 1.0f) * tie_step(1.0f - raw));
-        const float dnum = G / den, dden = -(G * raw) / den;
+        const float dnum = G * rden, dden = -(G * raw) * rden;
         const float dA = dnum * B, dB = dnum * A, dCc = dden * D, dD = dden * Cc;
         const float de12 = 2.0f * dB;
         const float dm12 = 2.0f * dA - de12;
         const float de11 = dD * tie_step(d11);
         const float dm11 = dCc - de11;
-        gmap[p] = 2.0f * mu1 * dm11 + mu2 * dm12;
-        gmap[plane + p] = de11;
-        gmap[2 * plane + p] = de12;
+        Gs[0][hr][tc] = 2.0f * mu1 * dm11 + mu2 * dm12;
+        Gs[1][hr][tc] = de11;
+        Gs[2][hr][tc] = de12;
+      }
+    }
+    if (gmap != nullptr) {
+      __syncthreads();
+      // wave w writes rows w, w + 4, ... of the 3 x 16 staged rows, one value per lane
+      const int lane = tid & 63, wv = tid >> 6;
+      const int ncol = min(kSTW, W - ox);
+      for (int row = wv; row < 3 * kSTH; row += 4) {
+        const int m = row / kSTH, rr = row % kSTH, orow = r0 + rr;
+        if (orow < H && lane < ncol) gmap[m * plane + (ch * H + orow) * W + ox + lane] = Gs[m][rr][lane];
       }
     }
   }
   const float l1s = block_sum256(l1_acc, red);
   const float sss = block_sum256(ss_acc, red);
-  if (tid == 0) partial[blockIdx.y * gridDim.x + blockIdx.x] = make_float2(l1s, sss);
+  if (tid == 0) partial[tile] = make_float2(l1s, sss);
 }
 
 // out[0] = sum of |x - y| / count, out[1] = sum of the clipped map / count.
@@ -207,55 +227,69 @@ __global__ __launch_bounds__(1024) void l1_ssim_sum_kernel(const float2* __restr
   }
 }
 
-__global__ __launch_bounds__(256) void l1_ssim_bwd_kernel(int H, int W, int C, const float* __restrict__ x,
-                                                          const float* __restrict__ y, Taps taps, float inv_count,
-                                                          const float* __restrict__ gmap,
-                                                          const float* __restrict__ grad_out,
-                                                          float* __restrict__ grad) {
+// Backward: the image gradient of the tile (every channel) is staged in LDS and leaves
+// as whole rows.
+template <int CC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void l1_ssim_bwd_kernel(
+    int H, int W, int TX, int T, const float* __restrict__ x, const float* __restrict__ y, Taps taps,
+    float inv_count, const float* __restrict__ gmap, const float* __restrict__ grad_out,
+    float* __restrict__ grad) {
   __shared__ __align__(16) float V[3][kSTH][kSPad];
+  __shared__ float Go[kSTH][kSTW * CC];
+  const int tile = ssim_tile_of_block(blockIdx.x, T);
+  if (tile >= T) return;
   const int tid = threadIdx.x;
-  const int ox = blockIdx.x * kSTW, r0 = blockIdx.y * kSTH;
+  const int ox = (tile % TX) * kSTW, r0 = (tile / TX) * kSTH;
   for (int i = tid; i < 3 * kSTH * 4; i += 256) V[i / (kSTH * 4)][(i / 4) % kSTH][kSCols + (i & 3)] = 0.0f;
   const int vj = tid & 63, vq = tid >> 6;
   const int vcol = ox - kSR + vj;
   const bool vcol_in = vcol >= 0 && vcol < W;
   const int hr = tid >> 4, hs = tid & 15;
   const bool h_on = 4 * hs < kSTW;
-  const int64_t plane = (int64_t)H * W * C;
+  const int plane = H * W * CC;
   const float g_l1 = grad_out[0] * inv_count, g_ss = grad_out[1];
-  for (int ch = 0; ch < C; ++ch) {
+#pragma unroll 1
+  for (int ch = 0; ch < CC; ++ch) {
     float a[3][4];
     vertical4<3>(taps, r0 + 4 * vq - kSR, H, vcol_in,
                  [&](bool in, int r, float* v) {
-                   v[0] = v[1] = v[2] = 0.0f;
-                   if (in) {
-                     const int64_t o = ((int64_t)r * W + vcol) * C + ch;
-                     v[0] = gmap[o];
-                     v[1] = gmap[plane + o];
-                     v[2] = gmap[2 * plane + o];
-                   }
+                   const int q = (ch * H + r) * W + vcol;
+                   v[0] = in ? gmap[q] : 0.0f;
+                   v[1] = in ? gmap[plane + q] : 0.0f;
+                   v[2] = in ? gmap[2 * plane + q] : 0.0f;
                  },
                  a);
-    __syncthreads();
+    if (ch > 0) __syncthreads();
 #pragma unroll
     for (int m = 0; m < 3; ++m)
 #pragma unroll
       for (int o = 0; o < 4; ++o) V[m][4 * vq + o][vj] = a[m][o];
     __syncthreads();
-    if (!h_on) continue;
-    float b[3][4];
-    horizontal4<3>(taps, V, hr, 4 * hs, b);
-    const int orow = r0 + hr;
+    if (h_on) {
+      float b[3][4];
+      horizontal4<3>(taps, V, hr, 4 * hs, b);
+      const int orow = r0 + hr;
 #pragma unroll
-    for (int o = 0; o < 4; ++o) {
-      const int ocol = ox + 4 * hs + o;
-      if (4 * hs + o >= kSTW || ocol >= W || orow >= H) continue;
-      const int64_t p = ((int64_t)orow * W + ocol) * C + ch;
-      const float xv = x[p], yv = y[p], d = xv - yv;
-      const float sg = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f);
-      const float gs = b[0][o] + 2.0f * xv * b[1][o] + yv * b[2][o];
-      grad[p] = g_ss * gs + g_l1 * sg;
+      for (int o = 0; o < 4; ++o) {
+        const int tc = 4 * hs + o, ocol = ox + tc;
+        if (tc >= kSTW || ocol >= W || orow >= H) continue;
+        const int p = (orow * W + ocol) * CC + ch;
+        const float xv = x[p], yv = y[p], d = xv - yv;
+        const float sg = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f);
+        const float gs = b[0][o] + 2.0f * xv * b[1][o] + yv * b[2][o];
+        Go[hr][tc * CC + ch] = g_ss * gs + g_l1 * sg;
+      }
     }
+  }
+  __syncthreads();
+  // wave w writes rows w, w + 4, ...: a row is min(54, W - ox) * CC contiguous values
+  const int lane = tid & 63, wv = tid >> 6;
+  const int wcols = min(kSTW, W - ox) * CC;
+  for (int rr = wv; rr < kSTH; rr += 4) {
+    const int orow = r0 + rr;
+    if (orow >= H) break;
+    float* __restrict__ dst = grad + (orow * W + ox) * CC;
+    for (int cc = lane; cc < wcols; cc += 64) dst[cc] = Go[rr][cc];
   }
 }
 
@@ -273,6 +307,7 @@ Taps make_taps() {
 
 struct SsimLayout {
   int64_t count;
+  int TX, T;  // tiles per row, tiles
   dim3 grid;
   size_t gmap_off, part_off, total;
 };
@@ -280,10 +315,12 @@ struct SsimLayout {
 SsimLayout ssim_layout(int H, int W, int C) {
   SsimLayout L;
   L.count = (int64_t)H * W * C;
-  L.grid = dim3((unsigned)div_up(W, kSTW), (unsigned)div_up(H, kSTH));
+  L.TX = div_up(W, kSTW);
+  L.T = L.TX * div_up(H, kSTH);
+  L.grid = dim3((unsigned)(div_up(L.T, 8) * 8));
   L.gmap_off = 0;
   L.part_off = ((size_t)3 * L.count * sizeof(float) + 255) & ~(size_t)255;
-  L.total = L.part_off + (size_t)L.grid.x * L.grid.y * sizeof(float2);
+  L.total = L.part_off + (size_t)L.T * sizeof(float2);
   return L;
 }
 
@@ -293,27 +330,33 @@ SsimLayout ssim_layout(int H, int W, int C) {
 using namespace gs;
 
 extern "C" size_t gs_l1_ssim_workspace_size(int height, int width, int channels) {
-  if (height <= 0 || width <= 0 || channels <= 0) return 0;
+  if (height <= 0 || width <= 0 || channels <= 0 || channels > 4) return 0;
   return ssim_layout(height, width, channels).total;
 }
 
 extern "C" int gs_l1_ssim(void* stream, int height, int width, int channels, const float* pred,
                           const float* target, float* out, int with_grad, void* workspace, size_t workspace_bytes) {
-  GS_REQUIRE(height > 0 && width > 0 && channels > 0, "gs_l1_ssim: bad image shape %dx%dx%d", height, width,
-             channels);
+  GS_REQUIRE(height > 0 && width > 0 && channels > 0 && channels <= 4, "gs_l1_ssim: bad image shape %dx%dx%d",
+             height, width, channels);
   GS_REQUIRE(pred && target && out && workspace, "gs_l1_ssim: NULL argument");
-  GS_REQUIRE(height <= 65535 * kSTH, "gs_l1_ssim: height %d too large", height);
+  GS_REQUIRE(3 * (int64_t)height * width * channels < ((int64_t)1 << 31),
+             "gs_l1_ssim: image %dx%dx%d too large", height, width, channels);
   const SsimLayout L = ssim_layout(height, width, channels);
   GS_REQUIRE(workspace_bytes >= L.total, "gs_l1_ssim: workspace of %zu bytes, %zu needed", workspace_bytes, L.total);
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
   const float inv = (float)(1.0 / (double)L.count);
   float2* part = (float2*)(ws + L.part_off);
-  hipLaunchKernelGGL(l1_ssim_fwd_kernel, L.grid, dim3(256), 0, s, height, width, channels, pred, target, make_taps(),
-                     inv, with_grad ? (float*)(ws + L.gmap_off) : nullptr, part);
+  float* gmap = with_grad ? (float*)(ws + L.gmap_off) : nullptr;
+  const Taps taps = make_taps();
+  switch (channels) {
+    case 1: hipLaunchKernelGGL(l1_ssim_fwd_kernel<1>, L.grid, dim3(256), 0, s, height, width, L.TX, L.T, pred, target, taps, inv, gmap, part); break;
+    case 2: hipLaunchKernelGGL(l1_ssim_fwd_kernel<2>, L.grid, dim3(256), 0, s, height, width, L.TX, L.T, pred, target, taps, inv, gmap, part); break;
+    case 3: hipLaunchKernelGGL(l1_ssim_fwd_kernel<3>, L.grid, dim3(256), 0, s, height, width, L.TX, L.T, pred, target, taps, inv, gmap, part); break;
+    default: hipLaunchKernelGGL(l1_ssim_fwd_kernel<4>, L.grid, dim3(256), 0, s, height, width, L.TX, L.T, pred, target, taps, inv, gmap, part); break;
+  }
   GS_LAUNCH_CHECK("l1_ssim_fwd_kernel");
-  hipLaunchKernelGGL(l1_ssim_sum_kernel, dim3(1), dim3(1024), 0, s, (const float2*)part, (int)(L.grid.x * L.grid.y),
-                     inv, out);
+  hipLaunchKernelGGL(l1_ssim_sum_kernel, dim3(1), dim3(1024), 0, s, (const float2*)part, L.T, inv, out);
   GS_LAUNCH_CHECK("l1_ssim_sum_kernel");
   return GS_OK;
 }
@@ -321,17 +364,24 @@ extern "C" int gs_l1_ssim(void* stream, int height, int width, int channels, con
 extern "C" int gs_l1_ssim_bwd(void* stream, int height, int width, int channels, const float* pred,
                               const float* target, const float* grad_out, const void* workspace,
                               size_t workspace_bytes, float* grad_pred) {
-  GS_REQUIRE(height > 0 && width > 0 && channels > 0, "gs_l1_ssim_bwd: bad image shape %dx%dx%d", height, width,
-             channels);
+  GS_REQUIRE(height > 0 && width > 0 && channels > 0 && channels <= 4,
+             "gs_l1_ssim_bwd: bad image shape %dx%dx%d", height, width, channels);
   GS_REQUIRE(pred && target && grad_out && workspace && grad_pred, "gs_l1_ssim_bwd: NULL argument");
-  GS_REQUIRE(height <= 65535 * kSTH, "gs_l1_ssim_bwd: height %d too large", height);
+  GS_REQUIRE(3 * (int64_t)height * width * channels < ((int64_t)1 << 31),
+             "gs_l1_ssim_bwd: image %dx%dx%d too large", height, width, channels);
   const SsimLayout L = ssim_layout(height, width, channels);
   GS_REQUIRE(workspace_bytes >= L.total, "gs_l1_ssim_bwd: workspace of %zu bytes, %zu needed", workspace_bytes,
              L.total);
   hipStream_t s = (hipStream_t)stream;
   const float inv = (float)(1.0 / (double)L.count);
-  hipLaunchKernelGGL(l1_ssim_bwd_kernel, L.grid, dim3(256), 0, s, height, width, channels, pred, target, make_taps(),
-                     inv, (const float*)((const char*)workspace + L.gmap_off), grad_out, grad_pred);
+  const float* gmap = (const float*)((const char*)workspace + L.gmap_off);
+  const Taps taps = make_taps();
+  switch (channels) {
+    case 1: hipLaunchKernelGGL(l1_ssim_bwd_kernel<1>, L.grid, dim3(256), 0, s, height, width, L.TX, L.T, pred, target, taps, inv, gmap, grad_out, grad_pred); break;
+    case 2: hipLaunchKernelGGL(l1_ssim_bwd_kernel<2>, L.grid, dim3(256), 0, s, height, width, L.TX, L.T, pred, target, taps, inv, gmap, grad_out, grad_pred); break;
+    case 3: hipLaunchKernelGGL(l1_ssim_bwd_kernel<3>, L.grid, dim3(256), 0, s, height, width, L.TX, L.T, pred, target, taps, inv, gmap, grad_out, grad_pred); break;
+    default: hipLaunchKernelGGL(l1_ssim_bwd_kernel<4>, L.grid, dim3(256), 0, s, height, width, L.TX, L.T, pred, target, taps, inv, gmap, grad_out, grad_pred); break;
+  }
   GS_LAUNCH_CHECK("l1_ssim_bwd_kernel");
   return GS_OK;
 }
