@@ -137,9 +137,24 @@ def main():
             _lib.call("gs_l1_ssim_bwd", s_, Hc, Wc, Cc, _lib.ptr(image), _lib.ptr(tgt), _lib.ptr(gout), _lib.ptr(ws),
                       ws_bytes, _lib.ptr(gss))
             mark("s2")
+        # the trainer's optimizer step (train.py:127-155, trainer.py:44-53) on the gradients
+        # of the five arrays, with its moments
+        from jax_gs_amd.training.optimizer import make_optimizer
+
+        opt = make_optimizer(extent=3.0, num_iterations=30000)
+        params = type(g)(*[getattr(g, f).detach().clone() for f in fields])
+        grads = type(g)(*outs)
+        ostate = opt.init(params)
+        for _ in range(reps):
+            mark("a0")
+            opt.step(params, grads, ostate, mask)
+            mark("a1")
     torch.cuda.synchronize()
-    loss_ms = {nm: float(np.median([ev[a][r].elapsed_time(ev[z][r]) for r in range(reps)]))
-               for nm, a, z in (("l1_ssim_fwd", "s0", "s1"), ("l1_ssim_bwd", "s1", "s2"))}
+    extra_ms = {nm: float(np.median([ev[a][r].elapsed_time(ev[z][r]) for r in range(reps)]))
+                for nm, a, z in (("l1_ssim_fwd", "s0", "s1"), ("l1_ssim_bwd", "s1", "s2"), ("adam", "a0", "a1"))}
+    # Adam reads parameter, gradient and both moments (16 B) and writes three (12 B) per value
+    n_values = sum(getattr(g, f).numel() for f in fields)
+    extra_gbs = {"adam": 28 * n_values / (extra_ms["adam"] * 1e-3) / 1e9}
     names = ["preprocess_fwd", "binning", "composite_fwd", "l1_loss", "composite_bwd", "preprocess_bwd"]
     stage_ms = {}
     for i, nm in enumerate(names):
@@ -213,7 +228,8 @@ def main():
         "stage_ms": stage_ms,
         "stage_GBps": stage_gbs,
         "stage_TFLOPs": stage_tflops,
-        "loss_ms": loss_ms,
+        "extra_stage_ms": extra_ms,
+        "extra_stage_GBps": extra_gbs,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

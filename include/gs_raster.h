@@ -64,7 +64,7 @@ extern "C" {
 #define GS_NUM_STATS 16
 
 const char* gs_last_error(void);
-/* 2: gs_composite_fwd/bwd take the tile order; losses gs_mse_loss, gs_l1_ssim. */
+/* 2: gs_composite_fwd/bwd take the tile order; gs_mse_loss, gs_l1_ssim, gs_adam_step. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -180,6 +180,19 @@ int gs_l1_ssim(void* stream, int height, int width, int channels, const float* p
 int gs_l1_ssim_bwd(void* stream, int height, int width, int channels, const float* pred,
                    const float* target, const float* grad_out, const void* workspace,
                    size_t workspace_bytes, float* grad_pred);
+
+/* One Adam step, in place, of num_arrays (<= 8) float32 parameter arrays, each with
+ * its gradient and first/second moments (same sizes), counts[i] elements laid out as
+ * rows x row_lens[i] (row_lens[i] <= 64).  Replaces optax.adam (b1, b2, eps, eps_root 0)
+ * in the optax.multi_transform of train.py:127-155, the trainer's row mask
+ * (trainer.py:44-53: rows with active[row] == 0 get no update; active may be NULL) and
+ * optax.apply_updates.  step = the optimizer's count after this update (>= 1); lrs[i]
+ * is array i's learning rate at the count before it (schedules are evaluated by the
+ * caller).  All pointer arrays are host arrays of device pointers. */
+int gs_adam_step(void* stream, int num_arrays, float* const* params, const float* const* grads,
+                 float* const* mus, float* const* nus, const int64_t* counts, const int* row_lens,
+                 const double* lrs, const uint8_t* active, int64_t rows, int step, double b1,
+                 double b2, double eps);
 
 /* Densification statistics of one training step, updated in place.
  * Replaces jax_gs/training/trainer.py:278-294 (train_step, after value_and_grad):

@@ -359,3 +359,35 @@ def d_ssim_vjp(pred, target, g, dtype=np.float64):
     """Cotangent of pred for d_ssim_loss = max(0, (1 - ssim) / 2) with cotangent g."""
     s = ssim(pred, target, dtype)
     return ssim_vjp(pred, target, -0.5 * g * float(_tie_grad(np.float64((1.0 - s) / 2.0))), dtype)
+
+
+# ---------------------------------------------------------------------------------------
+# Optimizer (train.py:127-155 optax.multi_transform of optax.adam; trainer.py:44-53
+# _mask_updates; optax.apply_updates), restated operation by operation in float32.
+def exponential_decay(init_value, transition_steps, decay_rate):
+    """optax.exponential_decay (transition_begin 0, no staircase): init * rate^(count/steps)."""
+    def schedule(count):
+        if count <= 0:
+            return np.float32(init_value)
+        p = np.float32(count) / np.float32(transition_steps)
+        return np.float32(np.float32(init_value) * np.power(np.float32(decay_rate), p))
+    return schedule
+
+
+def adam_step(param, grad, mu, nu, count, lr, active=None, b1=0.9, b2=0.999, eps=1e-8):
+    """One optax.adam update of one parameter array followed by the trainer's row mask
+    and optax.apply_updates.  count is the optimizer's step count before this update
+    (the learning-rate schedule is evaluated at it); returns (param, mu, nu) new."""
+    f = np.float32
+    g = grad.astype(f)
+    mu = (f(1.0 - b1) * g + f(b1) * mu).astype(f)                  # update_moment
+    nu = (f(1.0 - b2) * (g * g) + f(b2) * nu).astype(f)            # update_moment_per_elem_norm
+    t = count + 1
+    bc1 = f(1.0) - np.power(f(b1), f(t))                            # bias_correction
+    bc2 = f(1.0) - np.power(f(b2), f(t))
+    u = (mu / bc1) / (np.sqrt(nu / bc2) + f(eps))                   # eps_root = 0
+    u = u * f(-lr)                                                  # scale_by_learning_rate
+    if active is not None:                                          # _mask_updates
+        m = np.asarray(active, bool).reshape((-1,) + (1,) * (param.ndim - 1))
+        u = np.where(m, u, f(0.0))
+    return (param + u).astype(f), mu, nu

@@ -527,3 +527,44 @@ def test_mse_closed_form():
     loss, seed = oracle.mse_loss_and_grad(pred, target)
     assert np.isclose(loss, 0.00666667, atol=1e-7)
     np.testing.assert_allclose(seed, 2 * (pred - target) / 3, rtol=1e-6)
+
+
+# ---------------------------------------------------------------------------------------
+# Optimizer restatement (optax.adam, trainer.py:44-53 mask)
+def test_adam_first_step_and_constant_gradient_closed_forms():
+    """With zero moments, or after t steps of one constant gradient g, the bias-corrected
+    moments are g and g^2, so every update is -lr g / (|g| + eps)."""
+    rng = np.random.default_rng(0)
+    g = rng.normal(size=(50, 3)).astype(np.float32)
+    p = rng.normal(size=(50, 3)).astype(np.float32)
+    mu = np.zeros_like(p)
+    nu = np.zeros_like(p)
+    lr = 0.005
+    want = -lr * g.astype(np.float64) / (np.abs(g.astype(np.float64)) + 1e-8)
+    q = p.copy()
+    for t in range(5):
+        q_new, mu, nu = oracle.adam_step(q, g, mu, nu, t, lr)
+        np.testing.assert_allclose(q_new.astype(np.float64) - q, want, rtol=2e-3, atol=1e-9)
+        q = q_new
+    np.testing.assert_allclose(mu, g * (1 - 0.9 ** 5), rtol=1e-5)
+    np.testing.assert_allclose(nu, g * g * (1 - 0.999 ** 5), rtol=1e-4)
+
+
+def test_adam_mask_keeps_inactive_rows_but_moves_their_moments():
+    rng = np.random.default_rng(1)
+    p = rng.normal(size=(8, 4)).astype(np.float32)
+    g = rng.normal(size=(8, 4)).astype(np.float32)
+    active = np.array([1, 0, 1, 1, 0, 0, 1, 0], bool)
+    q, mu, nu = oracle.adam_step(p, g, np.zeros_like(p), np.zeros_like(p), 0, 0.001, active)
+    np.testing.assert_array_equal(q[~active], p[~active])
+    assert np.all(q[active] != p[active])
+    np.testing.assert_allclose(mu, 0.1 * g, rtol=1e-6)
+
+
+def test_exponential_decay_schedule():
+    """train.py:127-135: lr(0) = init, lr(T) = end, lr(T/2) = sqrt(init * end)."""
+    init, end, T = 0.00016 * 3.0 * 2.5, 0.0000016 * 3.0 * 2.5, 30000
+    s = oracle.exponential_decay(init, T, end / init)
+    assert s(0) == np.float32(init)
+    assert np.isclose(s(T), end, rtol=1e-5)
+    assert np.isclose(s(T // 2), np.sqrt(init * end), rtol=1e-5)
