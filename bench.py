@@ -149,9 +149,28 @@ def main():
             mark("a0")
             opt.step(params, grads, ostate, mask)
             mark("a1")
+        # density control (density.py:98-211) on the frame's Gaussians padded to 1.5x, with
+        # the optimizer moments moving along; statistics from this frame's 2-D gradients
+        from jax_gs_amd.training import density
+
+        dstate = density.init_density_state(type(g)(*[getattr(g, f).detach() for f in fields]), opt,
+                                             N + N // 2)
+        dgen = torch.Generator(device=dev)
+        dgen.manual_seed(0)
+        base_accum = torch.rand((N + N // 2,), device=dev, generator=dgen) * 0.00025
+        for _ in range(reps):
+            dstate.grad_accum.copy_(base_accum)
+            dstate.denom.fill_(1)
+            dstate.active_mask[:N] = 1
+            dstate.active_mask[N:] = 0
+            mark("d0")
+            density.densify_and_prune(dstate, dgen, extent=3.0)
+            mark("d1")
     torch.cuda.synchronize()
     extra_ms = {nm: float(np.median([ev[a][r].elapsed_time(ev[z][r]) for r in range(reps)]))
-                for nm, a, z in (("l1_ssim_fwd", "s0", "s1"), ("l1_ssim_bwd", "s1", "s2"), ("adam", "a0", "a1"))}
+                for nm, a, z in (("l1_ssim_fwd", "s0", "s1"), ("l1_ssim_bwd", "s1", "s2"), ("adam", "a0", "a1"),
+                                 ("densify_and_prune", "d0", "d1"))}
+    extra_counts = {"densify_and_prune": [int(v) for v in dstate.last_counts.tolist()]}
     # Adam reads parameter, gradient and both moments (16 B) and writes three (12 B) per value
     n_values = sum(getattr(g, f).numel() for f in fields)
     extra_gbs = {"adam": 28 * n_values / (extra_ms["adam"] * 1e-3) / 1e9}
@@ -230,6 +249,7 @@ def main():
         "stage_TFLOPs": stage_tflops,
         "extra_stage_ms": extra_ms,
         "extra_stage_GBps": extra_gbs,
+        "extra_counts": extra_counts,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

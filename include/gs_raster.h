@@ -64,7 +64,8 @@ extern "C" {
 #define GS_NUM_STATS 16
 
 const char* gs_last_error(void);
-/* 2: gs_composite_fwd/bwd take the tile order; gs_mse_loss, gs_l1_ssim, gs_adam_step. */
+/* 2: gs_composite_fwd/bwd take the tile order; gs_mse_loss, gs_l1_ssim, gs_adam_step,
+ * gs_densify_and_prune, gs_reset_opacities. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -193,6 +194,35 @@ int gs_adam_step(void* stream, int num_arrays, float* const* params, const float
                  float* const* mus, float* const* nus, const int64_t* counts, const int* row_lens,
                  const double* lrs, const uint8_t* active, int64_t rows, int step, double b1,
                  double b2, double eps);
+
+/* Workspace bytes of gs_densify_and_prune for a capacity of M Gaussians. */
+size_t gs_densify_workspace_size(int64_t capacity);
+
+/* Densify and prune the static-capacity arrays in place.  Replaces
+ * jax_gs/training/density.py:98-211 (densify_and_prune) with :63-67
+ * (_reset_accumulators): prunes active Gaussians with sigmoid(opacity) < min_opacity,
+ * max exp(scale) > 0.1 extent or max_radii > max_screen_size; clones (max exp(scale)
+ * <= 0.01 extent) or splits the remaining ones whose grad_accum / denom >=
+ * grad_threshold into the empty slots (in index order; nothing is added when
+ * densify_enabled is 0 or the new ones do not fit), splits taking scale - log(1.6) and
+ * mean + noise * exp(new scale) on both copies; updates active, clears grad_accum and
+ * denom.  The num_moments (0, 5 or 10) arrays of moments (host array of device
+ * pointers, in the order means, scales, quaternions, opacities, sh_coeffs, repeated)
+ * move with their Gaussians.  noise[M,3] holds standard normal draws (the reference's
+ * jax.random.normal).  counts (may be NULL; device int32[5]) receives clones, splits,
+ * pruned, available slots, densified (0/1). */
+int gs_densify_and_prune(void* stream, int64_t capacity, int sh_k, float* means, float* scales,
+                         float* quats, float* opacities, float* sh_coeffs, int num_moments,
+                         float* const* moments, uint8_t* active, float* grad_accum, int32_t* denom,
+                         const float* max_radii, const float* noise, int densify_enabled,
+                         double grad_threshold, double min_opacity, double extent,
+                         double max_screen_size, void* workspace, size_t workspace_bytes,
+                         int32_t* counts);
+
+/* opacities[i] = log(reset_value / (1 - reset_value)) where active[i] (in place).
+ * Replaces jax_gs/training/density.py:69-93 (reset_opacities). */
+int gs_reset_opacities(void* stream, int64_t capacity, const uint8_t* active, double reset_value,
+                       float* opacities);
 
 /* Densification statistics of one training step, updated in place.
  * Replaces jax_gs/training/trainer.py:278-294 (train_step, after value_and_grad):

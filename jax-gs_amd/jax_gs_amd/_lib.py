@@ -45,11 +45,16 @@ _SIGS = {
     "gs_l1_ssim_workspace_size": [_I, _I, _I],
     "gs_l1_ssim": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _SZ],
     "gs_l1_ssim_bwd": [_P, _I, _I, _I, _P, _P, _P, _P, _SZ, _P],
+    "gs_densify_workspace_size": [_I64],
+    "gs_densify_and_prune": [_P, _I64, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, ctypes.c_double,
+                             ctypes.c_double, ctypes.c_double, ctypes.c_double, _P, _SZ, _P],
+    "gs_reset_opacities": [_P, _I64, _P, ctypes.c_double, _P],
     "gs_adam_step": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, ctypes.c_double, ctypes.c_double,
                      ctypes.c_double],
     "gs_densify_accumulate": [_P, _I64, _P, _P, _P, _F, _F, _P, _P, _P, _P, _P, _P],
 }
-_RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_l1_ssim_workspace_size": _SZ}
+_RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_l1_ssim_workspace_size": _SZ,
+            "gs_densify_workspace_size": _SZ}
 
 _lib = None
 

@@ -391,3 +391,71 @@ def adam_step(param, grad, mu, nu, count, lr, active=None, b1=0.9, b2=0.999, eps
         m = np.asarray(active, bool).reshape((-1,) + (1,) * (param.ndim - 1))
         u = np.where(m, u, f(0.0))
     return (param + u).astype(f), mu, nu
+
+
+def expf_array(a):
+    """gso_expf elementwise (float32)."""
+    a = np.ascontiguousarray(a, np.float32)
+    out = np.empty_like(a)
+    lib().gso_expf_array(ctypes.c_int64(a.size), _p(a), _p(out))
+    return out
+
+
+# ---------------------------------------------------------------------------------------
+# Densification (density.py:98-211 densify_and_prune, :63-67 _reset_accumulators)
+def densify_and_prune(state, noise, densify_enabled=True, grad_threshold=0.0002, min_opacity=0.005, extent=5.0,
+                      max_screen_size=512):
+    """Restates densify_and_prune on NumPy copies.  state: dict with the five parameter
+    arrays (means, scales, quaternions, opacities, sh_coeffs), 'moments' (dict of extra
+    arrays with the capacity as leading dimension, gathered like the parameters), 'active'
+    (bool [M]), 'grad_accum', 'denom', 'max_radii'.  noise: [M, 3] standard normal draws
+    (the reference draws them with jax.random.normal).  Returns the new state and a dict
+    of counts."""
+    f = np.float32
+    M = state["active"].shape[0]
+    active = state["active"].astype(bool)
+    sig = f(1.0) / (f(1.0) + expf_array(-state["opacities"][:, 0]))
+    prune = sig < f(min_opacity)
+    max_scales = expf_array(state["scales"]).max(axis=-1)
+    prune |= max_scales > f(0.1 * extent)
+    prune |= state["max_radii"] > f(max_screen_size)
+    prune &= active
+    after = active & ~prune
+    denom = state["denom"]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        avg = np.where(denom > 0, state["grad_accum"] / denom.astype(f), f(0.0)).astype(f)
+    densify = (avg >= f(grad_threshold)) & after
+    split = densify & (max_scales > f(0.01 * extent))
+    clone = densify & ~split
+    empty = ~after
+    can = bool(clone.sum() + split.sum() <= empty.sum()) and bool(densify_enabled)
+    if not can:
+        clone[:] = False
+        split[:] = False
+    nc, ns = int(clone.sum()), int(split.sum())
+    # stable argsorts of (not empty), (not clone), (not split): the k-th empty slot takes the
+    # k-th clone source, then the (k - nc)-th split source
+    empty_idx = np.argsort((~empty).astype(np.int8), kind="stable")
+    clone_src = np.argsort((~clone).astype(np.int8), kind="stable")
+    split_src = np.argsort((~split).astype(np.int8), kind="stable")
+    gather = np.arange(M)
+    is_split_dest = np.zeros(M, bool)
+    for k in range(nc + ns):
+        dst = empty_idx[k]
+        gather[dst] = clone_src[k] if k < nc else split_src[k - nc]
+        is_split_dest[dst] = k >= nc
+    out = {}
+    for key in ("means", "scales", "quaternions", "opacities", "sh_coeffs"):
+        out[key] = state[key][gather].copy()
+    out["moments"] = {k: v[gather].copy() for k, v in state.get("moments", {}).items()}
+    do_split = split | is_split_dest
+    out["scales"] = np.where(do_split[:, None], out["scales"] - f(np.log(1.6)), out["scales"]).astype(f)
+    jitter = (noise.astype(f) * expf_array(out["scales"])).astype(f)
+    out["means"] = np.where(do_split[:, None], out["means"] + jitter, out["means"]).astype(f)
+    added = np.zeros(M, bool)
+    added[empty_idx[:nc + ns]] = True
+    out["active"] = after | added
+    out["grad_accum"] = np.zeros_like(state["grad_accum"])
+    out["denom"] = np.zeros_like(state["denom"])
+    out["max_radii"] = state["max_radii"].copy()
+    return out, dict(clones=nc, splits=ns, pruned=int(prune.sum()), available=int(empty.sum()), gather=gather)

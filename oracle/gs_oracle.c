@@ -56,6 +56,11 @@ float gso_expf(float x) {
   return p * s.f;
 }
 
+/* gso_expf over an array (vectorised callers in the NumPy layer). */
+void gso_expf_array(int64_t n, const float* x, float* y) {
+  for (int64_t i = 0; i < n; ++i) y[i] = gso_expf(x[i]);
+}
+
 static float gso_sigmoidf(float x) { return 1.0f / (1.0f + gso_expf(-x)); }
 static double gso_sigmoid(double x) { return 1.0 / (1.0 + exp(-x)); }
 

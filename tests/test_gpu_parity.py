@@ -337,7 +337,7 @@ def test_ssim_identical_images_and_losses_module(cuda):
     total.backward()
     want_l1, seed = oracle.l1_loss_and_grad(p_np, t_np)
     want_total = 0.8 * want_l1 + 0.2 * oracle.d_ssim_loss(p_np, t_np)
-    assert abs(float(total) - want_total) <= 1e-6
+    assert abs(float(total.detach()) - want_total) <= 1e-6
     want_g = 0.8 * seed.astype(np.float64) + 0.2 * oracle.d_ssim_vjp(p_np, t_np, 1.0)
     assert _rel(_np(p.grad), want_g) <= 1e-4
 
@@ -388,3 +388,50 @@ def test_adam_step_parity(cuda):
         np.testing.assert_array_equal(got[~active], p_np[f][~active])
         np.testing.assert_allclose(_np(state.mu[f]), mu[f], rtol=1e-6, atol=1e-30)
         np.testing.assert_allclose(_np(state.nu[f]), nu[f], rtol=1e-6, atol=1e-30)
+
+
+@pytest.mark.parametrize("enabled", [True, False])
+def test_densify_and_prune_parity(cuda, enabled):
+    """density.py:98-211 with the optimizer moments moving along: every array, the mask,
+    the cleared statistics and the counts bit-identical to the oracle (same noise)."""
+    from jax_gs_amd.core.gaussians import Gaussians
+    from jax_gs_amd.training import density
+    from jax_gs_amd.training.optimizer import FIELDS, AdamState
+
+    rng = np.random.default_rng(21)
+    M, K = 6007, 16
+    f = np.float32
+    s = {"means": rng.normal(size=(M, 3)).astype(f), "scales": np.log(rng.uniform(0.002, 0.08, (M, 3))).astype(f),
+         "quaternions": rng.normal(size=(M, 4)).astype(f), "opacities": rng.normal(0, 3, (M, 1)).astype(f),
+         "sh_coeffs": rng.normal(size=(M, K, 3)).astype(f), "active": rng.uniform(size=M) < 0.7,
+         "grad_accum": rng.uniform(0, 0.0004, M).astype(f), "denom": rng.integers(0, 5, M).astype(np.int32),
+         "max_radii": rng.uniform(0, 600, M).astype(f)}
+    s["moments"] = {f"{k}_{fl}": rng.normal(size=s[fl].shape).astype(f) for k in ("mu", "nu") for fl in FIELDS}
+    noise = rng.normal(size=(M, 3)).astype(f)
+    want, c = oracle.densify_and_prune(s, noise, densify_enabled=enabled, extent=5.0)
+    if enabled:
+        assert c["clones"] > 0 and c["splits"] > 0
+
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    st = density.DensityState(
+        gaussians=Gaussians(*[T(s[fl]) for fl in FIELDS]),
+        opt_state=AdamState(mu={fl: T(s["moments"][f"mu_{fl}"]) for fl in FIELDS},
+                            nu={fl: T(s["moments"][f"nu_{fl}"]) for fl in FIELDS}, count=3),
+        active_mask=T(s["active"].astype(np.uint8)), num_active=int(s["active"].sum()),
+        grad_accum=T(s["grad_accum"]), denom=T(s["denom"]), max_radii=T(s["max_radii"]))
+    density.densify_and_prune(st, densify_enabled=enabled, extent=5.0, noise=T(noise))
+    got_counts = _np(st.last_counts)
+    assert list(got_counts) == [c["clones"], c["splits"], c["pruned"], c["available"], int(enabled)]
+    for fl in FIELDS:
+        np.testing.assert_array_equal(_np(getattr(st.gaussians, fl)), want[fl], err_msg=fl)
+        np.testing.assert_array_equal(_np(st.opt_state.mu[fl]), want["moments"][f"mu_{fl}"], err_msg=fl)
+        np.testing.assert_array_equal(_np(st.opt_state.nu[fl]), want["moments"][f"nu_{fl}"], err_msg=fl)
+    np.testing.assert_array_equal(_np(st.active_mask).astype(bool), want["active"])
+    assert not _np(st.grad_accum).any() and not _np(st.denom).any()
+    np.testing.assert_array_equal(_np(st.max_radii), s["max_radii"])
+    # reset_opacities (density.py:69-93) on the new mask
+    density.reset_opacities(st, 0.01)
+    op = _np(st.gaussians.opacities)[:, 0]
+    a = want["active"]
+    np.testing.assert_array_equal(op[a], np.full(a.sum(), np.float32(np.log(0.01 / 0.99)), np.float32))
+    np.testing.assert_array_equal(op[~a], want["opacities"][~a, 0])

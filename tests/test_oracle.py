@@ -568,3 +568,84 @@ def test_exponential_decay_schedule():
     assert s(0) == np.float32(init)
     assert np.isclose(s(T), end, rtol=1e-5)
     assert np.isclose(s(T // 2), np.sqrt(init * end), rtol=1e-5)
+
+
+# ---------------------------------------------------------------------------------------
+# densify_and_prune restatement (density.py:98-211)
+def _den_state(M, K=1):
+    f = np.float32
+    return {"means": np.zeros((M, 3), f), "scales": np.full((M, 3), np.log(0.02), f),
+            "quaternions": np.tile(np.array([1, 0, 0, 0], f), (M, 1)), "opacities": np.zeros((M, 1), f),
+            "sh_coeffs": np.zeros((M, K, 3), f), "active": np.zeros(M, bool), "grad_accum": np.zeros(M, f),
+            "denom": np.zeros(M, np.int32), "max_radii": np.zeros(M, f), "moments": {}}
+
+
+def test_densify_hand_built_case():
+    """Slots 0-3 active, 4-7 empty; 1 is transparent (pruned), 2 has a high average
+    gradient and a small scale (cloned), 3 a high gradient and a scale above 1% of the
+    extent (split).  Empty slots after pruning are 1, 4, 5, 6, 7: slot 1 takes the
+    clone of 2, slot 4 the split copy of 3."""
+    s = _den_state(8)
+    s["active"][:4] = True
+    s["means"][:] = np.arange(24, dtype=np.float32).reshape(8, 3)
+    s["opacities"][1, 0] = -10.0
+    s["grad_accum"][2], s["denom"][2] = 0.001, 2        # avg 5e-4 >= 2e-4
+    s["grad_accum"][3], s["denom"][3] = 0.003, 3        # avg 1e-3
+    s["scales"][3] = np.log(0.2)                        # 0.05 < 0.2 < 0.5 (extent 5)
+    s["sh_coeffs"][:, 0, 0] = np.arange(8)
+    s["moments"] = {"mu": np.arange(8, dtype=np.float32)[:, None] * np.ones((1, 3), np.float32)}
+    noise = np.random.default_rng(0).normal(size=(8, 3)).astype(np.float32)
+    out, c = oracle.densify_and_prune(s, noise, extent=5.0)
+    assert (c["clones"], c["splits"], c["pruned"], c["available"]) == (1, 1, 1, 5)
+    assert list(np.flatnonzero(out["active"])) == [0, 1, 2, 3, 4]
+    assert list(c["gather"]) == [0, 2, 2, 3, 3, 5, 6, 7]
+    np.testing.assert_array_equal(out["means"][1], s["means"][2])
+    assert out["sh_coeffs"][1, 0, 0] == 2 and out["sh_coeffs"][4, 0, 0] == 3
+    np.testing.assert_array_equal(out["moments"]["mu"][[1, 4], 0], [2, 3])
+    s_new = np.float32(np.float32(np.log(0.2)) - np.float32(np.log(1.6)))
+    for slot in (3, 4):
+        np.testing.assert_array_equal(out["scales"][slot], np.full(3, s_new, np.float32))
+        want = s["means"][3] + noise[slot] * oracle.expf_array(np.full(3, s_new, np.float32))
+        np.testing.assert_allclose(out["means"][slot], want, rtol=1e-6)
+    assert not out["grad_accum"].any() and not out["denom"].any()
+
+
+def test_densify_capacity_and_switch():
+    """Nothing is added when the new Gaussians do not fit or densify_enabled is False;
+    pruning (opacity, world size, screen size) still applies."""
+    s = _den_state(6)
+    s["active"][:] = True
+    s["grad_accum"][:3], s["denom"][:3] = 0.01, 1        # three clone candidates, no room
+    s["max_radii"][5] = 600.0                           # pruned by screen size
+    s["scales"][4] = np.log(0.6)                        # pruned by world size (> 0.5)
+    out, c = oracle.densify_and_prune(s, np.zeros((6, 3), np.float32), extent=5.0)
+    assert (c["clones"], c["splits"], c["pruned"], c["available"]) == (0, 0, 2, 2)
+    assert list(np.flatnonzero(out["active"])) == [0, 1, 2, 3]
+    s["max_radii"][5] = 0.0
+    s["scales"][4] = np.log(0.02)
+    s["active"][4:] = False
+    out, c = oracle.densify_and_prune(s, np.zeros((6, 3), np.float32), densify_enabled=False, extent=5.0)
+    assert (c["clones"], c["splits"]) == (0, 0) and list(np.flatnonzero(out["active"])) == [0, 1, 2, 3]
+
+
+def test_densify_random_invariants():
+    rng = np.random.default_rng(5)
+    M = 500
+    s = _den_state(M, K=4)
+    s["active"] = rng.uniform(size=M) < 0.6
+    s["opacities"][:, 0] = rng.normal(0, 3, M)
+    s["scales"][:] = np.log(rng.uniform(0.005, 0.3, (M, 3)))
+    s["grad_accum"][:] = rng.uniform(0, 0.002, M)
+    s["denom"][:] = rng.integers(0, 5, M)
+    s["means"][:] = rng.normal(size=(M, 3))
+    s["sh_coeffs"][:] = rng.normal(size=(M, 4, 3))
+    noise = rng.normal(size=(M, 3)).astype(np.float32)
+    out, c = oracle.densify_and_prune(s, noise, extent=5.0)
+    added = c["clones"] + c["splits"]
+    assert added > 0
+    after = int(s["active"].sum()) - c["pruned"]
+    assert int(out["active"].sum()) == after + added
+    moved = np.flatnonzero(c["gather"] != np.arange(M))
+    assert len(moved) == added and not s["active"][moved].all()
+    for slot in moved:   # copies carry their source's SH and quaternion exactly
+        np.testing.assert_array_equal(out["sh_coeffs"][slot], s["sh_coeffs"][c["gather"][slot]])
