@@ -166,14 +166,27 @@ def main():
             mark("d0")
             density.densify_and_prune(dstate, dgen, extent=3.0)
             mark("d1")
+        # PLY checkpoint records (ply.py:6-66) packed on the device: 236 B read, 248 B
+        # written per Gaussian with degree-3 SH
+        if g.sh_coeffs.shape[1] == 16:
+            recs = torch.empty((N, 62), device=dev)
+            for _ in range(reps):
+                mark("p0")
+                _lib.call("gs_ply_pack", s_, N, 16, *[_lib.ptr(getattr(g, f).detach()) for f in fields],
+                          _lib.ptr(recs))
+                mark("p1")
     torch.cuda.synchronize()
     extra_ms = {nm: float(np.median([ev[a][r].elapsed_time(ev[z][r]) for r in range(reps)]))
                 for nm, a, z in (("l1_ssim_fwd", "s0", "s1"), ("l1_ssim_bwd", "s1", "s2"), ("adam", "a0", "a1"),
                                  ("densify_and_prune", "d0", "d1"))}
+    if "p0" in ev:
+        extra_ms["ply_pack"] = float(np.median([ev["p0"][r].elapsed_time(ev["p1"][r]) for r in range(reps)]))
     extra_counts = {"densify_and_prune": [int(v) for v in dstate.last_counts.tolist()]}
     # Adam reads parameter, gradient and both moments (16 B) and writes three (12 B) per value
     n_values = sum(getattr(g, f).numel() for f in fields)
     extra_gbs = {"adam": 28 * n_values / (extra_ms["adam"] * 1e-3) / 1e9}
+    if "ply_pack" in extra_ms:
+        extra_gbs["ply_pack"] = (236 + 248) * N / (extra_ms["ply_pack"] * 1e-3) / 1e9
     names = ["preprocess_fwd", "binning", "composite_fwd", "l1_loss", "composite_bwd", "preprocess_bwd"]
     stage_ms = {}
     for i, nm in enumerate(names):

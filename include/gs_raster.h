@@ -65,7 +65,7 @@ extern "C" {
 
 const char* gs_last_error(void);
 /* 2: gs_composite_fwd/bwd take the tile order; gs_mse_loss, gs_l1_ssim, gs_adam_step,
- * gs_densify_and_prune, gs_reset_opacities. */
+ * gs_densify_and_prune, gs_reset_opacities, gs_ply_pack/unpack. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -223,6 +223,15 @@ int gs_densify_and_prune(void* stream, int64_t capacity, int sh_k, float* means,
  * Replaces jax_gs/training/density.py:69-93 (reset_opacities). */
 int gs_reset_opacities(void* stream, int64_t capacity, const uint8_t* active, double reset_value,
                        float* opacities);
+
+/* PLY vertex records [N, 62] float32 (x y z, nx ny nz = 0, f_dc_0..2, f_rest_0..44 with
+ * f_rest_i = sh[1 + i/3][i%3], opacity, scale_0..2, rot_0..3) from the five arrays, and
+ * back (normals ignored).  sh_k must be 16.  Replaces the record assembly of
+ * jax_gs/io/ply.py:6-123 (save_ply / load_ply); the host writes the header. */
+int gs_ply_pack(void* stream, int64_t n, int sh_k, const float* means, const float* scales,
+                const float* quats, const float* opacities, const float* sh_coeffs, float* records);
+int gs_ply_unpack(void* stream, int64_t n, int sh_k, const float* records, float* means,
+                  float* scales, float* quats, float* opacities, float* sh_coeffs);
 
 /* Densification statistics of one training step, updated in place.
  * Replaces jax_gs/training/trainer.py:278-294 (train_step, after value_and_grad):

@@ -49,6 +49,8 @@ _SIGS = {
     "gs_densify_and_prune": [_P, _I64, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, ctypes.c_double,
                              ctypes.c_double, ctypes.c_double, ctypes.c_double, _P, _SZ, _P],
     "gs_reset_opacities": [_P, _I64, _P, ctypes.c_double, _P],
+    "gs_ply_pack": [_P, _I64, _I, _P, _P, _P, _P, _P, _P],
+    "gs_ply_unpack": [_P, _I64, _I, _P, _P, _P, _P, _P, _P],
     "gs_adam_step": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, ctypes.c_double, ctypes.c_double,
                      ctypes.c_double],
     "gs_densify_accumulate": [_P, _I64, _P, _P, _P, _F, _F, _P, _P, _P, _P, _P, _P],

@@ -459,3 +459,33 @@ def densify_and_prune(state, noise, densify_enabled=True, grad_threshold=0.0002,
     out["denom"] = np.zeros_like(state["denom"])
     out["max_radii"] = state["max_radii"].copy()
     return out, dict(clones=nc, splits=ns, pruned=int(prune.sum()), available=int(empty.sum()), gather=gather)
+
+
+# ---------------------------------------------------------------------------------------
+# PLY checkpoint bytes (ply.py:6-123), restated with the reference's structured dtype
+def ply_dtype():
+    names = (["x", "y", "z", "nx", "ny", "nz", "f_dc_0", "f_dc_1", "f_dc_2"] + [f"f_rest_{i}" for i in range(45)] +
+             ["opacity", "scale_0", "scale_1", "scale_2", "rot_0", "rot_1", "rot_2", "rot_3"])
+    return [(n, "<f4") for n in names]
+
+
+def ply_bytes(means, scales, quats, opacities, sh):
+    """The file save_ply writes for these arrays (sh [N, 16, 3])."""
+    dt = ply_dtype()
+    n = means.shape[0]
+    data = np.zeros(n, dtype=dt)
+    data["x"], data["y"], data["z"] = means[:, 0], means[:, 1], means[:, 2]
+    f_dc = sh[:, 0, :].reshape(-1, 3)
+    f_rest = sh[:, 1:, :].reshape(-1, 45)
+    for c in range(3):
+        data[f"f_dc_{c}"] = f_dc[:, c]
+    for i in range(45):
+        data[f"f_rest_{i}"] = f_rest[:, i]
+    data["opacity"] = opacities[:, 0]
+    for c in range(3):
+        data[f"scale_{c}"] = scales[:, c]
+    for c in range(4):
+        data[f"rot_{c}"] = quats[:, c]
+    head = b"ply\nformat binary_little_endian 1.0\n" + f"element vertex {n}\n".encode()
+    head += b"".join(f"property float {name}\n".encode() for name, _ in dt) + b"end_header\n"
+    return head + data.tobytes()

@@ -48,3 +48,13 @@ def test_argument_errors_are_reported_without_launching():
     rc = L.gs_bin(None, 10, None, None, None, None, 64, 64, 0, None, 0, None, None, None, None)
     assert rc == 1
     assert b"workspace" in L.gs_last_error()
+
+
+def test_load_ply_missing_file():
+    """test_io.py:42-44: a missing path raises FileNotFoundError (before any GPU work)."""
+    import pytest
+
+    from jax_gs_amd.io.ply import load_ply
+
+    with pytest.raises(FileNotFoundError):
+        load_ply("non_existent_file.ply")

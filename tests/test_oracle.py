@@ -649,3 +649,34 @@ def test_densify_random_invariants():
     assert len(moved) == added and not s["active"][moved].all()
     for slot in moved:   # copies carry their source's SH and quaternion exactly
         np.testing.assert_array_equal(out["sh_coeffs"][slot], s["sh_coeffs"][c["gather"][slot]])
+
+
+# ---------------------------------------------------------------------------------------
+# PLY bytes (ply.py:6-123)
+def test_ply_bytes_layout():
+    """Header lines and the byte offset of every property: value j of vertex v sits at
+    header + (62 v + j) * 4, little-endian float32, f_rest_i = sh[1 + i // 3][i % 3]."""
+    n = 3
+    v = np.arange(n, dtype=np.float32)[:, None]
+    means = 1000 * v + np.arange(3, dtype=np.float32)
+    sh = (1000 * v[:, :, None] + 100 + np.arange(48, dtype=np.float32).reshape(1, 16, 3)).astype(np.float32)
+    opac = 1000 * v + 200
+    scales = 1000 * v + 300 + np.arange(3, dtype=np.float32)
+    quats = 1000 * v + 400 + np.arange(4, dtype=np.float32)
+    b = oracle.ply_bytes(means, scales, quats, opac, sh)
+    head, body = b.split(b"end_header\n")
+    lines = head.decode().splitlines()
+    assert lines[:3] == ["ply", "format binary_little_endian 1.0", "element vertex 3"]
+    assert lines[3] == "property float x" and lines[9] == "property float f_dc_0"
+    assert lines[12] == "property float f_rest_0" and lines[56] == "property float f_rest_44"
+    assert lines[57:] == ["property float opacity"] + [f"property float scale_{c}" for c in range(3)] + \
+        [f"property float rot_{c}" for c in range(4)]
+    rec = np.frombuffer(body, dtype="<f4").reshape(n, 62)
+    for k in range(n):
+        assert list(rec[k, :3]) == [1000 * k + c for c in range(3)] and not rec[k, 3:6].any()
+        assert list(rec[k, 6:9]) == [1000 * k + 100 + c for c in range(3)]            # f_dc = sh[0]
+        for i in range(45):                                                           # f_rest_i
+            assert rec[k, 9 + i] == 1000 * k + 100 + 3 * (1 + i // 3) + i % 3
+        assert rec[k, 54] == 1000 * k + 200
+        assert list(rec[k, 55:58]) == [1000 * k + 300 + c for c in range(3)]
+        assert list(rec[k, 58:62]) == [1000 * k + 400 + c for c in range(4)]
