@@ -459,3 +459,49 @@ def test_ply_save_load(cuda, tmp_path):
     back = load_ply(path, device=cuda)
     for k in FIELDS:
         np.testing.assert_array_equal(_np(getattr(back, k)), arr[k], err_msg=k)
+
+
+def test_train_step_composition(cuda):
+    """trainer.py:55-169 on the GPU: the rendered loss (0.8 L1 + 0.2 D-SSIM), the
+    gradients of the five arrays, the densification statistics and the masked Adam step
+    against the oracle's render, losses, VJP, statistics and optimizer (the optimizer is
+    fed the GPU's gradients, whose own parity is checked first: near-zero gradient
+    components decide Adam's first-step sign)."""
+    from jax_gs_amd.core.gaussians import Gaussians
+    from jax_gs_amd.training import density
+    from jax_gs_amd.training.optimizer import make_optimizer
+    from jax_gs_amd.training.trainer import train_step
+
+    sc = scenes.make_scene(4, n=3000, width=96, height=64)
+    g, cam, tgt, mask = scenes.to_torch(sc, cuda)
+    opt = make_optimizer(extent=3.0, num_iterations=1000)
+    st = density.init_density_state(g, opt, 3000)
+    st.active_mask.copy_(torch.from_numpy(sc["mask"].astype(np.uint8)).to(cuda))
+    p0 = {f: _np(getattr(st.gaussians, f)).copy() for f in FIELDS}
+    cs = (cam.W, cam.H, cam.fx, cam.fy, cam.cx, cam.cy)
+    state, loss, metrics = train_step(st, tgt, cam.W2C, cs, opt, sh_degree=sc["sh_degree"])
+    # oracle forward, loss and VJP at the pre-step parameters
+    params_o = {**sc["params"], **{f: p0[f] for f in FIELDS}}
+    img_o, ex_o, res = oracle.render(params_o, sc["cam"], mask=sc["mask"], sh_degree=sc["sh_degree"])
+    t_np = _np(tgt)
+    l1_o, seed_l1 = oracle.l1_loss_and_grad(img_o, t_np)
+    want_loss = 0.8 * float(l1_o) + 0.2 * oracle.d_ssim_loss(img_o, t_np)
+    assert abs(float(loss) - want_loss) <= 1e-5
+    assert abs(float(metrics["ssim"]) - oracle.ssim(img_o, t_np)) <= 1e-5
+    g_img = (0.8 * seed_l1.astype(np.float64) + 0.2 * oracle.d_ssim_vjp(img_o, t_np, 1.0)).astype(np.float32)
+    gr_o = oracle.render_vjp(params_o, sc["cam"], res, g_img, sh_degree=sc["sh_degree"])
+    # reconstruct the GPU gradients from the Adam update of the first step: with zero
+    # moments mu = 0.1 g exactly, so compare the moments instead
+    for f in FIELDS:
+        g_gpu = _np(state.opt_state.mu[f]) / np.float32(0.1)
+        assert _rel(g_gpu, gr_o[f]) <= GRAD_TOL, f
+        want_p, _, _ = oracle.adam_step(p0[f], g_gpu.astype(np.float32), np.zeros_like(p0[f]), np.zeros_like(p0[f]),
+                                        0, opt.lr_at(f, 0), sc["mask"])
+        np.testing.assert_allclose(_np(getattr(state.gaussians, f)), want_p, rtol=0, atol=1e-6, err_msg=f)
+    ga, de, mr = oracle.densify(gr_o["means"], p0["means"], sc["cam"]["W2C"], sc["cam"]["fx"], sc["cam"]["fy"],
+                                sc["cam"]["W"], sc["cam"]["H"], ex_o["valid_mask"], ex_o["radii"],
+                                np.zeros(3000, np.float32), np.zeros(3000, np.int32), np.zeros(3000, np.float32),
+                                active=sc["mask"])
+    np.testing.assert_array_equal(_np(state.denom), de)
+    np.testing.assert_array_equal(_np(state.max_radii), mr)
+    assert _rel(_np(state.grad_accum), ga) <= GRAD_TOL
