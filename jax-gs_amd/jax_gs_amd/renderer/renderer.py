@@ -57,7 +57,8 @@ class _Render(torch.autograd.Function):
         s = _lib.stream_handle(dev)
         g_image = g_image.contiguous()
         grec = torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=dev)
-        gbg = torch.empty((3,), dtype=torch.float32, device=dev)
+        # dL/dbackground only when the background is differentiated (the trainer's is not)
+        gbg = torch.empty((3,), dtype=torch.float32, device=dev) if ctx.needs_input_grad[6] else None
         _lib.call("gs_composite_bwd", s, n, _lib.ptr(rec), _lib.ptr(gids), gids.shape[0], _lib.ptr(ranges), int(W), int(H),
                   _lib.ptr(bg), _lib.ptr(g_image), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec),
                   _lib.ptr(gbg))
