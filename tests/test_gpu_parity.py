@@ -505,3 +505,67 @@ def test_train_step_composition(cuda):
     np.testing.assert_array_equal(_np(state.denom), de)
     np.testing.assert_array_equal(_np(state.max_radii), mr)
     assert _rel(_np(state.grad_accum), ga) <= GRAD_TOL
+
+
+def _subscene(sc, idx):
+    """The Gaussians idx of scene sc (same camera)."""
+    out = dict(sc)
+    out["params"] = {k: np.ascontiguousarray(v[idx]) for k, v in sc["params"].items()}
+    out["mask"] = None if sc["mask"] is None else np.ascontiguousarray(sc["mask"][idx])
+    return out
+
+
+@pytest.mark.parametrize("case", ["empty", "one", "behind", "mixed_behind"])
+def test_degenerate_scenes(cuda, case):
+    """No Gaussians, a single one, all behind the camera (depth sign bit set: the
+    reference's tile -1 slots), and a scene with a quarter of them behind: image,
+    extras and gradients against the oracle."""
+    sc = scenes.make_scene(1, n=400, width=96, height=80)
+    n = 400
+    if case == "empty":
+        sc = _subscene(sc, np.arange(0))
+    elif case == "one":
+        sc = _subscene(sc, np.arange(1))
+        sc["params"]["means"][0] = [0.0, 0.0, 3.0]
+        sc["params"]["scales"][0] = np.log([0.05, 0.08, 0.05])
+    elif case == "behind":
+        sc["params"]["means"][:, 2] = -np.abs(sc["params"]["means"][:, 2])
+    else:
+        sc["params"]["means"][: n // 4, 2] = -np.abs(sc["params"]["means"][: n // 4, 2])
+    if sc["target"] is None:
+        sc["target"] = np.random.default_rng(1).uniform(0, 1, (80, 96, 3)).astype(np.float32)
+    image, extras, g, img_o, ex_o, gr_o = _render_both(sc, cuda)
+    assert np.abs(_np(image) - img_o).max() <= IMG_TOL
+    for k in ("n_interactions", "max_interactions_per_tile", "overflow_tiles", "truncated_tiles",
+              "radius_cap_violations"):
+        assert int(extras[k]) == int(ex_o[k]), k
+    np.testing.assert_array_equal(_np(extras["valid_mask"]), ex_o["valid_mask"])
+    for f in FIELDS:
+        got = _np(getattr(g, f).grad)
+        assert got.shape == gr_o[f].shape
+        if np.linalg.norm(gr_o[f]) == 0.0:
+            assert not got.any(), f
+        else:
+            assert _rel(got, gr_o[f]) <= GRAD_TOL, f
+
+
+def test_capacity_exceeded_is_flagged(cuda):
+    """An entry capacity below the scene's count: the binning flags it, keeps the first
+    `capacity` entries of the reference order, and compositing stays inside them."""
+    from jax_gs_amd import _lib
+
+    sc = scenes.make_scene(1, n=3000, width=160, height=120)
+    g, cam, _, _ = scenes.to_torch(sc, cuda)
+    with torch.no_grad():
+        pre = preprocess(g, cam, sh_degree=sc["sh_degree"])
+        full = rasterizer.bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], cam.H, cam.W)
+        n_int = int(full["n_interactions"])
+        cap = n_int // 2
+        part = rasterizer.bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], cam.H, cam.W,
+                                        capacity=cap)
+        st = _np(part["stats"])
+        assert st[_lib.STAT["capacity_exceeded"]] == 1 and st[_lib.STAT["n_interactions"]] == n_int
+        np.testing.assert_array_equal(_np(part["sorted_gids"])[:cap], _np(full["sorted_gids"])[:cap])
+        image, _, _, _ = rasterizer.composite(pre["records"], part["sorted_gids"], part["ranges"], cam.H, cam.W,
+                                              torch.zeros(3, device=cuda))
+        assert torch.isfinite(image).all()
