@@ -175,16 +175,44 @@ def main():
                 _lib.call("gs_ply_pack", s_, N, 16, *[_lib.ptr(getattr(g, f).detach()) for f in fields],
                           _lib.ptr(recs))
                 mark("p1")
+    # the reference's whole training step (trainer.py:55-169: render, 0.8 L1 + 0.2 D-SSIM,
+    # backward, densification statistics, masked Adam) on the same frame and Gaussians,
+    # timed beside the headline step (wall clock of `reps` steps between synchronisations)
+    from jax_gs_amd.training.trainer import train_step
+
+    tstate = density.init_density_state(type(g)(*[getattr(g, f).detach().clone() for f in fields]),
+                                        make_optimizer(extent=3.0, num_iterations=30000), N)
+    cs = (cam.W, cam.H, cam.fx, cam.fy, cam.cx, cam.cy)
+    for _ in range(2):
+        train_step(tstate, tgt, cam.W2C, cs, make_optimizer(extent=3.0, num_iterations=30000), sh_degree=D)
+    topt = make_optimizer(extent=3.0, num_iterations=30000)
     torch.cuda.synchronize()
+    t_ts = time.perf_counter()
+    for _ in range(reps):
+        train_step(tstate, tgt, cam.W2C, cs, topt, sh_degree=D)
+    torch.cuda.synchronize()
+    train_step_ms = (time.perf_counter() - t_ts) / reps * 1e3
     extra_ms = {nm: float(np.median([ev[a][r].elapsed_time(ev[z][r]) for r in range(reps)]))
                 for nm, a, z in (("l1_ssim_fwd", "s0", "s1"), ("l1_ssim_bwd", "s1", "s2"), ("adam", "a0", "a1"),
                                  ("densify_and_prune", "d0", "d1"))}
     if "p0" in ev:
         extra_ms["ply_pack"] = float(np.median([ev["p0"][r].elapsed_time(ev["p1"][r]) for r in range(reps)]))
+    extra_ms["train_step"] = train_step_ms
     extra_counts = {"densify_and_prune": [int(v) for v in dstate.last_counts.tolist()]}
     # Adam reads parameter, gradient and both moments (16 B) and writes three (12 B) per value
     n_values = sum(getattr(g, f).numel() for f in fields)
     extra_gbs = {"adam": 28 * n_values / (extra_ms["adam"] * 1e-3) / 1e9}
+    # L1 + SSIM: forward reads both images and writes 3 derivative maps (20 B per value),
+    # backward reads the maps and both images and writes the gradient (24 B per value)
+    n_img = image.numel()
+    extra_gbs["l1_ssim_fwd"] = 20 * n_img / (extra_ms["l1_ssim_fwd"] * 1e-3) / 1e9
+    extra_gbs["l1_ssim_bwd"] = 24 * n_img / (extra_ms["l1_ssim_bwd"] * 1e-3) / 1e9
+    # densify-and-prune: 29 B read per slot for the flags (scales, opacity, mask, statistics,
+    # radius) plus the filled slots' rows, read and written (4 B per value)
+    dc = extra_counts["densify_and_prune"]
+    row_vals = sum(getattr(g, f)[0].numel() for f in fields) * 3  # parameters and two moments
+    den_bytes = 29 * (N + N // 2) + 8 * row_vals * (dc[0] + dc[1])
+    extra_gbs["densify_and_prune"] = den_bytes / (extra_ms["densify_and_prune"] * 1e-3) / 1e9
     if "ply_pack" in extra_ms:
         extra_gbs["ply_pack"] = (236 + 248) * N / (extra_ms["ply_pack"] * 1e-3) / 1e9
     names = ["preprocess_fwd", "binning", "composite_fwd", "l1_loss", "composite_bwd", "preprocess_bwd"]

@@ -65,7 +65,8 @@ extern "C" {
 
 const char* gs_last_error(void);
 /* 2: gs_composite_fwd/bwd take the tile order; gs_mse_loss, gs_l1_ssim, gs_adam_step,
- * gs_densify_and_prune, gs_reset_opacities, gs_ply_pack/unpack. */
+ * gs_densify_and_prune, gs_reset_opacities, gs_ply_pack/unpack, gs_preprocess_bwd_adam,
+ * gs_l1_ssim_terms. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -151,6 +152,22 @@ int gs_preprocess_bwd(void* stream, int64_t n, int sh_k, int sh_degree, const fl
                       float* grad_means, float* grad_scales, float* grad_quats,
                       float* grad_opacities, float* grad_sh);
 
+/* The training step's tail in one pass: gs_preprocess_bwd's gradients, the
+ * densification statistics of gs_densify_accumulate (from the means before the update;
+ * skipped when grad_accum is NULL) and gs_adam_step's masked update of the five arrays,
+ * in place; no parameter gradient is written.  Replaces trainer.py:66-103 after the
+ * rasterizer's VJP, with optax.adam of train.py:127-155.  moments: host array of 10 device
+ * pointers (first moments of means, scales, quaternions, opacities, sh_coeffs, then the
+ * second moments), lrs[5] the learning rates, step the optimizer count after the update. */
+int gs_preprocess_bwd_adam(void* stream, int64_t n, int sh_k, int sh_degree, float* means,
+                           float* scales, float* quats, float* opacities, float* sh_coeffs,
+                           const float* w2c, int width, int height, float fx, float fy, float cx,
+                           float cy, const float* grad_records, float* const* moments,
+                           const double* lrs, int step, double b1, double b2, double eps,
+                           const uint8_t* active, const uint8_t* valid, const float* radii,
+                           float focal, float pixel_scale, float* grad_accum, int32_t* denom,
+                           float* max_radii);
+
 /* mean(|pred - target|) into loss[0] and, when grad is not NULL, its gradient
  * sign(pred - target) / count.  Replaces jax_gs/training/losses.py:4-8 (l1_loss)
  * and its autodiff seed. */
@@ -181,6 +198,13 @@ int gs_l1_ssim(void* stream, int height, int width, int channels, const float* p
 int gs_l1_ssim_bwd(void* stream, int height, int width, int channels, const float* pred,
                    const float* target, const float* grad_out, const void* workspace,
                    size_t workspace_bytes, float* grad_pred);
+
+/* The trainer's loss from gs_l1_ssim's out[2] (trainer.py:18-26): terms[0] = d_ssim =
+ * max(0, (1 - ssim) / 2) (losses.py:70-75), terms[1] = (1 - lambda) l1 + lambda d_ssim,
+ * terms[2..3] = the cotangents of (l1, ssim) for a unit cotangent of terms[1] (the
+ * grad_out of gs_l1_ssim_bwd; max passes half at a tie), terms[4] = 1 - 2 d_ssim (the
+ * reported SSIM, trainer.py:30).  Device arrays, one launch. */
+int gs_l1_ssim_terms(void* stream, const float* l1_ssim, double lambda_ssim, float* terms);
 
 /* One Adam step, in place, of num_arrays (<= 8) float32 parameter arrays, each with
  * its gradient and first/second moments (same sizes), counts[i] elements laid out as

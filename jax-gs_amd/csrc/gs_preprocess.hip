@@ -546,6 +546,133 @@ __global__ __launch_bounds__(64) void preprocess_bwd_kernel(
   }
 }
 
+// The training step's tail in one pass (trainer.py:66-103 with optax.adam of
+// train.py:127-155): the preprocessing VJP as in preprocess_bwd_kernel, the
+// densification statistics from the pre-update means, and the masked Adam update of
+// all five arrays in place, so that no parameter gradient goes through HBM.  The
+// per-element arithmetic is gs_adam_step's and the statistics are densify_kernel's, so
+// the result equals the three-launch sequence bit for bit.
+struct AdamConsts {
+  float neg_lr[5];  // means, scales, quaternions, opacities, sh
+  float b1, b2, omb1, omb2, bc1, bc2, eps;
+};
+struct MomentPtrs {
+  float* mu[5];
+  float* nu[5];
+};
+
+__device__ inline float adam_delta(const AdamConsts& A, int k, float g, float& m, float& v, bool on) {
+  m = A.omb1 * g + A.b1 * m;
+  v = A.omb2 * (g * g) + A.b2 * v;
+  const float u = ((m / A.bc1) / (sqrtf(v / A.bc2) + A.eps)) * A.neg_lr[k];
+  return on ? u : 0.0f;
+}
+
+template <int L>
+__device__ inline void adam_row(const AdamConsts& A, int k, float* __restrict__ p, float* __restrict__ mu,
+                                float* __restrict__ nu, const float* g, int64_t i, bool on) {
+#pragma unroll
+  for (int j = 0; j < L; ++j) {
+    float m = mu[L * i + j], v = nu[L * i + j];
+    const float d = adam_delta(A, k, g[j], m, v, on);
+    p[L * i + j] = p[L * i + j] + d;
+    mu[L * i + j] = m;
+    nu[L * i + j] = v;
+  }
+}
+
+template <int DEG>
+__global__ __launch_bounds__(64) void preprocess_bwd_adam_kernel(
+    int64_t n, int K, float* __restrict__ means, float* __restrict__ scales, float* __restrict__ quats,
+    float* __restrict__ opac, float* __restrict__ sh, const float* __restrict__ w2c, float fx, float fy,
+    const float* __restrict__ grec, MomentPtrs M, AdamConsts A, const uint8_t* __restrict__ active,
+    const uint8_t* __restrict__ valid, const float* __restrict__ radii, float focal, float pixel_scale,
+    float* __restrict__ grad_accum, int32_t* __restrict__ denom, float* __restrict__ max_radii) {
+  constexpr int NB = (DEG + 1) * (DEG + 1);
+  constexpr int LS = 49, LG = 13;
+  __shared__ float shs[64 * LS];
+  __shared__ float grs[64 * LG];
+  const int lane = threadIdx.x;
+  const int64_t g0 = (int64_t)blockIdx.x * 64;
+  const int KC = 3 * K;
+  const int64_t i = g0 + lane;
+  const GaussIn in = load_gauss(means, scales, quats, opac, i < n ? i : n - 1);
+  stage_rows<3 * NB>(sh, g0, n, (int64_t)KC, shs, LS, lane);
+  stage_rows<kRec>(grec, g0, n, (int64_t)kRec, grs, LG, lane);
+  __syncthreads();
+  if (i < n) {
+    float gm[3], gsc[3], gq[4], go[1];
+    preprocess_bwd_one<DEG>(0, K, in, w2c, fx, fy, grs + lane * LG, shs + lane * LS, gm, gsc, gq, go);
+    const bool on = active == nullptr || active[i] != 0;
+    if (grad_accum != nullptr) {
+      // trainer.py:280-294 from the means before the update
+      const float zc = ((in.mx * w2c[8] + in.my * w2c[9]) + in.mz * w2c[10]) + w2c[11];
+      const float z = jmax(zc, 0.01f);
+      const float gn = sqrtf((gm[0] * gm[0] + gm[1] * gm[1]) + gm[2] * gm[2]);
+      grad_accum[i] = grad_accum[i] + (gn * (z / focal)) * pixel_scale;
+      const bool v = valid[i] != 0;
+      denom[i] = denom[i] + ((v && on) ? 1 : 0);
+      if (v) max_radii[i] = jmax(max_radii[i], radii[i]);
+    }
+    adam_row<3>(A, 0, means, M.mu[0], M.nu[0], gm, i, on);
+    adam_row<3>(A, 1, scales, M.mu[1], M.nu[1], gsc, i, on);
+    adam_row<4>(A, 2, quats, M.mu[2], M.nu[2], gq, i, on);
+    adam_row<1>(A, 3, opac, M.mu[3], M.nu[3], go, i, on);
+  }
+  __syncthreads();
+  // SH rows g0.. are contiguous: consecutive lanes update consecutive values (row of
+  // element e as in preprocess_bwd_kernel)
+  const float inv = 1.0f / (float)KC;
+  const int64_t rows = n - g0 < 64 ? n - g0 : 64;
+  const int total = (int)rows * KC;
+  float* __restrict__ p = sh + g0 * KC;
+  float* __restrict__ mu = M.mu[4] + g0 * KC;
+  float* __restrict__ nu = M.nu[4] + g0 * KC;
+  if ((KC & 3) == 0 && ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(mu) |
+                         reinterpret_cast<uintptr_t>(nu)) & 15) == 0) {
+    // 16-byte vectors, four in flight per lane (a row holds a whole number of vectors)
+    const int nv = total >> 2;
+    for (int v0 = lane; v0 < nv; v0 += 4 * 64) {
+      float4 pp[4], mm[4], vv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int q = v0 + 64 * u;
+        if (q < nv) {
+          pp[u] = reinterpret_cast<const float4*>(p)[q];
+          mm[u] = reinterpret_cast<const float4*>(mu)[q];
+          vv[u] = reinterpret_cast<const float4*>(nu)[q];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int q = v0 + 64 * u;
+        if (q >= nv) continue;
+        const int e = 4 * q;
+        const int r = (int)(((float)e + 0.5f) * inv);
+        const bool on = active == nullptr || active[g0 + r] != 0;
+        const float* gr = shs + r * LS + (e - r * KC);
+        pp[u].x = pp[u].x + adam_delta(A, 4, gr[0], mm[u].x, vv[u].x, on);
+        pp[u].y = pp[u].y + adam_delta(A, 4, gr[1], mm[u].y, vv[u].y, on);
+        pp[u].z = pp[u].z + adam_delta(A, 4, gr[2], mm[u].z, vv[u].z, on);
+        pp[u].w = pp[u].w + adam_delta(A, 4, gr[3], mm[u].w, vv[u].w, on);
+        reinterpret_cast<float4*>(p)[q] = pp[u];
+        reinterpret_cast<float4*>(mu)[q] = mm[u];
+        reinterpret_cast<float4*>(nu)[q] = vv[u];
+      }
+    }
+  } else {
+    for (int e = lane; e < total; e += 64) {
+      const int r = (int)(((float)e + 0.5f) * inv);
+      const bool on = active == nullptr || active[g0 + r] != 0;
+      float m = mu[e], v = nu[e];
+      const float d = adam_delta(A, 4, shs[r * LS + (e - r * KC)], m, v, on);
+      p[e] = p[e] + d;
+      mu[e] = m;
+      nu[e] = v;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void densify_kernel(int64_t n, const float* __restrict__ g_means,
                                                       const float* __restrict__ means,
                                                       const float* __restrict__ w2c, float focal,
@@ -667,5 +794,56 @@ extern "C" int gs_densify_accumulate(void* stream, int64_t n, const float* grad_
                      grad_means, means, w2c, focal, pixel_scale, valid, active, radii, grad_accum, denom,
                      max_radii);
   GS_LAUNCH_CHECK("densify_kernel");
+  return GS_OK;
+}
+
+extern "C" int gs_preprocess_bwd_adam(void* stream, int64_t n, int sh_k, int sh_degree, float* means, float* scales,
+                                      float* quats, float* opacities, float* sh_coeffs, const float* w2c, int width,
+                                      int height, float fx, float fy, float cx, float cy, const float* grad_records,
+                                      float* const* moments, const double* lrs, int step, double b1, double b2,
+                                      double eps, const uint8_t* active, const uint8_t* valid, const float* radii,
+                                      float focal, float pixel_scale, float* grad_accum, int32_t* denom,
+                                      float* max_radii) {
+  GS_REQUIRE(n >= 0, "gs_preprocess_bwd_adam: n must be >= 0");
+  GS_REQUIRE(sh_degree >= 0 && sh_degree <= 3 && sh_k >= (sh_degree + 1) * (sh_degree + 1) && sh_k <= 16,
+             "gs_preprocess_bwd_adam: sh_k %d / degree %d", sh_k, sh_degree);
+  GS_REQUIRE(width > 0 && height > 0, "gs_preprocess_bwd_adam: bad image size %dx%d", width, height);
+  GS_REQUIRE(step >= 1, "gs_preprocess_bwd_adam: step (count after this update) must be >= 1");
+  GS_REQUIRE(moments && lrs, "gs_preprocess_bwd_adam: NULL moments / learning rates");
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(means && scales && quats && opacities && sh_coeffs && w2c && grad_records,
+             "gs_preprocess_bwd_adam: NULL array argument");
+  GS_REQUIRE(grad_accum == nullptr || (denom && max_radii && valid && radii),
+             "gs_preprocess_bwd_adam: statistics need denom, max_radii, valid and radii");
+  MomentPtrs M;
+  for (int k = 0; k < 5; ++k) {
+    GS_REQUIRE(moments[k] && moments[5 + k], "gs_preprocess_bwd_adam: NULL moment array %d", k);
+    M.mu[k] = moments[k];
+    M.nu[k] = moments[5 + k];
+  }
+  // the same float32 constants as gs_adam_step
+  AdamConsts A;
+  for (int k = 0; k < 5; ++k) A.neg_lr[k] = (float)(-lrs[k]);
+  A.b1 = (float)b1;
+  A.b2 = (float)b2;
+  A.omb1 = (float)(1.0 - b1);
+  A.omb2 = (float)(1.0 - b2);
+  A.bc1 = 1.0f - powf((float)b1, (float)step);
+  A.bc2 = 1.0f - powf((float)b2, (float)step);
+  A.eps = (float)eps;
+  (void)cx;
+  (void)cy;
+#define GS_PRE_BWD_ADAM(D)                                                                                       \
+  hipLaunchKernelGGL(preprocess_bwd_adam_kernel<D>, dim3(div_up(n, 64)), dim3(64), 0, (hipStream_t)stream, n,     \
+                     sh_k, means, scales, quats, opacities, sh_coeffs, w2c, fx, fy, grad_records, M, A, active, valid, \
+                     radii, focal, pixel_scale, grad_accum, denom, max_radii)
+  switch (sh_degree) {
+    case 0: GS_PRE_BWD_ADAM(0); break;
+    case 1: GS_PRE_BWD_ADAM(1); break;
+    case 2: GS_PRE_BWD_ADAM(2); break;
+    default: GS_PRE_BWD_ADAM(3); break;
+  }
+#undef GS_PRE_BWD_ADAM
+  GS_LAUNCH_CHECK("preprocess_bwd_adam_kernel");
   return GS_OK;
 }

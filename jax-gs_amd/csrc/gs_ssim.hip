@@ -293,6 +293,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void l
   }
 }
 
+// trainer.py:18-26 from the two means: terms[0] = d_ssim = max(0, (1 - ssim) / 2),
+// terms[1] = total = (1 - lambda) l1 + lambda d_ssim, and the cotangents of (l1, ssim)
+// for a unit cotangent of the total: terms[2] = 1 - lambda, terms[3] = -lambda/2 times
+// max's derivative (1 above 0, 1/2 at 0, as lax.max), and terms[4] = the reported metric
+// 1 - 2 d_ssim (trainer.py:30).  Same float32 operations as the host-side formula.
+__global__ void l1_ssim_terms_kernel(const float* __restrict__ l1_ssim, float lam, float one_minus_lam,
+                                     float* __restrict__ terms) {
+  const float l1 = l1_ssim[0], ssim = l1_ssim[1];
+  const float half = (1.0f - ssim) / 2.0f;
+  const float d = fmaxf(0.0f, half);
+  terms[0] = d;
+  terms[1] = one_minus_lam * l1 + lam * d;
+  terms[2] = one_minus_lam;
+  const float gate = half > 0.0f ? 1.0f : (half == 0.0f ? 0.5f : 0.0f);
+  terms[3] = -(lam * 0.5f) * gate;
+  terms[4] = 1.0f - d * 2.0f;
+}
+
 Taps make_taps() {
   Taps t;
   double s = 0.0, e[kSTaps];
@@ -383,5 +401,14 @@ extern "C" int gs_l1_ssim_bwd(void* stream, int height, int width, int channels,
     default: hipLaunchKernelGGL(l1_ssim_bwd_kernel<4>, L.grid, dim3(256), 0, s, height, width, L.TX, L.T, pred, target, taps, inv, gmap, grad_out, grad_pred); break;
   }
   GS_LAUNCH_CHECK("l1_ssim_bwd_kernel");
+  return GS_OK;
+}
+
+extern "C" int gs_l1_ssim_terms(void* stream, const float* l1_ssim, double lambda_ssim, float* terms) {
+  GS_REQUIRE(l1_ssim && terms, "gs_l1_ssim_terms: NULL argument");
+  GS_REQUIRE(lambda_ssim >= 0.0 && lambda_ssim <= 1.0, "gs_l1_ssim_terms: lambda must be in [0, 1]");
+  hipLaunchKernelGGL(l1_ssim_terms_kernel, dim3(1), dim3(1), 0, (hipStream_t)stream, l1_ssim, (float)lambda_ssim,
+                     (float)(1.0 - lambda_ssim), terms);
+  GS_LAUNCH_CHECK("l1_ssim_terms_kernel");
   return GS_OK;
 }

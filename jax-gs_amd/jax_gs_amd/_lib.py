@@ -51,6 +51,9 @@ _SIGS = {
     "gs_reset_opacities": [_P, _I64, _P, ctypes.c_double, _P],
     "gs_ply_pack": [_P, _I64, _I, _P, _P, _P, _P, _P, _P],
     "gs_ply_unpack": [_P, _I64, _I, _P, _P, _P, _P, _P, _P],
+    "gs_preprocess_bwd_adam": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _I,
+                               ctypes.c_double, ctypes.c_double, ctypes.c_double, _P, _P, _P, _F, _F, _P, _P, _P],
+    "gs_l1_ssim_terms": [_P, _P, ctypes.c_double, _P],
     "gs_adam_step": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, ctypes.c_double, ctypes.c_double,
                      ctypes.c_double],
     "gs_densify_accumulate": [_P, _I64, _P, _P, _P, _F, _F, _P, _P, _P, _P, _P, _P],

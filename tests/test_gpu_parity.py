@@ -569,3 +569,65 @@ def test_capacity_exceeded_is_flagged(cuda):
         image, _, _, _ = rasterizer.composite(pre["records"], part["sorted_gids"], part["ranges"], cam.H, cam.W,
                                               torch.zeros(3, device=cuda))
         assert torch.isfinite(image).all()
+
+
+@pytest.mark.gpu
+def test_l1_ssim_terms(cuda):
+    """gs_l1_ssim_terms against the loss composition of trainer.py:18-30 in float32, over
+    SSIM values above, at and below the max's tie (1) and outside [0, 1]."""
+    from jax_gs_amd import _lib
+
+    lam = 0.2
+    s = _lib.stream_handle(cuda)
+    for l1, ssim_v in ((0.125, 0.6), (0.3, 1.0), (0.01, 1.25), (0.5, -0.3), (0.0, 0.9999999)):
+        out = torch.tensor([l1, ssim_v], dtype=torch.float32, device=cuda)
+        terms = torch.full((5,), float("nan"), dtype=torch.float32, device=cuda)
+        _lib.call("gs_l1_ssim_terms", s, _lib.ptr(out), lam, _lib.ptr(terms))
+        t = _np(terms)
+        f = np.float32
+        half = (f(1.0) - f(ssim_v)) / f(2.0)
+        d = max(f(0.0), half)
+        assert t[0] == d
+        assert t[1] == f(1.0 - lam) * f(l1) + f(lam) * d
+        assert t[2] == f(1.0 - lam)
+        assert t[3] == f(-(lam * 0.5)) * f(oracle._tie_grad(np.float64(half)))
+        assert t[4] == f(1.0) - d * f(2.0)
+
+
+@pytest.mark.gpu
+def test_fused_train_step_matches_autograd_step(cuda):
+    """The fused step (one kernel for the preprocessing VJP, statistics and Adam) against
+    the autograd step (render's backward, accumulate_from_extras, Adam.step) over two steps
+    from the same state.  The rasterizer's VJP sums with atomics, so the two see gradients
+    equal up to float summation order: moments and statistics within 1e-4 relative."""
+    from jax_gs_amd.training import density
+    from jax_gs_amd.training.optimizer import make_optimizer
+    from jax_gs_amd.training.trainer import train_step
+
+    sc = scenes.make_scene(4, n=3000, width=96, height=64)
+    g, cam, tgt, _ = scenes.to_torch(sc, cuda)
+    states = []
+    for _ in range(2):
+        st = density.init_density_state(g, make_optimizer(extent=3.0, num_iterations=1000), 3000)
+        st.active_mask.copy_(torch.from_numpy(sc["mask"].astype(np.uint8)).to(cuda))
+        states.append(st)
+    opt = make_optimizer(extent=3.0, num_iterations=1000)
+    cs = (cam.W, cam.H, cam.fx, cam.fy, cam.cx, cam.cy)
+    for step in range(2):
+        _, loss_f, met_f = train_step(states[0], tgt, cam.W2C, cs, opt, sh_degree=sc["sh_degree"], fused=True)
+        _, loss_a, met_a = train_step(states[1], tgt, cam.W2C, cs, opt, sh_degree=sc["sh_degree"], fused=False)
+        assert abs(float(loss_f) - float(loss_a)) <= 1e-6
+        assert abs(float(met_f["ssim"]) - float(met_a["ssim"])) <= 1e-6
+        assert float(met_f["n_interactions"]) == float(met_a["n_interactions"])
+        f, a = states
+        assert f.opt_state.count == a.opt_state.count == step + 1
+        for fl in FIELDS:
+            assert _rel(_np(f.opt_state.mu[fl]), _np(a.opt_state.mu[fl])) <= 1e-4, fl
+            assert _rel(_np(f.opt_state.nu[fl]), _np(a.opt_state.nu[fl])) <= 1e-4, fl
+            pf, pa = _np(getattr(f.gaussians, fl)), _np(getattr(a.gaussians, fl))
+            # Adam's early updates are about -lr sign(g): a few near-zero gradients may
+            # differ in sign between summation orders
+            assert np.mean(np.abs(pf - pa) > 1e-6) <= 1e-3, fl
+        np.testing.assert_array_equal(_np(f.denom), _np(a.denom))
+        np.testing.assert_array_equal(_np(f.max_radii), _np(a.max_radii))
+        assert _rel(_np(f.grad_accum), _np(a.grad_accum)) <= 1e-4
