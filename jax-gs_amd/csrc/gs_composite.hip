@@ -38,7 +38,7 @@
 // dL/dalpha_k = T_k (c_k . g - Rg_k).  Per lane the entry's power cotangents are kept
 // as sums that the lane's pixels (one column, one dx) share; the 9 sums of two
 // contributing entries are reduce-scattered across the wave together (recursive
-// halving, so lane c ends with the total of sum c) and added to the Gaussians'
+// halving, so each of 18 lanes ends with the total of one sum) and added to the Gaussians'
 // gradient records with one atomic instruction (18 lanes).  Gradients follow JAX autodiff of the reference: the cap
 // min(0.99, .) passes no gradient when it binds (half at a tie), gated entries pass
 // none.
@@ -72,57 +72,96 @@ __device__ inline float wave_sum(float v) {
   return bcast(x, 63);
 }
 
-// Reduce-scatter of per-lane values over the wave by recursive halving: at level k a
-// lane keeps the half of its values whose index bit k equals its own lane bit k and
-// adds the partner's copy of them (partner = lane ^ 2^k: DPP quad_perm for 1 and 2,
-// ds_swizzle for 4, 8, 16), then the two 32-lane halves are summed (ds_bpermute).
-__device__ inline float swz_xor(float v, int pattern_xor) {
-  // ds_swizzle bit mode: and_mask 0x1F, or_mask 0, xor_mask in bits 14:10
-  switch (pattern_xor) {
-    case 4: return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (4 << 10) | 0x1F));
-    case 8: return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (8 << 10) | 0x1F));
-    default: return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (16 << 10) | 0x1F));
+// Reduce-scatter of per-lane values over the wave by recursive halving.  A level pairs
+// the values (2k, 2k+1); a lane keeps the member selected by one of its lane bits and
+// adds the partner lane's copy of it (partner = lane ^ distance).  The levels run in
+// the order of lane distance 32, 16, 8, 4, 2, so the wide levels (many values) use the
+// two-instruction forms:
+//   32, 16: v_permlane32_swap / v_permlane16_swap exchange the upper half of the low
+//           value with the lower half of the high value, after which every lane adds
+//           its two registers;
+//   8, 4:   two DPP adds restricted by bank masks (banks = groups of 4 lanes of a
+//           16-lane row): the lanes with a clear distance bit add the low value of
+//           lane + d into their low register, then the others add the high value of
+//           lane - d into the same register;
+//   2:      select the kept and the sent value and add the partner's (quad_perm DPP).
+// The last level (distance 1) is a plain pairwise sum.  Lane l ends with the wave
+// total of value index  b5 + 2 b4 + 4 b3 + 8 b2 + 16 b1  (b_i = bit i of l), the
+// same total in lanes l and l ^ 1.
+__device__ inline float add_swap32(float lo, float hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float add_swap16(float lo, float hi) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// The DPP adds are inline assembly (a masked DPP add that keeps the other lanes'
+// destination has no builtin form).  Each starts with two wait states: a VALU write of
+// a VGPR followed by a DPP read of it needs them, and the compiler's hazard checks do
+// not look inside inline assembly.
+#define GS_DPP_ADD_SELF(dst, ctrl, banks) \
+  asm volatile("s_nop 1\n\tv_add_f32_dpp %0, %0, %0 " ctrl " row_mask:0xf bank_mask:" banks : "+v"(dst))
+#define GS_DPP_ADD(dst, src, ctrl, banks) \
+  asm volatile("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 " ctrl " row_mask:0xf bank_mask:" banks : "+v"(dst) : "v"(src))
+
+template <int D>
+__device__ inline float add_banked(float lo, float hi, bool has_hi) {
+  if (D == 8) {
+    GS_DPP_ADD_SELF(lo, "row_shl:8", "0x3");
+    if (has_hi) GS_DPP_ADD(lo, hi, "row_shr:8", "0xc");
+  } else {
+    GS_DPP_ADD_SELF(lo, "row_shl:4", "0x5");
+    if (has_hi) GS_DPP_ADD(lo, hi, "row_shr:4", "0xa");
   }
+  return lo;
 }
+#undef GS_DPP_ADD
+#undef GS_DPP_ADD_SELF
 
-// Value of the lane's partner at lane distance 2^l (l = 0..4).
-template <int L>
-__device__ inline float xor_lane(float v) {
-  if (L == 0) return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
-  if (L == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
-  return swz_xor(v, 1 << L);
-}
-
-// One halving level: pairs (2k, 2k+1) of the n values; the lane keeps the member
-// selected by its bit L and adds the partner's copy of it.
-template <int L, int N>
-__device__ inline void halve(float* cur, int lane) {
-  const bool bit = (lane >> L) & 1;
+template <int D, int N>
+__device__ inline void halve_level(float* cur, int lane) {
 #pragma unroll
   for (int k = 0; k < (N + 1) / 2; ++k) {
+    const bool has_hi = 2 * k + 1 < N;
     const float lo = cur[2 * k];
-    const float hi = (2 * k + 1 < N) ? cur[2 * k + 1] : 0.0f;
-    const float keep = bit ? hi : lo, send = bit ? lo : hi;
-    cur[k] = keep + xor_lane<L>(send);
+    const float hi = has_hi ? cur[2 * k + 1] : lo;  // a missing high value: its slot is never read
+    if (D == 32) {
+      cur[k] = add_swap32(lo, hi);
+    } else if (D == 16) {
+      cur[k] = add_swap16(lo, hi);
+    } else if (D == 8 || D == 4) {
+      cur[k] = add_banked<D>(lo, hi, has_hi);
+    } else {  // D == 2
+      const bool bit = (lane >> 1) & 1;
+      const float keep = bit ? hi : lo, send = bit ? lo : hi;
+      cur[k] = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x4E, 0xF, 0xF, false));
+    }
   }
 }
 
-// Reduce-scatter of NV <= 32 per-lane values: afterwards lane L holds the wave total
-// of value L % 32 (0 for L % 32 >= NV).
+// Value index whose total lane l holds after reduce_scatter.
+__device__ inline int scatter_index(int l) {
+  return ((l >> 5) & 1) | ((l >> 3) & 2) | ((l >> 1) & 4) | ((l << 1) & 8) | ((l << 3) & 16);
+}
+
+// Reduce-scatter of NV <= 32 per-lane values: afterwards lane l holds the wave total of
+// value scatter_index(l) (undefined for indices >= NV).
 template <int NV>
 __device__ inline float reduce_scatter(const float* v, int lane) {
+  static_assert(NV >= 1 && NV <= 32, "at most 32 values");
   float cur[NV];
 #pragma unroll
   for (int k = 0; k < NV; ++k) cur[k] = v[k];
   constexpr int N1 = (NV + 1) / 2, N2 = (N1 + 1) / 2, N3 = (N2 + 1) / 2, N4 = (N3 + 1) / 2;
-  halve<0, NV>(cur, lane);
-  halve<1, N1>(cur, lane);
-  halve<2, N2>(cur, lane);
-  halve<3, N3>(cur, lane);
-  halve<4, N4>(cur, lane);
-  float t = cur[0];
-  t = t + __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __float_as_int(t)));
-  return t;
+  halve_level<32, NV>(cur, lane);
+  halve_level<16, N1>(cur, lane);
+  halve_level<8, N2>(cur, lane);
+  halve_level<4, N3>(cur, lane);
+  halve_level<2, N4>(cur, lane);
+  const float t = cur[0];
+  return t + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0xB1, 0xF, 0xF, false));
 }
 
 // XCD-aware tile order: consecutive workgroups go round-robin to the 8 XCDs, so
@@ -428,13 +467,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
         const float dx = px - e.mx;
         const float Adx2l = fmaf(e.A * dx, dx, e.lop), Bdx = e.B * dx;
         // per-lane sums over the lane's pixels: P = sum dpower, Q = sum dpower*dy,
-        // V = sum dpower*dy^2, colour cotangents
-        float P = 0.0f, Q = 0.0f, V = 0.0f, gc0 = 0.0f, gc1 = 0.0f, gc2 = 0.0f;
+        // V = sum dpower*dy^2, colour cotangents (from -0, so that the first term is
+        // the sum itself)
+        float P = -0.0f, Q = -0.0f, V = -0.0f, gc0 = -0.0f, gc1 = -0.0f, gc2 = -0.0f;
+        if (live) {
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
           const float dy = py[i] - e.my;
           const float q = q_of(dy, Adx2l, Bdx, e.C);
-          if (k >= 0 && k < kp[i] && q > e.thr) {
+          if (k < kp[i] && q > e.thr) {
             any = true;
             const float araw = __builtin_amdgcn_exp2f(q);
             const float al = araw < 0.99f ? araw : 0.99f;
@@ -459,6 +500,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
             V = fmaf(dpy, dy, V);
           }
         }
+        }
         // gradient record sums: [0] dpw dx, [1] dpw dy, [2] dpw dx^2, [3] dpw dx dy,
         // [4] dpw dy^2, [5] dpw, [6..8] colour
         const float Sx = P * dx;
@@ -474,8 +516,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
       }
       if (__ballot(any) != 0ull) {
         const float mine = reduce_scatter<18>(v, lane);
-        if (lane < 18 && mine != 0.0f)
-          atomicAdd(&grec[(int64_t)(lane < 9 ? ga : gb) * kRec + (lane < 9 ? lane : lane - 9)], mine);
+        const int vi = scatter_index(lane);
+        if ((lane & 1) == 0 && vi < 18 && mine != 0.0f)
+          atomicAdd(&grec[(int64_t)(vi < 9 ? ga : gb) * kRec + (vi < 9 ? vi : vi - 9)], mine);
       }
     }
   }
