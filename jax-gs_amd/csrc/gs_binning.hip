@@ -18,10 +18,11 @@
 //                      generated on the fly from the depth-sorted words and counting-
 //                      sorted by superblock in one 8-bit radix pass (two when the image
 //                      has more than 256 superblocks) -> per superblock the list of
-//                      Gaussians touching it, in (bucket, id) order.  A Gaussian's pair
-//                      for superblock (sx, sy) is produced in slot (sx % 3, sy % 3), so
-//                      all pairs of one superblock come from the same slot and are
-//                      ranked in Gaussian order.
+//                      Gaussians touching it, in (bucket, id) order.  A wave lists the
+//                      pairs of its 64 Gaussians in LDS in Gaussian order and ranks
+//                      the list 64 pairs at a time; a Gaussian has one pair per
+//                      superblock at most, so each superblock's pairs keep Gaussian
+//                      order.
 //   4. tile pass       a superblock's list is cut into chunks of 256 Gaussians; a wave
 //                      takes a chunk 64 Gaussians at a time and forms 8 column and 8
 //                      row lane masks with ballots; lane u owns tile u of the
@@ -99,13 +100,6 @@ __device__ inline SBRect sb_rect(const Packed& p) {
   r.sy0 = p.y0 / kSB;
   r.sy1 = (p.y0 + p.h - 1) / kSB;
   return r;
-}
-
-// The superblock coordinate in [c0, c1] congruent to j mod 3 (at most one exists,
-// since c1 - c0 < 3); returns c1 + 1 when there is none.
-__device__ inline int slot_coord(int c0, int c1, int j) {
-  const int c = c0 + (j - c0 % kSBSpan + kSBSpan) % kSBSpan;
-  return c <= c1 ? c : c1 + 1;
 }
 
 // Lanes (among `act` lanes) whose value d (RB bits) equals this lane's.
@@ -384,6 +378,10 @@ __global__ __launch_bounds__(256) void pair_upsweep_kernel(const uint64_t* __res
   table[(int64_t)threadIdx.x * G + blockIdx.x] = hist[threadIdx.x];
 }
 
+// Each round of 64 Gaussians lists its (superblock, lane) pairs in LDS in lane order
+// (a wave prefix sum of the pair counts gives each Gaussian its place) and ranks the
+// list 64 pairs at a time.  A Gaussian has at most one pair per superblock, so the
+// pairs of any one superblock stay in Gaussian order: the pass is stable.
 template <bool WITH_KEYS>
 __global__ __launch_bounds__(64) void pair_downsweep_kernel(const uint64_t* __restrict__ words, int64_t n, int SX,
                                                             int G, const uint32_t* __restrict__ table,
@@ -393,6 +391,8 @@ __global__ __launch_bounds__(64) void pair_downsweep_kernel(const uint64_t* __re
                                                             uint32_t* __restrict__ n_pairs) {
   constexpr int NB = 1 << kPairRB;
   __shared__ uint32_t cnt[NB];
+  __shared__ uint32_t list[64 * kSBSpan * kSBSpan];  // (superblock << 6) | lane
+  __shared__ uint64_t wl[64];
   const int lane = threadIdx.x;
   const uint32_t total = init_digit_counters<kPairRB>(cnt, table, digit_tot, G, blockIdx.x, lane);
   if (blockIdx.x == 0 && lane == 0) *n_pairs = total;
@@ -405,29 +405,36 @@ __global__ __launch_bounds__(64) void pair_downsweep_kernel(const uint64_t* __re
     const bool in = i < end;
     const uint64_t wv = in ? words[i] : 0ull;
     const SBRect b = sb_rect(unpack(wv));
-    const bool has = in && b.has;
-#pragma unroll
-    for (int jy = 0; jy < kSBSpan; ++jy) {
-      const int sy = slot_coord(b.sy0, b.sy1, jy);
-#pragma unroll
-      for (int jx = 0; jx < kSBSpan; ++jx) {
-        const int sx = slot_coord(b.sx0, b.sx1, jx);
-        const bool act = has && sx <= b.sx1 && sy <= b.sy1;
-        const uint32_t s = (uint32_t)(sy * SX + sx);
-        const uint32_t d = s & (NB - 1);
-        const uint64_t m = match_any<kPairRB>(d, act);
-        if (act) {
-          const uint64_t before = m & lt;
-          const uint32_t base_d = cnt[d];
-          const uint32_t dst = base_d + (uint32_t)__popcll(before);
-          if (before == 0) cnt[d] = base_d + (uint32_t)__popcll(m);
-          if (dst < total) {  // always true for a consistent table
-            vals_out[dst] = wv;
-            if (WITH_KEYS) keys_out[dst] = s;
-          }
+    const int nx = (in && b.has) ? b.sx1 - b.sx0 + 1 : 0;
+    const int ny = (in && b.has) ? b.sy1 - b.sy0 + 1 : 0;
+    const uint32_t c = (uint32_t)(nx * ny);
+    const uint32_t inc = wave_incl_scan(c);
+    const uint32_t P = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+    uint32_t at = inc - c;
+    wl[lane] = wv;
+    for (int jy = 0; jy < ny; ++jy)
+      for (int jx = 0; jx < nx; ++jx) list[at++] = ((uint32_t)((b.sy0 + jy) * SX + b.sx0 + jx) << 6) | (uint32_t)lane;
+    __syncthreads();
+    for (uint32_t b0 = 0; b0 < P; b0 += 64) {
+      const bool act = b0 + lane < P;
+      const uint32_t e = act ? list[b0 + lane] : 0u;
+      const uint32_t sb = e >> 6;
+      const uint32_t d = sb & (NB - 1);
+      const uint64_t m = match_any<kPairRB>(d, act);
+      if (act) {
+        const uint64_t before = m & lt;
+        const uint32_t base_d = cnt[d];
+        const uint32_t dst = base_d + (uint32_t)__popcll(before);
+        // All lanes have read cnt[] before the group's first lane writes it back:
+        // LDS operations of one wave execute in program order.
+        if (before == 0) cnt[d] = base_d + (uint32_t)__popcll(m);
+        if (dst < total) {  // always true for a consistent table
+          vals_out[dst] = wl[e & 63];
+          if (WITH_KEYS) keys_out[dst] = sb;
         }
       }
     }
+    __syncthreads();  // the list and words are rewritten by the next round
   }
 }
 
@@ -586,31 +593,63 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
                                                                int32_t* __restrict__ stats) {
   __shared__ int64_t red[7][kBig / 64];
   int64_t acc[7] = {0, 0, 0, 0, 0, 0, 0};  // max, ovf tiles, ovf inter, trunc tiles, trunc inter, cap, neg
+  // the loads of a group are issued together (the values were written by other XCDs)
+  constexpr int kGroup = 8;
   const int per = (T + kBig - 1) / kBig;
   const int t0 = threadIdx.x * per;
   uint32_t run = 0;
-  for (int k = 0; k < per; ++k) {
-    const int t = t0 + k;
-    const uint32_t c = t < T ? tot[t] : 0u;
-    run += c;
-    acc[0] = acc[0] > (int64_t)c ? acc[0] : (int64_t)c;
-    acc[1] += c > (uint32_t)kBlock;
-    acc[2] += c > (uint32_t)kBlock ? c - kBlock : 0;
-    acc[3] += c > (uint32_t)kMaxTileEntries;
-    acc[4] += c > (uint32_t)kMaxTileEntries ? c - kMaxTileEntries : 0;
+  for (int g0 = 0; g0 < per; g0 += kGroup) {
+    uint32_t v[kGroup];
+#pragma unroll
+    for (int k = 0; k < kGroup; ++k) {
+      const int t = t0 + g0 + k;
+      v[k] = (g0 + k < per && t < T) ? tot[t] : 0u;
+    }
+#pragma unroll
+    for (int k = 0; k < kGroup; ++k) {
+      const uint32_t c = v[k];
+      run += c;
+      acc[0] = acc[0] > (int64_t)c ? acc[0] : (int64_t)c;
+      acc[1] += c > (uint32_t)kBlock;
+      acc[2] += c > (uint32_t)kBlock ? c - kBlock : 0;
+      acc[3] += c > (uint32_t)kMaxTileEntries;
+      acc[4] += c > (uint32_t)kMaxTileEntries ? c - kMaxTileEntries : 0;
+    }
+  }
+  {
+    uint32_t s5 = 0, s6 = 0;
+    for (int b0 = 0; b0 < nblk; b0 += 4 * kBig) {
+      uint32_t a[4], z[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int b = b0 + k * kBig + (int)threadIdx.x;
+        a[k] = b < nblk ? blkstat[2 * b] : 0u;
+        z[k] = b < nblk ? blkstat[2 * b + 1] : 0u;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        s5 += a[k];
+        s6 += z[k];
+      }
+    }
+    acc[5] = s5;
+    acc[6] = s6;
   }
   uint32_t total;
   uint32_t pos = block_excl_scan<kBig>(run, &total);
-  for (int k = 0; k < per; ++k) {
-    const int t = t0 + k;
-    if (t < T) {
-      ranges[t] = (int32_t)pos;
-      pos += tot[t];
+  for (int g0 = 0; g0 < per; g0 += kGroup) {
+    uint32_t v[kGroup];
+#pragma unroll
+    for (int k = 0; k < kGroup; ++k) {
+      const int t = t0 + g0 + k;
+      v[k] = (g0 + k < per && t < T) ? tot[t] : 0u;
     }
-  }
-  for (int b = threadIdx.x; b < nblk; b += kBig) {
-    acc[5] += blkstat[2 * b];
-    acc[6] += blkstat[2 * b + 1];
+#pragma unroll
+    for (int k = 0; k < kGroup; ++k) {
+      const int t = t0 + g0 + k;
+      if (g0 + k < per && t < T) ranges[t] = (int32_t)pos;
+      pos += v[k];
+    }
   }
   // reduce the 7 accumulators over the block
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
