@@ -562,26 +562,35 @@ __device__ inline int tile_of(int sx, int sy, int lane, int TX, int TY) {
   return (tx < TX && ty < TY) ? ty * TX + tx : -1;
 }
 
-// 4a. counts per (chunk, tile of its superblock) -> cnt[c*64 + u].
+// 4a. counts per (chunk, tile of its superblock) -> cnt[c*64 + u], and the chunk's
+// descriptor (first pair, pair count, superblock column and row) for the write sweep.
+// The chunk's 256 words are loaded at once (one memory round trip, not four).
+static_assert(kChunk == 4 * 64, "a chunk is four steps of 64 Gaussians");
 __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restrict__ n_chunks, int64_t cmax,
                                                          const uint32_t* __restrict__ chunk_sb,
                                                          const uint32_t* __restrict__ chunk_base,
                                                          const int32_t* __restrict__ sb_ranges, int S,
                                                          const uint64_t* __restrict__ pval, int SX,
-                                                         uint32_t* __restrict__ cnt) {
+                                                         uint32_t* __restrict__ cnt, uint4* __restrict__ desc) {
   const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
   const uint32_t C = (uint32_t)min<int64_t>((int64_t)*n_chunks, cmax);
   for (uint32_t c = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); c < C; c += nwaves) {
     const ChunkSpan cs = chunk_span(c, chunk_sb, chunk_base, sb_ranges, S, SX);
+    const int len = (int)(cs.end - cs.begin);
+    uint64_t wv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) wv[k] = 64 * k + lane < len ? pval[cs.begin + 64 * k + lane] : 0ull;
     uint32_t mycount = 0;  // lane u counts tile u
-    for (int64_t base = cs.begin; base < cs.end; base += 64) {
-      const int64_t q = base + lane;
-      const bool act = q < cs.end;
-      const Packed g = unpack(act ? pval[q] : 0ull);
-      mycount += (uint32_t)__popcll(tile_lane_mask(act, g, cs.sx, cs.sy, lane));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (64 * k < len) {
+        const bool act = 64 * k + lane < len;
+        mycount += (uint32_t)__popcll(tile_lane_mask(act, unpack(wv[k]), cs.sx, cs.sy, lane));
+      }
     }
     cnt[(int64_t)c * 64 + lane] = mycount;
+    if (lane == 0) desc[c] = make_uint4((uint32_t)cs.begin, (uint32_t)len, (uint32_t)cs.sx, (uint32_t)cs.sy);
   }
 }
 
@@ -729,68 +738,92 @@ __global__ __launch_bounds__(kBig) void chunk_scan_kernel(const uint32_t* __rest
 // in an unrolled loop with wave-uniform masks (column & row ballots), and the lanes
 // of a tile's mask store their ids at base + popcount(mask & lanes-below): one
 // contiguous run per store.  Lane u holds tile u's next slot (read with v_readlane,
-// advanced once per step).
+// advanced once per step).  A chunk costs two memory round trips: its descriptor
+// (with its counts), then its 256 words and the tiles' range starts together.
+// CHECK: some entries fall beyond the capacity and are dropped.
+template <bool WITH_TILES, bool CHECK>
+__device__ inline void write_step(uint64_t word, bool act, int sx, int sy, int lane, uint32_t n_gauss, int TX,
+                                  uint32_t cap32, uint32_t& base, int32_t* __restrict__ out_gid,
+                                  int32_t* __restrict__ out_tile) {
+  const Packed g = unpack(act ? word : 0ull);
+  act = act && g.gid < n_gauss;  // ids are < n by construction
+  // column and row masks are wave-uniform; tile (ux, uy)'s mask is their AND
+  uint64_t cm[kSB], rm[kSB];
+#pragma unroll
+  for (int k = 0; k < kSB; ++k) {
+    const int tx = sx * kSB + k, ty = sy * kSB + k;
+    cm[k] = __ballot(act && g.x0 <= tx && tx < g.x0 + g.w);
+    rm[k] = __ballot(act && g.y0 <= ty && ty < g.y0 + g.h);
+  }
+#pragma unroll
+  for (int uy = 0; uy < kSB; ++uy) {
+    if (rm[uy] == 0ull) continue;
+#pragma unroll
+    for (int ux = 0; ux < kSB; ++ux) {
+      const uint64_t m = cm[ux] & rm[uy];
+      if (m == 0ull) continue;
+      const uint32_t b = __builtin_amdgcn_readlane(base, uy * kSB + ux);
+      if (__builtin_amdgcn_inverse_ballot_w64(m)) {
+        // lanes of m store their ids at b + (lanes of m below them): one run
+        const uint32_t dst =
+            b + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        if (!CHECK || dst < cap32) {
+          out_gid[dst] = (int32_t)g.gid;
+          if (WITH_TILES) out_tile[dst] = (sy * kSB + uy) * TX + sx * kSB + ux;
+        }
+      }
+    }
+  }
+  // lane u advances tile u's slot by its count in this step
+  uint64_t mine = 0;
+  const int ux = lane & 7, uy = lane >> 3;
+#pragma unroll
+  for (int k = 0; k < kSB; ++k) mine = ux == k ? cm[k] : mine;
+  uint64_t rmine = 0;
+#pragma unroll
+  for (int k = 0; k < kSB; ++k) rmine = uy == k ? rm[k] : rmine;
+  base += (uint32_t)__popcll(mine & rmine);
+}
+
+template <bool WITH_TILES, bool CHECK>
+__device__ inline void write_chunk(uint32_t c, const uint4& d, const uint64_t* __restrict__ pval, uint32_t n_gauss,
+                                   int TX, int TY, uint32_t cnt_c, const int32_t* __restrict__ ranges, uint32_t cap32,
+                                   int lane, int32_t* __restrict__ out_gid, int32_t* __restrict__ out_tile) {
+  const int len = (int)d.y, sx = (int)d.z, sy = (int)d.w;
+  const int t = tile_of(sx, sy, lane, TX, TY);
+  uint64_t wv[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) wv[k] = 64 * k + lane < len ? pval[d.x + 64 * k + lane] : 0ull;
+  // lane u: next slot of tile u (tiles outside the image never get entries)
+  uint32_t base = (t >= 0 ? (uint32_t)ranges[t] : 0u) + cnt_c;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    if (64 * k < len)
+      write_step<WITH_TILES, CHECK>(wv[k], 64 * k + lane < len, sx, sy, lane, n_gauss, TX, cap32, base, out_gid,
+                                    out_tile);
+}
+
 template <bool WITH_TILES>
 __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restrict__ n_chunks, int64_t cmax,
-                                                         const uint32_t* __restrict__ chunk_sb,
-                                                         const uint32_t* __restrict__ chunk_base,
-                                                         const int32_t* __restrict__ sb_ranges, int S,
-                                                         const uint64_t* __restrict__ pval, uint32_t n_gauss, int SX,
-                                                         int TX, int TY, const uint32_t* __restrict__ cnt,
-                                                         const int32_t* __restrict__ ranges, int64_t cap,
+                                                         const uint4* __restrict__ desc,
+                                                         const uint64_t* __restrict__ pval, uint32_t n_gauss, int TX,
+                                                         int TY, const uint32_t* __restrict__ cnt,
+                                                         const int32_t* __restrict__ ranges, int T, int64_t cap,
                                                          int32_t* __restrict__ out_gid,
                                                          int32_t* __restrict__ out_tile) {
   const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
   const uint32_t C = (uint32_t)min<int64_t>((int64_t)*n_chunks, cmax);
   const uint32_t cap32 = (uint32_t)cap;  // gs_bin checks cap < 2^31
+  // every entry fits (the usual case): no per-store capacity test
+  const bool fits = ranges[T] >= 0 && (int64_t)ranges[T] <= cap;
   for (uint32_t c = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); c < C; c += nwaves) {
-    const ChunkSpan cs = chunk_span(c, chunk_sb, chunk_base, sb_ranges, S, SX);
-    const int t = tile_of(cs.sx, cs.sy, lane, TX, TY);
-    // lane u: next slot of tile u (tiles outside the image never get entries)
-    uint32_t base = (t >= 0 ? (uint32_t)ranges[t] : 0u) + cnt[(int64_t)c * 64 + lane];
-    for (int64_t b0 = cs.begin; b0 < cs.end; b0 += 64) {
-      const int64_t q = b0 + lane;
-      bool act = q < cs.end;
-      const Packed g = unpack(act ? pval[q] : 0ull);
-      act = act && g.gid < n_gauss;  // ids are < n by construction
-      // column and row masks are wave-uniform; tile (ux, uy)'s mask is their AND
-      uint64_t cm[kSB], rm[kSB];
-#pragma unroll
-      for (int k = 0; k < kSB; ++k) {
-        const int tx = cs.sx * kSB + k, ty = cs.sy * kSB + k;
-        cm[k] = __ballot(act && g.x0 <= tx && tx < g.x0 + g.w);
-        rm[k] = __ballot(act && g.y0 <= ty && ty < g.y0 + g.h);
-      }
-#pragma unroll
-      for (int uy = 0; uy < kSB; ++uy) {
-        if (rm[uy] == 0ull) continue;
-#pragma unroll
-        for (int ux = 0; ux < kSB; ++ux) {
-          const uint64_t m = cm[ux] & rm[uy];
-          if (m == 0ull) continue;
-          const uint32_t b = __builtin_amdgcn_readlane(base, uy * kSB + ux);
-          if (__builtin_amdgcn_inverse_ballot_w64(m)) {
-            // lanes of m store their ids at b + (lanes of m below them): one run
-            const uint32_t dst = b + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-            if (dst < cap32) {
-              out_gid[dst] = (int32_t)g.gid;
-              if (WITH_TILES) out_tile[dst] = (cs.sy * kSB + uy) * TX + cs.sx * kSB + ux;
-            }
-          }
-        }
-      }
-      // lane u advances tile u's slot by its count in this step
-      uint64_t mine = 0;
-      const int ux = lane & 7, uy = lane >> 3;
-#pragma unroll
-      for (int k = 0; k < kSB; ++k) mine = ux == k ? cm[k] : mine;
-      uint64_t rmine = 0;
-#pragma unroll
-      for (int k = 0; k < kSB; ++k) rmine = uy == k ? rm[k] : rmine;
-      base += (uint32_t)__popcll(mine & rmine);
-    }
+    const uint4 d = desc[c];
+    const uint32_t cnt_c = cnt[(int64_t)c * 64 + lane];
+    if (fits)
+      write_chunk<WITH_TILES, false>(c, d, pval, n_gauss, TX, TY, cnt_c, ranges, cap32, lane, out_gid, out_tile);
+    else
+      write_chunk<WITH_TILES, true>(c, d, pval, n_gauss, TX, TY, cnt_c, ranges, cap32, lane, out_gid, out_tile);
   }
 }
 
@@ -808,7 +841,7 @@ struct BinPlan {
   int G_p;        // workgroups of the second pair pass
   int sb_passes;  // 1 when S <= 256, else 2
   size_t o_dkey, o_word, o_ka, o_wa, o_kb, o_wb, o_table, o_dtot, o_scal, o_pk0, o_pv0, o_pk1, o_pv1, o_sbr,
-      o_cbase, o_csb, o_cnt, o_tot, o_blk, total;
+      o_cbase, o_csb, o_cnt, o_desc, o_tot, o_blk, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -855,6 +888,7 @@ BinPlan make_plan(int64_t n, int width, int height, int64_t capacity) {
   P.o_cbase = take(((size_t)P.S + 1) * 4);
   P.o_csb = take((size_t)P.cmax * 4);
   P.o_cnt = take((size_t)P.cmax * 64 * 4);
+  P.o_desc = take((size_t)P.cmax * 16);
   P.o_tot = take((size_t)P.T * 4);
   P.o_blk = take((size_t)P.G_d * 2 * 4);
   P.total = o;
@@ -924,6 +958,7 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   uint32_t* cbase = (uint32_t*)(ws + P.o_cbase);
   uint32_t* csb = (uint32_t*)(ws + P.o_csb);
   uint32_t* cnt = (uint32_t*)(ws + P.o_cnt);
+  uint4* desc = (uint4*)(ws + P.o_desc);
   uint32_t* tot = (uint32_t*)(ws + P.o_tot);
   uint32_t* blk = (uint32_t*)(ws + P.o_blk);
   uint32_t* n_pairs = scal + 0;
@@ -971,20 +1006,22 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   hipLaunchKernelGGL(chunks_kernel, dim3(1), dim3(kBig), 0, s, P.S, P.sb_passes == 1, dtot, sbr, P.cmax, cbase, csb,
                      n_chunks);
   GS_LAUNCH_CHECK("chunks_kernel");
-  const int pass_blocks = 2048;
+  // one chunk per wave: the chunk count is known on the device only, so the grid covers
+  // the bound and surplus waves exit at once; waves start as others finish
+  const int pass_blocks = (int)std::min<int64_t>(div_up(P.cmax, 4), (int64_t)1 << 20);
   hipLaunchKernelGGL(tile_count_kernel, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, csb, cbase, sbr, P.S,
-                     sbval, P.SX, cnt);
+                     sbval, P.SX, cnt, desc);
   GS_LAUNCH_CHECK("tile_count_kernel");
   hipLaunchKernelGGL(chunk_scan_kernel, dim3(P.S), dim3(kBig), 0, s, cbase, P.SX, P.TX, P.TY, cnt, tot);
   GS_LAUNCH_CHECK("chunk_scan_kernel");
   hipLaunchKernelGGL(tile_scan_stats_kernel, dim3(1), dim3(kBig), 0, s, tot, P.T, blk, P.G_d, P.cap, ranges, stats);
   GS_LAUNCH_CHECK("tile_scan_stats_kernel");
   if (sorted_tiles != nullptr)
-    hipLaunchKernelGGL(tile_write_kernel<true>, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, csb, cbase, sbr,
-                       P.S, sbval, (uint32_t)n, P.SX, P.TX, P.TY, cnt, ranges, P.cap, sorted_gids, sorted_tiles);
+    hipLaunchKernelGGL(tile_write_kernel<true>, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, desc, sbval,
+                       (uint32_t)n, P.TX, P.TY, cnt, ranges, P.T, P.cap, sorted_gids, sorted_tiles);
   else
-    hipLaunchKernelGGL(tile_write_kernel<false>, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, csb, cbase, sbr,
-                       P.S, sbval, (uint32_t)n, P.SX, P.TX, P.TY, cnt, ranges, P.cap, sorted_gids, sorted_tiles);
+    hipLaunchKernelGGL(tile_write_kernel<false>, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, desc, sbval,
+                       (uint32_t)n, P.TX, P.TY, cnt, ranges, P.T, P.cap, sorted_gids, sorted_tiles);
   GS_LAUNCH_CHECK("tile_write_kernel");
   return GS_OK;
 }
