@@ -28,8 +28,9 @@
 //                      row lane masks with ballots; lane u owns tile u of the
 //                      superblock and its mask (column & row) says which Gaussians of
 //                      the step hit it.  A counting sweep gives per (chunk, tile) counts,
-//                      a per-superblock scan turns them into chunk offsets and tile
-//                      totals, one scan gives the tile ranges, and a writing
+//                      a two-level scan (segments of 16 chunks, then each superblock's
+//                      segments) turns them into chunk offsets and tile totals, one
+//                      scan gives the tile ranges, and a writing
 //                      sweep stores, tile by tile, the ids of the lanes in the tile's
 //                      mask at range + counts of earlier chunks + popcount(mask &
 //                      lanes-below): stable by construction, one contiguous run per
@@ -50,6 +51,7 @@ constexpr int kScanBlock = 256;
 constexpr int kSB = 8;                            // superblock = 8x8 tiles
 constexpr int kSBSpan = 3;                        // superblocks a Gaussian meets per axis
 constexpr int kChunk = 256;                       // Gaussians per chunk of the tile pass
+constexpr int kSeg = 16;                          // chunks per segment of the chunk-offset scan
 constexpr int kPrepBlock = 256;
 constexpr int kPrepPer = 4;                       // Gaussians per bin_prep thread
 constexpr int kSpan = kPrepBlock * kPrepPer;      // Gaussians per depth-sort workgroup
@@ -457,16 +459,21 @@ __global__ __launch_bounds__(256) void ranges_kernel(const uint32_t* __restrict_
 
 // One block: superblock ranges (from the digit totals when the pair sort had one
 // pass, digit = superblock id), chunk count per superblock -> exclusive scan ->
-// chunk_base[S+1] and the chunk -> superblock map.
+// chunk_base[S+1] and the chunk -> superblock map; likewise the superblock's segments
+// (runs of kSeg chunks, the unit of the chunk-offset scan): seg_base[S+1] and the
+// segment -> superblock map.
 __global__ __launch_bounds__(kBig) void chunks_kernel(int S, bool from_digits, const uint32_t* __restrict__ digit_tot,
                                                       int32_t* __restrict__ sb_ranges, int64_t cmax,
                                                       uint32_t* __restrict__ chunk_base,
-                                                      uint32_t* __restrict__ chunk_sb, uint32_t* __restrict__ n_chunks) {
+                                                      uint32_t* __restrict__ chunk_sb, uint32_t* __restrict__ n_chunks,
+                                                      int64_t gmax, uint32_t* __restrict__ seg_base,
+                                                      uint32_t* __restrict__ seg_sb, uint32_t* __restrict__ n_segs) {
   __shared__ uint32_t cb[kBig + 1];  // chunk bases, when S <= kBig
-  __shared__ uint32_t carry_p, carry_c;
+  __shared__ uint32_t gb[kBig + 1];  // segment bases, when S <= kBig
+  __shared__ uint32_t carry_c, carry_g;
   if (threadIdx.x == 0) {
-    carry_p = 0;
     carry_c = 0;
+    carry_g = 0;
   }
   __syncthreads();
   for (int s0 = 0; s0 < S; s0 += kBig) {
@@ -475,7 +482,7 @@ __global__ __launch_bounds__(kBig) void chunks_kernel(int S, bool from_digits, c
     if (from_digits) {  // S <= 256: one iteration
       const uint32_t c = sb < S ? digit_tot[sb] : 0u;
       uint32_t sum;
-      lo = carry_p + block_excl_scan<kBig>(c, &sum);
+      lo = block_excl_scan<kBig>(c, &sum);
       hi = lo + c;
       if (sb < S) sb_ranges[sb] = (int32_t)lo;
       if (sb == S - 1) sb_ranges[S] = (int32_t)hi;
@@ -484,29 +491,42 @@ __global__ __launch_bounds__(kBig) void chunks_kernel(int S, bool from_digits, c
       hi = (uint32_t)sb_ranges[sb + 1];
     }
     const uint32_t nc = sb < S ? (hi - lo + kChunk - 1) / kChunk : 0u;
-    uint32_t sum;
-    const uint32_t c0 = carry_c + block_excl_scan<kBig>(nc, &sum);
+    const uint32_t ng = (nc + kSeg - 1) / kSeg;
+    uint32_t sum_c, sum_g;
+    const uint32_t c0 = carry_c + block_excl_scan<kBig>(nc, &sum_c);
+    const uint32_t g0 = carry_g + block_excl_scan<kBig>(ng, &sum_g);
     if (sb < S) {
       chunk_base[sb] = c0;
+      seg_base[sb] = g0;
       if (S <= kBig) {
         cb[sb] = c0;
+        gb[sb] = g0;
       } else {
         for (uint32_t c = c0; c < c0 + nc && (int64_t)c < cmax; ++c) chunk_sb[c] = (uint32_t)sb;
+        for (uint32_t g = g0; g < g0 + ng && (int64_t)g < gmax; ++g) seg_sb[g] = (uint32_t)sb;
       }
     }
     __syncthreads();
-    if (threadIdx.x == 0) carry_c += sum;
+    if (threadIdx.x == 0) {
+      carry_c += sum_c;
+      carry_g += sum_g;
+    }
     __syncthreads();
   }
-  const uint32_t total = carry_c;
+  const uint32_t total = carry_c, total_g = carry_g;
   if (threadIdx.x == 0) {
     chunk_base[S] = total;
     *n_chunks = total;
+    seg_base[S] = total_g;
+    *n_segs = total_g;
   }
   if (S <= kBig) {
-    if (threadIdx.x == 0) cb[S] = total;
+    if (threadIdx.x == 0) {
+      cb[S] = total;
+      gb[S] = total_g;
+    }
     __syncthreads();
-    // chunk j belongs to the last superblock whose base is <= j
+    // chunk j belongs to the last superblock whose base is <= j (likewise segments)
     const uint32_t lim = (int64_t)total < cmax ? total : (uint32_t)cmax;
     for (uint32_t j = threadIdx.x; j < lim; j += kBig) {
       int lo = 0, hi = S;  // invariant: cb[lo] <= j < cb[hi]
@@ -515,6 +535,15 @@ __global__ __launch_bounds__(kBig) void chunks_kernel(int S, bool from_digits, c
         if (cb[mid] <= j) lo = mid; else hi = mid;
       }
       chunk_sb[j] = (uint32_t)lo;
+    }
+    const uint32_t glim = (int64_t)total_g < gmax ? total_g : (uint32_t)gmax;
+    for (uint32_t j = threadIdx.x; j < glim; j += kBig) {
+      int lo = 0, hi = S;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (gb[mid] <= j) lo = mid; else hi = mid;
+      }
+      seg_sb[j] = (uint32_t)lo;
     }
   }
 }
@@ -571,6 +600,7 @@ __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restr
                                                          const uint32_t* __restrict__ chunk_base,
                                                          const int32_t* __restrict__ sb_ranges, int S,
                                                          const uint64_t* __restrict__ pval, int SX,
+                                                         const uint32_t* __restrict__ seg_base,
                                                          uint32_t* __restrict__ cnt, uint4* __restrict__ desc) {
   const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
@@ -590,7 +620,9 @@ __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restr
       }
     }
     cnt[(int64_t)c * 64 + lane] = mycount;
-    if (lane == 0) desc[c] = make_uint4((uint32_t)cs.begin, (uint32_t)len, (uint32_t)cs.sx, (uint32_t)cs.sy);
+    if (lane == 0)
+      desc[c] = make_uint4((uint32_t)cs.begin, (uint32_t)len, (uint32_t)cs.sx | ((uint32_t)cs.sy << 16),
+                           seg_base[cs.s] + (c - cs.first) / kSeg);
   }
 }
 
@@ -694,24 +726,56 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
   }
 }
 
-// 4b. One block per superblock: per tile (lane), exclusive prefix of the counts over
-// the superblock's chunks, in place, and the tile's total.  16 waves split the
-// chunks into contiguous runs: run sums, a scan over the 16 runs, then a second walk
-// writes the prefixes.
-__global__ __launch_bounds__(kBig) void chunk_scan_kernel(const uint32_t* __restrict__ chunk_base, int SX, int TX,
-                                                          int TY, uint32_t* __restrict__ cnt,
+// 4b. Chunk offsets per tile (lane), in two levels so that a superblock with
+// thousands of chunks (a dense cluster) is spread over many waves: a wave per segment
+// of kSeg chunks turns the counts into exclusive prefixes within the segment (in place)
+// and writes the segment totals; then one block per superblock turns its segments'
+// totals into exclusive prefixes (in place) and writes the tile totals.  A chunk's
+// offset is the sum of its two prefixes.
+__global__ __launch_bounds__(256) void chunk_seg_kernel(const uint32_t* __restrict__ n_segs, int64_t gmax,
+                                                        const uint32_t* __restrict__ seg_sb,
+                                                        const uint32_t* __restrict__ seg_base,
+                                                        const uint32_t* __restrict__ chunk_base, int64_t cmax,
+                                                        uint32_t* __restrict__ cnt, uint32_t* __restrict__ seg_sum) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
+  const uint32_t G = (uint32_t)min<int64_t>((int64_t)*n_segs, gmax);
+  for (uint32_t g = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); g < G; g += nwaves) {
+    const uint32_t sb = seg_sb[g];
+    const int64_t c0 = (int64_t)chunk_base[sb] + (int64_t)(g - seg_base[sb]) * kSeg;
+    int64_t c1 = (int64_t)chunk_base[sb + 1];
+    c1 = c1 < c0 + kSeg ? c1 : c0 + kSeg;
+    c1 = c1 < cmax ? c1 : cmax;
+    uint32_t v[kSeg];
+#pragma unroll
+    for (int k = 0; k < kSeg; ++k) v[k] = c0 + k < c1 ? cnt[(c0 + k) * 64 + lane] : 0u;
+    uint32_t run = 0;
+#pragma unroll
+    for (int k = 0; k < kSeg; ++k) {
+      if (c0 + k < c1) cnt[(c0 + k) * 64 + lane] = run;
+      run += v[k];
+    }
+    seg_sum[(int64_t)g * 64 + lane] = run;
+  }
+}
+
+// One block per superblock over its segments: 16 waves split them into contiguous
+// runs, sum, scan the 16 run sums, then write the prefixes.
+__global__ __launch_bounds__(kBig) void chunk_scan_kernel(const uint32_t* __restrict__ seg_base, int64_t gmax,
+                                                          int SX, int TX, int TY, uint32_t* __restrict__ seg_sum,
                                                           uint32_t* __restrict__ tot) {
   constexpr int NW = kBig / 64;
   __shared__ uint32_t part[NW][64];
   const int sb = blockIdx.x;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const uint32_t c0 = chunk_base[sb], c1 = chunk_base[sb + 1];
-  const uint32_t per = (c1 - c0 + NW - 1) / NW;
-  const uint32_t a = c0 + wid * per;
-  const uint32_t b = a + per < c1 ? a + per : c1;
+  const uint32_t g0 = seg_base[sb];
+  const uint32_t g1 = (int64_t)seg_base[sb + 1] < gmax ? seg_base[sb + 1] : (uint32_t)gmax;
+  const uint32_t per = g1 > g0 ? (g1 - g0 + NW - 1) / NW : 0u;
+  const uint32_t a = g0 + wid * per < g1 ? g0 + wid * per : g1;
+  const uint32_t b = a + per < g1 ? a + per : g1;
   uint32_t sum = 0;
 #pragma unroll 8
-  for (uint32_t c = a; c < b; ++c) sum += cnt[(int64_t)c * 64 + lane];
+  for (uint32_t g = a; g < b; ++g) sum += seg_sum[(int64_t)g * 64 + lane];
   part[wid][lane] = sum;
   __syncthreads();
   if (wid == 0) {
@@ -726,9 +790,9 @@ __global__ __launch_bounds__(kBig) void chunk_scan_kernel(const uint32_t* __rest
   }
   __syncthreads();
   uint32_t run = part[wid][lane];
-  for (uint32_t c = a; c < b; ++c) {
-    const uint32_t v = cnt[(int64_t)c * 64 + lane];
-    cnt[(int64_t)c * 64 + lane] = run;
+  for (uint32_t g = a; g < b; ++g) {
+    const uint32_t v = seg_sum[(int64_t)g * 64 + lane];
+    seg_sum[(int64_t)g * 64 + lane] = run;
     run += v;
   }
 }
@@ -786,16 +850,18 @@ __device__ inline void write_step(uint64_t word, bool act, int sx, int sy, int l
 }
 
 template <bool WITH_TILES, bool CHECK>
-__device__ inline void write_chunk(uint32_t c, const uint4& d, const uint64_t* __restrict__ pval, uint32_t n_gauss,
-                                   int TX, int TY, uint32_t cnt_c, const int32_t* __restrict__ ranges, uint32_t cap32,
-                                   int lane, int32_t* __restrict__ out_gid, int32_t* __restrict__ out_tile) {
-  const int len = (int)d.y, sx = (int)d.z, sy = (int)d.w;
+__device__ inline void write_chunk(const uint4& d, const uint64_t* __restrict__ pval, uint32_t n_gauss, int TX, int TY,
+                                   uint32_t cnt_c, const uint32_t* __restrict__ seg_pre,
+                                   const int32_t* __restrict__ ranges, uint32_t cap32, int lane,
+                                   int32_t* __restrict__ out_gid, int32_t* __restrict__ out_tile) {
+  const int len = (int)d.y, sx = (int)(d.z & 0xFFFFu), sy = (int)(d.z >> 16);
   const int t = tile_of(sx, sy, lane, TX, TY);
   uint64_t wv[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) wv[k] = 64 * k + lane < len ? pval[d.x + 64 * k + lane] : 0ull;
-  // lane u: next slot of tile u (tiles outside the image never get entries)
-  uint32_t base = (t >= 0 ? (uint32_t)ranges[t] : 0u) + cnt_c;
+  // lane u: next slot of tile u (tiles outside the image never get entries): the
+  // tile's range start + the superblock's earlier segments + earlier chunks of this one
+  uint32_t base = (t >= 0 ? (uint32_t)ranges[t] : 0u) + seg_pre[(int64_t)d.w * 64 + lane] + cnt_c;
 #pragma unroll
   for (int k = 0; k < 4; ++k)
     if (64 * k < len)
@@ -808,6 +874,7 @@ __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restr
                                                          const uint4* __restrict__ desc,
                                                          const uint64_t* __restrict__ pval, uint32_t n_gauss, int TX,
                                                          int TY, const uint32_t* __restrict__ cnt,
+                                                         const uint32_t* __restrict__ seg_pre,
                                                          const int32_t* __restrict__ ranges, int T, int64_t cap,
                                                          int32_t* __restrict__ out_gid,
                                                          int32_t* __restrict__ out_tile) {
@@ -821,9 +888,9 @@ __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restr
     const uint4 d = desc[c];
     const uint32_t cnt_c = cnt[(int64_t)c * 64 + lane];
     if (fits)
-      write_chunk<WITH_TILES, false>(c, d, pval, n_gauss, TX, TY, cnt_c, ranges, cap32, lane, out_gid, out_tile);
+      write_chunk<WITH_TILES, false>(d, pval, n_gauss, TX, TY, cnt_c, seg_pre, ranges, cap32, lane, out_gid, out_tile);
     else
-      write_chunk<WITH_TILES, true>(c, d, pval, n_gauss, TX, TY, cnt_c, ranges, cap32, lane, out_gid, out_tile);
+      write_chunk<WITH_TILES, true>(d, pval, n_gauss, TX, TY, cnt_c, seg_pre, ranges, cap32, lane, out_gid, out_tile);
   }
 }
 
@@ -834,14 +901,14 @@ __global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
 
 // ---------------------------------------------------------------------------------
 struct BinPlan {
-  int64_t n, cap, pcap, cmax;
+  int64_t n, cap, pcap, cmax, gmax;
   int T, TX, TY, SX, SY, S;
   int G_d;        // depth-sort workgroups (= bin_prep blocks)
   int G_q;        // workgroups of the first superblock pass
   int G_p;        // workgroups of the second pair pass
   int sb_passes;  // 1 when S <= 256, else 2
   size_t o_dkey, o_word, o_ka, o_wa, o_kb, o_wb, o_table, o_dtot, o_scal, o_pk0, o_pv0, o_pk1, o_pv1, o_sbr,
-      o_cbase, o_csb, o_cnt, o_desc, o_tot, o_blk, total;
+      o_cbase, o_csb, o_cnt, o_desc, o_tot, o_blk, o_gbase, o_gsb, o_gsum, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -860,6 +927,7 @@ BinPlan make_plan(int64_t n, int width, int height, int64_t capacity) {
   const int64_t nn = std::max<int64_t>(n, 1);
   P.pcap = (int64_t)kSBSpan * kSBSpan * nn;
   P.cmax = (P.pcap + kChunk - 1) / kChunk + P.S;
+  P.gmax = (P.cmax + kSeg - 1) / kSeg + P.S;
   P.G_d = (int)((nn + kSpan - 1) / kSpan);
   P.G_q = (int)((nn + kPairSpan - 1) / kPairSpan);
   P.G_p = (int)std::min<int64_t>(8192, std::max<int64_t>(1, (2 * nn + 1023) / 1024));
@@ -891,6 +959,9 @@ BinPlan make_plan(int64_t n, int width, int height, int64_t capacity) {
   P.o_desc = take((size_t)P.cmax * 16);
   P.o_tot = take((size_t)P.T * 4);
   P.o_blk = take((size_t)P.G_d * 2 * 4);
+  P.o_gbase = take(((size_t)P.S + 1) * 4);
+  P.o_gsb = take((size_t)P.gmax * 4);
+  P.o_gsum = take((size_t)P.gmax * 64 * 4);
   P.total = o;
   return P;
 }
@@ -961,8 +1032,12 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   uint4* desc = (uint4*)(ws + P.o_desc);
   uint32_t* tot = (uint32_t*)(ws + P.o_tot);
   uint32_t* blk = (uint32_t*)(ws + P.o_blk);
+  uint32_t* gbase = (uint32_t*)(ws + P.o_gbase);
+  uint32_t* gsb = (uint32_t*)(ws + P.o_gsb);
+  uint32_t* gsum = (uint32_t*)(ws + P.o_gsum);
   uint32_t* n_pairs = scal + 0;
   uint32_t* n_chunks = scal + 1;
+  uint32_t* n_segs = scal + 2;
 
   if (n == 0) {
     hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, s, stats, (int64_t)GS_NUM_STATS, 0);
@@ -1004,24 +1079,27 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   }
   // 4. tile pass
   hipLaunchKernelGGL(chunks_kernel, dim3(1), dim3(kBig), 0, s, P.S, P.sb_passes == 1, dtot, sbr, P.cmax, cbase, csb,
-                     n_chunks);
+                     n_chunks, P.gmax, gbase, gsb, n_segs);
   GS_LAUNCH_CHECK("chunks_kernel");
   // one chunk per wave: the chunk count is known on the device only, so the grid covers
   // the bound and surplus waves exit at once; waves start as others finish
   const int pass_blocks = (int)std::min<int64_t>(div_up(P.cmax, 4), (int64_t)1 << 20);
   hipLaunchKernelGGL(tile_count_kernel, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, csb, cbase, sbr, P.S,
-                     sbval, P.SX, cnt, desc);
+                     sbval, P.SX, gbase, cnt, desc);
   GS_LAUNCH_CHECK("tile_count_kernel");
-  hipLaunchKernelGGL(chunk_scan_kernel, dim3(P.S), dim3(kBig), 0, s, cbase, P.SX, P.TX, P.TY, cnt, tot);
+  hipLaunchKernelGGL(chunk_seg_kernel, dim3(div_up(P.gmax, 4)), dim3(256), 0, s, n_segs, P.gmax, gsb, gbase, cbase,
+                     P.cmax, cnt, gsum);
+  GS_LAUNCH_CHECK("chunk_seg_kernel");
+  hipLaunchKernelGGL(chunk_scan_kernel, dim3(P.S), dim3(kBig), 0, s, gbase, P.gmax, P.SX, P.TX, P.TY, gsum, tot);
   GS_LAUNCH_CHECK("chunk_scan_kernel");
   hipLaunchKernelGGL(tile_scan_stats_kernel, dim3(1), dim3(kBig), 0, s, tot, P.T, blk, P.G_d, P.cap, ranges, stats);
   GS_LAUNCH_CHECK("tile_scan_stats_kernel");
   if (sorted_tiles != nullptr)
     hipLaunchKernelGGL(tile_write_kernel<true>, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, desc, sbval,
-                       (uint32_t)n, P.TX, P.TY, cnt, ranges, P.T, P.cap, sorted_gids, sorted_tiles);
+                       (uint32_t)n, P.TX, P.TY, cnt, gsum, ranges, P.T, P.cap, sorted_gids, sorted_tiles);
   else
     hipLaunchKernelGGL(tile_write_kernel<false>, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, desc, sbval,
-                       (uint32_t)n, P.TX, P.TY, cnt, ranges, P.T, P.cap, sorted_gids, sorted_tiles);
+                       (uint32_t)n, P.TX, P.TY, cnt, gsum, ranges, P.T, P.cap, sorted_gids, sorted_tiles);
   GS_LAUNCH_CHECK("tile_write_kernel");
   return GS_OK;
 }
