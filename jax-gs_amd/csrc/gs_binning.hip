@@ -626,29 +626,56 @@ __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restr
   }
 }
 
-// 4c + 5. One block: ranges = exclusive scan of the tile totals (each thread a
-// contiguous run of tiles), and the stats.
+// 4c + 5. One block: ranges = exclusive scan of the tile totals, and the stats.  Rounds
+// of 8192 tiles: coalesced loads into LDS, each thread scans 8 consecutive tiles from
+// LDS (row stride 9: no bank conflicts), a block scan, prefixes back through LDS and
+// coalesced stores.
 __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* __restrict__ tot, int T,
                                                                const uint32_t* __restrict__ blkstat, int nblk,
                                                                int64_t cap, int32_t* __restrict__ ranges,
                                                                int32_t* __restrict__ stats) {
+  constexpr int kPer = 8, kRound = kBig * kPer;
+  __shared__ uint32_t stage[kBig * (kPer + 1)];
   __shared__ int64_t red[7][kBig / 64];
+  const int tid = threadIdx.x;
   int64_t acc[7] = {0, 0, 0, 0, 0, 0, 0};  // max, ovf tiles, ovf inter, trunc tiles, trunc inter, cap, neg
-  // the loads of a group are issued together (the values were written by other XCDs)
-  constexpr int kGroup = 8;
-  const int per = (T + kBig - 1) / kBig;
-  const int t0 = threadIdx.x * per;
-  uint32_t run = 0;
-  for (int g0 = 0; g0 < per; g0 += kGroup) {
-    uint32_t v[kGroup];
+  uint32_t carry = 0;
+  // blkstat loads first: they are independent of the tile rounds
+  uint32_t s5 = 0, s6 = 0;
+  for (int b0 = 0; b0 < nblk; b0 += 4 * kBig) {
+    uint32_t a[4], z[4];
 #pragma unroll
-    for (int k = 0; k < kGroup; ++k) {
-      const int t = t0 + g0 + k;
-      v[k] = (g0 + k < per && t < T) ? tot[t] : 0u;
+    for (int k = 0; k < 4; ++k) {
+      const int b = b0 + k * kBig + tid;
+      a[k] = b < nblk ? blkstat[2 * b] : 0u;
+      z[k] = b < nblk ? blkstat[2 * b + 1] : 0u;
     }
 #pragma unroll
-    for (int k = 0; k < kGroup; ++k) {
-      const uint32_t c = v[k];
+    for (int k = 0; k < 4; ++k) {
+      s5 += a[k];
+      s6 += z[k];
+    }
+  }
+  acc[5] = s5;
+  acc[6] = s6;
+  for (int r0 = 0; r0 < T; r0 += kRound) {
+    uint32_t v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int p = tid + kBig * k, t = r0 + p;
+      v[k] = t < T ? tot[t] : 0u;
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int p = tid + kBig * k;
+      stage[(p / kPer) * (kPer + 1) + p % kPer] = v[k];
+    }
+    __syncthreads();
+    uint32_t w[kPer], run = 0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const uint32_t c = stage[tid * (kPer + 1) + i];
+      w[i] = c;
       run += c;
       acc[0] = acc[0] > (int64_t)c ? acc[0] : (int64_t)c;
       acc[1] += c > (uint32_t)kBlock;
@@ -656,60 +683,40 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
       acc[3] += c > (uint32_t)kMaxTileEntries;
       acc[4] += c > (uint32_t)kMaxTileEntries ? c - kMaxTileEntries : 0;
     }
-  }
-  {
-    uint32_t s5 = 0, s6 = 0;
-    for (int b0 = 0; b0 < nblk; b0 += 4 * kBig) {
-      uint32_t a[4], z[4];
+    uint32_t round_total;
+    uint32_t pos = carry + block_excl_scan<kBig>(run, &round_total);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int b = b0 + k * kBig + (int)threadIdx.x;
-        a[k] = b < nblk ? blkstat[2 * b] : 0u;
-        z[k] = b < nblk ? blkstat[2 * b + 1] : 0u;
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        s5 += a[k];
-        s6 += z[k];
-      }
+    for (int i = 0; i < kPer; ++i) {
+      stage[tid * (kPer + 1) + i] = pos;
+      pos += w[i];
     }
-    acc[5] = s5;
-    acc[6] = s6;
-  }
-  uint32_t total;
-  uint32_t pos = block_excl_scan<kBig>(run, &total);
-  for (int g0 = 0; g0 < per; g0 += kGroup) {
-    uint32_t v[kGroup];
+    __syncthreads();
 #pragma unroll
-    for (int k = 0; k < kGroup; ++k) {
-      const int t = t0 + g0 + k;
-      v[k] = (g0 + k < per && t < T) ? tot[t] : 0u;
+    for (int k = 0; k < kPer; ++k) {
+      const int p = tid + kBig * k, t = r0 + p;
+      if (t < T) ranges[t] = (int32_t)stage[(p / kPer) * (kPer + 1) + p % kPer];
     }
-#pragma unroll
-    for (int k = 0; k < kGroup; ++k) {
-      const int t = t0 + g0 + k;
-      if (g0 + k < per && t < T) ranges[t] = (int32_t)pos;
-      pos += v[k];
-    }
+    carry += round_total;
+    __syncthreads();  // the stage is rewritten by the next round
   }
   // reduce the 7 accumulators over the block
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int lane = tid & 63, wid = tid >> 6;
 #pragma unroll
   for (int k = 0; k < 7; ++k) {
-    int64_t v = acc[k];
+    int64_t x = acc[k];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
-      const int64_t w = __shfl_xor(v, o, 64);
-      v = k == 0 ? (v > w ? v : w) : v + w;
+      const int64_t y = __shfl_xor(x, o, 64);
+      x = k == 0 ? (x > y ? x : y) : x + y;
     }
-    if (lane == 0) red[k][wid] = v;
+    if (lane == 0) red[k][wid] = x;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     int64_t r[7] = {0, 0, 0, 0, 0, 0, 0};
     for (int w = 0; w < kBig / 64; ++w)
       for (int k = 0; k < 7; ++k) r[k] = k == 0 ? (r[0] > red[0][w] ? r[0] : red[0][w]) : r[k] + red[k][w];
-    const int64_t m = total;
+    const int64_t m = carry;
     ranges[T] = (int32_t)m;
     for (int k = 0; k < GS_NUM_STATS; ++k) stats[k] = 0;
     stats[GS_STAT_N_INTERACTIONS] = (int32_t)m;
