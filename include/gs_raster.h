@@ -66,7 +66,7 @@ extern "C" {
 const char* gs_last_error(void);
 /* 2: gs_composite_fwd/bwd take the tile order; gs_mse_loss, gs_l1_ssim, gs_adam_step,
  * gs_densify_and_prune, gs_reset_opacities, gs_ply_pack/unpack, gs_preprocess_bwd_adam,
- * gs_l1_ssim_terms. */
+ * gs_l1_ssim_terms.  3: gs_l1_loss_bwd, gs_mse_loss_bwd. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -178,6 +178,14 @@ int gs_l1_loss(void* stream, int64_t count, const float* pred, const float* targ
  * 2 (pred - target) / count.  Replaces jax_gs/training/losses.py:10-14 (mse_loss). */
 int gs_mse_loss(void* stream, int64_t count, const float* pred, const float* target,
                 float* loss, float* grad);
+
+/* VJP of gs_l1_loss / gs_mse_loss for a loss cotangent grad_out[0] on the device
+ * (losses.py:4-14 under jax.grad): grad = sign(pred - target) * (g / count), or
+ * 2 (pred - target) * (g / count).  One pass, no reduction. */
+int gs_l1_loss_bwd(void* stream, int64_t count, const float* pred, const float* target, const float* grad_out,
+                   float* grad);
+int gs_mse_loss_bwd(void* stream, int64_t count, const float* pred, const float* target, const float* grad_out,
+                    float* grad);
 
 /* Workspace bytes of gs_l1_ssim / gs_l1_ssim_bwd for an image of height x width x
  * channels (0 for a bad shape). */

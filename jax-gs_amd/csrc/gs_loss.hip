@@ -4,6 +4,8 @@
 // losses.py:10-14, mse_loss = mean((pred - target)^2), seed 2 (pred - target) / count.
 #include "gs_common.h"
 
+#include <algorithm>
+
 namespace gs {
 namespace {
 
@@ -53,6 +55,28 @@ __global__ __launch_bounds__(256) void loss_kernel(int64_t count, bool vec, cons
   if (threadIdx.x == 0) atomicAdd(loss, ((ws[0] + ws[1]) + (ws[2] + ws[3])) * inv_count);
 }
 
+// The VJP with the loss cotangent g on the device: grad = seed(d) * (g / count), the
+// reference's order (the mean's VJP divides g by the count, the elementwise VJP then
+// multiplies by the seed).  One pass: reads both images, writes the gradient.
+template <bool SQ>
+__global__ __launch_bounds__(256) void loss_bwd_kernel(int64_t count, bool vec, const float* __restrict__ pred,
+                                                     const float* __restrict__ target, const float* __restrict__ gout,
+                                                     float* __restrict__ grad) {
+  const float sc = gout[0] / (float)count;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nq = vec ? count >> 2 : 0;
+  const float4* __restrict__ p4 = reinterpret_cast<const float4*>(pred);
+  const float4* __restrict__ t4 = reinterpret_cast<const float4*>(target);
+  float4* __restrict__ g4 = reinterpret_cast<float4*>(grad);
+  for (int64_t q = tid; q < nq; q += stride) {
+    const float4 a = p4[q], b = t4[q];
+    g4[q] = make_float4(seed<SQ>(a.x - b.x) * sc, seed<SQ>(a.y - b.y) * sc, seed<SQ>(a.z - b.z) * sc,
+                        seed<SQ>(a.w - b.w) * sc);
+  }
+  for (int64_t i = 4 * nq + tid; i < count; i += stride) grad[i] = seed<SQ>(pred[i] - target[i]) * sc;
+}
+
 }  // namespace
 }  // namespace gs
 
@@ -76,7 +100,29 @@ int mean_loss(const char* name, void* stream, int64_t count, const float* pred, 
   GS_LAUNCH_CHECK("loss_kernel");
   return GS_OK;
 }
+template <bool SQ>
+int mean_loss_bwd(const char* name, void* stream, int64_t count, const float* pred, const float* target,
+                  const float* grad_out, float* grad) {
+  GS_REQUIRE(count > 0, "%s: count must be > 0", name);
+  GS_REQUIRE(pred && target && grad_out && grad, "%s: NULL argument", name);
+  const bool vec = ((uintptr_t)pred | (uintptr_t)target | (uintptr_t)grad) % 16 == 0;
+  const int blocks = (int)std::min<int64_t>(div_up(vec ? (count + 3) / 4 : count, 256), 8192);
+  hipLaunchKernelGGL(loss_bwd_kernel<SQ>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, count, vec, pred, target,
+                     grad_out, grad);
+  GS_LAUNCH_CHECK("loss_bwd_kernel");
+  return GS_OK;
+}
 }  // namespace
+
+extern "C" int gs_l1_loss_bwd(void* stream, int64_t count, const float* pred, const float* target,
+                              const float* grad_out, float* grad) {
+  return mean_loss_bwd<false>("gs_l1_loss_bwd", stream, count, pred, target, grad_out, grad);
+}
+
+extern "C" int gs_mse_loss_bwd(void* stream, int64_t count, const float* pred, const float* target,
+                               const float* grad_out, float* grad) {
+  return mean_loss_bwd<true>("gs_mse_loss_bwd", stream, count, pred, target, grad_out, grad);
+}
 
 extern "C" int gs_l1_loss(void* stream, int64_t count, const float* pred, const float* target, float* loss,
                           float* grad) {

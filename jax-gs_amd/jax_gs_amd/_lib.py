@@ -42,6 +42,8 @@ _SIGS = {
     "gs_preprocess_bwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P, _P],
     "gs_l1_loss": [_P, _I64, _P, _P, _P, _P],
     "gs_mse_loss": [_P, _I64, _P, _P, _P, _P],
+    "gs_l1_loss_bwd": [_P, _I64, _P, _P, _P, _P],
+    "gs_mse_loss_bwd": [_P, _I64, _P, _P, _P, _P],
     "gs_l1_ssim_workspace_size": [_I, _I, _I],
     "gs_l1_ssim": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _SZ],
     "gs_l1_ssim_bwd": [_P, _I, _I, _I, _P, _P, _P, _P, _SZ, _P],
@@ -64,7 +66,7 @@ _RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_
 _lib = None
 
 
-ABI_VERSION = 2  # gs_abi_version() of the signatures bound below
+ABI_VERSION = 3  # gs_abi_version() of the signatures bound below
 
 
 class NativeLibraryMissing(RuntimeError):

@@ -14,21 +14,28 @@ from .. import _lib
 
 
 class _MeanLoss(torch.autograd.Function):
+    """Forward: the mean only.  Backward: one kernel writes seed(pred - target) * (g / count)
+    with the loss cotangent g read on the device (no host sync, no separate scaling pass)."""
+
     @staticmethod
     def forward(ctx, pred, target, entry):
         pred = pred.contiguous()
         target = target.contiguous()
         loss = torch.empty((), dtype=torch.float32, device=pred.device)
-        grad = torch.empty_like(pred)
         _lib.call(entry, _lib.stream_handle(pred.device), pred.numel(), _lib.ptr(pred), _lib.ptr(target),
-                  _lib.ptr(loss), _lib.ptr(grad))
-        ctx.save_for_backward(grad)
+                  _lib.ptr(loss), None)
+        ctx.save_for_backward(pred, target)
+        ctx.entry = entry
         return loss
 
     @staticmethod
     def backward(ctx, g):
-        (grad,) = ctx.saved_tensors
-        return grad * g, None, None
+        pred, target = ctx.saved_tensors
+        g = g.to(device=pred.device, dtype=torch.float32).contiguous()
+        grad = torch.empty_like(pred)
+        _lib.call(ctx.entry + "_bwd", _lib.stream_handle(pred.device), pred.numel(), _lib.ptr(pred),
+                  _lib.ptr(target), _lib.ptr(g), _lib.ptr(grad))
+        return grad, None, None
 
 
 def _check(name, pred, target):

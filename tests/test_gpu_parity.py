@@ -205,6 +205,28 @@ def test_l1_loss(cuda, shape, offset):
     np.testing.assert_array_equal(_np(pred.grad), seed)
 
 
+@pytest.mark.parametrize("kind", ["l1", "mse"])
+def test_loss_vjp_with_cotangent(cuda, kind):
+    """The loss VJP reads the cotangent on the device: (2.5 * loss).backward() gives
+    seed(pred - target) * (2.5 / count), the mean's VJP dividing the cotangent by the
+    count first (losses.py:4-14 under jax.grad), bit for bit in float32."""
+    from jax_gs_amd.training.losses import l1_loss, mse_loss
+
+    rng = np.random.default_rng(11)
+    shape = (45, 67, 3)
+    p_np = rng.uniform(0, 1, shape).astype(np.float32)
+    t_np = rng.uniform(0, 1, shape).astype(np.float32)
+    t_np[3, 4, 1] = p_np[3, 4, 1]
+    pred = torch.from_numpy(p_np).to(cuda).requires_grad_(True)
+    tgt = torch.from_numpy(t_np).to(cuda)
+    loss = (l1_loss if kind == "l1" else mse_loss)(pred, tgt)
+    (2.5 * loss).backward()
+    d = p_np - t_np
+    sc = np.float32(2.5) / np.float32(d.size)
+    want = (np.sign(d) if kind == "l1" else np.float32(2.0) * d).astype(np.float32) * sc
+    np.testing.assert_array_equal(_np(pred.grad), want.astype(np.float32))
+
+
 def test_background_forward_and_grad(cuda):
     """A coloured background (rasterizer.py:244, C + T * bg) and its cotangent."""
     sc = scenes.make_scene(1, n=4000, width=200, height=150)
