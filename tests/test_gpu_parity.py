@@ -140,9 +140,10 @@ def test_cfg1_full_fwd_bwd(cuda):
         assert _rel(_np(getattr(g, f).grad), gr_o[f]) <= GRAD_TOL, f
 
 
-@pytest.mark.parametrize("cfg,n,w,h", [(1, 20000, 4400, 2600), (3, 30000, 2100, 2100)])
+@pytest.mark.parametrize("cfg,n,w,h", [(1, 20000, 4400, 2600), (3, 30000, 2100, 2100), (1, 20000, 5200, 5200)])
 def test_binning_large_image(cuda, cfg, n, w, h):
-    """Images with more than 256 superblocks of 8x8 tiles (two-pass superblock sort)."""
+    """Images with more than 256 superblocks of 8x8 tiles (two-pass superblock sort); the
+    5200x5200 case has more than 1024 (chunk and segment maps filled per superblock)."""
     sc = scenes.make_scene(cfg, n=n, width=w, height=h)
     pre, pre_o = _check_preprocess(sc, cuda)
     b, _ = _check_binning(sc, cuda, pre, pre_o)
