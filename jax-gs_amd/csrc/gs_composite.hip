@@ -303,7 +303,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
   const float ry0 = (float)(ty * kTile + part * 4 * PPT) + 0.5f, ry1 = ry0 + (float)(4 * PPT - 1);
 
   bool done = false;
-  int walked = 0;
+  int walked = 0, next_check = 8;
   int g_ahead = probe_gid(gids, start, 64 + lane, n, num_g);
   Probe p_next = probe_load(rec, probe_gid(gids, start, lane, n, num_g));
   for (int b0 = 0; b0 < n && !done; b0 += 64) {
@@ -312,15 +312,29 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
     g_ahead = probe_gid(gids, start, b0 + 128 + lane, n, num_g);
     const int gl = pr.g;
     uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
-    Rec nxt = zero_rec();
-    int jn = 0;
-    if (m != 0ull) {
-      jn = __builtin_ctzll(m);
-      nxt = load_rec(rec, bcast_i(gl, jn));
+    // Survivors are walked in groups of G (G = 2 when a lane holds one pixel): the
+    // group's records are in SGPRs before it is blended and the next group's scalar
+    // loads are issued first, so their latency is covered by G entries' arithmetic
+    // (scalar loads complete out of order: waiting for one is waiting for all, so
+    // requests go out per group).  With four pixels per lane the arithmetic of one
+    // entry already covers the load and G = 1 keeps the instruction count down.
+    constexpr int G = PPT == 1 ? 2 : 1;
+    Rec r[G];
+    int j[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      r[h] = zero_rec();
+      j[h] = -1;
+      if (m != 0ull) {
+        j[h] = __builtin_ctzll(m);
+        m &= m - 1ull;
+        r[h] = load_rec(rec, bcast_i(gl, j[h]));
+      }
     }
-    while (m != 0ull) {
+    while (j[0] >= 0) {
       // every 8 walked entries: stop when no pixel of the wave is still open
-      if (walked != 0 && (walked & 7) == 0) {
+      if (walked >= next_check) {
+        next_check = walked + 8;
         bool live = false;
 #pragma unroll
         for (int i = 0; i < PPT; ++i) live = live || Tr[i] > kTMin;
@@ -329,29 +343,40 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
           break;
         }
       }
-      ++walked;
-      const Rec e = nxt;
-      const int kk = b0 + jn + 1;  // entries met so far, this one included
-      m &= m - 1ull;
-      if (m != 0ull) {
-        jn = __builtin_ctzll(m);
-        nxt = load_rec(rec, bcast_i(gl, jn));
-      }
-      const float dx = px - e.mx;
-      const float Adx2l = fmaf(e.A * dx, dx, e.lop), Bdx = e.B * dx;
+      Rec e[G];
+      int k[G];
 #pragma unroll
-      for (int i = 0; i < PPT; ++i) {
-        const float q = q_of(py[i] - e.my, Adx2l, Bdx, e.C);
-        const bool act = Tr[i] > kTMin;  // rasterizer.py:206
-        float al = __builtin_amdgcn_exp2f(q);
-        al = al < 0.99f ? al : 0.99f;
-        al = (act && q > e.thr) ? al : 0.0f;  // rasterizer.py:212
-        const float w = al * Tr[i];
-        c0[i] = fmaf(w, e.r, c0[i]);
-        c1[i] = fmaf(w, e.g, c1[i]);
-        c2[i] = fmaf(w, e.b, c2[i]);
-        Tr[i] = Tr[i] - w;  // T (1 - alpha)
-        cnt[i] = act ? kk : cnt[i];
+      for (int h = 0; h < G; ++h) {
+        e[h] = r[h];
+        k[h] = j[h];
+        j[h] = -1;
+        if (m != 0ull) {
+          j[h] = __builtin_ctzll(m);
+          m &= m - 1ull;
+          r[h] = load_rec(rec, bcast_i(gl, j[h]));
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        if (k[h] < 0) break;
+        ++walked;
+        const int kk = b0 + k[h] + 1;  // entries met so far, this one included
+        const float dx = px - e[h].mx;
+        const float Adx2l = fmaf(e[h].A * dx, dx, e[h].lop), Bdx = e[h].B * dx;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+          const float q = q_of(py[i] - e[h].my, Adx2l, Bdx, e[h].C);
+          const bool act = Tr[i] > kTMin;  // rasterizer.py:206
+          float al = __builtin_amdgcn_exp2f(q);
+          al = al < 0.99f ? al : 0.99f;
+          al = (act && q > e[h].thr) ? al : 0.0f;  // rasterizer.py:212
+          const float w = al * Tr[i];
+          c0[i] = fmaf(w, e[h].r, c0[i]);
+          c1[i] = fmaf(w, e[h].g, c1[i]);
+          c2[i] = fmaf(w, e[h].b, c2[i]);
+          Tr[i] = Tr[i] - w;  // T (1 - alpha)
+          cnt[i] = act ? kk : cnt[i];
+        }
       }
     }
   }
