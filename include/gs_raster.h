@@ -66,7 +66,8 @@ extern "C" {
 const char* gs_last_error(void);
 /* 2: gs_composite_fwd/bwd take the tile order; gs_mse_loss, gs_l1_ssim, gs_adam_step,
  * gs_densify_and_prune, gs_reset_opacities, gs_ply_pack/unpack, gs_preprocess_bwd_adam,
- * gs_l1_ssim_terms.  3: gs_l1_loss_bwd, gs_mse_loss_bwd. */
+ * gs_l1_ssim_terms.  3: gs_l1_loss_bwd, gs_mse_loss_bwd.  4: gs_composite_fwd takes
+ * clear_records, gs_composite_bwd accumulate. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -125,20 +126,25 @@ int gs_tile_ranges(void* stream, const int32_t* sorted_tiles, int64_t length, in
  * does).  Per pixel it also writes the final
  * transmittance final_T[H,W] and n_contrib[H,W] = number of leading entries blended
  * while T > 1e-4, and tile_order[T] = the tiles sorted by decreasing walk length, the
- * launch order of gs_composite_bwd (residuals for gs_composite_bwd; each may be NULL). */
+ * launch order of gs_composite_bwd (residuals for gs_composite_bwd; each may be NULL).
+ * clear_records (may be NULL): an [n, GS_REC_STRIDE] array the launch sets to zero on
+ * the side (its waves are arithmetic-bound, so the stores cost nothing), for a later
+ * gs_composite_bwd with accumulate = 1. */
 int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                      int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
-                     float* image, float* final_T, int32_t* n_contrib, int32_t* tile_order);
+                     float* image, float* final_T, int32_t* n_contrib, int32_t* tile_order, float* clear_records);
 
 /* Vector-Jacobian product of gs_composite_fwd (JAX autodiff of render_tiles).
  * tile_order is the forward's (NULL: a fixed order; results agree up to the order of
- * floating-point additions).  grad_records[N,GS_REC_STRIDE] is overwritten with the
- * gradient record (layout above); grad_background[3] (may be NULL) with
- * dL/d(background). */
+ * floating-point additions).  grad_records[N,GS_REC_STRIDE] receives the gradient
+ * record (layout above): overwritten when accumulate = 0, added to what it holds when
+ * accumulate = 1 (records cleared by gs_composite_fwd's clear_records, or gradients of
+ * several views summed in one buffer); grad_background[3] (may be NULL) is overwritten
+ * with dL/d(background). */
 int gs_composite_bwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                      int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
                      const float* grad_image, const float* final_T, const int32_t* n_contrib,
-                     const int32_t* tile_order, float* grad_records, float* grad_background);
+                     const int32_t* tile_order, float* grad_records, float* grad_background, int accumulate);
 
 /* Vector-Jacobian product of gs_preprocess_fwd's compositing records with respect to
  * the five Gaussian parameter arrays (JAX autodiff of project_gaussians, eval_sh,

@@ -276,11 +276,24 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
     float* __restrict__ img, float* __restrict__ finalT, int32_t* __restrict__ ncontrib,
-    int32_t* __restrict__ tile_cost) {
+    int32_t* __restrict__ tile_cost, float4* __restrict__ clear, int64_t n_clear) {
   constexpr int WPT = 4 / PPT;  // waves per tile
+  // Every workgroup clears its slice of the caller's array after its own outputs (stores
+  // and loads share one wait counter, so stores issued before the walk would hold up its
+  // first loads).
+  auto clear_slice = [&]() {
+    if (clear != nullptr) {
+      const int64_t per = (n_clear + gridDim.x - 1) / gridDim.x;
+      const int64_t c0 = per * blockIdx.x, c1 = c0 + per < n_clear ? c0 + per : n_clear;
+      for (int64_t c = c0 + threadIdx.x; c < c1; c += 64) clear[c] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  };
   const int b = blockIdx.x / WPT, part = blockIdx.x % WPT;
   const int tile = tile_of_block(b, T);
-  if (tile >= T) return;
+  if (tile >= T) {
+    clear_slice();
+    return;
+  }
   const int lane = threadIdx.x;
   const int tx = tile % TX, ty = tile / TX;
   const int X = tx * kTile + (lane & 15);
@@ -396,6 +409,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
   }
   // walk length of the tile (first wave of the tile): the backward's cost estimate
   if (tile_cost && part == 0 && lane == 0) tile_cost[tile] = walked;
+  clear_slice();
 }
 
 template <int PPT>
@@ -645,7 +659,7 @@ using namespace gs;
 extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                                 int64_t n_entries, const int32_t* ranges, int width, int height,
                                 const float* background, float* image, float* final_T, int32_t* n_contrib,
-                                int32_t* tile_order) {
+                                int32_t* tile_order, float* clear_records) {
   GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "gs_composite_fwd: n out of range");
   GS_REQUIRE(n_entries >= 0, "gs_composite_fwd: n_entries must be >= 0");
   GS_REQUIRE(width > 0 && height > 0, "gs_composite_fwd: bad image size %dx%d", width, height);
@@ -655,14 +669,17 @@ extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, c
   const int T = TX * TY;
   const int nblk = ((T + 7) / 8) * 8;
   hipStream_t s = (hipStream_t)stream;
+  GS_REQUIRE(clear_records == nullptr || ((uintptr_t)clear_records & 15) == 0,
+             "gs_composite_fwd: clear_records must be 16-byte aligned");
+  const int64_t n4_clear = clear_records ? n * kRec / 4 : 0;  // kRec = 12: whole float4s
   if (pick_ppt(T) == 4) {
     hipLaunchKernelGGL(composite_fwd_kernel<4>, dim3(nblk), dim3(64), 0, s, (const float4*)records, (int)n,
                        sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib,
-                       tile_order);
+                       tile_order, (float4*)clear_records, n4_clear);
   } else {
     hipLaunchKernelGGL(composite_fwd_kernel<1>, dim3(nblk * 4), dim3(64), 0, s, (const float4*)records, (int)n,
                        sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib,
-                       tile_order);
+                       tile_order, (float4*)clear_records, n4_clear);
   }
   GS_LAUNCH_CHECK("composite_fwd_kernel");
   if (tile_order) {
@@ -676,7 +693,7 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
                                 int64_t n_entries, const int32_t* ranges, int width, int height,
                                 const float* background, const float* grad_image, const float* final_T,
                                 const int32_t* n_contrib, const int32_t* tile_order, float* grad_records,
-                                float* grad_background) {
+                                float* grad_background, int accumulate) {
   GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "gs_composite_bwd: n out of range");
   GS_REQUIRE(n_entries >= 0, "gs_composite_bwd: n_entries must be >= 0");
   GS_REQUIRE(width > 0 && height > 0, "gs_composite_bwd: bad image size %dx%d", width, height);
@@ -684,9 +701,10 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
   GS_REQUIRE(n == 0 || n_entries == 0 || (records && sorted_gids && grad_records),
              "gs_composite_bwd: NULL records/gids");
   hipStream_t s = (hipStream_t)stream;
-  if (n > 0 || grad_background) {
-    hipLaunchKernelGGL(zero_grads_kernel, dim3(1024), dim3(256), 0, s, (float4*)grad_records, n * kRec / 4,
-                       grad_background);
+  if ((n > 0 && !accumulate) || grad_background) {
+    // clears the records unless accumulating, and the background cotangent
+    hipLaunchKernelGGL(zero_grads_kernel, dim3(accumulate ? 1 : 1024), dim3(256), 0, s, (float4*)grad_records,
+                       accumulate ? (int64_t)0 : n * kRec / 4, grad_background);
     GS_LAUNCH_CHECK("zero_grads_kernel");
   }
   if (grad_background) {

@@ -93,10 +93,12 @@ def composite_records(means2D, cov2D, opacities, colors) -> torch.Tensor:
 
 
 def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Tensor, H: int, W: int,
-              background: torch.Tensor, residuals: bool = True):
+              background: torch.Tensor, residuals: bool = True, clear_records: torch.Tensor | None = None):
     """Front-to-back compositing; returns (image [H,W,3], final_T [H,W], n_contrib [H,W],
     tile_order [T]), the last three the backward's residuals (None unless residuals):
-    tile_order lists the tiles longest walk first, the backward's launch order."""
+    tile_order lists the tiles longest walk first, the backward's launch order.
+    clear_records ([n, GS_REC_STRIDE] float32), when given, is set to zero by the same launch
+    (for a backward that accumulates into it)."""
     dev = records.device
     _, _, T = num_tiles(W, H)
     image = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
@@ -105,7 +107,7 @@ def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Te
     order = torch.empty((T,), dtype=torch.int32, device=dev) if residuals else None
     _lib.call("gs_composite_fwd", _lib.stream_handle(dev), records.shape[0], _lib.ptr(records),
               _lib.ptr(sorted_gids), sorted_gids.shape[0], _lib.ptr(ranges), int(W), int(H), _lib.ptr(background), _lib.ptr(image),
-              _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order))
+              _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(clear_records))
     return image, fT, nc, order
 
 

@@ -34,12 +34,19 @@ class _Render(torch.autograd.Function):
         pre = preprocess(g, cam, mask=mask, sh_degree=sh_degree, records=True)
         b = bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W, capacity=capacity,
                           want_tiles=False)
-        image, fT, nc, order = composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg, residuals=True)
+        # the gradient records the backward accumulates into, cleared by the forward's
+        # compositing launch (its waves are arithmetic-bound: the stores are free)
+        n = means.shape[0]
+        grec = (torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=means.device)
+                if any(ctx.needs_input_grad[:5]) else None)
+        image, fT, nc, order = composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg, residuals=True,
+                                         clear_records=grec)
         ctx.static = static
+        ctx.grec_fresh = grec is not None
         # radii, valid and stats carry no gradient: no zero cotangents for them
         ctx.set_materialize_grads(False)
         ctx.save_for_backward(means, scales, quats, opac, sh, w2c, bg, pre["records"], b["sorted_gids"], b["ranges"],
-                              fT, nc, order)
+                              fT, nc, order, grec)
         radii = pre["radii"]
         valid = pre["valid"].view(torch.bool)  # the kernel writes 0/1 bytes
         stats = b["stats"]
@@ -51,17 +58,22 @@ class _Render(torch.autograd.Function):
         W, H, fx, fy, cx, cy, sh_degree, _ = ctx.static
         if g_image is None:
             return None, None, None, None, None, None, None, None, None
-        means, scales, quats, opac, sh, w2c, bg, rec, gids, ranges, fT, nc, order = ctx.saved_tensors
+        means, scales, quats, opac, sh, w2c, bg, rec, gids, ranges, fT, nc, order, grec = ctx.saved_tensors
         dev = means.device
         n = means.shape[0]
         s = _lib.stream_handle(dev)
         g_image = g_image.contiguous()
-        grec = torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=dev)
+        # the forward cleared grec: accumulate into it once; a repeated backward
+        # (retain_graph) starts from a fresh, cleared buffer
+        accumulate = 1 if ctx.grec_fresh else 0
+        ctx.grec_fresh = False
+        if not accumulate:
+            grec = torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=dev)
         # dL/dbackground only when the background is differentiated (the trainer's is not)
         gbg = torch.empty((3,), dtype=torch.float32, device=dev) if ctx.needs_input_grad[6] else None
         _lib.call("gs_composite_bwd", s, n, _lib.ptr(rec), _lib.ptr(gids), gids.shape[0], _lib.ptr(ranges), int(W), int(H),
                   _lib.ptr(bg), _lib.ptr(g_image), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec),
-                  _lib.ptr(gbg))
+                  _lib.ptr(gbg), accumulate)
         gm = torch.empty_like(means)
         gs_ = torch.empty_like(scales)
         gq = torch.empty_like(quats)

@@ -110,7 +110,9 @@ def _train_step_fused(state, target_image, camera, optimizer, sh_degree, lambda_
         pre = preprocess(params, camera, mask=active, sh_degree=sh_degree, records=True)
         b = bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W, want_tiles=False)
         bg = background_tensor(None, dev)
-        image, fT, nc, order = composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg, residuals=True)
+        grec = torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=dev)  # cleared by the forward
+        image, fT, nc, order = composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg, residuals=True,
+                                         clear_records=grec)
         # loss (trainer.py:18-26): one kernel for the L1 and SSIM means
         tgt = target_image.to(device=dev, dtype=torch.float32).contiguous()
         Hh, Ww, C = image.shape
@@ -125,10 +127,9 @@ def _train_step_fused(state, target_image, camera, optimizer, sh_degree, lambda_
         gimg = torch.empty_like(image)
         _lib.call("gs_l1_ssim_bwd", s, Hh, Ww, C, _lib.ptr(image), _lib.ptr(tgt), _lib.ptr(gout), _lib.ptr(ws), nbytes,
                   _lib.ptr(gimg))
-        grec = torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=dev)
         _lib.call("gs_composite_bwd", s, n, _lib.ptr(pre["records"]), _lib.ptr(b["sorted_gids"]),
                   b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), int(W), int(H), _lib.ptr(bg), _lib.ptr(gimg),
-                  _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec), None)
+                  _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec), None, 1)
         # preprocessing VJP + statistics + masked Adam, in place
         ost = state.opt_state
         moments = [ost.mu[f] for f in _FIELDS] + [ost.nu[f] for f in _FIELDS]

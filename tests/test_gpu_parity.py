@@ -269,6 +269,23 @@ def test_cfg4_masked_step_with_densify_accumulators(cuda):
     assert _rel(_np(state["grad_accum"]), ga) <= GRAD_TOL
 
 
+def test_render_backward_twice(cuda):
+    """The forward clears the gradient records its backward accumulates into; a second
+    backward through a retained graph starts from fresh records, so the parameter
+    gradients of two backward calls are twice those of one."""
+    sc = scenes.make_scene(1, n=4000, width=200, height=150)
+    g, cam, _, m = scenes.to_torch(sc, cuda)
+    for f in FIELDS:
+        getattr(g, f).requires_grad_(True)
+    image, _ = render(g, cam, mask=m, sh_degree=sc["sh_degree"])
+    seed = torch.from_numpy(np.random.default_rng(5).normal(0, 1, tuple(image.shape)).astype(np.float32)).to(cuda)
+    image.backward(seed, retain_graph=True)
+    once = {f: _np(getattr(g, f).grad).copy() for f in FIELDS}
+    image.backward(seed)
+    for f in FIELDS:
+        assert _rel(_np(getattr(g, f).grad), 2.0 * once[f]) <= 1e-5, f
+
+
 @pytest.mark.parametrize("cfg", [1, 2])
 def test_backward_tile_order(cuda, cfg):
     """The forward's tile order (tiles by decreasing walk length) is a permutation of
@@ -297,10 +314,23 @@ def test_backward_tile_order(cuda, cfg):
             gbg = torch.empty(3, device=cuda)
             _lib.call("gs_composite_bwd", _lib.stream_handle(cuda), n, _lib.ptr(pre["records"]),
                       _lib.ptr(b["sorted_gids"]), b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), W, H, _lib.ptr(bg),
-                      _lib.ptr(gimg), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(o), _lib.ptr(grec), _lib.ptr(gbg))
+                      _lib.ptr(gimg), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(o), _lib.ptr(grec), _lib.ptr(gbg), 0)
             out.append((_np(grec), _np(gbg)))
+        # records cleared by the forward, then accumulated into (twice: the sum doubles)
+        grec = torch.full((n, _lib.GS_REC_STRIDE), float("nan"), device=cuda)
+        rasterizer.composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg, clear_records=grec)
+        assert not torch.isnan(grec).any()
+        for rep in range(2):
+            _lib.call("gs_composite_bwd", _lib.stream_handle(cuda), n, _lib.ptr(pre["records"]),
+                      _lib.ptr(b["sorted_gids"]), b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), W, H, _lib.ptr(bg),
+                      _lib.ptr(gimg), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec), None, 1)
+            if rep == 0:
+                acc1 = _np(grec)
+        acc2 = _np(grec)
     assert _rel(out[0][0], out[1][0]) <= 1e-5
     assert _rel(out[0][1], out[1][1]) <= 1e-5
+    assert _rel(acc1, out[0][0]) <= 1e-5
+    assert _rel(acc2, 2.0 * out[0][0]) <= 1e-5
 
 
 def _l1_ssim_gpu(cuda, pred_np, tgt_np, gout):
