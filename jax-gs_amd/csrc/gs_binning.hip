@@ -196,7 +196,8 @@ __global__ __launch_bounds__(kPrepBlock) void bin_prep_kernel(int64_t n, const f
       }
       dkey[i] = key;
       word[i] = pack((uint32_t)i, v ? tminx : 0, v ? tminy : 0, w, h);
-      atomicAdd(&hist[key & (NB - 1)], 1u);
+      // Gaussians that meet no tile are dropped by the first radix pass: not counted
+      if (v) atomicAdd(&hist[key & (NB - 1)], 1u);
     }
     capc += (uint32_t)__popcll(__ballot(cap_violation));
     negc += (uint32_t)__popcll(__ballot(negative));
@@ -312,15 +313,20 @@ __device__ inline uint32_t init_digit_counters(uint32_t* cnt, const uint32_t* __
 
 constexpr int kUnroll = 4;
 
+// drop_empty: keys equal to kDepthBinEmpty (Gaussians meeting no tile, left out of the
+// histogram) are not written, so the output holds only the others, still stable; the
+// pass's output count goes to *n_kept (when given).
 template <int RB>
 __global__ __launch_bounds__(64) void radix_downsweep_kernel(
     const uint32_t* __restrict__ keys_in, const uint64_t* __restrict__ vals_in, const uint32_t* __restrict__ n_dev,
     int64_t n_static, int64_t cap, int shift, int G, int fixed_chunk, const uint32_t* __restrict__ table,
-    const uint32_t* __restrict__ digit_tot, uint32_t* __restrict__ keys_out, uint64_t* __restrict__ vals_out) {
+    const uint32_t* __restrict__ digit_tot, uint32_t* __restrict__ keys_out, uint64_t* __restrict__ vals_out,
+    bool drop_empty, uint32_t* __restrict__ n_kept) {
   constexpr int NB = 1 << RB;
   __shared__ uint32_t cnt[NB];
   const int lane = threadIdx.x;
-  init_digit_counters<RB>(cnt, table, digit_tot, G, blockIdx.x, lane);
+  const uint32_t total = init_digit_counters<RB>(cnt, table, digit_tot, G, blockIdx.x, lane);
+  if (n_kept != nullptr && blockIdx.x == 0 && lane == 0) *n_kept = total;
   __syncthreads();
   int64_t begin, end, n_pass;
   pass_range(n_dev, n_static, cap, G, fixed_chunk, begin, end, &n_pass);
@@ -338,7 +344,7 @@ __global__ __launch_bounds__(64) void radix_downsweep_kernel(
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int64_t i = base + u * 64 + lane;
-      const bool a = i < end;
+      const bool a = i < end && !(drop_empty && k[u] == (uint32_t)kDepthBinEmpty);
       const uint32_t d = (k[u] >> shift) & (NB - 1);
       const uint64_t m = match_any<RB>(d, a);
       uint32_t dst = 0;
@@ -362,8 +368,10 @@ __global__ __launch_bounds__(64) void radix_downsweep_kernel(
 // 3. Superblock pairs, generated from the depth-sorted words.  Workgroup g covers
 // Gaussians [g*256, (g+1)*256) (depth-sorted positions); the pass sorts on the low
 // 8 bits of the superblock id.
-__global__ __launch_bounds__(256) void pair_upsweep_kernel(const uint64_t* __restrict__ words, int64_t n, int SX,
-                                                           int G, uint32_t* __restrict__ table) {
+__global__ __launch_bounds__(256) void pair_upsweep_kernel(const uint64_t* __restrict__ words, int64_t n_static,
+                                                           const uint32_t* __restrict__ n_dev, int SX, int G,
+                                                           uint32_t* __restrict__ table) {
+  const int64_t n = n_static < (int64_t)*n_dev ? n_static : (int64_t)*n_dev;  // Gaussians with tiles
   constexpr int NB = 1 << kPairRB;
   __shared__ uint32_t hist[NB];
   hist[threadIdx.x] = 0;
@@ -385,7 +393,8 @@ __global__ __launch_bounds__(256) void pair_upsweep_kernel(const uint64_t* __res
 // list 64 pairs at a time.  A Gaussian has at most one pair per superblock, so the
 // pairs of any one superblock stay in Gaussian order: the pass is stable.
 template <bool WITH_KEYS>
-__global__ __launch_bounds__(64) void pair_downsweep_kernel(const uint64_t* __restrict__ words, int64_t n, int SX,
+__global__ __launch_bounds__(64) void pair_downsweep_kernel(const uint64_t* __restrict__ words, int64_t n_static,
+                                                            const uint32_t* __restrict__ n_dev, int SX,
                                                             int G, const uint32_t* __restrict__ table,
                                                             const uint32_t* __restrict__ digit_tot,
                                                             uint32_t* __restrict__ keys_out,
@@ -398,6 +407,7 @@ __global__ __launch_bounds__(64) void pair_downsweep_kernel(const uint64_t* __re
   const int lane = threadIdx.x;
   const uint32_t total = init_digit_counters<kPairRB>(cnt, table, digit_tot, G, blockIdx.x, lane);
   if (blockIdx.x == 0 && lane == 0) *n_pairs = total;
+  const int64_t n = n_static < (int64_t)*n_dev ? n_static : (int64_t)*n_dev;  // Gaussians with tiles
   __syncthreads();
   const int64_t begin = (int64_t)blockIdx.x * kPairSpan;
   const int64_t end = begin + kPairSpan < n ? begin + kPairSpan : n;
@@ -978,7 +988,7 @@ BinPlan make_plan(int64_t n, int width, int height, int64_t capacity) {
 template <int RB>
 int radix_pass(hipStream_t s, bool upsweep, const uint32_t* kin, const uint64_t* vin, uint32_t* kout, uint64_t* vout,
                const uint32_t* n_dev, int64_t n_static, int64_t cap, int shift, int G, int fixed_chunk,
-               uint32_t* table, uint32_t* dtot) {
+               uint32_t* table, uint32_t* dtot, bool drop_empty = false, uint32_t* n_kept = nullptr) {
   if (upsweep) {
     hipLaunchKernelGGL(radix_upsweep_kernel<RB>, dim3(G), dim3(64), 0, s, kin, n_dev, n_static, cap, shift, G,
                        fixed_chunk, table);
@@ -987,7 +997,7 @@ int radix_pass(hipStream_t s, bool upsweep, const uint32_t* kin, const uint64_t*
   hipLaunchKernelGGL(radix_spine_kernel, dim3(1 << RB), dim3(kScanBlock), 0, s, table, G, dtot);
   GS_LAUNCH_CHECK("radix_spine_kernel");
   hipLaunchKernelGGL(radix_downsweep_kernel<RB>, dim3(G), dim3(64), 0, s, kin, vin, n_dev, n_static, cap, shift, G,
-                     fixed_chunk, table, dtot, kout, vout);
+                     fixed_chunk, table, dtot, kout, vout, drop_empty, n_kept);
   GS_LAUNCH_CHECK("radix_downsweep_kernel");
   return GS_OK;
 }
@@ -1045,6 +1055,7 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   uint32_t* n_pairs = scal + 0;
   uint32_t* n_chunks = scal + 1;
   uint32_t* n_segs = scal + 2;
+  uint32_t* n_has = scal + 3;  // Gaussians that meet at least one tile
 
   if (n == 0) {
     hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, s, stats, (int64_t)GS_NUM_STATS, 0);
@@ -1058,23 +1069,27 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
                      width, height, P.G_d, dkey, word, table, blk);
   GS_LAUNCH_CHECK("bin_prep_kernel");
   // 2. stable depth sort of the packed words (13-bit bucket: 7 + 6 bits)
-  int rc = radix_pass<kDepthRB>(s, false, dkey, word, kb, wb, nullptr, n, n, 0, P.G_d, kSpan, table, dtot);
+  // (the first pass drops Gaussians that meet no tile; the later passes see n_has)
+  int rc = radix_pass<kDepthRB>(s, false, dkey, word, kb, wb, nullptr, n, n, 0, P.G_d, kSpan, table, dtot, true,
+                                n_has);
   if (rc != GS_OK) return rc;
-  rc = radix_pass<kDepthRB>(s, true, kb, wb, ka, wa, nullptr, n, n, kDepthRB, P.G_d, kSpan, table, dtot);
+  rc = radix_pass<kDepthRB>(s, true, kb, wb, ka, wa, n_has, n, n, kDepthRB, P.G_d, kSpan, table, dtot);
   if (rc != GS_OK) return rc;
   const uint64_t* sorted_word = wa;
   // 3. superblock pairs generated from the depth order, sorted by superblock
-  hipLaunchKernelGGL(pair_upsweep_kernel, dim3(P.G_q), dim3(256), 0, s, sorted_word, n, P.SX, P.G_q, table);
+  hipLaunchKernelGGL(pair_upsweep_kernel, dim3(P.G_q), dim3(256), 0, s, sorted_word, n, n_has, P.SX, P.G_q, table);
   GS_LAUNCH_CHECK("pair_upsweep_kernel");
   hipLaunchKernelGGL(radix_spine_kernel, dim3(1 << kPairRB), dim3(kScanBlock), 0, s, table, P.G_q, dtot);
   GS_LAUNCH_CHECK("radix_spine_kernel");
   const uint64_t* sbval = pv0;
   if (P.sb_passes == 1) {
-    hipLaunchKernelGGL(pair_downsweep_kernel<false>, dim3(P.G_q), dim3(64), 0, s, sorted_word, n, P.SX, P.G_q, table,
+    hipLaunchKernelGGL(pair_downsweep_kernel<false>, dim3(P.G_q), dim3(64), 0, s, sorted_word, n, n_has, P.SX, P.G_q,
+                       table,
                        dtot, nullptr, pv0, n_pairs);
     GS_LAUNCH_CHECK("pair_downsweep_kernel");
   } else {
-    hipLaunchKernelGGL(pair_downsweep_kernel<true>, dim3(P.G_q), dim3(64), 0, s, sorted_word, n, P.SX, P.G_q, table,
+    hipLaunchKernelGGL(pair_downsweep_kernel<true>, dim3(P.G_q), dim3(64), 0, s, sorted_word, n, n_has, P.SX, P.G_q,
+                       table,
                        dtot, pk0, pv0, n_pairs);
     GS_LAUNCH_CHECK("pair_downsweep_kernel");
     rc = radix_pass<kPairRB>(s, true, pk0, pv0, pk1, pv1, n_pairs, 0, P.pcap, kPairRB, P.G_p, 0, table, dtot);
