@@ -388,6 +388,91 @@ __global__ __launch_bounds__(256) void pair_upsweep_kernel(const uint64_t* __res
   table[(int64_t)threadIdx.x * G + blockIdx.x] = hist[threadIdx.x];
 }
 
+// The chunk and segment maps of the tile pass (chunks_kernel's outputs) computed inside
+// the superblock pass when the pass has one round (S <= 256: a superblock id is its
+// digit, so its pair range follows from the digit totals, final before the pass
+// starts).  Every workgroup scans the <= 256 totals itself (one wave, four superblocks
+// per lane) and fills its own slice of the chunk -> superblock and segment ->
+// superblock maps; workgroup 0 writes the bases and counts.  No workgroup waits for
+// another.
+struct ChunkMapArgs {
+  int S;
+  int64_t cmax, gmax;
+  int32_t* sb_ranges;
+  uint32_t *chunk_base, *chunk_sb, *n_chunks, *seg_base, *seg_sb, *n_segs;
+};
+
+__device__ inline void chunk_maps_from_digits(const ChunkMapArgs& A, const uint32_t* __restrict__ digit_tot,
+                                              uint32_t* cb, uint32_t* gb, int lane) {
+  constexpr int PER = 256 / 64;  // superblocks per lane
+  uint32_t cnt[PER], nc[PER], ng[PER], sum_p = 0, sum_c = 0, sum_g = 0;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int sb = PER * lane + k;
+    cnt[k] = sb < A.S ? digit_tot[sb] : 0u;
+    nc[k] = (cnt[k] + kChunk - 1) / kChunk;
+    ng[k] = (nc[k] + kSeg - 1) / kSeg;
+    sum_p += cnt[k];
+    sum_c += nc[k];
+    sum_g += ng[k];
+  }
+  const uint32_t ip = wave_incl_scan(sum_p), ic = wave_incl_scan(sum_c), ig = wave_incl_scan(sum_g);
+  uint32_t p = ip - sum_p, c = ic - sum_c, g = ig - sum_g;
+  const bool w0 = blockIdx.x == 0;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int sb = PER * lane + k;
+    if (sb < A.S) {
+      cb[sb] = c;
+      gb[sb] = g;
+      if (w0) {
+        A.sb_ranges[sb] = (int32_t)p;
+        A.chunk_base[sb] = c;
+        A.seg_base[sb] = g;
+      }
+    }
+    p += cnt[k];
+    c += nc[k];
+    g += ng[k];
+  }
+  const uint32_t tp = (uint32_t)__shfl(ip, 63, 64), tc = (uint32_t)__shfl(ic, 63, 64),
+                 tg = (uint32_t)__shfl(ig, 63, 64);
+  if (lane == 0) {
+    cb[A.S] = tc;
+    gb[A.S] = tg;
+    if (w0) {
+      A.sb_ranges[A.S] = (int32_t)tp;
+      A.chunk_base[A.S] = tc;
+      A.seg_base[A.S] = tg;
+      *A.n_chunks = tc;
+      *A.n_segs = tg;
+    }
+  }
+  __syncthreads();
+  // this workgroup's slices of the two maps: entry j belongs to the last superblock
+  // whose base is <= j
+  const uint32_t G = gridDim.x;
+  const uint32_t nch = (int64_t)tc < A.cmax ? tc : (uint32_t)A.cmax;
+  const uint32_t nsg = (int64_t)tg < A.gmax ? tg : (uint32_t)A.gmax;
+  const uint32_t pc = (nch + G - 1) / G, pg = (nsg + G - 1) / G;
+  for (uint32_t j = blockIdx.x * pc + lane; j < nch && j < (blockIdx.x + 1) * pc; j += 64) {
+    int lo = 0, hi = A.S;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (cb[mid] <= j) lo = mid; else hi = mid;
+    }
+    A.chunk_sb[j] = (uint32_t)lo;
+  }
+  for (uint32_t j = blockIdx.x * pg + lane; j < nsg && j < (blockIdx.x + 1) * pg; j += 64) {
+    int lo = 0, hi = A.S;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (gb[mid] <= j) lo = mid; else hi = mid;
+    }
+    A.seg_sb[j] = (uint32_t)lo;
+  }
+}
+
 // Each round of 64 Gaussians lists its (superblock, lane) pairs in LDS in lane order
 // (a wave prefix sum of the pair counts gives each Gaussian its place) and ranks the
 // list 64 pairs at a time.  A Gaussian has at most one pair per superblock, so the
@@ -399,15 +484,17 @@ __global__ __launch_bounds__(64) void pair_downsweep_kernel(const uint64_t* __re
                                                             const uint32_t* __restrict__ digit_tot,
                                                             uint32_t* __restrict__ keys_out,
                                                             uint64_t* __restrict__ vals_out,
-                                                            uint32_t* __restrict__ n_pairs) {
+                                                            uint32_t* __restrict__ n_pairs, ChunkMapArgs maps) {
   constexpr int NB = 1 << kPairRB;
   __shared__ uint32_t cnt[NB];
+  __shared__ uint32_t mcb[NB + 1], mgb[NB + 1];
   __shared__ uint32_t list[64 * kSBSpan * kSBSpan];  // (superblock << 6) | lane
   __shared__ uint64_t wl[64];
   const int lane = threadIdx.x;
   const uint32_t total = init_digit_counters<kPairRB>(cnt, table, digit_tot, G, blockIdx.x, lane);
   if (blockIdx.x == 0 && lane == 0) *n_pairs = total;
   const int64_t n = n_static < (int64_t)*n_dev ? n_static : (int64_t)*n_dev;  // Gaussians with tiles
+  if (maps.S > 0) chunk_maps_from_digits(maps, digit_tot, mcb, mgb, lane);
   __syncthreads();
   const int64_t begin = (int64_t)blockIdx.x * kPairSpan;
   const int64_t end = begin + kPairSpan < n ? begin + kPairSpan : n;
@@ -467,13 +554,12 @@ __global__ __launch_bounds__(256) void ranges_kernel(const uint32_t* __restrict_
   }
 }
 
-// One block: superblock ranges (from the digit totals when the pair sort had one
-// pass, digit = superblock id), chunk count per superblock -> exclusive scan ->
-// chunk_base[S+1] and the chunk -> superblock map; likewise the superblock's segments
-// (runs of kSeg chunks, the unit of the chunk-offset scan): seg_base[S+1] and the
-// segment -> superblock map.
-__global__ __launch_bounds__(kBig) void chunks_kernel(int S, bool from_digits, const uint32_t* __restrict__ digit_tot,
-                                                      int32_t* __restrict__ sb_ranges, int64_t cmax,
+// One block, for images whose superblock sort takes two passes (more than 256
+// superblocks; with one pass the superblock pass builds these maps itself): chunk count
+// per superblock (from the superblock ranges) -> exclusive scan -> chunk_base[S+1] and
+// the chunk -> superblock map; likewise the superblock's segments (runs of kSeg chunks,
+// the unit of the chunk-offset scan): seg_base[S+1] and the segment -> superblock map.
+__global__ __launch_bounds__(kBig) void chunks_kernel(int S, const int32_t* __restrict__ sb_ranges, int64_t cmax,
                                                       uint32_t* __restrict__ chunk_base,
                                                       uint32_t* __restrict__ chunk_sb, uint32_t* __restrict__ n_chunks,
                                                       int64_t gmax, uint32_t* __restrict__ seg_base,
@@ -489,14 +575,7 @@ __global__ __launch_bounds__(kBig) void chunks_kernel(int S, bool from_digits, c
   for (int s0 = 0; s0 < S; s0 += kBig) {
     const int sb = s0 + threadIdx.x;
     uint32_t lo = 0, hi = 0;
-    if (from_digits) {  // S <= 256: one iteration
-      const uint32_t c = sb < S ? digit_tot[sb] : 0u;
-      uint32_t sum;
-      lo = block_excl_scan<kBig>(c, &sum);
-      hi = lo + c;
-      if (sb < S) sb_ranges[sb] = (int32_t)lo;
-      if (sb == S - 1) sb_ranges[S] = (int32_t)hi;
-    } else if (sb < S) {
+    if (sb < S) {
       lo = (uint32_t)sb_ranges[sb];
       hi = (uint32_t)sb_ranges[sb + 1];
     }
@@ -1082,15 +1161,17 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   hipLaunchKernelGGL(radix_spine_kernel, dim3(1 << kPairRB), dim3(kScanBlock), 0, s, table, P.G_q, dtot);
   GS_LAUNCH_CHECK("radix_spine_kernel");
   const uint64_t* sbval = pv0;
+  ChunkMapArgs maps{0, P.cmax, P.gmax, sbr, cbase, csb, n_chunks, gbase, gsb, n_segs};
   if (P.sb_passes == 1) {
+    maps.S = P.S;  // one superblock pass: the pass also builds the chunk maps
     hipLaunchKernelGGL(pair_downsweep_kernel<false>, dim3(P.G_q), dim3(64), 0, s, sorted_word, n, n_has, P.SX, P.G_q,
                        table,
-                       dtot, nullptr, pv0, n_pairs);
+                       dtot, nullptr, pv0, n_pairs, maps);
     GS_LAUNCH_CHECK("pair_downsweep_kernel");
   } else {
     hipLaunchKernelGGL(pair_downsweep_kernel<true>, dim3(P.G_q), dim3(64), 0, s, sorted_word, n, n_has, P.SX, P.G_q,
                        table,
-                       dtot, pk0, pv0, n_pairs);
+                       dtot, pk0, pv0, n_pairs, maps);
     GS_LAUNCH_CHECK("pair_downsweep_kernel");
     rc = radix_pass<kPairRB>(s, true, pk0, pv0, pk1, pv1, n_pairs, 0, P.pcap, kPairRB, P.G_p, 0, table, dtot);
     if (rc != GS_OK) return rc;
@@ -1100,9 +1181,11 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
     GS_LAUNCH_CHECK("ranges_kernel");
   }
   // 4. tile pass
-  hipLaunchKernelGGL(chunks_kernel, dim3(1), dim3(kBig), 0, s, P.S, P.sb_passes == 1, dtot, sbr, P.cmax, cbase, csb,
-                     n_chunks, P.gmax, gbase, gsb, n_segs);
-  GS_LAUNCH_CHECK("chunks_kernel");
+  if (P.sb_passes != 1) {  // (one pass: built by the superblock pass)
+    hipLaunchKernelGGL(chunks_kernel, dim3(1), dim3(kBig), 0, s, P.S, sbr, P.cmax, cbase, csb, n_chunks, P.gmax,
+                       gbase, gsb, n_segs);
+    GS_LAUNCH_CHECK("chunks_kernel");
+  }
   // one chunk per wave: the chunk count is known on the device only, so the grid covers
   // the bound and surplus waves exit at once; waves start as others finish
   const int pass_blocks = (int)std::min<int64_t>(div_up(P.cmax, 4), (int64_t)1 << 20);
