@@ -159,8 +159,15 @@ __global__ __launch_bounds__(kPrepBlock) void bin_prep_kernel(int64_t n, const f
                                                               const float* __restrict__ depths, int W, int H, int G,
                                                               uint32_t* __restrict__ dkey, uint64_t* __restrict__ word,
                                                               uint32_t* __restrict__ table,
-                                                              uint32_t* __restrict__ blkstat) {
+                                                              uint32_t* __restrict__ blkstat,
+                                                              uint4* __restrict__ zero_buf, int64_t n_zero4) {
   constexpr int NB = 1 << kDepthRB;
+  {
+    // the tile pass's segment totals, accumulated with atomics later: cleared here
+    const int64_t per = (n_zero4 + gridDim.x - 1) / gridDim.x;
+    const int64_t z0 = per * blockIdx.x, z1 = z0 + per < n_zero4 ? z0 + per : n_zero4;
+    for (int64_t z = z0 + threadIdx.x; z < z1; z += kPrepBlock) zero_buf[z] = make_uint4(0u, 0u, 0u, 0u);
+  }
   __shared__ uint32_t hist[NB];
   __shared__ uint32_t wcnt[2][kPrepBlock / 64];
   for (int d = threadIdx.x; d < NB; d += kPrepBlock) hist[d] = 0;
@@ -399,11 +406,11 @@ struct ChunkMapArgs {
   int S;
   int64_t cmax, gmax;
   int32_t* sb_ranges;
-  uint32_t *chunk_base, *chunk_sb, *n_chunks, *seg_base, *seg_sb, *n_segs;
+  uint32_t *chunk_base, *chunk_sb, *n_chunks, *seg_base, *n_segs;
 };
 
 __device__ inline void chunk_maps_from_digits(const ChunkMapArgs& A, const uint32_t* __restrict__ digit_tot,
-                                              uint32_t* cb, uint32_t* gb, int lane) {
+                                              uint32_t* cb, int lane) {
   constexpr int PER = 256 / 64;  // superblocks per lane
   uint32_t cnt[PER], nc[PER], ng[PER], sum_p = 0, sum_c = 0, sum_g = 0;
 #pragma unroll
@@ -424,7 +431,6 @@ __device__ inline void chunk_maps_from_digits(const ChunkMapArgs& A, const uint3
     const int sb = PER * lane + k;
     if (sb < A.S) {
       cb[sb] = c;
-      gb[sb] = g;
       if (w0) {
         A.sb_ranges[sb] = (int32_t)p;
         A.chunk_base[sb] = c;
@@ -439,7 +445,6 @@ __device__ inline void chunk_maps_from_digits(const ChunkMapArgs& A, const uint3
                  tg = (uint32_t)__shfl(ig, 63, 64);
   if (lane == 0) {
     cb[A.S] = tc;
-    gb[A.S] = tg;
     if (w0) {
       A.sb_ranges[A.S] = (int32_t)tp;
       A.chunk_base[A.S] = tc;
@@ -449,12 +454,11 @@ __device__ inline void chunk_maps_from_digits(const ChunkMapArgs& A, const uint3
     }
   }
   __syncthreads();
-  // this workgroup's slices of the two maps: entry j belongs to the last superblock
+  // this workgroup's slice of the chunk map: chunk j belongs to the last superblock
   // whose base is <= j
   const uint32_t G = gridDim.x;
   const uint32_t nch = (int64_t)tc < A.cmax ? tc : (uint32_t)A.cmax;
-  const uint32_t nsg = (int64_t)tg < A.gmax ? tg : (uint32_t)A.gmax;
-  const uint32_t pc = (nch + G - 1) / G, pg = (nsg + G - 1) / G;
+  const uint32_t pc = (nch + G - 1) / G;
   for (uint32_t j = blockIdx.x * pc + lane; j < nch && j < (blockIdx.x + 1) * pc; j += 64) {
     int lo = 0, hi = A.S;
     while (hi - lo > 1) {
@@ -462,14 +466,6 @@ __device__ inline void chunk_maps_from_digits(const ChunkMapArgs& A, const uint3
       if (cb[mid] <= j) lo = mid; else hi = mid;
     }
     A.chunk_sb[j] = (uint32_t)lo;
-  }
-  for (uint32_t j = blockIdx.x * pg + lane; j < nsg && j < (blockIdx.x + 1) * pg; j += 64) {
-    int lo = 0, hi = A.S;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (gb[mid] <= j) lo = mid; else hi = mid;
-    }
-    A.seg_sb[j] = (uint32_t)lo;
   }
 }
 
@@ -487,14 +483,14 @@ __global__ __launch_bounds__(64) void pair_downsweep_kernel(const uint64_t* __re
                                                             uint32_t* __restrict__ n_pairs, ChunkMapArgs maps) {
   constexpr int NB = 1 << kPairRB;
   __shared__ uint32_t cnt[NB];
-  __shared__ uint32_t mcb[NB + 1], mgb[NB + 1];
+  __shared__ uint32_t mcb[NB + 1];
   __shared__ uint32_t list[64 * kSBSpan * kSBSpan];  // (superblock << 6) | lane
   __shared__ uint64_t wl[64];
   const int lane = threadIdx.x;
   const uint32_t total = init_digit_counters<kPairRB>(cnt, table, digit_tot, G, blockIdx.x, lane);
   if (blockIdx.x == 0 && lane == 0) *n_pairs = total;
   const int64_t n = n_static < (int64_t)*n_dev ? n_static : (int64_t)*n_dev;  // Gaussians with tiles
-  if (maps.S > 0) chunk_maps_from_digits(maps, digit_tot, mcb, mgb, lane);
+  if (maps.S > 0) chunk_maps_from_digits(maps, digit_tot, mcb, lane);
   __syncthreads();
   const int64_t begin = (int64_t)blockIdx.x * kPairSpan;
   const int64_t end = begin + kPairSpan < n ? begin + kPairSpan : n;
@@ -563,9 +559,8 @@ __global__ __launch_bounds__(kBig) void chunks_kernel(int S, const int32_t* __re
                                                       uint32_t* __restrict__ chunk_base,
                                                       uint32_t* __restrict__ chunk_sb, uint32_t* __restrict__ n_chunks,
                                                       int64_t gmax, uint32_t* __restrict__ seg_base,
-                                                      uint32_t* __restrict__ seg_sb, uint32_t* __restrict__ n_segs) {
+                                                      uint32_t* __restrict__ n_segs) {
   __shared__ uint32_t cb[kBig + 1];  // chunk bases, when S <= kBig
-  __shared__ uint32_t gb[kBig + 1];  // segment bases, when S <= kBig
   __shared__ uint32_t carry_c, carry_g;
   if (threadIdx.x == 0) {
     carry_c = 0;
@@ -589,10 +584,8 @@ __global__ __launch_bounds__(kBig) void chunks_kernel(int S, const int32_t* __re
       seg_base[sb] = g0;
       if (S <= kBig) {
         cb[sb] = c0;
-        gb[sb] = g0;
       } else {
         for (uint32_t c = c0; c < c0 + nc && (int64_t)c < cmax; ++c) chunk_sb[c] = (uint32_t)sb;
-        for (uint32_t g = g0; g < g0 + ng && (int64_t)g < gmax; ++g) seg_sb[g] = (uint32_t)sb;
       }
     }
     __syncthreads();
@@ -612,7 +605,6 @@ __global__ __launch_bounds__(kBig) void chunks_kernel(int S, const int32_t* __re
   if (S <= kBig) {
     if (threadIdx.x == 0) {
       cb[S] = total;
-      gb[S] = total_g;
     }
     __syncthreads();
     // chunk j belongs to the last superblock whose base is <= j (likewise segments)
@@ -624,15 +616,6 @@ __global__ __launch_bounds__(kBig) void chunks_kernel(int S, const int32_t* __re
         if (cb[mid] <= j) lo = mid; else hi = mid;
       }
       chunk_sb[j] = (uint32_t)lo;
-    }
-    const uint32_t glim = (int64_t)total_g < gmax ? total_g : (uint32_t)gmax;
-    for (uint32_t j = threadIdx.x; j < glim; j += kBig) {
-      int lo = 0, hi = S;
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (gb[mid] <= j) lo = mid; else hi = mid;
-      }
-      seg_sb[j] = (uint32_t)lo;
     }
   }
 }
@@ -690,7 +673,8 @@ __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restr
                                                          const int32_t* __restrict__ sb_ranges, int S,
                                                          const uint64_t* __restrict__ pval, int SX,
                                                          const uint32_t* __restrict__ seg_base,
-                                                         uint32_t* __restrict__ cnt, uint4* __restrict__ desc) {
+                                                         uint32_t* __restrict__ cnt, uint4* __restrict__ desc,
+                                                         uint32_t* __restrict__ seg_sum) {
   const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
   const uint32_t C = (uint32_t)min<int64_t>((int64_t)*n_chunks, cmax);
@@ -709,9 +693,12 @@ __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restr
       }
     }
     cnt[(int64_t)c * 64 + lane] = mycount;
+    // the chunk's segment (kSeg consecutive chunks of the superblock) and its place in it
+    const uint32_t g = seg_base[cs.s] + (c - cs.first) / kSeg, p = (c - cs.first) % kSeg;
+    if (mycount != 0u) atomicAdd(&seg_sum[(int64_t)g * 64 + lane], mycount);
     if (lane == 0)
-      desc[c] = make_uint4((uint32_t)cs.begin, (uint32_t)len, (uint32_t)cs.sx | ((uint32_t)cs.sy << 16),
-                           seg_base[cs.s] + (c - cs.first) / kSeg);
+      desc[c] = make_uint4((uint32_t)cs.begin, (uint32_t)len | (p << 16), (uint32_t)cs.sx | ((uint32_t)cs.sy << 16),
+                           g);
   }
 }
 
@@ -823,38 +810,11 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
 }
 
 // 4b. Chunk offsets per tile (lane), in two levels so that a superblock with
-// thousands of chunks (a dense cluster) is spread over many waves: a wave per segment
-// of kSeg chunks turns the counts into exclusive prefixes within the segment (in place)
-// and writes the segment totals; then one block per superblock turns its segments'
-// totals into exclusive prefixes (in place) and writes the tile totals.  A chunk's
-// offset is the sum of its two prefixes.
-__global__ __launch_bounds__(256) void chunk_seg_kernel(const uint32_t* __restrict__ n_segs, int64_t gmax,
-                                                        const uint32_t* __restrict__ seg_sb,
-                                                        const uint32_t* __restrict__ seg_base,
-                                                        const uint32_t* __restrict__ chunk_base, int64_t cmax,
-                                                        uint32_t* __restrict__ cnt, uint32_t* __restrict__ seg_sum) {
-  const int lane = threadIdx.x & 63;
-  const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
-  const uint32_t G = (uint32_t)min<int64_t>((int64_t)*n_segs, gmax);
-  for (uint32_t g = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); g < G; g += nwaves) {
-    const uint32_t sb = seg_sb[g];
-    const int64_t c0 = (int64_t)chunk_base[sb] + (int64_t)(g - seg_base[sb]) * kSeg;
-    int64_t c1 = (int64_t)chunk_base[sb + 1];
-    c1 = c1 < c0 + kSeg ? c1 : c0 + kSeg;
-    c1 = c1 < cmax ? c1 : cmax;
-    uint32_t v[kSeg];
-#pragma unroll
-    for (int k = 0; k < kSeg; ++k) v[k] = c0 + k < c1 ? cnt[(c0 + k) * 64 + lane] : 0u;
-    uint32_t run = 0;
-#pragma unroll
-    for (int k = 0; k < kSeg; ++k) {
-      if (c0 + k < c1) cnt[(c0 + k) * 64 + lane] = run;
-      run += v[k];
-    }
-    seg_sum[(int64_t)g * 64 + lane] = run;
-  }
-}
-
+// thousands of chunks (a dense cluster) is spread over many waves: the counting sweep
+// adds each chunk's counts into its segment's totals (segments of kSeg chunks); one
+// block per superblock turns its segments' totals into exclusive prefixes (in place)
+// and writes the tile totals; the write sweep adds the counts of the chunk's earlier
+// chunks in its segment.
 // One block per superblock over its segments: 16 waves split them into contiguous
 // runs, sum, scan the 16 run sums, then write the prefixes.
 __global__ __launch_bounds__(kBig) void chunk_scan_kernel(const uint32_t* __restrict__ seg_base, int64_t gmax,
@@ -950,7 +910,7 @@ __device__ inline void write_chunk(const uint4& d, const uint64_t* __restrict__ 
                                    uint32_t cnt_c, const uint32_t* __restrict__ seg_pre,
                                    const int32_t* __restrict__ ranges, uint32_t cap32, int lane,
                                    int32_t* __restrict__ out_gid, int32_t* __restrict__ out_tile) {
-  const int len = (int)d.y, sx = (int)(d.z & 0xFFFFu), sy = (int)(d.z >> 16);
+  const int len = (int)(d.y & 0xFFFFu), sx = (int)(d.z & 0xFFFFu), sy = (int)(d.z >> 16);
   const int t = tile_of(sx, sy, lane, TX, TY);
   uint64_t wv[4];
 #pragma unroll
@@ -982,7 +942,11 @@ __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restr
   const bool fits = ranges[T] >= 0 && (int64_t)ranges[T] <= cap;
   for (uint32_t c = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); c < C; c += nwaves) {
     const uint4 d = desc[c];
-    const uint32_t cnt_c = cnt[(int64_t)c * 64 + lane];
+    // counts of the chunk's earlier chunks in its segment (p of them), loaded together
+    const uint32_t p = d.y >> 16;
+    uint32_t cnt_c = 0;
+#pragma unroll
+    for (int k = 1; k < kSeg; ++k) cnt_c += (uint32_t)k <= p ? cnt[(int64_t)(c - k) * 64 + lane] : 0u;
     if (fits)
       write_chunk<WITH_TILES, false>(d, pval, n_gauss, TX, TY, cnt_c, seg_pre, ranges, cap32, lane, out_gid, out_tile);
     else
@@ -1004,7 +968,7 @@ struct BinPlan {
   int G_p;        // workgroups of the second pair pass
   int sb_passes;  // 1 when S <= 256, else 2
   size_t o_dkey, o_word, o_ka, o_wa, o_kb, o_wb, o_table, o_dtot, o_scal, o_pk0, o_pv0, o_pk1, o_pv1, o_sbr,
-      o_cbase, o_csb, o_cnt, o_desc, o_tot, o_blk, o_gbase, o_gsb, o_gsum, total;
+      o_cbase, o_csb, o_cnt, o_desc, o_tot, o_blk, o_gbase, o_gsum, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1056,7 +1020,6 @@ BinPlan make_plan(int64_t n, int width, int height, int64_t capacity) {
   P.o_tot = take((size_t)P.T * 4);
   P.o_blk = take((size_t)P.G_d * 2 * 4);
   P.o_gbase = take(((size_t)P.S + 1) * 4);
-  P.o_gsb = take((size_t)P.gmax * 4);
   P.o_gsum = take((size_t)P.gmax * 64 * 4);
   P.total = o;
   return P;
@@ -1129,7 +1092,6 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   uint32_t* tot = (uint32_t*)(ws + P.o_tot);
   uint32_t* blk = (uint32_t*)(ws + P.o_blk);
   uint32_t* gbase = (uint32_t*)(ws + P.o_gbase);
-  uint32_t* gsb = (uint32_t*)(ws + P.o_gsb);
   uint32_t* gsum = (uint32_t*)(ws + P.o_gsum);
   uint32_t* n_pairs = scal + 0;
   uint32_t* n_chunks = scal + 1;
@@ -1145,7 +1107,7 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   }
   // 1. prep (+ histogram of the first depth digit)
   hipLaunchKernelGGL(bin_prep_kernel, dim3(P.G_d), dim3(kPrepBlock), 0, s, n, means2d, radii, valid, depths,
-                     width, height, P.G_d, dkey, word, table, blk);
+                     width, height, P.G_d, dkey, word, table, blk, (uint4*)gsum, P.gmax * 64 / 4);
   GS_LAUNCH_CHECK("bin_prep_kernel");
   // 2. stable depth sort of the packed words (13-bit bucket: 7 + 6 bits)
   // (the first pass drops Gaussians that meet no tile; the later passes see n_has)
@@ -1161,7 +1123,7 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   hipLaunchKernelGGL(radix_spine_kernel, dim3(1 << kPairRB), dim3(kScanBlock), 0, s, table, P.G_q, dtot);
   GS_LAUNCH_CHECK("radix_spine_kernel");
   const uint64_t* sbval = pv0;
-  ChunkMapArgs maps{0, P.cmax, P.gmax, sbr, cbase, csb, n_chunks, gbase, gsb, n_segs};
+  ChunkMapArgs maps{0, P.cmax, P.gmax, sbr, cbase, csb, n_chunks, gbase, n_segs};
   if (P.sb_passes == 1) {
     maps.S = P.S;  // one superblock pass: the pass also builds the chunk maps
     hipLaunchKernelGGL(pair_downsweep_kernel<false>, dim3(P.G_q), dim3(64), 0, s, sorted_word, n, n_has, P.SX, P.G_q,
@@ -1183,18 +1145,15 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   // 4. tile pass
   if (P.sb_passes != 1) {  // (one pass: built by the superblock pass)
     hipLaunchKernelGGL(chunks_kernel, dim3(1), dim3(kBig), 0, s, P.S, sbr, P.cmax, cbase, csb, n_chunks, P.gmax,
-                       gbase, gsb, n_segs);
+                       gbase, n_segs);
     GS_LAUNCH_CHECK("chunks_kernel");
   }
   // one chunk per wave: the chunk count is known on the device only, so the grid covers
   // the bound and surplus waves exit at once; waves start as others finish
   const int pass_blocks = (int)std::min<int64_t>(div_up(P.cmax, 4), (int64_t)1 << 20);
   hipLaunchKernelGGL(tile_count_kernel, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, csb, cbase, sbr, P.S,
-                     sbval, P.SX, gbase, cnt, desc);
+                     sbval, P.SX, gbase, cnt, desc, gsum);
   GS_LAUNCH_CHECK("tile_count_kernel");
-  hipLaunchKernelGGL(chunk_seg_kernel, dim3(div_up(P.gmax, 4)), dim3(256), 0, s, n_segs, P.gmax, gsb, gbase, cbase,
-                     P.cmax, cnt, gsum);
-  GS_LAUNCH_CHECK("chunk_seg_kernel");
   hipLaunchKernelGGL(chunk_scan_kernel, dim3(P.S), dim3(kBig), 0, s, gbase, P.gmax, P.SX, P.TX, P.TY, gsum, tot);
   GS_LAUNCH_CHECK("chunk_scan_kernel");
   hipLaunchKernelGGL(tile_scan_stats_kernel, dim3(1), dim3(kBig), 0, s, tot, P.T, blk, P.G_d, P.cap, ranges, stats);
