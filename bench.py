@@ -100,7 +100,7 @@ def main():
     with torch.no_grad():
         for _ in range(reps):
             mark("t0")
-            pre = preprocess(g, cam, mask=mask, sh_degree=D)
+            pre = preprocess(g, cam, mask=mask, sh_degree=D, projected=False)
             mark("t1")
             b = rasterizer.bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W,
                                          want_tiles=False)
@@ -226,11 +226,12 @@ def main():
     nb = (D + 1) ** 2
     # Algorithmic bytes per launch (what each stage must move at minimum):
     #   preprocess fwd: read means 12 + scales 12 + quats 16 + opacity 4 + (D+1)^2 SH triples
-    #                   12 each; write means2d 8, cov2d 16, radius 4, valid 1, depth 4,
-    #                   colour 12, compositing record 48.
+    #                   12 each; write means2d 8, radius 4, valid 1, depth 4 (binning's inputs)
+    #                   and the compositing record 48 (conic and colour: the renderer writes no
+    #                   separate cov2d and colour arrays).
     #   preprocess bwd: the same inputs + gradient record 48; write 5 gradient arrays
     #                   (12 + 12 + 16 + 4 + 12 K).
-    pre_fwd_bytes = N * (44 + 12 * nb) + N * (8 + 16 + 4 + 1 + 4 + 12 + 48)
+    pre_fwd_bytes = N * (44 + 12 * nb) + N * (8 + 4 + 1 + 4 + 48)
     pre_bwd_bytes = N * (44 + 12 * nb) + N * 48 + N * (12 + 12 + 16 + 4 + 12 * K)
     #   binning: read means2d 8 + radius 4 + valid 1 + depth 4 per Gaussian; write the entry
     #            list (4 B per entry) and the tile ranges (4 B per tile).

@@ -75,9 +75,10 @@ int gs_abi_version(void);
  * jax_gs/core/gaussians.py:58-92 (get_covariance_3d), jax_gs/renderer/renderer.py:40-49
  * with jax_gs/renderer/sh.py:25-74 (view directions, eval_sh, +0.5, clip) and the
  * conic/sigmoid preparation of jax_gs/renderer/rasterizer.py:147-156.
- * mask may be NULL (all active).  records may be NULL.
+ * mask may be NULL (all active).
  * Outputs: means2d[N,2] cov2d[N,2,2] radii[N] valid[N] (0/1) depths[N] colors[N,3]
- * records[N,GS_REC_STRIDE]. */
+ * records[N,GS_REC_STRIDE].  records may be NULL; when it is not, cov2d and colors may be
+ * NULL (not written: the records carry the conic and colour that compositing reads). */
 int gs_preprocess_fwd(void* stream, int64_t n, int sh_k, int sh_degree,
                       const float* means, const float* scales, const float* quats,
                       const float* opacities, const float* sh_coeffs, const uint8_t* mask,

@@ -252,13 +252,15 @@ __global__ __launch_bounds__(64) void preprocess_fwd_kernel(
   }
   means2d[2 * i] = m2x;
   means2d[2 * i + 1] = m2y;
-  reinterpret_cast<float4*>(cov2d)[i] = make_float4(p.c00, p.c01, p.c10, p.c11);
+  if (cov2d != nullptr) reinterpret_cast<float4*>(cov2d)[i] = make_float4(p.c00, p.c01, p.c10, p.c11);
   radii[i] = radius;
   valid[i] = v ? 1 : 0;
   depths[i] = p.z;
-  colors[3 * i] = col[0];
-  colors[3 * i + 1] = col[1];
-  colors[3 * i + 2] = col[2];
+  if (colors != nullptr) {
+    colors[3 * i] = col[0];
+    colors[3 * i + 1] = col[1];
+    colors[3 * i + 2] = col[2];
+  }
   if (records != nullptr) write_record(records + i * kRec, m2x, m2y, p.c00, p.c01, p.c11, logit, col);
 }
 
@@ -717,9 +719,9 @@ extern "C" int gs_preprocess_fwd(void* stream, int64_t n, int sh_k, int sh_degre
              (sh_degree + 1) * (sh_degree + 1));
   GS_REQUIRE(width > 0 && height > 0, "gs_preprocess_fwd: bad image size %dx%d", width, height);
   if (n == 0) return GS_OK;
-  GS_REQUIRE(means && scales && quats && opacities && sh_coeffs && w2c && means2d && cov2d && radii &&
-                 valid && depths && colors,
+  GS_REQUIRE(means && scales && quats && opacities && sh_coeffs && w2c && means2d && radii && valid && depths,
              "gs_preprocess_fwd: NULL array argument");
+  GS_REQUIRE((cov2d && colors) || records, "gs_preprocess_fwd: cov2d and colors may be NULL only with records");
   (void)width;
   (void)height;
 #define GS_PRE_FWD(D)                                                                                          \

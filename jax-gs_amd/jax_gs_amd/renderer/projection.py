@@ -9,11 +9,16 @@ from ..core.gaussians import Gaussians
 from ._buffers import as_mask, check_f32
 
 
-def preprocess(gaussians: Gaussians, camera: Camera, mask=None, sh_degree: int = 0, records: bool = True) -> dict:
+def preprocess(gaussians: Gaussians, camera: Camera, mask=None, sh_degree: int = 0, records: bool = True,
+               projected: bool = True) -> dict:
     """Fused projection + covariance + SH colour (+ compositing records) for every Gaussian.
 
     Returns a dict of device tensors: means2d [N,2], cov2d [N,2,2], radii [N] (float,
-    integer-valued), valid [N] (bool), depths [N], colors [N,3] and records [N,12]."""
+    integer-valued), valid [N] (bool), depths [N], colors [N,3] and records [N,12].
+    projected=False (with records) leaves cov2d and colors out (None): the records hold
+    the conic and colour compositing reads, and the renderer needs nothing else of them."""
+    if not projected and not records:
+        raise ValueError("preprocess: projected=False needs records=True")
     means = gaussians.means
     dev = means.device
     n = means.shape[0]
@@ -29,11 +34,11 @@ def preprocess(gaussians: Gaussians, camera: Camera, mask=None, sh_degree: int =
     m = as_mask(mask, n, dev)
     out = dict(
         means2d=torch.empty((n, 2), dtype=torch.float32, device=dev),
-        cov2d=torch.empty((n, 2, 2), dtype=torch.float32, device=dev),
+        cov2d=torch.empty((n, 2, 2), dtype=torch.float32, device=dev) if projected else None,
         radii=torch.empty((n,), dtype=torch.float32, device=dev),
         valid=torch.empty((n,), dtype=torch.uint8, device=dev),
         depths=torch.empty((n,), dtype=torch.float32, device=dev),
-        colors=torch.empty((n, 3), dtype=torch.float32, device=dev),
+        colors=torch.empty((n, 3), dtype=torch.float32, device=dev) if projected else None,
         records=torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=dev) if records else None,
     )
     _lib.call("gs_preprocess_fwd", _lib.stream_handle(dev), n, sh.shape[1], int(sh_degree), _lib.ptr(means),

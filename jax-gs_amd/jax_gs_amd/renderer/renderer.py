@@ -31,7 +31,7 @@ class _Render(torch.autograd.Function):
         W, H, fx, fy, cx, cy, sh_degree, capacity = static
         g = Gaussians(means, scales, quats, opac, sh)
         cam = Camera(W, H, fx, fy, cx, cy, w2c, None)
-        pre = preprocess(g, cam, mask=mask, sh_degree=sh_degree, records=True)
+        pre = preprocess(g, cam, mask=mask, sh_degree=sh_degree, records=True, projected=False)
         b = bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W, capacity=capacity,
                           want_tiles=False)
         # the gradient records the backward accumulates into, cleared by the forward's

@@ -107,7 +107,7 @@ def _train_step_fused(state, target_image, camera, optimizer, sh_degree, lambda_
     fields = [getattr(params, f) for f in _FIELDS]
     with torch.no_grad():
         active = state.active_mask.view(torch.bool)  # 0/1 bytes
-        pre = preprocess(params, camera, mask=active, sh_degree=sh_degree, records=True)
+        pre = preprocess(params, camera, mask=active, sh_degree=sh_degree, records=True, projected=False)
         b = bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W, want_tiles=False)
         bg = background_tensor(None, dev)
         grec = torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=dev)  # cleared by the forward

@@ -55,6 +55,11 @@ def _check_preprocess(sc, cuda):
     for k in ("means2d", "cov2d", "radii", "depths", "colors"):
         np.testing.assert_array_equal(_np(pre[k]), o[k], err_msg=k)
     np.testing.assert_array_equal(_np(pre["valid"]).astype(bool), o["valid"])
+    # the renderer's call writes no cov2d / colour arrays; everything else is identical
+    lean = preprocess(g, cam, mask=m, sh_degree=sc["sh_degree"], projected=False)
+    assert lean["cov2d"] is None and lean["colors"] is None
+    for k in ("means2d", "radii", "valid", "depths", "records"):
+        np.testing.assert_array_equal(_np(lean[k]), _np(pre[k]), err_msg=k)
     return pre, o
 
 
