@@ -358,9 +358,9 @@ __device__ inline GaussIn load_gauss(const float* __restrict__ means, const floa
   return a;
 }
 
-// Backward of one Gaussian.  shv: its SH row in LDS, overwritten with the SH
-// cotangent row (K triples, coefficients >= (D+1)^2 get 0); grow: its gradient record
-// in LDS.
+// Backward of one Gaussian.  shv: its SH row (registers or LDS), overwritten with the
+// SH cotangent row (K triples, coefficients >= (D+1)^2 get 0); grow: its gradient
+// record.
 template <int DEG>
 __device__ inline void preprocess_bwd_one(int64_t i, int K, const GaussIn& in, const float* __restrict__ w2c,
                                           float fx, float fy, const float* grow, float* shv,
@@ -526,9 +526,10 @@ __device__ inline void preprocess_bwd_one(int64_t i, int K, const GaussIn& in, c
   for (int k = 0; k < 4; ++k) g_quats[4 * i + k] = (gq[k] - p.qn[k] * qd) / p.qnorm;
 }
 
-// One wave per 64 Gaussians: the SH rows and gradient records are staged into LDS
-// with coalesced loads, and the SH cotangent rows leave through the same LDS rows
-// with coalesced stores (rows of K <= 16 triples, odd row stride 49).
+// One thread per Gaussian, one wave per 64 Gaussians.  Each lane loads its SH row and
+// gradient record straight into registers and stores its SH cotangent row from them
+// (16-byte accesses when rows are 16-byte aligned); no LDS, so occupancy is set by
+// registers alone.
 template <int DEG>
 __global__ __launch_bounds__(64) void preprocess_bwd_kernel(
     int64_t n, int K, const float* __restrict__ means, const float* __restrict__ scales,
@@ -537,32 +538,29 @@ __global__ __launch_bounds__(64) void preprocess_bwd_kernel(
     float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_quats,
     float* __restrict__ g_opac, float* __restrict__ g_sh) {
   constexpr int NB = (DEG + 1) * (DEG + 1);
-  constexpr int LS = 49, LG = 13;
-  __shared__ float shs[64 * LS];
-  __shared__ float grs[64 * LG];
-  const int lane = threadIdx.x;
-  const int64_t g0 = (int64_t)blockIdx.x * 64;
   const int KC = 3 * K;
-  const int64_t i = g0 + lane;
-  // per-Gaussian inputs first (clamped index) so that their loads overlap the staging
-  const GaussIn in = load_gauss(means, scales, quats, opac, i < n ? i : n - 1);
-  stage_rows<3 * NB>(sh, g0, n, (int64_t)KC, shs, LS, lane);
-  stage_rows<kRec>(grec, g0, n, (int64_t)kRec, grs, LG, lane);
-  __syncthreads();
-  if (i < n)
-    preprocess_bwd_one<DEG>(i, K, in, w2c, fx, fy, grs + lane * LG, shs + lane * LS, g_means, g_scales, g_quats,
-                            g_opac);
-  __syncthreads();
-  // rows g0.. are contiguous in g_sh: consecutive lanes store consecutive floats.
-  // Row of element e: e / KC computed as floor((e + 0.5) / KC) in float, exact since
-  // (e + 0.5) / KC is at least 0.5 / KC away from an integer and e < 3072.
-  const float inv = 1.0f / (float)KC;
-  const int64_t rows = n - g0 < 64 ? n - g0 : 64;
-  const int total = (int)rows * KC;
-  float* dst = g_sh + g0 * KC;
-  for (int e = lane; e < total; e += 64) {
-    const int r = (int)(((float)e + 0.5f) * inv);
-    dst[e] = shs[r * LS + (e - r * KC)];
+  const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  // every input load of the lane is issued before the first use (clamped index)
+  const int64_t ic = i < n ? i : n - 1;
+  const GaussIn in = load_gauss(means, scales, quats, opac, ic);
+  const bool aligned = (KC & 3) == 0 && (reinterpret_cast<uintptr_t>(sh) & 15) == 0 &&
+                       (reinterpret_cast<uintptr_t>(g_sh) & 15) == 0;
+  float shv[3 * NB], grow[kRec];
+  load_row<3 * NB>(sh + ic * KC, aligned, shv);
+  load_row<kRec>(grec + ic * kRec, (reinterpret_cast<uintptr_t>(grec) & 15) == 0, grow);
+  if (i >= n) return;
+  // K = NB: the register row holds the first 3 NB values only; the rest is zeroed below
+  preprocess_bwd_one<DEG>(i, NB, in, w2c, fx, fy, grow, shv, g_means, g_scales, g_quats, g_opac);
+  float* __restrict__ dst = g_sh + i * KC;
+  if (aligned && (3 * NB) % 4 == 0) {
+#pragma unroll
+    for (int t = 0; t < 3 * NB / 4; ++t)
+      reinterpret_cast<float4*>(dst)[t] = make_float4(shv[4 * t], shv[4 * t + 1], shv[4 * t + 2], shv[4 * t + 3]);
+    for (int t = 3 * NB / 4; t < KC / 4; ++t) reinterpret_cast<float4*>(dst)[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+  } else {
+#pragma unroll
+    for (int t = 0; t < 3 * NB; ++t) dst[t] = shv[t];
+    for (int t = 3 * NB; t < KC; ++t) dst[t] = 0.0f;
   }
 }
 
