@@ -552,13 +552,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
             gc2 = fmaf(w, g2[i], gc2);
             const float cg = fmaf(e.b, g2[i], fmaf(e.g, g1[i], e.r * g0[i]));
             const float dR = cg - Rg[i];
-            const float dal = Tk * dR;
+            // dL/dalpha = T dR; d alpha/d power = araw below the cap, where alpha = araw,
+            // so dL/dpower = (alpha T) dR = w dR (one product instead of two)
+            const float wd = w * dR;
             Rg[i] = fmaf(al, dR, Rg[i]);  // alpha c.g + (1 - alpha) Rg
             Tr[i] = Tk;
             // min(araw, 0.99): the cotangent passes below the cap, half of it at a tie
-            float dae = araw < 0.99f ? dal : 0.0f;
-            if (__builtin_expect(araw == 0.99f, 0)) dae = 0.5f * dal;
-            const float dpw = dae * araw;  // d/d power (natural units)
+            // (where alpha = araw too)
+            float dpw = araw < 0.99f ? wd : 0.0f;  // d/d power (natural units)
+            if (__builtin_expect(araw == 0.99f, 0)) dpw = 0.5f * wd;
             P += dpw;
             const float dpy = dpw * dy;
             Q += dpy;
