@@ -440,7 +440,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
 }
 
 template <int PPT>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void composite_bwd_kernel(
+__device__ __forceinline__ void composite_bwd_body(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
     const float* __restrict__ gimg, const float* __restrict__ finalT, const int32_t* __restrict__ ncontrib,
@@ -591,6 +591,25 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void
   }
 }
 
+#define GS_BWD_PARAMS                                                                                       \
+  const float4 *__restrict__ rec, int num_g, const int32_t *__restrict__ gids, int64_t n_entries,               \
+      const int32_t *__restrict__ ranges, int W, int H, int TX, int T, const float *__restrict__ bg,            \
+      const float *__restrict__ gimg, const float *__restrict__ finalT, const int32_t *__restrict__ ncontrib, \
+      float *__restrict__ grec, const int32_t *__restrict__ order
+#define GS_BWD_ARGS rec, num_g, gids, n_entries, ranges, W, H, TX, T, bg, gimg, finalT, ncontrib, grec, order
+
+// The backward in two register budgets.  Capped at 64 VGPRs (8 waves per SIMD) it runs
+// best when a SIMD holds few of the launch's waves (cfg4, 3600 tiles: 250 vs 282 us);
+// with the compiler's own allocation (68 VGPRs, 7 waves per SIMD) it runs best when the
+// launch fills every slot (cfg2, 8160 tiles: 351 vs 369 us).  The host picks by tile count.
+template <int PPT>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void composite_bwd_kernel(GS_BWD_PARAMS) {
+  composite_bwd_body<PPT>(GS_BWD_ARGS);
+}
+__global__ __launch_bounds__(64) void composite_bwd_wide_kernel(GS_BWD_PARAMS) { composite_bwd_body<4>(GS_BWD_ARGS); }
+#undef GS_BWD_PARAMS
+#undef GS_BWD_ARGS
+
 // Clears the gradient records (and the 3 background cotangents when given).
 __global__ void zero_grads_kernel(float4* __restrict__ p, int64_t n4, float* __restrict__ gbg) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -678,6 +697,8 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(int32_t* __restrict__ 
 
 // Large images have enough tiles to fill the GPU with one wave per tile.
 inline int pick_ppt(int T) { return T >= 2048 ? 4 : 1; }
+// tiles from which the backward uses its uncapped register budget (6 waves per SIMD)
+constexpr int kBwdWideTiles = 6 * 1024;
 
 }  // namespace
 }  // namespace gs
@@ -744,7 +765,11 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
   const int TX = (width + kTile - 1) / kTile, TY = (height + kTile - 1) / kTile;
   const int T = TX * TY;
   const int nblk = tile_blocks(TX, TY);
-  if (pick_ppt(T) == 4) {
+  if (pick_ppt(T) == 4 && T >= kBwdWideTiles) {
+    hipLaunchKernelGGL(composite_bwd_wide_kernel, dim3(nblk), dim3(64), 0, s, (const float4*)records, (int)n,
+                       sorted_gids, n_entries, ranges, width, height, TX, T, background, grad_image, final_T,
+                       n_contrib, grad_records, tile_order);
+  } else if (pick_ppt(T) == 4) {
     hipLaunchKernelGGL(composite_bwd_kernel<4>, dim3(nblk), dim3(64), 0, s, (const float4*)records, (int)n,
                        sorted_gids, n_entries, ranges, width, height, TX, T, background, grad_image, final_T,
                        n_contrib, grad_records, tile_order);
