@@ -600,13 +600,14 @@ __device__ __forceinline__ void composite_bwd_body(
 
 // The backward in two register budgets.  Capped at 64 VGPRs (8 waves per SIMD) it runs
 // best when a SIMD holds few of the launch's waves (cfg4, 3600 tiles: 250 vs 282 us);
-// with the compiler's own allocation (68 VGPRs, 7 waves per SIMD) it runs best when the
-// launch fills every slot (cfg2, 8160 tiles: 351 vs 369 us).  The host picks by tile count.
+// scheduled for 6 waves per SIMD (68 VGPRs, so 7 are resident) it runs best when the
+// launch fills every slot (cfg2, 8160 tiles: 344 us, against 351 with no occupancy target
+// and 369 capped).  The host picks by tile count.
 template <int PPT>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void composite_bwd_kernel(GS_BWD_PARAMS) {
   composite_bwd_body<PPT>(GS_BWD_ARGS);
 }
-__global__ __launch_bounds__(64) void composite_bwd_wide_kernel(GS_BWD_PARAMS) { composite_bwd_body<4>(GS_BWD_ARGS); }
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6, 6))) void composite_bwd_wide_kernel(GS_BWD_PARAMS) { composite_bwd_body<4>(GS_BWD_ARGS); }
 #undef GS_BWD_PARAMS
 #undef GS_BWD_ARGS
 
