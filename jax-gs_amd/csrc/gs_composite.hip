@@ -435,7 +435,14 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
     }
   }
   // walk length of the tile (first wave of the tile): the backward's cost estimate
-  if (tile_cost && part == 0 && lane == 0) tile_cost[tile] = walked;
+  // (two waves per tile: each stores its own length in one 16-bit half, the order takes
+  // the longer; lengths are at most kMaxTileEntries)
+  if (tile_cost && lane == 0) {
+    if (WPT == 2)
+      reinterpret_cast<uint16_t*>(tile_cost)[2 * tile + part] = (uint16_t)walked;
+    else if (part == 0)
+      tile_cost[tile] = walked;
+  }
   clear_slice();
 }
 
@@ -673,8 +680,9 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(int32_t* __restrict__ 
   start[tid] = 0;
   __syncthreads();
   for (int t = tid; t < T; t += 1024) {
-    const int c = order[t];
-    const int bk = min(max(c, 0) >> 3, kOrderBuckets - 1);
+    const uint32_t w = (uint32_t)order[t];
+    const int c = (int)max(w & 0xFFFFu, w >> 16);  // the longer of the tile's (one or two) walks
+    const int bk = min(c >> 3, kOrderBuckets - 1);
     bucket[t] = (uint16_t)bk;
     atomicAdd(&start[bk], 1);
   }
@@ -700,6 +708,11 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(int32_t* __restrict__ 
 inline int pick_ppt(int T) { return T >= 2048 ? 4 : 1; }
 // tiles from which the backward uses its uncapped register budget (6 waves per SIMD)
 constexpr int kBwdWideTiles = 6 * 1024;
+// Tiles from which the forward gives a tile one wave (four pixels per lane); below that (and
+// from 2048 tiles) two waves of eight rows each: at 3600 tiles a launch holds 3-4 waves per
+// SIMD, and halving the work units evens them out (cfg4 forward 189 -> 176 us) where at
+// 8160 tiles the duplicated per-entry work costs more than it balances (227 -> 255 us).
+constexpr int kFwdOneWaveTiles = 6 * 1024;
 
 }  // namespace
 }  // namespace gs
@@ -722,8 +735,12 @@ extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, c
   GS_REQUIRE(clear_records == nullptr || ((uintptr_t)clear_records & 15) == 0,
              "gs_composite_fwd: clear_records must be 16-byte aligned");
   const int64_t n4_clear = clear_records ? n * kRec / 4 : 0;  // kRec = 12: whole float4s
-  if (pick_ppt(T) == 4) {
+  if (pick_ppt(T) == 4 && T >= kFwdOneWaveTiles) {
     hipLaunchKernelGGL(composite_fwd_kernel<4>, dim3(nblk), dim3(64), 0, s, (const float4*)records, (int)n,
+                       sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib,
+                       tile_order, (float4*)clear_records, n4_clear);
+  } else if (pick_ppt(T) == 4) {
+    hipLaunchKernelGGL(composite_fwd_kernel<2>, dim3(nblk * 2), dim3(64), 0, s, (const float4*)records, (int)n,
                        sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib,
                        tile_order, (float4*)clear_records, n4_clear);
   } else {

@@ -105,7 +105,7 @@ def _render_both(sc, cuda, seed_kind="l1"):
 
 
 @pytest.mark.parametrize("cfg,n,w,h", [(0, 3000, 128, 96), (1, 4000, 200, 150), (3, 6000, 160, 96),
-                                       (4, 5000, 160, 90)])
+                                       (4, 5000, 160, 90), (2, 3000, 1024, 768)])
 def test_small_scene_parity(cuda, cfg, n, w, h):
     sc = scenes.make_scene(cfg, n=n, width=w, height=h)
     pre, pre_o = _check_preprocess(sc, cuda)
