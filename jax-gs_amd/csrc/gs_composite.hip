@@ -16,7 +16,7 @@
 // to a Gaussian is shared by the lane's pixels.  Waves are independent (no LDS, no
 // barriers).  With PPT = 4 a wave covers the whole tile (used for large images);
 // PPT = 1 uses four waves per tile for small images that would otherwise leave CUs
-// idle.
+// idle; the forward of mid-size images uses PPT = 2 (two waves per tile).
 //
 // Culling: a Gaussian is binned to every tile its square 3-sigma box touches, but its
 // "power > -10" region is an ellipse, and for about a third of the (tile, entry) pairs
