@@ -67,7 +67,7 @@ const char* gs_last_error(void);
 /* 2: gs_composite_fwd/bwd take the tile order; gs_mse_loss, gs_l1_ssim, gs_adam_step,
  * gs_densify_and_prune, gs_reset_opacities, gs_ply_pack/unpack, gs_preprocess_bwd_adam,
  * gs_l1_ssim_terms.  3: gs_l1_loss_bwd, gs_mse_loss_bwd.  4: gs_composite_fwd takes
- * clear_records, gs_composite_bwd accumulate. */
+ * clear_records, gs_composite_bwd accumulate.  5: gs_composite_fwd takes window_rule. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -130,10 +130,19 @@ int gs_tile_ranges(void* stream, const int32_t* sorted_tiles, int64_t length, in
  * launch order of gs_composite_bwd (residuals for gs_composite_bwd; each may be NULL).
  * clear_records (may be NULL): an [n, GS_REC_STRIDE] array the launch sets to zero on
  * the side (its waves are arithmetic-bound, so the stores cost nothing), for a later
- * gs_composite_bwd with accumulate = 1. */
+ * gs_composite_bwd with accumulate = 1.
+ * window_rule selects which ids entry k = 512 c + i of a tile reads:
+ *   0  its own entries, sorted_gids[ranges[t] + k] (rasterizer_tpu.py:90-97, and
+ *      rasterizer.py:184-190 whenever no chunk starts within 512 entries of the end);
+ *   1  the default path's chunk windows (rasterizer.py:184-190): sorted_gids[s + i] with
+ *      s = min(ranges[t] + 512 c, n_entries - 512), which for a chunk near the end of
+ *      the array reads the array's last 512 entries (n_entries >= 512; shorter arrays,
+ *      which the reference cannot slice, read as 0).
+ * gs_composite_bwd replays rule 0. */
 int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                      int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
-                     float* image, float* final_T, int32_t* n_contrib, int32_t* tile_order, float* clear_records);
+                     float* image, float* final_T, int32_t* n_contrib, int32_t* tile_order, float* clear_records,
+                     int window_rule);
 
 /* Vector-Jacobian product of gs_composite_fwd (JAX autodiff of render_tiles).
  * tile_order is the forward's (NULL: a fixed order; results agree up to the order of

@@ -259,8 +259,18 @@ struct Probe {
   float mx, my, A, B, C;
 };
 
-__device__ inline int probe_gid(const int32_t* __restrict__ gids, int start, int k, int n, int num_g) {
-  return (k >= 0 && k < n) ? clamp_gid(gids[start + k], num_g) : -1;
+// Id of entry k of a tile whose entries start at `start` (-1 past the n entries).
+// win_hi < 0: the tile's own entries (rasterizer_tpu.py:90-97 gathers them one by one).
+// win_hi >= 0: the default path's chunk windows (rasterizer.py:184-190): chunk c = k / 512
+// reads a 512-entry slice whose start, start + 512 c, is clamped to [0, win_hi] with
+// win_hi = (array length) - 512, so a chunk that starts within 512 entries of the end
+// of the array reads the array's last 512 entries instead.
+__device__ inline int probe_gid(const int32_t* __restrict__ gids, int start, int k, int n, int num_g,
+                                int64_t win_hi = -1) {
+  if (k < 0 || k >= n) return -1;
+  int64_t at = (int64_t)start + k;
+  if (win_hi >= 0 && (int64_t)start + (k & ~(kBlock - 1)) > win_hi) at = win_hi + (k & (kBlock - 1));
+  return clamp_gid(gids[at], num_g);
 }
 
 __device__ inline Probe probe_load(const float4* __restrict__ rec, int g) {
@@ -286,7 +296,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
     float* __restrict__ img, float* __restrict__ finalT, int32_t* __restrict__ ncontrib,
-    int32_t* __restrict__ tile_cost, float4* __restrict__ clear, int64_t n_clear) {
+    int32_t* __restrict__ tile_cost, float4* __restrict__ clear, int64_t n_clear, int64_t win_hi) {
   constexpr int WPT = 4 / PPT;  // waves per tile
   // Every workgroup clears its slice of the caller's array after its own outputs (stores
   // and loads share one wait counter, so stores issued before the walk would hold up its
@@ -327,12 +337,12 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
 
   bool done = false;
   int walked = 0, next_check = 8;
-  int g_ahead = probe_gid(gids, start, 64 + lane, n, num_g);
-  Probe p_next = probe_load(rec, probe_gid(gids, start, lane, n, num_g));
+  int g_ahead = probe_gid(gids, start, 64 + lane, n, num_g, win_hi);
+  Probe p_next = probe_load(rec, probe_gid(gids, start, lane, n, num_g, win_hi));
   for (int b0 = 0; b0 < n && !done; b0 += 64) {
     const Probe pr = p_next;
     p_next = probe_load(rec, g_ahead);
-    g_ahead = probe_gid(gids, start, b0 + 128 + lane, n, num_g);
+    g_ahead = probe_gid(gids, start, b0 + 128 + lane, n, num_g, win_hi);
     const int gl = pr.g;
     uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
     // Survivors are walked in groups of G (G = 2 when a lane holds one pixel): the
@@ -722,8 +732,9 @@ using namespace gs;
 extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                                 int64_t n_entries, const int32_t* ranges, int width, int height,
                                 const float* background, float* image, float* final_T, int32_t* n_contrib,
-                                int32_t* tile_order, float* clear_records) {
+                                int32_t* tile_order, float* clear_records, int window_rule) {
   GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "gs_composite_fwd: n out of range");
+  GS_REQUIRE(window_rule == 0 || window_rule == 1, "gs_composite_fwd: window_rule must be 0 or 1");
   GS_REQUIRE(n_entries >= 0, "gs_composite_fwd: n_entries must be >= 0");
   GS_REQUIRE(width > 0 && height > 0, "gs_composite_fwd: bad image size %dx%d", width, height);
   GS_REQUIRE(ranges && background && image, "gs_composite_fwd: NULL argument");
@@ -735,18 +746,20 @@ extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, c
   GS_REQUIRE(clear_records == nullptr || ((uintptr_t)clear_records & 15) == 0,
              "gs_composite_fwd: clear_records must be 16-byte aligned");
   const int64_t n4_clear = clear_records ? n * kRec / 4 : 0;  // kRec = 12: whole float4s
+  // the reference slices 512 entries per chunk, which needs an array of at least 512
+  const int64_t win_hi = (window_rule == 1 && n_entries >= kBlock) ? n_entries - kBlock : -1;
   if (pick_ppt(T) == 4 && T >= kFwdOneWaveTiles) {
     hipLaunchKernelGGL(composite_fwd_kernel<4>, dim3(nblk), dim3(64), 0, s, (const float4*)records, (int)n,
                        sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib,
-                       tile_order, (float4*)clear_records, n4_clear);
+                       tile_order, (float4*)clear_records, n4_clear, win_hi);
   } else if (pick_ppt(T) == 4) {
     hipLaunchKernelGGL(composite_fwd_kernel<2>, dim3(nblk * 2), dim3(64), 0, s, (const float4*)records, (int)n,
                        sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib,
-                       tile_order, (float4*)clear_records, n4_clear);
+                       tile_order, (float4*)clear_records, n4_clear, win_hi);
   } else {
     hipLaunchKernelGGL(composite_fwd_kernel<1>, dim3(nblk * 4), dim3(64), 0, s, (const float4*)records, (int)n,
                        sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib,
-                       tile_order, (float4*)clear_records, n4_clear);
+                       tile_order, (float4*)clear_records, n4_clear, win_hi);
   }
   GS_LAUNCH_CHECK("composite_fwd_kernel");
   if (tile_order) {

@@ -37,7 +37,7 @@ _SIGS = {
     "gs_bin_workspace_size": [_I64, _I, _I, _I64],
     "gs_bin": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _SZ, _P, _P, _P, _P],
     "gs_tile_ranges": [_P, _P, _I64, _I, _P],
-    "gs_composite_fwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P],
+    "gs_composite_fwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _I],
     "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I],
     "gs_preprocess_bwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P, _P],
     "gs_l1_loss": [_P, _I64, _P, _P, _P, _P],
@@ -66,7 +66,7 @@ _RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_
 _lib = None
 
 
-ABI_VERSION = 4  # gs_abi_version() of the signatures bound below
+ABI_VERSION = 5  # gs_abi_version() of the signatures bound below
 
 
 class NativeLibraryMissing(RuntimeError):

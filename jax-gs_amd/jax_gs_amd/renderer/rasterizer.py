@@ -93,12 +93,16 @@ def composite_records(means2D, cov2D, opacities, colors) -> torch.Tensor:
 
 
 def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Tensor, H: int, W: int,
-              background: torch.Tensor, residuals: bool = True, clear_records: torch.Tensor | None = None):
+              background: torch.Tensor, residuals: bool = True, clear_records: torch.Tensor | None = None,
+              window_rule: int = 0):
     """Front-to-back compositing; returns (image [H,W,3], final_T [H,W], n_contrib [H,W],
     tile_order [T]), the last three the backward's residuals (None unless residuals):
     tile_order lists the tiles longest walk first, the backward's launch order.
     clear_records ([n, GS_REC_STRIDE] float32), when given, is set to zero by the same launch
-    (for a backward that accumulates into it)."""
+    (for a backward that accumulates into it).  window_rule 0 reads each tile's own
+    entries (rasterizer_tpu.py:90-97), 1 the default path's clamped 512-entry chunk
+    windows (rasterizer.py:184-190), which differ only for chunks that start within 512
+    entries of the end of sorted_gids."""
     dev = records.device
     _, _, T = num_tiles(W, H)
     image = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
@@ -107,20 +111,36 @@ def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Te
     order = torch.empty((T,), dtype=torch.int32, device=dev) if residuals else None
     _lib.call("gs_composite_fwd", _lib.stream_handle(dev), records.shape[0], _lib.ptr(records),
               _lib.ptr(sorted_gids), sorted_gids.shape[0], _lib.ptr(ranges), int(W), int(H), _lib.ptr(background), _lib.ptr(image),
-              _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(clear_records))
+              _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(clear_records), int(window_rule))
     return image, fT, nc, order
 
 
-def render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W,
-                 tile_size: int = TILE_SIZE, background=None):
-    """rasterizer.py:119-248 (forward).  Entries of tile t are the ones whose sorted
-    tile id equals t (searchsorted ranges), capped at 4096 per tile."""
-    if tile_size != TILE_SIZE:
-        raise ValueError("only 16x16 tiles are supported (rasterizer.py:6)")
+def _render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W, background,
+                  window_rule):
     dev = means2D.device
     _, _, T = num_tiles(W, H)
     rec = composite_records(means2D, cov2D, opacities, colors)
     ranges = tile_ranges(sorted_tile_ids, T)
     bg = background_tensor(background, dev)
-    image, _, _, _ = composite(rec, sorted_gaussian_ids.to(torch.int32).contiguous(), ranges, H, W, bg, residuals=False)
+    image, _, _, _ = composite(rec, sorted_gaussian_ids.to(torch.int32).contiguous(), ranges, H, W, bg,
+                               residuals=False, window_rule=window_rule)
     return image
+
+
+def render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W,
+                 tile_size: int = TILE_SIZE, background=None):
+    """rasterizer.py:119-248 (forward).  Entries of tile t are the ones whose sorted
+    tile id equals t (searchsorted ranges), capped at 4096 per tile, read through the
+    reference's 512-entry chunk windows: a chunk that starts within 512 entries of the
+    end of the arrays reads their last 512 entries (rasterizer.py:184-190)."""
+    if tile_size != TILE_SIZE:
+        raise ValueError("only 16x16 tiles are supported (rasterizer.py:6)")
+    return _render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W, background,
+                         window_rule=1)
+
+
+def render_tiles_tpu(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W, background=None):
+    """rasterizer_tpu.py:13-135 (forward): the same compositing with every entry of a
+    tile gathered one by one (its own entries, whatever its position in the arrays)."""
+    return _render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W, background,
+                         window_rule=0)

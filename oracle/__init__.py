@@ -45,7 +45,17 @@ def lib():
         _lib = ctypes.CDLL(_LIBPATH)
         _lib.gso_expf.restype = ctypes.c_float
         _lib.gso_expf.argtypes = [ctypes.c_float]
+        _lib.gso_set_threads.argtypes = [ctypes.c_int]
     return _lib
+
+
+def set_threads(n: int) -> None:
+    """Threads of the oracle's parallel loops (OpenMP; default: OMP_NUM_THREADS or all CPUs)."""
+    lib().gso_set_threads(int(n))
+
+
+def threads() -> int:
+    return int(lib().gso_max_threads())
 
 
 def _p(a):
@@ -96,8 +106,8 @@ def tile_interactions(means2d, radii, valid, depths, H, W, dtype=np.float32):
     v = _c(valid, np.uint8)
     n = means2d.shape[0]
     Lsz = max(256 * n, BLOCK_SIZE)
-    st = np.zeros((Lsz,), np.int32)
-    sg = np.zeros((Lsz,), np.int32)
+    st = np.empty((Lsz,), np.int32)  # every slot is written
+    sg = np.empty((Lsz,), np.int32)
     cnt = ctypes.c_int64(0)
     fn = getattr(lib(), "gso_tile_interactions_" + _sfx(dtype))
     rc = fn(ctypes.c_int64(n), _p(means2d), _p(radii), _p(v), _p(depths), ctypes.c_int(W), ctypes.c_int(H),
@@ -163,7 +173,8 @@ def preprocess_bwd(means, scales, quats, sh, w2c, fx, fy, sh_degree, g_means2d, 
 
 def tile_boundaries(sorted_tiles, num_tiles):
     """renderer.py:60: jnp.searchsorted(sorted_tile_ids, arange(T+1)) (side='left')."""
-    return np.searchsorted(np.asarray(sorted_tiles), np.arange(num_tiles + 1), side="left").astype(np.int32)
+    st = np.asarray(sorted_tiles)
+    return np.searchsorted(st, np.arange(num_tiles + 1, dtype=st.dtype), side="left").astype(np.int32)
 
 
 def extras_from(pre, sorted_tiles, n_interactions, H, W):

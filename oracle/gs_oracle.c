@@ -10,11 +10,20 @@
  * check the float restatement and its backward by finite differences).
  *
  * Build (also done by __graft_entry__.build() and oracle/Makefile):
- *   gcc -O2 -std=c99 -ffp-contract=off -fno-fast-math -shared -fPIC gs_oracle.c -o libgsoracle.so -lm
+ *   gcc -O2 -std=c99 -fopenmp -ffp-contract=off -fno-fast-math -shared -fPIC gs_oracle.c -o libgsoracle.so -lm
  * -ffp-contract=off keeps every a*b+c as two roundings, as in the reference's
  * float32 expressions evaluated by XLA:CPU without fast-math.
+ *
+ * Threads (OpenMP): per-Gaussian loops are split over Gaussians, compositing over
+ * tiles, the slot sort over contiguous blocks (a stable parallel LSD radix sort).
+ * Every output is independent of the thread count except the compositing backward's
+ * per-Gaussian sums, which are added per thread and then over the threads in order
+ * (the reference's scatter-adds have no specified order either).
  */
+#define _GNU_SOURCE
 #include <math.h>
+#include <omp.h>
+#include <sys/mman.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -54,6 +63,22 @@ float gso_expf(float x) {
   }
   s.u = (uint32_t)(k + 127) << 23;
   return p * s.f;
+}
+
+/* Large scratch arrays (the 256*n slot keys) on 2 MiB pages: 4 KiB page faults on
+ * gigabytes of fresh memory cost more than the sort itself when threads fault in
+ * parallel.  gso_hint_huge asks the same for an existing range (the caller's output
+ * arrays); both are hints only. */
+static void gso_hint_huge(void* p, size_t bytes) {
+  const uintptr_t a = ((uintptr_t)p + ((1u << 21) - 1)) & ~(uintptr_t)((1u << 21) - 1);
+  const uintptr_t e = ((uintptr_t)p + bytes) & ~(uintptr_t)((1u << 21) - 1);
+  if (e > a) madvise((void*)a, e - a, MADV_HUGEPAGE);
+}
+static void* gso_big_alloc(size_t bytes) {
+  void* p = NULL;
+  if (posix_memalign(&p, (size_t)1 << 21, bytes ? bytes : 1) != 0) return NULL;
+  gso_hint_huge(p, bytes);
+  return p;
 }
 
 /* gso_expf over an array (vectorised callers in the NumPy layer). */
@@ -96,4 +121,10 @@ static double gso_sigmoid(double x) { return 1.0 / (1.0 + exp(-x)); }
 #undef CEIL
 #undef FLOOR
 
-int gso_abi_version(void) { return 1; }
+int gso_abi_version(void) { return 2; }
+
+/* Threads used by the parallel loops (0 or less: leave OpenMP's default). */
+void gso_set_threads(int n) {
+  if (n > 0) omp_set_num_threads(n);
+}
+int gso_max_threads(void) { return omp_get_max_threads(); }

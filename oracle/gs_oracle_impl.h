@@ -150,6 +150,7 @@ int FN(gso_preprocess)(int64_t n, int K, int deg, const REAL* means, const REAL*
   (void)opac;
   (void)W;
   (void)H;
+#pragma omp parallel for schedule(static)
   for (i = 0; i < n; ++i) {
     FN(proj_t) p;
     REAL v[3], nrm, d[3];
@@ -188,16 +189,19 @@ int FN(gso_tile_interactions)(int64_t n, const REAL* means2d, const REAL* radii,
   uint32_t *key = NULL, *val = NULL, *k2 = NULL, *v2 = NULL;
   int64_t i, cnt = 0;
   int pass;
+  gso_hint_huge(sorted_tiles, sizeof(int32_t) * (size_t)L);
+  gso_hint_huge(sorted_gids, sizeof(int32_t) * (size_t)L);
   if (total > 0) {
-    key = (uint32_t*)malloc(sizeof(uint32_t) * total);
-    val = (uint32_t*)malloc(sizeof(uint32_t) * total);
-    k2 = (uint32_t*)malloc(sizeof(uint32_t) * total);
-    v2 = (uint32_t*)malloc(sizeof(uint32_t) * total);
+    key = (uint32_t*)gso_big_alloc(sizeof(uint32_t) * total);
+    val = (uint32_t*)gso_big_alloc(sizeof(uint32_t) * total);
+    k2 = (uint32_t*)gso_big_alloc(sizeof(uint32_t) * total);
+    v2 = (uint32_t*)gso_big_alloc(sizeof(uint32_t) * total);
     if (!key || !val || !k2 || !v2) {
       free(key); free(val); free(k2); free(v2);
       return -1;
     }
   }
+#pragma omp parallel for schedule(static) reduction(+ : cnt)
   for (i = 0; i < n; ++i) {
     const REAL mx = means2d[2 * i], my = means2d[2 * i + 1], r = radii[i];
     const REAL minx = FN(r_min)(FN(r_max)(mx - r, (REAL)0), (REAL)(W - 1));
@@ -228,22 +232,51 @@ int FN(gso_tile_interactions)(int64_t n, const REAL* means2d, const REAL* radii,
         cnt += in_range;
       }
   }
-  /* stable LSD radix sort, 4 x 8 bits */
-  for (pass = 0; pass < 4 && total > 0; ++pass) {
-    int64_t hist[257];
-    const int sh = pass * 8;
-    uint32_t* t;
-    memset(hist, 0, sizeof(hist));
-    for (i = 0; i < total; ++i) hist[((key[i] >> sh) & 255) + 1]++;
-    for (i = 0; i < 256; ++i) hist[i + 1] += hist[i];
-    for (i = 0; i < total; ++i) {
-      const int64_t dst = hist[(key[i] >> sh) & 255]++;
-      k2[dst] = key[i];
-      v2[dst] = val[i];
+  /* stable LSD radix sort, 4 x 8 bits.  Each thread owns a contiguous block of the
+   * array; per-thread digit counts are turned into destinations in (digit, thread)
+   * order, so equal digits keep their input order across blocks (stability). */
+  if (total > 0) {
+    const int nt_max = omp_get_max_threads();
+    int64_t* th = (int64_t*)calloc((size_t)nt_max * 256, sizeof(int64_t));
+    if (!th) {
+      free(key); free(val); free(k2); free(v2);
+      return -1;
     }
-    t = key; key = k2; k2 = t;
-    t = val; val = v2; v2 = t;
+    for (pass = 0; pass < 4; ++pass) {
+      const int sh = pass * 8;
+      uint32_t* t;
+#pragma omp parallel num_threads(nt_max)
+      {
+        const int tid = omp_get_thread_num(), nth = omp_get_num_threads();
+        const int64_t lo = total * tid / nth, hi = total * (tid + 1) / nth;
+        int64_t* h = th + (size_t)tid * 256;
+        int64_t j;
+        memset(h, 0, sizeof(int64_t) * 256);
+        for (j = lo; j < hi; ++j) h[(key[j] >> sh) & 255]++;
+#pragma omp barrier
+#pragma omp single
+        {
+          int64_t run = 0, c;
+          int dg, tt;
+          for (dg = 0; dg < 256; ++dg)
+            for (tt = 0; tt < nth; ++tt) {
+              c = th[(size_t)tt * 256 + dg];
+              th[(size_t)tt * 256 + dg] = run;
+              run += c;
+            }
+        }
+        for (j = lo; j < hi; ++j) {
+          const int64_t dst = h[(key[j] >> sh) & 255]++;
+          k2[dst] = key[j];
+          v2[dst] = val[j];
+        }
+      }
+      t = key; key = k2; k2 = t;
+      t = val; val = v2; v2 = t;
+    }
+    free(th);
   }
+#pragma omp parallel for schedule(static)
   for (i = 0; i < L; ++i) {
     if (i < total) {
       const int32_t k = (int32_t)(key[i] ^ 0x80000000u);
@@ -342,6 +375,7 @@ int FN(gso_render_tiles)(int64_t n, const REAL* means2d, const REAL* cov2d, cons
   const int TX = (W + 15) / 16, TY = (H + 15) / 16, T = TX * TY;
   int t;
   (void)n;
+#pragma omp parallel for schedule(dynamic, 1)
   for (t = 0; t < T; ++t) {
     const int tx = t % TX, ty = t / TX;
     FN(tile_t) ts;
@@ -404,116 +438,162 @@ int FN(gso_render_tiles_bwd)(int64_t n, const REAL* means2d, const REAL* cov2d, 
                              int W, int H, const REAL* bg, int tpu_gather, const REAL* g_image, REAL* g_means2d,
                              REAL* g_cov2d, REAL* g_opac, REAL* g_colors, REAL* g_bg) {
   const int TX = (W + 15) / 16, TY = (H + 15) / 16, T = TX * TY;
-  /* per-Gaussian cotangents of the prologue outputs */
-  REAL* g_ic = (REAL*)calloc((size_t)(n > 0 ? n : 1) * 3, sizeof(REAL)); /* ic00, ic01_2, ic11 */
-  REAL* g_sig = (REAL*)calloc((size_t)(n > 0 ? n : 1), sizeof(REAL));
-  REAL* Tk = (REAL*)malloc(sizeof(REAL) * 4097);
-  int64_t* gk = (int64_t*)malloc(sizeof(int64_t) * 4096);
-  int t;
+  /* Per-thread cotangent accumulators (the reference's gather transposes are
+   * scatter-adds, whose order XLA leaves unspecified): 9 values per Gaussian, laid out
+   * [ic00, ic01_2, ic11 | sigmoid | means2d x, y | colour r, g, b] blocks of n each,
+   * summed in thread order after the tiles. */
+  const int nt_max = omp_get_max_threads();
+  const size_t nn = (size_t)(n > 0 ? n : 1);
+  REAL* acc = (REAL*)calloc(nn * 9 * (size_t)nt_max, sizeof(REAL));
+  REAL* bgacc = (REAL*)calloc((size_t)nt_max * 3, sizeof(REAL));
   int64_t g;
-  if (!g_ic || !g_sig || !Tk || !gk) {
-    free(g_ic); free(g_sig); free(Tk); free(gk);
+  int fail = 0;
+  if (!acc || !bgacc) {
+    free(acc); free(bgacc);
     return -1;
   }
-  memset(g_means2d, 0, sizeof(REAL) * 2 * n);
-  memset(g_cov2d, 0, sizeof(REAL) * 4 * n);
-  memset(g_opac, 0, sizeof(REAL) * n);
-  memset(g_colors, 0, sizeof(REAL) * 3 * n);
-  g_bg[0] = g_bg[1] = g_bg[2] = 0;
-  for (t = 0; t < T; ++t) {
-    const int tx = t % TX, ty = t / TX;
-    FN(tile_t) ts;
-    int pi;
-    FN(tile_setup)(sorted_tiles, L, t, &ts);
-    for (pi = 0; pi < 256; ++pi) {
-      const int lx = pi % 16, ly = pi / 16;
-      const int X = tx * 16 + lx, Y = ty * 16 + ly;
-      const REAL px = (REAL)(tx * 16) + ((REAL)lx + (REAL)0.5);
-      const REAL py = (REAL)(ty * 16) + ((REAL)ly + (REAL)0.5);
-      const REAL* gp;
-      REAL ctC[3], ctT;
-      int k, nk = 0, ch, i;
-      if (X >= W || Y >= H) continue;
-      gp = g_image + 3 * ((int64_t)Y * W + X);
-      if (ts.count == 0) { /* empty tile: image = background */
-        g_bg[0] += gp[0]; g_bg[1] += gp[1]; g_bg[2] += gp[2];
-        continue;
-      }
-      /* forward replay, keeping T before every step */
-      Tk[0] = 1;
-      for (ch = 0; ch < 8; ++ch) {
-        if (ch >= (tpu_gather ? 8 : ts.required)) break;
-        for (i = 0; i < 512; ++i) {
-          const int local = ch * 512 + i;
-          if (!(local < ts.count)) continue;
-          gk[nk] = sorted_gids[FN(entry_index)(&ts, ch, i, L, tpu_gather)];
-          {
-            FN(prim_t) pr;
-            REAL dx, dy, pw, alpha = 0;
-            FN(prim_of)(means2d, cov2d, opac, colors, gk[nk], &pr);
-            if (Tk[nk] > (REAL)1e-4) {
-              dx = px - pr.mx; dy = py - pr.my;
-              pw = FN(power)(dx, dy, &pr, tpu_gather);
-              alpha = pw > (REAL)-10 ? FN(r_min)((REAL)0.99, EXP(pw) * pr.op) : (REAL)0;
-            }
-            Tk[nk + 1] = Tk[nk] * ((REAL)1 - alpha);
-          }
-          ++nk;
+#pragma omp parallel num_threads(nt_max) reduction(| : fail)
+  {
+    const int tid = omp_get_thread_num();
+    REAL* a = acc + nn * 9 * (size_t)tid;
+    REAL* g_ic = a;             /* [n][3] */
+    REAL* g_sig = a + 3 * nn;   /* [n] */
+    REAL* g_m2 = a + 4 * nn;    /* [n][2] */
+    REAL* g_col = a + 6 * nn;   /* [n][3] */
+    REAL* g_b = bgacc + 3 * tid;
+    REAL* Tk = (REAL*)malloc(sizeof(REAL) * 4097);
+    int64_t* gk = (int64_t*)malloc(sizeof(int64_t) * 4096);
+    int t;
+    if (!Tk || !gk) fail = 1;
+#pragma omp for schedule(dynamic, 1)
+    for (t = 0; t < T; ++t) {
+      const int tx = t % TX, ty = t / TX;
+      FN(tile_t) ts;
+      int pi;
+      if (!Tk || !gk) continue;
+      FN(tile_setup)(sorted_tiles, L, t, &ts);
+      for (pi = 0; pi < 256; ++pi) {
+        const int lx = pi % 16, ly = pi / 16;
+        const int X = tx * 16 + lx, Y = ty * 16 + ly;
+        const REAL px = (REAL)(tx * 16) + ((REAL)lx + (REAL)0.5);
+        const REAL py = (REAL)(ty * 16) + ((REAL)ly + (REAL)0.5);
+        const REAL* gp;
+        REAL ctC[3], ctT;
+        int k, nk = 0, ch, i;
+        if (X >= W || Y >= H) continue;
+        gp = g_image + 3 * ((int64_t)Y * W + X);
+        if (ts.count == 0) { /* empty tile: image = background */
+          g_b[0] += gp[0]; g_b[1] += gp[1]; g_b[2] += gp[2];
+          continue;
         }
-      }
-      /* out = C_n + T_n * bg */
-      ctC[0] = gp[0]; ctC[1] = gp[1]; ctC[2] = gp[2];
-      ctT = (gp[0] * bg[0] + gp[1] * bg[1]) + gp[2] * bg[2];
-      g_bg[0] += Tk[nk] * gp[0]; g_bg[1] += Tk[nk] * gp[1]; g_bg[2] += Tk[nk] * gp[2];
-      for (k = nk - 1; k >= 0; --k) {
-        FN(prim_t) pr;
-        REAL dx, dy, pw, e, araw, alpha, ct_alpha, ct_araw, ct_pw, cdot;
-        const REAL Tb = Tk[k];
-        if (!(Tb > (REAL)1e-4)) continue; /* inactive: C and T pass through */
-        FN(prim_of)(means2d, cov2d, opac, colors, gk[k], &pr);
-        dx = px - pr.mx; dy = py - pr.my;
-        pw = FN(power)(dx, dy, &pr, tpu_gather);
-        if (!(pw > (REAL)-10)) continue; /* alpha = 0: pass through, no cotangent */
-        e = EXP(pw);
-        araw = e * pr.op;
-        alpha = FN(r_min)((REAL)0.99, araw);
-        /* C' = C + (alpha T) col ; T' = T (1 - alpha) */
-        cdot = (pr.col[0] * ctC[0] + pr.col[1] * ctC[1]) + pr.col[2] * ctC[2];
-        ct_alpha = Tb * cdot - Tb * ctT;
-        g_colors[3 * gk[k] + 0] += (alpha * Tb) * ctC[0];
-        g_colors[3 * gk[k] + 1] += (alpha * Tb) * ctC[1];
-        g_colors[3 * gk[k] + 2] += (alpha * Tb) * ctC[2];
-        ctT = alpha * cdot + ((REAL)1 - alpha) * ctT;
-        ct_araw = ct_alpha * FN(d_min)(araw, (REAL)0.99);
-        g_sig[gk[k]] += ct_araw * e;
-        ct_pw = ct_araw * araw;
-        {
-          const REAL h = (REAL)-0.5 * ct_pw;
-          const REAL ctdx = h * ((REAL)2 * dx * pr.ic00 + dy * pr.ic01_2);
-          const REAL ctdy = h * (dx * pr.ic01_2 + (REAL)2 * dy * pr.ic11);
-          g_ic[3 * gk[k] + 0] += h * (dx * dx);
-          g_ic[3 * gk[k] + 1] += h * (dx * dy);
-          g_ic[3 * gk[k] + 2] += h * (dy * dy);
-          g_means2d[2 * gk[k]] -= ctdx;
-          g_means2d[2 * gk[k] + 1] -= ctdy;
+        /* forward replay, keeping T before every step */
+        Tk[0] = 1;
+        for (ch = 0; ch < 8; ++ch) {
+          if (ch >= (tpu_gather ? 8 : ts.required)) break;
+          for (i = 0; i < 512; ++i) {
+            const int local = ch * 512 + i;
+            if (!(local < ts.count)) continue;
+            gk[nk] = sorted_gids[FN(entry_index)(&ts, ch, i, L, tpu_gather)];
+            {
+              FN(prim_t) pr;
+              REAL dx, dy, pw, alpha = 0;
+              FN(prim_of)(means2d, cov2d, opac, colors, gk[nk], &pr);
+              if (Tk[nk] > (REAL)1e-4) {
+                dx = px - pr.mx; dy = py - pr.my;
+                pw = FN(power)(dx, dy, &pr, tpu_gather);
+                alpha = pw > (REAL)-10 ? FN(r_min)((REAL)0.99, EXP(pw) * pr.op) : (REAL)0;
+              }
+              Tk[nk + 1] = Tk[nk] * ((REAL)1 - alpha);
+            }
+            ++nk;
+          }
+        }
+        /* out = C_n + T_n * bg */
+        ctC[0] = gp[0]; ctC[1] = gp[1]; ctC[2] = gp[2];
+        ctT = (gp[0] * bg[0] + gp[1] * bg[1]) + gp[2] * bg[2];
+        g_b[0] += Tk[nk] * gp[0]; g_b[1] += Tk[nk] * gp[1]; g_b[2] += Tk[nk] * gp[2];
+        for (k = nk - 1; k >= 0; --k) {
+          FN(prim_t) pr;
+          REAL dx, dy, pw, e, araw, alpha, ct_alpha, ct_araw, ct_pw, cdot;
+          const REAL Tb = Tk[k];
+          const int64_t gg = gk[k];
+          if (!(Tb > (REAL)1e-4)) continue; /* inactive: C and T pass through */
+          FN(prim_of)(means2d, cov2d, opac, colors, gg, &pr);
+          dx = px - pr.mx; dy = py - pr.my;
+          pw = FN(power)(dx, dy, &pr, tpu_gather);
+          if (!(pw > (REAL)-10)) continue; /* alpha = 0: pass through, no cotangent */
+          e = EXP(pw);
+          araw = e * pr.op;
+          alpha = FN(r_min)((REAL)0.99, araw);
+          /* C' = C + (alpha T) col ; T' = T (1 - alpha) */
+          cdot = (pr.col[0] * ctC[0] + pr.col[1] * ctC[1]) + pr.col[2] * ctC[2];
+          ct_alpha = Tb * cdot - Tb * ctT;
+          g_col[3 * gg + 0] += (alpha * Tb) * ctC[0];
+          g_col[3 * gg + 1] += (alpha * Tb) * ctC[1];
+          g_col[3 * gg + 2] += (alpha * Tb) * ctC[2];
+          ctT = alpha * cdot + ((REAL)1 - alpha) * ctT;
+          ct_araw = ct_alpha * FN(d_min)(araw, (REAL)0.99);
+          g_sig[gg] += ct_araw * e;
+          ct_pw = ct_araw * araw;
+          {
+            const REAL h = (REAL)-0.5 * ct_pw;
+            const REAL ctdx = h * ((REAL)2 * dx * pr.ic00 + dy * pr.ic01_2);
+            const REAL ctdy = h * (dx * pr.ic01_2 + (REAL)2 * dy * pr.ic11);
+            g_ic[3 * gg + 0] += h * (dx * dx);
+            g_ic[3 * gg + 1] += h * (dx * dy);
+            g_ic[3 * gg + 2] += h * (dy * dy);
+            g_m2[2 * gg] -= ctdx;
+            g_m2[2 * gg + 1] -= ctdy;
+          }
         }
       }
     }
+    free(Tk);
+    free(gk);
   }
-  /* prologue: det clamp, inverse, sigmoid */
+  if (fail) {
+    free(acc); free(bgacc);
+    return -1;
+  }
+  g_bg[0] = g_bg[1] = g_bg[2] = 0;
+  {
+    int tt;
+    for (tt = 0; tt < nt_max; ++tt) {
+      g_bg[0] += bgacc[3 * tt]; g_bg[1] += bgacc[3 * tt + 1]; g_bg[2] += bgacc[3 * tt + 2];
+    }
+  }
+  /* thread sums, then the prologue: det clamp, inverse, sigmoid */
+#pragma omp parallel for schedule(static)
   for (g = 0; g < n; ++g) {
-    const REAL c00 = cov2d[4 * g], c01 = cov2d[4 * g + 1], c11 = cov2d[4 * g + 3];
-    const REAL draw = c00 * c11 - c01 * c01;
-    const REAL det = FN(r_max)(draw, (REAL)1e-6);
-    const REAL ct00 = g_ic[3 * g], ct01 = (REAL)2 * g_ic[3 * g + 1], ct11 = g_ic[3 * g + 2];
-    const REAL ct_det = -((ct00 * c11 + ct01 * (-c01)) + ct11 * c00) / (det * det) * FN(d_max)(draw, (REAL)1e-6);
-    const REAL sg = SIGMOID(opac[g]);
-    g_cov2d[4 * g + 3] += ct00 / det + ct_det * c00;
-    g_cov2d[4 * g + 1] += -ct01 / det - (REAL)2 * c01 * ct_det;
-    g_cov2d[4 * g + 0] += ct11 / det + ct_det * c11;
-    g_opac[g] = g_sig[g] * sg * ((REAL)1 - sg);
+    REAL s[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    int tt;
+    for (tt = 0; tt < nt_max; ++tt) {
+      const REAL* a = acc + nn * 9 * (size_t)tt;
+      s[0] += a[3 * g]; s[1] += a[3 * g + 1]; s[2] += a[3 * g + 2];
+      s[3] += a[3 * nn + g];
+      s[4] += a[4 * nn + 2 * g]; s[5] += a[4 * nn + 2 * g + 1];
+      s[6] += a[6 * nn + 3 * g]; s[7] += a[6 * nn + 3 * g + 1]; s[8] += a[6 * nn + 3 * g + 2];
+    }
+    {
+      const REAL c00 = cov2d[4 * g], c01 = cov2d[4 * g + 1], c11 = cov2d[4 * g + 3];
+      const REAL draw = c00 * c11 - c01 * c01;
+      const REAL det = FN(r_max)(draw, (REAL)1e-6);
+      const REAL ct00 = s[0], ct01 = (REAL)2 * s[1], ct11 = s[2];
+      const REAL ct_det = -((ct00 * c11 + ct01 * (-c01)) + ct11 * c00) / (det * det) * FN(d_max)(draw, (REAL)1e-6);
+      const REAL sg = SIGMOID(opac[g]);
+      g_cov2d[4 * g + 0] = ct11 / det + ct_det * c11;
+      g_cov2d[4 * g + 1] = -ct01 / det - (REAL)2 * c01 * ct_det;
+      g_cov2d[4 * g + 2] = 0;
+      g_cov2d[4 * g + 3] = ct00 / det + ct_det * c00;
+      g_opac[g] = s[3] * sg * ((REAL)1 - sg);
+      g_means2d[2 * g] = s[4];
+      g_means2d[2 * g + 1] = s[5];
+      g_colors[3 * g] = s[6];
+      g_colors[3 * g + 1] = s[7];
+      g_colors[3 * g + 2] = s[8];
+    }
   }
-  free(g_ic); free(g_sig); free(Tk); free(gk);
+  free(acc); free(bgacc);
   return 0;
 }
 
@@ -526,6 +606,7 @@ int FN(gso_preprocess_bwd)(int64_t n, int K, int deg, const REAL* means, const R
                            REAL* g_sh) {
   const REAL* w = w2c;
   int64_t i;
+#pragma omp parallel for schedule(static)
   for (i = 0; i < n; ++i) {
     FN(proj_t) p;
     REAL v[3], nrm, d[3], g_pre[3], g_d[3] = {0, 0, 0}, g_m[3];

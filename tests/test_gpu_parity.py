@@ -1,107 +1,25 @@
 """GPU parity: the HIP path (through the C ABI) against the CPU oracle.
 
-Bars:
-  * integer outputs bit-exact: per-Gaussian tile rectangles/counts (via the entry
-    list), the sorted entry list (tile, Gaussian id) and the tile ranges;
-  * image max-abs error <= 1e-4;
-  * gradients: relative L2 error <= 1e-3 per parameter tensor.
-The per-Gaussian preprocessing is compared bit-for-bit (same float32 operation
-order, no FMA contraction, same exp on both sides).
-
-Reference-order note: the reference's arrays carry 256 slots of every Gaussian whose
-depth has its sign bit set in front of the valid entries (tile -1); the GPU list
-holds only the valid entries, so its boundaries are compared after that shift and
-its entries against the reference's valid sub-list.
+The bars and the reference-order note are in gpu_helpers.py; scenes here are the
+configurations' families at reduced sizes plus the full sizes of configurations 0 and 1
+(configurations 2-4 at full size: test_gpu_fullsize.py).
 """
 import numpy as np
 import pytest
 import torch
 
 import oracle
+from gpu_helpers import FIELDS, GRAD_TOL, IMG_TOL
+from gpu_helpers import check_binning as _check_binning
+from gpu_helpers import check_preprocess as _check_preprocess
+from gpu_helpers import np_ as _np
+from gpu_helpers import rel as _rel
+from gpu_helpers import render_both as _render_both
 from jax_gs_amd import render, scenes
 from jax_gs_amd.renderer import rasterizer
 from jax_gs_amd.renderer.projection import preprocess
 
 pytestmark = pytest.mark.gpu
-
-IMG_TOL = 1e-4
-GRAD_TOL = 1e-3
-FIELDS = ("means", "scales", "quaternions", "opacities", "sh_coeffs")
-
-
-def _np(t):
-    return t.detach().cpu().numpy()
-
-
-def _rel(a, b):
-    a = np.asarray(a, np.float64)
-    b = np.asarray(b, np.float64)
-    return np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)
-
-
-def _ref_valid_sublist(st, sg, n_neg, n_int):
-    off = 256 * n_neg
-    return st[off:off + n_int], sg[off:off + n_int]
-
-
-def _check_preprocess(sc, cuda):
-    g, cam, _, m = scenes.to_torch(sc, cuda)
-    pre = preprocess(g, cam, mask=m, sh_degree=sc["sh_degree"])
-    c = sc["cam"]
-    f32 = np.float32
-    o = oracle.preprocess(sc["params"]["means"], sc["params"]["scales"], sc["params"]["quaternions"],
-                          sc["params"]["sh_coeffs"], c["W2C"], c["W"], c["H"], f32(c["fx"]), f32(c["fy"]),
-                          f32(c["cx"]), f32(c["cy"]), sc["sh_degree"], mask=sc["mask"])
-    for k in ("means2d", "cov2d", "radii", "depths", "colors"):
-        np.testing.assert_array_equal(_np(pre[k]), o[k], err_msg=k)
-    np.testing.assert_array_equal(_np(pre["valid"]).astype(bool), o["valid"])
-    # the renderer's call writes no cov2d / colour arrays; everything else is identical
-    lean = preprocess(g, cam, mask=m, sh_degree=sc["sh_degree"], projected=False)
-    assert lean["cov2d"] is None and lean["colors"] is None
-    for k in ("means2d", "radii", "valid", "depths", "records"):
-        np.testing.assert_array_equal(_np(lean[k]), _np(pre[k]), err_msg=k)
-    return pre, o
-
-
-def _check_binning(sc, cuda, pre_gpu, pre_o):
-    c = sc["cam"]
-    W, H = c["W"], c["H"]
-    b = rasterizer.bin_gaussians(pre_gpu["means2d"], pre_gpu["radii"], pre_gpu["valid"], pre_gpu["depths"], H, W)
-    st, sg, n_int = oracle.tile_interactions(pre_o["means2d"], pre_o["radii"], pre_o["valid"], pre_o["depths"], H, W)
-    stats = _np(b["stats"])
-    n_neg = int((np.signbit(pre_o["depths"])).sum())
-    assert stats[7] == n_neg
-    assert stats[0] == n_int
-    assert stats[8] == 0
-    st_v, sg_v = _ref_valid_sublist(st, sg, n_neg, n_int)
-    np.testing.assert_array_equal(_np(b["sorted_tiles"])[:n_int], st_v)
-    np.testing.assert_array_equal(_np(b["sorted_gids"])[:n_int], sg_v)
-    T = ((W + 15) // 16) * ((H + 15) // 16)
-    b_ref = oracle.tile_boundaries(st, T)
-    np.testing.assert_array_equal(_np(b["ranges"]) + 256 * n_neg, b_ref)
-    ex = oracle.extras_from(pre_o, st, n_int, H, W)
-    for k, idx in (("max_interactions_per_tile", 1), ("overflow_tiles", 2), ("overflow_interactions", 3),
-                   ("truncated_tiles", 4), ("truncated_interactions", 5), ("radius_cap_violations", 6)):
-        assert stats[idx] == ex[k], k
-    return b, (st, sg, n_int)
-
-
-def _render_both(sc, cuda, seed_kind="l1"):
-    g, cam, tgt, m = scenes.to_torch(sc, cuda)
-    for f in FIELDS:
-        getattr(g, f).requires_grad_(True)
-    image, extras = render(g, cam, mask=m, sh_degree=sc["sh_degree"])
-    img_o, ex_o, res = oracle.render(sc["params"], sc["cam"], mask=sc["mask"], sh_degree=sc["sh_degree"])
-    if seed_kind == "l1":
-        target = sc["target"] if sc["target"] is not None else np.random.default_rng(7).uniform(
-            0, 1, img_o.shape).astype(np.float32)
-        # one seed for both sides (the L1 sign must not flip between them)
-        _, seed = oracle.l1_loss_and_grad(img_o, target)
-    else:
-        seed = np.random.default_rng(11).normal(0, 1, img_o.shape).astype(np.float32)
-    image.backward(torch.from_numpy(seed).to(cuda))
-    gr_o = oracle.render_vjp(sc["params"], sc["cam"], res, seed, sh_degree=sc["sh_degree"])
-    return image, extras, g, img_o, ex_o, gr_o
 
 
 @pytest.mark.parametrize("cfg,n,w,h", [(0, 3000, 128, 96), (1, 4000, 200, 150), (3, 6000, 160, 96),
@@ -164,28 +82,6 @@ def test_cfg3_truncated_tiles(cuda):
     assert int(_np(b["stats"])[4]) > 0  # truncated tiles present
     image, extras, g, img_o, ex_o, gr_o = _render_both(sc, cuda)
     assert np.abs(_np(image) - img_o).max() <= IMG_TOL
-    for f in FIELDS:
-        assert _rel(_np(getattr(g, f).grad), gr_o[f]) <= GRAD_TOL, f
-
-
-def test_cfg2_binning_full(cuda):
-    """Headline configuration (1M Gaussians, 1920x1080): preprocessing and the whole
-    entry list bit-exact against the oracle."""
-    sc = scenes.make_scene(2)
-    pre, pre_o = _check_preprocess(sc, cuda)
-    _check_binning(sc, cuda, pre, pre_o)
-
-
-def test_cfg2_band_fwd_bwd(cuda):
-    """All 1M Gaussians of the headline scene rendered into the top 1920x128 band of
-    its camera: image and gradients against the oracle."""
-    sc = scenes.make_scene(2)
-    sc["cam"] = dict(sc["cam"])
-    sc["cam"]["H"] = 128
-    sc["target"] = sc["target"][:128]
-    image, extras, g, img_o, ex_o, gr_o = _render_both(sc, cuda)
-    assert np.abs(_np(image) - img_o).max() <= IMG_TOL
-    assert int(extras["n_interactions"]) == ex_o["n_interactions"]
     for f in FIELDS:
         assert _rel(_np(getattr(g, f).grad), gr_o[f]) <= GRAD_TOL, f
 
