@@ -113,6 +113,21 @@ int gs_bin(void* stream, int64_t n, const float* means2d, const float* radii,
            int64_t capacity, void* workspace, size_t workspace_bytes, int32_t* sorted_gids,
            int32_t* sorted_tiles, int32_t* ranges, int32_t* stats);
 
+/* gs_bin without a workspace argument and without any allocation: the workspace is a
+ * library-owned device array of GS_BIN_STATIC_SCRATCH_BYTES (128 MiB) that every GPU
+ * the library runs on holds until the process ends.  No counterpart in the reference
+ * (its sort allocates through XLA): it is for callers that cannot allocate, such as
+ * code under HIP graph capture or serving loops that forbid hipMalloc.
+ * Arguments and outputs as gs_bin; returns GS_ERR_INVALID when
+ * gs_bin_workspace_size(n, width, height, capacity) exceeds the array (1080p: about
+ * 1.09M Gaussians).  Calls share their GPU's array: calls that overlap on one GPU
+ * (other streams or threads) race; calls in stream order do not. */
+#define GS_BIN_STATIC_SCRATCH_BYTES ((size_t)128 << 20)
+int gs_bin_static(void* stream, int64_t n, const float* means2d, const float* radii,
+                  const uint8_t* valid, const float* depths, int width, int height,
+                  int64_t capacity, int32_t* sorted_gids, int32_t* sorted_tiles, int32_t* ranges,
+                  int32_t* stats);
+
 /* Tile boundaries of an arbitrary sorted tile-id array (length L, entries in
  * [-1, T]): ranges[t] = first index with tile >= t for t in 0..T.
  * Replaces the searchsorted of jax_gs/renderer/renderer.py:57-61 and

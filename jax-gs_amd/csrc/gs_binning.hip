@@ -43,6 +43,7 @@
 #include "gs_common.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace gs {
 namespace {
@@ -1194,4 +1195,57 @@ extern "C" int gs_tile_ranges(void* stream, const int32_t* sorted_tiles, int64_t
                      (hipStream_t)stream, sorted_tiles, length, num_tiles, ranges);
   GS_LAUNCH_CHECK("ranges_any_kernel");
   return GS_OK;
+}
+
+// ---------------------------------------------------------------------------------
+// gs_bin_static: gs_bin with its workspace in a library-owned device array, for callers
+// that cannot allocate.  Every GPU the library runs on holds its own copy of `scratch`
+// (GS_BIN_STATIC_SCRATCH_BYTES) until the process ends.  Host code never passes the
+// array's name to a kernel: its device address, per device, comes from
+// hipGetSymbolAddress on the entry point's first call with that device current.
+// gs_bin's kernels need no cleared workspace (whatever must start at zero is cleared
+// by its first launch), so a call may follow any other on the same array; calls that
+// overlap on one GPU (other streams or threads) share it and race.
+static __device__ __align__(256) unsigned char scratch[GS_BIN_STATIC_SCRATCH_BYTES];
+
+namespace gs {
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  int rc = hip_check(hipGetDevice(&dev), "gs_bin_static: hipGetDevice");
+  if (rc != GS_OK) return rc;
+  GS_REQUIRE(dev >= 0 && dev < kMaxDevices, "gs_bin_static: device %d out of the supported range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    rc = hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "gs_bin_static: hipGetSymbolAddress");
+    if (rc != GS_OK) return rc;
+    GS_REQUIRE(ptr != nullptr, "gs_bin_static: no device address for the scratch array");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return GS_OK;
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" int gs_bin_static(void* stream, int64_t n, const float* means2d, const float* radii, const uint8_t* valid,
+                             const float* depths, int width, int height, int64_t capacity, int32_t* sorted_gids,
+                             int32_t* sorted_tiles, int32_t* ranges, int32_t* stats) {
+  GS_REQUIRE(n >= 0 && width > 0 && height > 0, "gs_bin_static: bad sizes (n %lld, image %dx%d)", (long long)n,
+             width, height);
+  const size_t need = gs_bin_workspace_size(n, width, height, capacity);
+  GS_REQUIRE(need <= (size_t)GS_BIN_STATIC_SCRATCH_BYTES,
+             "gs_bin_static: %lld Gaussians on a %dx%d image need %zu bytes of workspace, more than the %zu of "
+             "the static scratch array (use gs_bin with a caller workspace)",
+             (long long)n, width, height, need, (size_t)GS_BIN_STATIC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = scratch_on_current_device(&ws);
+  if (rc != GS_OK) return rc;
+  return gs_bin(stream, n, means2d, radii, valid, depths, width, height, capacity, ws,
+                (size_t)GS_BIN_STATIC_SCRATCH_BYTES, sorted_gids, sorted_tiles, ranges, stats);
 }

@@ -36,6 +36,7 @@ _SIGS = {
     "gs_composite_prep": [_P, _I64, _P, _P, _P, _P, _P],
     "gs_bin_workspace_size": [_I64, _I, _I, _I64],
     "gs_bin": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _SZ, _P, _P, _P, _P],
+    "gs_bin_static": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _P, _P, _P],
     "gs_tile_ranges": [_P, _P, _I64, _I, _P],
     "gs_composite_fwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _I],
     "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I],
