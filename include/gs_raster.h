@@ -186,7 +186,7 @@ int gs_preprocess_bwd(void* stream, int64_t n, int sh_k, int sh_degree, const fl
 /* The training step's tail in one pass: gs_preprocess_bwd's gradients, the
  * densification statistics of gs_densify_accumulate (from the means before the update;
  * skipped when grad_accum is NULL) and gs_adam_step's masked update of the five arrays,
- * in place; no parameter gradient is written.  Replaces trainer.py:66-103 after the
+ * in place; no parameter gradient is written.  Replaces trainer.py:137-159 after the
  * rasterizer's VJP, with optax.adam of train.py:127-155.  moments: host array of 10 device
  * pointers (first moments of means, scales, quaternions, opacities, sh_coeffs, then the
  * second moments), lrs[5] the learning rates, step the optimizer count after the update. */
@@ -297,7 +297,7 @@ int gs_ply_unpack(void* stream, int64_t n, int sh_k, const float* records, float
                   float* scales, float* quats, float* opacities, float* sh_coeffs);
 
 /* Densification statistics of one training step, updated in place.
- * Replaces jax_gs/training/trainer.py:278-294 (train_step, after value_and_grad):
+ * Replaces jax_gs/training/trainer.py:143-159 (train_step, after value_and_grad):
  *   grad_accum += (|grad_means| * (max(z_cam,0.01) / focal)) * pixel_scale
  *   denom      += valid & active
  *   max_radii   = valid ? max(max_radii, radii) : max_radii

@@ -43,6 +43,7 @@
 // min(0.99, .) passes no gradient when it binds (half at a tie), gated entries pass
 // none.
 #include "gs_common.h"
+#include "gs_cull.h"
 
 #include <algorithm>
 
@@ -171,6 +172,10 @@ __device__ inline float reduce_scatter(const float* v, int lane) {
 // scene's content lies (contiguous bands of rows gave the busiest XCD 1.23x the mean on a
 // centred scene), while the four tiles of a cell, which share most of their Gaussians, hit
 // one L2. A cell's tiles go to consecutive workgroups of the XCD, i.e. to different SIMDs.
+// This holds for one wave per tile.  With WPT waves per tile the kernels take
+// b = blockIdx.x / WPT, so a tile's waves are consecutive workgroups on WPT different XCDs
+// and each of those L2s fetches the tile's records; keeping a tile's waves on one XCD was
+// measured no faster (those launches are latency-bound, not L2-bound).
 __host__ __device__ inline int tile_blocks(int TX, int TY) { return ((TX + 7) & ~7) * ((TY + 3) & ~3); }
 
 // Tile of workgroup b (b < tile_blocks(TX, TY)), or -1 for a padding workgroup.
@@ -209,46 +214,8 @@ __device__ inline Rec load_rec(const float4* __restrict__ rec, int g) {
   return Rec{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z};
 }
 
-// q = log2(e) * power + log2(opacity) with (A, B, C) = log2(e) * (-ic00/2, -ic01,
-// -ic11/2), evaluated as (C dy + B dx) dy + (A dx^2 + log2(opacity)); the last term
-// and B dx are shared by a lane's pixels.  The forward and backward kernels share
-// this exact expression, so they gate the same (pixel, entry) pairs.
-__device__ inline float q_of(float dy, float Adx2l, float Bdx, float C) {
-  return fmaf(fmaf(C, dy, Bdx), dy, Adx2l);
-}
-
 // Ids are clamped like XLA's gather.
 __device__ inline int clamp_gid(int g, int num_g) { return min(max(g, 0), num_g - 1); }
-
-// True when no point of the rectangle [x0,x1] x [y0,y1] can pass the gate
-// power > -10 for the entry (mx, my, A, B, C), where A dx^2 + B dx dy + C dy^2 =
-// log2(e) * power.  f = -(A dx^2 + B dx dy + C dy^2) is a convex quadratic when A < 0,
-// C < 0 and B^2 < 4AC (anything else, NaN included, is kept); its minimum over the
-// rectangle is 0 when the centre lies inside, else it lies on an edge, where it is
-// the 1-D minimum at the clamped stationary point.  The threshold exceeds
-// 10 log2(e) by an allowance for the rounding of both this minimum and the per-pixel
-// exponent (a few ulp of the largest term), so a dropped entry fails the gate at
-// every pixel centre of the rectangle as the compositing loops compute it.
-__host__ __device__ inline bool entry_misses_rect(float mx, float my, float A, float B, float C, float x0,
-                                                  float x1, float y0, float y1) {
-  const float a = -A, b = -B, c = -C;
-  if (!(a > 0.0f && c > 0.0f && b * b < 4.0f * a * c)) return false;
-  const float dx0 = x0 - mx, dx1 = x1 - mx, dy0 = y0 - my, dy1 = y1 - my;
-  if (dx0 <= 0.0f && dx1 >= 0.0f && dy0 <= 0.0f && dy1 >= 0.0f) return false;
-  const float sx = -0.5f * b / a, sy = -0.5f * b / c;  // stationary points: dx* = sx dy, dy* = sy dx
-  auto on_x_edge = [&](float dx) {
-    const float dy = fminf(fmaxf(sy * dx, dy0), dy1);
-    return (a * dx) * dx + (b * dx) * dy + (c * dy) * dy;
-  };
-  auto on_y_edge = [&](float dy) {
-    const float dx = fminf(fmaxf(sx * dy, dx0), dx1);
-    return (a * dx) * dx + (b * dx) * dy + (c * dy) * dy;
-  };
-  const float fmin = fminf(fminf(on_x_edge(dx0), on_x_edge(dx1)), fminf(on_y_edge(dy0), on_y_edge(dy1)));
-  const float ex = fmaxf(dx0 * dx0, dx1 * dx1), ey = fmaxf(dy0 * dy0, dy1 * dy1);
-  const float scale = a * ex + fabsf(b) * sqrtf(ex * ey) + c * ey;
-  return fmin >= 10.25f * 1.4426950408889634f + 1e-5f * scale;
-}
 
 // What a lane fetches to test one entry of a batch against the wave's pixel
 // rectangle: the (clamped) id, or -1 past the tile's list, and the record's centre

@@ -2,8 +2,9 @@
 // SH colour and compositing records (forward), and their vector-Jacobian product
 // (backward).  One thread per Gaussian, one wave per 64 Gaussians; every input row
 // is read once and every output row written once, so both kernels are HBM-bound.
-// The SH rows (192 bytes per Gaussian at degree 3) move between HBM and LDS with
-// coalesced accesses.
+// Each lane loads its SH row (192 bytes per Gaussian at degree 3) and, backward, its
+// gradient record straight into registers with 16-byte loads, which cover the row's
+// cache lines whole.
 //
 // Forward semantics follow, operation by operation and in float32:
 //   jax_gs/renderer/projection.py:26-77 (project_gaussians)
@@ -566,7 +567,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   }
 }
 
-// The training step's tail in one pass (trainer.py:66-103 with optax.adam of
+// The training step's tail in one pass (trainer.py:137-159 with optax.adam of
 // train.py:127-155): the preprocessing VJP as in preprocess_bwd_kernel, the
 // densification statistics from the pre-update means, and the masked Adam update of
 // all five arrays in place, so that no parameter gradient goes through HBM.  The
@@ -625,7 +626,7 @@ __global__ __launch_bounds__(64) void preprocess_bwd_adam_kernel(
     preprocess_bwd_one<DEG>(0, K, in, w2c, fx, fy, grs + lane * LG, shs + lane * LS, gm, gsc, gq, go);
     const bool on = active == nullptr || active[i] != 0;
     if (grad_accum != nullptr) {
-      // trainer.py:280-294 from the means before the update
+      // trainer.py:143-159 from the means before the update
       const float zc = ((in.mx * w2c[8] + in.my * w2c[9]) + in.mz * w2c[10]) + w2c[11];
       const float z = jmax(zc, 0.01f);
       const float gn = sqrtf((gm[0] * gm[0] + gm[1] * gm[1]) + gm[2] * gm[2]);
@@ -704,15 +705,15 @@ __global__ __launch_bounds__(256) void densify_kernel(int64_t n, const float* __
                                                       float* __restrict__ max_radii) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  // trainer.py:280-282
+  // trainer.py:145-147
   const float mx = means[3 * i], my = means[3 * i + 1], mz = means[3 * i + 2];
   const float zc = ((mx * w2c[8] + my * w2c[9]) + mz * w2c[10]) + w2c[11];
   const float z = jmax(zc, 0.01f);
-  // trainer.py:285
+  // trainer.py:148-152
   const float gx = g_means[3 * i], gy = g_means[3 * i + 1], gz = g_means[3 * i + 2];
   const float gn = sqrtf((gx * gx + gy * gy) + gz * gz);
   grad_accum[i] = grad_accum[i] + (gn * (z / focal)) * pixel_scale;
-  // trainer.py:288-294
+  // trainer.py:153-159
   const bool v = valid[i] != 0;
   const bool act = (active == nullptr) || active[i] != 0;
   denom[i] = denom[i] + ((v && act) ? 1 : 0);

@@ -16,6 +16,23 @@ OFFSET_SIZE = 16  # rasterizer.py:7
 BLOCK_SIZE = 512  # rasterizer.py:8
 MAX_TILE_CHUNKS = 8  # rasterizer.py:9
 MAX_TILE_INTERACTIONS = BLOCK_SIZE * MAX_TILE_CHUNKS  # rasterizer.py:10
+# entries are indexed with int32 (ranges, ids): the largest entry list the kernels take
+MAX_ENTRIES = 2 ** 31 - 1
+
+
+def default_capacity(n: int) -> int:
+    """The reference's static entry bound max(256 n, 512) (rasterizer.py:56-69, 107-110),
+    limited to what int32 indices address (n >= 8,388,608 reaches that limit; a count above
+    it is flagged in the binning stats, GS_STAT_CAPACITY_EXCEEDED, and the first entries of
+    the reference order are kept)."""
+    return min(max(256 * int(n), BLOCK_SIZE), MAX_ENTRIES)
+
+
+def check_capacity(capacity: int | None, n: int) -> int:
+    cap = default_capacity(n) if not capacity else int(capacity)
+    if not 0 < cap <= MAX_ENTRIES:
+        raise ValueError(f"capacity {cap} outside [1, {MAX_ENTRIES}] (entries are indexed with int32)")
+    return cap
 
 
 class BinResult(dict):
@@ -34,7 +51,7 @@ def bin_gaussians(means2d: torch.Tensor, radii: torch.Tensor, valid: torch.Tenso
     radii = check_f32("radii", radii.to(torch.float32), (n,), dev)
     depths = check_f32("depths", depths, (n,), dev)
     v = valid.to(device=dev, dtype=torch.uint8).contiguous()
-    cap = int(capacity) if capacity else max(256 * n, BLOCK_SIZE)
+    cap = check_capacity(capacity, n)
     ws_bytes = _lib.lib().gs_bin_workspace_size(n, int(W), int(H), cap)
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     _, _, T = num_tiles(W, H)

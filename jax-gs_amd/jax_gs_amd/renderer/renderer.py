@@ -10,8 +10,12 @@ and the backward's tile order as residuals; its backward runs the compositing VJ
 returns cotangents of the five Gaussian arrays (equal to JAX autodiff of the
 reference forward, with its tie conventions) and of the background.  W2C gets no
 gradient (the reference's trainer never differentiates it) and mask gets None.
-``fast_tpu_rasterizer`` is accepted for signature parity: both reference
-rasterizers produce the same image and there is a single implementation here.
+``fast_tpu_rasterizer`` is accepted for signature parity: there is a single
+implementation, which reads each tile's own entries (rasterizer_tpu.py:90-97).  The
+reference's default path slices 512-entry chunk windows clamped to the end of its 256*N
+slot arrays (rasterizer.py:184-190), which reads other entries only when the sentinel
+tail of those arrays is shorter than 512 slots (two Gaussians, or every Gaussian covering
+nearly 16x16 tiles); ``rasterizer.render_tiles`` reproduces that rule on caller arrays.
 """
 from __future__ import annotations
 
@@ -22,7 +26,7 @@ from ..core.camera import Camera
 from ..core.gaussians import Gaussians
 from ._buffers import as_mask, background_tensor, check_f32, num_tiles
 from .projection import preprocess
-from .rasterizer import BLOCK_SIZE, bin_gaussians, composite
+from .rasterizer import bin_gaussians, check_capacity, composite
 
 
 class _Render(torch.autograd.Function):
@@ -91,7 +95,8 @@ def render(gaussians: Gaussians, camera: Camera, background=None, fast_tpu_raste
     """Render one view; returns (image [H,W,3] float32, extras dict) like renderer.py:15-107.
 
     capacity bounds the number of (Gaussian, tile) entries; the default is the
-    reference's static bound 256*N (every Gaussian may touch 16x16 tiles)."""
+    reference's static bound 256*N (every Gaussian may touch 16x16 tiles), limited to the
+    2^31 - 1 entries int32 indices address (N >= 8,388,608)."""
     del fast_tpu_rasterizer  # single implementation (see module docstring)
     means = gaussians.means
     dev = means.device
@@ -100,7 +105,7 @@ def render(gaussians: Gaussians, camera: Camera, background=None, fast_tpu_raste
     w2c = torch.as_tensor(camera.W2C, dtype=torch.float32, device=dev).contiguous()
     bg = background_tensor(background, dev)
     m = as_mask(mask, n, dev)
-    cap = int(capacity) if capacity else max(256 * n, BLOCK_SIZE)
+    cap = check_capacity(capacity, n)
     static = (int(camera.W), int(camera.H), float(camera.fx), float(camera.fy), float(camera.cx), float(camera.cy),
               int(sh_degree), cap)
     image, radii, valid, stats = _Render.apply(means, gaussians.scales.contiguous(),

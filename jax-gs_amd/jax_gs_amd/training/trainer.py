@@ -5,7 +5,7 @@
 rasterizer, accumulates the densification statistics from the pre-update means and
 applies the masked Adam step -- the same sequence as the reference's jitted step, with the
 state's tensors updated in place.  ``accumulate_from_extras`` is the statistics part
-(trainer.py:278-294) on its own.
+(trainer.py:143-159) on its own.
 """
 from __future__ import annotations
 
