@@ -258,12 +258,15 @@ __device__ inline uint64_t probe_test(const Probe& p, float x0, float x1, float 
   return __ballot(p.g >= 0 && !entry_misses_rect(p.mx, p.my, p.A, p.B, p.C, x0, x1, y0, y1));
 }
 
-template <int PPT>
+// WIN: the default path's chunk windows (win_hi, see probe_gid); without it the id fetch
+// compiles to the plain one.
+template <int PPT, bool WIN>
 __global__ __launch_bounds__(64) void composite_fwd_kernel(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
     float* __restrict__ img, float* __restrict__ finalT, int32_t* __restrict__ ncontrib,
-    int32_t* __restrict__ tile_cost, float4* __restrict__ clear, int64_t n_clear, int64_t win_hi) {
+    int32_t* __restrict__ tile_cost, float4* __restrict__ clear, int64_t n_clear, int64_t win_arg) {
+  const int64_t win_hi = WIN ? win_arg : -1;
   constexpr int WPT = 4 / PPT;  // waves per tile
   // Every workgroup clears its slice of the caller's array after its own outputs (stores
   // and loads share one wait counter, so stores issued before the walk would hold up its
@@ -715,19 +718,19 @@ extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, c
   const int64_t n4_clear = clear_records ? n * kRec / 4 : 0;  // kRec = 12: whole float4s
   // the reference slices 512 entries per chunk, which needs an array of at least 512
   const int64_t win_hi = (window_rule == 1 && n_entries >= kBlock) ? n_entries - kBlock : -1;
+#define GS_FWD_LAUNCH(PPT, WPT, WIN)                                                                          \
+  hipLaunchKernelGGL((composite_fwd_kernel<PPT, WIN>), dim3(nblk * (WPT)), dim3(64), 0, s, (const float4*)records, \
+                     (int)n, sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T,       \
+                     n_contrib, tile_order, (float4*)clear_records, n4_clear, win_hi)
+  const bool win = win_hi >= 0;
   if (pick_ppt(T) == 4 && T >= kFwdOneWaveTiles) {
-    hipLaunchKernelGGL(composite_fwd_kernel<4>, dim3(nblk), dim3(64), 0, s, (const float4*)records, (int)n,
-                       sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib,
-                       tile_order, (float4*)clear_records, n4_clear, win_hi);
+    if (win) GS_FWD_LAUNCH(4, 1, true); else GS_FWD_LAUNCH(4, 1, false);
   } else if (pick_ppt(T) == 4) {
-    hipLaunchKernelGGL(composite_fwd_kernel<2>, dim3(nblk * 2), dim3(64), 0, s, (const float4*)records, (int)n,
-                       sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib,
-                       tile_order, (float4*)clear_records, n4_clear, win_hi);
+    if (win) GS_FWD_LAUNCH(2, 2, true); else GS_FWD_LAUNCH(2, 2, false);
   } else {
-    hipLaunchKernelGGL(composite_fwd_kernel<1>, dim3(nblk * 4), dim3(64), 0, s, (const float4*)records, (int)n,
-                       sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T, n_contrib,
-                       tile_order, (float4*)clear_records, n4_clear, win_hi);
+    if (win) GS_FWD_LAUNCH(1, 4, true); else GS_FWD_LAUNCH(1, 4, false);
   }
+#undef GS_FWD_LAUNCH
   GS_LAUNCH_CHECK("composite_fwd_kernel");
   if (tile_order) {
     hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(1024), 0, s, tile_order, T);

@@ -359,16 +359,90 @@ __device__ inline GaussIn load_gauss(const float* __restrict__ means, const floa
   return a;
 }
 
-// Backward of one Gaussian.  shv: its SH row (registers or LDS), overwritten with the
-// SH cotangent row (K triples, coefficients >= (D+1)^2 get 0); grow: its gradient
-// record.
+// The colour VJP of one Gaussian (renderer.py:40-49 and sh.py:25-72, reversed).  One pass
+// over the SH row forms the three colours from eval_sh_channel's terms in its order (so the
+// clip mask is the forward's, bit for bit) together with the nine partials
+// V[c] = sum_k sh[k][c] dbasis_k/dd; the row is dead afterwards.  Outputs: E[k], the
+// signed basis value multiplying coefficient k in that sum (the SH cotangent row is
+// E[k] * g_pre[c]), g_pre[c] = dL/d(colour before the clip), and the mean's cotangent
+// through the view direction, added to g_m.
 template <int DEG>
-__device__ inline void preprocess_bwd_one(int64_t i, int K, const GaussIn& in, const float* __restrict__ w2c,
-                                          float fx, float fy, const float* grow, float* shv,
-                                          float* __restrict__ g_means, float* __restrict__ g_scales,
-                                          float* __restrict__ g_quats, float* __restrict__ g_opac) {
-  float w[16];
-  load_w2c(w2c, w);
+__device__ inline void colour_vjp(const float* w, float mx, float my, float mz, const float* shv, const float* g_col,
+                                  float* E, float* g_pre, float* g_m) {
+  constexpr int NB = (DEG + 1) * (DEG + 1);
+  float vv[3], nrm, d[3];
+  view_dir(w, mx, my, mz, vv, nrm, d);
+  const float x = d[0], y = d[1], z = d[2];
+  const float xx = x * x, yy = y * y, zz = z * z;
+  const float xy = x * y, yz = y * z, xz = x * z;
+  // eval_sh_channel's factors; k = 1 and 3 enter with a minus sign
+  float F[16];
+  F[0] = SH_C0;
+  if (DEG > 0) {
+    F[1] = SH_C1 * y;
+    F[2] = SH_C1 * z;
+    F[3] = SH_C1 * x;
+  }
+  if (DEG > 1) {
+    F[4] = SH_C2_0 * xy;
+    F[5] = SH_C2_1 * yz;
+    F[6] = SH_C2_2 * ((2.0f * zz - xx) - yy);
+    F[7] = SH_C2_3 * xz;
+    F[8] = SH_C2_4 * (xx - yy);
+  }
+  if (DEG > 2) {
+    F[9] = (SH_C3_0 * y) * (3.0f * xx - yy);
+    F[10] = (SH_C3_1 * xy) * z;
+    F[11] = (SH_C3_2 * y) * ((4.0f * zz - xx) - yy);
+    F[12] = (SH_C3_3 * z) * ((2.0f * zz - 3.0f * xx) - 3.0f * yy);
+    F[13] = (SH_C3_4 * x) * ((4.0f * zz - xx) - yy);
+    F[14] = (SH_C3_5 * z) * (xx - yy);
+    F[15] = (SH_C3_6 * x) * (xx - 3.0f * yy);
+  }
+  float B[16], dB[16][3];
+  sh_basis_and_grad<DEG>(d, B, dB);  // (only the derivatives are used)
+  float res[3], V[3][3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    res[c] = F[0] * shv[c];
+    V[c][0] = V[c][1] = V[c][2] = 0.0f;
+  }
+#pragma unroll
+  for (int k = 1; k < NB; ++k) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      const float sk = shv[3 * k + c];
+      res[c] = (k == 1 || k == 3) ? res[c] - F[k] * sk : res[c] + F[k] * sk;
+      V[c][0] += sk * dB[k][0];
+      V[c][1] += sk * dB[k][1];
+      V[c][2] += sk * dB[k][2];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NB; ++k) E[k] = (k == 1 || k == 3) ? -F[k] : F[k];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const float pre = res[c] + 0.5f;
+    const float lo = jmax(0.0f, pre);
+    g_pre[c] = g_col[c] * dmin_first(lo, 1.0f) * dmax_first(pre, 0.0f);
+  }
+  if (DEG > 0) {
+    float g_d[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) g_d[j] = (g_pre[0] * V[0][j] + g_pre[1] * V[1][j]) + g_pre[2] * V[2][j];
+    const float dg = (d[0] * g_d[0] + d[1] * g_d[1]) + d[2] * g_d[2];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) g_m[k] += (g_d[k] - d[k] * dg) / nrm;
+  }
+}
+
+// Geometric part of the backward of one Gaussian (projection, covariance, conic, opacity)
+// given its gradient record grow; g_mcol: the mean's cotangent through the view direction
+// (colour_vjp), added last.
+__device__ inline void preprocess_bwd_geom(int64_t i, const GaussIn& in, const float* w, float fx, float fy,
+                                           const float* grow, const float* g_mcol, float* __restrict__ g_means,
+                                           float* __restrict__ g_scales, float* __restrict__ g_quats,
+                                           float* __restrict__ g_opac) {
   const float mx = in.mx, my = in.my, mz = in.mz;
   float q[4], ls[3];
 #pragma unroll
@@ -380,14 +454,12 @@ __device__ inline void preprocess_bwd_one(int64_t i, int K, const GaussIn& in, c
 
   const float4 ga = make_float4(grow[0], grow[1], grow[2], grow[3]);
   const float4 gb = make_float4(grow[4], grow[5], grow[6], grow[7]);
-  const float4 gc = make_float4(grow[8], grow[9], grow[10], grow[11]);
   // gradient record (sums over the Gaussian's pixels of dL/dpower times):
   // [0] dx, [1] dy, [2] dx^2, [3] dx dy, [4] dy^2, [5] 1; [6..8] dL/dcolour
   // power = -0.5 (ic00 dx^2 + 2 ic01 dx dy + ic11 dy^2), dx = px - mean2d.x
   const float g_ic00 = -0.5f * ga.z;
   const float g_ic01 = -ga.w;
   const float g_ic11 = -0.5f * gb.x;
-  const float g_col[3] = {gb.z, gb.w, gc.x};
 
   // ---- opacity: alpha = exp(power) * sigmoid(logit); sum dL/dpower = sigmoid * dL/dsigmoid
   const float sg = det_sigmoidf(in.logit);
@@ -452,36 +524,9 @@ __device__ inline void preprocess_bwd_one(int64_t i, int K, const GaussIn& in, c
 #pragma unroll
   for (int k = 0; k < 3; ++k) g_m[k] = (w[0 * 4 + k] * g_x + w[1 * 4 + k] * g_y) + w[2 * 4 + k] * g_z;
 
-  // ---- colour: clip(SH + 0.5, 0, 1)
-  float vv[3], nrm, d[3];
-  view_dir(w, mx, my, mz, vv, nrm, d);
-  constexpr int NB = (DEG + 1) * (DEG + 1);
-  float g_pre[3];
+  // ---- the colour's share through the view direction (colour_vjp)
 #pragma unroll
-  for (int c = 0; c < 3; ++c) {
-    const float pre = eval_sh_channel<DEG>(shv, c, d) + 0.5f;
-    const float lo = jmax(0.0f, pre);
-    g_pre[c] = g_col[c] * dmin_first(lo, 1.0f) * dmax_first(pre, 0.0f);
-  }
-  float B[16], dB[16][3];
-  sh_basis_and_grad<DEG>(d, B, dB);
-  float g_d[3] = {0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int k = 0; k < NB; ++k) {
-    const float sk = (shv[3 * k] * g_pre[0] + shv[3 * k + 1] * g_pre[1]) + shv[3 * k + 2] * g_pre[2];
-    g_d[0] += sk * dB[k][0];
-    g_d[1] += sk * dB[k][1];
-    g_d[2] += sk * dB[k][2];
-    shv[3 * k] = B[k] * g_pre[0];
-    shv[3 * k + 1] = B[k] * g_pre[1];
-    shv[3 * k + 2] = B[k] * g_pre[2];
-  }
-  for (int q = 3 * NB; q < 3 * K; ++q) shv[q] = 0.0f;
-  if (DEG > 0) {
-    const float dg = (d[0] * g_d[0] + d[1] * g_d[1]) + d[2] * g_d[2];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) g_m[k] += (g_d[k] - d[k] * dg) / nrm;
-  }
+  for (int k = 0; k < 3; ++k) g_m[k] += g_mcol[k];
   g_means[3 * i] = g_m[0];
   g_means[3 * i + 1] = g_m[1];
   g_means[3 * i + 2] = g_m[2];
@@ -527,6 +572,27 @@ __device__ inline void preprocess_bwd_one(int64_t i, int K, const GaussIn& in, c
   for (int k = 0; k < 4; ++k) g_quats[4 * i + k] = (gq[k] - p.qn[k] * qd) / p.qnorm;
 }
 
+// Backward of one Gaussian.  shv: its SH row (registers), overwritten with the SH
+// cotangent row (K triples, coefficients >= (D+1)^2 get 0); grow: its gradient record.
+template <int DEG>
+__device__ inline void preprocess_bwd_one(int64_t i, int K, const GaussIn& in, const float* __restrict__ w2c,
+                                          float fx, float fy, const float* grow, float* shv,
+                                          float* __restrict__ g_means, float* __restrict__ g_scales,
+                                          float* __restrict__ g_quats, float* __restrict__ g_opac) {
+  constexpr int NB = (DEG + 1) * (DEG + 1);
+  float w[16];
+  load_w2c(w2c, w);
+  float E[16], g_pre[3], g_mcol[3] = {0.0f, 0.0f, 0.0f};
+  const float g_col[3] = {grow[6], grow[7], grow[8]};
+  colour_vjp<DEG>(w, in.mx, in.my, in.mz, shv, g_col, E, g_pre, g_mcol);
+#pragma unroll
+  for (int k = 0; k < NB; ++k)
+#pragma unroll
+    for (int c = 0; c < 3; ++c) shv[3 * k + c] = E[k] * g_pre[c];
+  for (int q = 3 * NB; q < 3 * K; ++q) shv[q] = 0.0f;
+  preprocess_bwd_geom(i, in, w, fx, fy, grow, g_mcol, g_means, g_scales, g_quats, g_opac);
+}
+
 // One thread per Gaussian, one wave per 64 Gaussians.  Each lane loads its SH row and
 // gradient record straight into registers and stores its SH cotangent row from them
 // (16-byte accesses when rows are 16-byte aligned); no LDS, so occupancy is set by
@@ -552,19 +618,26 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   load_row<3 * NB>(sh + ic * KC, aligned, shv);
   load_row<kRec>(grec + ic * kRec, (reinterpret_cast<uintptr_t>(grec) & 15) == 0, grow);
   if (i >= n) return;
-  // K = NB: the register row holds the first 3 NB values only; the rest is zeroed below
-  preprocess_bwd_one<DEG>(i, NB, in, w2c, fx, fy, grow, shv, g_means, g_scales, g_quats, g_opac);
+  float w[16];
+  load_w2c(w2c, w);
+  // the colour VJP first: the SH row is dead once it returns, so the geometric VJP
+  // below does not hold it
+  float E[16], g_pre[3], g_mcol[3] = {0.0f, 0.0f, 0.0f};
+  const float g_col[3] = {grow[6], grow[7], grow[8]};
+  colour_vjp<DEG>(w, in.mx, in.my, in.mz, shv, g_col, E, g_pre, g_mcol);
   float* __restrict__ dst = g_sh + i * KC;
+  auto cot = [&](int t) { return t < 3 * NB ? E[t / 3] * g_pre[t % 3] : 0.0f; };
   if (aligned && (3 * NB) % 4 == 0) {
 #pragma unroll
     for (int t = 0; t < 3 * NB / 4; ++t)
-      reinterpret_cast<float4*>(dst)[t] = make_float4(shv[4 * t], shv[4 * t + 1], shv[4 * t + 2], shv[4 * t + 3]);
+      reinterpret_cast<float4*>(dst)[t] = make_float4(cot(4 * t), cot(4 * t + 1), cot(4 * t + 2), cot(4 * t + 3));
     for (int t = 3 * NB / 4; t < KC / 4; ++t) reinterpret_cast<float4*>(dst)[t] = make_float4(0.f, 0.f, 0.f, 0.f);
   } else {
 #pragma unroll
-    for (int t = 0; t < 3 * NB; ++t) dst[t] = shv[t];
+    for (int t = 0; t < 3 * NB; ++t) dst[t] = cot(t);
     for (int t = 3 * NB; t < KC; ++t) dst[t] = 0.0f;
   }
+  preprocess_bwd_geom(i, in, w, fx, fy, grow, g_mcol, g_means, g_scales, g_quats, g_opac);
 }
 
 // The training step's tail in one pass (trainer.py:137-159 with optax.adam of
