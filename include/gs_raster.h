@@ -61,6 +61,8 @@ extern "C" {
 #define GS_STAT_NEGATIVE_DEPTH 7   /* Gaussians whose depth has its sign bit set */
 #define GS_STAT_CAPACITY_EXCEEDED 8 /* 1 when n_interactions > capacity */
 #define GS_STAT_MEAN_PER_TILE 9     /* float32 bits of float(n_interactions) / num_tiles */
+#define GS_STAT_TILE_ENTRIES 10     /* entries of tiles 0..T-1 (= ranges[T]); n_interactions also
+                                       counts valid slots of negative-depth Gaussians (tile -1) */
 #define GS_NUM_STATS 16
 
 const char* gs_last_error(void);
@@ -127,6 +129,23 @@ int gs_bin_static(void* stream, int64_t n, const float* means2d, const float* ra
                   const uint8_t* valid, const float* depths, int width, int height,
                   int64_t capacity, int32_t* sorted_gids, int32_t* sorted_tiles, int32_t* ranges,
                   int32_t* stats);
+
+/* Workspace bytes gs_bin_reference needs. */
+size_t gs_bin_reference_workspace_size(int64_t n, int width, int height);
+
+/* The reference's own output arrays of get_tile_interactions, all L = max(256 n, 512)
+ * slots in the order of its stable sort of every slot's key (tile << 13) | depth
+ * quantum (jax_gs/renderer/rasterizer.py:56-116): the 256 slots of each Gaussian whose
+ * depth has its sign bit set (tile -1), then gs_bin's entries, then the remaining
+ * 256 - count slots of every other Gaussian (tile T), both runs with Gaussians in
+ * (quantum, id) order, then padding (tile T, id 0).  ranges[T+1] are the searchsorted-left
+ * boundaries of these arrays (renderer.py:57-61); stats as gs_bin's (n_interactions is the
+ * reference's n, which also counts valid slots of negative-depth Gaussians).
+ * n < 2^23 (256 n slots indexed with int32). */
+int gs_bin_reference(void* stream, int64_t n, const float* means2d, const float* radii,
+                     const uint8_t* valid, const float* depths, int width, int height, void* workspace,
+                     size_t workspace_bytes, int32_t* sorted_tiles, int32_t* sorted_gids, int32_t* ranges,
+                     int32_t* stats);
 
 /* Tile boundaries of an arbitrary sorted tile-id array (length L, entries in
  * [-1, T]): ranges[t] = first index with tile >= t for t in 0..T.

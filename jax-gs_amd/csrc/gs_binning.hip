@@ -60,6 +60,7 @@ constexpr int kPairSpan = 256;                    // Gaussians per superblock-so
 constexpr int kBig = 1024;                        // single-block kernels
 constexpr int kDepthRB = 7;                       // depth buckets: two 7-bit digits
 constexpr int kPairRB = 8;                        // superblock ids: 8-bit digits
+constexpr int kBlkStats = 3;  // per bin_prep block: cap violations, negative depths, their entries
 
 __device__ inline uint64_t lanemask_lt() {
   const unsigned lane = threadIdx.x & 63;
@@ -149,6 +150,34 @@ __device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t* total) {
   return wbase + inc - v;
 }
 
+// rasterizer.py:36-51 for one Gaussian: the tile rectangle of its box clipped to the
+// image (floor(x / 16) of clipped coordinates; NaN, only for invalid Gaussians,
+// converts to 0 as XLA's does), the strict on-screen test, and v, whether its slots
+// hold entries; count = the number of entries (slots of the 16 x 16 offset grid inside
+// the rectangle, rasterizer.py:56-69).
+struct TileRect {
+  int tminx, tminy, spanx, spany;
+  bool proj_valid, on_screen, v;
+  __device__ int count() const { return v ? (spanx < kOffset ? spanx : kOffset) * (spany < kOffset ? spany : kOffset) : 0; }
+};
+__device__ inline TileRect tile_rect(float mx, float my, float rr, bool proj_valid, int W, int H) {
+  TileRect t;
+  const float wm1 = (float)(W - 1), hm1 = (float)(H - 1);
+  const float minx = jmin(jmax(mx - rr, 0.0f), wm1);
+  const float maxx = jmin(jmax(mx + rr, 0.0f), wm1);
+  const float miny = jmin(jmax(my - rr, 0.0f), hm1);
+  const float maxy = jmin(jmax(my + rr, 0.0f), hm1);
+  t.tminx = (int)floorf(minx / 16.0f);
+  t.tminy = (int)floorf(miny / 16.0f);
+  const int tmaxx = (int)floorf(maxx / 16.0f), tmaxy = (int)floorf(maxy / 16.0f);
+  t.on_screen = (mx + rr > 0.0f) && (mx - rr < (float)W) && (my + rr > 0.0f) && (my - rr < (float)H);
+  t.proj_valid = proj_valid;
+  t.v = proj_valid && t.on_screen && (tmaxx >= t.tminx) && (tmaxy >= t.tminy);
+  t.spanx = tmaxx - t.tminx + 1;
+  t.spany = tmaxy - t.tminy + 1;
+  return t;
+}
+
 // ---------------------------------------------------------------------------------
 // 1. per-Gaussian rectangle and depth bucket (rasterizer.py:36-51, 84-94;
 //    renderer.py:63-75 for the radius-cap statistic).  Block b handles Gaussians
@@ -170,55 +199,52 @@ __global__ __launch_bounds__(kPrepBlock) void bin_prep_kernel(int64_t n, const f
     for (int64_t z = z0 + threadIdx.x; z < z1; z += kPrepBlock) zero_buf[z] = make_uint4(0u, 0u, 0u, 0u);
   }
   __shared__ uint32_t hist[NB];
-  __shared__ uint32_t wcnt[2][kPrepBlock / 64];
+  __shared__ uint32_t wcnt[kBlkStats][kPrepBlock / 64];
   for (int d = threadIdx.x; d < NB; d += kPrepBlock) hist[d] = 0;
   __syncthreads();
-  uint32_t capc = 0, negc = 0;
+  uint32_t capc = 0, negc = 0, neg_entries = 0;
   for (int r = 0; r < kPrepPer; ++r) {
     const int64_t i = (int64_t)blockIdx.x * kSpan + r * kPrepBlock + threadIdx.x;
     bool cap_violation = false, negative = false;
     if (i < n) {
-      const float mx = means2d[2 * i], my = means2d[2 * i + 1], rr = radii[i];
-      const float wm1 = (float)(W - 1), hm1 = (float)(H - 1);
-      const float minx = jmin(jmax(mx - rr, 0.0f), wm1);
-      const float maxx = jmin(jmax(mx + rr, 0.0f), wm1);
-      const float miny = jmin(jmax(my - rr, 0.0f), hm1);
-      const float maxy = jmin(jmax(my + rr, 0.0f), hm1);
-      // floor(x/16) of values in [0, W-1] (NaN only for Gaussians that are invalid).
-      const int tminx = (int)floorf(minx / 16.0f), tmaxx = (int)floorf(maxx / 16.0f);
-      const int tminy = (int)floorf(miny / 16.0f), tmaxy = (int)floorf(maxy / 16.0f);
-      const bool on_screen = (mx + rr > 0.0f) && (mx - rr < (float)W) && (my + rr > 0.0f) && (my - rr < (float)H);
-      const bool proj_valid = valid[i] != 0;
-      const bool v = proj_valid && on_screen && (tmaxx >= tminx) && (tmaxy >= tminy);
-      const int spanx = tmaxx - tminx + 1, spany = tmaxy - tminy + 1;
-      cap_violation = proj_valid && on_screen && (spanx > kOffset || spany > kOffset);
+      const TileRect t = tile_rect(means2d[2 * i], means2d[2 * i + 1], radii[i], valid[i] != 0, W, H);
+      cap_violation = t.proj_valid && t.on_screen && (t.spanx > kOffset || t.spany > kOffset);
       const uint32_t zb = float_to_bits(depths[i]);
       negative = (zb >> 31) != 0;
+      // A depth with its sign bit set makes every key of the Gaussian negative, so its
+      // valid slots sort in front with tile -1 (rasterizer.py:98-104): they count as
+      // interactions but are no tile's entries.  (project_gaussians never marks such a
+      // Gaussian valid; get_tile_interactions' caller may.)
+      const bool e = t.v && !negative;
+      if (t.v && negative) neg_entries += (uint32_t)t.count();
       uint32_t key = kDepthBinEmpty;
       int w = 0, h = 0;
-      if (v) {
-        w = spanx < kOffset ? spanx : kOffset;
-        h = spany < kOffset ? spany : kOffset;
-        // v implies depth > 0.01, so the 13-bit bucket is in [3848, 8191].
-        key = (zb >> (31 - kDepthBits)) - kDepthBucketLo;
+      if (e) {
+        w = t.spanx < kOffset ? t.spanx : kOffset;
+        h = t.spany < kOffset ? t.spany : kOffset;
+        key = depth_key(zb);
       }
       dkey[i] = key;
-      word[i] = pack((uint32_t)i, v ? tminx : 0, v ? tminy : 0, w, h);
+      word[i] = pack((uint32_t)i, e ? t.tminx : 0, e ? t.tminy : 0, w, h);
       // Gaussians that meet no tile are dropped by the first radix pass: not counted
-      if (v) atomicAdd(&hist[key & (NB - 1)], 1u);
+      if (e) atomicAdd(&hist[key & (NB - 1)], 1u);
     }
     capc += (uint32_t)__popcll(__ballot(cap_violation));
     negc += (uint32_t)__popcll(__ballot(negative));
   }
+  // entries of negative-depth Gaussians: a wave sum (at most 256 per Gaussian)
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) neg_entries += __shfl_xor(neg_entries, o, 64);
   if ((threadIdx.x & 63) == 0) {
     wcnt[0][threadIdx.x >> 6] = capc;
     wcnt[1][threadIdx.x >> 6] = negc;
+    wcnt[2][threadIdx.x >> 6] = neg_entries;
   }
   __syncthreads();
-  if (threadIdx.x < 2) {
+  if (threadIdx.x < kBlkStats) {
     uint32_t s = 0;
     for (int k = 0; k < kPrepBlock / 64; ++k) s += wcnt[threadIdx.x][k];
-    blkstat[2 * (int64_t)blockIdx.x + threadIdx.x] = s;
+    blkstat[kBlkStats * (int64_t)blockIdx.x + threadIdx.x] = s;
   }
   for (int d = threadIdx.x; d < NB; d += kPrepBlock) table[(int64_t)d * G + blockIdx.x] = hist[d];
 }
@@ -713,28 +739,32 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
                                                                int32_t* __restrict__ stats) {
   constexpr int kPer = 8, kRound = kBig * kPer;
   __shared__ uint32_t stage[kBig * (kPer + 1)];
-  __shared__ int64_t red[7][kBig / 64];
+  __shared__ int64_t red[8][kBig / 64];
   const int tid = threadIdx.x;
-  int64_t acc[7] = {0, 0, 0, 0, 0, 0, 0};  // max, ovf tiles, ovf inter, trunc tiles, trunc inter, cap, neg
+  // max, ovf tiles, ovf inter, trunc tiles, trunc inter, cap, neg, negative-depth entries
+  int64_t acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   uint32_t carry = 0;
   // blkstat loads first: they are independent of the tile rounds
-  uint32_t s5 = 0, s6 = 0;
+  uint32_t s5 = 0, s6 = 0, s7 = 0;
   for (int b0 = 0; b0 < nblk; b0 += 4 * kBig) {
-    uint32_t a[4], z[4];
+    uint32_t a[4], z[4], y[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int b = b0 + k * kBig + tid;
-      a[k] = b < nblk ? blkstat[2 * b] : 0u;
-      z[k] = b < nblk ? blkstat[2 * b + 1] : 0u;
+      a[k] = b < nblk ? blkstat[kBlkStats * b] : 0u;
+      z[k] = b < nblk ? blkstat[kBlkStats * b + 1] : 0u;
+      y[k] = b < nblk ? blkstat[kBlkStats * b + 2] : 0u;
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       s5 += a[k];
       s6 += z[k];
+      s7 += y[k];
     }
   }
   acc[5] = s5;
   acc[6] = s6;
+  acc[7] = s7;
   for (int r0 = 0; r0 < T; r0 += kRound) {
     uint32_t v[kPer];
 #pragma unroll
@@ -776,10 +806,10 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
     carry += round_total;
     __syncthreads();  // the stage is rewritten by the next round
   }
-  // reduce the 7 accumulators over the block
+  // reduce the 8 accumulators over the block
   const int lane = tid & 63, wid = tid >> 6;
 #pragma unroll
-  for (int k = 0; k < 7; ++k) {
+  for (int k = 0; k < 8; ++k) {
     int64_t x = acc[k];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -790,13 +820,16 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
   }
   __syncthreads();
   if (tid == 0) {
-    int64_t r[7] = {0, 0, 0, 0, 0, 0, 0};
+    int64_t r[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int w = 0; w < kBig / 64; ++w)
-      for (int k = 0; k < 7; ++k) r[k] = k == 0 ? (r[0] > red[0][w] ? r[0] : red[0][w]) : r[k] + red[k][w];
+      for (int k = 0; k < 8; ++k) r[k] = k == 0 ? (r[0] > red[0][w] ? r[0] : red[0][w]) : r[k] + red[k][w];
     const int64_t m = carry;
+    // the reference counts the valid slots of negative-depth Gaussians too (tile -1)
+    const int64_t n_int = m + r[7];
     ranges[T] = (int32_t)m;
     for (int k = 0; k < GS_NUM_STATS; ++k) stats[k] = 0;
-    stats[GS_STAT_N_INTERACTIONS] = (int32_t)m;
+    stats[GS_STAT_N_INTERACTIONS] = (int32_t)n_int;
+    stats[GS_STAT_TILE_ENTRIES] = (int32_t)m;
     stats[GS_STAT_MAX_PER_TILE] = (int32_t)r[0];
     stats[GS_STAT_OVERFLOW_TILES] = (int32_t)r[1];
     stats[GS_STAT_OVERFLOW_INTERACTIONS] = (int32_t)r[2];
@@ -806,7 +839,7 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
     stats[GS_STAT_NEGATIVE_DEPTH] = (int32_t)r[6];
     stats[GS_STAT_CAPACITY_EXCEEDED] = m > cap ? 1 : 0;
     // renderer.py:81: float32(n_interactions) / num_tiles
-    stats[GS_STAT_MEAN_PER_TILE] = (int32_t)float_to_bits((float)(int32_t)m / (float)T);
+    stats[GS_STAT_MEAN_PER_TILE] = (int32_t)float_to_bits((float)(int32_t)n_int / (float)T);
   }
 }
 
@@ -926,7 +959,10 @@ __device__ inline void write_chunk(const uint4& d, const uint64_t* __restrict__ 
                                     out_tile);
 }
 
-template <bool WITH_TILES>
+// OFFSET: the entries go after the 256 slots of every negative-depth Gaussian (the
+// reference's full arrays): the outputs start at 256 * stats[GS_STAT_NEGATIVE_DEPTH],
+// which tile_scan_stats_kernel has written.
+template <bool WITH_TILES, bool OFFSET>
 __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restrict__ n_chunks, int64_t cmax,
                                                          const uint4* __restrict__ desc,
                                                          const uint64_t* __restrict__ pval, uint32_t n_gauss, int TX,
@@ -934,10 +970,17 @@ __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restr
                                                          const uint32_t* __restrict__ seg_pre,
                                                          const int32_t* __restrict__ ranges, int T, int64_t cap,
                                                          int32_t* __restrict__ out_gid,
-                                                         int32_t* __restrict__ out_tile) {
+                                                         int32_t* __restrict__ out_tile,
+                                                         const int32_t* __restrict__ stats) {
   const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
   const uint32_t C = (uint32_t)min<int64_t>((int64_t)*n_chunks, cmax);
+  if (OFFSET) {
+    const int64_t off = 256 * (int64_t)stats[GS_STAT_NEGATIVE_DEPTH];
+    out_gid += off;
+    if (WITH_TILES) out_tile += off;
+    cap -= off;  // >= the entry count: every Gaussian's entries fit in its 256 slots
+  }
   const uint32_t cap32 = (uint32_t)cap;  // gs_bin checks cap < 2^31
   // every entry fits (the usual case): no per-store capacity test
   const bool fits = ranges[T] >= 0 && (int64_t)ranges[T] <= cap;
@@ -1019,7 +1062,7 @@ BinPlan make_plan(int64_t n, int width, int height, int64_t capacity) {
   P.o_cnt = take((size_t)P.cmax * 64 * 4);
   P.o_desc = take((size_t)P.cmax * 16);
   P.o_tot = take((size_t)P.T * 4);
-  P.o_blk = take((size_t)P.G_d * 2 * 4);
+  P.o_blk = take((size_t)P.G_d * kBlkStats * 4);
   P.o_gbase = take(((size_t)P.S + 1) * 4);
   P.o_gsum = take((size_t)P.gmax * 64 * 4);
   P.total = o;
@@ -1055,10 +1098,11 @@ extern "C" size_t gs_bin_workspace_size(int64_t n, int width, int height, int64_
   return make_plan(n, width, height, capacity).total;
 }
 
-extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float* radii, const uint8_t* valid,
-                      const float* depths, int width, int height, int64_t capacity, void* workspace,
-                      size_t workspace_bytes, int32_t* sorted_gids, int32_t* sorted_tiles, int32_t* ranges,
-                      int32_t* stats) {
+namespace gs {
+namespace {
+int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, const uint8_t* valid,
+            const float* depths, int width, int height, int64_t capacity, void* workspace, size_t workspace_bytes,
+            int32_t* sorted_gids, int32_t* sorted_tiles, int32_t* ranges, int32_t* stats, bool ref_offset) {
   GS_REQUIRE(n >= 0 && n <= ((int64_t)1 << 26), "gs_bin: n must be in [0, 2^26] (got %lld)", (long long)n);
   GS_REQUIRE(width > 0 && height > 0 && width <= 4096 * kTile && height <= 4096 * kTile,
              "gs_bin: bad image size %dx%d (each side at most 65536)", width, height);
@@ -1159,14 +1203,28 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   GS_LAUNCH_CHECK("chunk_scan_kernel");
   hipLaunchKernelGGL(tile_scan_stats_kernel, dim3(1), dim3(kBig), 0, s, tot, P.T, blk, P.G_d, P.cap, ranges, stats);
   GS_LAUNCH_CHECK("tile_scan_stats_kernel");
-  if (sorted_tiles != nullptr)
-    hipLaunchKernelGGL(tile_write_kernel<true>, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, desc, sbval,
-                       (uint32_t)n, P.TX, P.TY, cnt, gsum, ranges, P.T, P.cap, sorted_gids, sorted_tiles);
+#define GS_WRITE_LAUNCH(TILES, OFF)                                                                             \
+  hipLaunchKernelGGL((tile_write_kernel<TILES, OFF>), dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, desc, \
+                     sbval, (uint32_t)n, P.TX, P.TY, cnt, gsum, ranges, P.T, P.cap, sorted_gids, sorted_tiles, stats)
+  if (ref_offset)
+    GS_WRITE_LAUNCH(true, true);
+  else if (sorted_tiles != nullptr)
+    GS_WRITE_LAUNCH(true, false);
   else
-    hipLaunchKernelGGL(tile_write_kernel<false>, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, desc, sbval,
-                       (uint32_t)n, P.TX, P.TY, cnt, gsum, ranges, P.T, P.cap, sorted_gids, sorted_tiles);
+    GS_WRITE_LAUNCH(false, false);
+#undef GS_WRITE_LAUNCH
   GS_LAUNCH_CHECK("tile_write_kernel");
   return GS_OK;
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float* radii, const uint8_t* valid,
+                      const float* depths, int width, int height, int64_t capacity, void* workspace,
+                      size_t workspace_bytes, int32_t* sorted_gids, int32_t* sorted_tiles, int32_t* ranges,
+                      int32_t* stats) {
+  return bin_run(stream, n, means2d, radii, valid, depths, width, height, capacity, workspace, workspace_bytes,
+                 sorted_gids, sorted_tiles, ranges, stats, false);
 }
 
 // Same boundary rule on a caller-provided sorted array that may hold -1 (negative
@@ -1248,4 +1306,204 @@ extern "C" int gs_bin_static(void* stream, int64_t n, const float* means2d, cons
   if (rc != GS_OK) return rc;
   return gs_bin(stream, n, means2d, radii, valid, depths, width, height, capacity, ws,
                 (size_t)GS_BIN_STATIC_SCRATCH_BYTES, sorted_gids, sorted_tiles, ranges, stats);
+}
+
+// ---------------------------------------------------------------------------------
+// The reference's full arrays (rasterizer.py:84-114): all 256 n slots in the order of the
+// stable sort of their keys (tile << 13) | dq, with dq the Gaussian's signed depth
+// quantum and tile = T for a slot that holds no entry; a negative dq makes every key of
+// its Gaussian negative (tile -1).  In order:
+//   * the 256 slots of every negative-depth Gaussian, tile -1, Gaussians in (dq, id) order;
+//   * the entries, tiles 0..T-1 (gs_bin's list, written there by the offset write sweep);
+//   * the 256 - count empty slots of every other Gaussian, tile T, in (dq, id) order;
+//   * when 256 n < 512, padding up to 512 with tile T and id 0 (rasterizer.py:107-114).
+// The two runs of slots come from one stable sort of all Gaussians by dq (two 7-bit
+// radix passes: negative quanta sort first) and a scan of their slot counts.
+namespace gs {
+namespace {
+
+// per Gaussian: sort key dq + 8192 and value id | (slots << 32), slots = 256 for a
+// negative depth, else 256 - (its entries)
+__global__ __launch_bounds__(kPrepBlock) void ref_prep_kernel(int64_t n, const float* __restrict__ means2d,
+                                                              const float* __restrict__ radii,
+                                                              const uint8_t* __restrict__ valid,
+                                                              const float* __restrict__ depths, int W, int H,
+                                                              uint32_t* __restrict__ keys,
+                                                              uint64_t* __restrict__ vals) {
+  for (int r = 0; r < kPrepPer; ++r) {
+    const int64_t i = (int64_t)blockIdx.x * kSpan + r * kPrepBlock + threadIdx.x;
+    if (i >= n) continue;
+    const TileRect t = tile_rect(means2d[2 * i], means2d[2 * i + 1], radii[i], valid[i] != 0, W, H);
+    const uint32_t zb = float_to_bits(depths[i]);
+    const uint32_t slots = (zb >> 31) ? 256u : 256u - (uint32_t)t.count();
+    keys[i] = depth_key(zb);
+    vals[i] = (uint64_t)i | ((uint64_t)slots << 32);
+  }
+}
+
+// slots of the kSpan sorted Gaussians of each workgroup
+__global__ __launch_bounds__(kPrepBlock) void ref_sum_kernel(int64_t n, const uint64_t* __restrict__ vals,
+                                                             uint32_t* __restrict__ gsum) {
+  uint32_t s = 0;
+  for (int r = 0; r < kPrepPer; ++r) {
+    const int64_t i = (int64_t)blockIdx.x * kSpan + r * kPrepBlock + threadIdx.x;
+    if (i < n) s += (uint32_t)(vals[i] >> 32);
+  }
+  uint32_t tot;
+  block_excl_scan<kPrepBlock>(s, &tot);
+  if (threadIdx.x == 0) gsum[blockIdx.x] = tot;
+}
+
+// one block: exclusive scan of the G workgroup sums in place
+__global__ __launch_bounds__(kBig) void ref_scan_kernel(uint32_t* __restrict__ gsum, int G) {
+  uint32_t carry = 0;
+  for (int r0 = 0; r0 < G; r0 += kBig) {
+    const int g = r0 + threadIdx.x;
+    const uint32_t v = g < G ? gsum[g] : 0u;
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan<kBig>(v, &tot);
+    if (g < G) gsum[g] = carry + ex;
+    carry += tot;
+    __syncthreads();
+  }
+}
+
+// Each workgroup places its kSpan sorted Gaussians' runs: the first slot of a Gaussian is
+// its workgroup's base plus the slots before it in the workgroup; Gaussians after the
+// n_neg negative-depth ones also skip the entries.  Each wave writes the runs of every
+// fourth Gaussian (at most 256 slots each).  Workgroup 0 also writes the padding and
+// moves the tile ranges past the tile -1 slots.
+__global__ __launch_bounds__(kPrepBlock) void ref_fill_kernel(int64_t n, const uint64_t* __restrict__ vals,
+                                                              const uint32_t* __restrict__ gsum,
+                                                              const int32_t* __restrict__ stats, int T, int64_t L,
+                                                              int32_t* __restrict__ out_tiles,
+                                                              int32_t* __restrict__ out_gids,
+                                                              int32_t* __restrict__ ranges) {
+  __shared__ uint32_t pos_s[kSpan], gid_s[kSpan];
+  __shared__ uint16_t cnt_s[kSpan];
+  const int tid = threadIdx.x;
+  const int64_t b0 = (int64_t)blockIdx.x * kSpan;
+  const int64_t n_neg = stats[GS_STAT_NEGATIVE_DEPTH];
+  const uint32_t n_ent = (uint32_t)stats[GS_STAT_TILE_ENTRIES];
+  static_assert(kSpan == 4 * kPrepBlock, "four consecutive Gaussians per thread");
+  uint32_t e[4], g[4], run = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t i = b0 + 4 * tid + k;
+    const uint64_t v = i < n ? vals[i] : 0ull;
+    e[k] = (uint32_t)(v >> 32);
+    g[k] = (uint32_t)v;
+    run += e[k];
+  }
+  uint32_t tot;
+  uint32_t p = gsum[blockIdx.x] + block_excl_scan<kPrepBlock>(run, &tot);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t i = b0 + 4 * tid + k;
+    pos_s[4 * tid + k] = p + (i >= n_neg ? n_ent : 0u);
+    gid_s[4 * tid + k] = g[k];
+    cnt_s[4 * tid + k] = (uint16_t)e[k];
+    p += e[k];
+  }
+  __syncthreads();
+  const int lane = tid & 63, w = tid >> 6;
+  for (int j = w; j < kSpan; j += kPrepBlock / 64) {
+    const int64_t i = b0 + j;
+    if (i >= n) break;
+    const uint32_t c = cnt_s[j], base = pos_s[j];
+    const int32_t gid = (int32_t)gid_s[j], tile = i < n_neg ? -1 : T;
+    for (uint32_t q = lane; q < c; q += 64) {
+      if ((int64_t)base + q >= L) break;  // never, for stats consistent with the slot counts
+      out_gids[base + q] = gid;
+      out_tiles[base + q] = tile;
+    }
+  }
+  if (blockIdx.x == 0) {
+    for (int64_t q = 256 * n + tid; q < L; q += kPrepBlock) {
+      out_tiles[q] = T;
+      out_gids[q] = 0;
+    }
+    for (int t = tid; t <= T; t += kPrepBlock) ranges[t] += (int32_t)(256 * n_neg);
+  }
+}
+
+struct RefPlan {
+  BinPlan bin;
+  int64_t L;
+  int G;
+  size_t o_keys, o_vals, o_keys2, o_vals2, o_table, o_dtot, o_gsum, total;
+};
+
+RefPlan make_ref_plan(int64_t n, int width, int height) {
+  RefPlan R;
+  R.L = std::max<int64_t>(256 * n, kBlock);
+  R.bin = make_plan(n, width, height, R.L);
+  const int64_t nn = std::max<int64_t>(n, 1);
+  R.G = (int)((nn + kSpan - 1) / kSpan);
+  size_t o = R.bin.total;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o = align256(o + bytes);
+    return at;
+  };
+  R.o_keys = take(nn * 4);
+  R.o_vals = take(nn * 8);
+  R.o_keys2 = take(nn * 4);
+  R.o_vals2 = take(nn * 8);
+  R.o_table = take((size_t)(1 << kDepthRB) * R.G * 4);
+  R.o_dtot = take((1 << kDepthRB) * 4);
+  R.o_gsum = take((size_t)R.G * 4);
+  R.total = o;
+  return R;
+}
+
+}  // namespace
+}  // namespace gs
+
+extern "C" size_t gs_bin_reference_workspace_size(int64_t n, int width, int height) {
+  if (n < 0 || width <= 0 || height <= 0) return 0;
+  return make_ref_plan(n, width, height).total;
+}
+
+extern "C" int gs_bin_reference(void* stream, int64_t n, const float* means2d, const float* radii,
+                                const uint8_t* valid, const float* depths, int width, int height, void* workspace,
+                                size_t workspace_bytes, int32_t* sorted_tiles, int32_t* sorted_gids, int32_t* ranges,
+                                int32_t* stats) {
+  GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 23), "gs_bin_reference: n must be in [0, 2^23) (got %lld): the %s",
+             (long long)n, "256 n slots are indexed with int32");
+  GS_REQUIRE(width > 0 && height > 0, "gs_bin_reference: bad image size %dx%d", width, height);
+  const RefPlan R = make_ref_plan(n, width, height);
+  GS_REQUIRE(workspace != nullptr && workspace_bytes >= R.total,
+             "gs_bin_reference: workspace of %zu bytes is smaller than the %zu required", workspace_bytes, R.total);
+  GS_REQUIRE(sorted_tiles && sorted_gids && ranges && stats, "gs_bin_reference: NULL output");
+  hipStream_t s = (hipStream_t)stream;
+  int rc = bin_run(stream, n, means2d, radii, valid, depths, width, height, R.L, workspace, R.bin.total, sorted_gids,
+                   sorted_tiles, ranges, stats, true);
+  if (rc != GS_OK) return rc;
+  char* ws = (char*)workspace;
+  uint32_t* keys = (uint32_t*)(ws + R.o_keys);
+  uint64_t* vals = (uint64_t*)(ws + R.o_vals);
+  uint32_t* keys2 = (uint32_t*)(ws + R.o_keys2);
+  uint64_t* vals2 = (uint64_t*)(ws + R.o_vals2);
+  uint32_t* table = (uint32_t*)(ws + R.o_table);
+  uint32_t* dtot = (uint32_t*)(ws + R.o_dtot);
+  uint32_t* gsum = (uint32_t*)(ws + R.o_gsum);
+  if (n > 0) {
+    hipLaunchKernelGGL(ref_prep_kernel, dim3(R.G), dim3(kPrepBlock), 0, s, n, means2d, radii, valid, depths, width,
+                       height, keys, vals);
+    GS_LAUNCH_CHECK("ref_prep_kernel");
+    rc = radix_pass<kDepthRB>(s, true, keys, vals, keys2, vals2, nullptr, n, n, 0, R.G, kSpan, table, dtot);
+    if (rc != GS_OK) return rc;
+    rc = radix_pass<kDepthRB>(s, true, keys2, vals2, keys, vals, nullptr, n, n, kDepthRB, R.G, kSpan, table, dtot);
+    if (rc != GS_OK) return rc;
+    hipLaunchKernelGGL(ref_sum_kernel, dim3(R.G), dim3(kPrepBlock), 0, s, n, vals, gsum);
+    GS_LAUNCH_CHECK("ref_sum_kernel");
+    hipLaunchKernelGGL(ref_scan_kernel, dim3(1), dim3(kBig), 0, s, gsum, R.G);
+    GS_LAUNCH_CHECK("ref_scan_kernel");
+  }
+  // with n = 0 gs_bin has cleared the stats and ranges: one workgroup writes the padding
+  hipLaunchKernelGGL(ref_fill_kernel, dim3(n > 0 ? R.G : 1), dim3(kPrepBlock), 0, s, n, vals, gsum, stats,
+                     R.bin.T, R.L, sorted_tiles, sorted_gids, ranges);
+  GS_LAUNCH_CHECK("ref_fill_kernel");
+  return GS_OK;
 }

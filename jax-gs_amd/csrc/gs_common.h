@@ -19,11 +19,15 @@ constexpr int kBlock = GS_BLOCK_SIZE;               // rasterizer.py:8
 constexpr int kMaxTileEntries = GS_MAX_TILE_INTERACTIONS;  // rasterizer.py:10
 constexpr int kRec = GS_REC_STRIDE;
 constexpr int kDepthBits = 13;                      // rasterizer.py:84
-// A valid entry has depth z > 0.01, so bits(z) >> 18 lies in [3848, 8191]:
-// the depth bucket is stored relative to 3848.
-constexpr int kDepthBucketLo = 3848;
-constexpr int kDepthBuckets = 8192 - kDepthBucketLo;  // 4344 live buckets
-constexpr int kDepthBinEmpty = kDepthBuckets;         // Gaussians with no tile
+// The depth quantum is bits(z) >> 18 with an arithmetic shift (rasterizer.py:94-95), a
+// signed 14-bit value in [-8192, 8191]; sort keys hold it plus 8192, so that the
+// quanta of negative depths (which the reference sorts first) come first.
+constexpr int kDepthKeyBias = 8192;
+constexpr int kDepthKeyBits = 14;
+constexpr int kDepthBinEmpty = 1 << kDepthKeyBits;  // Gaussians with no tile
+__host__ __device__ inline uint32_t depth_key(uint32_t depth_bits) {
+  return (uint32_t)(((int32_t)depth_bits >> (31 - kDepthBits)) + kDepthKeyBias);
+}
 
 // exp(x) in float32 from Cody-Waite reduction x = k*ln2 + r (|r| <= ln2/2, ln2 split
 // into a head with 11 trailing zero bits and a tail) and the degree-7 Taylor

@@ -19,7 +19,7 @@ GS_REC_STRIDE = 12
 GS_NUM_STATS = 16
 STAT = dict(n_interactions=0, max_interactions_per_tile=1, overflow_tiles=2, overflow_interactions=3,
             truncated_tiles=4, truncated_interactions=5, radius_cap_violations=6, negative_depth=7,
-            capacity_exceeded=8, mean_per_tile=9)
+            capacity_exceeded=8, mean_per_tile=9, tile_entries=10)
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -37,6 +37,8 @@ _SIGS = {
     "gs_bin_workspace_size": [_I64, _I, _I, _I64],
     "gs_bin": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _SZ, _P, _P, _P, _P],
     "gs_bin_static": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _P, _P, _P],
+    "gs_bin_reference_workspace_size": [_I64, _I, _I],
+    "gs_bin_reference": [_P, _I64, _P, _P, _P, _P, _I, _I, _P, _SZ, _P, _P, _P, _P],
     "gs_tile_ranges": [_P, _P, _I64, _I, _P],
     "gs_composite_fwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _I],
     "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I],
@@ -62,6 +64,7 @@ _SIGS = {
     "gs_densify_accumulate": [_P, _I64, _P, _P, _P, _F, _F, _P, _P, _P, _P, _P, _P],
 }
 _RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_l1_ssim_workspace_size": _SZ,
+            "gs_bin_reference_workspace_size": _SZ,
             "gs_densify_workspace_size": _SZ}
 
 _lib = None

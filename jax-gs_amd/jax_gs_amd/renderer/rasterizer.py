@@ -67,23 +67,31 @@ def bin_gaussians(means2d: torch.Tensor, radii: torch.Tensor, valid: torch.Tenso
 
 
 def get_tile_interactions(means2D, radii, valid_mask, depths, H, W, tile_size: int = TILE_SIZE):
-    """rasterizer.py:12-116 -> (sorted_tile_ids, sorted_gaussian_ids, n_interactions).
-
-    The first n_interactions entries equal the reference's valid entries in the
-    reference's order (tile, 13-bit depth bucket, Gaussian id).  Positions >= n hold
-    tile T and id 0.  Difference: the reference keeps 256 slots of every Gaussian
-    whose depth has its sign bit set in front of that list (tile -1), and the ids of
-    invalid slots in its tail; no consumer of the arrays reads either."""
+    """rasterizer.py:12-116 -> (sorted_tile_ids [L], sorted_gaussian_ids [L], n_interactions),
+    L = max(256 N, 512): the reference's own arrays, slot for slot -- the 256 slots of each
+    Gaussian whose depth has its sign bit set (tile -1), the entries in (tile, depth
+    quantum, id) order, the other Gaussians' empty slots (tile T), padding (tile T, id 0)."""
     if tile_size != TILE_SIZE:
         raise ValueError("only 16x16 tiles are supported (rasterizer.py:6)")
-    r = bin_gaussians(means2D, torch.as_tensor(radii, device=means2D.device), valid_mask, depths, H, W)
-    n = r["n_interactions"]
+    dev = means2D.device
+    n = means2D.shape[0]
+    if 256 * n >= 2 ** 31:
+        raise ValueError(f"get_tile_interactions: 256 * {n} slots exceed int32 indexing")
+    m2 = check_f32("means2D", means2D, (n, 2), dev)
+    r = check_f32("radii", torch.as_tensor(radii, device=dev).to(torch.float32), (n,), dev)
+    z = check_f32("depths", depths, (n,), dev)
+    v = torch.as_tensor(valid_mask, device=dev).to(torch.uint8).contiguous()
+    L = max(256 * n, BLOCK_SIZE)
     _, _, T = num_tiles(W, H)
-    idx = torch.arange(r["capacity"], device=means2D.device, dtype=torch.int32)
-    tail = idx >= n
-    tiles = torch.where(tail, torch.full_like(r["sorted_tiles"], T), r["sorted_tiles"])
-    gids = torch.where(tail, torch.zeros_like(r["sorted_gids"]), r["sorted_gids"])
-    return tiles, gids, n
+    nb = _lib.lib().gs_bin_reference_workspace_size(n, int(W), int(H))
+    ws = torch.empty((nb,), dtype=torch.uint8, device=dev)
+    tiles = torch.empty((L,), dtype=torch.int32, device=dev)
+    gids = torch.empty((L,), dtype=torch.int32, device=dev)
+    ranges = torch.empty((T + 1,), dtype=torch.int32, device=dev)
+    stats = torch.empty((_lib.GS_NUM_STATS,), dtype=torch.int32, device=dev)
+    _lib.call("gs_bin_reference", _lib.stream_handle(dev), n, _lib.ptr(m2), _lib.ptr(r), _lib.ptr(v), _lib.ptr(z),
+              int(W), int(H), _lib.ptr(ws), nb, _lib.ptr(tiles), _lib.ptr(gids), _lib.ptr(ranges), _lib.ptr(stats))
+    return tiles, gids, stats[_lib.STAT["n_interactions"]]
 
 
 def tile_ranges(sorted_tile_ids: torch.Tensor, num_tiles_total: int) -> torch.Tensor:

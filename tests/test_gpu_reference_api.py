@@ -60,8 +60,14 @@ def test_ka2_tile_interactions(cuda):
     np.testing.assert_array_equal(st[:5], [0, 0, 1, 2, 3])
     np.testing.assert_array_equal(sg[:5], [0, 1, 0, 0, 0])
     assert np.all(st[5:] == 4)
+    # the empty slots in the reference's order: g0's 252 (depth 5) before g1's 255 (depth 10)
+    np.testing.assert_array_equal(sg[5:], [0] * 252 + [1] * 255)
     b = rasterizer.tile_ranges(_t(st, cuda, torch.int32), 4)
     np.testing.assert_array_equal(np_(b), [0, 2, 3, 4, 5])
+    st_o, sg_o, n_o = oracle.tile_interactions(np.array([[16, 16], [0, 0]], F32), np.array([4, 2], F32),
+                                               np.array([True, True]), np.array([5.0, 10.0], F32), 32, 32)
+    np.testing.assert_array_equal(st, st_o)
+    np.testing.assert_array_equal(sg, sg_o)
 
 
 def test_ka3_full_render_and_capped_alpha(cuda):
@@ -161,3 +167,57 @@ def test_reference_layout_arrays_through_drop_ins(cuda, n_behind):
     img_o, _, _ = oracle.render_tiles(pre["means2d"], pre["cov2d"], p["opacities"], pre["colors"], st, sg, H, W)
     assert np.abs(np_(rasterizer.render_tiles(*dev, H, W)) - img_o).max() <= IMG_TOL
     assert np.abs(np_(rasterizer.render_tiles_tpu(*dev, H, W)) - img_o).max() <= IMG_TOL
+
+
+def _reference_arrays_case(cuda, means2d, radii, valid, depths, H, W):
+    st, sg, n = rasterizer.get_tile_interactions(_t(means2d, cuda), _t(radii, cuda), _t(valid, cuda, torch.bool),
+                                                 _t(depths, cuda), H, W)
+    st_o, sg_o, n_o = oracle.tile_interactions(means2d, radii, valid, depths, H, W)
+    assert int(n) == n_o
+    np.testing.assert_array_equal(np_(st), st_o)
+    np.testing.assert_array_equal(np_(sg), sg_o)
+    T = ((W + 15) // 16) * ((H + 15) // 16)
+    np.testing.assert_array_equal(np_(rasterizer.tile_ranges(st, T)), oracle.tile_boundaries(st_o, T))
+    return st_o, n_o
+
+
+@pytest.mark.parametrize("n,seed", [(1, 0), (2, 1), (3, 2), (57, 3), (3000, 4)])
+def test_get_tile_interactions_reference_arrays(cuda, n, seed):
+    """rasterizer.py:12-116 slot for slot on arbitrary inputs: negative depths (their 256
+    slots first, tile -1), -0.0, depths below the 0.01 near plane that the caller marks
+    valid, valid Gaussians behind the camera (counted in n, sorted with tile -1), radii past
+    the 16-tile cap, boxes off the image, equal depth quanta (ties by id), and the padding
+    to 512 slots for n <= 1."""
+    rng = np.random.default_rng(seed)
+    W, H = 200, 150
+    means2d = rng.uniform(-60, 260, (n, 2)).astype(F32)
+    radii = np.ceil(rng.uniform(0, 70, n)).astype(F32)
+    radii[rng.uniform(size=n) < 0.05] = 400.0
+    valid = rng.uniform(size=n) < 0.8
+    depths = rng.uniform(0.02, 20, n).astype(F32)
+    k = rng.uniform(size=n)
+    depths[k < 0.1] = -rng.uniform(0.01, 5, int((k < 0.1).sum())).astype(F32)
+    depths[(k >= 0.1) & (k < 0.13)] = np.float32(-0.0)
+    depths[(k >= 0.13) & (k < 0.16)] = rng.uniform(0, 0.01, int(((k >= 0.13) & (k < 0.16)).sum())).astype(F32)
+    if n > 4:
+        depths[1] = depths[3]
+        valid[1] = valid[3] = True
+    st_o, n_o = _reference_arrays_case(cuda, means2d, radii, valid, depths, H, W)
+    if n >= 57:
+        assert (st_o == -1).sum() > 0 and n_o > 0
+
+
+def test_get_tile_interactions_reference_arrays_cfg1(cuda):
+    """The configuration-1 scene (200k Gaussians, 51.2M slots) with a fifth of it moved
+    behind the camera: the projection's outputs through get_tile_interactions."""
+    from jax_gs_amd import scenes
+
+    sc = scenes.make_scene(1)
+    p = sc["params"]
+    p["means"][::5, 2] = -p["means"][::5, 2]
+    c = sc["cam"]
+    pre = oracle.preprocess(p["means"], p["scales"], p["quaternions"], p["sh_coeffs"], c["W2C"], c["W"], c["H"],
+                            F32(c["fx"]), F32(c["fy"]), F32(c["cx"]), F32(c["cy"]), sc["sh_degree"])
+    st_o, n_o = _reference_arrays_case(cuda, pre["means2d"], pre["radii"], pre["valid"], pre["depths"], c["H"],
+                                       c["W"])
+    assert (st_o == -1).sum() == 256 * len(range(0, p["means"].shape[0], 5))
