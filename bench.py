@@ -103,11 +103,11 @@ def main():
             pre = preprocess(g, cam, mask=mask, sh_degree=D, projected=False)
             mark("t1")
             b = rasterizer.bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W,
-                                         want_tiles=False)
+                                         want_tiles=False, window=True)
             mark("t2")
             grec = torch.empty((N, _lib.GS_REC_STRIDE), device=dev)  # cleared by the forward launch
             image, fT, nc, order = rasterizer.composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg,
-                                                        clear_records=grec)
+                                                        clear_records=grec, window=b["window"])
             mark("t3")
             loss = torch.empty((), device=dev)
             gimg = torch.empty_like(image)
@@ -115,7 +115,7 @@ def main():
             mark("t4")
             _lib.call("gs_composite_bwd", s_, N, _lib.ptr(pre["records"]), _lib.ptr(b["sorted_gids"]),
                       b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), W, H, _lib.ptr(bg), _lib.ptr(gimg), _lib.ptr(fT), _lib.ptr(nc),
-                      _lib.ptr(order), _lib.ptr(grec), None, 1)
+                      _lib.ptr(order), _lib.ptr(grec), None, 1, _lib.ptr(b["window"]))
             mark("t5")
             outs = [torch.empty_like(getattr(g, f)) for f in fields]
             _lib.call("gs_preprocess_bwd", s_, N, g.sh_coeffs.shape[1], D, *[_lib.ptr(getattr(g, f).detach())

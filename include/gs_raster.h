@@ -63,13 +63,18 @@ extern "C" {
 #define GS_STAT_MEAN_PER_TILE 9     /* float32 bits of float(n_interactions) / num_tiles */
 #define GS_STAT_TILE_ENTRIES 10     /* entries of tiles 0..T-1 (= ranges[T]); n_interactions also
                                        counts valid slots of negative-depth Gaussians (tile -1) */
+#define GS_STAT_WINDOW_CLAMPED 11   /* 1 when a tile's 512-entry chunk starts within 512 slots of the
+                                       end of the reference's max(256 n, 512)-slot arrays, i.e. when
+                                       its default path (rasterizer.py:184-190) reads other entries */
 #define GS_NUM_STATS 16
 
 const char* gs_last_error(void);
 /* 2: gs_composite_fwd/bwd take the tile order; gs_mse_loss, gs_l1_ssim, gs_adam_step,
  * gs_densify_and_prune, gs_reset_opacities, gs_ply_pack/unpack, gs_preprocess_bwd_adam,
  * gs_l1_ssim_terms.  3: gs_l1_loss_bwd, gs_mse_loss_bwd.  4: gs_composite_fwd takes
- * clear_records, gs_composite_bwd accumulate.  5: gs_composite_fwd takes window_rule. */
+ * clear_records, gs_composite_bwd accumulate.  5: gs_composite_fwd takes window_rule.
+ * 6: gs_composite_fwd/bwd take a gs_window_t in place of window_rule; gs_window_from_list,
+ * gs_window_from_bins; GS_STAT_WINDOW_CLAMPED. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -154,6 +159,34 @@ int gs_bin_reference(void* stream, int64_t n, const float* means2d, const float*
 int gs_tile_ranges(void* stream, const int32_t* sorted_tiles, int64_t length, int num_tiles,
                    int32_t* ranges);
 
+/* The 512 ids a clamped chunk of the reference's default compositing path reads.
+ * rasterizer.py:184-190 slices chunk c of tile t at min(start + 512 c, L - 512) of its
+ * L-slot arrays, L = max(256 n, 512) (get_tile_interactions, rasterizer.py:84-114); a
+ * chunk starting past L - 512 reads the arrays' last 512 slots, which may hold other
+ * tiles' entries, the empty slots of the Gaussians (tile T, in (depth quantum, id) order)
+ * or the slots of negative-depth Gaussians.  thr is L - 512 in the coordinates of the
+ * entry list the compositing launch is given; ids are the arrays' slots L-512..L-1. */
+typedef struct {
+  int64_t thr;
+  int32_t reserved[2];
+  int32_t ids[512];
+} gs_window_t;
+
+/* Window of a caller list in the reference's layout (sorted_gids of L = n_entries
+ * slots, e.g. from get_tile_interactions or gs_bin_reference): thr = L - 512 and the last
+ * 512 ids (L < 512, which the reference cannot slice: thr = INT64_MAX, no clamp).
+ * Replaces the clip of rasterizer.py:187 for gs_composite_fwd/bwd. */
+int gs_window_from_list(void* stream, const int32_t* sorted_gids, int64_t n_entries, gs_window_t* window);
+
+/* Window of gs_bin's compact list, from the same inputs and the stats of the same gs_bin
+ * call: thr = L - 512 - 256 (negative-depth Gaussians); when GS_STAT_WINDOW_CLAMPED is
+ * set, ids = slots L-512..L-1 of the reference's arrays rebuilt from the inputs (one
+ * workgroup; otherwise no chunk reads them and only thr is written).  sorted_gids holds
+ * capacity ids, as given to gs_bin. */
+int gs_window_from_bins(void* stream, int64_t n, const float* means2d, const float* radii, const uint8_t* valid,
+                        const float* depths, int width, int height, const int32_t* sorted_gids, int64_t capacity,
+                        const int32_t* stats, gs_window_t* window);
+
 /* Front-to-back compositing of every 16x16 tile.
  * Replaces jax_gs/renderer/rasterizer.py:157-248 (render_tiles body; its equivalent
  * jax_gs/renderer/rasterizer_tpu.py:13-135).  sorted_gids has n_entries elements and
@@ -165,18 +198,18 @@ int gs_tile_ranges(void* stream, const int32_t* sorted_tiles, int64_t length, in
  * clear_records (may be NULL): an [n, GS_REC_STRIDE] array the launch sets to zero on
  * the side (its waves are arithmetic-bound, so the stores cost nothing), for a later
  * gs_composite_bwd with accumulate = 1.
- * window_rule selects which ids entry k = 512 c + i of a tile reads:
- *   0  its own entries, sorted_gids[ranges[t] + k] (rasterizer_tpu.py:90-97, and
- *      rasterizer.py:184-190 whenever no chunk starts within 512 entries of the end);
- *   1  the default path's chunk windows (rasterizer.py:184-190): sorted_gids[s + i] with
- *      s = min(ranges[t] + 512 c, n_entries - 512), which for a chunk near the end of
- *      the array reads the array's last 512 entries (n_entries >= 512; shorter arrays,
- *      which the reference cannot slice, read as 0).
- * gs_composite_bwd replays rule 0. */
+ * window (may be NULL) selects which ids entry k = 512 c + i of a tile reads:
+ *   NULL  its own entries, sorted_gids[ranges[t] + k] (rasterizer_tpu.py:90-97);
+ *   else  a gs_window_t in device memory, built by gs_window_from_list or
+ *         gs_window_from_bins: the chunk reads window->ids[i] when its start
+ *         ranges[t] + 512 c exceeds window->thr, else its own entries -- the default
+ *         path's chunk windows (rasterizer.py:184-190), which slice 512 ids at
+ *         min(start, L - 512) of the reference's L-slot arrays.
+ * gs_composite_bwd takes the same window. */
 int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                      int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
                      float* image, float* final_T, int32_t* n_contrib, int32_t* tile_order, float* clear_records,
-                     int window_rule);
+                     const gs_window_t* window);
 
 /* Vector-Jacobian product of gs_composite_fwd (JAX autodiff of render_tiles).
  * tile_order is the forward's (NULL: a fixed order; results agree up to the order of
@@ -184,11 +217,12 @@ int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_
  * record (layout above): overwritten when accumulate = 0, added to what it holds when
  * accumulate = 1 (records cleared by gs_composite_fwd's clear_records, or gradients of
  * several views summed in one buffer); grad_background[3] (may be NULL) is overwritten
- * with dL/d(background). */
+ * with dL/d(background).  window: the forward's (entry ids read by the same rule). */
 int gs_composite_bwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                      int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
                      const float* grad_image, const float* final_T, const int32_t* n_contrib,
-                     const int32_t* tile_order, float* grad_records, float* grad_background, int accumulate);
+                     const int32_t* tile_order, float* grad_records, float* grad_background, int accumulate,
+                     const gs_window_t* window);
 
 /* Vector-Jacobian product of gs_preprocess_fwd's compositing records with respect to
  * the five Gaussian parameter arrays (JAX autodiff of project_gaussians, eval_sh,

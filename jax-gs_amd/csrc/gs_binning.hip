@@ -735,14 +735,16 @@ __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restr
 // coalesced stores.
 __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* __restrict__ tot, int T,
                                                                const uint32_t* __restrict__ blkstat, int nblk,
-                                                               int64_t cap, int32_t* __restrict__ ranges,
+                                                               int64_t cap, int64_t n_gauss,
+                                                               int32_t* __restrict__ ranges,
                                                                int32_t* __restrict__ stats) {
   constexpr int kPer = 8, kRound = kBig * kPer;
   __shared__ uint32_t stage[kBig * (kPer + 1)];
-  __shared__ int64_t red[8][kBig / 64];
+  __shared__ int64_t red[9][kBig / 64];
   const int tid = threadIdx.x;
-  // max, ovf tiles, ovf inter, trunc tiles, trunc inter, cap, neg, negative-depth entries
-  int64_t acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  // max, ovf tiles, ovf inter, trunc tiles, trunc inter, cap, neg, negative-depth entries,
+  // last 512-entry chunk start over the tiles (-1: no entries)
+  int64_t acc[9] = {0, 0, 0, 0, 0, 0, 0, 0, -1};
   uint32_t carry = 0;
   // blkstat loads first: they are independent of the tile rounds
   uint32_t s5 = 0, s6 = 0, s7 = 0;
@@ -795,6 +797,11 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       stage[tid * (kPer + 1) + i] = pos;
+      if (w[i] > 0) {  // its last chunk: min(ceil(count / 512), 8) chunks of 512
+        const int64_t last = (int64_t)pos + (int64_t)kBlock * (((w[i] < (uint32_t)kMaxTileEntries ? w[i]
+                                                                 : (uint32_t)kMaxTileEntries) - 1) / kBlock);
+        acc[8] = acc[8] > last ? acc[8] : last;
+      }
       pos += w[i];
     }
     __syncthreads();
@@ -806,23 +813,24 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
     carry += round_total;
     __syncthreads();  // the stage is rewritten by the next round
   }
-  // reduce the 8 accumulators over the block
+  // reduce the 9 accumulators over the block (0 and 8: maxima)
   const int lane = tid & 63, wid = tid >> 6;
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
+  for (int k = 0; k < 9; ++k) {
     int64_t x = acc[k];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       const int64_t y = __shfl_xor(x, o, 64);
-      x = k == 0 ? (x > y ? x : y) : x + y;
+      x = (k == 0 || k == 8) ? (x > y ? x : y) : x + y;
     }
     if (lane == 0) red[k][wid] = x;
   }
   __syncthreads();
   if (tid == 0) {
-    int64_t r[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int64_t r[9] = {0, 0, 0, 0, 0, 0, 0, 0, -1};
     for (int w = 0; w < kBig / 64; ++w)
-      for (int k = 0; k < 8; ++k) r[k] = k == 0 ? (r[0] > red[0][w] ? r[0] : red[0][w]) : r[k] + red[k][w];
+      for (int k = 0; k < 9; ++k)
+        r[k] = (k == 0 || k == 8) ? (r[k] > red[k][w] ? r[k] : red[k][w]) : r[k] + red[k][w];
     const int64_t m = carry;
     // the reference counts the valid slots of negative-depth Gaussians too (tile -1)
     const int64_t n_int = m + r[7];
@@ -838,6 +846,10 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
     stats[GS_STAT_RADIUS_CAP_VIOLATIONS] = (int32_t)r[5];
     stats[GS_STAT_NEGATIVE_DEPTH] = (int32_t)r[6];
     stats[GS_STAT_CAPACITY_EXCEEDED] = m > cap ? 1 : 0;
+    // the reference's arrays hold max(256 n, 512) slots with 256 per negative-depth
+    // Gaussian in front of the entries: a chunk starting past L - 512 there is clamped
+    const int64_t L = 256 * n_gauss > kBlock ? 256 * n_gauss : kBlock;
+    stats[GS_STAT_WINDOW_CLAMPED] = (r[8] >= 0 && 256 * r[6] + r[8] > L - kBlock) ? 1 : 0;
     // renderer.py:81: float32(n_interactions) / num_tiles
     stats[GS_STAT_MEAN_PER_TILE] = (int32_t)float_to_bits((float)(int32_t)n_int / (float)T);
   }
@@ -1201,7 +1213,8 @@ int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, c
   GS_LAUNCH_CHECK("tile_count_kernel");
   hipLaunchKernelGGL(chunk_scan_kernel, dim3(P.S), dim3(kBig), 0, s, gbase, P.gmax, P.SX, P.TX, P.TY, gsum, tot);
   GS_LAUNCH_CHECK("chunk_scan_kernel");
-  hipLaunchKernelGGL(tile_scan_stats_kernel, dim3(1), dim3(kBig), 0, s, tot, P.T, blk, P.G_d, P.cap, ranges, stats);
+  hipLaunchKernelGGL(tile_scan_stats_kernel, dim3(1), dim3(kBig), 0, s, tot, P.T, blk, P.G_d, P.cap, n, ranges,
+                     stats);
   GS_LAUNCH_CHECK("tile_scan_stats_kernel");
 #define GS_WRITE_LAUNCH(TILES, OFF)                                                                             \
   hipLaunchKernelGGL((tile_write_kernel<TILES, OFF>), dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, desc, \
@@ -1505,5 +1518,151 @@ extern "C" int gs_bin_reference(void* stream, int64_t n, const float* means2d, c
   hipLaunchKernelGGL(ref_fill_kernel, dim3(n > 0 ? R.G : 1), dim3(kPrepBlock), 0, s, n, vals, gsum, stats,
                      R.bin.T, R.L, sorted_tiles, sorted_gids, ranges);
   GS_LAUNCH_CHECK("ref_fill_kernel");
+  return GS_OK;
+}
+
+// ---------------------------------------------------------------------------------
+// The window of gs_bin's compact list (gs_window_t): slots L-512..L-1 of the reference's
+// L = max(256 n, 512)-slot arrays, laid out as gs_bin_reference writes them (negative-depth
+// Gaussians' runs, the entries, the other Gaussians' empty slots in (dq, id) order,
+// padding).  A chunk of the default path reads them only when the binning's stats set
+// GS_STAT_WINDOW_CLAMPED, which needs fewer than 511 empty slots in all: then at most 510
+// Gaussians have any, and the window's negative-depth runs are those of the last two
+// negative-depth Gaussians in (dq, id) order.  One workgroup rebuilds them from the inputs.
+namespace gs {
+namespace {
+constexpr int kWinThreads = 1024;
+
+// the larger two of (a0 >= a1) and (b0 >= b1), keys offset by one (0: none)
+__device__ inline void top2_merge(uint64_t& a0, uint64_t& a1, uint64_t b0, uint64_t b1) {
+  const uint64_t hi = a0 > b0 ? a0 : b0, lo = a0 > b0 ? b0 : a0;
+  const uint64_t r1 = a1 > b1 ? a1 : b1;
+  a0 = hi;
+  a1 = lo > r1 ? lo : r1;
+}
+
+__global__ __launch_bounds__(kWinThreads) void window_bins_kernel(
+    int64_t n, const float* __restrict__ means2d, const float* __restrict__ radii, const uint8_t* __restrict__ valid,
+    const float* __restrict__ depths, int W, int H, const int32_t* __restrict__ gids, int64_t capacity,
+    const int32_t* __restrict__ stats, gs_window_t* __restrict__ win) {
+  __shared__ uint64_t key[kBlock];
+  __shared__ uint32_t cnt[kBlock], pre[kBlock];
+  __shared__ uint64_t top_s[2 * (kWinThreads / 64)];
+  __shared__ int n_tail;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t L = 256 * n > kBlock ? 256 * n : kBlock, lo = L - kBlock;
+  const int64_t n_neg = stats[GS_STAT_NEGATIVE_DEPTH], m = stats[GS_STAT_TILE_ENTRIES];
+  if (tid == 0) win->thr = lo - 256 * n_neg;
+  if (tid < 2) win->reserved[tid] = 0;
+  if (stats[GS_STAT_WINDOW_CLAMPED] == 0) return;  // no chunk reads the ids
+  if (tid == 0) n_tail = 0;
+  __syncthreads();
+  // Gaussians with empty slots (non-negative depth), and the top two negative-depth ones
+  uint64_t t0 = 0, t1 = 0;
+  for (int64_t i = tid; i < n; i += kWinThreads) {
+    const uint32_t zb = float_to_bits(depths[i]);
+    const uint64_t k = ((uint64_t)depth_key(zb) << 32) | (uint64_t)i;
+    if (zb >> 31) {
+      top2_merge(t0, t1, k + 1, 0);
+    } else {
+      const TileRect t = tile_rect(means2d[2 * i], means2d[2 * i + 1], radii[i], valid[i] != 0, W, H);
+      const uint32_t e = 256u - (uint32_t)t.count();
+      if (e > 0) {
+        const int at = atomicAdd(&n_tail, 1);
+        if (at < kBlock) {
+          key[at] = k;
+          cnt[at] = e;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t b0 = __shfl_xor(t0, o, 64), b1 = __shfl_xor(t1, o, 64);
+    top2_merge(t0, t1, b0, b1);
+  }
+  if (lane == 0) {
+    top_s[2 * wid] = t0;
+    top_s[2 * wid + 1] = t1;
+  }
+  __syncthreads();
+  const int nt = n_tail < kBlock ? n_tail : kBlock;
+  for (int i = tid; i < kBlock; i += kWinThreads)
+    if (i >= nt) {
+      key[i] = ~0ull;
+      cnt[i] = 0;
+    }
+  __syncthreads();
+  // bitonic sort of the (dq, id) keys, ascending
+  for (int k = 2; k <= kBlock; k <<= 1)
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (tid < kBlock) {
+        const int x = tid ^ j;
+        if (x > tid) {
+          const bool up = (tid & k) == 0;
+          if ((key[tid] > key[x]) == up) {
+            const uint64_t tk = key[tid];
+            key[tid] = key[x];
+            key[x] = tk;
+            const uint32_t tc = cnt[tid];
+            cnt[tid] = cnt[x];
+            cnt[x] = tc;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  if (tid == 0) {
+    uint32_t acc = 0;
+    for (int i = 0; i < kBlock; ++i) {
+      pre[i] = acc;
+      acc += cnt[i];
+    }
+    t0 = 0;
+    t1 = 0;
+    for (int w = 0; w < kWinThreads / 64; ++w) top2_merge(t0, t1, top_s[2 * w], top_s[2 * w + 1]);
+    top_s[0] = t0;
+    top_s[1] = t1;
+  }
+  __syncthreads();
+  if (tid < kBlock) {
+    const int64_t q = lo + tid;
+    int32_t id = 0;
+    if (q < 256 * n_neg) {
+      // rank q / 256 of the n_neg runs; the last two are top_s[1], top_s[0]
+      const int64_t d = n_neg - 1 - q / 256;
+      const uint64_t k = d == 0 ? top_s[0] : (d == 1 ? top_s[1] : 0);
+      id = k ? (int32_t)(uint32_t)(k - 1) : 0;
+    } else if (q < 256 * n_neg + m) {
+      const int64_t e = q - 256 * n_neg;
+      id = e < capacity ? gids[e] : 0;
+    } else if (q < 256 * n) {
+      const uint32_t u = (uint32_t)(q - 256 * n_neg - m);
+      int a = 0, b = nt - 1;  // last sorted Gaussian whose run starts at or before u
+      while (a < b) {
+        const int c = (a + b + 1) >> 1;
+        if (pre[c] <= u) a = c; else b = c - 1;
+      }
+      id = nt > 0 ? (int32_t)(uint32_t)key[a] : 0;
+    }
+    win->ids[tid] = id;
+  }
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" int gs_window_from_bins(void* stream, int64_t n, const float* means2d, const float* radii,
+                                   const uint8_t* valid, const float* depths, int width, int height,
+                                   const int32_t* sorted_gids, int64_t capacity, const int32_t* stats,
+                                   gs_window_t* window) {
+  GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 23), "gs_window_from_bins: n must be in [0, 2^23) (got %lld)",
+             (long long)n);
+  GS_REQUIRE(width > 0 && height > 0, "gs_window_from_bins: bad image size %dx%d", width, height);
+  GS_REQUIRE(capacity >= 0 && stats && window, "gs_window_from_bins: bad arguments");
+  GS_REQUIRE(n == 0 || (means2d && radii && valid && depths), "gs_window_from_bins: NULL inputs");
+  GS_REQUIRE(capacity == 0 || sorted_gids, "gs_window_from_bins: NULL sorted_gids");
+  hipLaunchKernelGGL(window_bins_kernel, dim3(1), dim3(kWinThreads), 0, (hipStream_t)stream, n, means2d, radii,
+                     valid, depths, width, height, sorted_gids, capacity, stats, window);
+  GS_LAUNCH_CHECK("window_bins_kernel");
   return GS_OK;
 }

@@ -227,17 +227,18 @@ struct Probe {
 };
 
 // Id of entry k of a tile whose entries start at `start` (-1 past the n entries).
-// win_hi < 0: the tile's own entries (rasterizer_tpu.py:90-97 gathers them one by one).
-// win_hi >= 0: the default path's chunk windows (rasterizer.py:184-190): chunk c = k / 512
-// reads a 512-entry slice whose start, start + 512 c, is clamped to [0, win_hi] with
-// win_hi = (array length) - 512, so a chunk that starts within 512 entries of the end
-// of the array reads the array's last 512 entries instead.
+// Without a window: the tile's own entries (rasterizer_tpu.py:90-97 gathers them one by
+// one).  With one (WIN): the default path's chunk windows (rasterizer.py:184-190): chunk
+// c = k / 512 slices 512 ids at min(start + 512 c, L - 512) of the reference's L-slot
+// arrays, so a chunk that starts past thr = L - 512 (in this list's coordinates) reads the
+// arrays' last 512 slots, held in win->ids.  The test is uniform over a batch of 64.
+template <bool WIN>
 __device__ inline int probe_gid(const int32_t* __restrict__ gids, int start, int k, int n, int num_g,
-                                int64_t win_hi = -1) {
+                                const gs_window_t* __restrict__ win, int64_t thr) {
   if (k < 0 || k >= n) return -1;
-  int64_t at = (int64_t)start + k;
-  if (win_hi >= 0 && (int64_t)start + (k & ~(kBlock - 1)) > win_hi) at = win_hi + (k & (kBlock - 1));
-  return clamp_gid(gids[at], num_g);
+  const int32_t* src = gids + ((int64_t)start + k);
+  if (WIN && (int64_t)start + (k & ~(kBlock - 1)) > thr) src = win->ids + (k & (kBlock - 1));
+  return clamp_gid(*src, num_g);
 }
 
 __device__ inline Probe probe_load(const float4* __restrict__ rec, int g) {
@@ -258,15 +259,15 @@ __device__ inline uint64_t probe_test(const Probe& p, float x0, float x1, float 
   return __ballot(p.g >= 0 && !entry_misses_rect(p.mx, p.my, p.A, p.B, p.C, x0, x1, y0, y1));
 }
 
-// WIN: the default path's chunk windows (win_hi, see probe_gid); without it the id fetch
-// compiles to the plain one.
+// WIN: the default path's chunk windows (see probe_gid); without it the id fetch compiles
+// to the plain one.
 template <int PPT, bool WIN>
 __global__ __launch_bounds__(64) void composite_fwd_kernel(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
     float* __restrict__ img, float* __restrict__ finalT, int32_t* __restrict__ ncontrib,
-    int32_t* __restrict__ tile_cost, float4* __restrict__ clear, int64_t n_clear, int64_t win_arg) {
-  const int64_t win_hi = WIN ? win_arg : -1;
+    int32_t* __restrict__ tile_cost, float4* __restrict__ clear, int64_t n_clear,
+    const gs_window_t* __restrict__ win) {
   constexpr int WPT = 4 / PPT;  // waves per tile
   // Every workgroup clears its slice of the caller's array after its own outputs (stores
   // and loads share one wait counter, so stores issued before the walk would hold up its
@@ -307,12 +308,13 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
 
   bool done = false;
   int walked = 0, next_check = 8;
-  int g_ahead = probe_gid(gids, start, 64 + lane, n, num_g, win_hi);
-  Probe p_next = probe_load(rec, probe_gid(gids, start, lane, n, num_g, win_hi));
+  const int64_t thr = WIN ? win->thr : 0;
+  int g_ahead = probe_gid<WIN>(gids, start, 64 + lane, n, num_g, win, thr);
+  Probe p_next = probe_load(rec, probe_gid<WIN>(gids, start, lane, n, num_g, win, thr));
   for (int b0 = 0; b0 < n && !done; b0 += 64) {
     const Probe pr = p_next;
     p_next = probe_load(rec, g_ahead);
-    g_ahead = probe_gid(gids, start, b0 + 128 + lane, n, num_g, win_hi);
+    g_ahead = probe_gid<WIN>(gids, start, b0 + 128 + lane, n, num_g, win, thr);
     const int gl = pr.g;
     uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
     // Survivors are walked in groups of G (G = 2 when a lane holds one pixel): the
@@ -426,12 +428,12 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
   clear_slice();
 }
 
-template <int PPT>
+template <int PPT, bool WIN>
 __device__ __forceinline__ void composite_bwd_body(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
     const float* __restrict__ gimg, const float* __restrict__ finalT, const int32_t* __restrict__ ncontrib,
-    float* __restrict__ grec, const int32_t* __restrict__ order) {
+    float* __restrict__ grec, const int32_t* __restrict__ order, const gs_window_t* __restrict__ win) {
   constexpr int WPT = 4 / PPT;
   const int b = blockIdx.x / WPT, part = blockIdx.x % WPT;
   const int tile = order ? (b < T ? order[b] : -1) : tile_of_block(b, TX, T / TX);
@@ -481,12 +483,13 @@ __device__ __forceinline__ void composite_bwd_body(
   // survivors are walked two at a time and their 9 + 9 sums reduced together (one
   // 18-value reduce-scatter costs fewer cross-lane steps than two 9-value ones)
   const int btop = (kmax - 1) & ~63;
-  int g_ahead = probe_gid(gids, start, btop - 64 + lane, kmax, num_g);
-  Probe p_next = probe_load(rec, probe_gid(gids, start, btop + lane, kmax, num_g));
+  const int64_t thr = WIN ? win->thr : 0;
+  int g_ahead = probe_gid<WIN>(gids, start, btop - 64 + lane, kmax, num_g, win, thr);
+  Probe p_next = probe_load(rec, probe_gid<WIN>(gids, start, btop + lane, kmax, num_g, win, thr));
   for (int b0 = btop; b0 >= 0; b0 -= 64) {
     const Probe pr = p_next;
     p_next = probe_load(rec, g_ahead);
-    g_ahead = probe_gid(gids, start, b0 - 128 + lane, kmax, num_g);
+    g_ahead = probe_gid<WIN>(gids, start, b0 - 128 + lane, kmax, num_g, win, thr);
     const int gl = pr.g;
     uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
     Rec nxt = zero_rec();
@@ -582,19 +585,21 @@ __device__ __forceinline__ void composite_bwd_body(
   const float4 *__restrict__ rec, int num_g, const int32_t *__restrict__ gids, int64_t n_entries,               \
       const int32_t *__restrict__ ranges, int W, int H, int TX, int T, const float *__restrict__ bg,            \
       const float *__restrict__ gimg, const float *__restrict__ finalT, const int32_t *__restrict__ ncontrib, \
-      float *__restrict__ grec, const int32_t *__restrict__ order
-#define GS_BWD_ARGS rec, num_g, gids, n_entries, ranges, W, H, TX, T, bg, gimg, finalT, ncontrib, grec, order
+      float *__restrict__ grec, const int32_t *__restrict__ order, const gs_window_t *__restrict__ win
+#define GS_BWD_ARGS rec, num_g, gids, n_entries, ranges, W, H, TX, T, bg, gimg, finalT, ncontrib, grec, order, win
 
 // The backward in two register budgets.  Capped at 64 VGPRs (8 waves per SIMD) it runs
 // best when a SIMD holds few of the launch's waves (cfg4, 3600 tiles: 250 vs 282 us);
 // scheduled for 6 waves per SIMD (68 VGPRs, so 7 are resident) it runs best when the
 // launch fills every slot (cfg2, 8160 tiles: 344 us, against 351 with no occupancy target
-// and 369 capped).  The host picks by tile count.
-template <int PPT>
+// and 369 capped).  The host picks by tile count.  WIN: the default path's chunk windows,
+// as the forward read them.
+template <int PPT, bool WIN>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void composite_bwd_kernel(GS_BWD_PARAMS) {
-  composite_bwd_body<PPT>(GS_BWD_ARGS);
+  composite_bwd_body<PPT, WIN>(GS_BWD_ARGS);
 }
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6, 6))) void composite_bwd_wide_kernel(GS_BWD_PARAMS) { composite_bwd_body<4>(GS_BWD_ARGS); }
+template <bool WIN>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6, 6))) void composite_bwd_wide_kernel(GS_BWD_PARAMS) { composite_bwd_body<4, WIN>(GS_BWD_ARGS); }
 #undef GS_BWD_PARAMS
 #undef GS_BWD_ARGS
 
@@ -699,12 +704,34 @@ constexpr int kFwdOneWaveTiles = 6 * 1024;
 
 using namespace gs;
 
+namespace gs {
+namespace {
+// thr = L - 512 and the last 512 ids of an L-slot list (no clamp for L < 512)
+__global__ __launch_bounds__(512) void window_list_kernel(const int32_t* __restrict__ gids, int64_t L,
+                                                          gs_window_t* __restrict__ win) {
+  const int i = threadIdx.x;
+  if (i == 0) win->thr = L >= kBlock ? L - kBlock : INT64_MAX;
+  if (i < 2) win->reserved[i] = 0;
+  win->ids[i] = L >= kBlock ? gids[L - kBlock + i] : 0;
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" int gs_window_from_list(void* stream, const int32_t* sorted_gids, int64_t n_entries,
+                                   gs_window_t* window) {
+  GS_REQUIRE(n_entries >= 0 && window != nullptr, "gs_window_from_list: bad arguments");
+  GS_REQUIRE(n_entries < kBlock || sorted_gids != nullptr, "gs_window_from_list: NULL sorted_gids");
+  hipLaunchKernelGGL(window_list_kernel, dim3(1), dim3(kBlock), 0, (hipStream_t)stream, sorted_gids, n_entries,
+                     window);
+  GS_LAUNCH_CHECK("window_list_kernel");
+  return GS_OK;
+}
+
 extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                                 int64_t n_entries, const int32_t* ranges, int width, int height,
                                 const float* background, float* image, float* final_T, int32_t* n_contrib,
-                                int32_t* tile_order, float* clear_records, int window_rule) {
+                                int32_t* tile_order, float* clear_records, const gs_window_t* window) {
   GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "gs_composite_fwd: n out of range");
-  GS_REQUIRE(window_rule == 0 || window_rule == 1, "gs_composite_fwd: window_rule must be 0 or 1");
   GS_REQUIRE(n_entries >= 0, "gs_composite_fwd: n_entries must be >= 0");
   GS_REQUIRE(width > 0 && height > 0, "gs_composite_fwd: bad image size %dx%d", width, height);
   GS_REQUIRE(ranges && background && image, "gs_composite_fwd: NULL argument");
@@ -716,13 +743,11 @@ extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, c
   GS_REQUIRE(clear_records == nullptr || ((uintptr_t)clear_records & 15) == 0,
              "gs_composite_fwd: clear_records must be 16-byte aligned");
   const int64_t n4_clear = clear_records ? n * kRec / 4 : 0;  // kRec = 12: whole float4s
-  // the reference slices 512 entries per chunk, which needs an array of at least 512
-  const int64_t win_hi = (window_rule == 1 && n_entries >= kBlock) ? n_entries - kBlock : -1;
 #define GS_FWD_LAUNCH(PPT, WPT, WIN)                                                                          \
   hipLaunchKernelGGL((composite_fwd_kernel<PPT, WIN>), dim3(nblk * (WPT)), dim3(64), 0, s, (const float4*)records, \
                      (int)n, sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T,       \
-                     n_contrib, tile_order, (float4*)clear_records, n4_clear, win_hi)
-  const bool win = win_hi >= 0;
+                     n_contrib, tile_order, (float4*)clear_records, n4_clear, window)
+  const bool win = window != nullptr;
   if (pick_ppt(T) == 4 && T >= kFwdOneWaveTiles) {
     if (win) GS_FWD_LAUNCH(4, 1, true); else GS_FWD_LAUNCH(4, 1, false);
   } else if (pick_ppt(T) == 4) {
@@ -743,7 +768,7 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
                                 int64_t n_entries, const int32_t* ranges, int width, int height,
                                 const float* background, const float* grad_image, const float* final_T,
                                 const int32_t* n_contrib, const int32_t* tile_order, float* grad_records,
-                                float* grad_background, int accumulate) {
+                                float* grad_background, int accumulate, const gs_window_t* window) {
   GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "gs_composite_bwd: n out of range");
   GS_REQUIRE(n_entries >= 0, "gs_composite_bwd: n_entries must be >= 0");
   GS_REQUIRE(width > 0 && height > 0, "gs_composite_bwd: bad image size %dx%d", width, height);
@@ -766,19 +791,19 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
   const int TX = (width + kTile - 1) / kTile, TY = (height + kTile - 1) / kTile;
   const int T = TX * TY;
   const int nblk = tile_blocks(TX, TY);
+#define GS_BWD_LAUNCH(KERNEL, WPT)                                                                                  \
+  hipLaunchKernelGGL(KERNEL, dim3(nblk * (WPT)), dim3(64), 0, s, (const float4*)records, (int)n, sorted_gids, n_entries, \
+                     ranges, width, height, TX, T, background, grad_image, final_T, n_contrib, grad_records,           \
+                     tile_order, window)
+  const bool win = window != nullptr;
   if (pick_ppt(T) == 4 && T >= kBwdWideTiles) {
-    hipLaunchKernelGGL(composite_bwd_wide_kernel, dim3(nblk), dim3(64), 0, s, (const float4*)records, (int)n,
-                       sorted_gids, n_entries, ranges, width, height, TX, T, background, grad_image, final_T,
-                       n_contrib, grad_records, tile_order);
+    if (win) GS_BWD_LAUNCH(composite_bwd_wide_kernel<true>, 1); else GS_BWD_LAUNCH(composite_bwd_wide_kernel<false>, 1);
   } else if (pick_ppt(T) == 4) {
-    hipLaunchKernelGGL(composite_bwd_kernel<4>, dim3(nblk), dim3(64), 0, s, (const float4*)records, (int)n,
-                       sorted_gids, n_entries, ranges, width, height, TX, T, background, grad_image, final_T,
-                       n_contrib, grad_records, tile_order);
+    if (win) GS_BWD_LAUNCH((composite_bwd_kernel<4, true>), 1); else GS_BWD_LAUNCH((composite_bwd_kernel<4, false>), 1);
   } else {
-    hipLaunchKernelGGL(composite_bwd_kernel<1>, dim3(nblk * 4), dim3(64), 0, s, (const float4*)records, (int)n,
-                       sorted_gids, n_entries, ranges, width, height, TX, T, background, grad_image, final_T,
-                       n_contrib, grad_records, tile_order);
+    if (win) GS_BWD_LAUNCH((composite_bwd_kernel<1, true>), 4); else GS_BWD_LAUNCH((composite_bwd_kernel<1, false>), 4);
   }
+#undef GS_BWD_LAUNCH
   GS_LAUNCH_CHECK("composite_bwd_kernel");
   return GS_OK;
 }

@@ -17,9 +17,10 @@ LIBPATH = os.path.join(_HERE, "libgsraster.so")
 GS_OK = 0
 GS_REC_STRIDE = 12
 GS_NUM_STATS = 16
+GS_WINDOW_BYTES = 16 + 4 * 512  # sizeof(gs_window_t): int64 thr, 2 reserved int32, 512 ids
 STAT = dict(n_interactions=0, max_interactions_per_tile=1, overflow_tiles=2, overflow_interactions=3,
             truncated_tiles=4, truncated_interactions=5, radius_cap_violations=6, negative_depth=7,
-            capacity_exceeded=8, mean_per_tile=9, tile_entries=10)
+            capacity_exceeded=8, mean_per_tile=9, tile_entries=10, window_clamped=11)
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -40,8 +41,10 @@ _SIGS = {
     "gs_bin_reference_workspace_size": [_I64, _I, _I],
     "gs_bin_reference": [_P, _I64, _P, _P, _P, _P, _I, _I, _P, _SZ, _P, _P, _P, _P],
     "gs_tile_ranges": [_P, _P, _I64, _I, _P],
-    "gs_composite_fwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _I],
-    "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I],
+    "gs_window_from_list": [_P, _P, _I64, _P],
+    "gs_window_from_bins": [_P, _I64, _P, _P, _P, _P, _I, _I, _P, _I64, _P, _P],
+    "gs_composite_fwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P],
+    "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P],
     "gs_preprocess_bwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P, _P],
     "gs_l1_loss": [_P, _I64, _P, _P, _P, _P],
     "gs_mse_loss": [_P, _I64, _P, _P, _P, _P],
@@ -70,7 +73,7 @@ _RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_
 _lib = None
 
 
-ABI_VERSION = 5  # gs_abi_version() of the signatures bound below
+ABI_VERSION = 6  # gs_abi_version() of the signatures bound below
 
 
 class NativeLibraryMissing(RuntimeError):

@@ -40,11 +40,29 @@ class BinResult(dict):
 
     sorted_gids / sorted_tiles: [capacity] int32, the first n entries valid;
     ranges: [T+1] int32 (searchsorted-left boundaries); stats: [16] int32;
-    n_interactions: 0-d int32 view of stats."""
+    n_interactions: 0-d int32 view of stats; window: the default path's chunk window
+    (gs_window_t bytes) when asked for, else None."""
+
+
+def new_window(dev) -> torch.Tensor:
+    """Device storage for one gs_window_t (8-byte aligned: torch allocations are)."""
+    return torch.empty((_lib.GS_WINDOW_BYTES,), dtype=torch.uint8, device=dev)
+
+
+def window_from_list(sorted_gids: torch.Tensor) -> torch.Tensor:
+    """The clamped chunk window of a list in the reference's layout (rasterizer.py:187):
+    thr = len - 512 and its last 512 ids."""
+    g = sorted_gids.to(torch.int32).contiguous()
+    win = new_window(g.device)
+    _lib.call("gs_window_from_list", _lib.stream_handle(g.device), _lib.ptr(g), g.shape[0], _lib.ptr(win))
+    return win
 
 
 def bin_gaussians(means2d: torch.Tensor, radii: torch.Tensor, valid: torch.Tensor, depths: torch.Tensor, H: int,
-                  W: int, capacity: int | None = None, want_tiles: bool = True) -> BinResult:
+                  W: int, capacity: int | None = None, want_tiles: bool = True, window: bool = False) -> BinResult:
+    """gs_bin: the entries in the reference's (tile, depth quantum, id) order, compact.
+    window=True also builds the default path's chunk window of that list (the reference's
+    rasterizer.py:184-190 clamp, gs_window_from_bins)."""
     dev = means2d.device
     n = means2d.shape[0]
     means2d = check_f32("means2D", means2d, (n, 2), dev)
@@ -62,8 +80,13 @@ def bin_gaussians(means2d: torch.Tensor, radii: torch.Tensor, valid: torch.Tenso
     _lib.call("gs_bin", _lib.stream_handle(dev), n, _lib.ptr(means2d), _lib.ptr(radii), _lib.ptr(v), _lib.ptr(depths),
               int(W), int(H), cap, _lib.ptr(ws), ws_bytes, _lib.ptr(gids), _lib.ptr(tiles), _lib.ptr(ranges),
               _lib.ptr(stats))
+    win = None
+    if window:
+        win = new_window(dev)
+        _lib.call("gs_window_from_bins", _lib.stream_handle(dev), n, _lib.ptr(means2d), _lib.ptr(radii), _lib.ptr(v),
+                  _lib.ptr(depths), int(W), int(H), _lib.ptr(gids), cap, _lib.ptr(stats), _lib.ptr(win))
     return BinResult(sorted_gids=gids, sorted_tiles=tiles, ranges=ranges, stats=stats,
-                     n_interactions=stats[_lib.STAT["n_interactions"]], capacity=cap, num_tiles=T)
+                     n_interactions=stats[_lib.STAT["n_interactions"]], capacity=cap, num_tiles=T, window=win)
 
 
 def get_tile_interactions(means2D, radii, valid_mask, depths, H, W, tile_size: int = TILE_SIZE):
@@ -119,15 +142,16 @@ def composite_records(means2D, cov2D, opacities, colors) -> torch.Tensor:
 
 def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Tensor, H: int, W: int,
               background: torch.Tensor, residuals: bool = True, clear_records: torch.Tensor | None = None,
-              window_rule: int = 0):
+              window: torch.Tensor | None = None):
     """Front-to-back compositing; returns (image [H,W,3], final_T [H,W], n_contrib [H,W],
     tile_order [T]), the last three the backward's residuals (None unless residuals):
     tile_order lists the tiles longest walk first, the backward's launch order.
     clear_records ([n, GS_REC_STRIDE] float32), when given, is set to zero by the same launch
-    (for a backward that accumulates into it).  window_rule 0 reads each tile's own
-    entries (rasterizer_tpu.py:90-97), 1 the default path's clamped 512-entry chunk
-    windows (rasterizer.py:184-190), which differ only for chunks that start within 512
-    entries of the end of sorted_gids."""
+    (for a backward that accumulates into it).  window None reads each tile's own entries
+    (rasterizer_tpu.py:90-97); a window (window_from_list, bin_gaussians(window=True))
+    reads the default path's clamped 512-entry chunk windows (rasterizer.py:184-190),
+    which differ only for chunks that start within 512 slots of the end of the
+    reference's arrays."""
     dev = records.device
     _, _, T = num_tiles(W, H)
     image = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
@@ -136,19 +160,20 @@ def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Te
     order = torch.empty((T,), dtype=torch.int32, device=dev) if residuals else None
     _lib.call("gs_composite_fwd", _lib.stream_handle(dev), records.shape[0], _lib.ptr(records),
               _lib.ptr(sorted_gids), sorted_gids.shape[0], _lib.ptr(ranges), int(W), int(H), _lib.ptr(background), _lib.ptr(image),
-              _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(clear_records), int(window_rule))
+              _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(clear_records), _lib.ptr(window))
     return image, fT, nc, order
 
 
 def _render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W, background,
-                  window_rule):
+                  clamped_windows):
     dev = means2D.device
     _, _, T = num_tiles(W, H)
     rec = composite_records(means2D, cov2D, opacities, colors)
     ranges = tile_ranges(sorted_tile_ids, T)
     bg = background_tensor(background, dev)
-    image, _, _, _ = composite(rec, sorted_gaussian_ids.to(torch.int32).contiguous(), ranges, H, W, bg,
-                               residuals=False, window_rule=window_rule)
+    gids = sorted_gaussian_ids.to(torch.int32).contiguous()
+    win = window_from_list(gids) if clamped_windows else None
+    image, _, _, _ = composite(rec, gids, ranges, H, W, bg, residuals=False, window=win)
     return image
 
 
@@ -161,11 +186,11 @@ def render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaus
     if tile_size != TILE_SIZE:
         raise ValueError("only 16x16 tiles are supported (rasterizer.py:6)")
     return _render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W, background,
-                         window_rule=1)
+                         clamped_windows=True)
 
 
 def render_tiles_tpu(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W, background=None):
     """rasterizer_tpu.py:13-135 (forward): the same compositing with every entry of a
     tile gathered one by one (its own entries, whatever its position in the arrays)."""
     return _render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W, background,
-                         window_rule=0)
+                         clamped_windows=False)

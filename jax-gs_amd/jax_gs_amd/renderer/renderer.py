@@ -10,12 +10,13 @@ and the backward's tile order as residuals; its backward runs the compositing VJ
 returns cotangents of the five Gaussian arrays (equal to JAX autodiff of the
 reference forward, with its tie conventions) and of the background.  W2C gets no
 gradient (the reference's trainer never differentiates it) and mask gets None.
-``fast_tpu_rasterizer`` is accepted for signature parity: there is a single
-implementation, which reads each tile's own entries (rasterizer_tpu.py:90-97).  The
-reference's default path slices 512-entry chunk windows clamped to the end of its 256*N
-slot arrays (rasterizer.py:184-190), which reads other entries only when the sentinel
-tail of those arrays is shorter than 512 slots (two Gaussians, or every Gaussian covering
-nearly 16x16 tiles); ``rasterizer.render_tiles`` reproduces that rule on caller arrays.
+``fast_tpu_rasterizer`` selects the reference's compositing path: True reads each tile's
+own entries (rasterizer_tpu.py:90-97); False (the default) slices 512-entry chunk windows
+clamped to the end of the reference's max(256*N, 512)-slot arrays (rasterizer.py:184-190),
+which reads other slots when a chunk starts within 512 slots of that end (one or two
+Gaussians, or every Gaussian covering nearly 16x16 tiles).  Both run the same kernels: the
+binning writes the clamped window (gs_window_from_bins) and the compositing kernels read
+it for the chunks past its threshold.
 """
 from __future__ import annotations
 
@@ -32,25 +33,26 @@ from .rasterizer import bin_gaussians, check_capacity, composite
 class _Render(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means, scales, quats, opac, sh, w2c, bg, mask, static):
-        W, H, fx, fy, cx, cy, sh_degree, capacity = static
+        W, H, fx, fy, cx, cy, sh_degree, capacity, tpu = static
         g = Gaussians(means, scales, quats, opac, sh)
         cam = Camera(W, H, fx, fy, cx, cy, w2c, None)
         pre = preprocess(g, cam, mask=mask, sh_degree=sh_degree, records=True, projected=False)
         b = bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W, capacity=capacity,
-                          want_tiles=False)
+                          want_tiles=False, window=not tpu)
         # the gradient records the backward accumulates into, cleared by the forward's
         # compositing launch (its waves are arithmetic-bound: the stores are free)
         n = means.shape[0]
         grec = (torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=means.device)
                 if any(ctx.needs_input_grad[:5]) else None)
+        win = b["window"]
         image, fT, nc, order = composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg, residuals=True,
-                                         clear_records=grec)
+                                         clear_records=grec, window=win)
         ctx.static = static
         ctx.grec_fresh = grec is not None
         # radii, valid and stats carry no gradient: no zero cotangents for them
         ctx.set_materialize_grads(False)
         ctx.save_for_backward(means, scales, quats, opac, sh, w2c, bg, pre["records"], b["sorted_gids"], b["ranges"],
-                              fT, nc, order, grec)
+                              fT, nc, order, grec, win)
         radii = pre["radii"]
         valid = pre["valid"].view(torch.bool)  # the kernel writes 0/1 bytes
         stats = b["stats"]
@@ -59,10 +61,10 @@ class _Render(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g_image, _g_radii, _g_valid, _g_stats):
-        W, H, fx, fy, cx, cy, sh_degree, _ = ctx.static
+        W, H, fx, fy, cx, cy, sh_degree, _, _ = ctx.static
         if g_image is None:
             return None, None, None, None, None, None, None, None, None
-        means, scales, quats, opac, sh, w2c, bg, rec, gids, ranges, fT, nc, order, grec = ctx.saved_tensors
+        means, scales, quats, opac, sh, w2c, bg, rec, gids, ranges, fT, nc, order, grec, win = ctx.saved_tensors
         dev = means.device
         n = means.shape[0]
         s = _lib.stream_handle(dev)
@@ -77,7 +79,7 @@ class _Render(torch.autograd.Function):
         gbg = torch.empty((3,), dtype=torch.float32, device=dev) if ctx.needs_input_grad[6] else None
         _lib.call("gs_composite_bwd", s, n, _lib.ptr(rec), _lib.ptr(gids), gids.shape[0], _lib.ptr(ranges), int(W), int(H),
                   _lib.ptr(bg), _lib.ptr(g_image), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec),
-                  _lib.ptr(gbg), accumulate)
+                  _lib.ptr(gbg), accumulate, _lib.ptr(win))
         gm = torch.empty_like(means)
         gs_ = torch.empty_like(scales)
         gq = torch.empty_like(quats)
@@ -97,7 +99,6 @@ def render(gaussians: Gaussians, camera: Camera, background=None, fast_tpu_raste
     capacity bounds the number of (Gaussian, tile) entries; the default is the
     reference's static bound 256*N (every Gaussian may touch 16x16 tiles), limited to the
     2^31 - 1 entries int32 indices address (N >= 8,388,608)."""
-    del fast_tpu_rasterizer  # single implementation (see module docstring)
     means = gaussians.means
     dev = means.device
     n = means.shape[0]
@@ -107,7 +108,7 @@ def render(gaussians: Gaussians, camera: Camera, background=None, fast_tpu_raste
     m = as_mask(mask, n, dev)
     cap = check_capacity(capacity, n)
     static = (int(camera.W), int(camera.H), float(camera.fx), float(camera.fy), float(camera.cx), float(camera.cy),
-              int(sh_degree), cap)
+              int(sh_degree), cap, bool(fast_tpu_rasterizer))
     image, radii, valid, stats = _Render.apply(means, gaussians.scales.contiguous(),
                                                gaussians.quaternions.contiguous(), gaussians.opacities.contiguous(),
                                                gaussians.sh_coeffs.contiguous(), w2c, bg, m, static)

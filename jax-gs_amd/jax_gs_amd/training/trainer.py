@@ -70,7 +70,7 @@ def train_step(state, target_image, w2c, camera_static, optimizer, fast_tpu_rast
                     torch.as_tensor(w2c, dtype=torch.float32, device=dev), None)
     if not fused:
         return _train_step_autograd(state, target_image, camera, optimizer, fast_tpu_rasterizer, sh_degree)
-    return _train_step_fused(state, target_image, camera, optimizer, sh_degree)
+    return _train_step_fused(state, target_image, camera, optimizer, sh_degree, fast_tpu_rasterizer)
 
 
 _FIELDS = ("means", "scales", "quaternions", "opacities", "sh_coeffs")
@@ -94,7 +94,8 @@ def _train_step_autograd(state, target_image, camera, optimizer, fast_tpu_raster
     return state, total.detach(), metrics
 
 
-def _train_step_fused(state, target_image, camera, optimizer, sh_degree, lambda_ssim: float = 0.2):
+def _train_step_fused(state, target_image, camera, optimizer, sh_degree, fast_tpu_rasterizer: bool = False,
+                      lambda_ssim: float = 0.2):
     from ..renderer.rasterizer import bin_gaussians, composite
     from ..renderer.projection import preprocess
     from ..renderer._buffers import background_tensor
@@ -108,11 +109,13 @@ def _train_step_fused(state, target_image, camera, optimizer, sh_degree, lambda_
     with torch.no_grad():
         active = state.active_mask.view(torch.bool)  # 0/1 bytes
         pre = preprocess(params, camera, mask=active, sh_degree=sh_degree, records=True, projected=False)
-        b = bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W, want_tiles=False)
+        # the default rasterizer's clamped chunk windows unless fast_tpu_rasterizer
+        b = bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W, want_tiles=False,
+                          window=not fast_tpu_rasterizer)
         bg = background_tensor(None, dev)
         grec = torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=dev)  # cleared by the forward
         image, fT, nc, order = composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg, residuals=True,
-                                         clear_records=grec)
+                                         clear_records=grec, window=b["window"])
         # loss (trainer.py:18-26): one kernel for the L1 and SSIM means
         tgt = target_image.to(device=dev, dtype=torch.float32).contiguous()
         Hh, Ww, C = image.shape
@@ -129,7 +132,7 @@ def _train_step_fused(state, target_image, camera, optimizer, sh_degree, lambda_
                   _lib.ptr(gimg))
         _lib.call("gs_composite_bwd", s, n, _lib.ptr(pre["records"]), _lib.ptr(b["sorted_gids"]),
                   b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), int(W), int(H), _lib.ptr(bg), _lib.ptr(gimg),
-                  _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec), None, 1)
+                  _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec), None, 1, _lib.ptr(b["window"]))
         # preprocessing VJP + statistics + masked Adam, in place
         ost = state.opt_state
         moments = [ost.mu[f] for f in _FIELDS] + [ost.nu[f] for f in _FIELDS]
