@@ -24,9 +24,16 @@ import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
-FP32_PEAK_TFLOPS = 157.3  # MI355X FP32 (vector) peak
-COMPOSITE_FWD_FLOP_PER_PAIR = 22  # ~22 FLOP + 1 exp per evaluated (pixel, entry) pair
-COMPOSITE_BWD_FLOP_PER_PAIR = 55  # ~2.5x the forward per pair
+FP32_PEAK_TFLOPS = 157.3  # MI355X published FP32 vector peak (packed FP32 instructions)
+# The issue rate without packed FP32, which this build disables: 256 CUs x 4 SIMDs x 16
+# lanes x 2 FLOP (FMA) x 2.4 GHz.
+FP32_NONPACKED_PEAK_TFLOPS = 78.6
+# Estimates of the reference algorithm's arithmetic per (pixel, entry) pair it evaluates:
+# ~22 FLOP + 1 exp forward, ~2.5x that backward.  The kernels skip the pairs their
+# rectangle cull drops and share per-column terms between a lane's pixels, so these count
+# the reference's work, not instructions issued (VALU busy, from the SQ counters, does).
+COMPOSITE_FWD_FLOP_PER_PAIR = 22
+COMPOSITE_BWD_FLOP_PER_PAIR = 55
 PROFILES = os.path.join(_ROOT, "profiles")
 
 
@@ -275,9 +282,16 @@ def main():
                     "frac": ach / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src}
     else:
         ach = stage_tflops.get(dominant, 0.0)
+        busy, busy_src = measured_valu_busy(dominant, args.config)
         roofline = {"kernel": dominant, "bound": "valu", "achieved": ach, "peak": FP32_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": ach / FP32_PEAK_TFLOPS, "traffic": traffic,
-                    "traffic_source": traffic_src, "pairs": pairs}
+                    "traffic_source": traffic_src, "pairs": pairs,
+                    "flop_per_pair": COMPOSITE_BWD_FLOP_PER_PAIR if dominant == "composite_bwd"
+                    else COMPOSITE_FWD_FLOP_PER_PAIR,
+                    "flops": "estimate: the reference algorithm's FLOP per (pixel, entry) pair x sum of n_contrib",
+                    # what the build can issue: non-packed FP32 (packed FP32 is disabled), and the
+                    # share of SIMD cycles the kernel issues VALU work on (SQ counters)
+                    "nonpacked_peak": FP32_NONPACKED_PEAK_TFLOPS, "valu_busy": busy, "valu_busy_source": busy_src}
 
     if args.copy_calibration:
         src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
@@ -331,6 +345,22 @@ def measured_traffic(kernel, config):
         if line.startswith("| " + kernel + " |"):
             try:
                 return float(line.split("|")[-2].strip()), os.path.relpath(path, _ROOT)
+            except ValueError:
+                return None, None
+    return None, None
+
+
+def measured_valu_busy(stage, config):
+    """VALU-busy fraction of the stage's kernel from the committed SQ-counter summary of the
+    same configuration, and that file; (None, None) when there is none."""
+    kernels = {"composite_bwd": "composite_bwd_wide_kernel", "composite_fwd": "composite_fwd_kernel<4>"}
+    path = os.path.join(PROFILES, f"composite_valu_cfg{config}.md")
+    if stage not in kernels or not os.path.exists(path):
+        return None, None
+    for line in open(path):
+        if line.startswith("| " + kernels[stage] + " |"):
+            try:
+                return float(line.split("|")[-3].strip()) / 100.0, os.path.relpath(path, _ROOT)
             except ValueError:
                 return None, None
     return None, None
