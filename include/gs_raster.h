@@ -74,7 +74,8 @@ const char* gs_last_error(void);
  * gs_l1_ssim_terms.  3: gs_l1_loss_bwd, gs_mse_loss_bwd.  4: gs_composite_fwd takes
  * clear_records, gs_composite_bwd accumulate.  5: gs_composite_fwd takes window_rule.
  * 6: gs_composite_fwd/bwd take a gs_window_t in place of window_rule; gs_window_from_list,
- * gs_window_from_bins; GS_STAT_WINDOW_CLAMPED. */
+ * gs_window_from_bins; GS_STAT_WINDOW_CLAMPED.  7: gs_preprocess_bwd_w2c, gs_eval_sh,
+ * gs_eval_sh_bwd. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -235,6 +236,34 @@ int gs_preprocess_bwd(void* stream, int64_t n, int sh_k, int sh_degree, const fl
                       float fx, float fy, float cx, float cy, const float* grad_records,
                       float* grad_means, float* grad_scales, float* grad_quats,
                       float* grad_opacities, float* grad_sh);
+
+/* Workspace bytes gs_preprocess_bwd_w2c needs (16 floats per 64 Gaussians). */
+size_t gs_preprocess_bwd_w2c_workspace_size(int64_t n);
+
+/* gs_preprocess_bwd plus the camera cotangent grad_w2c[4,4] (JAX autodiff with respect to
+ * Camera.W2C: through the camera-space means and W_rot of projection.py:26-57 and the view
+ * directions of renderer.py:40-41 with camera.center = -R^T t, camera.py:15-21; row 3,
+ * which never enters, is 0).  The per-Gaussian shares are summed per wave into workspace
+ * and then in a fixed order by one workgroup. */
+int gs_preprocess_bwd_w2c(void* stream, int64_t n, int sh_k, int sh_degree, const float* means,
+                          const float* scales, const float* quats, const float* opacities,
+                          const float* sh_coeffs, const float* w2c, int width, int height,
+                          float fx, float fy, float cx, float cy, const float* grad_records,
+                          float* grad_means, float* grad_scales, float* grad_quats,
+                          float* grad_opacities, float* grad_sh, float* grad_w2c, void* workspace,
+                          size_t workspace_bytes);
+
+/* jax_gs/renderer/sh.py:25-74 eval_sh: colors[N,3] = the real SH expansion of degree
+ * sh_degree (0..3) of sh_coeffs[N,K,3] (K >= (sh_degree+1)^2) in the directions
+ * view_dirs[N,3] (used as given), in the reference's association order; no +0.5 and no
+ * clip (renderer.py:44-49 adds them). */
+int gs_eval_sh(void* stream, int64_t n, int sh_k, int sh_degree, const float* sh_coeffs,
+               const float* view_dirs, float* colors);
+
+/* Vector-Jacobian product of gs_eval_sh: grad_sh[N,K,3] (coefficients >= (sh_degree+1)^2
+ * get 0) and grad_dirs[N,3] (may be NULL), overwritten. */
+int gs_eval_sh_bwd(void* stream, int64_t n, int sh_k, int sh_degree, const float* sh_coeffs,
+                   const float* view_dirs, const float* grad_colors, float* grad_sh, float* grad_dirs);
 
 /* The training step's tail in one pass: gs_preprocess_bwd's gradients, the
  * densification statistics of gs_densify_accumulate (from the means before the update;

@@ -295,6 +295,37 @@ __global__ __launch_bounds__(256) void composite_prep_kernel(int64_t n, const fl
   write_record(records + i * kRec, means2d[2 * i], means2d[2 * i + 1], c.x, c.y, c.w, opac[i], col);
 }
 
+// eval_sh_channel's factors F[k], rounded as it rounds them: colour c is
+// F[0] s0 - F[1] s1 + F[2] s2 - F[3] s3 + F[4] s4 + ... (k = 1 and 3 subtract).
+template <int DEG>
+__device__ inline void sh_factors(const float* d, float* F) {
+  const float x = d[0], y = d[1], z = d[2];
+  const float xx = x * x, yy = y * y, zz = z * z;
+  const float xy = x * y, yz = y * z, xz = x * z;
+  F[0] = SH_C0;
+  if (DEG > 0) {
+    F[1] = SH_C1 * y;
+    F[2] = SH_C1 * z;
+    F[3] = SH_C1 * x;
+  }
+  if (DEG > 1) {
+    F[4] = SH_C2_0 * xy;
+    F[5] = SH_C2_1 * yz;
+    F[6] = SH_C2_2 * ((2.0f * zz - xx) - yy);
+    F[7] = SH_C2_3 * xz;
+    F[8] = SH_C2_4 * (xx - yy);
+  }
+  if (DEG > 2) {
+    F[9] = (SH_C3_0 * y) * (3.0f * xx - yy);
+    F[10] = (SH_C3_1 * xy) * z;
+    F[11] = (SH_C3_2 * y) * ((4.0f * zz - xx) - yy);
+    F[12] = (SH_C3_3 * z) * ((2.0f * zz - 3.0f * xx) - 3.0f * yy);
+    F[13] = (SH_C3_4 * x) * ((4.0f * zz - xx) - yy);
+    F[14] = (SH_C3_5 * z) * (xx - yy);
+    F[15] = (SH_C3_6 * x) * (xx - 3.0f * yy);
+  }
+}
+
 // basis_k and d basis_k / d(x,y,z) of the degree<=3 real SH basis of eval_sh_channel.
 template <int DEG>
 __device__ inline void sh_basis_and_grad(const float* d, float* B, float (*dB)[3]) {
@@ -372,33 +403,9 @@ __device__ inline void colour_vjp(const float* w, float mx, float my, float mz, 
   constexpr int NB = (DEG + 1) * (DEG + 1);
   float vv[3], nrm, d[3];
   view_dir(w, mx, my, mz, vv, nrm, d);
-  const float x = d[0], y = d[1], z = d[2];
-  const float xx = x * x, yy = y * y, zz = z * z;
-  const float xy = x * y, yz = y * z, xz = x * z;
   // eval_sh_channel's factors; k = 1 and 3 enter with a minus sign
   float F[16];
-  F[0] = SH_C0;
-  if (DEG > 0) {
-    F[1] = SH_C1 * y;
-    F[2] = SH_C1 * z;
-    F[3] = SH_C1 * x;
-  }
-  if (DEG > 1) {
-    F[4] = SH_C2_0 * xy;
-    F[5] = SH_C2_1 * yz;
-    F[6] = SH_C2_2 * ((2.0f * zz - xx) - yy);
-    F[7] = SH_C2_3 * xz;
-    F[8] = SH_C2_4 * (xx - yy);
-  }
-  if (DEG > 2) {
-    F[9] = (SH_C3_0 * y) * (3.0f * xx - yy);
-    F[10] = (SH_C3_1 * xy) * z;
-    F[11] = (SH_C3_2 * y) * ((4.0f * zz - xx) - yy);
-    F[12] = (SH_C3_3 * z) * ((2.0f * zz - 3.0f * xx) - 3.0f * yy);
-    F[13] = (SH_C3_4 * x) * ((4.0f * zz - xx) - yy);
-    F[14] = (SH_C3_5 * z) * (xx - yy);
-    F[15] = (SH_C3_6 * x) * (xx - 3.0f * yy);
-  }
+  sh_factors<DEG>(d, F);
   float B[16], dB[16][3];
   sh_basis_and_grad<DEG>(d, B, dB);  // (only the derivatives are used)
   float res[3], V[3][3];
@@ -438,11 +445,13 @@ __device__ inline void colour_vjp(const float* w, float mx, float my, float mz, 
 
 // Geometric part of the backward of one Gaussian (projection, covariance, conic, opacity)
 // given its gradient record grow; g_mcol: the mean's cotangent through the view direction
-// (colour_vjp), added last.
+// (colour_vjp), added last.  part (may be NULL): the Gaussian's share of dL/dW2C through
+// the camera-space mean and W_rot, part[3a+b] for W2C[a][b] and part[9+a] for W2C[a][3]
+// (projection.py:26-27, 52-57).
 __device__ inline void preprocess_bwd_geom(int64_t i, const GaussIn& in, const float* w, float fx, float fy,
                                            const float* grow, const float* g_mcol, float* __restrict__ g_means,
                                            float* __restrict__ g_scales, float* __restrict__ g_quats,
-                                           float* __restrict__ g_opac) {
+                                           float* __restrict__ g_opac, float* part = nullptr) {
   const float mx = in.mx, my = in.my, mz = in.mz;
   float q[4], ls[3];
 #pragma unroll
@@ -519,6 +528,18 @@ __device__ inline void preprocess_bwd_geom(int64_t i, const GaussIn& in, const f
   g_x += g_m2x * fx / p.z;
   g_y += g_m2y * fy / p.z;
   g_z += -(g_m2x * (fx * p.x) + g_m2y * (fy * p.y)) / (p.z * p.z);
+  if (part != nullptr) {
+    // means_cam = W_rot m + t;  M2 = J W_rot with J = [[fx iz, 0, -fx x iz2], [0, fy iz, -fy y iz2]]
+    const float J0[3] = {fx * p.iz, 0.0f, ((-fx) * p.x) * p.iz2};
+    const float J1[3] = {0.0f, fy * p.iz, ((-fy) * p.y) * p.iz2};
+    const float gp[3] = {g_x, g_y, g_z}, m[3] = {mx, my, mz};
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+#pragma unroll
+      for (int b = 0; b < 3; ++b) part[3 * a + b] = gp[a] * m[b] + (J0[a] * g_M2[0][b] + J1[a] * g_M2[1][b]);
+      part[9 + a] = gp[a];
+    }
+  }
   // ---- camera-space mean <- world mean
   float g_m[3];
 #pragma unroll
@@ -593,31 +614,24 @@ __device__ inline void preprocess_bwd_one(int64_t i, int K, const GaussIn& in, c
   preprocess_bwd_geom(i, in, w, fx, fy, grow, g_mcol, g_means, g_scales, g_quats, g_opac);
 }
 
-// One thread per Gaussian, one wave per 64 Gaussians.  Each lane loads its SH row and
-// gradient record straight into registers and stores its SH cotangent row from them
-// (16-byte accesses when rows are 16-byte aligned); no LDS, so occupancy is set by
-// registers alone.
-// (scheduled for 2 waves per SIMD: the compiler then allocates 137 VGPRs instead of 162,
-// three waves stay resident either way, and the schedule measured 1-2 % faster)
+// Sum over the wave's 64 lanes (every lane gets it).
+__device__ inline float wave_total(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// The backward of Gaussian i from its inputs, SH row shv and gradient record grow;
+// part (may be NULL): its share of dL/dW2C (preprocess_bwd_geom's 12 values and the view
+// vector's cotangent in part[12..14]).
 template <int DEG>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void preprocess_bwd_kernel(
-    int64_t n, int K, const float* __restrict__ means, const float* __restrict__ scales,
-    const float* __restrict__ quats, const float* __restrict__ opac, const float* __restrict__ sh,
-    const float* __restrict__ w2c, float fx, float fy, const float* __restrict__ grec,
-    float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_quats,
-    float* __restrict__ g_opac, float* __restrict__ g_sh) {
+__device__ inline void preprocess_bwd_gauss(int64_t i, int K, const GaussIn& in, const float* __restrict__ w2c,
+                                            float fx, float fy, const float* shv, const float* grow, bool aligned,
+                                            float* __restrict__ g_means, float* __restrict__ g_scales,
+                                            float* __restrict__ g_quats, float* __restrict__ g_opac,
+                                            float* __restrict__ g_sh, float* part) {
   constexpr int NB = (DEG + 1) * (DEG + 1);
   const int KC = 3 * K;
-  const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
-  // every input load of the lane is issued before the first use (clamped index)
-  const int64_t ic = i < n ? i : n - 1;
-  const GaussIn in = load_gauss(means, scales, quats, opac, ic);
-  const bool aligned = (KC & 3) == 0 && (reinterpret_cast<uintptr_t>(sh) & 15) == 0 &&
-                       (reinterpret_cast<uintptr_t>(g_sh) & 15) == 0;
-  float shv[3 * NB], grow[kRec];
-  load_row<3 * NB>(sh + ic * KC, aligned, shv);
-  load_row<kRec>(grec + ic * kRec, (reinterpret_cast<uintptr_t>(grec) & 15) == 0, grow);
-  if (i >= n) return;
   float w[16];
   load_w2c(w2c, w);
   // the colour VJP first: the SH row is dead once it returns, so the geometric VJP
@@ -637,7 +651,91 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     for (int t = 0; t < 3 * NB; ++t) dst[t] = cot(t);
     for (int t = 3 * NB; t < KC; ++t) dst[t] = 0.0f;
   }
-  preprocess_bwd_geom(i, in, w, fx, fy, grow, g_mcol, g_means, g_scales, g_quats, g_opac);
+  preprocess_bwd_geom(i, in, w, fx, fy, grow, g_mcol, g_means, g_scales, g_quats, g_opac, part);
+  if (part != nullptr) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) part[12 + k] = g_mcol[k];
+  }
+}
+
+// One thread per Gaussian, one wave per 64 Gaussians.  Each lane loads its SH row and
+// gradient record straight into registers and stores its SH cotangent row from them
+// (16-byte accesses when rows are 16-byte aligned); no LDS, so occupancy is set by
+// registers alone.
+// (scheduled for 2 waves per SIMD: the compiler then allocates 137 VGPRs instead of 162,
+// three waves stay resident either way, and the schedule measured 1-2 % faster)
+// W2C: each wave also writes its 64 Gaussians' summed shares of dL/dW2C (15 floats:
+// through the mean and W_rot, then the view vector's cotangent) to w2c_part[16 * block].
+template <int DEG, bool W2C>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void preprocess_bwd_kernel(
+    int64_t n, int K, const float* __restrict__ means, const float* __restrict__ scales,
+    const float* __restrict__ quats, const float* __restrict__ opac, const float* __restrict__ sh,
+    const float* __restrict__ w2c, float fx, float fy, const float* __restrict__ grec,
+    float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_quats,
+    float* __restrict__ g_opac, float* __restrict__ g_sh, float* __restrict__ w2c_part) {
+  constexpr int NB = (DEG + 1) * (DEG + 1);
+  const int KC = 3 * K;
+  const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  // every input load of the lane is issued before the first use (clamped index)
+  const int64_t ic = i < n ? i : n - 1;
+  const GaussIn in = load_gauss(means, scales, quats, opac, ic);
+  const bool aligned = (KC & 3) == 0 && (reinterpret_cast<uintptr_t>(sh) & 15) == 0 &&
+                       (reinterpret_cast<uintptr_t>(g_sh) & 15) == 0;
+  float shv[3 * NB], grow[kRec];
+  load_row<3 * NB>(sh + ic * KC, aligned, shv);
+  load_row<kRec>(grec + ic * kRec, (reinterpret_cast<uintptr_t>(grec) & 15) == 0, grow);
+  if (W2C) {
+    float part[15];
+#pragma unroll
+    for (int k = 0; k < 15; ++k) part[k] = 0.0f;
+    if (i < n) preprocess_bwd_gauss<DEG>(i, K, in, w2c, fx, fy, shv, grow, aligned, g_means, g_scales, g_quats,
+                                         g_opac, g_sh, part);
+#pragma unroll
+    for (int k = 0; k < 15; ++k) {
+      const float t = wave_total(part[k]);
+      if (threadIdx.x == 0) w2c_part[16 * (int64_t)blockIdx.x + k] = t;
+    }
+    return;
+  }
+  if (i >= n) return;
+  preprocess_bwd_gauss<DEG>(i, K, in, w2c, fx, fy, shv, grow, aligned, g_means, g_scales, g_quats, g_opac, g_sh,
+                            nullptr);
+}
+
+// dL/dW2C from the waves' partial sums, in a fixed order (one workgroup): the shares through
+// the mean and W_rot plus the camera centre's (centre = -R^T t, camera.py:15-21: with S
+// the summed view-vector cotangent, dR[a][b] += t[a] S[b] and dt[a] += sum_b R[a][b] S[b]).
+// Row 3 of W2C never enters the projection (projection.py:27 keeps three rows): zero.
+__global__ __launch_bounds__(256) void w2c_finish_kernel(const float* __restrict__ part, int64_t nblk,
+                                                         const float* __restrict__ w2c, float* __restrict__ g_w2c) {
+  __shared__ float red[4][16];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  float acc[15];
+#pragma unroll
+  for (int k = 0; k < 15; ++k) acc[k] = 0.0f;
+  for (int64_t b = tid; b < nblk; b += 256)
+#pragma unroll
+    for (int k = 0; k < 15; ++k) acc[k] += part[16 * b + k];
+#pragma unroll
+  for (int k = 0; k < 15; ++k) {
+    const float t = wave_total(acc[k]);
+    if (lane == 0) red[wid][k] = t;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float tot[15];
+#pragma unroll
+    for (int k = 0; k < 15; ++k) tot[k] = (red[0][k] + red[1][k]) + (red[2][k] + red[3][k]);
+    for (int a = 0; a < 3; ++a) {
+      float gt = tot[9 + a];
+      for (int b = 0; b < 3; ++b) {
+        g_w2c[4 * a + b] = tot[3 * a + b] + w2c[4 * a + 3] * tot[12 + b];
+        gt += w2c[4 * a + b] * tot[12 + b];
+      }
+      g_w2c[4 * a + 3] = gt;
+    }
+    for (int b = 0; b < 4; ++b) g_w2c[12 + b] = 0.0f;
+  }
 }
 
 // The training step's tail in one pass (trainer.py:137-159 with optax.adam of
@@ -842,29 +940,34 @@ extern "C" int gs_composite_prep(void* stream, int64_t n, const float* means2d, 
   return GS_OK;
 }
 
-extern "C" int gs_preprocess_bwd(void* stream, int64_t n, int sh_k, int sh_degree, const float* means,
-                                 const float* scales, const float* quats, const float* opacities,
-                                 const float* sh_coeffs, const float* w2c, int width, int height,
-                                 float fx, float fy, float cx, float cy, const float* grad_records,
-                                 float* grad_means, float* grad_scales, float* grad_quats,
-                                 float* grad_opacities, float* grad_sh) {
-  GS_REQUIRE(n >= 0, "gs_preprocess_bwd: n must be >= 0");
-  GS_REQUIRE(sh_degree >= 0 && sh_degree <= 3, "gs_preprocess_bwd: sh_degree must be in 0..3 (got %d)", sh_degree);
+namespace gs {
+namespace {
+int preprocess_bwd_launch(void* stream, int64_t n, int sh_k, int sh_degree, const float* means,
+                          const float* scales, const float* quats, const float* opacities, const float* sh_coeffs,
+                          const float* w2c, float fx, float fy, const float* grad_records, float* grad_means,
+                          float* grad_scales, float* grad_quats, float* grad_opacities, float* grad_sh,
+                          float* w2c_part, const char* who) {
+  GS_REQUIRE(n >= 0, "%s: n must be >= 0", who);
+  GS_REQUIRE(sh_degree >= 0 && sh_degree <= 3, "%s: sh_degree must be in 0..3 (got %d)", who, sh_degree);
   GS_REQUIRE(sh_k >= (sh_degree + 1) * (sh_degree + 1) && sh_k <= 16,
-             "gs_preprocess_bwd: sh_coeffs has %d coefficients, degree %d needs %d (max 16)", sh_k,
-             sh_degree, (sh_degree + 1) * (sh_degree + 1));
+             "%s: sh_coeffs has %d coefficients, degree %d needs %d (max 16)", who, sh_k, sh_degree,
+             (sh_degree + 1) * (sh_degree + 1));
   if (n == 0) return GS_OK;
   GS_REQUIRE(means && scales && quats && opacities && sh_coeffs && w2c && grad_records && grad_means &&
                  grad_scales && grad_quats && grad_opacities && grad_sh,
-             "gs_preprocess_bwd: NULL array argument");
-  (void)width;
-  (void)height;
-  (void)cx;
-  (void)cy;
-#define GS_PRE_BWD(D)                                                                                          \
-  hipLaunchKernelGGL(preprocess_bwd_kernel<D>, dim3(div_up(n, 64)), dim3(64), 0, (hipStream_t)stream, n, sh_k,    \
-                     means, scales, quats, opacities, sh_coeffs, w2c, fx, fy, grad_records, grad_means, grad_scales, \
-                     grad_quats, grad_opacities, grad_sh)
+             "%s: NULL array argument", who);
+  const bool part = w2c_part != nullptr;
+#define GS_PRE_BWD(D)                                                                                            \
+  do {                                                                                                           \
+    if (part)                                                                                                    \
+      hipLaunchKernelGGL((preprocess_bwd_kernel<D, true>), dim3(div_up(n, 64)), dim3(64), 0, (hipStream_t)stream, \
+                         n, sh_k, means, scales, quats, opacities, sh_coeffs, w2c, fx, fy, grad_records,           \
+                         grad_means, grad_scales, grad_quats, grad_opacities, grad_sh, w2c_part);                 \
+    else                                                                                                         \
+      hipLaunchKernelGGL((preprocess_bwd_kernel<D, false>), dim3(div_up(n, 64)), dim3(64), 0,                   \
+                         (hipStream_t)stream, n, sh_k, means, scales, quats, opacities, sh_coeffs, w2c, fx, fy,   \
+                         grad_records, grad_means, grad_scales, grad_quats, grad_opacities, grad_sh, nullptr);   \
+  } while (0)
   switch (sh_degree) {
     case 0: GS_PRE_BWD(0); break;
     case 1: GS_PRE_BWD(1); break;
@@ -873,6 +976,149 @@ extern "C" int gs_preprocess_bwd(void* stream, int64_t n, int sh_k, int sh_degre
   }
 #undef GS_PRE_BWD
   GS_LAUNCH_CHECK("preprocess_bwd_kernel");
+  return GS_OK;
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" int gs_preprocess_bwd(void* stream, int64_t n, int sh_k, int sh_degree, const float* means,
+                                 const float* scales, const float* quats, const float* opacities,
+                                 const float* sh_coeffs, const float* w2c, int width, int height,
+                                 float fx, float fy, float cx, float cy, const float* grad_records,
+                                 float* grad_means, float* grad_scales, float* grad_quats,
+                                 float* grad_opacities, float* grad_sh) {
+  (void)width;
+  (void)height;
+  (void)cx;
+  (void)cy;
+  return preprocess_bwd_launch(stream, n, sh_k, sh_degree, means, scales, quats, opacities, sh_coeffs, w2c, fx, fy,
+                               grad_records, grad_means, grad_scales, grad_quats, grad_opacities, grad_sh, nullptr,
+                               "gs_preprocess_bwd");
+}
+
+extern "C" size_t gs_preprocess_bwd_w2c_workspace_size(int64_t n) {
+  return n <= 0 ? 64 : (size_t)div_up(n, 64) * 16 * sizeof(float);
+}
+
+extern "C" int gs_preprocess_bwd_w2c(void* stream, int64_t n, int sh_k, int sh_degree, const float* means,
+                                     const float* scales, const float* quats, const float* opacities,
+                                     const float* sh_coeffs, const float* w2c, int width, int height, float fx,
+                                     float fy, float cx, float cy, const float* grad_records, float* grad_means,
+                                     float* grad_scales, float* grad_quats, float* grad_opacities, float* grad_sh,
+                                     float* grad_w2c, void* workspace, size_t workspace_bytes) {
+  (void)width;
+  (void)height;
+  (void)cx;
+  (void)cy;
+  GS_REQUIRE(grad_w2c != nullptr && w2c != nullptr, "gs_preprocess_bwd_w2c: NULL grad_w2c or w2c");
+  GS_REQUIRE(workspace != nullptr && workspace_bytes >= gs_preprocess_bwd_w2c_workspace_size(n),
+             "gs_preprocess_bwd_w2c: workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
+             gs_preprocess_bwd_w2c_workspace_size(n));
+  const int rc = preprocess_bwd_launch(stream, n, sh_k, sh_degree, means, scales, quats, opacities, sh_coeffs, w2c,
+                                       fx, fy, grad_records, grad_means, grad_scales, grad_quats, grad_opacities,
+                                       grad_sh, (float*)workspace, "gs_preprocess_bwd_w2c");
+  if (rc != GS_OK) return rc;
+  hipLaunchKernelGGL(w2c_finish_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, (const float*)workspace,
+                     n > 0 ? div_up(n, 64) : (int64_t)0, w2c, grad_w2c);
+  GS_LAUNCH_CHECK("w2c_finish_kernel");
+  return GS_OK;
+}
+
+namespace gs {
+namespace {
+// sh.py:25-74 on its own: one thread per row, the expansion without the renderer's +0.5
+// and clip (eval_sh_channel, the reference's association order).
+template <int DEG>
+__global__ __launch_bounds__(256) void eval_sh_kernel(int64_t n, int K, const float* __restrict__ sh,
+                                                      const float* __restrict__ dirs, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float d[3] = {dirs[3 * i], dirs[3 * i + 1], dirs[3 * i + 2]};
+  const float* row = sh + i * 3 * K;
+#pragma unroll
+  for (int c = 0; c < 3; ++c) out[3 * i + c] = eval_sh_channel<DEG>(row, c, d);
+}
+
+// Its VJP: d colour_c / d s_kc = the signed factor E_k (exactly as the forward rounds it);
+// d colour / d dir through the basis derivatives (JAX autodiff of sh.py:25-74).
+template <int DEG>
+__global__ __launch_bounds__(256) void eval_sh_bwd_kernel(int64_t n, int K, const float* __restrict__ sh,
+                                                          const float* __restrict__ dirs,
+                                                          const float* __restrict__ g_out, float* __restrict__ g_sh,
+                                                          float* __restrict__ g_dirs) {
+  constexpr int NB = (DEG + 1) * (DEG + 1);
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float d[3] = {dirs[3 * i], dirs[3 * i + 1], dirs[3 * i + 2]};
+  const float g[3] = {g_out[3 * i], g_out[3 * i + 1], g_out[3 * i + 2]};
+  float F[16];
+  sh_factors<DEG>(d, F);
+  float* dst = g_sh + i * 3 * K;
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    const float e = (k == 1 || k == 3) ? -F[k] : F[k];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) dst[3 * k + c] = e * g[c];
+  }
+  for (int q = 3 * NB; q < 3 * K; ++q) dst[q] = 0.0f;
+  if (g_dirs == nullptr) return;
+  float gd[3] = {0.0f, 0.0f, 0.0f};
+  if (DEG > 0) {
+    float B[16], dB[16][3];
+    sh_basis_and_grad<DEG>(d, B, dB);
+    const float* row = sh + i * 3 * K;
+#pragma unroll
+    for (int k = 1; k < NB; ++k) {
+      const float sk = (row[3 * k] * g[0] + row[3 * k + 1] * g[1]) + row[3 * k + 2] * g[2];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) gd[j] += sk * dB[k][j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 3; ++j) g_dirs[3 * i + j] = gd[j];
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" int gs_eval_sh(void* stream, int64_t n, int sh_k, int sh_degree, const float* sh_coeffs,
+                          const float* view_dirs, float* colors) {
+  GS_REQUIRE(n >= 0, "gs_eval_sh: n must be >= 0");
+  GS_REQUIRE(sh_degree >= 0 && sh_degree <= 3, "gs_eval_sh: sh_degree must be in 0..3 (got %d)", sh_degree);
+  GS_REQUIRE(sh_k >= (sh_degree + 1) * (sh_degree + 1), "gs_eval_sh: sh_coeffs has %d coefficients, degree %d "
+             "needs %d", sh_k, sh_degree, (sh_degree + 1) * (sh_degree + 1));
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(sh_coeffs && view_dirs && colors, "gs_eval_sh: NULL array argument");
+  hipStream_t s = (hipStream_t)stream;
+  switch (sh_degree) {
+    case 0: hipLaunchKernelGGL(eval_sh_kernel<0>, dim3(div_up(n, 256)), dim3(256), 0, s, n, sh_k, sh_coeffs, view_dirs, colors); break;
+    case 1: hipLaunchKernelGGL(eval_sh_kernel<1>, dim3(div_up(n, 256)), dim3(256), 0, s, n, sh_k, sh_coeffs, view_dirs, colors); break;
+    case 2: hipLaunchKernelGGL(eval_sh_kernel<2>, dim3(div_up(n, 256)), dim3(256), 0, s, n, sh_k, sh_coeffs, view_dirs, colors); break;
+    default: hipLaunchKernelGGL(eval_sh_kernel<3>, dim3(div_up(n, 256)), dim3(256), 0, s, n, sh_k, sh_coeffs, view_dirs, colors); break;
+  }
+  GS_LAUNCH_CHECK("eval_sh_kernel");
+  return GS_OK;
+}
+
+extern "C" int gs_eval_sh_bwd(void* stream, int64_t n, int sh_k, int sh_degree, const float* sh_coeffs,
+                              const float* view_dirs, const float* grad_colors, float* grad_sh, float* grad_dirs) {
+  GS_REQUIRE(n >= 0, "gs_eval_sh_bwd: n must be >= 0");
+  GS_REQUIRE(sh_degree >= 0 && sh_degree <= 3, "gs_eval_sh_bwd: sh_degree must be in 0..3 (got %d)", sh_degree);
+  GS_REQUIRE(sh_k >= (sh_degree + 1) * (sh_degree + 1), "gs_eval_sh_bwd: sh_coeffs has %d coefficients, degree "
+             "%d needs %d", sh_k, sh_degree, (sh_degree + 1) * (sh_degree + 1));
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(sh_coeffs && view_dirs && grad_colors && grad_sh, "gs_eval_sh_bwd: NULL array argument");
+  hipStream_t s = (hipStream_t)stream;
+#define GS_SH_BWD(D)                                                                                          \
+  hipLaunchKernelGGL(eval_sh_bwd_kernel<D>, dim3(div_up(n, 256)), dim3(256), 0, s, n, sh_k, sh_coeffs, view_dirs, \
+                     grad_colors, grad_sh, grad_dirs)
+  switch (sh_degree) {
+    case 0: GS_SH_BWD(0); break;
+    case 1: GS_SH_BWD(1); break;
+    case 2: GS_SH_BWD(2); break;
+    default: GS_SH_BWD(3); break;
+  }
+#undef GS_SH_BWD
+  GS_LAUNCH_CHECK("eval_sh_bwd_kernel");
   return GS_OK;
 }
 

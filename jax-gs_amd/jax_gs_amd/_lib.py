@@ -46,6 +46,11 @@ _SIGS = {
     "gs_composite_fwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P],
     "gs_preprocess_bwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P, _P],
+    "gs_preprocess_bwd_w2c_workspace_size": [_I64],
+    "gs_preprocess_bwd_w2c": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P,
+                              _P, _P, _P, _SZ],
+    "gs_eval_sh": [_P, _I64, _I, _I, _P, _P, _P],
+    "gs_eval_sh_bwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P],
     "gs_l1_loss": [_P, _I64, _P, _P, _P, _P],
     "gs_mse_loss": [_P, _I64, _P, _P, _P, _P],
     "gs_l1_loss_bwd": [_P, _I64, _P, _P, _P, _P],
@@ -67,13 +72,13 @@ _SIGS = {
     "gs_densify_accumulate": [_P, _I64, _P, _P, _P, _F, _F, _P, _P, _P, _P, _P, _P],
 }
 _RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_l1_ssim_workspace_size": _SZ,
-            "gs_bin_reference_workspace_size": _SZ,
+            "gs_bin_reference_workspace_size": _SZ, "gs_preprocess_bwd_w2c_workspace_size": _SZ,
             "gs_densify_workspace_size": _SZ}
 
 _lib = None
 
 
-ABI_VERSION = 6  # gs_abi_version() of the signatures bound below
+ABI_VERSION = 7  # gs_abi_version() of the signatures bound below
 
 
 class NativeLibraryMissing(RuntimeError):

@@ -8,8 +8,9 @@ the preprocessing, binning and compositing kernels and keeps the per-Gaussian
 records, the sorted entry list, the tile ranges, per-pixel (final T, entry count)
 and the backward's tile order as residuals; its backward runs the compositing VJP and the preprocessing VJP and
 returns cotangents of the five Gaussian arrays (equal to JAX autodiff of the
-reference forward, with its tie conventions) and of the background.  W2C gets no
-gradient (the reference's trainer never differentiates it) and mask gets None.
+reference forward, with its tie conventions), of the background, and of the camera's
+W2C when it requires grad (through the camera-space means, W_rot and the view
+directions' camera centre); mask gets None.
 ``fast_tpu_rasterizer`` selects the reference's compositing path: True reads each tile's
 own entries (rasterizer_tpu.py:90-97); False (the default) slices 512-entry chunk windows
 clamped to the end of the reference's max(256*N, 512)-slot arrays (rasterizer.py:184-190),
@@ -85,11 +86,19 @@ class _Render(torch.autograd.Function):
         gq = torch.empty_like(quats)
         go = torch.empty_like(opac)
         gsh = torch.empty_like(sh)
-        _lib.call("gs_preprocess_bwd", s, n, sh.shape[1], int(sh_degree), _lib.ptr(means), _lib.ptr(scales),
-                  _lib.ptr(quats), _lib.ptr(opac), _lib.ptr(sh), _lib.ptr(w2c), int(W), int(H), float(fx), float(fy),
-                  float(cx), float(cy), _lib.ptr(grec), _lib.ptr(gm), _lib.ptr(gs_), _lib.ptr(gq), _lib.ptr(go),
-                  _lib.ptr(gsh))
-        return gm, gs_, gq, go, gsh, None, gbg, None, None
+        args = (s, n, sh.shape[1], int(sh_degree), _lib.ptr(means), _lib.ptr(scales), _lib.ptr(quats), _lib.ptr(opac),
+                _lib.ptr(sh), _lib.ptr(w2c), int(W), int(H), float(fx), float(fy), float(cx), float(cy), _lib.ptr(grec),
+                _lib.ptr(gm), _lib.ptr(gs_), _lib.ptr(gq), _lib.ptr(go), _lib.ptr(gsh))
+        gw = None
+        if ctx.needs_input_grad[5]:
+            # the camera's cotangent (the reference differentiates W2C like any input)
+            gw = torch.empty((4, 4), dtype=torch.float32, device=dev)
+            nb = _lib.lib().gs_preprocess_bwd_w2c_workspace_size(n)
+            ws = torch.empty((nb,), dtype=torch.uint8, device=dev)
+            _lib.call("gs_preprocess_bwd_w2c", *args, _lib.ptr(gw), _lib.ptr(ws), nb)
+        else:
+            _lib.call("gs_preprocess_bwd", *args)
+        return gm, gs_, gq, go, gsh, gw, gbg, None, None
 
 
 def render(gaussians: Gaussians, camera: Camera, background=None, fast_tpu_rasterizer: bool = False, mask=None,

@@ -156,19 +156,44 @@ def render_tiles_bwd(means2d, cov2d, opacities, colors, sorted_tiles, sorted_gid
 
 
 def preprocess_bwd(means, scales, quats, sh, w2c, fx, fy, sh_degree, g_means2d, g_cov2d, g_colors, dtype=np.float32):
-    """Reverse-mode derivative of preprocess w.r.t. means, scales, quaternions, sh_coeffs."""
+    """Reverse-mode derivative of preprocess w.r.t. means, scales, quaternions, sh_coeffs
+    and the camera's W2C (key "W2C", [4,4], row 3 zero)."""
     means, scales, quats, sh, w2c, g_means2d, g_cov2d, g_colors = (
         _c(a, dtype) for a in (means, scales, quats, sh, w2c, g_means2d, g_cov2d, g_colors))
     n, K = means.shape[0], sh.shape[1]
     out = dict(means=np.zeros((n, 3), dtype), scales=np.zeros((n, 3), dtype), quaternions=np.zeros((n, 4), dtype),
-               sh_coeffs=np.zeros((n, K, 3), dtype))
+               sh_coeffs=np.zeros((n, K, 3), dtype), W2C=np.zeros((4, 4), dtype))
     R = _real(dtype)
-    fn = getattr(lib(), "gso_preprocess_bwd_" + _sfx(dtype))
+    fn = getattr(lib(), "gso_preprocess_bwd_w2c_" + _sfx(dtype))
     rc = fn(ctypes.c_int64(n), ctypes.c_int(K), ctypes.c_int(sh_degree), _p(means), _p(scales), _p(quats), _p(sh),
             _p(w2c.reshape(16)), R(fx), R(fy), _p(g_means2d), _p(g_cov2d), _p(g_colors), _p(out["means"]),
-            _p(out["scales"]), _p(out["quaternions"]), _p(out["sh_coeffs"]))
+            _p(out["scales"]), _p(out["quaternions"]), _p(out["sh_coeffs"]), _p(out["W2C"]))
     assert rc == 0
     return out
+
+
+def eval_sh(sh_degree, sh_coeffs, view_dirs, dtype=np.float32):
+    """sh.py:25-74: the SH expansion [N, 3] (no +0.5, no clip)."""
+    sh, d = _c(sh_coeffs, dtype), _c(view_dirs, dtype)
+    n, K = sh.shape[0], sh.shape[1]
+    out = np.zeros((n, 3), dtype)
+    rc = getattr(lib(), "gso_eval_sh_" + _sfx(dtype))(ctypes.c_int64(n), ctypes.c_int(K), ctypes.c_int(sh_degree),
+                                                        _p(sh), _p(d), _p(out))
+    assert rc == 0
+    return out
+
+
+def eval_sh_vjp(sh_degree, sh_coeffs, view_dirs, g_colors, dtype=np.float32):
+    """Cotangents (sh_coeffs [N, K, 3], view_dirs [N, 3]) of eval_sh for g_colors [N, 3]."""
+    sh, d, g = _c(sh_coeffs, dtype), _c(view_dirs, dtype), _c(g_colors, dtype)
+    n, K = sh.shape[0], sh.shape[1]
+    g_sh = np.zeros((n, K, 3), dtype)
+    g_d = np.zeros((n, 3), dtype)
+    rc = getattr(lib(), "gso_eval_sh_bwd_" + _sfx(dtype))(ctypes.c_int64(n), ctypes.c_int(K),
+                                                            ctypes.c_int(sh_degree), _p(sh), _p(d), _p(g), _p(g_sh),
+                                                            _p(g_d))
+    assert rc == 0
+    return g_sh, g_d
 
 
 def tile_boundaries(sorted_tiles, num_tiles):
@@ -237,7 +262,7 @@ def render_vjp(params, cam, res, g_image, sh_degree=0, tpu_gather=False, dtype=n
     gp = preprocess_bwd(params["means"], params["scales"], params["quaternions"], params["sh_coeffs"], cam["W2C"],
                         f(cam["fx"]), f(cam["fy"]), sh_degree, gt["means2d"], gt["cov2d"], gt["colors"], dtype=dtype)
     return dict(means=gp["means"], scales=gp["scales"], quaternions=gp["quaternions"], opacities=gt["opacities"],
-                sh_coeffs=gp["sh_coeffs"], background=gt["background"])
+                sh_coeffs=gp["sh_coeffs"], background=gt["background"], W2C=gp["W2C"])
 
 
 def densify(g_means, means, w2c, fx, fy, W, H, valid, radii, grad_accum, denom, max_radii, active=None,

@@ -121,7 +121,7 @@ static double gso_sigmoid(double x) { return 1.0 / (1.0 + exp(-x)); }
 #undef CEIL
 #undef FLOOR
 
-int gso_abi_version(void) { return 2; }
+int gso_abi_version(void) { return 3; }
 
 /* Threads used by the parallel loops (0 or less: leave OpenMP's default). */
 void gso_set_threads(int n) {

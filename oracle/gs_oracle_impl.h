@@ -597,17 +597,94 @@ int FN(gso_render_tiles_bwd)(int64_t n, const REAL* means2d, const REAL* cov2d, 
   return 0;
 }
 
-/* Reverse-mode derivative of gso_preprocess w.r.t. means, scales, quaternions and
- * sh_coeffs given cotangents of means2d, cov2d and colors (radii, valid and depths
- * carry none into the image).  Outputs are overwritten. */
-int FN(gso_preprocess_bwd)(int64_t n, int K, int deg, const REAL* means, const REAL* scales, const REAL* quats,
-                           const REAL* sh, const REAL* w2c, REAL fx, REAL fy, const REAL* g_means2d,
-                           const REAL* g_cov2d, const REAL* g_colors, REAL* g_means, REAL* g_scales, REAL* g_quats,
-                           REAL* g_sh) {
-  const REAL* w = w2c;
+/* VJP of eval_sh (sh.py:25-74) for one Gaussian: gsh[k][c] = basis_k * g[c] (0 beyond the
+ * degree) and g_d += the cotangent of the view direction d. */
+static void FN(sh_vjp)(int K, int deg, const REAL* shi, const REAL* d, const REAL* g_pre, REAL* gsh, REAL* g_d) {
+  int c, k;
+  /* eval_sh is linear in sh: d/dsh_k = basis_k, obtained by evaluating with unit
+   * coefficient vectors; d/d(view dir) by the explicit basis derivatives below. */
+  for (k = 0; k < K; ++k) {
+    if (k < (deg + 1) * (deg + 1)) {
+      REAL unit[48];
+      REAL bk;
+      memset(unit, 0, sizeof(unit));
+      unit[k * 3] = 1;
+      bk = FN(eval_sh)(deg, unit, 0, d);
+      for (c = 0; c < 3; ++c) gsh[3 * k + c] = bk * g_pre[c];
+    } else {
+      for (c = 0; c < 3; ++c) gsh[3 * k + c] = 0;
+    }
+  }
+  if (deg > 0) {
+    /* directional derivative of sum_c g_pre[c] * eval_sh(c) via the basis gradients */
+    const REAL x = d[0], y = d[1], z = d[2];
+    const REAL* C2 = FN(C2);
+    const REAL* C3 = FN(C3);
+    REAL s[16];
+    REAL dB[16][3];
+    memset(dB, 0, sizeof(dB));
+    for (k = 0; k < 16; ++k) s[k] = (k < K && k < (deg + 1) * (deg + 1))
+                                        ? (shi[3 * k] * g_pre[0] + shi[3 * k + 1] * g_pre[1]) + shi[3 * k + 2] * g_pre[2]
+                                        : (REAL)0;
+    dB[1][1] = -FN(C1); dB[2][2] = FN(C1); dB[3][0] = -FN(C1);
+    if (deg > 1) {
+      dB[4][0] = C2[0] * y; dB[4][1] = C2[0] * x;
+      dB[5][1] = C2[1] * z; dB[5][2] = C2[1] * y;
+      dB[6][0] = C2[2] * (-2 * x); dB[6][1] = C2[2] * (-2 * y); dB[6][2] = C2[2] * (4 * z);
+      dB[7][0] = C2[3] * z; dB[7][2] = C2[3] * x;
+      dB[8][0] = C2[4] * (2 * x); dB[8][1] = C2[4] * (-2 * y);
+    }
+    if (deg > 2) {
+      dB[9][0] = C3[0] * 6 * x * y; dB[9][1] = C3[0] * (3 * x * x - 3 * y * y);
+      dB[10][0] = C3[1] * y * z; dB[10][1] = C3[1] * x * z; dB[10][2] = C3[1] * x * y;
+      dB[11][0] = C3[2] * (-2 * x * y); dB[11][1] = C3[2] * (4 * z * z - x * x - 3 * y * y); dB[11][2] = C3[2] * 8 * y * z;
+      dB[12][0] = C3[3] * (-6 * x * z); dB[12][1] = C3[3] * (-6 * y * z); dB[12][2] = C3[3] * (6 * z * z - 3 * x * x - 3 * y * y);
+      dB[13][0] = C3[4] * (4 * z * z - 3 * x * x - y * y); dB[13][1] = C3[4] * (-2 * x * y); dB[13][2] = C3[4] * 8 * x * z;
+      dB[14][0] = C3[5] * 2 * x * z; dB[14][1] = C3[5] * (-2 * y * z); dB[14][2] = C3[5] * (x * x - y * y);
+      dB[15][0] = C3[6] * (3 * x * x - 3 * y * y); dB[15][1] = C3[6] * (-6 * x * y);
+    }
+    for (k = 0; k < 16; ++k)
+      for (c = 0; c < 3; ++c) g_d[c] += s[k] * dB[k][c];
+  }
+}
+
+int FN(gso_eval_sh)(int64_t n, int K, int deg, const REAL* sh, const REAL* dirs, REAL* out) {
   int64_t i;
 #pragma omp parallel for schedule(static)
   for (i = 0; i < n; ++i) {
+    int c;
+    for (c = 0; c < 3; ++c) out[3 * i + c] = FN(eval_sh)(deg, sh + i * K * 3, c, dirs + 3 * i);
+  }
+  return 0;
+}
+
+int FN(gso_eval_sh_bwd)(int64_t n, int K, int deg, const REAL* sh, const REAL* dirs, const REAL* g_out, REAL* g_sh,
+                        REAL* g_dirs) {
+  int64_t i;
+#pragma omp parallel for schedule(static)
+  for (i = 0; i < n; ++i) {
+    REAL gd[3] = {0, 0, 0};
+    FN(sh_vjp)(K, deg, sh + i * K * 3, dirs + 3 * i, g_out + 3 * i, g_sh + i * K * 3, gd);
+    g_dirs[3 * i] = gd[0];
+    g_dirs[3 * i + 1] = gd[1];
+    g_dirs[3 * i + 2] = gd[2];
+  }
+  return 0;
+}
+
+/* Reverse-mode derivative of gso_preprocess for Gaussian i w.r.t. its mean, scales,
+ * quaternion and sh_coeffs given cotangents of means2d, cov2d and colors (radii, valid
+ * and depths carry none into the image).  part (may be NULL) receives the Gaussian's
+ * share of the W2C cotangent before the camera-centre term: part[3a+b] for W2C[a][b]
+ * through the camera-space mean (projection.py:26-27) and W_rot (:52-57), part[9+a] for
+ * W2C[a][3], and part[12..14] the cotangent of the view vector m - centre
+ * (renderer.py:40-41); the caller adds the centre's share (camera.py:15-21). */
+static void FN(pre_bwd_one)(int64_t i, int K, int deg, const REAL* means, const REAL* scales, const REAL* quats,
+                            const REAL* sh, const REAL* w2c, REAL fx, REAL fy, const REAL* g_means2d,
+                            const REAL* g_cov2d, const REAL* g_colors, REAL* g_means, REAL* g_scales,
+                            REAL* g_quats, REAL* g_sh, REAL* part) {
+  const REAL* w = w2c;
+  {
     FN(proj_t) p;
     REAL v[3], nrm, d[3], g_pre[3], g_d[3] = {0, 0, 0}, g_m[3];
     REAL gx = 0, gy = 0, gz = 0, g_iz, g_iz2, g_zs;
@@ -623,51 +700,7 @@ int FN(gso_preprocess_bwd)(int64_t n, int K, int deg, const REAL* means, const R
       const REAL lo = FN(r_max)((REAL)0, pre);
       g_pre[c] = g_colors[3 * i + c] * FN(d_min)(lo, (REAL)1) * FN(d_max)(pre, (REAL)0);
     }
-    /* eval_sh is linear in sh: d/dsh_k = basis_k, obtained by evaluating with unit
-     * coefficient vectors; d/d(view dir) by the explicit basis derivatives below. */
-    for (k = 0; k < K; ++k) {
-      if (k < (deg + 1) * (deg + 1)) {
-        REAL unit[48];
-        REAL bk;
-        memset(unit, 0, sizeof(unit));
-        unit[k * 3] = 1;
-        bk = FN(eval_sh)(deg, unit, 0, d);
-        for (c = 0; c < 3; ++c) gsh[3 * k + c] = bk * g_pre[c];
-      } else {
-        for (c = 0; c < 3; ++c) gsh[3 * k + c] = 0;
-      }
-    }
-    if (deg > 0) {
-      /* directional derivative of sum_c g_pre[c] * eval_sh(c) via the basis gradients */
-      const REAL x = d[0], y = d[1], z = d[2];
-      const REAL* C2 = FN(C2);
-      const REAL* C3 = FN(C3);
-      REAL s[16];
-      REAL dB[16][3];
-      memset(dB, 0, sizeof(dB));
-      for (k = 0; k < 16; ++k) s[k] = (k < K && k < (deg + 1) * (deg + 1))
-                                          ? (shi[3 * k] * g_pre[0] + shi[3 * k + 1] * g_pre[1]) + shi[3 * k + 2] * g_pre[2]
-                                          : (REAL)0;
-      dB[1][1] = -FN(C1); dB[2][2] = FN(C1); dB[3][0] = -FN(C1);
-      if (deg > 1) {
-        dB[4][0] = C2[0] * y; dB[4][1] = C2[0] * x;
-        dB[5][1] = C2[1] * z; dB[5][2] = C2[1] * y;
-        dB[6][0] = C2[2] * (-2 * x); dB[6][1] = C2[2] * (-2 * y); dB[6][2] = C2[2] * (4 * z);
-        dB[7][0] = C2[3] * z; dB[7][2] = C2[3] * x;
-        dB[8][0] = C2[4] * (2 * x); dB[8][1] = C2[4] * (-2 * y);
-      }
-      if (deg > 2) {
-        dB[9][0] = C3[0] * 6 * x * y; dB[9][1] = C3[0] * (3 * x * x - 3 * y * y);
-        dB[10][0] = C3[1] * y * z; dB[10][1] = C3[1] * x * z; dB[10][2] = C3[1] * x * y;
-        dB[11][0] = C3[2] * (-2 * x * y); dB[11][1] = C3[2] * (4 * z * z - x * x - 3 * y * y); dB[11][2] = C3[2] * 8 * y * z;
-        dB[12][0] = C3[3] * (-6 * x * z); dB[12][1] = C3[3] * (-6 * y * z); dB[12][2] = C3[3] * (6 * z * z - 3 * x * x - 3 * y * y);
-        dB[13][0] = C3[4] * (4 * z * z - 3 * x * x - y * y); dB[13][1] = C3[4] * (-2 * x * y); dB[13][2] = C3[4] * 8 * x * z;
-        dB[14][0] = C3[5] * 2 * x * z; dB[14][1] = C3[5] * (-2 * y * z); dB[14][2] = C3[5] * (x * x - y * y);
-        dB[15][0] = C3[6] * (3 * x * x - 3 * y * y); dB[15][1] = C3[6] * (-6 * x * y);
-      }
-      for (k = 0; k < 16; ++k)
-        for (c = 0; c < 3; ++c) g_d[c] += s[k] * dB[k][c];
-    }
+    FN(sh_vjp)(K, deg, shi, d, g_pre, gsh, g_d);
     /* cov2D cotangent; cov2D[1,0] is never read by the renderer */
     G[0][0] = g_cov2d[4 * i]; G[0][1] = g_cov2d[4 * i + 1]; G[1][0] = g_cov2d[4 * i + 2]; G[1][1] = g_cov2d[4 * i + 3];
     /* cov = T1 M2^T, T1 = M2 Sig */
@@ -695,9 +728,23 @@ int FN(gso_preprocess_bwd)(int64_t n, int K, int deg, const REAL* means, const R
     gy += g_means2d[2 * i + 1] * fy / p.z;
     gz += -(g_means2d[2 * i] * fx * p.x + g_means2d[2 * i + 1] * fy * p.y) / (p.z * p.z);
     for (k = 0; k < 3; ++k) g_m[k] = (w[0 * 4 + k] * gx + w[1 * 4 + k] * gy) + w[2 * 4 + k] * gz;
+    if (part != NULL) {
+      /* means_cam = W2C[:3,:3] m + W2C[:3,3]; M2 = J W_rot */
+      const REAL gp[3] = {gx, gy, gz};
+      const REAL J[2][3] = {{fx * p.iz, 0, ((-fx) * p.x) * p.iz2}, {0, fy * p.iz, ((-fy) * p.y) * p.iz2}};
+      const REAL* m = means + 3 * i;
+      for (a = 0; a < 3; ++a) {
+        for (b = 0; b < 3; ++b) part[3 * a + b] += gp[a] * m[b] + (J[0][a] * gM2[0][b] + J[1][a] * gM2[1][b]);
+        part[9 + a] += gp[a];
+      }
+    }
     if (deg > 0) {
       const REAL dg = (d[0] * g_d[0] + d[1] * g_d[1]) + d[2] * g_d[2];
-      for (k = 0; k < 3; ++k) g_m[k] += (g_d[k] - d[k] * dg) / nrm;
+      for (k = 0; k < 3; ++k) {
+        const REAL gv = (g_d[k] - d[k] * dg) / nrm;
+        g_m[k] += gv;
+        if (part != NULL) part[12 + k] += gv;
+      }
     }
     for (k = 0; k < 3; ++k) g_means[3 * i + k] = g_m[k];
     /* Sig = Mm Mm^T */
@@ -732,6 +779,59 @@ int FN(gso_preprocess_bwd)(int64_t n, int K, int deg, const REAL* means, const R
     qd = ((p.qn[0] * gq[0] + p.qn[1] * gq[1]) + p.qn[2] * gq[2]) + p.qn[3] * gq[3];
     for (k = 0; k < 4; ++k) g_quats[4 * i + k] = (gq[k] - p.qn[k] * qd) / p.qnorm;
   }
+}
+
+/* Reverse-mode derivative of gso_preprocess w.r.t. means, scales, quaternions and
+ * sh_coeffs (outputs overwritten). */
+int FN(gso_preprocess_bwd)(int64_t n, int K, int deg, const REAL* means, const REAL* scales, const REAL* quats,
+                           const REAL* sh, const REAL* w2c, REAL fx, REAL fy, const REAL* g_means2d,
+                           const REAL* g_cov2d, const REAL* g_colors, REAL* g_means, REAL* g_scales, REAL* g_quats,
+                           REAL* g_sh) {
+  int64_t i;
+#pragma omp parallel for schedule(static)
+  for (i = 0; i < n; ++i)
+    FN(pre_bwd_one)(i, K, deg, means, scales, quats, sh, w2c, fx, fy, g_means2d, g_cov2d, g_colors, g_means,
+                    g_scales, g_quats, g_sh, NULL);
+  return 0;
+}
+
+/* gso_preprocess_bwd plus the W2C cotangent g_w2c[4][4] (row 3 zero: projection.py:27
+ * keeps the first three rows of [m, 1] @ W2C^T): the per-Gaussian shares summed per
+ * thread, the threads in order, then the camera centre's share
+ * (centre = -R^T t, camera.py:15-21: dR[a][b] += t[a] S[b], dt[a] += sum_b R[a][b] S[b],
+ * S = the summed view-vector cotangent). */
+int FN(gso_preprocess_bwd_w2c)(int64_t n, int K, int deg, const REAL* means, const REAL* scales,
+                               const REAL* quats, const REAL* sh, const REAL* w2c, REAL fx, REAL fy,
+                               const REAL* g_means2d, const REAL* g_cov2d, const REAL* g_colors, REAL* g_means,
+                               REAL* g_scales, REAL* g_quats, REAL* g_sh, REAL* g_w2c) {
+  const int nt = omp_get_max_threads();
+  REAL* acc = (REAL*)calloc((size_t)nt * 16, sizeof(REAL));
+  REAL tot[15];
+  int a, b, t;
+  if (acc == NULL) return 1;
+#pragma omp parallel num_threads(nt)
+  {
+    REAL* mine = acc + 16 * omp_get_thread_num();
+    int64_t j;
+#pragma omp for schedule(static)
+    for (j = 0; j < n; ++j)
+      FN(pre_bwd_one)(j, K, deg, means, scales, quats, sh, w2c, fx, fy, g_means2d, g_cov2d, g_colors, g_means,
+                      g_scales, g_quats, g_sh, mine);
+  }
+  for (a = 0; a < 15; ++a) {
+    tot[a] = 0;
+    for (t = 0; t < nt; ++t) tot[a] += acc[16 * t + a];
+  }
+  free(acc);
+  for (a = 0; a < 3; ++a) {
+    REAL gt = tot[9 + a];
+    for (b = 0; b < 3; ++b) {
+      g_w2c[4 * a + b] = tot[3 * a + b] + w2c[4 * a + 3] * tot[12 + b];
+      gt += w2c[4 * a + b] * tot[12 + b];
+    }
+    g_w2c[4 * a + 3] = gt;
+  }
+  for (b = 0; b < 4; ++b) g_w2c[12 + b] = 0;
   return 0;
 }
 

@@ -147,6 +147,64 @@ def test_sh_colour_matches_scipy_real_harmonics(deg):
     np.testing.assert_allclose(pre["colors"], want, atol=2e-6)
 
 
+@pytest.mark.parametrize("deg", [0, 1, 2, 3])
+def test_eval_sh_matches_scipy_and_the_render_colour(deg):
+    """oracle.eval_sh (sh.py:25-74 on its own) against scipy's real harmonics on
+    non-normalised directions' unit vectors, and bit-for-bit against the renderer's colour
+    (preprocess: clip(eval_sh + 0.5, 0, 1)) where the clip does not bind."""
+    rng = np.random.default_rng(30 + deg)
+    n = 200
+    d = rng.normal(0, 1, (n, 3))
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    sh = rng.normal(0, 0.2, (n, 16, 3)).astype(F32)
+    got = oracle.eval_sh(deg, sh, d.astype(F32))
+    want = np.zeros((n, 3))
+    k = 0
+    for l in range(deg + 1):
+        for m in range(-l, l + 1):
+            want += _real_sh_no_cs(l, m, d.astype(F32).astype(np.float64))[:, None] * sh[:, k, :].astype(np.float64)
+            k += 1
+    np.testing.assert_allclose(got, want, atol=2e-6)
+    means = (d * 4.0).astype(F32)
+    pre = oracle.preprocess(means, np.zeros((n, 3), F32), np.tile(np.array([[1, 0, 0, 0]], F32), (n, 1)), sh,
+                            np.eye(4), 64, 64, F32(50), F32(50), F32(32), F32(32), deg)
+    dirs = means / np.linalg.norm(means.astype(F32), axis=1, keepdims=True).astype(F32)
+    col = oracle.eval_sh(deg, sh, dirs) + F32(0.5)
+    inside = (col > 0) & (col < 1)
+    assert inside.mean() > 0.9
+    np.testing.assert_array_equal(pre["colors"][inside], col[inside])
+
+
+@pytest.mark.parametrize("deg", [1, 2, 3])
+def test_eval_sh_vjp_matches_finite_differences(deg):
+    """Both cotangents of the float64 eval_sh against central differences, with K = 16 >
+    (deg+1)^2 coefficients (the unused ones get 0)."""
+    rng = np.random.default_rng(40 + deg)
+    n = 6
+    d = rng.normal(0, 1, (n, 3))
+    sh = rng.normal(0, 0.3, (n, 16, 3))
+    g = rng.normal(0, 1, (n, 3))
+    g_sh, g_d = oracle.eval_sh_vjp(deg, sh, d, g, dtype=np.float64)
+    eps = 1e-6
+
+    def loss(shp, dp):
+        return float((oracle.eval_sh(deg, shp, dp, dtype=np.float64) * g).sum())
+
+    for idx in np.ndindex(sh.shape):
+        a, b = sh.copy(), sh.copy()
+        a[idx] += eps
+        b[idx] -= eps
+        fd = (loss(a, d) - loss(b, d)) / (2 * eps)
+        assert abs(fd - g_sh[idx]) <= 1e-7 + 1e-6 * abs(fd), (idx, fd, g_sh[idx])
+    for idx in np.ndindex(d.shape):
+        a, b = d.copy(), d.copy()
+        a[idx] += eps
+        b[idx] -= eps
+        fd = (loss(sh, a) - loss(sh, b)) / (2 * eps)
+        assert abs(fd - g_d[idx]) <= 1e-7 + 1e-6 * abs(fd), (idx, fd, g_d[idx])
+    assert np.all(g_sh[:, (deg + 1) ** 2:] == 0)
+
+
 # ---------------------------------------------------------------- binning
 def test_ka2_tile_interactions():
     st, sg, n = oracle.tile_interactions(np.array([[16, 16], [0, 0]], F32), np.array([4, 2], F32),
@@ -359,6 +417,42 @@ def test_backward_matches_finite_differences(seed):
     rng = np.random.default_rng(100 + seed)
     seed_img = rng.normal(0, 1, (cam["H"], cam["W"], 3))
     _fd_check(params, cam, deg, seed_img)
+
+
+def _oblique_w2c():
+    """A rotation by 0.2 rad about an oblique axis (Rodrigues) and a translation, so that
+    every entry of W2C's first three rows enters the projection."""
+    ax = np.array([0.3, -0.5, 0.8])
+    ax /= np.linalg.norm(ax)
+    Kx = np.array([[0, -ax[2], ax[1]], [ax[2], 0, -ax[0]], [-ax[1], ax[0], 0]])
+    w = np.eye(4)
+    w[:3, :3] = np.eye(3) + math.sin(0.2) * Kx + (1 - math.cos(0.2)) * Kx @ Kx
+    w[:3, 3] = [0.1, -0.05, 0.3]
+    return w
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_w2c_cotangent_matches_finite_differences(seed):
+    """dL/dW2C of the float64 oracle (projection.py:26-57 through the camera-space mean and
+    W_rot, renderer.py:40-41 and camera.py:15-21 through the view direction) against
+    central differences of the rendered loss in all 16 entries (row 3 never enters)."""
+    params, cam, deg = _tiny_scene(seed)
+    cam = dict(cam, W2C=_oblique_w2c())
+    seed_img = np.random.default_rng(200 + seed).normal(0, 1, (cam["H"], cam["W"], 3))
+    _, _, res = oracle.render(params, cam, sh_degree=deg, dtype=np.float64)
+    g = oracle.render_vjp(params, cam, res, seed_img, sh_degree=deg, dtype=np.float64)["W2C"]
+    eps = 1e-6
+    for a in range(4):
+        for b in range(4):
+            lv = []
+            for sgn in (1, -1):
+                w = cam["W2C"].copy()
+                w[a, b] += sgn * eps
+                im, _, _ = oracle.render(params, dict(cam, W2C=w), sh_degree=deg, dtype=np.float64)
+                lv.append(float((im * seed_img).sum()))
+            fd = (lv[0] - lv[1]) / (2 * eps)
+            assert abs(fd - g[a, b]) <= 1e-5 * max(1.0, abs(fd)) + 1e-7, (a, b, fd, g[a, b])
+    assert np.all(g[3] == 0) and np.abs(g[:3]).min() > 0
 
 
 def test_float32_backward_close_to_float64():
