@@ -75,7 +75,7 @@ const char* gs_last_error(void);
  * clear_records, gs_composite_bwd accumulate.  5: gs_composite_fwd takes window_rule.
  * 6: gs_composite_fwd/bwd take a gs_window_t in place of window_rule; gs_window_from_list,
  * gs_window_from_bins; GS_STAT_WINDOW_CLAMPED.  7: gs_preprocess_bwd_w2c, gs_eval_sh,
- * gs_eval_sh_bwd. */
+ * gs_eval_sh_bwd.  8: gs_l1_ssim_window, gs_l1_ssim_window_bwd. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -319,6 +319,19 @@ int gs_l1_ssim(void* stream, int height, int width, int channels, const float* p
 int gs_l1_ssim_bwd(void* stream, int height, int width, int channels, const float* pred,
                    const float* target, const float* grad_out, const void* workspace,
                    size_t workspace_bytes, float* grad_pred);
+
+/* gs_l1_ssim / gs_l1_ssim_bwd for any window size in [1, 63] and any channel count
+ * (losses.py:16 ssim(..., window_size)): taps exp(-(j - L/2)^2 / 4.5) / sum for j < L and
+ * XLA's 'SAME' correlation, which pads (L-1)/2 before and L/2 after (even L: the window is
+ * off centre).  Workspace: gs_l1_ssim_window_workspace_size bytes (32 B per value); the
+ * backward reads the gradient maps of a forward run with with_grad = 1 on the same
+ * workspace and overwrites the rest of it. */
+size_t gs_l1_ssim_window_workspace_size(int height, int width, int channels, int window_size);
+int gs_l1_ssim_window(void* stream, int height, int width, int channels, int window_size, const float* pred,
+                      const float* target, float* out, int with_grad, void* workspace, size_t workspace_bytes);
+int gs_l1_ssim_window_bwd(void* stream, int height, int width, int channels, int window_size, const float* pred,
+                          const float* target, const float* grad_out, void* workspace, size_t workspace_bytes,
+                          float* grad_pred);
 
 /* The trainer's loss from gs_l1_ssim's out[2] (trainer.py:18-26): terms[0] = d_ssim =
  * max(0, (1 - ssim) / 2) (losses.py:70-75), terms[1] = (1 - lambda) l1 + lambda d_ssim,

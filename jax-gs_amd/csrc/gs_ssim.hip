@@ -311,6 +311,166 @@ __global__ void l1_ssim_terms_kernel(const float* __restrict__ l1_ssim, float la
   terms[4] = 1.0f - d * 2.0f;
 }
 
+// ---------------------------------------------------------------------------------
+// Any window size (losses.py:16 window_size; the trainer uses 11, served above).  The
+// taps are w_j = exp(-(j - L/2)^2 / 4.5) / sum for j < L (x = arange(L) - L//2), and
+// XLA's 'SAME' correlation pads (L - 1) / 2 before and L / 2 after, so output i reads
+// input i + j - lo with lo = (L - 1) / 2 (for even L the window is not centred).  Planes
+// are channel-planar [C][H][W] in the workspace: V (5 vertical blurs), then G (the 3
+// gradient maps, as in the 11-tap path); one thread per value, the reads of a pass hit the
+// cache.  The backward applies the adjoint correlation, in_s = sum_j w_j out_{s - j + lo},
+// to G along W and then H (the two passes act on different axes and commute).
+constexpr int kMaxTaps = 63;
+struct TapsAny {
+  float w[kMaxTaps];
+  int L, lo;
+};
+
+// vertical blur of x, y, x^2, y^2, x y; x, y interleaved [H][W][C]
+__global__ __launch_bounds__(256) void ssim_any_vblur_kernel(int H, int W, int C, const float* __restrict__ x,
+                                                             const float* __restrict__ y, TapsAny t,
+                                                             float* __restrict__ V) {
+  const int64_t n = (int64_t)H * W * C;
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= n) return;
+  const int col = (int)(q % W), r = (int)((q / W) % H), ch = (int)(q / ((int64_t)W * H));
+  float a[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  for (int j = 0; j < t.L; ++j) {
+    const int rr = r + j - t.lo;
+    if (rr < 0 || rr >= H) continue;
+    const int64_t o = ((int64_t)rr * W + col) * C + ch;
+    const float xv = x[o], yv = y[o];
+    a[0] = fmaf(t.w[j], xv, a[0]);
+    a[1] = fmaf(t.w[j], yv, a[1]);
+    a[2] = fmaf(t.w[j], xv * xv, a[2]);
+    a[3] = fmaf(t.w[j], yv * yv, a[3]);
+    a[4] = fmaf(t.w[j], xv * yv, a[4]);
+  }
+#pragma unroll
+  for (int m = 0; m < 5; ++m) V[m * n + q] = a[m];
+}
+
+// horizontal blur, the map, |x - y|, per-workgroup sums and (G != NULL) the gradient maps
+__global__ __launch_bounds__(256) void ssim_any_map_kernel(int H, int W, int C, const float* __restrict__ x,
+                                                           const float* __restrict__ y, TapsAny t,
+                                                           const float* __restrict__ V, float inv_count,
+                                                           float* __restrict__ G, float2* __restrict__ partial) {
+  __shared__ float red[4];
+  const int64_t n = (int64_t)H * W * C;
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  float l1v = 0.0f, ssv = 0.0f;
+  if (q < n) {
+    const int col = (int)(q % W), r = (int)((q / W) % H), ch = (int)(q / ((int64_t)W * H));
+    float b[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < t.L; ++j) {
+      const int cc = col + j - t.lo;
+      if (cc < 0 || cc >= W) continue;
+#pragma unroll
+      for (int m = 0; m < 5; ++m) b[m] = fmaf(t.w[j], V[m * n + q - col + cc], b[m]);
+    }
+    const float mu1 = b[0], mu2 = b[1];
+    const float m11 = mu1 * mu1, m22 = mu2 * mu2, m12 = mu1 * mu2;
+    const float d11 = b[2] - m11;
+    const float s11 = fmaxf(0.0f, d11), s22 = fmaxf(0.0f, b[3] - m22);
+    const float s12 = b[4] - m12;
+    const float A = 2.0f * m12 + kC1, B = 2.0f * s12 + kC2;
+    const float Cc = (m11 + m22) + kC1, D = (s11 + s22) + kC2;
+    const float num = A * B, den = Cc * D;
+    const float raw = num / den;
+    ssv = fminf(1.0f, fmaxf(-1.0f, raw));
+    const int64_t p = ((int64_t)r * W + col) * C + ch;
+    l1v = fabsf(x[p] - y[p]);
+    if (G != nullptr) {
+      const float Gc = inv_count * (tie_step(raw + 1.0f) * tie_step(1.0f - raw));
+      const float dnum = Gc / den, dden = -(Gc * raw) / den;
+      const float dA = dnum * B, dB = dnum * A, dCc = dden * D, dD = dden * Cc;
+      const float de12 = 2.0f * dB;
+      const float dm12 = 2.0f * dA - de12;
+      const float de11 = dD * tie_step(d11);
+      const float dm11 = dCc - de11;
+      G[q] = 2.0f * mu1 * dm11 + mu2 * dm12;
+      G[n + q] = de11;
+      G[2 * n + q] = de12;
+    }
+  }
+  const float l1s = block_sum256(l1v, red);
+  const float sss = block_sum256(ssv, red);
+  if (threadIdx.x == 0) partial[blockIdx.x] = make_float2(l1s, sss);
+}
+
+// adjoint correlation of the 3 gradient maps along W
+__global__ __launch_bounds__(256) void ssim_any_hadj_kernel(int H, int W, int C, TapsAny t,
+                                                            const float* __restrict__ G, float* __restrict__ U) {
+  const int64_t n = (int64_t)H * W * C;
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= n) return;
+  const int col = (int)(q % W);
+  float a[3] = {0.0f, 0.0f, 0.0f};
+  for (int j = 0; j < t.L; ++j) {
+    const int cc = col - j + t.lo;
+    if (cc < 0 || cc >= W) continue;
+#pragma unroll
+    for (int m = 0; m < 3; ++m) a[m] = fmaf(t.w[j], G[m * n + q - col + cc], a[m]);
+  }
+#pragma unroll
+  for (int m = 0; m < 3; ++m) U[m * n + q] = a[m];
+}
+
+// adjoint along H, then dL/dx = g_ssim (B0 + 2 x B1 + y B2) + g_l1 sign(x - y) / count
+__global__ __launch_bounds__(256) void ssim_any_grad_kernel(int H, int W, int C, const float* __restrict__ x,
+                                                            const float* __restrict__ y, TapsAny t,
+                                                            const float* __restrict__ U, float inv_count,
+                                                            const float* __restrict__ grad_out,
+                                                            float* __restrict__ grad) {
+  const int64_t n = (int64_t)H * W * C;
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= n) return;
+  const int col = (int)(q % W), r = (int)((q / W) % H), ch = (int)(q / ((int64_t)W * H));
+  float b[3] = {0.0f, 0.0f, 0.0f};
+  for (int j = 0; j < t.L; ++j) {
+    const int rr = r - j + t.lo;
+    if (rr < 0 || rr >= H) continue;
+#pragma unroll
+    for (int m = 0; m < 3; ++m) b[m] = fmaf(t.w[j], U[m * n + q + (int64_t)(rr - r) * W], b[m]);
+  }
+  const int64_t p = ((int64_t)r * W + col) * C + ch;
+  const float xv = x[p], yv = y[p], d = xv - yv;
+  const float sg = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f);
+  const float gs = b[0] + 2.0f * xv * b[1] + yv * b[2];
+  grad[p] = grad_out[1] * gs + (grad_out[0] * inv_count) * sg;
+}
+
+TapsAny make_taps_any(int L) {
+  TapsAny t;
+  double s = 0.0, e[kMaxTaps];
+  for (int j = 0; j < L; ++j) {
+    const double d = (double)(j - L / 2);
+    e[j] = std::exp(-d * d / (2.0 * 1.5 * 1.5));
+    s += e[j];
+  }
+  for (int j = 0; j < kMaxTaps; ++j) t.w[j] = j < L ? (float)(e[j] / s) : 0.0f;
+  t.L = L;
+  t.lo = (L - 1) / 2;
+  return t;
+}
+
+struct AnyLayout {
+  int64_t count;
+  int nblk;
+  size_t v_off, g_off, part_off, total;
+};
+
+AnyLayout any_layout(int H, int W, int C) {
+  AnyLayout A;
+  A.count = (int64_t)H * W * C;
+  A.nblk = div_up(A.count, 256);
+  A.v_off = 0;
+  A.g_off = ((size_t)5 * A.count * sizeof(float) + 255) & ~(size_t)255;
+  A.part_off = A.g_off + (((size_t)3 * A.count * sizeof(float) + 255) & ~(size_t)255);
+  A.total = A.part_off + (size_t)A.nblk * sizeof(float2);
+  return A;
+}
+
 Taps make_taps() {
   Taps t;
   double s = 0.0, e[kSTaps];
@@ -410,5 +570,65 @@ extern "C" int gs_l1_ssim_terms(void* stream, const float* l1_ssim, double lambd
   hipLaunchKernelGGL(l1_ssim_terms_kernel, dim3(1), dim3(1), 0, (hipStream_t)stream, l1_ssim, (float)lambda_ssim,
                      (float)(1.0 - lambda_ssim), terms);
   GS_LAUNCH_CHECK("l1_ssim_terms_kernel");
+  return GS_OK;
+}
+
+extern "C" size_t gs_l1_ssim_window_workspace_size(int height, int width, int channels, int window_size) {
+  if (height <= 0 || width <= 0 || channels <= 0 || window_size < 1 || window_size > kMaxTaps) return 0;
+  return any_layout(height, width, channels).total;
+}
+
+extern "C" int gs_l1_ssim_window(void* stream, int height, int width, int channels, int window_size,
+                                 const float* pred, const float* target, float* out, int with_grad, void* workspace,
+                                 size_t workspace_bytes) {
+  GS_REQUIRE(height > 0 && width > 0 && channels > 0, "gs_l1_ssim_window: bad image shape %dx%dx%d", height, width,
+             channels);
+  GS_REQUIRE(window_size >= 1 && window_size <= kMaxTaps, "gs_l1_ssim_window: window_size must be in [1, %d] (got %d)",
+             kMaxTaps, window_size);
+  GS_REQUIRE(pred && target && out && workspace, "gs_l1_ssim_window: NULL argument");
+  GS_REQUIRE(5 * (int64_t)height * width * channels < ((int64_t)1 << 40), "gs_l1_ssim_window: image too large");
+  const AnyLayout A = any_layout(height, width, channels);
+  GS_REQUIRE(workspace_bytes >= A.total, "gs_l1_ssim_window: workspace of %zu bytes, %zu needed", workspace_bytes,
+             A.total);
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  const TapsAny t = make_taps_any(window_size);
+  const float inv = (float)(1.0 / (double)A.count);
+  float* V = (float*)(ws + A.v_off);
+  float* G = with_grad ? (float*)(ws + A.g_off) : nullptr;
+  float2* part = (float2*)(ws + A.part_off);
+  hipLaunchKernelGGL(ssim_any_vblur_kernel, dim3(A.nblk), dim3(256), 0, s, height, width, channels, pred, target, t,
+                     V);
+  GS_LAUNCH_CHECK("ssim_any_vblur_kernel");
+  hipLaunchKernelGGL(ssim_any_map_kernel, dim3(A.nblk), dim3(256), 0, s, height, width, channels, pred, target, t,
+                     (const float*)V, inv, G, part);
+  GS_LAUNCH_CHECK("ssim_any_map_kernel");
+  hipLaunchKernelGGL(l1_ssim_sum_kernel, dim3(1), dim3(1024), 0, s, (const float2*)part, A.nblk, inv, out);
+  GS_LAUNCH_CHECK("l1_ssim_sum_kernel");
+  return GS_OK;
+}
+
+extern "C" int gs_l1_ssim_window_bwd(void* stream, int height, int width, int channels, int window_size,
+                                     const float* pred, const float* target, const float* grad_out, void* workspace,
+                                     size_t workspace_bytes, float* grad_pred) {
+  GS_REQUIRE(height > 0 && width > 0 && channels > 0, "gs_l1_ssim_window_bwd: bad image shape %dx%dx%d", height,
+             width, channels);
+  GS_REQUIRE(window_size >= 1 && window_size <= kMaxTaps,
+             "gs_l1_ssim_window_bwd: window_size must be in [1, %d] (got %d)", kMaxTaps, window_size);
+  GS_REQUIRE(pred && target && grad_out && workspace && grad_pred, "gs_l1_ssim_window_bwd: NULL argument");
+  const AnyLayout A = any_layout(height, width, channels);
+  GS_REQUIRE(workspace_bytes >= A.total, "gs_l1_ssim_window_bwd: workspace of %zu bytes, %zu needed",
+             workspace_bytes, A.total);
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  const TapsAny t = make_taps_any(window_size);
+  const float inv = (float)(1.0 / (double)A.count);
+  const float* G = (const float*)(ws + A.g_off);
+  float* U = (float*)(ws + A.v_off);  // the forward's vertical blurs are dead by now
+  hipLaunchKernelGGL(ssim_any_hadj_kernel, dim3(A.nblk), dim3(256), 0, s, height, width, channels, t, G, U);
+  GS_LAUNCH_CHECK("ssim_any_hadj_kernel");
+  hipLaunchKernelGGL(ssim_any_grad_kernel, dim3(A.nblk), dim3(256), 0, s, height, width, channels, pred, target, t,
+                     (const float*)U, inv, grad_out, grad_pred);
+  GS_LAUNCH_CHECK("ssim_any_grad_kernel");
   return GS_OK;
 }

@@ -58,6 +58,9 @@ _SIGS = {
     "gs_l1_ssim_workspace_size": [_I, _I, _I],
     "gs_l1_ssim": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _SZ],
     "gs_l1_ssim_bwd": [_P, _I, _I, _I, _P, _P, _P, _P, _SZ, _P],
+    "gs_l1_ssim_window_workspace_size": [_I, _I, _I, _I],
+    "gs_l1_ssim_window": [_P, _I, _I, _I, _I, _P, _P, _P, _I, _P, _SZ],
+    "gs_l1_ssim_window_bwd": [_P, _I, _I, _I, _I, _P, _P, _P, _P, _SZ, _P],
     "gs_densify_workspace_size": [_I64],
     "gs_densify_and_prune": [_P, _I64, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, ctypes.c_double,
                              ctypes.c_double, ctypes.c_double, ctypes.c_double, _P, _SZ, _P],
@@ -73,12 +76,13 @@ _SIGS = {
 }
 _RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_l1_ssim_workspace_size": _SZ,
             "gs_bin_reference_workspace_size": _SZ, "gs_preprocess_bwd_w2c_workspace_size": _SZ,
+            "gs_l1_ssim_window_workspace_size": _SZ,
             "gs_densify_workspace_size": _SZ}
 
 _lib = None
 
 
-ABI_VERSION = 7  # gs_abi_version() of the signatures bound below
+ABI_VERSION = 8  # gs_abi_version() of the signatures bound below
 
 
 class NativeLibraryMissing(RuntimeError):

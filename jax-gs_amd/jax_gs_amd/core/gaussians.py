@@ -33,14 +33,18 @@ class Gaussians:
 def init_gaussians_from_pcd(points: torch.Tensor, colors: torch.Tensor) -> Gaussians:
     """Point-cloud initialiser with the reference's conventions (gaussians.py:13-56):
     log-scale -3, identity rotation, opacity logit 0, SH DC = (c - 0.5) / C0, 16 coefficients.
-    (The reference's random recolouring of all-black clouds uses JAX's PRNG and is not
-    reproduced; such inputs raise.)"""
+    A cloud whose largest colour value is below 1e-3 gets uniform random colours in
+    [0.1, 0.9) (gaussians.py:40-42), decided on the device; the draw comes from torch's
+    generator seeded 42 where the reference uses jax.random with PRNGKey(42), so the
+    distribution matches and the values do not."""
     points = torch.as_tensor(points, dtype=torch.float32)
     colors = torch.as_tensor(colors, dtype=torch.float32, device=points.device)
-    if float(colors.max()) < 1e-3:
-        raise ValueError("init_gaussians_from_pcd: colours are all ~0 (reference recolours them with JAX's PRNG)")
     n = points.shape[0]
     dev = points.device
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(42)
+    rand = torch.rand(colors.shape, generator=gen, device=dev, dtype=torch.float32) * 0.8 + 0.1
+    colors = torch.where(colors.max() < 1e-3, rand, colors) if colors.numel() else colors
     sh = torch.zeros((n, 16, 3), dtype=torch.float32, device=dev)
     sh[:, 0, :] = (colors - 0.5) / SH_C0
     quats = torch.zeros((n, 4), dtype=torch.float32, device=dev)

@@ -56,19 +56,31 @@ def mse_loss(pred: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
 
 
 class _L1SSIM(torch.autograd.Function):
+    """window 11 with at most 4 channels: the tiled kernels (gs_l1_ssim); any other window
+    size or channel count: gs_l1_ssim_window."""
+
     @staticmethod
-    def forward(ctx, pred, target):
+    def forward(ctx, pred, target, window_size):
         pred = pred.contiguous()
         target = target.contiguous()
         H, W, C = pred.shape
         dev = pred.device
-        nbytes = _lib.lib().gs_l1_ssim_workspace_size(H, W, C)
+        fast = window_size == 11 and C <= 4
+        if fast:
+            nbytes = _lib.lib().gs_l1_ssim_workspace_size(H, W, C)
+        else:
+            nbytes = _lib.lib().gs_l1_ssim_window_workspace_size(H, W, C, window_size)
         ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
         out = torch.empty((2,), dtype=torch.float32, device=dev)
         grad_needed = ctx.needs_input_grad[0]
-        _lib.call("gs_l1_ssim", _lib.stream_handle(dev), H, W, C, _lib.ptr(pred), _lib.ptr(target), _lib.ptr(out),
-                  int(grad_needed), _lib.ptr(ws), nbytes)
+        if fast:
+            _lib.call("gs_l1_ssim", _lib.stream_handle(dev), H, W, C, _lib.ptr(pred), _lib.ptr(target),
+                      _lib.ptr(out), int(grad_needed), _lib.ptr(ws), nbytes)
+        else:
+            _lib.call("gs_l1_ssim_window", _lib.stream_handle(dev), H, W, C, int(window_size), _lib.ptr(pred),
+                      _lib.ptr(target), _lib.ptr(out), int(grad_needed), _lib.ptr(ws), nbytes)
         ctx.set_materialize_grads(False)
+        ctx.window = None if fast else int(window_size)
         if grad_needed:
             ctx.save_for_backward(pred, target, ws)
         return out[0], out[1]
@@ -82,26 +94,31 @@ class _L1SSIM(torch.autograd.Function):
                             zero if g_ssim is None else g_ssim.to(torch.float32)])
         H, W, C = pred.shape
         grad = torch.empty_like(pred)
-        _lib.call("gs_l1_ssim_bwd", _lib.stream_handle(dev), H, W, C, _lib.ptr(pred), _lib.ptr(target),
-                  _lib.ptr(gout), _lib.ptr(ws), ws.numel(), _lib.ptr(grad))
-        return grad, None
+        if ctx.window is None:
+            _lib.call("gs_l1_ssim_bwd", _lib.stream_handle(dev), H, W, C, _lib.ptr(pred), _lib.ptr(target),
+                      _lib.ptr(gout), _lib.ptr(ws), ws.numel(), _lib.ptr(grad))
+        else:
+            _lib.call("gs_l1_ssim_window_bwd", _lib.stream_handle(dev), H, W, C, ctx.window, _lib.ptr(pred),
+                      _lib.ptr(target), _lib.ptr(gout), _lib.ptr(ws), ws.numel(), _lib.ptr(grad))
+        return grad, None, None
 
 
-def l1_and_ssim(pred: torch.Tensor, target: torch.Tensor):
-    """(mean |pred - target|, mean SSIM) of [H, W, C] images from one forward kernel."""
+def l1_and_ssim(pred: torch.Tensor, target: torch.Tensor, window_size: int = 11):
+    """(mean |pred - target|, mean SSIM) of [H, W, C] images from one forward kernel;
+    window_size in [1, 63] (losses.py:16)."""
     _check("ssim", pred, target)
     if pred.dim() != 3:
         raise ValueError("ssim: images must be [H, W, C]")
-    return _L1SSIM.apply(pred, target)
+    if not 1 <= int(window_size) <= 63:
+        raise ValueError(f"ssim: window_size must be in [1, 63] (got {window_size})")
+    return _L1SSIM.apply(pred, target, int(window_size))
 
 
 def ssim(img1: torch.Tensor, img2: torch.Tensor, window_size: int = 11, size_average: bool = True) -> torch.Tensor:
-    """losses.py:16-68: mean SSIM with an 11-tap Gaussian window (sigma 1.5).  The
+    """losses.py:16-68: mean SSIM with a window_size-tap Gaussian window (sigma 1.5).  The
     reference's size_average=False also reduces over every axis of an [H, W, C] map."""
-    if window_size != 11:
-        raise ValueError("ssim: only the reference's 11-tap window is implemented")
     del size_average
-    return l1_and_ssim(img1, img2)[1]
+    return l1_and_ssim(img1, img2, window_size)[1]
 
 
 def _d_ssim(s: torch.Tensor) -> torch.Tensor:

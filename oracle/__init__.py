@@ -313,27 +313,36 @@ def ssim_window(size=11, sigma=1.5, dtype=np.float32):
     return (k / k.sum(dtype=dtype)).astype(dtype)
 
 
-def ssim_blur(img, w):
+def ssim_blur(img, w, adjoint=False):
     """losses.py:35-47: depthwise correlation with w along H, then along W, each with
-    'SAME' zero padding (len(w)//2 on both sides).  img is [H, W, C]."""
+    XLA's 'SAME' zero padding: (L-1)//2 before and L//2 after for L = len(w) taps, so
+    output i reads input i + k - (L-1)//2.  img is [H, W, C].  adjoint=True applies the
+    transposed operator (the correlation with the reversed taps and swapped padding; for
+    odd L, the same blur)."""
     H, W = img.shape[:2]
-    r = len(w) // 2
+    L = len(w)
+    lo = (L - 1) // 2
+    if adjoint:
+        w = w[::-1]
+        lo = L - 1 - lo
+    hi = L - 1 - lo
     dt = img.dtype
-    p = np.zeros((H + 2 * r,) + img.shape[1:], dt)
-    p[r:r + H] = img
+    p = np.zeros((H + L - 1,) + img.shape[1:], dt)
+    p[lo:lo + H] = img
     v = np.zeros_like(img)
-    for k in range(len(w)):
+    for k in range(L):
         v = v + w[k] * p[k:k + H]
-    p = np.zeros((H, W + 2 * r) + img.shape[2:], dt)
-    p[:, r:r + W] = v
+    p = np.zeros((H, W + L - 1) + img.shape[2:], dt)
+    p[:, lo:lo + W] = v
     out = np.zeros_like(img)
-    for k in range(len(w)):
+    for k in range(L):
         out = out + w[k] * p[:, k:k + W]
+    del hi
     return out
 
 
-def _ssim_parts(img1, img2, dtype):
-    w = ssim_window(dtype=dtype)
+def _ssim_parts(img1, img2, dtype, window_size=11):
+    w = ssim_window(window_size, dtype=dtype)
     x = np.asarray(img1, dtype)
     y = np.asarray(img2, dtype)
     mu1, mu2 = ssim_blur(x, w), ssim_blur(y, w)
@@ -349,14 +358,14 @@ def _ssim_parts(img1, img2, dtype):
     return dict(w=w, x=x, y=y, mu1=mu1, mu2=mu2, d11=d11, A=A, B=B, Cc=Cc, D=D, raw=raw)
 
 
-def ssim_map(img1, img2, dtype=np.float64):
+def ssim_map(img1, img2, dtype=np.float64, window_size=11):
     """losses.py:49-64: the clipped per-value SSIM map [H, W, C]."""
-    return np.clip(_ssim_parts(img1, img2, dtype)["raw"], -1.0, 1.0)
+    return np.clip(_ssim_parts(img1, img2, dtype, window_size)["raw"], -1.0, 1.0)
 
 
-def ssim(img1, img2, dtype=np.float64):
+def ssim(img1, img2, dtype=np.float64, window_size=11):
     """losses.py:16-68 (size_average): mean of the clipped SSIM map."""
-    return ssim_map(img1, img2, dtype).astype(np.float64).mean()
+    return ssim_map(img1, img2, dtype, window_size).astype(np.float64).mean()
 
 
 def d_ssim_loss(pred, target, dtype=np.float64):
@@ -369,12 +378,11 @@ def _tie_grad(z):
     return np.where(z > 0, 1.0, np.where(z == 0, 0.5, 0.0))
 
 
-def ssim_vjp(img1, img2, g_ssim, dtype=np.float64):
+def ssim_vjp(img1, img2, g_ssim, dtype=np.float64, window_size=11):
     """Cotangent of img1 for the mean SSIM given its cotangent g_ssim: reverse-mode AD
     of losses.py:49-68 written out by hand.  Ties of max/clip pass half the cotangent
-    (lax.max/min).  The blur is a correlation with a symmetric kernel and zero
-    padding, so its adjoint is the same blur."""
-    P = _ssim_parts(img1, img2, dtype)
+    (lax.max/min).  The blur's adjoint is ssim_blur(..., adjoint=True)."""
+    P = _ssim_parts(img1, img2, dtype, window_size)
     raw, A, B, Cc, D = P["raw"], P["A"], P["B"], P["Cc"], P["D"]
     # clip(raw, -1, 1) = minimum(1, maximum(-1, raw))
     clip_d = _tie_grad(raw + 1.0) * _tie_grad(1.0 - raw)
@@ -388,7 +396,8 @@ def ssim_vjp(img1, img2, g_ssim, dtype=np.float64):
     dm11 = dCc - de11
     dmu1 = dtype(2) * P["mu1"] * dm11 + P["mu2"] * dm12    # m11 = mu1^2, m12 = mu1 mu2
     w = P["w"]
-    return ssim_blur(dmu1, w) + dtype(2) * P["x"] * ssim_blur(de11, w) + P["y"] * ssim_blur(de12, w)
+    return (ssim_blur(dmu1, w, True) + dtype(2) * P["x"] * ssim_blur(de11, w, True)
+            + P["y"] * ssim_blur(de12, w, True))
 
 
 def d_ssim_vjp(pred, target, g, dtype=np.float64):

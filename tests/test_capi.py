@@ -32,7 +32,7 @@ def test_binding_covers_every_declared_symbol():
 
 def test_abi_version_and_workspace_query_without_gpu():
     L = _lib.lib()
-    assert L.gs_abi_version() == _lib.ABI_VERSION == 7
+    assert L.gs_abi_version() == _lib.ABI_VERSION == 8
     # size query: pure host arithmetic, grows with the number of Gaussians
     a = L.gs_bin_workspace_size(1000, 64, 64, 0)
     b = L.gs_bin_workspace_size(100000, 64, 64, 0)
@@ -58,3 +58,28 @@ def test_load_ply_missing_file():
 
     with pytest.raises(FileNotFoundError):
         load_ply("non_existent_file.ply")
+
+
+def test_init_from_pcd_conventions_and_black_cloud_recolour():
+    """gaussians.py:13-56 on the CPU (host logic): log-scale -3, identity rotation, logit 0,
+    SH DC (c - 0.5) / C0 and zeros elsewhere; a cloud whose colours are all below 1e-3 gets
+    uniform colours in [0.1, 0.9) (gaussians.py:40-42), the same draw on every call, and a
+    coloured cloud keeps its colours."""
+    import torch
+
+    from jax_gs_amd import init_gaussians_from_pcd
+
+    pts = torch.arange(30, dtype=torch.float32).reshape(10, 3)
+    col = torch.linspace(0.0, 1.0, 30).reshape(10, 3)
+    g = init_gaussians_from_pcd(pts, col)
+    assert torch.equal(g.means, pts) and torch.all(g.scales == -3.0) and torch.all(g.opacities == 0.0)
+    assert torch.all(g.quaternions[:, 0] == 1.0) and torch.all(g.quaternions[:, 1:] == 0.0)
+    assert torch.allclose(g.sh_coeffs[:, 0, :], (col - 0.5) / 0.28209479177387814)
+    assert g.sh_coeffs.shape == (10, 16, 3) and torch.all(g.sh_coeffs[:, 1:] == 0.0)
+    black = torch.full((1000, 3), 5e-4)
+    g1 = init_gaussians_from_pcd(torch.zeros(1000, 3), black)
+    g2 = init_gaussians_from_pcd(torch.zeros(1000, 3), black)
+    c = g1.sh_coeffs[:, 0, :] * 0.28209479177387814 + 0.5
+    assert float(c.min()) >= 0.1 - 1e-6 and float(c.max()) < 0.9 + 1e-6
+    assert 0.45 < float(c.mean()) < 0.55 and float(c.std()) > 0.2
+    assert torch.equal(g1.sh_coeffs, g2.sh_coeffs)

@@ -272,6 +272,30 @@ def test_l1_ssim_parity(cuda, shape):
     assert np.abs(grad - want_g).max() <= 1e-3 * np.abs(want_g).max()
 
 
+@pytest.mark.parametrize("shape,L", [((32, 40, 3), 3), ((33, 29, 3), 4), ((40, 52, 2), 7), ((24, 31, 5), 11),
+                                     ((64, 70, 3), 15), ((18, 20, 1), 1)])
+def test_l1_ssim_any_window_parity(cuda, shape, L):
+    """losses.py:16 ssim(..., window_size) through the module (gs_l1_ssim_window: any
+    window, even ones off centre, any channel count): both means against the float64 oracle
+    and the image gradient of a * l1 + b * ssim against the oracle's VJP."""
+    from jax_gs_amd.training import losses
+
+    rng = np.random.default_rng(7 * L + shape[2])
+    tgt = rng.uniform(0, 1, shape).astype(np.float32)
+    pred = np.clip(tgt + rng.normal(0, 0.2, shape), 0, 1).astype(np.float32)
+    p = torch.from_numpy(pred).to(cuda).requires_grad_(True)
+    l1, ss = losses.l1_and_ssim(p, torch.from_numpy(tgt).to(cuda), window_size=L)
+    want_l1, seed = oracle.l1_loss_and_grad(pred, tgt)
+    want_s = oracle.ssim(pred, tgt, window_size=L)
+    assert abs(float(l1.detach()) - want_l1) <= 1e-6 * want_l1
+    assert abs(float(ss.detach()) - want_s) <= 1e-5
+    a, b = 0.8, -0.1
+    (a * l1 + b * ss).backward()
+    want_g = a * seed.astype(np.float64) + oracle.ssim_vjp(pred, tgt, b, window_size=L)
+    assert _rel(_np(p.grad), want_g) <= 1e-4
+    assert abs(float(losses.ssim(p.detach(), p.detach(), window_size=L)) - 1.0) <= 1e-5
+
+
 def test_ssim_identical_images_and_losses_module(cuda):
     """test_training.py:21-38 through the host module: ssim(t, t) = 1, d_ssim(t, t) = 0,
     bounds, d_ssim = (1 - ssim) / 2, and l1_ssim_loss's total and gradient."""

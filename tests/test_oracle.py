@@ -561,6 +561,49 @@ def test_ssim_blur_matches_scipy():
         np.testing.assert_allclose(got[..., c], convolve2d(img[..., c], np.outer(w, w), mode="same"), atol=1e-13)
 
 
+@pytest.mark.parametrize("L", [1, 4, 7, 10, 15])
+def test_ssim_blur_any_window_is_xla_same_correlation(L):
+    """Any window size: XLA's 'SAME' padding (TensorFlow's documented rule: L - 1 padded
+    values, (L - 1) // 2 of them before) and a 'valid' correlation of the padded image
+    (scipy.signal.correlate), per axis; the adjoint is the transposed matrix."""
+    from scipy.signal import correlate
+
+    rng = np.random.default_rng(L)
+    img = rng.normal(size=(12, 17, 2))
+    w = oracle.ssim_window(L, dtype=np.float64)
+    lo = (L - 1) // 2
+    pad = np.pad(img, ((lo, L - 1 - lo), (lo, L - 1 - lo), (0, 0)))
+    want = np.stack([correlate(pad[..., c], np.outer(w, w), mode="valid") for c in range(2)], -1)
+    np.testing.assert_allclose(oracle.ssim_blur(img, w), want, atol=1e-13)
+    # adjoint: <blur(a), b> = <a, blur^T(b)>
+    b = rng.normal(size=img.shape)
+    lhs = (oracle.ssim_blur(img, w) * b).sum()
+    rhs = (img * oracle.ssim_blur(b, w, adjoint=True)).sum()
+    assert abs(lhs - rhs) <= 1e-12 * abs(lhs)
+
+
+@pytest.mark.parametrize("L", [4, 7])
+def test_ssim_any_window_vjp_and_fixture(L):
+    """The reference's test_training.py:21-38 properties at another window size, and the
+    VJP against central differences (even L: the off-centre window)."""
+    rng = np.random.default_rng(20 + L)
+    target = rng.uniform(0, 1, (16, 18, 3))
+    pred = target + 0.1 * rng.uniform(0, 1, target.shape)
+    s = oracle.ssim(pred, target, window_size=L)
+    assert 0.0 <= s <= 1.0 and np.isclose(oracle.ssim(target, target, window_size=L), 1.0)
+    x = rng.uniform(0, 1, (7, 9, 2))
+    y = rng.uniform(0, 1, (7, 9, 2))
+    g = oracle.ssim_vjp(x, y, 1.0, window_size=L)
+    num = np.zeros_like(x)
+    eps = 1e-6
+    for idx in np.ndindex(x.shape):
+        xp, xm = x.copy(), x.copy()
+        xp[idx] += eps
+        xm[idx] -= eps
+        num[idx] = (oracle.ssim(xp, y, window_size=L) - oracle.ssim(xm, y, window_size=L)) / (2 * eps)
+    assert np.linalg.norm(num - g) / np.linalg.norm(num) < 1e-6
+
+
 def test_ssim_reference_fixture():
     """test_training.py:21-38: bounds, d_ssim = (1 - ssim) / 2, perfect match."""
     rng = np.random.default_rng(0)
