@@ -407,11 +407,16 @@ __global__ __launch_bounds__(256) void pair_upsweep_kernel(const uint64_t* __res
                                                            uint32_t* __restrict__ table) {
   const int64_t n = n_static < (int64_t)*n_dev ? n_static : (int64_t)*n_dev;  // Gaussians with tiles
   constexpr int NB = 1 << kPairRB;
+  // column g of the table: workgroups of one XCD (b mod 8) take a contiguous run of
+  // columns, so each row's cache lines are written by one L2
+  const int per = (G + 7) >> 3;
+  const int g = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (g >= G) return;
   __shared__ uint32_t hist[NB];
   hist[threadIdx.x] = 0;
   __syncthreads();
   static_assert(kPairSpan == 256, "one Gaussian per thread");
-  const int64_t i = (int64_t)blockIdx.x * kPairSpan + threadIdx.x;
+  const int64_t i = (int64_t)g * kPairSpan + threadIdx.x;
   if (i < n) {
     const SBRect b = sb_rect(unpack(words[i]));
     if (b.has)
@@ -419,7 +424,7 @@ __global__ __launch_bounds__(256) void pair_upsweep_kernel(const uint64_t* __res
         for (int sx = b.sx0; sx <= b.sx1; ++sx) atomicAdd(&hist[(uint32_t)(sy * SX + sx) & (NB - 1)], 1u);
   }
   __syncthreads();
-  table[(int64_t)threadIdx.x * G + blockIdx.x] = hist[threadIdx.x];
+  table[(int64_t)threadIdx.x * G + g] = hist[threadIdx.x];
 }
 
 // The chunk and segment maps of the tile pass (chunks_kernel's outputs) computed inside
@@ -1175,7 +1180,8 @@ int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, c
   if (rc != GS_OK) return rc;
   const uint64_t* sorted_word = wa;
   // 3. superblock pairs generated from the depth order, sorted by superblock
-  hipLaunchKernelGGL(pair_upsweep_kernel, dim3(P.G_q), dim3(256), 0, s, sorted_word, n, n_has, P.SX, P.G_q, table);
+  hipLaunchKernelGGL(pair_upsweep_kernel, dim3(div_up(P.G_q, 8) * 8), dim3(256), 0, s, sorted_word, n, n_has, P.SX,
+                     P.G_q, table);
   GS_LAUNCH_CHECK("pair_upsweep_kernel");
   hipLaunchKernelGGL(radix_spine_kernel, dim3(1 << kPairRB), dim3(kScanBlock), 0, s, table, P.G_q, dtot);
   GS_LAUNCH_CHECK("radix_spine_kernel");
