@@ -357,11 +357,15 @@ def measured_valu_busy(stage, config):
     path = os.path.join(PROFILES, f"composite_valu_cfg{config}.md")
     if stage not in kernels or not os.path.exists(path):
         return None, None
+    col = None
     for line in open(path):
-        if line.startswith("| " + kernels[stage] + " |"):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if col is None and "VALU busy %" in cells:
+            col = cells.index("VALU busy %")
+        elif col is not None and cells and cells[0] == kernels[stage]:
             try:
-                return float(line.split("|")[-3].strip()) / 100.0, os.path.relpath(path, _ROOT)
-            except ValueError:
+                return float(cells[col]) / 100.0, os.path.relpath(path, _ROOT)
+            except (ValueError, IndexError):
                 return None, None
     return None, None
 
