@@ -86,9 +86,8 @@ __device__ inline float wave_sum(float v) {
 //           lane + d into their low register, then the others add the high value of
 //           lane - d into the same register;
 //   2:      select the kept and the sent value and add the partner's (quad_perm DPP).
-// The last level (distance 1) is a plain pairwise sum.  Lane l ends with the wave
-// total of value index  b5 + 2 b4 + 4 b3 + 8 b2 + 16 b1  (b_i = bit i of l), the
-// same total in lanes l and l ^ 1.
+// The last level (distance 1) is a plain pairwise sum, so lanes l and l ^ 1 end with the
+// same total.
 __device__ inline float add_swap32(float lo, float hi) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
@@ -142,26 +141,32 @@ __device__ inline void halve_level(float* cur, int lane) {
   }
 }
 
-// Value index whose total lane l holds after reduce_scatter.
-__device__ inline int scatter_index(int l) {
-  return ((l >> 5) & 1) | ((l >> 3) & 2) | ((l >> 1) & 4) | ((l << 1) & 8) | ((l << 3) & 16);
-}
+// The backward's reduce-scatter of two walked entries.  Per entry a lane holds six sums
+// over its pixels, (P, Q, V, c0, c1, c2) = sum dpower, sum dpower dy, sum dpower dy^2 and the
+// colour cotangents, all for its own column dx = px - mean.x.  Lanes l and l ^ 32 share the
+// column, so the first level pairs entry a's values with entry b's (lane bit 5 keeps the
+// entry) before the column factor is applied: each lane then expands its entry's six column
+// sums into the record's nine, (P dx, Q, P dx^2, Q dx, V, P, c0, c1, c2), and the levels 16 ..
+// 1 reduce-scatter those.  Lane l ends with the total of record value
+// pair9_index(l) of entry (l >> 5) & 1, the same in lanes l and l ^ 1.
+__device__ inline int pair9_index(int l) { return ((l >> 4) & 1) | ((l >> 2) & 2) | (l & 4) | ((l << 2) & 8); }
 
-// Reduce-scatter of NV <= 32 per-lane values: afterwards lane l holds the wave total of
-// value scatter_index(l) (undefined for indices >= NV).
-template <int NV>
-__device__ inline float reduce_scatter(const float* v, int lane) {
-  static_assert(NV >= 1 && NV <= 32, "at most 32 values");
-  float cur[NV];
+__device__ inline float reduce_scatter_pair9(const float* sa, const float* sb, float dxa, float dxb, int lane) {
+  float cur[12];
 #pragma unroll
-  for (int k = 0; k < NV; ++k) cur[k] = v[k];
-  constexpr int N1 = (NV + 1) / 2, N2 = (N1 + 1) / 2, N3 = (N2 + 1) / 2, N4 = (N3 + 1) / 2;
-  halve_level<32, NV>(cur, lane);
-  halve_level<16, N1>(cur, lane);
-  halve_level<8, N2>(cur, lane);
-  halve_level<4, N3>(cur, lane);
-  halve_level<2, N4>(cur, lane);
-  const float t = cur[0];
+  for (int k = 0; k < 6; ++k) {
+    cur[2 * k] = sa[k];
+    cur[2 * k + 1] = sb[k];
+  }
+  halve_level<32, 12>(cur, lane);
+  const float dx = (lane & 32) ? dxb : dxa;
+  const float Sx = cur[0] * dx;
+  float v[9] = {Sx, cur[1], Sx * dx, cur[1] * dx, cur[2], cur[0], cur[3], cur[4], cur[5]};
+  halve_level<16, 9>(v, lane);
+  halve_level<8, 5>(v, lane);
+  halve_level<4, 3>(v, lane);
+  halve_level<2, 2>(v, lane);
+  const float t = v[0];
   return t + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0xB1, 0xF, 0xF, false));
 }
 
@@ -500,7 +505,7 @@ __device__ __forceinline__ void composite_bwd_body(
       nxt = load_rec(rec, gn);
     }
     while (m != 0ull) {
-      float v[18];
+      float s6[2][6], dxh[2];
       bool any = false;
       int ga = 0, gb = 0;
 #pragma unroll
@@ -558,24 +563,21 @@ __device__ __forceinline__ void composite_bwd_body(
           }
         }
         }
-        // gradient record sums: [0] dpw dx, [1] dpw dy, [2] dpw dx^2, [3] dpw dx dy,
-        // [4] dpw dy^2, [5] dpw, [6..8] colour
-        const float Sx = P * dx;
-        v[9 * h + 0] = Sx;
-        v[9 * h + 1] = Q;
-        v[9 * h + 2] = Sx * dx;
-        v[9 * h + 3] = Q * dx;
-        v[9 * h + 4] = V;
-        v[9 * h + 5] = P;
-        v[9 * h + 6] = gc0;
-        v[9 * h + 7] = gc1;
-        v[9 * h + 8] = gc2;
+        // the column sums; the gradient record's [0] dpw dx, [1] dpw dy, [2] dpw dx^2,
+        // [3] dpw dx dy, [4] dpw dy^2, [5] dpw, [6..8] colour follow in the reduce-scatter
+        s6[h][0] = P;
+        s6[h][1] = Q;
+        s6[h][2] = V;
+        s6[h][3] = gc0;
+        s6[h][4] = gc1;
+        s6[h][5] = gc2;
+        dxh[h] = dx;
       }
       if (__ballot(any) != 0ull) {
-        const float mine = reduce_scatter<18>(v, lane);
-        const int vi = scatter_index(lane);
-        if ((lane & 1) == 0 && vi < 18 && mine != 0.0f)
-          atomicAdd(&grec[(int64_t)(vi < 9 ? ga : gb) * kRec + (vi < 9 ? vi : vi - 9)], mine);
+        const float mine = reduce_scatter_pair9(s6[0], s6[1], dxh[0], dxh[1], lane);
+        const int vi = pair9_index(lane);
+        if ((lane & 1) == 0 && vi < 9 && mine != 0.0f)
+          atomicAdd(&grec[(int64_t)((lane & 32) ? gb : ga) * kRec + vi], mine);
       }
     }
   }
