@@ -1661,7 +1661,7 @@ extern "C" int gs_window_from_bins(void* stream, int64_t n, const float* means2d
                                    const uint8_t* valid, const float* depths, int width, int height,
                                    const int32_t* sorted_gids, int64_t capacity, const int32_t* stats,
                                    gs_window_t* window) {
-  GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 23), "gs_window_from_bins: n must be in [0, 2^23) (got %lld)",
+  GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "gs_window_from_bins: n must be in [0, 2^31) (got %lld)",
              (long long)n);
   GS_REQUIRE(width > 0 && height > 0, "gs_window_from_bins: bad image size %dx%d", width, height);
   GS_REQUIRE(capacity >= 0 && stats && window, "gs_window_from_bins: bad arguments");
