@@ -50,6 +50,29 @@ def test_argument_errors_are_reported_without_launching():
     assert b"workspace" in L.gs_last_error()
 
 
+def test_argument_errors_of_the_window_sh_ssim_and_camera_entry_points():
+    """The entry points added for the default path's chunk windows, eval_sh, SSIM window
+    sizes and the camera cotangent reject bad arguments before launching anything."""
+    L = _lib.lib()
+    assert L.gs_window_from_list(None, None, 600, None) == 1
+    assert b"gs_window_from_list" in L.gs_last_error()
+    assert L.gs_window_from_bins(None, -1, None, None, None, None, 64, 64, None, 0, None, None) == 1
+    assert b"gs_window_from_bins" in L.gs_last_error()
+    assert L.gs_eval_sh(None, 10, 4, 3, None, None, None) == 1
+    assert b"needs 16" in L.gs_last_error()
+    assert L.gs_eval_sh_bwd(None, 10, 16, 4, None, None, None, None, None) == 1
+    assert b"sh_degree" in L.gs_last_error()
+    assert L.gs_l1_ssim_window_workspace_size(8, 8, 3, 0) == 0
+    assert L.gs_l1_ssim_window_workspace_size(8, 8, 3, 64) == 0
+    assert L.gs_l1_ssim_window_workspace_size(8, 8, 5, 63) > 0
+    assert L.gs_l1_ssim_window(None, 8, 8, 3, 64, None, None, None, 1, None, 0) == 1
+    assert b"window_size" in L.gs_last_error()
+    nb = L.gs_preprocess_bwd_w2c_workspace_size(1000)
+    assert nb == 16 * 16 * 4
+    rc = L.gs_preprocess_bwd_w2c(None, 1000, 16, 3, *([None] * 6), 64, 64, 1.0, 1.0, 0.0, 0.0, *([None] * 7), None, 0)
+    assert rc == 1 and b"gs_preprocess_bwd_w2c" in L.gs_last_error()
+
+
 def test_load_ply_missing_file():
     """test_io.py:42-44: a missing path raises FileNotFoundError (before any GPU work)."""
     import pytest
