@@ -710,7 +710,7 @@ __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restr
   const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
   const uint32_t C = (uint32_t)min<int64_t>((int64_t)*n_chunks, cmax);
-  for (uint32_t c = wave_uniform(blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)); c < C; c += nwaves) {
+  for (uint32_t c = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); c < C; c += nwaves) {
     const ChunkSpan cs = chunk_span(c, chunk_sb, chunk_base, sb_ranges, S, SX);
     const int len = (int)(cs.end - cs.begin);
     uint64_t wv[4];
@@ -1001,11 +1001,8 @@ __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restr
   const uint32_t cap32 = (uint32_t)cap;  // gs_bin checks cap < 2^31
   // every entry fits (the usual case): no per-store capacity test
   const bool fits = ranges[T] >= 0 && (int64_t)ranges[T] <= cap;
-  // the chunk and its descriptor are the wave's: in scalar registers (scalar loads,
-  // scalar branches on the step count)
-  for (uint32_t c = wave_uniform(blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)); c < C; c += nwaves) {
-    const uint4 dv = desc[c];
-    const uint4 d = make_uint4(wave_uniform(dv.x), wave_uniform(dv.y), wave_uniform(dv.z), wave_uniform(dv.w));
+  for (uint32_t c = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); c < C; c += nwaves) {
+    const uint4 d = desc[c];
     // counts of the chunk's earlier chunks in its segment (p of them), loaded together
     const uint32_t p = d.y >> 16;
     uint32_t cnt_c = 0;

@@ -113,11 +113,6 @@ constexpr float SH_C3_4 = -0.4570457994644658f;
 constexpr float SH_C3_5 = 1.445305721320277f;
 constexpr float SH_C3_6 = -0.5900435899266435f;
 
-// A value every lane of the wave holds (say, one computed from threadIdx.x >> 6), moved
-// to a scalar register: loads it addresses become scalar loads and branches on it
-// scalar branches, which the compiler cannot infer for values derived from threadIdx.
-__device__ inline uint32_t wave_uniform(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
-
 inline int div_up(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
 }  // namespace gs
