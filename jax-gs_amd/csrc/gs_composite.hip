@@ -51,6 +51,9 @@ namespace gs {
 namespace {
 
 constexpr float kTMin = 1e-4f;
+// exp2(q) < 0.99, the alpha cap of rasterizer.py:211, for every q below this (2^-0.015 =
+// 0.98966, far more than exp2's rounding below 0.99)
+constexpr float kBelowCapQ = -0.015f;
 
 __device__ inline float bcast(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
@@ -433,7 +436,9 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
   clear_slice();
 }
 
-template <int PPT, bool WIN>
+// NOCAP: entries that no pixel of the wave sees at the 0.99 alpha cap take a body without
+// the cap's selections (bit-identical; more registers live, so not for the 64-VGPR build).
+template <int PPT, bool WIN, bool NOCAP>
 __device__ __forceinline__ void composite_bwd_body(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
@@ -531,10 +536,46 @@ __device__ __forceinline__ void composite_bwd_body(
         // the sum itself)
         float P = -0.0f, Q = -0.0f, V = -0.0f, gc0 = -0.0f, gc1 = -0.0f, gc2 = -0.0f;
         if (live) {
+        float dyv[PPT], qv[PPT];
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
-          const float dy = py[i] - e.my;
-          const float q = q_of(dy, Adx2l, Bdx, e.C);
+          dyv[i] = py[i] - e.my;
+          qv[i] = q_of(dyv[i], Adx2l, Bdx, e.C);
+        }
+        float qmax = qv[0];
+#pragma unroll
+        for (int i = 1; i < PPT; ++i) qmax = fmaxf(qmax, qv[i]);
+        if (NOCAP && __ballot(qmax >= kBelowCapQ) == 0ull) {
+          // No pixel of the wave reaches the 0.99 cap with this entry: alpha = exp2(q) and
+          // its cotangent passes whole (the general body below with its cap and tie
+          // selections gives the same values here), 4 VALU instructions fewer per pixel.
+#pragma unroll
+          for (int i = 0; i < PPT; ++i) {
+            const float dy = dyv[i];
+            if (k < kp[i] && qv[i] > e.thr) {
+              any = true;
+              const float al = __builtin_amdgcn_exp2f(qv[i]);
+              const float Tk = Tr[i] * __builtin_amdgcn_rcpf(1.0f - al);
+              const float w = al * Tk;
+              gc0 = fmaf(w, g0[i], gc0);
+              gc1 = fmaf(w, g1[i], gc1);
+              gc2 = fmaf(w, g2[i], gc2);
+              const float cg = fmaf(e.b, g2[i], fmaf(e.g, g1[i], e.r * g0[i]));
+              const float dR = cg - Rg[i];
+              const float dpw = w * dR;  // (alpha T) dR
+              Rg[i] = fmaf(al, dR, Rg[i]);
+              Tr[i] = Tk;
+              P += dpw;
+              const float dpy = dpw * dy;
+              Q += dpy;
+              V = fmaf(dpy, dy, V);
+            }
+          }
+        } else {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+          const float dy = dyv[i];
+          const float q = qv[i];
           if (k < kp[i] && q > e.thr) {
             any = true;
             const float araw = __builtin_amdgcn_exp2f(q);
@@ -561,6 +602,7 @@ __device__ __forceinline__ void composite_bwd_body(
             Q += dpy;
             V = fmaf(dpy, dy, V);
           }
+        }
         }
         }
         // the column sums; the gradient record's [0] dpw dx, [1] dpw dy, [2] dpw dx^2,
@@ -598,10 +640,10 @@ __device__ __forceinline__ void composite_bwd_body(
 // as the forward read them.
 template <int PPT, bool WIN>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void composite_bwd_kernel(GS_BWD_PARAMS) {
-  composite_bwd_body<PPT, WIN>(GS_BWD_ARGS);
+  composite_bwd_body<PPT, WIN, PPT == 1>(GS_BWD_ARGS);
 }
 template <bool WIN>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6, 6))) void composite_bwd_wide_kernel(GS_BWD_PARAMS) { composite_bwd_body<4, WIN>(GS_BWD_ARGS); }
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6, 6))) void composite_bwd_wide_kernel(GS_BWD_PARAMS) { composite_bwd_body<4, WIN, true>(GS_BWD_ARGS); }
 #undef GS_BWD_PARAMS
 #undef GS_BWD_ARGS
 
