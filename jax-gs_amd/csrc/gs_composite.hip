@@ -654,15 +654,16 @@ __device__ __forceinline__ void composite_bwd_body(
       float *__restrict__ grec, const int32_t *__restrict__ order, const gs_window_t *__restrict__ win
 #define GS_BWD_ARGS rec, num_g, gids, n_entries, ranges, W, H, TX, T, bg, gimg, finalT, ncontrib, grec, order, win
 
-// The backward in two register budgets.  Capped at 64 VGPRs (8 waves per SIMD) it runs
-// best when a SIMD holds few of the launch's waves (cfg4, 3600 tiles: 250 vs 282 us);
-// scheduled for 6 waves per SIMD (68 VGPRs, so 7 are resident) it runs best when the
-// launch fills every slot (cfg2, 8160 tiles: 344 us, against 351 with no occupancy target
-// and 369 capped).  The host picks by tile count.  WIN: the default path's chunk windows,
-// as the forward read them.
+// The backward's two builds.  One pixel per lane (images below 2048 tiles, four waves per
+// tile): 64 VGPRs, 8 waves per SIMD, the general body only (the no-cap path's per-entry test
+// costs more than it saves with one pixel per lane: cfg0 169 -> 174 us, cfg1 230 -> 236).
+// Four pixels per lane: scheduled for 6 waves per SIMD (80 VGPRs) with the no-cap path,
+// which beats the 64-VGPR build without it at every size (cfg2, 8160 tiles: 306 vs 332 us;
+// cfg4, 3600 tiles: 233 vs 248; cfg3: 198 vs 207).  WIN: the default path's chunk
+// windows, as the forward read them.
 template <int PPT, bool WIN>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void composite_bwd_kernel(GS_BWD_PARAMS) {
-  composite_bwd_body<PPT, WIN, PPT == 1>(GS_BWD_ARGS);
+  composite_bwd_body<PPT, WIN, false>(GS_BWD_ARGS);
 }
 template <bool WIN>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6, 6))) void composite_bwd_wide_kernel(GS_BWD_PARAMS) { composite_bwd_body<4, WIN, true>(GS_BWD_ARGS); }
@@ -757,8 +758,6 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(int32_t* __restrict__ 
 
 // Large images have enough tiles to fill the GPU with one wave per tile.
 inline int pick_ppt(int T) { return T >= 2048 ? 4 : 1; }
-// tiles from which the backward uses its uncapped register budget (6 waves per SIMD)
-constexpr int kBwdWideTiles = 6 * 1024;
 // Tiles from which the forward gives a tile one wave (four pixels per lane); below that (and
 // from 2048 tiles) two waves of eight rows each: at 3600 tiles a launch holds 3-4 waves per
 // SIMD, and halving the work units evens them out (cfg4 forward 189 -> 176 us) where at
@@ -862,10 +861,8 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
                      ranges, width, height, TX, T, background, grad_image, final_T, n_contrib, grad_records,           \
                      tile_order, window)
   const bool win = window != nullptr;
-  if (pick_ppt(T) == 4 && T >= kBwdWideTiles) {
+  if (pick_ppt(T) == 4) {
     if (win) GS_BWD_LAUNCH(composite_bwd_wide_kernel<true>, 1); else GS_BWD_LAUNCH(composite_bwd_wide_kernel<false>, 1);
-  } else if (pick_ppt(T) == 4) {
-    if (win) GS_BWD_LAUNCH((composite_bwd_kernel<4, true>), 1); else GS_BWD_LAUNCH((composite_bwd_kernel<4, false>), 1);
   } else {
     if (win) GS_BWD_LAUNCH((composite_bwd_kernel<1, true>), 4); else GS_BWD_LAUNCH((composite_bwd_kernel<1, false>), 4);
   }

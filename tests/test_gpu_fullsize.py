@@ -5,10 +5,10 @@ configured sizes, against the CPU oracle (same bars as gpu_helpers.py).
 Kernel builds by tile count T (gs_composite.hip dispatch):
   T < 2048          forward and backward with four waves per tile (one pixel per lane)
   2048 <= T < 6144  two waves per tile forward (composite_fwd_kernel<2>), one wave per
-                    tile backward (composite_bwd_kernel<4>, 64-VGPR build)
-  T >= 6144         one wave per tile forward (composite_fwd_kernel<4>) and the
-                    uncapped-register backward (composite_bwd_wide_kernel): the builds
-                    behind the headline numbers.
+                    tile backward (composite_bwd_wide_kernel, with the path for entries
+                    no pixel of the wave sees at the 0.99 alpha cap)
+  T >= 6144         one wave per tile forward (composite_fwd_kernel<4>) and the same
+                    backward: the builds behind the headline numbers.
 The dense scenes saturate many pixels (T <= 1e-4), so the wave-wide early exit, the
 per-pixel n_contrib < count and the backward's replay from saturated pixels are compared,
 not only the open-pixel paths.
@@ -97,7 +97,7 @@ def _full_check(sc, cuda, seed_kind="l1", min_saturated=0.0):
     return dict(g=g, cam=cam, mask=m, extras=extras, ex_o=ex_o, gr_o=gr_o, res=res)
 
 
-@pytest.mark.parametrize("n,w,h,build", [(100000, 1024, 768, "fwd<2>/bwd<4>"), (100000, 1920, 832, "fwd<4>/bwd_wide")])
+@pytest.mark.parametrize("n,w,h,build", [(100000, 1024, 768, "fwd<2>/bwd_wide"), (100000, 1920, 832, "fwd<4>/bwd_wide")])
 def test_dense_scene_per_kernel_build(cuda, n, w, h, build):
     """The configuration-2 family, dense enough that 40 % of the pixels saturate, at a
     tile count of each large-image build."""
@@ -105,6 +105,22 @@ def test_dense_scene_per_kernel_build(cuda, n, w, h, build):
     assert (2048 <= T < 6144) if build.startswith("fwd<2>") else T >= 6144
     sc = scenes.make_scene(2, n=n, width=w, height=h)
     _full_check(sc, cuda, min_saturated=0.3)
+
+
+@pytest.mark.parametrize("w,h", [(1024, 768), (1920, 832)])
+def test_alpha_cap_in_large_image_builds(cuda, w, h):
+    """Near-opaque Gaussians (opacity logits 4.6 to 9: sigmoid >= 0.99 for most) on both
+    large-image builds, so that many entries reach the 0.99 alpha cap (rasterizer.py:211)
+    and the backward takes its general body for them (the cap's zero derivative, the tie's
+    half) beside the no-cap path for the rest."""
+    sc = scenes.make_scene(1, n=30000, width=w, height=h)
+    rng = np.random.default_rng(5)
+    op = sc["params"]["opacities"]
+    sel = rng.random(op.shape[0]) < 0.5
+    op[sel, 0] = rng.uniform(4.6, 9.0, int(sel.sum())).astype(np.float32)
+    # a third of the Gaussians at opacity >= 0.99: their alpha reaches the cap near their centres
+    assert float((1.0 / (1.0 + np.exp(-op[:, 0].astype(np.float64))) >= 0.99).mean()) > 0.3
+    _full_check(sc, cuda, seed_kind="normal")
 
 
 def test_cfg2_full_frame(cuda):
