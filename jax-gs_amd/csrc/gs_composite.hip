@@ -458,8 +458,13 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
   clear_slice();
 }
 
-// NOCAP: entries that no pixel of the wave sees at the 0.99 alpha cap take a body without
-// the cap's selections (bit-identical; more registers live, so not for the 64-VGPR build).
+// NOCAP: the body without the cap's per-pixel selections (the cap is applied to the alphas
+// in place, and the power sums redone with its selections, only for entries that some pixel
+// of the wave can see at the cap), with 1/T as the per-pixel state: T_k = 1/(1/T_{k+1} *
+// (1 - alpha_k)) costs an fma and an rcp where T_{k+1}/(1 - alpha_k) costs a subtraction,
+// an rcp and a product.  Both NOCAP changes keep the loop-carried state in place (a body
+// chosen per entry between two versions made the compiler copy that state at every entry).
+// More registers live than the 64-VGPR build allows.
 template <int PPT, bool WIN, bool NOCAP>
 __device__ __forceinline__ void composite_bwd_body(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
@@ -486,13 +491,13 @@ __device__ __forceinline__ void composite_bwd_body(
   for (int i = 0; i < PPT; ++i) {
     const int yl = part * 4 * PPT + (lane >> 4) + 4 * i;
     py[i] = (float)(ty * kTile) + ((float)yl + 0.5f);
-    Tr[i] = 1.0f;
+    Tr[i] = 1.0f;  // NOCAP: the reciprocal 1/T (see the body)
     g0[i] = g1[i] = g2[i] = 0.0f;
     kp[i] = 0;
     const int Y = Y0 + 4 * i;
     if (X < W && Y < H) {
       const int64_t p = (int64_t)Y * W + X;
-      Tr[i] = finalT[p];
+      Tr[i] = NOCAP ? 1.0f / fmaxf(finalT[p], 1e-30f) : finalT[p];  // finite for T = 0
       const int k = ncontrib[p];
       kp[i] = k < 0 ? 0 : (k > n ? n : k);  // entries beyond the tile's list never load
       g0[i] = gimg[3 * p];
@@ -538,11 +543,11 @@ __device__ __forceinline__ void composite_bwd_body(
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         // h = 1 with no survivor left: an empty second half (all sums 0)
-        const bool live = m != 0ull;
+        // live half: k >= 0 (a wave-uniform integer, so the tests below stay scalar)
         const Rec e = nxt;
         const int g = gn;
-        const int k = live ? b0 + jn : -1;
-        if (live) {
+        const int k = m != 0ull ? b0 + jn : -1;
+        if (k >= 0) {
           m &= ~(1ull << jn);
           if (m != 0ull) {
             jn = 63 - __builtin_clzll(m);
@@ -550,14 +555,14 @@ __device__ __forceinline__ void composite_bwd_body(
             nxt = load_rec(rec, gn);
           }
         }
-        if (h == 0) ga = g; else gb = live ? g : ga;
+        if (h == 0) ga = g; else gb = k >= 0 ? g : ga;
         const float dx = px - e.mx;
         const float Adx2l = fmaf(e.A * dx, dx, e.lop), Bdx = e.B * dx;
         // per-lane sums over the lane's pixels: P = sum dpower, Q = sum dpower*dy,
         // V = sum dpower*dy^2, colour cotangents (from -0, so that the first term is
         // the sum itself)
         float P = -0.0f, Q = -0.0f, V = -0.0f, gc0 = -0.0f, gc1 = -0.0f, gc2 = -0.0f;
-        if (live) {
+        if (k >= 0) {
         float dyv[PPT], qv[PPT];
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
@@ -567,17 +572,30 @@ __device__ __forceinline__ void composite_bwd_body(
         float qmax = qv[0];
 #pragma unroll
         for (int i = 1; i < PPT; ++i) qmax = fmaxf(qmax, qv[i]);
-        if (NOCAP && __ballot(qmax >= kBelowCapQ) == 0ull) {
-          // No pixel of the wave reaches the 0.99 cap with this entry: alpha = exp2(q) and
-          // its cotangent passes whole (the general body below with its cap and tie
-          // selections gives the same values here), 4 VALU instructions fewer per pixel.
+        if (NOCAP) {
+          // alpha of each pixel, capped only when some pixel of the wave can reach the
+          // 0.99 cap with this entry (rare): below it min(araw, 0.99) = araw, and the
+          // cotangent passes whole, so the body needs no selections; the rare capped
+          // entry redoes its power sums with the cap's selections afterwards.  One body
+          // for both keeps the per-pixel state (T, Rg) in place across entries.
+          const bool capw = __ballot(qmax >= kBelowCapQ) != 0ull;
+          float alv[PPT], wdv[PPT];  // wdv[i] is read only where it was written
+#pragma unroll
+          for (int i = 0; i < PPT; ++i) alv[i] = __builtin_amdgcn_exp2f(qv[i]);
+          if (capw) {
+#pragma unroll
+            for (int i = 0; i < PPT; ++i) alv[i] = alv[i] < 0.99f ? alv[i] : 0.99f;
+          }
 #pragma unroll
           for (int i = 0; i < PPT; ++i) {
             const float dy = dyv[i];
             if (k < kp[i] && qv[i] > e.thr) {
               any = true;
-              const float al = __builtin_amdgcn_exp2f(qv[i]);
-              const float Tk = Tr[i] * __builtin_amdgcn_rcpf(1.0f - al);
+              const float al = alv[i];
+              // 1/T_k = (1 - alpha) / T_{k+1}, one rounding; T_k from it by rcp, which
+              // does not feed back into the recursion
+              const float iTk = fmaf(-al, Tr[i], Tr[i]);
+              const float Tk = __builtin_amdgcn_rcpf(iTk);
               const float w = al * Tk;
               gc0 = fmaf(w, g0[i], gc0);
               gc1 = fmaf(w, g1[i], gc1);
@@ -585,12 +603,33 @@ __device__ __forceinline__ void composite_bwd_body(
               const float cg = fmaf(e.b, g2[i], fmaf(e.g, g1[i], e.r * g0[i]));
               const float dR = cg - Rg[i];
               const float dpw = w * dR;  // (alpha T) dR
+              wdv[i] = dpw;
               Rg[i] = fmaf(al, dR, Rg[i]);
-              Tr[i] = Tk;
+              Tr[i] = iTk;
               P += dpw;
               const float dpy = dpw * dy;
               Q += dpy;
               V = fmaf(dpy, dy, V);
+            }
+          }
+          if (capw) {
+            P = -0.0f;
+            Q = -0.0f;
+            V = -0.0f;
+#pragma unroll
+            for (int i = 0; i < PPT; ++i) {
+              if (k < kp[i] && qv[i] > e.thr) {
+                // the alpha before the cap again (a fresh exp2: not kept live across the body)
+                float qi = qv[i];
+                asm volatile("" : "+v"(qi));
+                const float araw = __builtin_amdgcn_exp2f(qi);
+                float dpw = araw < 0.99f ? wdv[i] : 0.0f;
+                if (__builtin_expect(araw == 0.99f, 0)) dpw = 0.5f * wdv[i];
+                P += dpw;
+                const float dpy = dpw * dyv[i];
+                Q += dpy;
+                V = fmaf(dpy, dyv[i], V);
+              }
             }
           }
         } else {
@@ -657,10 +696,12 @@ __device__ __forceinline__ void composite_bwd_body(
 // The backward's two builds.  One pixel per lane (images below 2048 tiles, four waves per
 // tile): 64 VGPRs, 8 waves per SIMD, the general body only (the no-cap path's per-entry test
 // costs more than it saves with one pixel per lane: cfg0 169 -> 174 us, cfg1 230 -> 236).
-// Four pixels per lane: scheduled for 6 waves per SIMD (80 VGPRs) with the no-cap path,
-// which beats the 64-VGPR build without it at every size (cfg2, 8160 tiles: 306 vs 332 us;
-// cfg4, 3600 tiles: 233 vs 248; cfg3: 198 vs 207).  WIN: the default path's chunk
-// windows, as the forward read them.
+// Four pixels per lane: scheduled for 6 waves per SIMD (at most 80 VGPRs) with the no-cap
+// body, which beats the 64-VGPR build without it at every size (cfg2, 8160 tiles: 306 vs
+// 332 us; cfg4, 3600 tiles: 233 vs 248; cfg3: 198 vs 207); one body with the cap applied in
+// place and the 1/T state took cfg2 from 310 to 304 us (8 % fewer VALU instructions, the
+// copies of the state between two bodies gone).  WIN: the default path's chunk windows, as
+// the forward read them.
 template <int PPT, bool WIN>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void composite_bwd_kernel(GS_BWD_PARAMS) {
   composite_bwd_body<PPT, WIN, false>(GS_BWD_ARGS);
