@@ -54,6 +54,8 @@ constexpr float kTMin = 1e-4f;
 // exp2(q) < 0.99, the alpha cap of rasterizer.py:211, for every q below this (2^-0.015 =
 // 0.98966, far more than exp2's rounding below 0.99)
 constexpr float kBelowCapQ = -0.015f;
+// s_waitcnt immediate (gfx9 layout) that waits for lgkmcnt = 0 and for nothing else
+constexpr int kWaitLgkm0 = 0xC07F;
 
 __device__ inline float bcast(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
@@ -351,9 +353,100 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
     // group's records are in SGPRs before it is blended and the next group's scalar
     // loads are issued first, so their latency is covered by G entries' arithmetic
     // (scalar loads complete out of order: waiting for one is waiting for all, so
-    // requests go out per group).  With four pixels per lane the arithmetic of one
-    // entry already covers the load and G = 1 keeps the instruction count down.
+    // requests go out per group).  With two or four pixels per lane the arithmetic of one
+    // entry covers the load and G = 1 keeps the instruction count down; its two record
+    // registers are used in turn, with an explicit wait before each request (two-wave
+    // forward, cfg4 175 -> 155 us, cfg3 148 -> 135 us; one-wave cfg2 unchanged).
     constexpr int G = PPT == 1 ? 2 : 1;
+    // one walked entry e (tile index kidx within the batch) blended into the lane's pixels
+    auto blend = [&](const Rec& e, int kidx) {
+      const int kk = b0 + kidx + 1;  // entries met so far, this one included
+      const float dx = px - e.mx;
+      const float Adx2l = fmaf(e.A * dx, dx, e.lop), Bdx = e.B * dx;
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const float q = q_of(py[i] - e.my, Adx2l, Bdx, e.C);
+        const bool act = Tr[i] > kTMin;  // rasterizer.py:206
+        if (PPT == 1) {
+          cnt[i] = act ? kk : cnt[i];
+          // gated-out pixels blend alpha = 0, which leaves C and T unchanged, so only the
+          // lanes that pass run the blend (the wave skips it when none does); with four
+          // pixels per lane the branch-free form measured faster (226 vs 251 us on cfg2),
+          // with one it is the branch (cfg1 187 -> 180 us)
+          if (act && q > e.thr) {  // rasterizer.py:212
+            float al = __builtin_amdgcn_exp2f(q);
+            al = al < 0.99f ? al : 0.99f;
+            const float w = al * Tr[i];
+            c0[i] = fmaf(w, e.r, c0[i]);
+            c1[i] = fmaf(w, e.g, c1[i]);
+            c2[i] = fmaf(w, e.b, c2[i]);
+            Tr[i] = Tr[i] - w;  // T (1 - alpha)
+          }
+        } else {
+          float al = __builtin_amdgcn_exp2f(q);
+          al = al < 0.99f ? al : 0.99f;
+          al = (act && q > e.thr) ? al : 0.0f;  // rasterizer.py:212
+          const float w = al * Tr[i];
+          c0[i] = fmaf(w, e.r, c0[i]);
+          c1[i] = fmaf(w, e.g, c1[i]);
+          c2[i] = fmaf(w, e.b, c2[i]);
+          Tr[i] = Tr[i] - w;  // T (1 - alpha)
+          cnt[i] = act ? kk : cnt[i];
+        }
+      }
+    };
+    // every 8 walked entries: stop when no pixel of the wave is still open
+    auto all_closed = [&]() {
+      if (walked < next_check) return false;
+      next_check = walked + 8;
+      bool live = false;
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) live = live || Tr[i] > kTMin;
+      return __ballot(live) == 0ull;
+    };
+    if constexpr (G == 1) {
+      // one entry at a time, the next survivor's record requested before the blend; two
+      // record registers used in turn (no copy of the prefetched record per entry)
+      Rec ra = zero_rec(), rb = zero_rec();
+      int ja = -1, jb = -1;
+      if (m != 0ull) {
+        ja = __builtin_ctzll(m);
+        m &= m - 1ull;
+        ra = load_rec(rec, bcast_i(gl, ja));
+      }
+      while (ja >= 0) {
+        if (all_closed()) {
+          done = true;
+          break;
+        }
+        // ra's record was requested a whole entry ago: wait for it before the next
+        // request goes out (scalar loads complete out of order, so a wait at its first
+        // use would also wait for the request issued just before)
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+        jb = -1;
+        if (m != 0ull) {
+          jb = __builtin_ctzll(m);
+          m &= m - 1ull;
+          rb = load_rec(rec, bcast_i(gl, jb));
+        }
+        ++walked;
+        blend(ra, ja);
+        if (jb < 0) break;
+        if (all_closed()) {
+          done = true;
+          break;
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+        ja = -1;
+        if (m != 0ull) {
+          ja = __builtin_ctzll(m);
+          m &= m - 1ull;
+          ra = load_rec(rec, bcast_i(gl, ja));
+        }
+        ++walked;
+        blend(rb, jb);
+      }
+    } else {
     Rec r[G];
     int j[G];
 #pragma unroll
@@ -367,16 +460,9 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
       }
     }
     while (j[0] >= 0) {
-      // every 8 walked entries: stop when no pixel of the wave is still open
-      if (walked >= next_check) {
-        next_check = walked + 8;
-        bool live = false;
-#pragma unroll
-        for (int i = 0; i < PPT; ++i) live = live || Tr[i] > kTMin;
-        if (__ballot(live) == 0ull) {
-          done = true;
-          break;
-        }
+      if (all_closed()) {
+        done = true;
+        break;
       }
       Rec e[G];
       int k[G];
@@ -395,41 +481,9 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
       for (int h = 0; h < G; ++h) {
         if (k[h] < 0) break;
         ++walked;
-        const int kk = b0 + k[h] + 1;  // entries met so far, this one included
-        const float dx = px - e[h].mx;
-        const float Adx2l = fmaf(e[h].A * dx, dx, e[h].lop), Bdx = e[h].B * dx;
-#pragma unroll
-        for (int i = 0; i < PPT; ++i) {
-          const float q = q_of(py[i] - e[h].my, Adx2l, Bdx, e[h].C);
-          const bool act = Tr[i] > kTMin;  // rasterizer.py:206
-          if (PPT == 1) {
-            cnt[i] = act ? kk : cnt[i];
-            // gated-out pixels blend alpha = 0, which leaves C and T unchanged, so only the
-            // lanes that pass run the blend (the wave skips it when none does); with four
-            // pixels per lane the branch-free form measured faster (226 vs 251 us on cfg2),
-            // with one it is the branch (cfg1 187 -> 180 us)
-            if (act && q > e[h].thr) {  // rasterizer.py:212
-              float al = __builtin_amdgcn_exp2f(q);
-              al = al < 0.99f ? al : 0.99f;
-              const float w = al * Tr[i];
-              c0[i] = fmaf(w, e[h].r, c0[i]);
-              c1[i] = fmaf(w, e[h].g, c1[i]);
-              c2[i] = fmaf(w, e[h].b, c2[i]);
-              Tr[i] = Tr[i] - w;  // T (1 - alpha)
-            }
-          } else {
-            float al = __builtin_amdgcn_exp2f(q);
-            al = al < 0.99f ? al : 0.99f;
-            al = (act && q > e[h].thr) ? al : 0.0f;  // rasterizer.py:212
-            const float w = al * Tr[i];
-            c0[i] = fmaf(w, e[h].r, c0[i]);
-            c1[i] = fmaf(w, e[h].g, c1[i]);
-            c2[i] = fmaf(w, e[h].b, c2[i]);
-            Tr[i] = Tr[i] - w;  // T (1 - alpha)
-            cnt[i] = act ? kk : cnt[i];
-          }
-        }
+        blend(e[h], k[h]);
       }
+    }
     }
   }
   const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];
