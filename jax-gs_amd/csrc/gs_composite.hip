@@ -583,12 +583,14 @@ __device__ __forceinline__ void composite_bwd_body(
     g_ahead = probe_gid_ahead<WIN>(gids, start, b0 - 128 + lane, kmax, win, thr);
     const int gl = pr.g;
     uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
-    Rec nxt = zero_rec();
+    // the next survivor's record is requested one entry ahead, into ra for the first
+    // half of a pair and rb for the second (used in turn: no copy per entry)
+    Rec ra = zero_rec(), rb = zero_rec();
     int jn = 0, gn = 0;
     if (m != 0ull) {
       jn = 63 - __builtin_clzll(m);
       gn = bcast_i(gl, jn);
-      nxt = load_rec(rec, gn);
+      ra = load_rec(rec, gn);
     }
     while (m != 0ull) {
       float s6[2][6], dxh[2];
@@ -598,15 +600,19 @@ __device__ __forceinline__ void composite_bwd_body(
       for (int h = 0; h < 2; ++h) {
         // h = 1 with no survivor left: an empty second half (all sums 0)
         // live half: k >= 0 (a wave-uniform integer, so the tests below stay scalar)
-        const Rec e = nxt;
+        const Rec& e = h == 0 ? ra : rb;
+        Rec& ahead = h == 0 ? rb : ra;
         const int g = gn;
         const int k = m != 0ull ? b0 + jn : -1;
         if (k >= 0) {
+          // e was requested an entry ago: wait for it before the next request goes out
+          // (scalar loads complete out of order)
+          __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
           m &= ~(1ull << jn);
           if (m != 0ull) {
             jn = 63 - __builtin_clzll(m);
             gn = bcast_i(gl, jn);
-            nxt = load_rec(rec, gn);
+            ahead = load_rec(rec, gn);
           }
         }
         if (h == 0) ga = g; else gb = k >= 0 ? g : ga;
