@@ -359,6 +359,9 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
     // forward, cfg4 175 -> 155 us, cfg3 148 -> 135 us; one-wave cfg2 unchanged).
     constexpr int G = PPT == 1 ? 2 : 1;
     // one walked entry e (tile index kidx within the batch) blended into the lane's pixels
+    // (two or four pixels per lane: branch-free, gated-out pixels blend alpha = 0, which
+    // leaves C and T unchanged; measured faster than per-pixel branches, 226 vs 251 us
+    // on cfg2)
     auto blend = [&](const Rec& e, int kidx) {
       const int kk = b0 + kidx + 1;  // entries met so far, this one included
       const float dx = px - e.mx;
@@ -367,32 +370,15 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
       for (int i = 0; i < PPT; ++i) {
         const float q = q_of(py[i] - e.my, Adx2l, Bdx, e.C);
         const bool act = Tr[i] > kTMin;  // rasterizer.py:206
-        if (PPT == 1) {
-          cnt[i] = act ? kk : cnt[i];
-          // gated-out pixels blend alpha = 0, which leaves C and T unchanged, so only the
-          // lanes that pass run the blend (the wave skips it when none does); with four
-          // pixels per lane the branch-free form measured faster (226 vs 251 us on cfg2),
-          // with one it is the branch (cfg1 187 -> 180 us)
-          if (act && q > e.thr) {  // rasterizer.py:212
-            float al = __builtin_amdgcn_exp2f(q);
-            al = al < 0.99f ? al : 0.99f;
-            const float w = al * Tr[i];
-            c0[i] = fmaf(w, e.r, c0[i]);
-            c1[i] = fmaf(w, e.g, c1[i]);
-            c2[i] = fmaf(w, e.b, c2[i]);
-            Tr[i] = Tr[i] - w;  // T (1 - alpha)
-          }
-        } else {
-          float al = __builtin_amdgcn_exp2f(q);
-          al = al < 0.99f ? al : 0.99f;
-          al = (act && q > e.thr) ? al : 0.0f;  // rasterizer.py:212
-          const float w = al * Tr[i];
-          c0[i] = fmaf(w, e.r, c0[i]);
-          c1[i] = fmaf(w, e.g, c1[i]);
-          c2[i] = fmaf(w, e.b, c2[i]);
-          Tr[i] = Tr[i] - w;  // T (1 - alpha)
-          cnt[i] = act ? kk : cnt[i];
-        }
+        float al = __builtin_amdgcn_exp2f(q);
+        al = al < 0.99f ? al : 0.99f;
+        al = (act && q > e.thr) ? al : 0.0f;  // rasterizer.py:212
+        const float w = al * Tr[i];
+        c0[i] = fmaf(w, e.r, c0[i]);
+        c1[i] = fmaf(w, e.g, c1[i]);
+        c2[i] = fmaf(w, e.b, c2[i]);
+        Tr[i] = Tr[i] - w;  // T (1 - alpha)
+        cnt[i] = act ? kk : cnt[i];
       }
     };
     // every 8 walked entries: stop when no pixel of the wave is still open
@@ -481,7 +467,26 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
       for (int h = 0; h < G; ++h) {
         if (k[h] < 0) break;
         ++walked;
-        blend(e[h], k[h]);
+        const int kk = b0 + k[h] + 1;  // entries met so far, this one included
+        const float dx = px - e[h].mx;
+        const float Adx2l = fmaf(e[h].A * dx, dx, e[h].lop), Bdx = e[h].B * dx;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+          const float q = q_of(py[i] - e[h].my, Adx2l, Bdx, e[h].C);
+          const bool act = Tr[i] > kTMin;  // rasterizer.py:206
+          cnt[i] = act ? kk : cnt[i];
+          // one pixel per lane: only the lanes that pass run the blend (the wave skips it
+          // when none does; cfg1 187 -> 180 us against the branch-free form)
+          if (act && q > e[h].thr) {  // rasterizer.py:212
+            float al = __builtin_amdgcn_exp2f(q);
+            al = al < 0.99f ? al : 0.99f;
+            const float w = al * Tr[i];
+            c0[i] = fmaf(w, e[h].r, c0[i]);
+            c1[i] = fmaf(w, e[h].g, c1[i]);
+            c2[i] = fmaf(w, e[h].b, c2[i]);
+            Tr[i] = Tr[i] - w;  // T (1 - alpha)
+          }
+        }
       }
     }
     }
