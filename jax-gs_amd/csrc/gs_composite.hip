@@ -253,9 +253,8 @@ __device__ inline int probe_gid(const int32_t* __restrict__ gids, int start, int
 
 // The same split in two: the load of a batch ahead (raw id, and whether k is an entry),
 // and the clamp where the id is used, a batch later, so that nothing waits for the load
-// in between (a clamp right after it waits for every load in flight).  The backward walks
-// with it (cfg2 311 -> 307 us); the forward measured slower with it (230 -> 235 us) and
-// keeps the clamp at the load.
+// in between (a clamp right after it waits for every load in flight).  Both walks use it
+// (backward cfg2 311 -> 307 us).
 struct Ahead {
   int raw;
   bool ok;
@@ -341,14 +340,17 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
   bool done = false;
   int walked = 0, next_check = 8;
   const int64_t thr = WIN ? win->thr : 0;
-  int g_ahead = probe_gid<WIN>(gids, start, 64 + lane, n, num_g, win, thr);
-  Probe p_next = probe_load(rec, probe_gid<WIN>(gids, start, lane, n, num_g, win, thr));
+  // The batch's probe records were requested a batch ago; the next batch's go out after
+  // the batch's test, so that the test waits for nothing requested since (loads complete
+  // in order: a wait for one waits for every earlier one), and the id two batches ahead is
+  // clamped where it is used, a batch later.
+  Ahead g_ahead = probe_gid_ahead<WIN>(gids, start, 64 + lane, n, win, thr);
+  Probe pr = probe_load(rec, probe_gid<WIN>(gids, start, lane, n, num_g, win, thr));
   for (int b0 = 0; b0 < n && !done; b0 += 64) {
-    const Probe pr = p_next;
-    p_next = probe_load(rec, g_ahead);
-    g_ahead = probe_gid<WIN>(gids, start, b0 + 128 + lane, n, num_g, win, thr);
     const int gl = pr.g;
     uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
+    pr = probe_load(rec, ahead_gid(g_ahead, num_g));
+    g_ahead = probe_gid_ahead<WIN>(gids, start, b0 + 128 + lane, n, win, thr);
     // Survivors are walked in groups of G (G = 2 when a lane holds one pixel): the
     // group's records are in SGPRs before it is blended and the next group's scalar
     // loads are issued first, so their latency is covered by G entries' arithmetic
