@@ -224,6 +224,27 @@ __device__ inline Rec load_rec(const float4* __restrict__ rec, int g) {
   return Rec{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z};
 }
 
+// A walked entry's record is addressed by a value read from the testing lane: with O32
+// the byte offset gid * 48 (records below 4 GiB), which scalar loads take as their
+// offset register (one lane read and the loads, no 64-bit address arithmetic per entry);
+// otherwise the id.  The gradient records have the same 48-byte stride.
+template <bool O32>
+__device__ inline int rec_key(int g) { return O32 ? (int)((uint32_t)g * (uint32_t)(kRec * 4)) : g; }
+
+template <bool O32>
+__device__ inline Rec load_rec_key(const float4* __restrict__ rec, int key) {
+  if (!O32) return load_rec(rec, key);
+  const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(rec) + (uint32_t)key);
+  const float4 a = p[0], b = p[1], c = p[2];
+  return Rec{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z};
+}
+
+template <bool O32>
+__device__ inline float* grec_at(float* __restrict__ grec, int key, int v) {
+  return O32 ? reinterpret_cast<float*>(reinterpret_cast<char*>(grec) + (uint32_t)key) + v
+             : grec + (int64_t)key * kRec + v;
+}
+
 // Ids are clamped like XLA's gather.
 __device__ inline int clamp_gid(int g, int num_g) { return min(max(g, 0), num_g - 1); }
 
@@ -292,7 +313,7 @@ __device__ inline uint64_t probe_test(const Probe& p, float x0, float x1, float 
 
 // WIN: the default path's chunk windows (see probe_gid); without it the id fetch compiles
 // to the plain one.
-template <int PPT, bool WIN>
+template <int PPT, bool WIN, bool O32>
 __global__ __launch_bounds__(64) void composite_fwd_kernel(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
@@ -347,7 +368,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
   Ahead g_ahead = probe_gid_ahead<WIN>(gids, start, 64 + lane, n, win, thr);
   Probe pr = probe_load(rec, probe_gid<WIN>(gids, start, lane, n, num_g, win, thr));
   for (int b0 = 0; b0 < n && !done; b0 += 64) {
-    const int gl = pr.g;
+    const int gk = rec_key<O32>(pr.g);  // the lane's record key (read where the lane survives)
     uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
     pr = probe_load(rec, ahead_gid(g_ahead, num_g));
     g_ahead = probe_gid_ahead<WIN>(gids, start, b0 + 128 + lane, n, win, thr);
@@ -399,8 +420,8 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
       int ja = -1, jb = -1;
       if (m != 0ull) {
         ja = __builtin_ctzll(m);
-        m &= m - 1ull;
-        ra = load_rec(rec, bcast_i(gl, ja));
+        m &= ~(1ull << ja);
+        ra = load_rec_key<O32>(rec, bcast_i(gk, ja));
       }
       while (ja >= 0) {
         if (all_closed()) {
@@ -414,8 +435,8 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
         jb = -1;
         if (m != 0ull) {
           jb = __builtin_ctzll(m);
-          m &= m - 1ull;
-          rb = load_rec(rec, bcast_i(gl, jb));
+          m &= ~(1ull << jb);
+          rb = load_rec_key<O32>(rec, bcast_i(gk, jb));
         }
         ++walked;
         blend(ra, ja);
@@ -428,8 +449,8 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
         ja = -1;
         if (m != 0ull) {
           ja = __builtin_ctzll(m);
-          m &= m - 1ull;
-          ra = load_rec(rec, bcast_i(gl, ja));
+          m &= ~(1ull << ja);
+          ra = load_rec_key<O32>(rec, bcast_i(gk, ja));
         }
         ++walked;
         blend(rb, jb);
@@ -444,7 +465,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
       if (m != 0ull) {
         j[h] = __builtin_ctzll(m);
         m &= m - 1ull;
-        r[h] = load_rec(rec, bcast_i(gl, j[h]));
+        r[h] = load_rec_key<O32>(rec, bcast_i(gk, j[h]));
       }
     }
     while (j[0] >= 0) {
@@ -462,7 +483,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
         if (m != 0ull) {
           j[h] = __builtin_ctzll(m);
           m &= m - 1ull;
-          r[h] = load_rec(rec, bcast_i(gl, j[h]));
+          r[h] = load_rec_key<O32>(rec, bcast_i(gk, j[h]));
         }
       }
 #pragma unroll
@@ -526,7 +547,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
 // an rcp and a product.  Both NOCAP changes keep the loop-carried state in place (a body
 // chosen per entry between two versions made the compiler copy that state at every entry).
 // More registers live than the 64-VGPR build allows.
-template <int PPT, bool WIN, bool NOCAP>
+template <int PPT, bool WIN, bool NOCAP, bool O32>
 __device__ __forceinline__ void composite_bwd_body(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
@@ -588,7 +609,7 @@ __device__ __forceinline__ void composite_bwd_body(
     const Probe pr = p_next;
     p_next = probe_load(rec, ahead_gid(g_ahead, num_g));
     g_ahead = probe_gid_ahead<WIN>(gids, start, b0 - 128 + lane, kmax, win, thr);
-    const int gl = pr.g;
+    const int gk = rec_key<O32>(pr.g);  // the lane's record key (read where the lane survives)
     uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
     // the next survivor's record is requested one entry ahead, into ra for the first
     // half of a pair and rb for the second (used in turn: no copy per entry)
@@ -596,8 +617,8 @@ __device__ __forceinline__ void composite_bwd_body(
     int jn = 0, gn = 0;
     if (m != 0ull) {
       jn = 63 - __builtin_clzll(m);
-      gn = bcast_i(gl, jn);
-      ra = load_rec(rec, gn);
+      gn = bcast_i(gk, jn);
+      ra = load_rec_key<O32>(rec, gn);
     }
     while (m != 0ull) {
       float s6[2][6], dxh[2];
@@ -618,8 +639,8 @@ __device__ __forceinline__ void composite_bwd_body(
           m &= ~(1ull << jn);
           if (m != 0ull) {
             jn = 63 - __builtin_clzll(m);
-            gn = bcast_i(gl, jn);
-            ahead = load_rec(rec, gn);
+            gn = bcast_i(gk, jn);
+            ahead = load_rec_key<O32>(rec, gn);
           }
         }
         if (h == 0) ga = g; else gb = k >= 0 ? g : ga;
@@ -747,7 +768,7 @@ __device__ __forceinline__ void composite_bwd_body(
         const float mine = reduce_scatter_pair9(s6[0], s6[1], dxh[0], dxh[1], lane);
         const int vi = pair9_index(lane);
         if ((lane & 1) == 0 && vi < 9 && mine != 0.0f)
-          atomicAdd(&grec[(int64_t)((lane & 32) ? gb : ga) * kRec + vi], mine);
+          atomicAdd(grec_at<O32>(grec, (lane & 32) ? gb : ga, vi), mine);
       }
     }
   }
@@ -769,12 +790,14 @@ __device__ __forceinline__ void composite_bwd_body(
 // place and the 1/T state took cfg2 from 310 to 304 us (8 % fewer VALU instructions, the
 // copies of the state between two bodies gone).  WIN: the default path's chunk windows, as
 // the forward read them.
-template <int PPT, bool WIN>
+template <int PPT, bool WIN, bool O32>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void composite_bwd_kernel(GS_BWD_PARAMS) {
-  composite_bwd_body<PPT, WIN, false>(GS_BWD_ARGS);
+  composite_bwd_body<PPT, WIN, false, O32>(GS_BWD_ARGS);
 }
-template <bool WIN>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6, 6))) void composite_bwd_wide_kernel(GS_BWD_PARAMS) { composite_bwd_body<4, WIN, true>(GS_BWD_ARGS); }
+template <bool WIN, bool O32>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6, 6))) void composite_bwd_wide_kernel(GS_BWD_PARAMS) {
+  composite_bwd_body<4, WIN, true, O32>(GS_BWD_ARGS);
+}
 #undef GS_BWD_PARAMS
 #undef GS_BWD_ARGS
 
@@ -864,6 +887,9 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(int32_t* __restrict__ 
   for (int t = tid; t < T; t += 1024) order[atomicAdd(&start[bucket[t]], 1)] = t;
 }
 
+// Record byte offsets (gid * 48) fit the 32-bit offset register of scalar loads.
+inline bool rec_offsets_fit(int64_t n) { return n * (int64_t)(kRec * 4) <= (int64_t)0xFFFFFFFF - 64; }
+
 // Large images have enough tiles to fill the GPU with one wave per tile.
 inline int pick_ppt(int T) { return T >= 2048 ? 4 : 1; }
 // Tiles from which the forward gives a tile one wave (four pixels per lane); below that (and
@@ -916,19 +942,22 @@ extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, c
   GS_REQUIRE(clear_records == nullptr || ((uintptr_t)clear_records & 15) == 0,
              "gs_composite_fwd: clear_records must be 16-byte aligned");
   const int64_t n4_clear = clear_records ? n * kRec / 4 : 0;  // kRec = 12: whole float4s
-#define GS_FWD_LAUNCH(PPT, WPT, WIN)                                                                          \
-  hipLaunchKernelGGL((composite_fwd_kernel<PPT, WIN>), dim3(nblk * (WPT)), dim3(64), 0, s, (const float4*)records, \
-                     (int)n, sorted_gids, n_entries, ranges, width, height, TX, T, background, image, final_T,       \
-                     n_contrib, tile_order, (float4*)clear_records, n4_clear, window)
-  const bool win = window != nullptr;
+#define GS_FWD_LAUNCH1(PPT, WPT, WIN, O32)                                                                    \
+  hipLaunchKernelGGL((composite_fwd_kernel<PPT, WIN, O32>), dim3(nblk * (WPT)), dim3(64), 0, s,                 \
+                     (const float4*)records, (int)n, sorted_gids, n_entries, ranges, width, height, TX, T,        \
+                     background, image, final_T, n_contrib, tile_order, (float4*)clear_records, n4_clear, window)
+#define GS_FWD_LAUNCH(PPT, WPT, WIN) \
+  if (o32) GS_FWD_LAUNCH1(PPT, WPT, WIN, true); else GS_FWD_LAUNCH1(PPT, WPT, WIN, false)
+  const bool win = window != nullptr, o32 = rec_offsets_fit(n);
   if (pick_ppt(T) == 4 && T >= kFwdOneWaveTiles) {
-    if (win) GS_FWD_LAUNCH(4, 1, true); else GS_FWD_LAUNCH(4, 1, false);
+    if (win) { GS_FWD_LAUNCH(4, 1, true); } else { GS_FWD_LAUNCH(4, 1, false); }
   } else if (pick_ppt(T) == 4) {
-    if (win) GS_FWD_LAUNCH(2, 2, true); else GS_FWD_LAUNCH(2, 2, false);
+    if (win) { GS_FWD_LAUNCH(2, 2, true); } else { GS_FWD_LAUNCH(2, 2, false); }
   } else {
-    if (win) GS_FWD_LAUNCH(1, 4, true); else GS_FWD_LAUNCH(1, 4, false);
+    if (win) { GS_FWD_LAUNCH(1, 4, true); } else { GS_FWD_LAUNCH(1, 4, false); }
   }
 #undef GS_FWD_LAUNCH
+#undef GS_FWD_LAUNCH1
   GS_LAUNCH_CHECK("composite_fwd_kernel");
   if (tile_order) {
     hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(1024), 0, s, tile_order, T);
@@ -968,11 +997,23 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
   hipLaunchKernelGGL(KERNEL, dim3(nblk * (WPT)), dim3(64), 0, s, (const float4*)records, (int)n, sorted_gids, n_entries, \
                      ranges, width, height, TX, T, background, grad_image, final_T, n_contrib, grad_records,           \
                      tile_order, window)
-  const bool win = window != nullptr;
+  const bool win = window != nullptr, o32 = rec_offsets_fit(n);
   if (pick_ppt(T) == 4) {
-    if (win) GS_BWD_LAUNCH(composite_bwd_wide_kernel<true>, 1); else GS_BWD_LAUNCH(composite_bwd_wide_kernel<false>, 1);
+    if (o32) {
+      if (win) GS_BWD_LAUNCH((composite_bwd_wide_kernel<true, true>), 1);
+      else GS_BWD_LAUNCH((composite_bwd_wide_kernel<false, true>), 1);
+    } else {
+      if (win) GS_BWD_LAUNCH((composite_bwd_wide_kernel<true, false>), 1);
+      else GS_BWD_LAUNCH((composite_bwd_wide_kernel<false, false>), 1);
+    }
   } else {
-    if (win) GS_BWD_LAUNCH((composite_bwd_kernel<1, true>), 4); else GS_BWD_LAUNCH((composite_bwd_kernel<1, false>), 4);
+    if (o32) {
+      if (win) GS_BWD_LAUNCH((composite_bwd_kernel<1, true, true>), 4);
+      else GS_BWD_LAUNCH((composite_bwd_kernel<1, false, true>), 4);
+    } else {
+      if (win) GS_BWD_LAUNCH((composite_bwd_kernel<1, true, false>), 4);
+      else GS_BWD_LAUNCH((composite_bwd_kernel<1, false, false>), 4);
+    }
   }
 #undef GS_BWD_LAUNCH
   GS_LAUNCH_CHECK("composite_bwd_kernel");

@@ -234,6 +234,52 @@ def test_backward_tile_order(cuda, cfg):
     assert _rel(acc2, 2.0 * out[0][0]) <= 1e-5
 
 
+@pytest.mark.parametrize("w,h", [(504, 378), (1280, 720), (1920, 1080)])
+def test_records_beyond_4gib(cuda, w, h):
+    """Compositing addresses a walked entry's record by its byte offset in a 32-bit
+    register while the records span less than 4 GiB, and by its id beyond.  The same scene
+    placed at the end of a 4.3 GB record array (ids shifted, the other builds) must give
+    the same image, final T and entry counts bit for bit, and the same gradient records up
+    to the order of the atomic additions (one, two and four pixels per lane)."""
+    from jax_gs_amd import _lib
+
+    sc = scenes.make_scene(2, n=20000, width=w, height=h)
+    g, cam, _, mask = scenes.to_torch(sc, cuda)
+    W, H = cam.W, cam.H
+    n_big = (2**32 - 64) // (4 * _lib.GS_REC_STRIDE) + 1  # records past 32-bit byte offsets
+    with torch.no_grad():
+        pre = preprocess(g, cam, mask=mask, sh_degree=sc["sh_degree"])
+        b = rasterizer.bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W,
+                                     want_tiles=False)
+        rec, gids, ranges = pre["records"], b["sorted_gids"], b["ranges"]
+        n = rec.shape[0]
+        shift = n_big - n
+        rec_big = torch.empty((n_big, _lib.GS_REC_STRIDE), device=cuda)
+        rec_big[shift:] = rec
+        gids_big = gids + shift
+        bg = torch.tensor([0.1, 0.2, 0.3], device=cuda)
+        small = rasterizer.composite(rec, gids, ranges, H, W, bg)
+        big = rasterizer.composite(rec_big, gids_big, ranges, H, W, bg)
+        for a, c in zip(small[:3], big[:3]):
+            assert torch.equal(a, c)
+        # the tile order within a bucket of equal cost follows the order of LDS atomics
+        assert torch.equal(torch.sort(small[3]).values, torch.sort(big[3]).values)
+        image, fT, nc, order = small
+        gimg = torch.from_numpy(np.random.default_rng(3).normal(0, 1, (H, W, 3)).astype(np.float32)).to(cuda)
+        grads = []
+        for rr, gg, nn in ((rec, gids, n), (rec_big, gids_big, n_big)):
+            grec = torch.empty((nn, _lib.GS_REC_STRIDE), device=cuda)
+            _lib.call("gs_composite_bwd", _lib.stream_handle(cuda), nn, _lib.ptr(rr), _lib.ptr(gg), gg.shape[0],
+                      _lib.ptr(ranges), W, H, _lib.ptr(bg), _lib.ptr(gimg), _lib.ptr(fT), _lib.ptr(nc),
+                      _lib.ptr(order), _lib.ptr(grec), None, 0, None)
+            grads.append(_np(grec[-n:]))
+            assert nn == n or not grec[:shift].any()
+        del rec_big, grec
+        torch.cuda.empty_cache()
+    assert np.abs(grads[0]).max() > 0
+    assert _rel(grads[1], grads[0]) <= 1e-5
+
+
 def _l1_ssim_gpu(cuda, pred_np, tgt_np, gout):
     from jax_gs_amd import _lib
 
