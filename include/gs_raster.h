@@ -38,10 +38,12 @@ extern "C" {
 
 /* Per-Gaussian compositing record: 12 floats, L = log2(e)
  *   [0]=mean2d.x [1]=mean2d.y [2]=-0.5*ic00*L [3]=-ic01*L [4]=-0.5*ic11*L
- *   [5]=log2(op) [6..8]=colour rgb [9]=op [10]=log2(op) - 10*L [11]=0
+ *   [5]=log2(op) [6..8]=colour rgb [9]=op [10]=log2(op) - 10*L [11]=may_cap
  * where op = sigmoid(opacity) and ic = inverse of cov2D with det clamped to 1e-6
  * (rasterizer.py:147-156), so that alpha = exp2([2]dx^2 + [3]dx dy + [4]dy^2 + [5])
- * and the gate power > -10 is exponent > [10].
+ * and the gate power > -10 is exponent > [10]; may_cap = 0 when op < 0.98 and cov2D is
+ * positive definite (no alpha can reach the 0.99 cap), else 1 (gs_composite_bwd takes
+ * the capped path only for such records).
  * The gradient record produced by gs_composite_bwd holds, with dP = dL/dpower of one
  * (pixel, entry) pair, dx = pixel.x - mean2d.x, dy = pixel.y - mean2d.y, summed over
  * the Gaussian's pairs:

@@ -212,16 +212,16 @@ __device__ inline void tile_span(const int32_t* __restrict__ ranges, int tile, i
 
 // One compositing record (layout of GS_REC_STRIDE floats in gs_raster.h).
 struct Rec {
-  float mx, my, A, B, C, lop, r, g, b, op, thr;
+  float mx, my, A, B, C, lop, r, g, b, op, thr, may_cap;
 };
 
-__device__ inline Rec zero_rec() { return Rec{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}; }
+__device__ inline Rec zero_rec() { return Rec{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}; }
 
 __device__ inline Rec load_rec(const float4* __restrict__ rec, int g) {
   const float4 a = rec[(int64_t)g * 3];
   const float4 b = rec[(int64_t)g * 3 + 1];
   const float4 c = rec[(int64_t)g * 3 + 2];
-  return Rec{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z};
+  return Rec{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w};
 }
 
 // A walked entry's record is addressed by a value read from the testing lane: with O32
@@ -236,7 +236,7 @@ __device__ inline Rec load_rec_key(const float4* __restrict__ rec, int key) {
   if (!O32) return load_rec(rec, key);
   const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(rec) + (uint32_t)key);
   const float4 a = p[0], b = p[1], c = p[2];
-  return Rec{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z};
+  return Rec{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w};
 }
 
 template <bool O32>
@@ -657,16 +657,20 @@ __device__ __forceinline__ void composite_bwd_body(
           dyv[i] = py[i] - e.my;
           qv[i] = q_of(dyv[i], Adx2l, Bdx, e.C);
         }
-        float qmax = qv[0];
-#pragma unroll
-        for (int i = 1; i < PPT; ++i) qmax = fmaxf(qmax, qv[i]);
         if (NOCAP) {
           // alpha of each pixel, capped only when some pixel of the wave can reach the
           // 0.99 cap with this entry (rare): below it min(araw, 0.99) = araw, and the
           // cotangent passes whole, so the body needs no selections; the rare capped
           // entry redoes its power sums with the cap's selections afterwards.  One body
           // for both keeps the per-pixel state (T, Rg) in place across entries.
-          const bool capw = __ballot(qmax >= kBelowCapQ) != 0ull;
+          // (the record's flag first: most records cannot reach the cap at all)
+          bool capw = false;
+          if ((__float_as_uint(e.may_cap) >> 23) != 0u) {  // 1.0f or 0.0f (a scalar compare)
+            float qmax = qv[0];
+#pragma unroll
+            for (int i = 1; i < PPT; ++i) qmax = fmaxf(qmax, qv[i]);
+            capw = __ballot(qmax >= kBelowCapQ) != 0ull;
+          }
           float alv[PPT], wdv[PPT];  // wdv[i] is read only where it was written
 #pragma unroll
           for (int i = 0; i < PPT; ++i) alv[i] = __builtin_amdgcn_exp2f(qv[i]);

@@ -145,10 +145,14 @@ __device__ inline float eval_sh_channel(const float* sh, int c, const float* d) 
   return res;
 }
 
-// rasterizer.py:147-156 and :198 -- record = (mean, -0.5*conic terms, sigmoid, colour).
+// rasterizer.py:147-156 and :198 -- record = (mean, -0.5*conic terms, sigmoid, colour),
+// and a flag that compositing's backward reads: 0 when no pixel's alpha can reach the
+// 0.99 cap (op < 0.98 and cov2D positive definite, so the exponent never exceeds
+// log2(op) beyond rounding), 1 otherwise.
 __device__ inline void write_record(float* __restrict__ rec, float m2x, float m2y, float c00,
                                     float c01, float c11, float logit, const float* col) {
-  const float det = jmax(c00 * c11 - c01 * c01, 1e-6f);
+  const float det_raw = c00 * c11 - c01 * c01;
+  const float det = jmax(det_raw, 1e-6f);
   const float ic00 = c11 / det;
   const float ic01 = (-c01) / det;
   const float ic11 = c00 / det;
@@ -158,7 +162,8 @@ __device__ inline void write_record(float* __restrict__ rec, float m2x, float m2
   float4* r4 = reinterpret_cast<float4*>(rec);
   r4[0] = make_float4(m2x, m2y, (-0.5f * ic00) * kL2E, (-ic01) * kL2E);
   r4[1] = make_float4((-0.5f * ic11) * kL2E, lop, col[0], col[1]);
-  r4[2] = make_float4(col[2], op, lop - 10.0f * kL2E, 0.0f);
+  const float may_cap = (op < 0.98f && det_raw > 0.0f && c00 > 0.0f) ? 0.0f : 1.0f;
+  r4[2] = make_float4(col[2], op, lop - 10.0f * kL2E, may_cap);
 }
 
 // Copies the first COLS floats of rows [g0, g0+64) of a row-major array (row
