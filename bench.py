@@ -353,7 +353,8 @@ def measured_traffic(kernel, config):
 def measured_valu_busy(stage, config):
     """VALU-busy fraction of the stage's kernel from the committed SQ-counter summary of the
     same configuration, and that file; (None, None) when there is none."""
-    kernels = {"composite_bwd": "composite_bwd_wide_kernel<true>", "composite_fwd": "composite_fwd_kernel<4, true>"}
+    kernels = {"composite_bwd": "composite_bwd_wide_kernel<true, true>",
+               "composite_fwd": "composite_fwd_kernel<4, true, true>"}
     path = os.path.join(PROFILES, f"composite_valu_cfg{config}.md")
     if stage not in kernels or not os.path.exists(path):
         return None, None
