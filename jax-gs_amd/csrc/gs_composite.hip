@@ -626,13 +626,14 @@ __device__ __forceinline__ void composite_bwd_body(
       int ga = 0, gb = 0;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        // h = 1 with no survivor left: an empty second half (all sums 0)
-        // live half: k >= 0 (a wave-uniform integer, so the tests below stay scalar)
+        // h = 1 with no survivor left: an empty second half (all sums 0); the first half
+        // always has one (the loop's condition)
         const Rec& e = h == 0 ? ra : rb;
         Rec& ahead = h == 0 ? rb : ra;
         const int g = gn;
-        const int k = m != 0ull ? b0 + jn : -1;
-        if (k >= 0) {
+        const bool live = h == 0 || m != 0ull;
+        const int k = b0 + jn;
+        if (live) {
           // e was requested an entry ago: wait for it before the next request goes out
           // (scalar loads complete out of order)
           __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
@@ -643,14 +644,14 @@ __device__ __forceinline__ void composite_bwd_body(
             ahead = load_rec_key<O32>(rec, gn);
           }
         }
-        if (h == 0) ga = g; else gb = k >= 0 ? g : ga;
+        if (h == 0) ga = g; else gb = live ? g : ga;
         const float dx = px - e.mx;
         const float Adx2l = fmaf(e.A * dx, dx, e.lop), Bdx = e.B * dx;
         // per-lane sums over the lane's pixels: P = sum dpower, Q = sum dpower*dy,
         // V = sum dpower*dy^2, colour cotangents (from -0, so that the first term is
         // the sum itself)
         float P = -0.0f, Q = -0.0f, V = -0.0f, gc0 = -0.0f, gc1 = -0.0f, gc2 = -0.0f;
-        if (k >= 0) {
+        if (live) {
         float dyv[PPT], qv[PPT];
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
@@ -768,7 +769,9 @@ __device__ __forceinline__ void composite_bwd_body(
         s6[h][5] = gc2;
         dxh[h] = dx;
       }
-      if (__ballot(any) != 0ull) {
+      // the four-pixel build reduces every pair (testing for one with no blending pixel
+      // cost more than the reductions it saved: cfg4 217 -> 212 us without the test)
+      if (NOCAP || __ballot(any) != 0ull) {
         const float mine = reduce_scatter_pair9(s6[0], s6[1], dxh[0], dxh[1], lane);
         const int vi = pair9_index(lane);
         if ((lane & 1) == 0 && vi < 9 && mine != 0.0f)
