@@ -423,37 +423,49 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
         m &= ~(1ull << ja);
         ra = load_rec_key<O32>(rec, bcast_i(gk, ja));
       }
-      while (ja >= 0) {
-        if (all_closed()) {
+      // survivors in groups of 8 (four rounds of the two registers), the wave's exit test
+      // once per group: no per-entry bookkeeping for it
+      bool more = ja >= 0;
+      while (more) {
+        bool live = false;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) live = live || Tr[i] > kTMin;
+        if (__ballot(live) == 0ull) {
           done = true;
           break;
         }
-        // ra's record was requested a whole entry ago: wait for it before the next
-        // request goes out (scalar loads complete out of order, so a wait at its first
-        // use would also wait for the request issued just before)
-        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-        jb = -1;
-        if (m != 0ull) {
-          jb = __builtin_ctzll(m);
-          m &= ~(1ull << jb);
-          rb = load_rec_key<O32>(rec, bcast_i(gk, jb));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          // ra's record was requested a whole entry ago: wait for it before the next
+          // request goes out (scalar loads complete out of order, so a wait at its first
+          // use would also wait for the request issued just before)
+          __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+          jb = -1;
+          if (m != 0ull) {
+            jb = __builtin_ctzll(m);
+            m &= ~(1ull << jb);
+            rb = load_rec_key<O32>(rec, bcast_i(gk, jb));
+          }
+          ++walked;
+          blend(ra, ja);
+          if (jb < 0) {
+            more = false;
+            break;
+          }
+          __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+          ja = -1;
+          if (m != 0ull) {
+            ja = __builtin_ctzll(m);
+            m &= ~(1ull << ja);
+            ra = load_rec_key<O32>(rec, bcast_i(gk, ja));
+          }
+          ++walked;
+          blend(rb, jb);
+          if (ja < 0) {
+            more = false;
+            break;
+          }
         }
-        ++walked;
-        blend(ra, ja);
-        if (jb < 0) break;
-        if (all_closed()) {
-          done = true;
-          break;
-        }
-        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-        ja = -1;
-        if (m != 0ull) {
-          ja = __builtin_ctzll(m);
-          m &= ~(1ull << ja);
-          ra = load_rec_key<O32>(rec, bcast_i(gk, ja));
-        }
-        ++walked;
-        blend(rb, jb);
       }
     } else {
     Rec r[G];
