@@ -691,12 +691,15 @@ __device__ __forceinline__ void composite_bwd_body(
 #pragma unroll
             for (int i = 0; i < PPT; ++i) alv[i] = alv[i] < 0.99f ? alv[i] : 0.99f;
           }
+          // Pixel 0 runs for every lane, with alpha 0 where it does not blend (1/T and Rg
+          // keep their values, the sums get +0): its sums need no clearing per entry.
 #pragma unroll
           for (int i = 0; i < PPT; ++i) {
             const float dy = dyv[i];
-            if (k < kp[i] && qv[i] > e.thr) {
-              any = true;
-              const float al = alv[i];
+            const bool blends = k < kp[i] && qv[i] > e.thr;
+            if (i == 0 || blends) {
+              any = any || blends;
+              const float al = i == 0 ? (blends ? alv[0] : 0.0f) : alv[i];
               // 1/T_k = (1 - alpha) / T_{k+1}, one rounding; T_k from it by rcp, which
               // does not feed back into the recursion
               const float iTk = fmaf(-al, Tr[i], Tr[i]);
