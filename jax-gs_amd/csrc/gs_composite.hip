@@ -359,7 +359,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
   const float ry0 = (float)(ty * kTile + part * 4 * PPT) + 0.5f, ry1 = ry0 + (float)(4 * PPT - 1);
 
   bool done = false;
-  int walked = 0, next_check = 8;
+  int walked = 0;
   const int64_t thr = WIN ? win->thr : 0;
   // The batch's probe records were requested a batch ago; the next batch's go out after
   // the batch's test, so that the test waits for nothing requested since (loads complete
@@ -403,15 +403,6 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
         Tr[i] = Tr[i] - w;  // T (1 - alpha)
         cnt[i] = act ? kk : cnt[i];
       }
-    };
-    // every 8 walked entries: stop when no pixel of the wave is still open
-    auto all_closed = [&]() {
-      if (walked < next_check) return false;
-      next_check = walked + 8;
-      bool live = false;
-#pragma unroll
-      for (int i = 0; i < PPT; ++i) live = live || Tr[i] > kTMin;
-      return __ballot(live) == 0ull;
     };
     if constexpr (G == 1) {
       // one entry at a time, the next survivor's record requested before the blend; two
@@ -468,62 +459,78 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
         }
       }
     } else {
-    Rec r[G];
-    int j[G];
+      // one pixel per lane: survivors in pairs, both records requested together a pair
+      // ahead, two pairs of record registers used in turn, the exit test once per 8
+      auto take = [&](Rec* r, int* j) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      r[h] = zero_rec();
-      j[h] = -1;
-      if (m != 0ull) {
-        j[h] = __builtin_ctzll(m);
-        m &= m - 1ull;
-        r[h] = load_rec_key<O32>(rec, bcast_i(gk, j[h]));
-      }
-    }
-    while (j[0] >= 0) {
-      if (all_closed()) {
-        done = true;
-        break;
-      }
-      Rec e[G];
-      int k[G];
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        e[h] = r[h];
-        k[h] = j[h];
-        j[h] = -1;
-        if (m != 0ull) {
-          j[h] = __builtin_ctzll(m);
-          m &= m - 1ull;
-          r[h] = load_rec_key<O32>(rec, bcast_i(gk, j[h]));
+        for (int h = 0; h < G; ++h) {
+          j[h] = -1;
+          if (m != 0ull) {
+            j[h] = __builtin_ctzll(m);
+            m &= ~(1ull << j[h]);
+            r[h] = load_rec_key<O32>(rec, bcast_i(gk, j[h]));
+          }
         }
-      }
+      };
+      auto blend_pair = [&](const Rec* e, const int* k) {
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        if (k[h] < 0) break;
-        ++walked;
-        const int kk = b0 + k[h] + 1;  // entries met so far, this one included
-        const float dx = px - e[h].mx;
-        const float Adx2l = fmaf(e[h].A * dx, dx, e[h].lop), Bdx = e[h].B * dx;
+        for (int h = 0; h < G; ++h) {
+          if (k[h] < 0) break;
+          ++walked;
+          const int kk = b0 + k[h] + 1;  // entries met so far, this one included
+          const float dx = px - e[h].mx;
+          const float Adx2l = fmaf(e[h].A * dx, dx, e[h].lop), Bdx = e[h].B * dx;
 #pragma unroll
-        for (int i = 0; i < PPT; ++i) {
-          const float q = q_of(py[i] - e[h].my, Adx2l, Bdx, e[h].C);
-          const bool act = Tr[i] > kTMin;  // rasterizer.py:206
-          cnt[i] = act ? kk : cnt[i];
-          // one pixel per lane: only the lanes that pass run the blend (the wave skips it
-          // when none does; cfg1 187 -> 180 us against the branch-free form)
-          if (act && q > e[h].thr) {  // rasterizer.py:212
-            float al = __builtin_amdgcn_exp2f(q);
-            al = al < 0.99f ? al : 0.99f;
-            const float w = al * Tr[i];
-            c0[i] = fmaf(w, e[h].r, c0[i]);
-            c1[i] = fmaf(w, e[h].g, c1[i]);
-            c2[i] = fmaf(w, e[h].b, c2[i]);
-            Tr[i] = Tr[i] - w;  // T (1 - alpha)
+          for (int i = 0; i < PPT; ++i) {
+            const float q = q_of(py[i] - e[h].my, Adx2l, Bdx, e[h].C);
+            const bool act = Tr[i] > kTMin;  // rasterizer.py:206
+            cnt[i] = act ? kk : cnt[i];
+            // one pixel per lane: only the lanes that pass run the blend (the wave skips it
+            // when none does; cfg1 187 -> 180 us against the branch-free form)
+            if (act && q > e[h].thr) {  // rasterizer.py:212
+              float al = __builtin_amdgcn_exp2f(q);
+              al = al < 0.99f ? al : 0.99f;
+              const float w = al * Tr[i];
+              c0[i] = fmaf(w, e[h].r, c0[i]);
+              c1[i] = fmaf(w, e[h].g, c1[i]);
+              c2[i] = fmaf(w, e[h].b, c2[i]);
+              Tr[i] = Tr[i] - w;  // T (1 - alpha)
+            }
+          }
+        }
+      };
+      Rec ra[G], rb[G];
+      int ja[G], jb[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) ra[h] = rb[h] = zero_rec();
+      take(ra, ja);
+      bool more = ja[0] >= 0;
+      while (more) {
+        bool live = false;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) live = live || Tr[i] > kTMin;
+        if (__ballot(live) == 0ull) {
+          done = true;
+          break;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+          take(rb, jb);
+          blend_pair(ra, ja);
+          if (jb[0] < 0) {
+            more = false;
+            break;
+          }
+          __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+          take(ra, ja);
+          blend_pair(rb, jb);
+          if (ja[0] < 0) {
+            more = false;
+            break;
           }
         }
       }
-    }
     }
   }
   const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];
