@@ -77,7 +77,8 @@ const char* gs_last_error(void);
  * clear_records, gs_composite_bwd accumulate.  5: gs_composite_fwd takes window_rule.
  * 6: gs_composite_fwd/bwd take a gs_window_t in place of window_rule; gs_window_from_list,
  * gs_window_from_bins; GS_STAT_WINDOW_CLAMPED.  7: gs_preprocess_bwd_w2c, gs_eval_sh,
- * gs_eval_sh_bwd.  8: gs_l1_ssim_window, gs_l1_ssim_window_bwd. */
+ * gs_eval_sh_bwd.  8: gs_l1_ssim_window, gs_l1_ssim_window_bwd.  9: compositing records carry
+ * may_cap in slot 11 (gs_composite_bwd reads it; records of an earlier build hold 0 there). */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
