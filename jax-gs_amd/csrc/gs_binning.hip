@@ -290,35 +290,44 @@ __global__ __launch_bounds__(64) void radix_upsweep_kernel(const uint32_t* __res
 
 // One block per digit: exclusive scan of that digit's row of the table (over the G
 // workgroups) in place, and the digit's total.  Rows of up to kSpineMax entries move
-// through LDS with coalesced loads and stores; each thread scans a contiguous run.
+// through LDS with coalesced loads and stores; each thread scans a contiguous run.  The
+// LDS copy is skewed by one word per 32 (entry k at k + k / 32): the runs start `per`
+// words apart, which unskewed put a wave's reads on two banks when per is 16 (the
+// superblock pass at 1M Gaussians: 3907 workgroups).
 constexpr int kSpineMax = 8192;
+__device__ inline int spine_at(int k) { return k + (k >> 5); }
 __global__ __launch_bounds__(kScanBlock) void radix_spine_kernel(uint32_t* __restrict__ table, int G,
                                                                  uint32_t* __restrict__ digit_tot) {
-  __shared__ uint32_t row_s[kSpineMax];
+  __shared__ uint32_t row_s[kSpineMax + kSpineMax / 32];
   const int d = blockIdx.x;
   uint32_t* row = table + (int64_t)d * G;
-  const bool staged = G <= kSpineMax;
-  uint32_t* r = staged ? row_s : row;
-  if (staged) {
-    for (int k = threadIdx.x; k < G; k += kScanBlock) row_s[k] = row[k];
-    __syncthreads();
-  }
   const int per = (G + kScanBlock - 1) / kScanBlock;
   const int b0 = threadIdx.x * per;
-  uint32_t s = 0;
-  for (int k = 0; k < per; ++k)
-    if (b0 + k < G) s += r[b0 + k];
-  uint32_t tot;
-  uint32_t run = block_excl_scan<kScanBlock>(s, &tot);
-  for (int k = 0; k < per; ++k)
-    if (b0 + k < G) {
-      const uint32_t v = r[b0 + k];
-      r[b0 + k] = run;
-      run += v;
-    }
-  if (staged) {
+  uint32_t s = 0, tot;
+  if (G <= kSpineMax) {
+    for (int k = threadIdx.x; k < G; k += kScanBlock) row_s[spine_at(k)] = row[k];
     __syncthreads();
-    for (int k = threadIdx.x; k < G; k += kScanBlock) row[k] = row_s[k];
+    for (int k = 0; k < per; ++k)
+      if (b0 + k < G) s += row_s[spine_at(b0 + k)];
+    uint32_t run = block_excl_scan<kScanBlock>(s, &tot);
+    for (int k = 0; k < per; ++k)
+      if (b0 + k < G) {
+        const uint32_t v = row_s[spine_at(b0 + k)];
+        row_s[spine_at(b0 + k)] = run;
+        run += v;
+      }
+    __syncthreads();
+    for (int k = threadIdx.x; k < G; k += kScanBlock) row[k] = row_s[spine_at(k)];
+  } else {
+    for (int k = 0; k < per; ++k)
+      if (b0 + k < G) s += row[b0 + k];
+    uint32_t run = block_excl_scan<kScanBlock>(s, &tot);
+    for (int k = 0; k < per; ++k)
+      if (b0 + k < G) {
+        const uint32_t v = row[b0 + k];
+        row[b0 + k] = run;
+        run += v;
+      }
   }
   if (threadIdx.x == 0) digit_tot[d] = tot;
 }
