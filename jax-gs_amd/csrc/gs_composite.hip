@@ -138,10 +138,14 @@ __device__ inline void halve_level(float* cur, int lane) {
       cur[k] = add_swap16(lo, hi);
     } else if (D == 8 || D == 4) {
       cur[k] = add_banked<D>(lo, hi, has_hi);
-    } else {  // D == 2
+    } else if (D == 2) {
       const bool bit = (lane >> 1) & 1;
       const float keep = bit ? hi : lo, send = bit ? lo : hi;
       cur[k] = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x4E, 0xF, 0xF, false));
+    } else {  // D == 1
+      const bool bit = lane & 1;
+      const float keep = bit ? hi : lo, send = bit ? lo : hi;
+      cur[k] = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0xB1, 0xF, 0xF, false));
     }
   }
 }
@@ -173,6 +177,52 @@ __device__ inline float reduce_scatter_pair9(const float* sa, const float* sb, f
   halve_level<2, 2>(v, lane);
   const float t = v[0];
   return t + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0xB1, 0xF, 0xF, false));
+}
+
+// The reduce-scatter of four walked entries (the four-pixel build).  The first level runs
+// per pair of entries as soon as the pair is walked (lane bit 5 keeps entry 0 of the pair,
+// else entry 1), so only one pair's twelve sums are live at a time; the second (distance
+// 16) keeps pair 0 where lane bit 4 is clear.  Lanes l, l ^ 16, l ^ 32 and l ^ 48 share
+// the column, so after these two levels each lane holds the column sums of entry
+// quad_entry(l) = 2 bit4 + bit5; it expands them into the record's nine values and the
+// levels 8 .. 1 reduce-scatter those over the 16 lanes of the entry: lane l ends with the
+// total of record value quad9_index(l) (bit-reversed low four bits; 9 .. 15 hold nothing).
+// Per entry this takes about 16 VALU instructions against about 22 for two entries at a
+// time.
+__device__ inline int quad_entry(int l) { return ((l >> 3) & 2) | ((l >> 5) & 1); }
+__device__ inline int quad9_index(int l) { return ((l & 1) << 3) | ((l & 2) << 1) | ((l >> 1) & 2) | ((l >> 3) & 1); }
+
+__device__ inline void pair_level32(const float* sa, const float* sb, float* out) {
+  float cur[12];
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    cur[2 * k] = sa[k];
+    cur[2 * k + 1] = sb[k];
+  }
+  halve_level<32, 12>(cur, 0);
+#pragma unroll
+  for (int k = 0; k < 6; ++k) out[k] = cur[k];
+}
+
+__device__ inline float reduce_scatter_quad9(const float* p0, const float* p1, float dx0, float dx1, float dx2,
+                                             float dx3, int lane) {
+  float cur[12];
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    cur[2 * k] = p0[k];
+    cur[2 * k + 1] = p1[k];
+  }
+  halve_level<16, 12>(cur, lane);
+  const bool b4 = (lane >> 4) & 1, b5 = (lane >> 5) & 1;
+  const float dx01 = b5 ? dx1 : dx0, dx23 = b5 ? dx3 : dx2;
+  const float dx = b4 ? dx23 : dx01;
+  const float Sx = cur[0] * dx;
+  float v[9] = {Sx, cur[1], Sx * dx, cur[1] * dx, cur[2], cur[0], cur[3], cur[4], cur[5]};
+  halve_level<8, 9>(v, lane);
+  halve_level<4, 5>(v, lane);
+  halve_level<2, 3>(v, lane);
+  halve_level<1, 2>(v, lane);
+  return v[0];
 }
 
 // XCD-aware tile order. Consecutive workgroups go round-robin to the 8 XCDs. The tile grid,
@@ -618,8 +668,9 @@ __device__ __forceinline__ void composite_bwd_body(
   // the highest down, ids from the testing lane, records by scalar loads, prefetched
   const float rx0 = (float)(tx * kTile) + 0.5f, rx1 = rx0 + (float)(kTile - 1);
   const float ry0 = (float)(ty * kTile + part * 4 * PPT) + 0.5f, ry1 = ry0 + (float)(4 * PPT - 1);
-  // survivors are walked two at a time and their 9 + 9 sums reduced together (one
-  // 18-value reduce-scatter costs fewer cross-lane steps than two 9-value ones)
+  // survivors are walked four at a time (four-pixel build) or two at a time and their
+  // sums reduced together (one reduce-scatter of several entries' sums costs fewer
+  // cross-lane steps per entry than one per entry)
   const int btop = (kmax - 1) & ~63;
   const int64_t thr = WIN ? win->thr : 0;
   Ahead g_ahead = probe_gid_ahead<WIN>(gids, start, btop - 64 + lane, kmax, win, thr);
@@ -640,15 +691,17 @@ __device__ __forceinline__ void composite_bwd_body(
       ra = load_rec_key<O32>(rec, gn);
     }
     while (m != 0ull) {
-      float s6[2][6], dxh[2];
+      // entries per reduce-scatter: four in the four-pixel build, two in the other
+      constexpr int E = NOCAP ? 4 : 2;
+      float s6[E][6], dxh[E], p0[6];
       bool any = false;
-      int ga = 0, gb = 0;
+      int gh[E];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        // h = 1 with no survivor left: an empty second half (all sums 0); the first half
-        // always has one (the loop's condition)
-        const Rec& e = h == 0 ? ra : rb;
-        Rec& ahead = h == 0 ? rb : ra;
+      for (int h = 0; h < E; ++h) {
+        // h > 0 with no survivor left: an empty entry (all sums 0); the first always has
+        // one (the loop's condition)
+        const Rec& e = (h & 1) == 0 ? ra : rb;
+        Rec& ahead = (h & 1) == 0 ? rb : ra;
         const int g = gn;
         const bool live = h == 0 || m != 0ull;
         const int k = b0 + jn;
@@ -663,7 +716,7 @@ __device__ __forceinline__ void composite_bwd_body(
             ahead = load_rec_key<O32>(rec, gn);
           }
         }
-        if (h == 0) ga = g; else gb = live ? g : ga;
+        gh[h] = (h == 0 || live) ? g : gh[0];
         const float dx = px - e.mx;
         const float Adx2l = fmaf(e.A * dx, dx, e.lop), Bdx = e.B * dx;
         // per-lane sums over the lane's pixels: P = sum dpower, Q = sum dpower*dy,
@@ -790,14 +843,25 @@ __device__ __forceinline__ void composite_bwd_body(
         s6[h][4] = gc1;
         s6[h][5] = gc2;
         dxh[h] = dx;
+        if (E == 4 && h == 1) pair_level32(s6[0], s6[1], p0);
       }
-      // the four-pixel build reduces every pair (testing for one with no blending pixel
-      // cost more than the reductions it saved: cfg4 217 -> 212 us without the test)
-      if (NOCAP || __ballot(any) != 0ull) {
+      if constexpr (E == 4) {
+        // the four-pixel build reduces every group (testing for one with no blending pixel
+        // cost more than the reductions it saved: cfg4 217 -> 212 us without the test)
+        float p1[6];
+        pair_level32(s6[2], s6[3], p1);
+        const float mine = reduce_scatter_quad9(p0, p1, dxh[0], dxh[1], dxh[2], dxh[E - 1], lane);
+        const int vi = quad9_index(lane);
+        // the record of entry quad_entry(lane) = 2 bit4 + bit5
+        const bool b4 = (lane >> 4) & 1, b5 = (lane >> 5) & 1;
+        const int g01 = b5 ? gh[1] : gh[0], g23 = b5 ? gh[E - 1] : gh[2];
+        const int gq = b4 ? g23 : g01;
+        if (vi < 9 && mine != 0.0f) atomicAdd(grec_at<O32>(grec, gq, vi), mine);
+      } else if (__ballot(any) != 0ull) {
         const float mine = reduce_scatter_pair9(s6[0], s6[1], dxh[0], dxh[1], lane);
         const int vi = pair9_index(lane);
         if ((lane & 1) == 0 && vi < 9 && mine != 0.0f)
-          atomicAdd(grec_at<O32>(grec, (lane & 32) ? gb : ga, vi), mine);
+          atomicAdd(grec_at<O32>(grec, (lane & 32) ? gh[1] : gh[0], vi), mine);
       }
     }
   }
@@ -813,18 +877,20 @@ __device__ __forceinline__ void composite_bwd_body(
 // The backward's two builds.  One pixel per lane (images below 2048 tiles, four waves per
 // tile): 64 VGPRs, 8 waves per SIMD, the general body only (the no-cap path's per-entry test
 // costs more than it saves with one pixel per lane: cfg0 169 -> 174 us, cfg1 230 -> 236).
-// Four pixels per lane: scheduled for 6 waves per SIMD (at most 80 VGPRs) with the no-cap
-// body, which beats the 64-VGPR build without it at every size (cfg2, 8160 tiles: 306 vs
-// 332 us; cfg4, 3600 tiles: 233 vs 248; cfg3: 198 vs 207); one body with the cap applied in
-// place and the 1/T state took cfg2 from 310 to 304 us (8 % fewer VALU instructions, the
-// copies of the state between two bodies gone).  WIN: the default path's chunk windows, as
-// the forward read them.
+// Four pixels per lane: the no-cap body, which beats the 64-VGPR build without it at every
+// size (cfg2, 8160 tiles: 306 vs 332 us; cfg4, 3600 tiles: 233 vs 248; cfg3: 198 vs 207);
+// one body with the cap applied in place and the 1/T state took cfg2 from 310 to 304 us
+// (8 % fewer VALU instructions, the copies of the state between two bodies gone).  Its
+// reduce-scatter takes four walked entries at a time, which needs 91 VGPRs, so the build
+// is scheduled for 5 waves per SIMD (at 6, 80 VGPRs, it spilled): cfg2 285 -> 273 us and
+// cfg4 223 -> 214 against two entries at 6 waves per SIMD.  WIN: the default path's chunk
+// windows, as the forward read them.
 template <int PPT, bool WIN, bool O32>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void composite_bwd_kernel(GS_BWD_PARAMS) {
   composite_bwd_body<PPT, WIN, false, O32>(GS_BWD_ARGS);
 }
 template <bool WIN, bool O32>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6, 6))) void composite_bwd_wide_kernel(GS_BWD_PARAMS) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5, 5))) void composite_bwd_wide_kernel(GS_BWD_PARAMS) {
   composite_bwd_body<4, WIN, true, O32>(GS_BWD_ARGS);
 }
 #undef GS_BWD_PARAMS
