@@ -691,8 +691,8 @@ __device__ __forceinline__ void composite_bwd_body(
       ra = load_rec_key<O32>(rec, gn);
     }
     while (m != 0ull) {
-      // entries per reduce-scatter: four in the four-pixel build, two in the other
-      constexpr int E = NOCAP ? 4 : 2;
+      // entries per reduce-scatter: four in the four- and one-pixel builds, two otherwise
+      constexpr int E = (NOCAP || PPT == 1) ? 4 : 2;
       float s6[E][6], dxh[E], p0[6];
       bool any = false;
       int gh[E];
@@ -847,7 +847,9 @@ __device__ __forceinline__ void composite_bwd_body(
       }
       if constexpr (E == 4) {
         // the four-pixel build reduces every group (testing for one with no blending pixel
-        // cost more than the reductions it saved: cfg4 217 -> 212 us without the test)
+        // cost more than the reductions it saved: cfg4 217 -> 212 us without the test); the
+        // one-pixel build skips groups that blend nothing
+        if (!NOCAP && __ballot(any) == 0ull) continue;
         float p1[6];
         pair_level32(s6[2], s6[3], p1);
         const float mine = reduce_scatter_quad9(p0, p1, dxh[0], dxh[1], dxh[2], dxh[E - 1], lane);
@@ -876,7 +878,9 @@ __device__ __forceinline__ void composite_bwd_body(
 
 // The backward's two builds.  One pixel per lane (images below 2048 tiles, four waves per
 // tile): 64 VGPRs, 8 waves per SIMD, the general body only (the no-cap path's per-entry test
-// costs more than it saves with one pixel per lane: cfg0 169 -> 174 us, cfg1 230 -> 236).
+// costs more than it saves with one pixel per lane: cfg0 169 -> 174 us, cfg1 230 -> 236), four
+// walked entries per reduce-scatter (skipped when none of them blends a pixel of the wave):
+// cfg0 154 -> 142 us, cfg1 210 -> 199 against two.
 // Four pixels per lane: the no-cap body, which beats the 64-VGPR build without it at every
 // size (cfg2, 8160 tiles: 306 vs 332 us; cfg4, 3600 tiles: 233 vs 248; cfg3: 198 vs 207);
 // one body with the cap applied in place and the 1/T state took cfg2 from 310 to 304 us
