@@ -150,39 +150,12 @@ __device__ inline void halve_level(float* cur, int lane) {
   }
 }
 
-// The backward's reduce-scatter of two walked entries.  Per entry a lane holds six sums
-// over its pixels, (P, Q, V, c0, c1, c2) = sum dpower, sum dpower dy, sum dpower dy^2 and the
-// colour cotangents, all for its own column dx = px - mean.x.  Lanes l and l ^ 32 share the
-// column, so the first level pairs entry a's values with entry b's (lane bit 5 keeps the
-// entry) before the column factor is applied: each lane then expands its entry's six column
-// sums into the record's nine, (P dx, Q, P dx^2, Q dx, V, P, c0, c1, c2), and the levels 16 ..
-// 1 reduce-scatter those.  Lane l ends with the total of record value
-// pair9_index(l) of entry (l >> 5) & 1, the same in lanes l and l ^ 1.
-__device__ inline int pair9_index(int l) { return ((l >> 4) & 1) | ((l >> 2) & 2) | (l & 4) | ((l << 2) & 8); }
-
-__device__ inline float reduce_scatter_pair9(const float* sa, const float* sb, float dxa, float dxb, int lane) {
-  float cur[12];
-#pragma unroll
-  for (int k = 0; k < 6; ++k) {
-    cur[2 * k] = sa[k];
-    cur[2 * k + 1] = sb[k];
-  }
-  halve_level<32, 12>(cur, lane);
-  const float dx = (lane & 32) ? dxb : dxa;
-  const float Sx = cur[0] * dx;
-  float v[9] = {Sx, cur[1], Sx * dx, cur[1] * dx, cur[2], cur[0], cur[3], cur[4], cur[5]};
-  halve_level<16, 9>(v, lane);
-  halve_level<8, 5>(v, lane);
-  halve_level<4, 3>(v, lane);
-  halve_level<2, 2>(v, lane);
-  const float t = v[0];
-  return t + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0xB1, 0xF, 0xF, false));
-}
-
-// The reduce-scatter of four walked entries (the four-pixel build).  The first level runs
-// per pair of entries as soon as the pair is walked (lane bit 5 keeps entry 0 of the pair,
-// else entry 1), so only one pair's twelve sums are live at a time; the second (distance
-// 16) keeps pair 0 where lane bit 4 is clear.  Lanes l, l ^ 16, l ^ 32 and l ^ 48 share
+// The backward's reduce-scatter of four walked entries.  Per entry a lane holds six sums
+// over its pixels, (P, Q, V, c0, c1, c2) = sum dpower, sum dpower dy, sum dpower dy^2 and
+// the colour cotangents, all for its own column dx = px - mean.x.  The first level runs per
+// pair of entries as soon as the pair is walked (lane bit 5 keeps entry 0 of the pair, else
+// entry 1), so only one pair's twelve sums are live at a time; the second (distance 16)
+// keeps pair 0 where lane bit 4 is clear.  Lanes l, l ^ 16, l ^ 32 and l ^ 48 share
 // the column, so after these two levels each lane holds the column sums of entry
 // quad_entry(l) = 2 bit4 + bit5; it expands them into the record's nine values and the
 // levels 8 .. 1 reduce-scatter those over the 16 lanes of the entry: lane l ends with the
@@ -691,8 +664,7 @@ __device__ __forceinline__ void composite_bwd_body(
       ra = load_rec_key<O32>(rec, gn);
     }
     while (m != 0ull) {
-      // entries per reduce-scatter: four in the four- and one-pixel builds, two otherwise
-      constexpr int E = (NOCAP || PPT == 1) ? 4 : 2;
+      constexpr int E = 4;  // walked entries per reduce-scatter
       float s6[E][6], dxh[E], p0[6];
       bool any = false;
       int gh[E];
@@ -843,28 +815,21 @@ __device__ __forceinline__ void composite_bwd_body(
         s6[h][4] = gc1;
         s6[h][5] = gc2;
         dxh[h] = dx;
-        if (E == 4 && h == 1) pair_level32(s6[0], s6[1], p0);
+        if (h == 1) pair_level32(s6[0], s6[1], p0);
       }
-      if constexpr (E == 4) {
-        // the four-pixel build reduces every group (testing for one with no blending pixel
-        // cost more than the reductions it saved: cfg4 217 -> 212 us without the test); the
-        // one-pixel build skips groups that blend nothing
-        if (!NOCAP && __ballot(any) == 0ull) continue;
-        float p1[6];
-        pair_level32(s6[2], s6[3], p1);
-        const float mine = reduce_scatter_quad9(p0, p1, dxh[0], dxh[1], dxh[2], dxh[E - 1], lane);
-        const int vi = quad9_index(lane);
-        // the record of entry quad_entry(lane) = 2 bit4 + bit5
-        const bool b4 = (lane >> 4) & 1, b5 = (lane >> 5) & 1;
-        const int g01 = b5 ? gh[1] : gh[0], g23 = b5 ? gh[E - 1] : gh[2];
-        const int gq = b4 ? g23 : g01;
-        if (vi < 9 && mine != 0.0f) atomicAdd(grec_at<O32>(grec, gq, vi), mine);
-      } else if (__ballot(any) != 0ull) {
-        const float mine = reduce_scatter_pair9(s6[0], s6[1], dxh[0], dxh[1], lane);
-        const int vi = pair9_index(lane);
-        if ((lane & 1) == 0 && vi < 9 && mine != 0.0f)
-          atomicAdd(grec_at<O32>(grec, (lane & 32) ? gh[1] : gh[0], vi), mine);
-      }
+      // the four-pixel build reduces every group (testing for one with no blending pixel
+      // cost more than the reductions it saved: cfg4 217 -> 212 us without the test); the
+      // one-pixel build skips groups that blend nothing
+      if (!NOCAP && __ballot(any) == 0ull) continue;
+      float p1[6];
+      pair_level32(s6[2], s6[3], p1);
+      const float mine = reduce_scatter_quad9(p0, p1, dxh[0], dxh[1], dxh[2], dxh[3], lane);
+      const int vi = quad9_index(lane);
+      // the record of entry quad_entry(lane) = 2 bit4 + bit5
+      const bool b4 = (lane >> 4) & 1, b5 = (lane >> 5) & 1;
+      const int g01 = b5 ? gh[1] : gh[0], g23 = b5 ? gh[3] : gh[2];
+      const int gq = b4 ? g23 : g01;
+      if (vi < 9 && mine != 0.0f) atomicAdd(grec_at<O32>(grec, gq, vi), mine);
     }
   }
 }
