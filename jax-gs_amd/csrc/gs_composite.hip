@@ -36,10 +36,11 @@
 // T_k = T_{k+1} / (1 - alpha_k) and the colour behind entry k projected on the
 // pixel's image cotangent g, Rg_{k-1} = alpha_k (c_k . g) + (1 - alpha_k) Rg_k, so
 // dL/dalpha_k = T_k (c_k . g - Rg_k).  Per lane the entry's power cotangents are kept
-// as sums that the lane's pixels (one column, one dx) share; the 9 sums of two
-// contributing entries are reduce-scattered across the wave together (recursive
-// halving, so each of 18 lanes ends with the total of one sum) and added to the Gaussians'
-// gradient records with one atomic instruction (18 lanes).  Gradients follow JAX autodiff of the reference: the cap
+// as sums that the lane's pixels (one column, one dx) share; the 9 sums of four
+// walked entries are reduce-scattered across the wave together (recursive halving, so
+// each of 36 lanes ends with the total of one sum) and added to the Gaussians' gradient
+// records with one atomic instruction (36 lanes).  Gradients follow JAX autodiff of the
+// reference: the cap
 // min(0.99, .) passes no gradient when it binds (half at a tie), gated entries pass
 // none.
 #include "gs_common.h"
@@ -641,9 +642,9 @@ __device__ __forceinline__ void composite_bwd_body(
   // the highest down, ids from the testing lane, records by scalar loads, prefetched
   const float rx0 = (float)(tx * kTile) + 0.5f, rx1 = rx0 + (float)(kTile - 1);
   const float ry0 = (float)(ty * kTile + part * 4 * PPT) + 0.5f, ry1 = ry0 + (float)(4 * PPT - 1);
-  // survivors are walked four at a time (four-pixel build) or two at a time and their
-  // sums reduced together (one reduce-scatter of several entries' sums costs fewer
-  // cross-lane steps per entry than one per entry)
+  // survivors are walked four at a time and their sums reduced together (one
+  // reduce-scatter of several entries' sums costs fewer cross-lane steps per entry than
+  // one per entry)
   const int btop = (kmax - 1) & ~63;
   const int64_t thr = WIN ? win->thr : 0;
   Ahead g_ahead = probe_gid_ahead<WIN>(gids, start, btop - 64 + lane, kmax, win, thr);
