@@ -289,11 +289,13 @@ __global__ __launch_bounds__(64) void radix_upsweep_kernel(const uint32_t* __res
 }
 
 // One block per digit: exclusive scan of that digit's row of the table (over the G
-// workgroups) in place, and the digit's total.  Rows of up to kSpineMax entries move
-// through LDS with coalesced loads and stores; each thread scans a contiguous run.  The
-// LDS copy is skewed by one word per 32 (entry k at k + k / 32): the runs start `per`
-// words apart, which unskewed put a wave's reads on two banks when per is 16 (the
-// superblock pass at 1M Gaussians: 3907 workgroups).
+// workgroups) in place, and the digit's total.  The row moves through LDS in pieces of up to
+// kSpineMax entries with coalesced loads and stores (a running carry joins the pieces); each
+// thread scans a contiguous run of a piece.  The LDS copy is skewed by one word per 32
+// (entry k at k + k / 32): the runs start `per` words apart, which unskewed put a wave's
+// reads on two banks when per is 16 (the superblock pass at 1M Gaussians: 3907 workgroups).
+// Rows longer than one piece (the superblock pass above 2M Gaussians: 11,719 workgroups at
+// 3M) were scanned from global memory by the threads' runs, uncoalesced: 33 us at 3M.
 constexpr int kSpineMax = 8192;
 __device__ inline int spine_at(int k) { return k + (k >> 5); }
 __global__ __launch_bounds__(kScanBlock) void radix_spine_kernel(uint32_t* __restrict__ table, int G,
@@ -301,35 +303,29 @@ __global__ __launch_bounds__(kScanBlock) void radix_spine_kernel(uint32_t* __res
   __shared__ uint32_t row_s[kSpineMax + kSpineMax / 32];
   const int d = blockIdx.x;
   uint32_t* row = table + (int64_t)d * G;
-  const int per = (G + kScanBlock - 1) / kScanBlock;
-  const int b0 = threadIdx.x * per;
-  uint32_t s = 0, tot;
-  if (G <= kSpineMax) {
-    for (int k = threadIdx.x; k < G; k += kScanBlock) row_s[spine_at(k)] = row[k];
+  uint32_t carry = 0;
+  for (int c0 = 0; c0 < G; c0 += kSpineMax) {
+    const int len = G - c0 < kSpineMax ? G - c0 : kSpineMax;
+    for (int k = threadIdx.x; k < len; k += kScanBlock) row_s[spine_at(k)] = row[c0 + k];
     __syncthreads();
+    const int per = (len + kScanBlock - 1) / kScanBlock;
+    const int b0 = threadIdx.x * per;
+    uint32_t s = 0, tot;
     for (int k = 0; k < per; ++k)
-      if (b0 + k < G) s += row_s[spine_at(b0 + k)];
-    uint32_t run = block_excl_scan<kScanBlock>(s, &tot);
+      if (b0 + k < len) s += row_s[spine_at(b0 + k)];
+    uint32_t run = carry + block_excl_scan<kScanBlock>(s, &tot);
     for (int k = 0; k < per; ++k)
-      if (b0 + k < G) {
+      if (b0 + k < len) {
         const uint32_t v = row_s[spine_at(b0 + k)];
         row_s[spine_at(b0 + k)] = run;
         run += v;
       }
     __syncthreads();
-    for (int k = threadIdx.x; k < G; k += kScanBlock) row[k] = row_s[spine_at(k)];
-  } else {
-    for (int k = 0; k < per; ++k)
-      if (b0 + k < G) s += row[b0 + k];
-    uint32_t run = block_excl_scan<kScanBlock>(s, &tot);
-    for (int k = 0; k < per; ++k)
-      if (b0 + k < G) {
-        const uint32_t v = row[b0 + k];
-        row[b0 + k] = run;
-        run += v;
-      }
+    for (int k = threadIdx.x; k < len; k += kScanBlock) row[c0 + k] = row_s[spine_at(k)];
+    carry += tot;
+    __syncthreads();  // the piece's stores read row_s before the next piece overwrites it
   }
-  if (threadIdx.x == 0) digit_tot[d] = tot;
+  if (threadIdx.x == 0) digit_tot[d] = carry;
 }
 
 // Per-lane digit counters of workgroup g: base of each digit (exclusive scan of the
