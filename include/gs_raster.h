@@ -38,12 +38,14 @@ extern "C" {
 
 /* Per-Gaussian compositing record: 12 floats, L = log2(e)
  *   [0]=mean2d.x [1]=mean2d.y [2]=-0.5*ic00*L [3]=-ic01*L [4]=-0.5*ic11*L
- *   [5]=log2(op) [6..8]=colour rgb [9]=op [10]=log2(op) - 10*L [11]=may_cap
+ *   [5]=log2(op) [6..8]=colour rgb [9]=op [10]=log2(op) - 10*L [11]=no_cap
  * where op = sigmoid(opacity) and ic = inverse of cov2D with det clamped to 1e-6
  * (rasterizer.py:147-156), so that alpha = exp2([2]dx^2 + [3]dx dy + [4]dy^2 + [5])
- * and the gate power > -10 is exponent > [10]; may_cap = 0 when op < 0.98 and cov2D is
- * positive definite (no alpha can reach the 0.99 cap), else 1 (gs_composite_bwd takes
- * the capped path only for such records).
+ * and the gate power > -10 is exponent > [10]; no_cap = 1.0 when no point that passes the
+ * gate can reach the 0.99 alpha cap, the exponent's float32 rounding included (the conic
+ * is positive definite and log2(op) plus a bound of that rounding, which grows with the
+ * conic's tr^2/det, stays below log2(0.99)), else 0.0.  gs_composite_bwd skips its
+ * per-wave cap test only for records holding exactly 1.0 there; any other value is safe.
  * The gradient record produced by gs_composite_bwd holds, with dP = dL/dpower of one
  * (pixel, entry) pair, dx = pixel.x - mean2d.x, dy = pixel.y - mean2d.y, summed over
  * the Gaussian's pairs:
@@ -78,7 +80,8 @@ const char* gs_last_error(void);
  * 6: gs_composite_fwd/bwd take a gs_window_t in place of window_rule; gs_window_from_list,
  * gs_window_from_bins; GS_STAT_WINDOW_CLAMPED.  7: gs_preprocess_bwd_w2c, gs_eval_sh,
  * gs_eval_sh_bwd.  8: gs_l1_ssim_window, gs_l1_ssim_window_bwd.  9: compositing records carry
- * may_cap in slot 11 (gs_composite_bwd reads it; records of an earlier build hold 0 there). */
+ * a cap flag in slot 11.  10: that flag is no_cap (1.0 = proven below the cap, rounding
+ * included; 0.0 = not proven), read by gs_composite_bwd. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.

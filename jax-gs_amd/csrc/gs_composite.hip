@@ -52,9 +52,6 @@ namespace gs {
 namespace {
 
 constexpr float kTMin = 1e-4f;
-// exp2(q) < 0.99, the alpha cap of rasterizer.py:211, for every q below this (2^-0.015 =
-// 0.98966, far more than exp2's rounding below 0.99)
-constexpr float kBelowCapQ = -0.015f;
 // s_waitcnt immediate (gfx9 layout) that waits for lgkmcnt = 0 and for nothing else
 constexpr int kWaitLgkm0 = 0xC07F;
 
@@ -236,7 +233,7 @@ __device__ inline void tile_span(const int32_t* __restrict__ ranges, int tile, i
 
 // One compositing record (layout of GS_REC_STRIDE floats in gs_raster.h).
 struct Rec {
-  float mx, my, A, B, C, lop, r, g, b, op, thr, may_cap;
+  float mx, my, A, B, C, lop, r, g, b, op, thr, no_cap;
 };
 
 __device__ inline Rec zero_rec() { return Rec{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}; }
@@ -709,9 +706,10 @@ __device__ __forceinline__ void composite_bwd_body(
           // cotangent passes whole, so the body needs no selections; the rare capped
           // entry redoes its power sums with the cap's selections afterwards.  One body
           // for both keeps the per-pixel state (T, Rg) in place across entries.
-          // (the record's flag first: most records cannot reach the cap at all)
+          // (the record's flag first: most records provably cannot reach the cap at all;
+          // only the exact value 1.0 skips the test, so zeroed or foreign records take it)
           bool capw = false;
-          if ((__float_as_uint(e.may_cap) >> 23) != 0u) {  // 1.0f or 0.0f (a scalar compare)
+          if (__float_as_uint(e.no_cap) != 0x3F800000u) {  // a scalar compare
             float qmax = qv[0];
 #pragma unroll
             for (int i = 1; i < PPT; ++i) qmax = fmaxf(qmax, qv[i]);

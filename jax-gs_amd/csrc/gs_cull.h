@@ -46,4 +46,31 @@ __host__ __device__ inline bool entry_misses_rect(float mx, float my, float A, f
   return fmin >= 10.25f * 1.4426950408889634f + 1e-5f * scale;
 }
 
+// Exponents at or above this may give exp2(q) >= 0.99, the alpha cap of rasterizer.py:211
+// (2^-0.015 = 0.98966: a margin far beyond the rounding of the hardware exp2).
+constexpr float kBelowCapQ = -0.015f;
+
+// True when the record (A, B, C, lop) provably keeps q_of below kBelowCapQ at every point
+// that passes the gate q > lop - 10 log2(e), wherever the point lies, so that compositing's
+// backward may skip the 0.99 cap for it.  With x = (dx, dy), M = [[a, -B/2], [-B/2, c]],
+// a = -A, c = -C, the exact form is q* = lop - x^T M x; for M positive definite (eigenvalues
+// l1 >= l2 > 0, l1 + l2 = tr, l1 l2 = det) q* <= lop.  q_of's five roundings (A dx, the two
+// fmas of the row term, B dx, the last fma) stay within 3u (T + |lop|), u = 2^-24,
+// T = |A| dx^2 + |B| |dx dy| + |C| dy^2 <= 2 tr |x|^2.  A gated point has
+// x^T M x < 10 log2(e) + err + |lop| u, so with err <= 1, |x|^2 <= 15.5 / l2 <= 15.5 tr / det
+// and err <= u (93 tr^2 / det + 3 |lop|).  The test takes u (128 tr^2 / det + 4 |lop| + 4)
+// as the bound and asks lop + bound < kBelowCapQ and bound <= 1; every product of two
+// floats is exact in double, so det carries one rounding.  NaN or infinite inputs, and
+// every matrix that is not positive definite, give false.  Thin Gaussians (tr^2 / det in
+// the thousands) and opacities near the cap fail the test and take the per-wave cap test.
+__host__ __device__ inline bool record_cannot_cap(float A, float B, float C, float lop) {
+  const double a = -(double)A, c = -(double)C, hb = 0.5 * (double)B, l = (double)lop;
+  const double det = a * c - hb * hb;
+  if (!(a > 0.0 && c > 0.0 && det > 0.0 && l <= 0.0)) return false;
+  const double room = (double)kBelowCapQ - l;  // > 0 here
+  const double tr = a + c;
+  const double lhs = 0x1p-24 * (128.0 * tr * tr + (4.0 * (-l) + 4.0) * det);
+  return lhs < (room < 1.0 ? room : 1.0) * det;
+}
+
 }  // namespace gs

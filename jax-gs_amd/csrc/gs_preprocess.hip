@@ -16,6 +16,7 @@
 // conventions: ties of maximum/minimum/clip split the cotangent 0.5/0.5, the
 // radius (ceil) and all masks carry no gradient, and cov2D[1,0] is unused.
 #include "gs_common.h"
+#include "gs_cull.h"
 
 namespace gs {
 namespace {
@@ -146,9 +147,9 @@ __device__ inline float eval_sh_channel(const float* sh, int c, const float* d) 
 }
 
 // rasterizer.py:147-156 and :198 -- record = (mean, -0.5*conic terms, sigmoid, colour),
-// and a flag that compositing's backward reads: 0 when no pixel's alpha can reach the
-// 0.99 cap (op < 0.98 and cov2D positive definite, so the exponent never exceeds
-// log2(op) beyond rounding), 1 otherwise.
+// and a flag that compositing's backward reads: 1.0 when no pixel that passes the gate
+// can reach the 0.99 alpha cap with this record, rounding of the exponent included
+// (record_cannot_cap), else 0.0 (the backward then tests the cap per wave).
 __device__ inline void write_record(float* __restrict__ rec, float m2x, float m2y, float c00,
                                     float c01, float c11, float logit, const float* col) {
   const float det_raw = c00 * c11 - c01 * c01;
@@ -160,10 +161,10 @@ __device__ inline void write_record(float* __restrict__ rec, float m2x, float m2
   const float op = det_sigmoidf(logit);
   const float lop = log2f(op);
   float4* r4 = reinterpret_cast<float4*>(rec);
-  r4[0] = make_float4(m2x, m2y, (-0.5f * ic00) * kL2E, (-ic01) * kL2E);
-  r4[1] = make_float4((-0.5f * ic11) * kL2E, lop, col[0], col[1]);
-  const float may_cap = (op < 0.98f && det_raw > 0.0f && c00 > 0.0f) ? 0.0f : 1.0f;
-  r4[2] = make_float4(col[2], op, lop - 10.0f * kL2E, may_cap);
+  const float A = (-0.5f * ic00) * kL2E, B = (-ic01) * kL2E, C = (-0.5f * ic11) * kL2E;
+  r4[0] = make_float4(m2x, m2y, A, B);
+  r4[1] = make_float4(C, lop, col[0], col[1]);
+  r4[2] = make_float4(col[2], op, lop - 10.0f * kL2E, record_cannot_cap(A, B, C, lop) ? 1.0f : 0.0f);
 }
 
 // Copies the first COLS floats of rows [g0, g0+64) of a row-major array (row

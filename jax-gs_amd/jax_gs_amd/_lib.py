@@ -82,7 +82,7 @@ _RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_
 _lib = None
 
 
-ABI_VERSION = 9  # gs_abi_version() of the signatures bound below
+ABI_VERSION = 10  # gs_abi_version() of the signatures bound below
 
 
 class NativeLibraryMissing(RuntimeError):

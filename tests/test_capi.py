@@ -32,7 +32,7 @@ def test_binding_covers_every_declared_symbol():
 
 def test_abi_version_and_workspace_query_without_gpu():
     L = _lib.lib()
-    assert L.gs_abi_version() == _lib.ABI_VERSION == 9
+    assert L.gs_abi_version() == _lib.ABI_VERSION == 10
     # size query: pure host arithmetic, grows with the number of Gaussians
     a = L.gs_bin_workspace_size(1000, 64, 64, 0)
     b = L.gs_bin_workspace_size(100000, 64, 64, 0)

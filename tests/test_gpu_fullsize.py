@@ -131,6 +131,44 @@ def test_cfg2_full_frame(cuda):
     _full_check(sc, cuda, min_saturated=0.9)
 
 
+def test_cfg2_full_frame_oblique_camera(cuda):
+    """Configuration 2 at full size under a rotated, translated camera whose W2C requires
+    grad: the whole-frame image, the five cotangents and dL/dW2C against the oracle's VJP.
+    The camera cotangent is the sum of 1M per-Gaussian shares, reduced in 15,625 wave
+    partials and one finishing workgroup (gs_preprocess_bwd_w2c), where float32
+    cancellation in the twelve sums is the risk."""
+    sc = scenes.make_scene(2)
+    ax = np.array([0.3, -0.5, 0.8])
+    ax /= np.linalg.norm(ax)
+    K = np.array([[0, -ax[2], ax[1]], [ax[2], 0, -ax[0]], [-ax[1], ax[0], 0]])
+    w = np.eye(4)
+    w[:3, :3] = np.eye(3) + np.sin(0.15) * K + (1 - np.cos(0.15)) * K @ K
+    w[:3, 3] = [0.05, -0.03, 0.2]
+    sc["cam"]["W2C"] = w.astype(np.float32)
+    c = sc["cam"]
+    log(f"cfg2 oblique camera: oracle forward ({oracle.threads()} threads)")
+    img_o, ex_o, res = oracle.render(sc["params"], c, sh_degree=sc["sh_degree"])
+    g, cam, _, _ = scenes.to_torch(sc, cuda)
+    for f in FIELDS:
+        getattr(g, f).requires_grad_(True)
+    cam = cam._replace(W2C=cam.W2C.clone().requires_grad_(True))
+    image, extras = render(g, cam, sh_degree=sc["sh_degree"])
+    assert int(np_(extras["n_interactions"])) == int(ex_o["n_interactions"])
+    err = float(np.abs(np_(image) - img_o).max())
+    log(f"image max-abs {err:.2e}, {int(ex_o['n_interactions'])} entries")
+    assert err <= IMG_TOL
+    seed = l1_seed(sc, img_o)
+    image.backward(torch.from_numpy(seed).to(cuda))
+    gr_o = oracle.render_vjp(sc["params"], c, res, seed, sh_degree=sc["sh_degree"])
+    errs = {f: rel(np_(getattr(g, f).grad), gr_o[f]) for f in FIELDS}
+    gw = np_(cam.W2C.grad)
+    errs["W2C"] = rel(gw, gr_o["W2C"])
+    log("gradient relative L2: " + ", ".join(f"{f} {e:.1e}" for f, e in errs.items()))
+    assert np.all(gw[3] == 0)
+    for f, e in errs.items():
+        assert e <= GRAD_TOL, f
+
+
 def test_cfg3_full_size(cuda):
     """Configuration 3 (3M Gaussians, SH1, 1280x720, 70 % in four tight clusters): 65M
     entries, tiles past 10k entries composited to 4096, the whole frame forward and

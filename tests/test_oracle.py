@@ -9,6 +9,9 @@ preprocess: projection/cov/rad  known answers KA1, KA3 (closed form); float64 Nu
                                 numpy.linalg.eigvalsh; Sigma symmetric PSD
 preprocess: SH colour           scipy.special.sph_harm_y real harmonics (basis =
                                 (-1)^m x Condon-Shortley real SH), degrees 0..3
+preprocess: camera transform    float64 closed forms under a scipy-rotated, translated
+                                W2C: R m + t, J R Sigma R^T J^T + 0.3 I, radii, and the
+                                colour from the centre -R^T t (R^T for R, -R t rejected)
 tile_interactions               known answer KA2; pure-Python brute force over all
                                 256*N slots with Python's stable sorted(); invariants
 render_tiles                    KA4, KA5 closed forms (exactly 48 blends in KA5);
@@ -110,6 +113,94 @@ def test_projection_matches_float64_linear_algebra():
     np.testing.assert_array_equal(pre["radii"][safe], r64[safe])
     # Sigma from the float32 path is symmetric positive semi-definite
     assert np.all(np.linalg.eigvalsh(Sig) > -1e-7)
+
+
+def _camera_closed_form(means, scales, quats, sh, w2c, fx, fy, cx, cy, deg, rot_t=False, centre_rt=False):
+    """float64 closed forms of the projection and the colour under a general W2C:
+    camera-space mean R m + t (projection.py:26-27), cov2D = J R Sigma R^T J^T + 0.3 I with J
+    at the camera-space mean (projection.py:52-57), view direction from the camera centre
+    -R^T t (camera.py:15-21, renderer.py:40-41) through scipy's real harmonics.
+    rot_t / centre_rt compute the plausible mistakes (R^T for R in the covariance; the centre
+    -R t) so that a test can show they fail."""
+    n = means.shape[0]
+    R = w2c[:3, :3].astype(np.float64)
+    t = w2c[:3, 3].astype(np.float64)
+    m = means.astype(np.float64)
+    pc = m @ R.T + t
+    x, y, z = pc[:, 0], pc[:, 1], pc[:, 2]
+    q64 = quats.astype(np.float64)
+    Rg = Rotation.from_quat(np.concatenate([q64[:, 1:], q64[:, :1]], 1)).as_matrix()
+    A = Rg * np.exp(scales.astype(np.float64))[:, None, :]
+    Sig = A @ A.transpose(0, 2, 1)
+    J = np.zeros((n, 2, 3))
+    J[:, 0, 0] = fx / z
+    J[:, 0, 2] = -fx * x / z ** 2
+    J[:, 1, 1] = fy / z
+    J[:, 1, 2] = -fy * y / z ** 2
+    Rw = R.T if rot_t else R
+    cov = J @ Rw @ Sig @ Rw.T @ J.transpose(0, 2, 1) + 0.3 * np.eye(2)
+    m2 = np.stack([fx * x / z + cx, fy * y / z + cy], 1)
+    centre = -(R @ t) if centre_rt else -(R.T @ t)
+    d = m - centre
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    res = np.zeros((n, 3))
+    k = 0
+    for l in range(deg + 1):
+        for mm in range(-l, l + 1):
+            res += _real_sh_no_cs(l, mm, d)[:, None] * sh[:, k, :].astype(np.float64)
+            k += 1
+    return pc, cov, m2, np.clip(res + 0.5, 0.0, 1.0)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_projection_and_colour_with_rotated_translated_camera(seed):
+    """The oracle's forward under a rotated and translated camera (scipy rotation, a
+    translation of about half a unit) against the float64 closed forms of
+    _camera_closed_form: depth, means2D, cov2D, radii (numpy eigvalsh, away from integer
+    boundaries) and the SH-3 colour.  The same comparison rejects R^T in place of R in the
+    covariance and the camera centre -R t in place of -R^T t."""
+    rng = np.random.default_rng(200 + seed)
+    n = 3000
+    rot = Rotation.from_rotvec(rng.normal(0.0, 0.5, 3)).as_matrix()
+    t = rng.normal(0.0, 0.5, 3)
+    w2c = np.eye(4)
+    w2c[:3, :3] = rot
+    w2c[:3, 3] = t
+    w2c = w2c.astype(F32)
+    R = w2c[:3, :3].astype(np.float64)
+    tt = w2c[:3, 3].astype(np.float64)
+    # points in front of the camera, mapped back to the world: m = R^T (p - t)
+    z = rng.uniform(1.5, 8.0, n)
+    pcam = np.stack([rng.uniform(-0.8, 0.8, n) * z, rng.uniform(-0.6, 0.6, n) * z, z], 1)
+    means = ((pcam - tt) @ R).astype(F32)
+    scales = rng.normal(-3.0, 0.7, (n, 3)).astype(F32)
+    quats = rng.normal(0, 1, (n, 4)).astype(F32)
+    sh = rng.normal(0, 0.25, (n, 16, 3)).astype(F32)
+    fx, fy, cx, cy = F32(310.0), F32(290.0), F32(200.0), F32(150.0)
+    pre = oracle.preprocess(means, scales, quats, sh, w2c, 400, 300, fx, fy, cx, cy, 3)
+    pc, cov, m2, col = _camera_closed_form(means, scales, quats, sh, w2c, float(fx), float(fy), float(cx),
+                                           float(cy), 3)
+    assert pre["valid"].all()
+    np.testing.assert_allclose(pre["depths"], pc[:, 2], rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(pre["means2d"], m2, rtol=1e-6, atol=2e-4)
+    # per Gaussian, relative to the matrix's norm (float32 cancellation in small off-diagonals)
+    cerr = np.linalg.norm(pre["cov2d"] - cov, axis=(1, 2)) / np.linalg.norm(cov, axis=(1, 2))
+    assert cerr.max() <= 2e-5, cerr.max()
+    lam = np.linalg.eigvalsh(cov)[:, 1]
+    r = 3.0 * np.sqrt(lam)
+    frac = r - np.floor(r)
+    safe = (frac > 1e-3) & (frac < 1 - 1e-3)
+    assert safe.mean() > 0.99
+    np.testing.assert_array_equal(pre["radii"][safe], np.ceil(r[safe]))
+    np.testing.assert_allclose(pre["colors"], col, atol=2e-6)
+    # the plausible mistakes fail the same bars
+    _, cov_t, _, _ = _camera_closed_form(means, scales, quats, sh, w2c, float(fx), float(fy), float(cx), float(cy), 3,
+                                         rot_t=True)
+    cerr_t = np.linalg.norm(pre["cov2d"] - cov_t, axis=(1, 2)) / np.linalg.norm(cov_t, axis=(1, 2))
+    assert cerr_t.max() > 1e-2
+    _, _, _, col_rt = _camera_closed_form(means, scales, quats, sh, w2c, float(fx), float(fy), float(cx), float(cy), 3,
+                                          centre_rt=True)
+    assert not np.allclose(pre["colors"], col_rt, atol=2e-6)
 
 
 def _real_sh_no_cs(l, m, d):
