@@ -81,7 +81,8 @@ const char* gs_last_error(void);
  * gs_window_from_bins; GS_STAT_WINDOW_CLAMPED.  7: gs_preprocess_bwd_w2c, gs_eval_sh,
  * gs_eval_sh_bwd.  8: gs_l1_ssim_window, gs_l1_ssim_window_bwd.  9: compositing records carry
  * a cap flag in slot 11.  10: that flag is no_cap (1.0 = proven below the cap, rounding
- * included; 0.0 = not proven), read by gs_composite_bwd. */
+ * included; 0.0 = not proven), read by gs_composite_bwd; gs_composite_prep_bwd,
+ * gs_project_bwd. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -258,6 +259,26 @@ int gs_preprocess_bwd_w2c(void* stream, int64_t n, int sh_k, int sh_degree, cons
                           float* grad_means, float* grad_scales, float* grad_quats,
                           float* grad_opacities, float* grad_sh, float* grad_w2c, void* workspace,
                           size_t workspace_bytes);
+
+/* Vector-Jacobian product of gs_composite_prep on its own (JAX autodiff of the prologue of
+ * jax_gs/renderer/rasterizer.py:119-156, render_tiles: det clamp, inverse covariance,
+ * sigmoid): from the gradient records of gs_composite_bwd to the cotangents of
+ * render_tiles' inputs, grad_means2d[N,2], grad_cov2d[N,2,2] ([1,0] is 0: render_tiles
+ * reads cov2D[0,1] only), grad_opacities[N,1] (logits) and grad_colors[N,3]. */
+int gs_composite_prep_bwd(void* stream, int64_t n, const float* cov2d, const float* opacities,
+                          const float* grad_records, float* grad_means2d, float* grad_cov2d,
+                          float* grad_opacities, float* grad_colors);
+
+/* Vector-Jacobian product of jax_gs/renderer/projection.py:6-79 (project_gaussians, with
+ * jax_gs/core/gaussians.py:58-92) on its own: from the cotangents of its outputs means2D
+ * [N,2], cov2D [N,2,2] (all four entries) and z [N] (grad_depths, may be NULL = zero) to
+ * those of means, scales and quaternions; radii and valid_mask carry none.  grad_w2c[4,4]
+ * (may be NULL) receives dL/dW2C through the camera-space means and W_rot (row 3 is 0),
+ * with a workspace of gs_preprocess_bwd_w2c_workspace_size(n) bytes (unused when NULL). */
+int gs_project_bwd(void* stream, int64_t n, const float* means, const float* scales, const float* quats,
+                   const float* w2c, float fx, float fy, const float* grad_means2d, const float* grad_cov2d,
+                   const float* grad_depths, float* grad_means, float* grad_scales, float* grad_quats,
+                   float* grad_w2c, void* workspace, size_t workspace_bytes);
 
 /* jax_gs/renderer/sh.py:25-74 eval_sh: colors[N,3] = the real SH expansion of degree
  * sh_degree (0..3) of sh_coeffs[N,K,3] (K >= (sh_degree+1)^2) in the directions

@@ -449,24 +449,12 @@ __device__ inline void colour_vjp(const float* w, float mx, float my, float mz, 
   }
 }
 
-// Geometric part of the backward of one Gaussian (projection, covariance, conic, opacity)
-// given its gradient record grow; g_mcol: the mean's cotangent through the view direction
-// (colour_vjp), added last.  part (may be NULL): the Gaussian's share of dL/dW2C through
-// the camera-space mean and W_rot, part[3a+b] for W2C[a][b] and part[9+a] for W2C[a][3]
-// (projection.py:26-27, 52-57).
-__device__ inline void preprocess_bwd_geom(int64_t i, const GaussIn& in, const float* w, float fx, float fy,
-                                           const float* grow, const float* g_mcol, float* __restrict__ g_means,
-                                           float* __restrict__ g_scales, float* __restrict__ g_quats,
-                                           float* __restrict__ g_opac, float* part = nullptr) {
-  const float mx = in.mx, my = in.my, mz = in.mz;
-  float q[4], ls[3];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) q[k] = in.q[k];
-#pragma unroll
-  for (int k = 0; k < 3; ++k) ls[k] = in.ls[k];
-  Proj p;
-  project(w, mx, my, mz, q, ls, fx, fy, p);
-
+// The conic and opacity part of the backward (rasterizer.py:147-156 reversed): from a
+// Gaussian's gradient record grow and its cov2D (c00, c01, c11) and opacity logit, the
+// cotangents of means2D, of cov2D (G; render_tiles never reads cov2D[1,0], so G[1][0] = 0)
+// and of the logit.
+__device__ inline void conic_vjp(const float* grow, float c00, float c01, float c11, float logit, float& g_m2x,
+                                 float& g_m2y, float (&G)[2][2], float& g_logit) {
   const float4 ga = make_float4(grow[0], grow[1], grow[2], grow[3]);
   const float4 gb = make_float4(grow[4], grow[5], grow[6], grow[7]);
   // gradient record (sums over the Gaussian's pixels of dL/dpower times):
@@ -477,25 +465,43 @@ __device__ inline void preprocess_bwd_geom(int64_t i, const GaussIn& in, const f
   const float g_ic11 = -0.5f * gb.x;
 
   // ---- opacity: alpha = exp(power) * sigmoid(logit); sum dL/dpower = sigmoid * dL/dsigmoid
-  const float sg = det_sigmoidf(in.logit);
-  g_opac[i] = gb.y * (1.0f - sg);
+  const float sg = det_sigmoidf(logit);
+  g_logit = gb.y * (1.0f - sg);
 
   // ---- conic <- cov2D (rasterizer.py:147-153)
-  const float det_raw = p.c00 * p.c11 - p.c01 * p.c01;
+  const float det_raw = c00 * c11 - c01 * c01;
   const float det = jmax(det_raw, 1e-6f);
-  const float ic00 = p.c11 / det, ic01 = (-p.c01) / det, ic11 = p.c00 / det;
+  const float ic00 = c11 / det, ic01 = (-c01) / det, ic11 = c00 / det;
   // ---- d power / d mean2d = (ic00 dx + ic01 dy, ic01 dx + ic11 dy)
-  const float g_m2x = ic00 * ga.x + ic01 * ga.y;
-  const float g_m2y = ic01 * ga.x + ic11 * ga.y;
+  g_m2x = ic00 * ga.x + ic01 * ga.y;
+  g_m2y = ic01 * ga.x + ic11 * ga.y;
   float g_c00 = g_ic11 / det;
   float g_c11 = g_ic00 / det;
   float g_c01 = -g_ic01 / det;
   const float g_det = -((g_ic00 * ic00 + g_ic01 * ic01) + g_ic11 * ic11) / det * dmax_first(det_raw, 1e-6f);
-  g_c00 += g_det * p.c11;
-  g_c11 += g_det * p.c00;
-  g_c01 += -2.0f * p.c01 * g_det;
-  const float G[2][2] = {{g_c00, g_c01}, {0.0f, g_c11}};
+  g_c00 += g_det * c11;
+  g_c11 += g_det * c00;
+  g_c01 += -2.0f * c01 * g_det;
+  G[0][0] = g_c00;
+  G[0][1] = g_c01;
+  G[1][0] = 0.0f;
+  G[1][1] = g_c11;
+}
 
+// The projection part of the backward of one Gaussian (project_gaussians and
+// get_covariance_3d reversed, projection.py:26-79, gaussians.py:58-92): from the
+// cotangents of means2D (g_m2x, g_m2y), cov2D (G, all four entries) and, with DEPTH, of
+// the depth z (g_depth), to those of the mean, log-scales and quaternion.  p is the
+// Gaussian's forward projection.  g_mcol: the mean's cotangent through the view direction
+// (colour_vjp), added last.  part (may be NULL): the Gaussian's share of dL/dW2C through
+// the camera-space mean and W_rot, part[3a+b] for W2C[a][b] and part[9+a] for W2C[a][3]
+// (projection.py:26-27, 52-57).
+template <bool DEPTH>
+__device__ inline void project_vjp(int64_t i, const GaussIn& in, const Proj& p, const float* w, float fx, float fy,
+                                   float g_m2x, float g_m2y, const float (&G)[2][2], float g_depth,
+                                   const float* g_mcol, float* __restrict__ g_means, float* __restrict__ g_scales,
+                                   float* __restrict__ g_quats, float* part) {
+  const float mx = in.mx, my = in.my, mz = in.mz;
   // ---- cov2D = (M2 Sig) M2^T + 0.3 I
   float g_T1[2][3], g_M2[2][3], g_Sig[3][3];
 #pragma unroll
@@ -534,6 +540,8 @@ __device__ inline void preprocess_bwd_geom(int64_t i, const GaussIn& in, const f
   g_x += g_m2x * fx / p.z;
   g_y += g_m2y * fy / p.z;
   g_z += -(g_m2x * (fx * p.x) + g_m2y * (fy * p.y)) / (p.z * p.z);
+  // ---- z itself (project_gaussians returns it)
+  if (DEPTH) g_z += g_depth;
   if (part != nullptr) {
     // means_cam = W_rot m + t;  M2 = J W_rot with J = [[fx iz, 0, -fx x iz2], [0, fy iz, -fy y iz2]]
     const float J0[3] = {fx * p.iz, 0.0f, ((-fx) * p.x) * p.iz2};
@@ -597,6 +605,25 @@ __device__ inline void preprocess_bwd_geom(int64_t i, const GaussIn& in, const f
   const float qd = ((p.qn[0] * gq[0] + p.qn[1] * gq[1]) + p.qn[2] * gq[2]) + p.qn[3] * gq[3];
 #pragma unroll
   for (int k = 0; k < 4; ++k) g_quats[4 * i + k] = (gq[k] - p.qn[k] * qd) / p.qnorm;
+}
+
+// Geometric part of the backward of one Gaussian from its gradient record grow (conic,
+// opacity, projection, covariance); g_mcol and part as for project_vjp.
+__device__ inline void preprocess_bwd_geom(int64_t i, const GaussIn& in, const float* w, float fx, float fy,
+                                           const float* grow, const float* g_mcol, float* __restrict__ g_means,
+                                           float* __restrict__ g_scales, float* __restrict__ g_quats,
+                                           float* __restrict__ g_opac, float* part = nullptr) {
+  float q[4], ls[3];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) q[k] = in.q[k];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) ls[k] = in.ls[k];
+  Proj p;
+  project(w, in.mx, in.my, in.mz, q, ls, fx, fy, p);
+  float g_m2x, g_m2y, G[2][2], g_logit;
+  conic_vjp(grow, p.c00, p.c01, p.c11, in.logit, g_m2x, g_m2y, G, g_logit);
+  g_opac[i] = g_logit;
+  project_vjp<false>(i, in, p, w, fx, fy, g_m2x, g_m2y, G, 0.0f, g_mcol, g_means, g_scales, g_quats, part);
 }
 
 // Backward of one Gaussian.  shv: its SH row (registers), overwritten with the SH
@@ -706,6 +733,74 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (i >= n) return;
   preprocess_bwd_gauss<DEG>(i, K, in, w2c, fx, fy, shv, grow, aligned, g_means, g_scales, g_quats, g_opac, g_sh,
                             nullptr);
+}
+
+// The VJP of composite_prep_kernel on its own (render_tiles' prologue, rasterizer.py:147-156):
+// one thread per Gaussian, from its gradient record to the cotangents of means2D, cov2D
+// (0 in [1,0], which render_tiles never reads), the opacity logit and the colour.
+__global__ __launch_bounds__(256) void composite_prep_bwd_kernel(
+    int64_t n, const float* __restrict__ cov2d, const float* __restrict__ opac, const float* __restrict__ grec,
+    float* __restrict__ g_means2d, float* __restrict__ g_cov2d, float* __restrict__ g_opac,
+    float* __restrict__ g_colors) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float4 c = reinterpret_cast<const float4*>(cov2d)[i];
+  float grow[kRec];
+  load_row<kRec>(grec + i * kRec, (reinterpret_cast<uintptr_t>(grec) & 15) == 0, grow);
+  float g_m2x, g_m2y, G[2][2], g_logit;
+  conic_vjp(grow, c.x, c.y, c.w, opac[i], g_m2x, g_m2y, G, g_logit);
+  g_means2d[2 * i] = g_m2x;
+  g_means2d[2 * i + 1] = g_m2y;
+  reinterpret_cast<float4*>(g_cov2d)[i] = make_float4(G[0][0], G[0][1], G[1][0], G[1][1]);
+  g_opac[i] = g_logit;
+  g_colors[3 * i] = grow[6];
+  g_colors[3 * i + 1] = grow[7];
+  g_colors[3 * i + 2] = grow[8];
+}
+
+// The VJP of project_gaussians (projection.py:6-79) on its own: one thread per Gaussian,
+// from the cotangents of means2D, cov2D (all four entries) and, with DEPTH, the depth z to
+// those of the mean, log-scales and quaternion; with W2C each wave also writes its 64
+// Gaussians' summed shares of dL/dW2C to w2c_part[16 * block] (the view-vector slots 12-14
+// stay 0: project_gaussians computes no colour).
+template <bool W2C, bool DEPTH>
+__global__ __launch_bounds__(64) void project_bwd_kernel(
+    int64_t n, const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ quats,
+    const float* __restrict__ w2c, float fx, float fy, const float* __restrict__ g_means2d,
+    const float* __restrict__ g_cov2d, const float* __restrict__ g_depths, float* __restrict__ g_means,
+    float* __restrict__ g_scales, float* __restrict__ g_quats, float* __restrict__ w2c_part) {
+  const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  const int64_t ic = i < n ? i : n - 1;
+  GaussIn in;
+  in.mx = means[3 * ic];
+  in.my = means[3 * ic + 1];
+  in.mz = means[3 * ic + 2];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) in.q[k] = quats[4 * ic + k];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) in.ls[k] = scales[3 * ic + k];
+  in.logit = 0.0f;
+  float w[16];
+  load_w2c(w2c, w);
+  float part[15];
+#pragma unroll
+  for (int k = 0; k < 15; ++k) part[k] = 0.0f;
+  if (i < n) {
+    Proj p;
+    project(w, in.mx, in.my, in.mz, in.q, in.ls, fx, fy, p);
+    const float4 gc = reinterpret_cast<const float4*>(g_cov2d)[i];
+    const float G[2][2] = {{gc.x, gc.y}, {gc.z, gc.w}};
+    const float g_mcol[3] = {0.0f, 0.0f, 0.0f};
+    project_vjp<DEPTH>(i, in, p, w, fx, fy, g_means2d[2 * i], g_means2d[2 * i + 1], G, DEPTH ? g_depths[i] : 0.0f,
+                       g_mcol, g_means, g_scales, g_quats, W2C ? part : nullptr);
+  }
+  if (W2C) {
+#pragma unroll
+    for (int k = 0; k < 15; ++k) {
+      const float t = wave_total(part[k]);
+      if (threadIdx.x == 0) w2c_part[16 * (int64_t)blockIdx.x + k] = t;
+    }
+  }
 }
 
 // dL/dW2C from the waves' partial sums, in a fixed order (one workgroup): the shares through
@@ -1027,6 +1122,56 @@ extern "C" int gs_preprocess_bwd_w2c(void* stream, int64_t n, int sh_k, int sh_d
   hipLaunchKernelGGL(w2c_finish_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, (const float*)workspace,
                      n > 0 ? div_up(n, 64) : (int64_t)0, w2c, grad_w2c);
   GS_LAUNCH_CHECK("w2c_finish_kernel");
+  return GS_OK;
+}
+
+extern "C" int gs_composite_prep_bwd(void* stream, int64_t n, const float* cov2d, const float* opacities,
+                                     const float* grad_records, float* grad_means2d, float* grad_cov2d,
+                                     float* grad_opacities, float* grad_colors) {
+  GS_REQUIRE(n >= 0, "gs_composite_prep_bwd: n must be >= 0");
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(cov2d && opacities && grad_records && grad_means2d && grad_cov2d && grad_opacities && grad_colors,
+             "gs_composite_prep_bwd: NULL array argument");
+  hipLaunchKernelGGL(composite_prep_bwd_kernel, dim3(div_up(n, 256)), dim3(256), 0, (hipStream_t)stream, n, cov2d,
+                     opacities, grad_records, grad_means2d, grad_cov2d, grad_opacities, grad_colors);
+  GS_LAUNCH_CHECK("composite_prep_bwd_kernel");
+  return GS_OK;
+}
+
+extern "C" int gs_project_bwd(void* stream, int64_t n, const float* means, const float* scales, const float* quats,
+                              const float* w2c, float fx, float fy, const float* grad_means2d,
+                              const float* grad_cov2d, const float* grad_depths, float* grad_means,
+                              float* grad_scales, float* grad_quats, float* grad_w2c, void* workspace,
+                              size_t workspace_bytes) {
+  GS_REQUIRE(n >= 0, "gs_project_bwd: n must be >= 0");
+  GS_REQUIRE(w2c != nullptr, "gs_project_bwd: NULL w2c");
+  if (grad_w2c != nullptr)
+    GS_REQUIRE(workspace != nullptr && workspace_bytes >= gs_preprocess_bwd_w2c_workspace_size(n),
+               "gs_project_bwd: workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
+               gs_preprocess_bwd_w2c_workspace_size(n));
+  hipStream_t s = (hipStream_t)stream;
+  if (n > 0) {
+    GS_REQUIRE(means && scales && quats && grad_means2d && grad_cov2d && grad_means && grad_scales && grad_quats,
+               "gs_project_bwd: NULL array argument");
+    float* part = (float*)workspace;
+#define GS_PROJ_BWD(W, D)                                                                                        \
+  hipLaunchKernelGGL((project_bwd_kernel<W, D>), dim3(div_up(n, 64)), dim3(64), 0, s, n, means, scales, quats, w2c, \
+                     fx, fy, grad_means2d, grad_cov2d, grad_depths, grad_means, grad_scales, grad_quats, part)
+    if (grad_w2c != nullptr) {
+      if (grad_depths != nullptr) GS_PROJ_BWD(true, true);
+      else GS_PROJ_BWD(true, false);
+    } else {
+      if (grad_depths != nullptr) GS_PROJ_BWD(false, true);
+      else GS_PROJ_BWD(false, false);
+    }
+#undef GS_PROJ_BWD
+    GS_LAUNCH_CHECK("project_bwd_kernel");
+  }
+  if (grad_w2c != nullptr) {
+    hipLaunchKernelGGL(w2c_finish_kernel, dim3(1), dim3(256), 0, s, (const float*)workspace,
+                       n > 0 ? div_up(n, 64) : (int64_t)0, w2c, grad_w2c);
+    GS_LAUNCH_CHECK("w2c_finish_kernel");
+  }
   return GS_OK;
 }
 

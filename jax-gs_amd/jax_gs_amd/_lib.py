@@ -49,6 +49,8 @@ _SIGS = {
     "gs_preprocess_bwd_w2c_workspace_size": [_I64],
     "gs_preprocess_bwd_w2c": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P,
                               _P, _P, _P, _SZ],
+    "gs_composite_prep_bwd": [_P, _I64, _P, _P, _P, _P, _P, _P, _P],
+    "gs_project_bwd": [_P, _I64, _P, _P, _P, _P, _F, _F, _P, _P, _P, _P, _P, _P, _P, _P, _SZ],
     "gs_eval_sh": [_P, _I64, _I, _I, _P, _P, _P],
     "gs_eval_sh_bwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P],
     "gs_l1_loss": [_P, _I64, _P, _P, _P, _P],

@@ -164,33 +164,76 @@ def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Te
     return image, fT, nc, order
 
 
+class _RenderTiles(torch.autograd.Function):
+    """render_tiles with its VJP (JAX autodiff of rasterizer.py:119-248): the image's
+    cotangent reaches means2D, cov2D ([1,0] gets 0: render_tiles reads cov2D[0,1] only),
+    the opacity logits, the colours and the background through gs_composite_bwd (the
+    compositing replay, gradient records) and gs_composite_prep_bwd (the prologue)."""
+
+    @staticmethod
+    def forward(ctx, means2D, cov2D, opacities, colors, bg, gids, ranges, win, static):
+        H, W = static
+        rec = composite_records(means2D, cov2D, opacities, colors)
+        image, fT, nc, order = composite(rec, gids, ranges, H, W, bg, residuals=True, window=win)
+        ctx.static = static
+        ctx.save_for_backward(cov2D, opacities, bg, rec, gids, ranges, win, fT, nc, order)
+        return image
+
+    @staticmethod
+    def backward(ctx, g_image):
+        H, W = ctx.static
+        cov2D, opacities, bg, rec, gids, ranges, win, fT, nc, order = ctx.saved_tensors
+        dev = rec.device
+        n = rec.shape[0]
+        s = _lib.stream_handle(dev)
+        g_image = g_image.contiguous()
+        grec = torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=dev)
+        gbg = torch.empty((3,), dtype=torch.float32, device=dev) if ctx.needs_input_grad[4] else None
+        _lib.call("gs_composite_bwd", s, n, _lib.ptr(rec), _lib.ptr(gids), gids.shape[0], _lib.ptr(ranges), int(W),
+                  int(H), _lib.ptr(bg), _lib.ptr(g_image), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order),
+                  _lib.ptr(grec), _lib.ptr(gbg), 0, _lib.ptr(win))
+        gm = torch.empty((n, 2), dtype=torch.float32, device=dev)
+        gc = torch.empty((n, 2, 2), dtype=torch.float32, device=dev)
+        go = torch.empty((n, 1), dtype=torch.float32, device=dev)
+        gcol = torch.empty((n, 3), dtype=torch.float32, device=dev)
+        _lib.call("gs_composite_prep_bwd", s, n, _lib.ptr(cov2D), _lib.ptr(opacities), _lib.ptr(grec), _lib.ptr(gm),
+                  _lib.ptr(gc), _lib.ptr(go), _lib.ptr(gcol))
+        return gm, gc, go, gcol, gbg, None, None, None, None
+
+
 def _render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W, background,
                   clamped_windows):
+    """Both reference compositing paths on caller arrays in the reference's layout,
+    differentiable in means2D, cov2D, opacities, colors and a tensor background."""
     dev = means2D.device
+    n = means2D.shape[0]
     _, _, T = num_tiles(W, H)
-    rec = composite_records(means2D, cov2D, opacities, colors)
+    m = check_f32("means2D", means2D, (n, 2), dev)
+    c = check_f32("cov2D", cov2D, (n, 2, 2), dev)
+    o = check_f32("opacities", opacities, (n, 1), dev)
+    col = check_f32("colors", colors, (n, 3), dev)
     ranges = tile_ranges(sorted_tile_ids, T)
     bg = background_tensor(background, dev)
     gids = sorted_gaussian_ids.to(torch.int32).contiguous()
     win = window_from_list(gids) if clamped_windows else None
-    image, _, _, _ = composite(rec, gids, ranges, H, W, bg, residuals=False, window=win)
-    return image
+    return _RenderTiles.apply(m, c, o, col, bg, gids, ranges, win, (int(H), int(W)))
 
 
 def render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W,
                  tile_size: int = TILE_SIZE, background=None):
-    """rasterizer.py:119-248 (forward).  Entries of tile t are the ones whose sorted
-    tile id equals t (searchsorted ranges), capped at 4096 per tile, read through the
-    reference's 512-entry chunk windows: a chunk that starts within 512 entries of the
-    end of the arrays reads their last 512 entries (rasterizer.py:184-190)."""
+    """rasterizer.py:119-248.  Entries of tile t are the ones whose sorted tile id equals t
+    (searchsorted ranges), capped at 4096 per tile, read through the reference's 512-entry
+    chunk windows: a chunk that starts within 512 entries of the end of the arrays reads
+    their last 512 entries (rasterizer.py:184-190).  Differentiable like the reference's:
+    the image's cotangent reaches means2D, cov2D, opacities, colors and a tensor background."""
     if tile_size != TILE_SIZE:
         raise ValueError("only 16x16 tiles are supported (rasterizer.py:6)")
     return _render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W, background,
                          clamped_windows=True)
 
 
-def render_tiles_tpu(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W, background=None):
-    """rasterizer_tpu.py:13-135 (forward): the same compositing with every entry of a
-    tile gathered one by one (its own entries, whatever its position in the arrays)."""
-    return _render_tiles(means2D, cov2D, opacities, colors, sorted_tile_ids, sorted_gaussian_ids, H, W, background,
-                         clamped_windows=False)
+def render_tiles_tpu(*args, **kwargs):
+    """rasterizer_tpu.py:13-135 (defined in rasterizer_tpu.py)."""
+    from .rasterizer_tpu import render_tiles_tpu as impl
+
+    return impl(*args, **kwargs)

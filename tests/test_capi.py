@@ -71,6 +71,15 @@ def test_argument_errors_of_the_window_sh_ssim_and_camera_entry_points():
     assert nb == 16 * 16 * 4
     rc = L.gs_preprocess_bwd_w2c(None, 1000, 16, 3, *([None] * 6), 64, 64, 1.0, 1.0, 0.0, 0.0, *([None] * 7), None, 0)
     assert rc == 1 and b"gs_preprocess_bwd_w2c" in L.gs_last_error()
+    # the module VJPs: a camera cotangent needs its workspace; NULL arrays are rejected
+    rc = L.gs_project_bwd(None, 1000, None, None, None, ctypes.c_void_p(8), 1.0, 1.0, *([None] * 6),
+                          ctypes.c_void_p(8), None, 0)
+    assert rc == 1 and b"workspace" in L.gs_last_error()
+    assert L.gs_project_bwd(None, 1000, *([None] * 3), ctypes.c_void_p(8), 1.0, 1.0, *([None] * 7), None, 0) == 1
+    assert b"gs_project_bwd" in L.gs_last_error()
+    assert L.gs_composite_prep_bwd(None, 10, *([None] * 7)) == 1
+    assert b"gs_composite_prep_bwd" in L.gs_last_error()
+    assert L.gs_composite_prep_bwd(None, 0, *([None] * 7)) == 0
 
 
 def test_load_ply_missing_file():
