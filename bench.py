@@ -43,6 +43,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--step", choices=["auto", "fwd", "fwdbwd", "fwdbwd_stats"], default="auto",
+                    help="what one timed step runs; auto = the configuration's own workload in BASELINE.json: "
+                         "forward only for configs 0 and 3, forward + L1 + backward for 1 and 2, and for 4 the "
+                         "same plus the densification statistics (trainer.py:143-159)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-runs", type=int, default=3, help="timed CPU baseline runs (after one warm-up)")
     ap.add_argument("--stages", action="store_true", help="print per-stage timings to stderr")
@@ -72,13 +76,25 @@ def main():
         getattr(g, f).requires_grad_(True)
     D = sc["sh_degree"]
     N = g.means.shape[0]
+    kind = args.step if args.step != "auto" else {0: "fwd", 3: "fwd", 4: "fwdbwd_stats"}.get(args.config, "fwdbwd")
+    # the densification statistics the trainer accumulates after the backward (trainer.py:143-159)
+    from jax_gs_amd.training.trainer import accumulate_from_extras
+
+    stats_state = {"grad_accum": torch.zeros(N, device=dev), "denom": torch.zeros(N, dtype=torch.int32, device=dev),
+                   "max_radii": torch.zeros(N, device=dev)}
 
     def step():
+        if kind == "fwd":
+            with torch.no_grad():
+                _, extras = render(g, cam, mask=mask, sh_degree=D)
+            return extras
         for f in fields:
             getattr(g, f).grad = None
         image, extras = render(g, cam, mask=mask, sh_degree=D)
         loss = l1_loss(image, tgt)
         loss.backward()
+        if kind == "fwdbwd_stats":
+            accumulate_from_extras(stats_state, g.means.grad, g.means.detach(), cam, extras, active=mask)
         return extras
 
     for _ in range(args.warmup):
@@ -130,6 +146,9 @@ def main():
                       _lib.ptr(cam.W2C.contiguous()), W, H, float(cam.fx), float(cam.fy), float(cam.cx),
                       float(cam.cy), _lib.ptr(grec), *[_lib.ptr(o) for o in outs])
             mark("t6")
+            accumulate_from_extras(stats_state, outs[0], g.means.detach(), cam,
+                                   {"valid_mask": pre["valid"], "radii": pre["radii"]}, active=mask)
+            mark("t7")
         # the trainer's other loss term (trainer.py:18-26): L1 + SSIM forward and VJP of
         # the same frame, timed beside the step (the headline step seeds L1 only)
         Hc, Wc, Cc = image.shape
@@ -224,7 +243,8 @@ def main():
     extra_gbs["densify_and_prune"] = den_bytes / (extra_ms["densify_and_prune"] * 1e-3) / 1e9
     if "ply_pack" in extra_ms:
         extra_gbs["ply_pack"] = (236 + 248) * N / (extra_ms["ply_pack"] * 1e-3) / 1e9
-    names = ["preprocess_fwd", "binning", "composite_fwd", "l1_loss", "composite_bwd", "preprocess_bwd"]
+    names = ["preprocess_fwd", "binning", "composite_fwd", "l1_loss", "composite_bwd", "preprocess_bwd",
+             "densify_stats"]
     stage_ms = {}
     for i, nm in enumerate(names):
         a, z = ev[f"t{i}"], ev[f"t{i + 1}"]
@@ -244,9 +264,13 @@ def main():
     #            list (4 B per entry) and the tile ranges (4 B per tile).
     T = b["ranges"].shape[0] - 1
     bin_bytes = N * 17 + 4 * n_int + 4 * (T + 1)
+    #   densify stats: read grad_means 12 + means 12 + valid 1 + active 1 + radius 4 + the three
+    #                  statistics 12; write the three statistics 12.
+    dens_bytes = N * (12 + 12 + 1 + (1 if mask is not None else 0) + 4 + 12 + 12)
     stage_gbs = {"preprocess_fwd": pre_fwd_bytes / (stage_ms["preprocess_fwd"] * 1e-3) / 1e9,
                  "binning": bin_bytes / (stage_ms["binning"] * 1e-3) / 1e9,
-                 "preprocess_bwd": pre_bwd_bytes / (stage_ms["preprocess_bwd"] * 1e-3) / 1e9}
+                 "preprocess_bwd": pre_bwd_bytes / (stage_ms["preprocess_bwd"] * 1e-3) / 1e9,
+                 "densify_stats": dens_bytes / (stage_ms["densify_stats"] * 1e-3) / 1e9}
     # Compositing is VALU-bound; its unit of work is an evaluated (pixel, entry) pair,
     # i.e. sum over pixels of n_contrib, at ~22 FLOP forward and ~55 FLOP backward.
     pairs = int(nc.to(torch.int64).sum())
@@ -270,7 +294,9 @@ def main():
                   # radix sort of every entry) would move, over the time this design takes
                   "reference_design_bytes": ks_bytes,
                   "reference_design_bytes_over_this_time_frac": ks_bytes / (hbm_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
-    dominant = max(stage_ms, key=stage_ms.get)
+    # the dominant kernel of the timed step's own stages
+    step_stages = {"fwd": names[:3], "fwdbwd": names[:6], "fwdbwd_stats": names}[kind]
+    dominant = max(step_stages, key=stage_ms.get)
     if args.stages:
         print(json.dumps({"stage_ms": stage_ms, "stage_GBps": stage_gbs, "stage_TFLOPs": stage_tflops,
                           "n_interactions": n_int, "pairs": pairs}), file=sys.stderr)
@@ -314,12 +340,15 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": dt * 1e3,
         "fwd_ms": stage_ms["preprocess_fwd"] + stage_ms["binning"] + stage_ms["composite_fwd"],
+        "step": kind,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded scene generator, configs[%d])" % args.config,
-        "config": {"workload": sc["name"] + " fwd+L1+bwd", "gaussians": N, "width": cam.W, "height": cam.H,
+        "config": {"workload": sc["name"] + {"fwd": " fwd", "fwdbwd": " fwd+L1+bwd",
+                                             "fwdbwd_stats": " fwd+L1+bwd+densify stats"}[kind],
+                   "gaussians": N, "width": cam.W, "height": cam.H,
                    "sh_degree": D, "n_interactions": n_int, "gaussians_per_s": N / dt},
         "stage_ms": stage_ms,
         "stage_GBps": stage_gbs,
