@@ -126,11 +126,11 @@ def main():
             pre = preprocess(g, cam, mask=mask, sh_degree=D, projected=False)
             mark("t1")
             b = rasterizer.bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W,
-                                         want_tiles=False, window=True)
+                                         want_tiles=False, window=True, deferred=True)
             mark("t2")
             grec = torch.empty((N, _lib.GS_REC_STRIDE), device=dev)  # cleared by the forward launch
             image, fT, nc, order = rasterizer.composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg,
-                                                        clear_records=grec, window=b["window"])
+                                                        clear_records=grec, window=b["window"], bins=b)
             mark("t3")
             loss = torch.empty((), device=dev)
             gimg = torch.empty_like(image)

@@ -82,7 +82,7 @@ const char* gs_last_error(void);
  * gs_eval_sh_bwd.  8: gs_l1_ssim_window, gs_l1_ssim_window_bwd.  9: compositing records carry
  * a cap flag in slot 11.  10: that flag is no_cap (1.0 = proven below the cap, rounding
  * included; 0.0 = not proven), read by gs_composite_bwd; gs_composite_prep_bwd,
- * gs_project_bwd. */
+ * gs_project_bwd.  11: gs_bin_deferred, gs_composite_fwd_deferred. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -127,6 +127,20 @@ int gs_bin(void* stream, int64_t n, const float* means2d, const float* radii,
            const uint8_t* valid, const float* depths, int width, int height,
            int64_t capacity, void* workspace, size_t workspace_bytes, int32_t* sorted_gids,
            int32_t* sorted_tiles, int32_t* ranges, int32_t* stats);
+
+/* gs_bin for the render path, with the entry list deferred to the compositing forward.
+ * Same inputs and outputs as gs_bin without sorted_tiles (capacity > 0), except that
+ * sorted_gids is written here only when the entries exceed the capacity or the stats set
+ * GS_STAT_WINDOW_CLAMPED.  Otherwise gs_composite_fwd_deferred, given this workspace
+ * untouched, writes each tile's entries up to those its walk meets, which cover every
+ * entry gs_composite_bwd reads (below the tile's largest n_contrib); the rest of the list
+ * stays unwritten.  At full size the compositing meets 2-10 % of the entries (tiles turn
+ * opaque early), and writing them all was the binning's costliest step.  Same reference
+ * interface as gs_bin (rasterizer.py:12-116, renderer.py:57-90). */
+int gs_bin_deferred(void* stream, int64_t n, const float* means2d, const float* radii,
+                    const uint8_t* valid, const float* depths, int width, int height,
+                    int64_t capacity, void* workspace, size_t workspace_bytes, int32_t* sorted_gids,
+                    int32_t* ranges, int32_t* stats);
 
 /* gs_bin without a workspace argument and without any allocation: the workspace is a
  * library-owned device array of GS_BIN_STATIC_SCRATCH_BYTES (128 MiB) that every GPU
@@ -218,6 +232,20 @@ int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_
                      int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
                      float* image, float* final_T, int32_t* n_contrib, int32_t* tile_order, float* clear_records,
                      const gs_window_t* window);
+
+/* gs_composite_fwd after gs_bin_deferred (the same n, width, height and capacity; its
+ * workspace, sorted_gids, ranges and stats).  When the binning deferred the entry list,
+ * each tile's walk reads its 8x8-tile superblock's list from the workspace (the words
+ * whose tile rectangle holds the tile, in the list's order, are the tile's entries) and
+ * writes the entries it meets into sorted_gids; otherwise it reads sorted_gids as
+ * gs_composite_fwd does.  Outputs are those of gs_composite_fwd on gs_bin's full list,
+ * bit for bit; gs_composite_bwd then takes sorted_gids as usual.  Replaces the same
+ * reference code as gs_composite_fwd (rasterizer.py:157-248). */
+int gs_composite_fwd_deferred(void* stream, int64_t n, const float* records, int32_t* sorted_gids,
+                              int64_t capacity, const int32_t* ranges, const int32_t* stats,
+                              const void* bin_workspace, size_t bin_workspace_bytes, int width, int height,
+                              const float* background, float* image, float* final_T, int32_t* n_contrib,
+                              int32_t* tile_order, float* clear_records, const gs_window_t* window);
 
 /* Vector-Jacobian product of gs_composite_fwd (JAX autodiff of render_tiles).
  * tile_order is the forward's (NULL: a fixed order; results agree up to the order of

@@ -40,6 +40,7 @@
 // Radix passes use one wave per workgroup over a contiguous range (in-wave rank with
 // ballot "match any"), a per-digit spine scan across workgroups, and no
 // inter-workgroup waiting.  There are no same-address global atomics.
+#include "gs_bins.h"
 #include "gs_common.h"
 
 #include <algorithm>
@@ -49,7 +50,6 @@ namespace gs {
 namespace {
 
 constexpr int kScanBlock = 256;
-constexpr int kSB = 8;                            // superblock = 8x8 tiles
 constexpr int kSBSpan = 3;                        // superblocks a Gaussian meets per axis
 constexpr int kChunk = 256;                       // Gaussians per chunk of the tile pass
 constexpr int kSeg = 16;                          // chunks per segment of the chunk-offset scan
@@ -65,30 +65,6 @@ constexpr int kBlkStats = 3;  // per bin_prep block: cap violations, negative de
 __device__ inline uint64_t lanemask_lt() {
   const unsigned lane = threadIdx.x & 63;
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
-}
-
-// Packed Gaussian word: id (26 bits) | tminx (12) | tminy (12) | w-1 (4) | h-1 (4) |
-// has-entries (1).
-struct Packed {
-  uint32_t gid;
-  int x0, y0, w, h;  // w = h = 0 when the Gaussian meets no tile
-};
-__device__ inline uint64_t pack(uint32_t gid, int x0, int y0, int w, int h) {
-  uint64_t v = gid;
-  if (w > 0 && h > 0)
-    v |= ((uint64_t)x0 << 26) | ((uint64_t)y0 << 38) | ((uint64_t)(w - 1) << 50) | ((uint64_t)(h - 1) << 54) |
-         (1ull << 58);
-  return v;
-}
-__device__ inline Packed unpack(uint64_t v) {
-  Packed p;
-  p.gid = (uint32_t)(v & 0x3FFFFFFull);
-  const bool has = (v >> 58) & 1;
-  p.x0 = (int)((v >> 26) & 0xFFF);
-  p.y0 = (int)((v >> 38) & 0xFFF);
-  p.w = has ? (int)((v >> 50) & 0xF) + 1 : 0;
-  p.h = has ? (int)((v >> 54) & 0xF) + 1 : 0;
-  return p;
 }
 
 // Superblock rectangle [sx0, sx1] x [sy0, sy1] of a Gaussian (empty when w == 0).
@@ -984,7 +960,9 @@ __device__ inline void write_chunk(const uint4& d, const uint64_t* __restrict__ 
 // OFFSET: the entries go after the 256 slots of every negative-depth Gaussian (the
 // reference's full arrays): the outputs start at 256 * stats[GS_STAT_NEGATIVE_DEPTH],
 // which tile_scan_stats_kernel has written.
-template <bool WITH_TILES, bool OFFSET>
+// DEFER (gs_bin_deferred): nothing is written when entries_deferred holds; the compositing
+// forward then writes the entries it meets.
+template <bool WITH_TILES, bool OFFSET, bool DEFER>
 __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restrict__ n_chunks, int64_t cmax,
                                                          const uint4* __restrict__ desc,
                                                          const uint64_t* __restrict__ pval, uint32_t n_gauss, int TX,
@@ -994,6 +972,7 @@ __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restr
                                                          int32_t* __restrict__ out_gid,
                                                          int32_t* __restrict__ out_tile,
                                                          const int32_t* __restrict__ stats) {
+  if (DEFER && entries_deferred(ranges, T, cap, stats)) return;
   const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
   const uint32_t C = (uint32_t)min<int64_t>((int64_t)*n_chunks, cmax);
@@ -1124,7 +1103,8 @@ namespace gs {
 namespace {
 int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, const uint8_t* valid,
             const float* depths, int width, int height, int64_t capacity, void* workspace, size_t workspace_bytes,
-            int32_t* sorted_gids, int32_t* sorted_tiles, int32_t* ranges, int32_t* stats, bool ref_offset) {
+            int32_t* sorted_gids, int32_t* sorted_tiles, int32_t* ranges, int32_t* stats, bool ref_offset,
+            bool deferred = false) {
   GS_REQUIRE(n >= 0 && n <= ((int64_t)1 << 26), "gs_bin: n must be in [0, 2^26] (got %lld)", (long long)n);
   GS_REQUIRE(width > 0 && height > 0 && width <= 4096 * kTile && height <= 4096 * kTile,
              "gs_bin: bad image size %dx%d (each side at most 65536)", width, height);
@@ -1227,15 +1207,18 @@ int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, c
   hipLaunchKernelGGL(tile_scan_stats_kernel, dim3(1), dim3(kBig), 0, s, tot, P.T, blk, P.G_d, P.cap, n, ranges,
                      stats);
   GS_LAUNCH_CHECK("tile_scan_stats_kernel");
-#define GS_WRITE_LAUNCH(TILES, OFF)                                                                             \
-  hipLaunchKernelGGL((tile_write_kernel<TILES, OFF>), dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, desc, \
-                     sbval, (uint32_t)n, P.TX, P.TY, cnt, gsum, ranges, P.T, P.cap, sorted_gids, sorted_tiles, stats)
+#define GS_WRITE_LAUNCH(TILES, OFF, DEFER)                                                                     \
+  hipLaunchKernelGGL((tile_write_kernel<TILES, OFF, DEFER>), dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, \
+                     desc, sbval, (uint32_t)n, P.TX, P.TY, cnt, gsum, ranges, P.T, P.cap, sorted_gids, sorted_tiles, \
+                     stats)
   if (ref_offset)
-    GS_WRITE_LAUNCH(true, true);
+    GS_WRITE_LAUNCH(true, true, false);
   else if (sorted_tiles != nullptr)
-    GS_WRITE_LAUNCH(true, false);
+    GS_WRITE_LAUNCH(true, false, false);
+  else if (deferred)
+    GS_WRITE_LAUNCH(false, false, true);
   else
-    GS_WRITE_LAUNCH(false, false);
+    GS_WRITE_LAUNCH(false, false, false);
 #undef GS_WRITE_LAUNCH
   GS_LAUNCH_CHECK("tile_write_kernel");
   return GS_OK;
@@ -1250,6 +1233,35 @@ extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float
   return bin_run(stream, n, means2d, radii, valid, depths, width, height, capacity, workspace, workspace_bytes,
                  sorted_gids, sorted_tiles, ranges, stats, false);
 }
+
+extern "C" int gs_bin_deferred(void* stream, int64_t n, const float* means2d, const float* radii,
+                               const uint8_t* valid, const float* depths, int width, int height, int64_t capacity,
+                               void* workspace, size_t workspace_bytes, int32_t* sorted_gids, int32_t* ranges,
+                               int32_t* stats) {
+  return bin_run(stream, n, means2d, radii, valid, depths, width, height, capacity, workspace, workspace_bytes,
+                 sorted_gids, nullptr, ranges, stats, false, true);
+}
+
+namespace gs {
+int superblock_lists(int64_t n, int width, int height, int64_t capacity, const void* workspace,
+                     size_t workspace_bytes, const int32_t* stats, SBLists* out) {
+  GS_REQUIRE(n >= 0 && n <= ((int64_t)1 << 26) && width > 0 && height > 0 && width <= 4096 * kTile &&
+                 height <= 4096 * kTile,
+             "superblock lists: bad sizes (n %lld, %dx%d)", (long long)n, width, height);
+  const BinPlan P = make_plan(n, width, height, capacity);
+  GS_REQUIRE(workspace != nullptr && workspace_bytes >= P.total,
+             "superblock lists: a workspace of %zu bytes is smaller than the binning's %zu", workspace_bytes,
+             P.total);
+  const char* ws = (const char*)workspace;
+  out->words = (const uint64_t*)(ws + (P.sb_passes == 1 ? P.o_pv0 : P.o_pv1));
+  out->ranges = (const int32_t*)(ws + P.o_sbr);
+  out->n_words = P.pcap;
+  out->SX = P.SX;
+  out->cap = P.cap;
+  out->stats = stats;
+  return GS_OK;
+}
+}  // namespace gs
 
 // Same boundary rule on a caller-provided sorted array that may hold -1 (negative
 // depth) and T (sentinel) entries.

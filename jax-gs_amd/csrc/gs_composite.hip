@@ -43,6 +43,7 @@
 // reference: the cap
 // min(0.99, .) passes no gradient when it binds (half at a tie), gated entries pass
 // none.
+#include "gs_bins.h"
 #include "gs_common.h"
 #include "gs_cull.h"
 
@@ -334,13 +335,21 @@ __device__ inline uint64_t probe_test(const Probe& p, float x0, float x1, float 
 
 // WIN: the default path's chunk windows (see probe_gid); without it the id fetch compiles
 // to the plain one.
-template <int PPT, bool WIN, bool O32>
+// SB (gs_composite_fwd_deferred): when the binning deferred the entry list
+// (entries_deferred), each wave walks its tile's superblock list instead (gs_bins.h): a
+// batch is 64 words of the list, a word is one of the tile's entries when its rectangle
+// holds the tile, and an entry's index in the tile's list is the number of member words
+// before it.  The wave writes the ids of the entries it meets to gids_out[start + index]
+// (its batches whole, so every entry below the tile's largest n_contrib is written: the
+// part of the list the backward replays) and stops where the walk over the entry list
+// would stop.  Otherwise it walks the entry list as without SB.
+template <int PPT, bool WIN, bool O32, bool SB>
 __global__ __launch_bounds__(64) void composite_fwd_kernel(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
     float* __restrict__ img, float* __restrict__ finalT, int32_t* __restrict__ ncontrib,
     int32_t* __restrict__ tile_cost, float4* __restrict__ clear, int64_t n_clear,
-    const gs_window_t* __restrict__ win) {
+    const gs_window_t* __restrict__ win, const SBLists sbl, int32_t* __restrict__ gids_out) {
   constexpr int WPT = 4 / PPT;  // waves per tile
   // Every workgroup clears its slice of the caller's array after its own outputs (stores
   // and loads share one wait counter, so stores issued before the walk would hold up its
@@ -381,18 +390,9 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
 
   bool done = false;
   int walked = 0;
-  const int64_t thr = WIN ? win->thr : 0;
-  // The batch's probe records were requested a batch ago; the next batch's go out after
-  // the batch's test, so that the test waits for nothing requested since (loads complete
-  // in order: a wait for one waits for every earlier one), and the id two batches ahead is
-  // clamped where it is used, a batch later.
-  Ahead g_ahead = probe_gid_ahead<WIN>(gids, start, 64 + lane, n, win, thr);
-  Probe pr = probe_load(rec, probe_gid<WIN>(gids, start, lane, n, num_g, win, thr));
-  for (int b0 = 0; b0 < n && !done; b0 += 64) {
-    const int gk = rec_key<O32>(pr.g);  // the lane's record key (read where the lane survives)
-    uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
-    pr = probe_load(rec, ahead_gid(g_ahead, num_g));
-    g_ahead = probe_gid_ahead<WIN>(gids, start, b0 + 128 + lane, n, win, thr);
+  // Walks the survivors m of a batch (lane j's record key in gk); kpos(j) is the index in
+  // the tile's list of the batch's entry j.
+  auto walk = [&](uint64_t m, const int gk, auto kpos) {
     // Survivors are walked in groups of G (G = 2 when a lane holds one pixel): the
     // group's records are in SGPRs before it is blended and the next group's scalar
     // loads are issued first, so their latency is covered by G entries' arithmetic
@@ -407,7 +407,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
     // leaves C and T unchanged; measured faster than per-pixel branches, 226 vs 251 us
     // on cfg2)
     auto blend = [&](const Rec& e, int kidx) {
-      const int kk = b0 + kidx + 1;  // entries met so far, this one included
+      const int kk = kpos(kidx) + 1;  // entries met so far, this one included
       const float dx = px - e.mx;
       const float Adx2l = fmaf(e.A * dx, dx, e.lop), Bdx = e.B * dx;
 #pragma unroll
@@ -498,7 +498,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
         for (int h = 0; h < G; ++h) {
           if (k[h] < 0) break;
           ++walked;
-          const int kk = b0 + k[h] + 1;  // entries met so far, this one included
+          const int kk = kpos(k[h]) + 1;  // entries met so far, this one included
           const float dx = px - e[h].mx;
           const float Adx2l = fmaf(e[h].A * dx, dx, e[h].lop), Bdx = e[h].B * dx;
 #pragma unroll
@@ -552,6 +552,66 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
           }
         }
       }
+    }
+  };
+
+  bool deferred = false;
+  if constexpr (SB) deferred = entries_deferred(ranges, T, sbl.cap, sbl.stats);
+  if (!deferred) {
+    const int64_t thr = WIN ? win->thr : 0;
+    // The batch's probe records were requested a batch ago; the next batch's go out after
+    // the batch's test, so that the test waits for nothing requested since (loads complete
+    // in order: a wait for one waits for every earlier one), and the id two batches ahead
+    // is clamped where it is used, a batch later.
+    Ahead g_ahead = probe_gid_ahead<WIN>(gids, start, 64 + lane, n, win, thr);
+    Probe pr = probe_load(rec, probe_gid<WIN>(gids, start, lane, n, num_g, win, thr));
+    for (int b0 = 0; b0 < n && !done; b0 += 64) {
+      const int gk = rec_key<O32>(pr.g);  // the lane's record key (read where the lane survives)
+      const uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
+      pr = probe_load(rec, ahead_gid(g_ahead, num_g));
+      g_ahead = probe_gid_ahead<WIN>(gids, start, b0 + 128 + lane, n, win, thr);
+      walk(m, gk, [&](int j) { return b0 + j; });
+    }
+  } else if (n > 0) {
+    // the tile's superblock list, clamped to the word array
+    const int s = (ty / kSB) * sbl.SX + tx / kSB;
+    int64_t j0 = sbl.ranges[s], j1 = sbl.ranges[s + 1];
+    j0 = j0 < 0 ? 0 : (j0 > sbl.n_words ? sbl.n_words : j0);
+    j1 = j1 < j0 ? j0 : (j1 > sbl.n_words ? sbl.n_words : j1);
+    int32_t* __restrict__ out = gids_out + start;  // start + index < start + n <= n_entries
+    // Entries of a batch of words: the lane's id (-1: not an entry), its index in the
+    // tile's list (kl); kb counts the entries of the batches seen so far.  The ids are
+    // stored for the backward.
+    int kb = 0;
+    auto members = [&](uint64_t w, int& kl) -> int {
+      const Packed p = unpack(w);
+      int g = (p.w > 0 && p.gid < (uint32_t)num_g && p.x0 <= tx && tx < p.x0 + p.w && p.y0 <= ty &&
+               ty < p.y0 + p.h)
+                  ? (int)p.gid
+                  : -1;
+      const uint64_t M = __ballot(g >= 0);
+      kl = kb + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(M >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)M, 0u));
+      kb += __popcll(M);
+      if (kl >= n) g = -1;  // the first n entries only (rasterizer.py:180-181)
+      if (g >= 0) out[kl] = g;
+      return g;
+    };
+    // Pipelined as the entry walk: the words two batches ahead and the records (with the
+    // member test) one batch ahead are in flight while a batch is walked.
+    uint64_t w_ahead = j0 + 64 + lane < j1 ? sbl.words[j0 + 64 + lane] : 0ull;
+    int kl = 0;
+    Probe pr = probe_load(rec, members(j0 + lane < j1 ? sbl.words[j0 + lane] : 0ull, kl));
+    int k_end = kb;  // entries up to the end of the batch being walked
+    for (int64_t jb = j0; jb < j1 && !done; jb += 64) {
+      const int gk = rec_key<O32>(pr.g);
+      const int klb = kl;
+      const uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
+      const bool more = k_end < n && jb + 64 < j1;
+      pr = probe_load(rec, more ? members(w_ahead, kl) : -1);
+      w_ahead = more && jb + 128 + lane < j1 ? sbl.words[jb + 128 + lane] : 0ull;
+      walk(m, gk, [&](int j) { return bcast_i(klb, j); });
+      if (!more) break;
+      k_end = kb;
     }
   }
   const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];
@@ -989,28 +1049,33 @@ extern "C" int gs_window_from_list(void* stream, const int32_t* sorted_gids, int
   return GS_OK;
 }
 
-extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
-                                int64_t n_entries, const int32_t* ranges, int width, int height,
-                                const float* background, float* image, float* final_T, int32_t* n_contrib,
-                                int32_t* tile_order, float* clear_records, const gs_window_t* window) {
-  GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "gs_composite_fwd: n out of range");
-  GS_REQUIRE(n_entries >= 0, "gs_composite_fwd: n_entries must be >= 0");
-  GS_REQUIRE(width > 0 && height > 0, "gs_composite_fwd: bad image size %dx%d", width, height);
-  GS_REQUIRE(ranges && background && image, "gs_composite_fwd: NULL argument");
-  GS_REQUIRE(n == 0 || n_entries == 0 || (records && sorted_gids), "gs_composite_fwd: NULL records/gids");
+namespace {
+int composite_fwd_run(const char* name, void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
+                      int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
+                      float* image, float* final_T, int32_t* n_contrib, int32_t* tile_order, float* clear_records,
+                      const gs_window_t* window, const SBLists* sbl, int32_t* gids_out) {
+  GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "%s: n out of range", name);
+  GS_REQUIRE(n_entries >= 0, "%s: n_entries must be >= 0", name);
+  GS_REQUIRE(width > 0 && height > 0, "%s: bad image size %dx%d", name, width, height);
+  GS_REQUIRE(ranges && background && image, "%s: NULL argument", name);
+  GS_REQUIRE(n == 0 || n_entries == 0 || (records && sorted_gids), "%s: NULL records/gids", name);
   const int TX = (width + kTile - 1) / kTile, TY = (height + kTile - 1) / kTile;
   const int T = TX * TY;
   const int nblk = tile_blocks(TX, TY);
   hipStream_t s = (hipStream_t)stream;
   GS_REQUIRE(clear_records == nullptr || ((uintptr_t)clear_records & 15) == 0,
-             "gs_composite_fwd: clear_records must be 16-byte aligned");
+             "%s: clear_records must be 16-byte aligned", name);
   const int64_t n4_clear = clear_records ? n * kRec / 4 : 0;  // kRec = 12: whole float4s
-#define GS_FWD_LAUNCH1(PPT, WPT, WIN, O32)                                                                    \
-  hipLaunchKernelGGL((composite_fwd_kernel<PPT, WIN, O32>), dim3(nblk * (WPT)), dim3(64), 0, s,                 \
+  const SBLists none{};
+#define GS_FWD_LAUNCH2(PPT, WPT, WIN, O32, SB)                                                                  \
+  hipLaunchKernelGGL((composite_fwd_kernel<PPT, WIN, O32, SB>), dim3(nblk * (WPT)), dim3(64), 0, s,             \
                      (const float4*)records, (int)n, sorted_gids, n_entries, ranges, width, height, TX, T,        \
-                     background, image, final_T, n_contrib, tile_order, (float4*)clear_records, n4_clear, window)
+                     background, image, final_T, n_contrib, tile_order, (float4*)clear_records, n4_clear, window, \
+                     SB ? *sbl : none, gids_out)
+#define GS_FWD_LAUNCH1(PPT, WPT, WIN, O32) \
+  if (sbl) GS_FWD_LAUNCH2(PPT, WPT, WIN, O32, true); else GS_FWD_LAUNCH2(PPT, WPT, WIN, O32, false)
 #define GS_FWD_LAUNCH(PPT, WPT, WIN) \
-  if (o32) GS_FWD_LAUNCH1(PPT, WPT, WIN, true); else GS_FWD_LAUNCH1(PPT, WPT, WIN, false)
+  if (o32) { GS_FWD_LAUNCH1(PPT, WPT, WIN, true); } else { GS_FWD_LAUNCH1(PPT, WPT, WIN, false); }
   const bool win = window != nullptr, o32 = rec_offsets_fit(n);
   if (pick_ppt(T) == 4 && T >= kFwdOneWaveTiles) {
     if (win) { GS_FWD_LAUNCH(4, 1, true); } else { GS_FWD_LAUNCH(4, 1, false); }
@@ -1021,12 +1086,38 @@ extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, c
   }
 #undef GS_FWD_LAUNCH
 #undef GS_FWD_LAUNCH1
+#undef GS_FWD_LAUNCH2
   GS_LAUNCH_CHECK("composite_fwd_kernel");
   if (tile_order) {
     hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(1024), 0, s, tile_order, T);
     GS_LAUNCH_CHECK("tile_order_kernel");
   }
   return GS_OK;
+}
+}  // namespace
+
+extern "C" int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
+                                int64_t n_entries, const int32_t* ranges, int width, int height,
+                                const float* background, float* image, float* final_T, int32_t* n_contrib,
+                                int32_t* tile_order, float* clear_records, const gs_window_t* window) {
+  return composite_fwd_run("gs_composite_fwd", stream, n, records, sorted_gids, n_entries, ranges, width, height,
+                           background, image, final_T, n_contrib, tile_order, clear_records, window, nullptr,
+                           nullptr);
+}
+
+extern "C" int gs_composite_fwd_deferred(void* stream, int64_t n, const float* records, int32_t* sorted_gids,
+                                         int64_t capacity, const int32_t* ranges, const int32_t* stats,
+                                         const void* bin_workspace, size_t bin_workspace_bytes, int width, int height,
+                                         const float* background, float* image, float* final_T, int32_t* n_contrib,
+                                         int32_t* tile_order, float* clear_records, const gs_window_t* window) {
+  GS_REQUIRE(capacity > 0, "gs_composite_fwd_deferred: capacity must be > 0 (got %lld)", (long long)capacity);
+  GS_REQUIRE(stats != nullptr && (n == 0 || sorted_gids != nullptr), "gs_composite_fwd_deferred: NULL argument");
+  SBLists sbl;
+  const int rc = superblock_lists(n, width, height, capacity, bin_workspace, bin_workspace_bytes, stats, &sbl);
+  if (rc != GS_OK) return rc;
+  return composite_fwd_run("gs_composite_fwd_deferred", stream, n, records, sorted_gids, capacity, ranges, width,
+                           height, background, image, final_T, n_contrib, tile_order, clear_records, window, &sbl,
+                           sorted_gids);
 }
 
 extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,

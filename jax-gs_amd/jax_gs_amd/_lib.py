@@ -37,6 +37,7 @@ _SIGS = {
     "gs_composite_prep": [_P, _I64, _P, _P, _P, _P, _P],
     "gs_bin_workspace_size": [_I64, _I, _I, _I64],
     "gs_bin": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _SZ, _P, _P, _P, _P],
+    "gs_bin_deferred": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _SZ, _P, _P, _P],
     "gs_bin_static": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _P, _P, _P],
     "gs_bin_reference_workspace_size": [_I64, _I, _I],
     "gs_bin_reference": [_P, _I64, _P, _P, _P, _P, _I, _I, _P, _SZ, _P, _P, _P, _P],
@@ -44,6 +45,7 @@ _SIGS = {
     "gs_window_from_list": [_P, _P, _I64, _P],
     "gs_window_from_bins": [_P, _I64, _P, _P, _P, _P, _I, _I, _P, _I64, _P, _P],
     "gs_composite_fwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P],
+    "gs_composite_fwd_deferred": [_P, _I64, _P, _P, _I64, _P, _P, _P, _SZ, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P],
     "gs_preprocess_bwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P, _P],
     "gs_preprocess_bwd_w2c_workspace_size": [_I64],
@@ -84,7 +86,7 @@ _RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_
 _lib = None
 
 
-ABI_VERSION = 10  # gs_abi_version() of the signatures bound below
+ABI_VERSION = 11  # gs_abi_version() of the signatures bound below
 
 
 class NativeLibraryMissing(RuntimeError):

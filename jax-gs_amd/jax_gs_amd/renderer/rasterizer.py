@@ -41,7 +41,9 @@ class BinResult(dict):
     sorted_gids / sorted_tiles: [capacity] int32, the first n entries valid;
     ranges: [T+1] int32 (searchsorted-left boundaries); stats: [16] int32;
     n_interactions: 0-d int32 view of stats; window: the default path's chunk window
-    (gs_window_t bytes) when asked for, else None."""
+    (gs_window_t bytes) when asked for, else None; deferred: the entry list is left to
+    the compositing forward (composite(..., bins=this)), which reads the superblock lists
+    in workspace."""
 
 
 def new_window(dev) -> torch.Tensor:
@@ -59,10 +61,15 @@ def window_from_list(sorted_gids: torch.Tensor) -> torch.Tensor:
 
 
 def bin_gaussians(means2d: torch.Tensor, radii: torch.Tensor, valid: torch.Tensor, depths: torch.Tensor, H: int,
-                  W: int, capacity: int | None = None, want_tiles: bool = True, window: bool = False) -> BinResult:
+                  W: int, capacity: int | None = None, want_tiles: bool = True, window: bool = False,
+                  deferred: bool = False) -> BinResult:
     """gs_bin: the entries in the reference's (tile, depth quantum, id) order, compact.
     window=True also builds the default path's chunk window of that list (the reference's
-    rasterizer.py:184-190 clamp, gs_window_from_bins)."""
+    rasterizer.py:184-190 clamp, gs_window_from_bins).  deferred=True (gs_bin_deferred, no
+    sorted_tiles) leaves the entry list to composite(..., bins=result), which writes the
+    entries its walk meets: the part gs_composite_bwd reads."""
+    if deferred and want_tiles:
+        raise ValueError("bin_gaussians: deferred binning writes no sorted_tiles (want_tiles=False)")
     dev = means2d.device
     n = means2d.shape[0]
     means2d = check_f32("means2D", means2d, (n, 2), dev)
@@ -77,16 +84,22 @@ def bin_gaussians(means2d: torch.Tensor, radii: torch.Tensor, valid: torch.Tenso
     tiles = torch.empty((cap,), dtype=torch.int32, device=dev) if want_tiles else None
     ranges = torch.empty((T + 1,), dtype=torch.int32, device=dev)
     stats = torch.empty((_lib.GS_NUM_STATS,), dtype=torch.int32, device=dev)
-    _lib.call("gs_bin", _lib.stream_handle(dev), n, _lib.ptr(means2d), _lib.ptr(radii), _lib.ptr(v), _lib.ptr(depths),
-              int(W), int(H), cap, _lib.ptr(ws), ws_bytes, _lib.ptr(gids), _lib.ptr(tiles), _lib.ptr(ranges),
-              _lib.ptr(stats))
+    if deferred:
+        _lib.call("gs_bin_deferred", _lib.stream_handle(dev), n, _lib.ptr(means2d), _lib.ptr(radii), _lib.ptr(v),
+                  _lib.ptr(depths), int(W), int(H), cap, _lib.ptr(ws), ws_bytes, _lib.ptr(gids), _lib.ptr(ranges),
+                  _lib.ptr(stats))
+    else:
+        _lib.call("gs_bin", _lib.stream_handle(dev), n, _lib.ptr(means2d), _lib.ptr(radii), _lib.ptr(v),
+                  _lib.ptr(depths), int(W), int(H), cap, _lib.ptr(ws), ws_bytes, _lib.ptr(gids), _lib.ptr(tiles),
+                  _lib.ptr(ranges), _lib.ptr(stats))
     win = None
     if window:
         win = new_window(dev)
         _lib.call("gs_window_from_bins", _lib.stream_handle(dev), n, _lib.ptr(means2d), _lib.ptr(radii), _lib.ptr(v),
                   _lib.ptr(depths), int(W), int(H), _lib.ptr(gids), cap, _lib.ptr(stats), _lib.ptr(win))
     return BinResult(sorted_gids=gids, sorted_tiles=tiles, ranges=ranges, stats=stats,
-                     n_interactions=stats[_lib.STAT["n_interactions"]], capacity=cap, num_tiles=T, window=win)
+                     n_interactions=stats[_lib.STAT["n_interactions"]], capacity=cap, num_tiles=T, window=win,
+                     deferred=deferred, workspace=ws if deferred else None, n=n)
 
 
 def get_tile_interactions(means2D, radii, valid_mask, depths, H, W, tile_size: int = TILE_SIZE):
@@ -142,7 +155,7 @@ def composite_records(means2D, cov2D, opacities, colors) -> torch.Tensor:
 
 def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Tensor, H: int, W: int,
               background: torch.Tensor, residuals: bool = True, clear_records: torch.Tensor | None = None,
-              window: torch.Tensor | None = None):
+              window: torch.Tensor | None = None, bins: BinResult | None = None):
     """Front-to-back compositing; returns (image [H,W,3], final_T [H,W], n_contrib [H,W],
     tile_order [T]), the last three the backward's residuals (None unless residuals):
     tile_order lists the tiles longest walk first, the backward's launch order.
@@ -151,16 +164,28 @@ def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Te
     (rasterizer_tpu.py:90-97); a window (window_from_list, bin_gaussians(window=True))
     reads the default path's clamped 512-entry chunk windows (rasterizer.py:184-190),
     which differ only for chunks that start within 512 slots of the end of the
-    reference's arrays."""
+    reference's arrays.  bins: the BinResult of a deferred binning whose sorted_gids and
+    ranges these are (gs_composite_fwd_deferred); the results are the same as with the
+    full list."""
     dev = records.device
     _, _, T = num_tiles(W, H)
     image = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
     fT = torch.empty((H, W), dtype=torch.float32, device=dev) if residuals else None
     nc = torch.empty((H, W), dtype=torch.int32, device=dev) if residuals else None
     order = torch.empty((T,), dtype=torch.int32, device=dev) if residuals else None
-    _lib.call("gs_composite_fwd", _lib.stream_handle(dev), records.shape[0], _lib.ptr(records),
-              _lib.ptr(sorted_gids), sorted_gids.shape[0], _lib.ptr(ranges), int(W), int(H), _lib.ptr(background), _lib.ptr(image),
-              _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(clear_records), _lib.ptr(window))
+    if bins is not None and bins["deferred"]:
+        if sorted_gids is not bins["sorted_gids"] or ranges is not bins["ranges"] or records.shape[0] != bins["n"]:
+            raise ValueError("composite: bins must be the deferred binning of these entries and records")
+        ws = bins["workspace"]
+        _lib.call("gs_composite_fwd_deferred", _lib.stream_handle(dev), records.shape[0], _lib.ptr(records),
+                  _lib.ptr(sorted_gids), bins["capacity"], _lib.ptr(ranges), _lib.ptr(bins["stats"]), _lib.ptr(ws),
+                  ws.shape[0], int(W), int(H), _lib.ptr(background), _lib.ptr(image), _lib.ptr(fT), _lib.ptr(nc),
+                  _lib.ptr(order), _lib.ptr(clear_records), _lib.ptr(window))
+    else:
+        _lib.call("gs_composite_fwd", _lib.stream_handle(dev), records.shape[0], _lib.ptr(records),
+                  _lib.ptr(sorted_gids), sorted_gids.shape[0], _lib.ptr(ranges), int(W), int(H),
+                  _lib.ptr(background), _lib.ptr(image), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order),
+                  _lib.ptr(clear_records), _lib.ptr(window))
     return image, fT, nc, order
 
 

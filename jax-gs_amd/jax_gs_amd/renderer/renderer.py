@@ -39,7 +39,7 @@ class _Render(torch.autograd.Function):
         cam = Camera(W, H, fx, fy, cx, cy, w2c, None)
         pre = preprocess(g, cam, mask=mask, sh_degree=sh_degree, records=True, projected=False)
         b = bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W, capacity=capacity,
-                          want_tiles=False, window=not tpu)
+                          want_tiles=False, window=not tpu, deferred=True)
         # the gradient records the backward accumulates into, cleared by the forward's
         # compositing launch (its waves are arithmetic-bound: the stores are free)
         n = means.shape[0]
@@ -47,7 +47,7 @@ class _Render(torch.autograd.Function):
                 if any(ctx.needs_input_grad[:5]) else None)
         win = b["window"]
         image, fT, nc, order = composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg, residuals=True,
-                                         clear_records=grec, window=win)
+                                         clear_records=grec, window=win, bins=b)
         ctx.static = static
         ctx.grec_fresh = grec is not None
         # radii, valid and stats carry no gradient: no zero cotangents for them

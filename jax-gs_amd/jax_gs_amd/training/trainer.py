@@ -111,11 +111,11 @@ def _train_step_fused(state, target_image, camera, optimizer, sh_degree, fast_tp
         pre = preprocess(params, camera, mask=active, sh_degree=sh_degree, records=True, projected=False)
         # the default rasterizer's clamped chunk windows unless fast_tpu_rasterizer
         b = bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], H, W, want_tiles=False,
-                          window=not fast_tpu_rasterizer)
+                          window=not fast_tpu_rasterizer, deferred=True)
         bg = background_tensor(None, dev)
         grec = torch.empty((n, _lib.GS_REC_STRIDE), dtype=torch.float32, device=dev)  # cleared by the forward
         image, fT, nc, order = composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg, residuals=True,
-                                         clear_records=grec, window=b["window"])
+                                         clear_records=grec, window=b["window"], bins=b)
         # loss (trainer.py:18-26): one kernel for the L1 and SSIM means
         tgt = target_image.to(device=dev, dtype=torch.float32).contiguous()
         Hh, Ww, C = image.shape

@@ -32,7 +32,7 @@ def test_binding_covers_every_declared_symbol():
 
 def test_abi_version_and_workspace_query_without_gpu():
     L = _lib.lib()
-    assert L.gs_abi_version() == _lib.ABI_VERSION == 10
+    assert L.gs_abi_version() == _lib.ABI_VERSION == 11
     # size query: pure host arithmetic, grows with the number of Gaussians
     a = L.gs_bin_workspace_size(1000, 64, 64, 0)
     b = L.gs_bin_workspace_size(100000, 64, 64, 0)
@@ -80,6 +80,28 @@ def test_argument_errors_of_the_window_sh_ssim_and_camera_entry_points():
     assert L.gs_composite_prep_bwd(None, 10, *([None] * 7)) == 1
     assert b"gs_composite_prep_bwd" in L.gs_last_error()
     assert L.gs_composite_prep_bwd(None, 0, *([None] * 7)) == 0
+
+
+def test_argument_errors_of_the_deferred_binning():
+    """gs_bin_deferred and gs_composite_fwd_deferred check their sizes, the capacity and the
+    binning workspace (the superblock lists are found in it) before launching anything."""
+    L = _lib.lib()
+    fake = ctypes.c_void_p(256)
+    assert L.gs_bin_deferred(None, 10, *([None] * 4), 64, 64, 1000, None, 0, None, None, None) == 1
+    assert b"workspace" in L.gs_last_error()
+    args = (fake, 1000, fake, fake)  # sorted_gids, capacity, ranges, stats
+    rc = L.gs_composite_fwd_deferred(None, 10, fake, fake, 0, fake, fake, fake, 1 << 20, 64, 64, *([fake] * 2),
+                                     *([None] * 5))
+    assert rc == 1 and b"capacity" in L.gs_last_error()
+    need = L.gs_bin_workspace_size(10, 64, 64, 1000)
+    rc = L.gs_composite_fwd_deferred(None, 10, fake, *args[:3], args[3], fake, need - 1, 64, 64, *([fake] * 2),
+                                     *([None] * 5))
+    assert rc == 1 and b"smaller than the binning" in L.gs_last_error()
+    rc = L.gs_composite_fwd_deferred(None, 10, fake, *args[:3], None, fake, need, 64, 64, *([fake] * 2),
+                                     *([None] * 5))
+    assert rc == 1 and b"NULL" in L.gs_last_error()
+    rc = L.gs_composite_fwd_deferred(None, 10, fake, *args, fake, need, 0, 64, *([fake] * 2), *([None] * 5))
+    assert rc == 1 and b"bad sizes" in L.gs_last_error()
 
 
 def test_load_ply_missing_file():
