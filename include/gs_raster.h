@@ -128,15 +128,20 @@ int gs_bin(void* stream, int64_t n, const float* means2d, const float* radii,
            int64_t capacity, void* workspace, size_t workspace_bytes, int32_t* sorted_gids,
            int32_t* sorted_tiles, int32_t* ranges, int32_t* stats);
 
+/* Workspace bytes of gs_bin_deferred (gs_bin's and the count sweep's tile masks, 2 KiB
+ * per chunk of 256 superblock words). */
+size_t gs_bin_deferred_workspace_size(int64_t n, int width, int height, int64_t capacity);
+
 /* gs_bin for the render path, with the entry list deferred to the compositing forward.
- * Same inputs and outputs as gs_bin without sorted_tiles (capacity > 0), except that
- * sorted_gids is written here only when the entries exceed the capacity or the stats set
- * GS_STAT_WINDOW_CLAMPED.  Otherwise gs_composite_fwd_deferred, given this workspace
- * untouched, writes each tile's entries up to those its walk meets, which cover every
- * entry gs_composite_bwd reads (below the tile's largest n_contrib); the rest of the list
- * stays unwritten.  At full size the compositing meets 2-10 % of the entries (tiles turn
- * opaque early), and writing them all was the binning's costliest step.  Same reference
- * interface as gs_bin (rasterizer.py:12-116, renderer.py:57-90). */
+ * Same inputs and outputs as gs_bin without sorted_tiles (capacity > 0; the workspace of
+ * gs_bin_deferred_workspace_size), except that sorted_gids is written here only when the
+ * entries exceed the capacity or the stats set GS_STAT_WINDOW_CLAMPED.  Otherwise
+ * gs_composite_fwd_deferred, given this workspace untouched, writes each tile's entries up
+ * to those its walk meets, which cover every entry gs_composite_bwd reads (below the
+ * tile's largest n_contrib); the rest of the list stays unwritten.  At full size the
+ * compositing meets 2-10 % of the entries (tiles turn opaque early), and writing them all
+ * was the binning's costliest step.  Same reference interface as gs_bin
+ * (rasterizer.py:12-116, renderer.py:57-90). */
 int gs_bin_deferred(void* stream, int64_t n, const float* means2d, const float* radii,
                     const uint8_t* valid, const float* depths, int width, int height,
                     int64_t capacity, void* workspace, size_t workspace_bytes, int32_t* sorted_gids,
@@ -236,8 +241,8 @@ int gs_composite_fwd(void* stream, int64_t n, const float* records, const int32_
 /* gs_composite_fwd after gs_bin_deferred (the same n, width, height and capacity; its
  * workspace, sorted_gids, ranges and stats).  When the binning deferred the entry list,
  * each tile's walk reads its 8x8-tile superblock's list from the workspace (the words
- * whose tile rectangle holds the tile, in the list's order, are the tile's entries) and
- * writes the entries it meets into sorted_gids; otherwise it reads sorted_gids as
+ * whose bit is set in the tile's step masks, in the list's order, are the tile's entries)
+ * and writes the entries it meets into sorted_gids; otherwise it reads sorted_gids as
  * gs_composite_fwd does.  Outputs are those of gs_composite_fwd on gs_bin's full list,
  * bit for bit; gs_composite_bwd then takes sorted_gids as usual.  Replaces the same
  * reference code as gs_composite_fwd (rasterizer.py:157-248). */

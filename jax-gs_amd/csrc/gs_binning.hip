@@ -687,7 +687,8 @@ __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restr
                                                          const uint64_t* __restrict__ pval, int SX,
                                                          const uint32_t* __restrict__ seg_base,
                                                          uint32_t* __restrict__ cnt, uint4* __restrict__ desc,
-                                                         uint32_t* __restrict__ seg_sum) {
+                                                         uint32_t* __restrict__ seg_sum,
+                                                         uint64_t* __restrict__ masks) {
   const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
   const uint32_t C = (uint32_t)min<int64_t>((int64_t)*n_chunks, cmax);
@@ -698,14 +699,21 @@ __global__ __launch_bounds__(256) void tile_count_kernel(const uint32_t* __restr
 #pragma unroll
     for (int k = 0; k < 4; ++k) wv[k] = 64 * k + lane < len ? pval[cs.begin + 64 * k + lane] : 0ull;
     uint32_t mycount = 0;  // lane u counts tile u
+    uint64_t mk[4] = {0ull, 0ull, 0ull, 0ull};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       if (64 * k < len) {
         const bool act = 64 * k + lane < len;
-        mycount += (uint32_t)__popcll(tile_lane_mask(act, unpack(wv[k]), cs.sx, cs.sy, lane));
+        mk[k] = tile_lane_mask(act, unpack(wv[k]), cs.sx, cs.sy, lane);
+        mycount += (uint32_t)__popcll(mk[k]);
       }
     }
     cnt[(int64_t)c * 64 + lane] = mycount;
+    if (masks != nullptr) {  // (chunk, tile) -> its four step masks, 32 bytes per lane
+      ulonglong2* mp = reinterpret_cast<ulonglong2*>(masks + ((int64_t)c * 64 + lane) * 4);
+      mp[0] = make_ulonglong2(mk[0], mk[1]);
+      mp[1] = make_ulonglong2(mk[2], mk[3]);
+    }
     // the chunk's segment (kSeg consecutive chunks of the superblock) and its place in it
     const uint32_t g = seg_base[cs.s] + (c - cs.first) / kSeg, p = (c - cs.first) % kSeg;
     if (mycount != 0u) atomicAdd(&seg_sum[(int64_t)g * 64 + lane], mycount);
@@ -1013,12 +1021,13 @@ struct BinPlan {
   int G_p;        // workgroups of the second pair pass
   int sb_passes;  // 1 when S <= 256, else 2
   size_t o_dkey, o_word, o_ka, o_wa, o_kb, o_wb, o_table, o_dtot, o_scal, o_pk0, o_pv0, o_pk1, o_pv1, o_sbr,
-      o_cbase, o_csb, o_cnt, o_desc, o_tot, o_blk, o_gbase, o_gsum, total;
+      o_cbase, o_csb, o_cnt, o_desc, o_tot, o_blk, o_gbase, o_gsum, o_masks, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-BinPlan make_plan(int64_t n, int width, int height, int64_t capacity) {
+// deferred: room for the count sweep's tile masks (gs_bin_deferred)
+BinPlan make_plan(int64_t n, int width, int height, int64_t capacity, bool deferred = false) {
   BinPlan P;
   P.n = n;
   P.cap = capacity > 0 ? capacity : 256 * (n > 2 ? n : 2);
@@ -1066,6 +1075,7 @@ BinPlan make_plan(int64_t n, int width, int height, int64_t capacity) {
   P.o_blk = take((size_t)P.G_d * kBlkStats * 4);
   P.o_gbase = take(((size_t)P.S + 1) * 4);
   P.o_gsum = take((size_t)P.gmax * 64 * 4);
+  P.o_masks = take(deferred ? (size_t)P.cmax * 64 * (kChunk / 64) * 8 : 0);  // [chunk][tile][step]
   P.total = o;
   return P;
 }
@@ -1099,6 +1109,11 @@ extern "C" size_t gs_bin_workspace_size(int64_t n, int width, int height, int64_
   return make_plan(n, width, height, capacity).total;
 }
 
+extern "C" size_t gs_bin_deferred_workspace_size(int64_t n, int width, int height, int64_t capacity) {
+  if (n < 0 || width <= 0 || height <= 0) return 0;
+  return make_plan(n, width, height, capacity, true).total;
+}
+
 namespace gs {
 namespace {
 int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, const uint8_t* valid,
@@ -1108,7 +1123,7 @@ int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, c
   GS_REQUIRE(n >= 0 && n <= ((int64_t)1 << 26), "gs_bin: n must be in [0, 2^26] (got %lld)", (long long)n);
   GS_REQUIRE(width > 0 && height > 0 && width <= 4096 * kTile && height <= 4096 * kTile,
              "gs_bin: bad image size %dx%d (each side at most 65536)", width, height);
-  const BinPlan P = make_plan(n, width, height, capacity);
+  const BinPlan P = make_plan(n, width, height, capacity, deferred);
   GS_REQUIRE(P.cap < ((int64_t)1 << 31), "gs_bin: capacity %lld too large", (long long)P.cap);
   GS_REQUIRE(P.S <= (1 << (2 * kPairRB)), "gs_bin: %d tiles exceed the supported 65536 superblocks of 8x8 tiles",
              P.T);
@@ -1140,6 +1155,7 @@ int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, c
   uint32_t* blk = (uint32_t*)(ws + P.o_blk);
   uint32_t* gbase = (uint32_t*)(ws + P.o_gbase);
   uint32_t* gsum = (uint32_t*)(ws + P.o_gsum);
+  uint64_t* masks = deferred ? (uint64_t*)(ws + P.o_masks) : nullptr;
   uint32_t* n_pairs = scal + 0;
   uint32_t* n_chunks = scal + 1;
   uint32_t* n_segs = scal + 2;
@@ -1200,7 +1216,7 @@ int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, c
   // the bound and surplus waves exit at once; waves start as others finish
   const int pass_blocks = (int)std::min<int64_t>(div_up(P.cmax, 4), (int64_t)1 << 20);
   hipLaunchKernelGGL(tile_count_kernel, dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, csb, cbase, sbr, P.S,
-                     sbval, P.SX, gbase, cnt, desc, gsum);
+                     sbval, P.SX, gbase, cnt, desc, gsum, masks);
   GS_LAUNCH_CHECK("tile_count_kernel");
   hipLaunchKernelGGL(chunk_scan_kernel, dim3(P.S), dim3(kBig), 0, s, gbase, P.gmax, P.SX, P.TX, P.TY, gsum, tot);
   GS_LAUNCH_CHECK("chunk_scan_kernel");
@@ -1248,13 +1264,16 @@ int superblock_lists(int64_t n, int width, int height, int64_t capacity, const v
   GS_REQUIRE(n >= 0 && n <= ((int64_t)1 << 26) && width > 0 && height > 0 && width <= 4096 * kTile &&
                  height <= 4096 * kTile,
              "superblock lists: bad sizes (n %lld, %dx%d)", (long long)n, width, height);
-  const BinPlan P = make_plan(n, width, height, capacity);
+  const BinPlan P = make_plan(n, width, height, capacity, true);
   GS_REQUIRE(workspace != nullptr && workspace_bytes >= P.total,
              "superblock lists: a workspace of %zu bytes is smaller than the binning's %zu", workspace_bytes,
              P.total);
   const char* ws = (const char*)workspace;
   out->words = (const uint64_t*)(ws + (P.sb_passes == 1 ? P.o_pv0 : P.o_pv1));
   out->ranges = (const int32_t*)(ws + P.o_sbr);
+  out->chunk_base = (const uint32_t*)(ws + P.o_cbase);
+  out->masks = (const uint64_t*)(ws + P.o_masks);
+  out->n_chunks = P.cmax;
   out->n_words = P.pcap;
   out->SX = P.SX;
   out->cap = P.cap;

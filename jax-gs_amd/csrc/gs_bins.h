@@ -41,14 +41,23 @@ __device__ inline Packed unpack(uint64_t v) {
   return p;
 }
 
-// A deferred binning's superblock lists, as the compositing forward reads them.
+// A deferred binning's superblock lists, as the compositing forward reads them.  A
+// superblock's list is cut into chunks of 256 words (4 steps of 64); its chunks are
+// chunk_base[s] .. chunk_base[s+1]-1, chunk c starting at word ranges[s] + 256 (c -
+// chunk_base[s]).  masks[(c * 64 + u) * 4 + k] says which words of step k of chunk c hold
+// tile u of the superblock (u = 8 row + column within it; bit l: word 64 k + l): the
+// binning's count sweep computes them anyway, and the forward reads them in place of the
+// words.
 struct SBLists {
-  const uint64_t* words;  // packed words, grouped by superblock
-  const int32_t* ranges;  // [S+1]: superblock s's words are words[ranges[s] .. ranges[s+1])
-  int64_t n_words;        // length of words
-  int SX;                 // superblocks per row
-  int64_t cap;            // entry capacity of the binning
-  const int32_t* stats;   // the binning's stats
+  const uint64_t* words;        // packed words, grouped by superblock
+  const int32_t* ranges;        // [S+1]: superblock s's words are words[ranges[s] .. ranges[s+1])
+  const uint32_t* chunk_base;   // [S+1]: first chunk of each superblock
+  const uint64_t* masks;        // [n_chunks][64][4] step masks
+  int64_t n_chunks;             // chunks the masks have room for
+  int64_t n_words;              // length of words
+  int SX;                       // superblocks per row
+  int64_t cap;                  // entry capacity of the binning
+  const int32_t* stats;         // the binning's stats
 };
 
 // True when the deferred binning left the entry list unwritten: every entry fits the

@@ -336,13 +336,12 @@ __device__ inline uint64_t probe_test(const Probe& p, float x0, float x1, float 
 // WIN: the default path's chunk windows (see probe_gid); without it the id fetch compiles
 // to the plain one.
 // SB (gs_composite_fwd_deferred): when the binning deferred the entry list
-// (entries_deferred), each wave walks its tile's superblock list instead (gs_bins.h): a
-// batch is 64 words of the list, a word is one of the tile's entries when its rectangle
-// holds the tile, and an entry's index in the tile's list is the number of member words
-// before it.  The wave writes the ids of the entries it meets to gids_out[start + index]
-// (its batches whole, so every entry below the tile's largest n_contrib is written: the
-// part of the list the backward replays) and stops where the walk over the entry list
-// would stop.  Otherwise it walks the entry list as without SB.
+// (entries_deferred), each wave takes its tile's entries from its superblock's list
+// (gs_bins.h): the words whose bit is set in the tile's step masks, in the list's order.
+// It writes the ids of the entries it probes to gids_out[start + k] (whole batches, so every
+// entry below the tile's largest n_contrib -- the part of the list the backward replays --
+// is written) and stops where the walk over the entry list would stop.  Otherwise it walks
+// the entry list as without SB.
 template <int PPT, bool WIN, bool O32, bool SB>
 __global__ __launch_bounds__(64) void composite_fwd_kernel(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
@@ -572,46 +571,81 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
       g_ahead = probe_gid_ahead<WIN>(gids, start, b0 + 128 + lane, n, win, thr);
       walk(m, gk, [&](int j) { return b0 + j; });
     }
-  } else if (n > 0) {
-    // the tile's superblock list, clamped to the word array
-    const int s = (ty / kSB) * sbl.SX + tx / kSB;
-    int64_t j0 = sbl.ranges[s], j1 = sbl.ranges[s + 1];
-    j0 = j0 < 0 ? 0 : (j0 > sbl.n_words ? sbl.n_words : j0);
-    j1 = j1 < j0 ? j0 : (j1 > sbl.n_words ? sbl.n_words : j1);
-    int32_t* __restrict__ out = gids_out + start;  // start + index < start + n <= n_entries
-    // Entries of a batch of words: the lane's id (-1: not an entry), its index in the
-    // tile's list (kl); kb counts the entries of the batches seen so far.  The ids are
-    // stored for the backward.
-    int kb = 0;
-    auto members = [&](uint64_t w, int& kl) -> int {
-      const Packed p = unpack(w);
-      int g = (p.w > 0 && p.gid < (uint32_t)num_g && p.x0 <= tx && tx < p.x0 + p.w && p.y0 <= ty &&
-               ty < p.y0 + p.h)
-                  ? (int)p.gid
-                  : -1;
-      const uint64_t M = __ballot(g >= 0);
-      kl = kb + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(M >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)M, 0u));
-      kb += __popcll(M);
-      if (kl >= n) g = -1;  // the first n entries only (rasterizer.py:180-181)
-      if (g >= 0) out[kl] = g;
-      return g;
-    };
-    // Pipelined as the entry walk: the words two batches ahead and the records (with the
-    // member test) one batch ahead are in flight while a batch is walked.
-    uint64_t w_ahead = j0 + 64 + lane < j1 ? sbl.words[j0 + 64 + lane] : 0ull;
-    int kl = 0;
-    Probe pr = probe_load(rec, members(j0 + lane < j1 ? sbl.words[j0 + lane] : 0ull, kl));
-    int k_end = kb;  // entries up to the end of the batch being walked
-    for (int64_t jb = j0; jb < j1 && !done; jb += 64) {
-      const int gk = rec_key<O32>(pr.g);
-      const int klb = kl;
-      const uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
-      const bool more = k_end < n && jb + 64 < j1;
-      pr = probe_load(rec, more ? members(w_ahead, kl) : -1);
-      w_ahead = more && jb + 128 + lane < j1 ? sbl.words[jb + 128 + lane] : 0ull;
-      walk(m, gk, [&](int j) { return bcast_i(klb, j); });
-      if (!more) break;
-      k_end = kb;
+  } else if constexpr (SB) {
+    if (n > 0) {
+      // The tile's entries, in order, are the words of its superblock's list whose bit is set
+      // in the tile's step masks (the binning's count sweep wrote them).  A ring of 256 word
+      // positions in LDS queues the entries, so that they are probed and walked in full
+      // batches of 64 as above: fill(t) queues entries until t are queued (or the list ends),
+      // one step (64 words, one mask) at a time.  The masks of 16 chunks (64 steps) come with
+      // one vector load (lane l: step l), the next 16 a group ahead.  Entry k's id is written
+      // to gids_out[start + k] when its batch is probed (the backward's list).
+      __shared__ int32_t q_lds[256];
+      volatile int32_t* q = q_lds;  // lanes read what other lanes wrote: keep the order
+      const int sx = tx / kSB, sy = ty / kSB;
+      const int sbi = sy * sbl.SX + sx;
+      const int u = (ty - sy * kSB) * kSB + (tx - sx * kSB);
+      int64_t c0 = sbl.chunk_base[sbi], c1 = sbl.chunk_base[sbi + 1];
+      c0 = c0 > sbl.n_chunks ? sbl.n_chunks : c0;
+      c1 = c1 < c0 ? c0 : (c1 > sbl.n_chunks ? sbl.n_chunks : c1);
+      const int64_t wbase = sbl.ranges[sbi];
+      const int nsteps = 4 * (int)(c1 - c0);
+      auto group = [&](int gi) -> uint64_t {
+        const int64_t c = c0 + 16 * (int64_t)gi + (lane >> 2);
+        return c < c1 ? sbl.masks[(c * 64 + u) * 4 + (lane & 3)] : 0ull;
+      };
+      uint64_t mg = group(0), mg_next = group(1);
+      int sidx = 0, filled = 0;
+      auto fill = [&](int target) {
+        while (filled < target && sidx < nsteps) {
+          if (sidx > 0 && (sidx & 63) == 0) {
+            mg = mg_next;
+            mg_next = group((sidx >> 6) + 1);
+          }
+          const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)mg, sidx & 63);
+          const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(mg >> 32), sidx & 63);
+          const uint64_t m = ((uint64_t)hi << 32) | lo;
+          if (m != 0ull) {
+            if (__builtin_amdgcn_inverse_ballot_w64(m))
+              q[(filled + (int)__builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u))) & 255] =
+                  (int32_t)(wbase + 64 * (int64_t)sidx + lane);
+            filled += __popcll(m);
+          }
+          ++sidx;
+        }
+      };
+      // entry k's word (loaded a batch ahead of its use), none past the queued entries
+      struct WordAhead {
+        uint64_t w;
+        bool ok;
+      };
+      auto word_ahead = [&](int k) {
+        WordAhead a{0ull, k < n && k < filled};
+        if (a.ok) {
+          const int64_t pos = q[k & 255];
+          a.ok = pos >= 0 && pos < sbl.n_words;
+          if (a.ok) a.w = sbl.words[pos];
+        }
+        return a;
+      };
+      // the id where it is used, a batch later; stored for the backward
+      auto take_gid = [&](const WordAhead& a, int k) {
+        if (!a.ok) return -1;
+        const int g = clamp_gid((int)(a.w & 0x3FFFFFFull), num_g);
+        gids_out[start + k] = g;  // k < n: inside the tile's range
+        return g;
+      };
+      fill(128);
+      WordAhead a_ahead = word_ahead(64 + lane);
+      Probe pr = probe_load(rec, take_gid(word_ahead(lane), lane));
+      for (int b0 = 0; b0 < n && !done; b0 += 64) {
+        const int gk = rec_key<O32>(pr.g);
+        const uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
+        pr = probe_load(rec, take_gid(a_ahead, b0 + 64 + lane));
+        fill(b0 + 192);
+        a_ahead = word_ahead(b0 + 128 + lane);
+        walk(m, gk, [&](int j) { return b0 + j; });
+      }
     }
   }
   const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];

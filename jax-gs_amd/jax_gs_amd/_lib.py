@@ -36,6 +36,7 @@ _SIGS = {
                           _P, _P],
     "gs_composite_prep": [_P, _I64, _P, _P, _P, _P, _P],
     "gs_bin_workspace_size": [_I64, _I, _I, _I64],
+    "gs_bin_deferred_workspace_size": [_I64, _I, _I, _I64],
     "gs_bin": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _SZ, _P, _P, _P, _P],
     "gs_bin_deferred": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _SZ, _P, _P, _P],
     "gs_bin_static": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _P, _P, _P],
@@ -79,6 +80,7 @@ _SIGS = {
     "gs_densify_accumulate": [_P, _I64, _P, _P, _P, _F, _F, _P, _P, _P, _P, _P, _P],
 }
 _RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_l1_ssim_workspace_size": _SZ,
+            "gs_bin_deferred_workspace_size": _SZ,
             "gs_bin_reference_workspace_size": _SZ, "gs_preprocess_bwd_w2c_workspace_size": _SZ,
             "gs_l1_ssim_window_workspace_size": _SZ,
             "gs_densify_workspace_size": _SZ}

@@ -77,7 +77,8 @@ def bin_gaussians(means2d: torch.Tensor, radii: torch.Tensor, valid: torch.Tenso
     depths = check_f32("depths", depths, (n,), dev)
     v = valid.to(device=dev, dtype=torch.uint8).contiguous()
     cap = check_capacity(capacity, n)
-    ws_bytes = _lib.lib().gs_bin_workspace_size(n, int(W), int(H), cap)
+    ws_bytes = (_lib.lib().gs_bin_deferred_workspace_size if deferred else _lib.lib().gs_bin_workspace_size)(
+        n, int(W), int(H), cap)
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     _, _, T = num_tiles(W, H)
     gids = torch.empty((cap,), dtype=torch.int32, device=dev)

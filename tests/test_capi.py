@@ -93,7 +93,8 @@ def test_argument_errors_of_the_deferred_binning():
     rc = L.gs_composite_fwd_deferred(None, 10, fake, fake, 0, fake, fake, fake, 1 << 20, 64, 64, *([fake] * 2),
                                      *([None] * 5))
     assert rc == 1 and b"capacity" in L.gs_last_error()
-    need = L.gs_bin_workspace_size(10, 64, 64, 1000)
+    need = L.gs_bin_deferred_workspace_size(10, 64, 64, 1000)
+    assert need > L.gs_bin_workspace_size(10, 64, 64, 1000)
     rc = L.gs_composite_fwd_deferred(None, 10, fake, *args[:3], args[3], fake, need - 1, 64, 64, *([fake] * 2),
                                      *([None] * 5))
     assert rc == 1 and b"smaller than the binning" in L.gs_last_error()
