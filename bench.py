@@ -256,14 +256,28 @@ def main():
     #                   12 each; write means2d 8, radius 4, valid 1, depth 4 (binning's inputs)
     #                   and the compositing record 48 (conic and colour: the renderer writes no
     #                   separate cov2d and colour arrays).
-    #   preprocess bwd: the same inputs + gradient record 48; write 5 gradient arrays
-    #                   (12 + 12 + 16 + 4 + 12 K).
+    #   preprocess bwd: read the gradient record 48; write 5 gradient arrays
+    #                   (12 + 12 + 16 + 4 + 12 K); read the parameters and SH rows (44 + 12
+    #                   (D+1)^2) of the Gaussians the compositing reached (a nonzero gradient
+    #                   record): the others' gradients are zero without them.
     pre_fwd_bytes = N * (44 + 12 * nb) + N * (8 + 4 + 1 + 4 + 48)
-    pre_bwd_bytes = N * (44 + 12 * nb) + N * 48 + N * (12 + 12 + 16 + 4 + 12 * K)
-    #   binning: read means2d 8 + radius 4 + valid 1 + depth 4 per Gaussian; write the entry
-    #            list (4 B per entry) and the tile ranges (4 B per tile).
+    n_reached = int((grec[:, :9] != 0).any(dim=1).sum())
+    pre_bwd_bytes = N * 48 + N * (12 + 12 + 16 + 4 + 12 * K) + n_reached * (44 + 12 * nb)
+    #   binning: read means2d 8 + radius 4 + valid 1 + depth 4 per Gaussian; write the tile
+    #            ranges (4 B per tile), and the entry list (4 B per entry) when the binning
+    #            writes it (the deferred binning leaves it to the compositing forward, which
+    #            writes the entries it meets, unless the window is clamped or the capacity
+    #            exceeded).
     T = b["ranges"].shape[0] - 1
-    bin_bytes = N * 17 + 4 * n_int + 4 * (T + 1)
+    st_np = b["stats"].cpu().numpy()
+    deferred = bool(st_np[_lib.STAT["window_clamped"]] == 0 and
+                    0 <= st_np[_lib.STAT["tile_entries"]] <= b["capacity"])
+    bin_bytes = N * 17 + 4 * (T + 1) + (0 if deferred else 4 * n_int)
+    # entries the compositing meets: per tile the largest n_contrib (what the backward reads)
+    TXn, TYn = (W + 15) // 16, (H + 15) // 16
+    ncp = torch.zeros((TYn * 16, TXn * 16), dtype=torch.int32, device=dev)
+    ncp[:H, :W] = nc
+    entries_met = int(ncp.view(TYn, 16, TXn, 16).amax(dim=(1, 3)).to(torch.int64).sum())
     #   densify stats: read grad_means 12 + means 12 + valid 1 + active 1 + radius 4 + the three
     #                  statistics 12; write the three statistics 12.
     dens_bytes = N * (12 + 12 + 1 + (1 if mask is not None else 0) + 4 + 12 + 12)
@@ -349,7 +363,8 @@ def main():
         "config": {"workload": sc["name"] + {"fwd": " fwd", "fwdbwd": " fwd+L1+bwd",
                                              "fwdbwd_stats": " fwd+L1+bwd+densify stats"}[kind],
                    "gaussians": N, "width": cam.W, "height": cam.H,
-                   "sh_degree": D, "n_interactions": n_int, "gaussians_per_s": N / dt},
+                   "sh_degree": D, "n_interactions": n_int, "gaussians_per_s": N / dt,
+                   "binning_deferred": deferred, "entries_met": entries_met, "gaussians_reached": n_reached},
         "stage_ms": stage_ms,
         "stage_GBps": stage_gbs,
         "stage_TFLOPs": stage_tflops,

@@ -1223,8 +1223,10 @@ int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, c
   hipLaunchKernelGGL(tile_scan_stats_kernel, dim3(1), dim3(kBig), 0, s, tot, P.T, blk, P.G_d, P.cap, n, ranges,
                      stats);
   GS_LAUNCH_CHECK("tile_scan_stats_kernel");
-#define GS_WRITE_LAUNCH(TILES, OFF, DEFER)                                                                     \
-  hipLaunchKernelGGL((tile_write_kernel<TILES, OFF, DEFER>), dim3(pass_blocks), dim3(256), 0, s, n_chunks, P.cmax, \
+  // the deferred sweep usually exits at once: a smaller grid (its loop covers every chunk)
+  const int write_blocks = deferred ? std::min(pass_blocks, 1024) : pass_blocks;
+#define GS_WRITE_LAUNCH(TILES, OFF, DEFER)                                                                      \
+  hipLaunchKernelGGL((tile_write_kernel<TILES, OFF, DEFER>), dim3(write_blocks), dim3(256), 0, s, n_chunks, P.cmax, \
                      desc, sbval, (uint32_t)n, P.TX, P.TY, cnt, gsum, ranges, P.T, P.cap, sorted_gids, sorted_tiles, \
                      stats)
   if (ref_offset)

@@ -343,7 +343,7 @@ __device__ inline uint64_t probe_test(const Probe& p, float x0, float x1, float 
 // is written) and stops where the walk over the entry list would stop.  Otherwise it walks
 // the entry list as without SB.
 template <int PPT, bool WIN, bool O32, bool SB>
-__global__ __launch_bounds__(64) void composite_fwd_kernel(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8))) void composite_fwd_kernel(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
     float* __restrict__ img, float* __restrict__ finalT, int32_t* __restrict__ ncontrib,
@@ -614,24 +614,26 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
           ++sidx;
         }
       };
-      // entry k's word (loaded a batch ahead of its use), none past the queued entries
+      // entry k's word (its low half, which holds the id; loaded a batch ahead of its use),
+      // none past the queued entries
       struct WordAhead {
-        uint64_t w;
+        uint32_t w;
         bool ok;
       };
+      const uint32_t* __restrict__ word_lo = reinterpret_cast<const uint32_t*>(sbl.words);
       auto word_ahead = [&](int k) {
-        WordAhead a{0ull, k < n && k < filled};
+        WordAhead a{0u, k < n && k < filled};
         if (a.ok) {
           const int64_t pos = q[k & 255];
           a.ok = pos >= 0 && pos < sbl.n_words;
-          if (a.ok) a.w = sbl.words[pos];
+          if (a.ok) a.w = word_lo[2 * pos];
         }
         return a;
       };
       // the id where it is used, a batch later; stored for the backward
       auto take_gid = [&](const WordAhead& a, int k) {
         if (!a.ok) return -1;
-        const int g = clamp_gid((int)(a.w & 0x3FFFFFFull), num_g);
+        const int g = clamp_gid((int)(a.w & 0x3FFFFFFu), num_g);
         gids_out[start + k] = g;  // k < n: inside the tile's range
         return g;
       };
