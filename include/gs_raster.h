@@ -93,7 +93,10 @@ int gs_abi_version(void);
  * mask may be NULL (all active).
  * Outputs: means2d[N,2] cov2d[N,2,2] radii[N] valid[N] (0/1) depths[N] colors[N,3]
  * records[N,GS_REC_STRIDE].  records may be NULL; when it is not, cov2d and colors may be
- * NULL (not written: the records carry the conic and colour that compositing reads). */
+ * NULL (not written: the records carry the conic and colour that compositing reads).  With
+ * colors NULL, the SH rows of masked-out Gaussians are not read and their records' colour
+ * is that of zero coefficients (0.5): such a Gaussian is never an entry, so no compositing
+ * reads it. */
 int gs_preprocess_fwd(void* stream, int64_t n, int sh_k, int sh_degree,
                       const float* means, const float* scales, const float* quats,
                       const float* opacities, const float* sh_coeffs, const uint8_t* mask,

@@ -250,8 +250,17 @@ __global__ __launch_bounds__(64) void preprocess_fwd_kernel(
 #pragma unroll
   for (int k = 0; k < 3; ++k) ls[k] = scales[3 * ic + k];
   const float logit = opac[ic];
+  // A masked-out Gaussian is never an entry, so no compositing reads its record's colour:
+  // without a colour output its SH row is not read (the record's colour is then that of
+  // zero coefficients).  Without a mask nothing waits for the mask byte.
+  const bool sh_needed = colors != nullptr || mask == nullptr || mask[ic] != 0;
   float shv[3 * NB];
-  load_row<3 * NB>(sh + ic * (int64_t)(3 * K), (3 * K) % 4 == 0, shv);
+  if (sh_needed) {
+    load_row<3 * NB>(sh + ic * (int64_t)(3 * K), (3 * K) % 4 == 0, shv);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 3 * NB; ++k) shv[k] = 0.0f;
+  }
   if (i >= n) return;
   float w[16];
   load_w2c(w2c, w);

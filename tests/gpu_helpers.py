@@ -64,11 +64,18 @@ def check_preprocess(sc, cuda, pre_o=None):
     for k in ("means2d", "cov2d", "radii", "depths", "colors"):
         np.testing.assert_array_equal(np_(pre[k]), o[k], err_msg=k)
     np.testing.assert_array_equal(np_(pre["valid"]).astype(bool), o["valid"])
-    # the renderer's call writes no cov2d / colour arrays; everything else is identical
+    # the renderer's call writes no cov2d / colour arrays; everything else is identical,
+    # except the colour slots (6-8) of masked-out Gaussians' records: their SH rows are not
+    # read (never an entry)
     lean = preprocess(g, cam, mask=m, sh_degree=sc["sh_degree"], projected=False)
     assert lean["cov2d"] is None and lean["colors"] is None
-    for k in ("means2d", "radii", "valid", "depths", "records"):
+    for k in ("means2d", "radii", "valid", "depths"):
         assert torch.equal(lean[k], pre[k]), k
+    rl, rf = lean["records"].clone(), pre["records"]
+    if m is not None:
+        off = ~m.to(torch.bool)
+        rl[off, 6:9] = rf[off, 6:9]
+    assert torch.equal(rl, rf)
     return pre, o
 
 
