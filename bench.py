@@ -266,11 +266,11 @@ def main():
     #   binning: read means2d 8 + radius 4 + valid 1 + depth 4 per Gaussian; write the tile
     #            ranges (4 B per tile), and the entry list (4 B per entry) when the binning
     #            writes it (the deferred binning leaves it to the compositing forward, which
-    #            writes the entries it meets, unless the window is clamped or the capacity
-    #            exceeded).
+    #            writes the entries it meets, unless the window is clamped, the capacity
+    #            exceeded or the image under 2048 tiles).
     T = b["ranges"].shape[0] - 1
     st_np = b["stats"].cpu().numpy()
-    deferred = bool(st_np[_lib.STAT["window_clamped"]] == 0 and
+    deferred = bool(st_np[_lib.STAT["window_clamped"]] == 0 and T >= 2048 and
                     0 <= st_np[_lib.STAT["tile_entries"]] <= b["capacity"])
     bin_bytes = N * 17 + 4 * (T + 1) + (0 if deferred else 4 * n_int)
     # entries the compositing meets: per tile the largest n_contrib (what the backward reads)

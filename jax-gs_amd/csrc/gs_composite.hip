@@ -343,7 +343,7 @@ __device__ inline uint64_t probe_test(const Probe& p, float x0, float x1, float 
 // is written) and stops where the walk over the entry list would stop.  Otherwise it walks
 // the entry list as without SB.
 template <int PPT, bool WIN, bool O32, bool SB>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8))) void composite_fwd_kernel(
+__global__ __launch_bounds__(64) void composite_fwd_kernel(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
     float* __restrict__ img, float* __restrict__ finalT, int32_t* __restrict__ ncontrib,
@@ -574,13 +574,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8))) void co
   } else if constexpr (SB) {
     if (n > 0) {
       // The tile's entries, in order, are the words of its superblock's list whose bit is set
-      // in the tile's step masks (the binning's count sweep wrote them).  A ring of 256 word
+      // in the tile's step masks (the binning's count sweep wrote them).  A ring of 512 word
       // positions in LDS queues the entries, so that they are probed and walked in full
       // batches of 64 as above: fill(t) queues entries until t are queued (or the list ends),
-      // one step (64 words, one mask) at a time.  The masks of 16 chunks (64 steps) come with
+      // one chunk (four steps of 64 words, one mask each) at a time.  The masks of 16 chunks (64 steps) come with
       // one vector load (lane l: step l), the next 16 a group ahead.  Entry k's id is written
       // to gids_out[start + k] when its batch is probed (the backward's list).
-      __shared__ int32_t q_lds[256];
+      constexpr int kRing = 512;  // live entries span < 64 + 256 (a fill overshoots by < 4 steps)
+      __shared__ int32_t q_lds[kRing];
       volatile int32_t* q = q_lds;  // lanes read what other lanes wrote: keep the order
       const int sx = tx / kSB, sy = ty / kSB;
       const int sbi = sy * sbl.SX + sx;
@@ -596,22 +597,30 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8))) void co
       };
       uint64_t mg = group(0), mg_next = group(1);
       int sidx = 0, filled = 0;
+      // a chunk (four steps) per round: its eight mask halves are read together
       auto fill = [&](int target) {
         while (filled < target && sidx < nsteps) {
           if (sidx > 0 && (sidx & 63) == 0) {
             mg = mg_next;
             mg_next = group((sidx >> 6) + 1);
           }
-          const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)mg, sidx & 63);
-          const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(mg >> 32), sidx & 63);
-          const uint64_t m = ((uint64_t)hi << 32) | lo;
-          if (m != 0ull) {
-            if (__builtin_amdgcn_inverse_ballot_w64(m))
-              q[(filled + (int)__builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u))) & 255] =
-                  (int32_t)(wbase + 64 * (int64_t)sidx + lane);
-            filled += __popcll(m);
+          uint32_t lo[4], hi[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            lo[k] = __builtin_amdgcn_readlane((uint32_t)mg, (sidx & 63) + k);
+            hi[k] = __builtin_amdgcn_readlane((uint32_t)(mg >> 32), (sidx & 63) + k);
           }
-          ++sidx;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint64_t m = ((uint64_t)hi[k] << 32) | lo[k];
+            if (m != 0ull) {
+              if (__builtin_amdgcn_inverse_ballot_w64(m))
+                q[(filled + (int)__builtin_amdgcn_mbcnt_hi(hi[k], __builtin_amdgcn_mbcnt_lo(lo[k], 0u))) &
+                  (kRing - 1)] = (int32_t)(wbase + 64 * (int64_t)(sidx + k) + lane);
+              filled += __popcll(m);
+            }
+          }
+          sidx += 4;
         }
       };
       // entry k's word (its low half, which holds the id; loaded a batch ahead of its use),
@@ -624,7 +633,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8))) void co
       auto word_ahead = [&](int k) {
         WordAhead a{0u, k < n && k < filled};
         if (a.ok) {
-          const int64_t pos = q[k & 255];
+          const int64_t pos = q[k & (kRing - 1)];
           a.ok = pos >= 0 && pos < sbl.n_words;
           if (a.ok) a.w = word_lo[2 * pos];
         }

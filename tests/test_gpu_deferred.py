@@ -49,6 +49,8 @@ def _prefix_positions(ranges, kmax):
 def _compare(sc, cuda, window, capacity=None, expect_deferred=True):
     c = sc["cam"]
     W, H = c["W"], c["H"]
+    # images under 2048 tiles (four waves per tile) get the whole list from the binning
+    expect_deferred = expect_deferred and ((W + 15) // 16) * ((H + 15) // 16) >= 2048
     g, cam, _, m = scenes.to_torch(sc, cuda)
     n = g.means.shape[0]
     bg = torch.tensor([0.1, 0.3, 0.2], device=cuda)
@@ -61,7 +63,8 @@ def _compare(sc, cuda, window, capacity=None, expect_deferred=True):
         defer = rasterizer.bin_gaussians(*args, capacity=capacity, want_tiles=False, window=window, deferred=True)
         stats = np_(defer["stats"])
         m_ent = int(stats[_lib.STAT["tile_entries"]])
-        deferred = bool(stats[_lib.STAT["window_clamped"]] == 0 and 0 <= m_ent <= defer["capacity"])
+        deferred = bool(stats[_lib.STAT["window_clamped"]] == 0 and 0 <= m_ent <= defer["capacity"] and
+                        defer["num_tiles"] >= 2048)
         assert deferred == expect_deferred
         if deferred:
             # the binning wrote no entry: every entry the forward and backward read must be
@@ -118,7 +121,8 @@ def _compare(sc, cuda, window, capacity=None, expect_deferred=True):
 @pytest.mark.parametrize("window", [True, False])
 @pytest.mark.parametrize("cfg,n,w,h", [(1, 20000, 256, 192), (2, 60000, 1024, 768), (2, 100000, 1920, 832)])
 def test_deferred_equals_full_per_build(cuda, window, cfg, n, w, h):
-    """Four (T < 2048), two (2048 <= T < 6144) and one (T >= 6144) forward waves per tile."""
+    """Four (T < 2048: the binning writes the whole list), two (2048 <= T < 6144) and one
+    (T >= 6144) forward waves per tile."""
     sc = scenes.make_scene(cfg, n=n, width=w, height=h)
     sc["name"] = f"cfg{cfg}-family"
     _compare(sc, cuda, window)
@@ -135,7 +139,7 @@ def test_deferred_equals_full_at_full_size(cuda, cfg):
 
 
 def test_deferred_with_gaussians_behind_the_camera_and_masked(cuda):
-    sc = scenes.make_scene(1, n=30000, width=640, height=480, seed=9)
+    sc = scenes.make_scene(1, n=60000, width=1024, height=768, seed=9)
     p = sc["params"]
     p["means"][:50, 2] = -np.abs(p["means"][:50, 2])
     mask = np.ones(p["means"].shape[0], bool)
@@ -148,11 +152,11 @@ def test_deferred_with_gaussians_behind_the_camera_and_masked(cuda):
 def test_deferred_falls_back_beyond_the_capacity(cuda):
     """A capacity below the entry count: the binning writes the first entries in full and
     the forward reads them (both binnings keep the same entries)."""
-    sc = scenes.make_scene(1, n=20000, width=256, height=192)
+    sc = scenes.make_scene(1, n=40000, width=1024, height=768)
     g, cam, _, m = scenes.to_torch(sc, cuda)
     with torch.no_grad():
         pre = preprocess(g, cam, mask=m, sh_degree=sc["sh_degree"], projected=False)
-        b = rasterizer.bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], 192, 256,
+        b = rasterizer.bin_gaussians(pre["means2d"], pre["radii"], pre["valid"], pre["depths"], 768, 1024,
                                      want_tiles=False)
     m_ent = int(np_(b["stats"])[_lib.STAT["tile_entries"]])
     sc["name"] = "capacity"
@@ -160,10 +164,17 @@ def test_deferred_falls_back_beyond_the_capacity(cuda):
 
 
 def test_deferred_falls_back_for_clamped_windows(cuda):
-    """The default path's clamped chunk window reads the entry list: written in full."""
-    from test_gpu_windows import CASES
+    """The default path's clamped chunk window reads the entry list: written in full.  Small
+    images (the window tests' scenes) and 300 Gaussians spanning 16 x 16 tiles of a 1024 x 768
+    image (3072 tiles: no empty slot, so the last tiles' chunks are clamped)."""
+    from test_gpu_windows import CASES, _scene
 
-    for name in ("two", "big"):
-        sc = CASES[name]()
+    rng = np.random.default_rng(5)
+    m = np.zeros((300, 3), F32)
+    m[:, :2] = rng.uniform(-0.05, 0.05, (300, 2))
+    m[:, 2] = rng.uniform(4.8, 5.2, 300)
+    wide = _scene(m, np.zeros(300), rng.uniform(-4.5, -3.5, 300), rng.uniform(0.0, 1.0, (300, 3)), 1024, 768,
+                  400.0)
+    for name, sc in (("two", CASES["two"]()), ("big", CASES["big"]()), ("wide", wide)):
         sc["name"] = f"window-{name}"
         _compare(sc, cuda, window=True, expect_deferred=False)
