@@ -724,7 +724,7 @@ __device__ inline void zero_grads(int64_t i, int KC, bool aligned, float* __rest
 // or occluded -- in a dense scene most are: 96 % of configuration 2's million, 77 % of
 // configuration 1's) has an all-zero gradient record, and its VJP is then exactly zero
 // (every term is a product with a record value; the parameters only need to be finite).
-// A workgroup takes kBwdSpan consecutive Gaussians: its threads read the span's records,
+// A workgroup takes SPAN consecutive Gaussians: its threads read the span's records,
 // write zero rows for the unreached Gaussians without reading their parameters or SH rows,
 // and list the reached ones in LDS; the list is then processed one Gaussian per thread, so
 // the arithmetic runs in full waves of reached Gaussians (with one thread per Gaussian
@@ -734,10 +734,9 @@ __device__ inline void zero_grads(int64_t i, int KC, bool aligned, float* __rest
 // W2C: each workgroup also writes its reached Gaussians' summed shares of dL/dW2C (15
 // floats: through the mean and W_rot, then the view vector's cotangent) to
 // w2c_part[16 * block].
-constexpr int kBwdSpan = 1024;
 constexpr int kBwdThreads = 256;
 
-template <int DEG, bool W2C>
+template <int DEG, bool W2C, int SPAN>
 __global__ __launch_bounds__(kBwdThreads) void preprocess_bwd_kernel(
     int64_t n, int K, const float* __restrict__ means, const float* __restrict__ scales,
     const float* __restrict__ quats, const float* __restrict__ opac, const float* __restrict__ sh,
@@ -745,14 +744,14 @@ __global__ __launch_bounds__(kBwdThreads) void preprocess_bwd_kernel(
     float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_quats,
     float* __restrict__ g_opac, float* __restrict__ g_sh, float* __restrict__ w2c_part) {
   constexpr int NB = (DEG + 1) * (DEG + 1);
-  constexpr int PER = kBwdSpan / kBwdThreads;
+  constexpr int PER = SPAN / kBwdThreads;
   constexpr int NW = kBwdThreads / 64;
-  __shared__ uint16_t reached_s[kBwdSpan];
+  __shared__ uint16_t reached_s[SPAN];
   __shared__ uint32_t wsum[NW];
   __shared__ float psum[NW][16];
   const int KC = 3 * K;
   const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
-  const int64_t g0 = (int64_t)blockIdx.x * kBwdSpan;
+  const int64_t g0 = (int64_t)blockIdx.x * SPAN;
   const bool aligned = (KC & 3) == 0 && (reinterpret_cast<uintptr_t>(sh) & 15) == 0 &&
                        (reinterpret_cast<uintptr_t>(g_sh) & 15) == 0;
   const bool grec16 = (reinterpret_cast<uintptr_t>(grec) & 15) == 0;
@@ -1138,6 +1137,11 @@ extern "C" int gs_composite_prep(void* stream, int64_t n, const float* means2d, 
 
 namespace gs {
 namespace {
+// Gaussians per workgroup of preprocess_bwd_kernel: 1024 fills the GPU from about half a
+// million Gaussians up (1M: 85 us against 90 with 256, 2M: 174 against 180); below, 256
+// (200k: 26.5 us against 31).
+inline int bwd_span(int64_t n) { return n < ((int64_t)1 << 19) ? 256 : 1024; }
+
 int preprocess_bwd_launch(void* stream, int64_t n, int sh_k, int sh_degree, const float* means,
                           const float* scales, const float* quats, const float* opacities, const float* sh_coeffs,
                           const float* w2c, float fx, float fy, const float* grad_records, float* grad_means,
@@ -1153,18 +1157,20 @@ int preprocess_bwd_launch(void* stream, int64_t n, int sh_k, int sh_degree, cons
                  grad_scales && grad_quats && grad_opacities && grad_sh,
              "%s: NULL array argument", who);
   const bool part = w2c_part != nullptr;
-#define GS_PRE_BWD(D)                                                                                            \
+  const int span = bwd_span(n);
+#define GS_PRE_BWD2(D, SP)                                                                                       \
   do {                                                                                                           \
     if (part)                                                                                                    \
-      hipLaunchKernelGGL((preprocess_bwd_kernel<D, true>), dim3(div_up(n, kBwdSpan)), dim3(kBwdThreads), 0,          \
-                         (hipStream_t)stream,                                                                  \
-                         n, sh_k, means, scales, quats, opacities, sh_coeffs, w2c, fx, fy, grad_records,           \
-                         grad_means, grad_scales, grad_quats, grad_opacities, grad_sh, w2c_part);                 \
+      hipLaunchKernelGGL((preprocess_bwd_kernel<D, true, SP>), dim3(div_up(n, SP)), dim3(kBwdThreads), 0,        \
+                         (hipStream_t)stream, n, sh_k, means, scales, quats, opacities, sh_coeffs, w2c, fx, fy,   \
+                         grad_records, grad_means, grad_scales, grad_quats, grad_opacities, grad_sh, w2c_part);  \
     else                                                                                                         \
-      hipLaunchKernelGGL((preprocess_bwd_kernel<D, false>), dim3(div_up(n, kBwdSpan)), dim3(kBwdThreads), 0,      \
+      hipLaunchKernelGGL((preprocess_bwd_kernel<D, false, SP>), dim3(div_up(n, SP)), dim3(kBwdThreads), 0,       \
                          (hipStream_t)stream, n, sh_k, means, scales, quats, opacities, sh_coeffs, w2c, fx, fy,   \
                          grad_records, grad_means, grad_scales, grad_quats, grad_opacities, grad_sh, nullptr);   \
   } while (0)
+#define GS_PRE_BWD(D) \
+  if (span == 1024) GS_PRE_BWD2(D, 1024); else GS_PRE_BWD2(D, 256)
   switch (sh_degree) {
     case 0: GS_PRE_BWD(0); break;
     case 1: GS_PRE_BWD(1); break;
@@ -1172,6 +1178,7 @@ int preprocess_bwd_launch(void* stream, int64_t n, int sh_k, int sh_degree, cons
     default: GS_PRE_BWD(3); break;
   }
 #undef GS_PRE_BWD
+#undef GS_PRE_BWD2
   GS_LAUNCH_CHECK("preprocess_bwd_kernel");
   return GS_OK;
 }
@@ -1216,7 +1223,7 @@ extern "C" int gs_preprocess_bwd_w2c(void* stream, int64_t n, int sh_k, int sh_d
                                        grad_sh, (float*)workspace, "gs_preprocess_bwd_w2c");
   if (rc != GS_OK) return rc;
   hipLaunchKernelGGL(w2c_finish_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, (const float*)workspace,
-                     n > 0 ? div_up(n, kBwdSpan) : (int64_t)0, w2c, grad_w2c);
+                     n > 0 ? div_up(n, bwd_span(n)) : (int64_t)0, w2c, grad_w2c);
   GS_LAUNCH_CHECK("w2c_finish_kernel");
   return GS_OK;
 }
