@@ -134,9 +134,9 @@ def test_cfg2_full_frame(cuda):
 def test_cfg2_full_frame_oblique_camera(cuda):
     """Configuration 2 at full size under a rotated, translated camera whose W2C requires
     grad: the whole-frame image, the five cotangents and dL/dW2C against the oracle's VJP.
-    The camera cotangent is the sum of 1M per-Gaussian shares, reduced in 15,625 wave
-    partials and one finishing workgroup (gs_preprocess_bwd_w2c), where float32
-    cancellation in the twelve sums is the risk."""
+    The camera cotangent is the sum of 1M per-Gaussian shares, reduced in one partial per
+    workgroup of the preprocessing VJP (977 of 1024 Gaussians) and one finishing workgroup
+    (gs_preprocess_bwd_w2c), where float32 cancellation in the twelve sums is the risk."""
     sc = scenes.make_scene(2)
     ax = np.array([0.3, -0.5, 0.8])
     ax /= np.linalg.norm(ax)
