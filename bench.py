@@ -397,8 +397,10 @@ def measured_traffic(kernel, config):
 def measured_valu_busy(stage, config):
     """VALU-busy fraction of the stage's kernel from the committed SQ-counter summary of the
     same configuration, and that file; (None, None) when there is none."""
+    # the builds of the bench's launches (the forward's first template argument is the pixels
+    # per lane, which the image size picks): matched by prefix
     kernels = {"composite_bwd": "composite_bwd_wide_kernel<true, true>",
-               "composite_fwd": "composite_fwd_kernel<4, true, true>"}
+               "composite_fwd": "composite_fwd_kernel<"}
     path = os.path.join(PROFILES, f"composite_valu_cfg{config}.md")
     if stage not in kernels or not os.path.exists(path):
         return None, None
@@ -407,7 +409,7 @@ def measured_valu_busy(stage, config):
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
         if col is None and "VALU busy %" in cells:
             col = cells.index("VALU busy %")
-        elif col is not None and cells and cells[0] == kernels[stage]:
+        elif col is not None and cells and cells[0].startswith(kernels[stage]):
             try:
                 return float(cells[col]) / 100.0, os.path.relpath(path, _ROOT)
             except (ValueError, IndexError):
