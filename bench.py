@@ -270,8 +270,7 @@ def main():
     #            exceeded or the image under 2048 tiles).
     T = b["ranges"].shape[0] - 1
     st_np = b["stats"].cpu().numpy()
-    deferred = bool(st_np[_lib.STAT["window_clamped"]] == 0 and T >= 2048 and
-                    0 <= st_np[_lib.STAT["tile_entries"]] <= b["capacity"])
+    deferred = bool(st_np[_lib.STAT["entries_deferred"]])
     bin_bytes = N * 17 + 4 * (T + 1) + (0 if deferred else 4 * n_int)
     # entries the compositing meets: per tile the largest n_contrib (what the backward reads)
     TXn, TYn = (W + 15) // 16, (H + 15) // 16

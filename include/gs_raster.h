@@ -70,6 +70,8 @@ extern "C" {
 #define GS_STAT_WINDOW_CLAMPED 11   /* 1 when a tile's 512-entry chunk starts within 512 slots of the
                                        end of the reference's max(256 n, 512)-slot arrays, i.e. when
                                        its default path (rasterizer.py:184-190) reads other entries */
+#define GS_STAT_ENTRIES_DEFERRED 12 /* 1 when gs_bin_deferred left the entry list to
+                                       gs_composite_fwd_deferred (0 from every other binning) */
 #define GS_NUM_STATS 16
 
 const char* gs_last_error(void);

@@ -731,7 +731,7 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
                                                                const uint32_t* __restrict__ blkstat, int nblk,
                                                                int64_t cap, int64_t n_gauss,
                                                                int32_t* __restrict__ ranges,
-                                                               int32_t* __restrict__ stats) {
+                                                               int32_t* __restrict__ stats, bool deferred) {
   constexpr int kPer = 8, kRound = kBig * kPer;
   __shared__ uint32_t stage[kBig * (kPer + 1)];
   __shared__ int64_t red[9][kBig / 64];
@@ -843,7 +843,9 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
     // the reference's arrays hold max(256 n, 512) slots with 256 per negative-depth
     // Gaussian in front of the entries: a chunk starting past L - 512 there is clamped
     const int64_t L = 256 * n_gauss > kBlock ? 256 * n_gauss : kBlock;
-    stats[GS_STAT_WINDOW_CLAMPED] = (r[8] >= 0 && 256 * r[6] + r[8] > L - kBlock) ? 1 : 0;
+    const bool clamped = r[8] >= 0 && 256 * r[6] + r[8] > L - kBlock;
+    stats[GS_STAT_WINDOW_CLAMPED] = clamped ? 1 : 0;
+    stats[GS_STAT_ENTRIES_DEFERRED] = deferred && defer_entries(T, m, cap, clamped) ? 1 : 0;
     // renderer.py:81: float32(n_interactions) / num_tiles
     stats[GS_STAT_MEAN_PER_TILE] = (int32_t)float_to_bits((float)(int32_t)n_int / (float)T);
   }
@@ -980,7 +982,7 @@ __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restr
                                                          int32_t* __restrict__ out_gid,
                                                          int32_t* __restrict__ out_tile,
                                                          const int32_t* __restrict__ stats) {
-  if (DEFER && entries_deferred(ranges, T, cap, stats)) return;
+  if (DEFER && entries_deferred(stats)) return;
   const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
   const uint32_t C = (uint32_t)min<int64_t>((int64_t)*n_chunks, cmax);
@@ -1221,7 +1223,7 @@ int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, c
   hipLaunchKernelGGL(chunk_scan_kernel, dim3(P.S), dim3(kBig), 0, s, gbase, P.gmax, P.SX, P.TX, P.TY, gsum, tot);
   GS_LAUNCH_CHECK("chunk_scan_kernel");
   hipLaunchKernelGGL(tile_scan_stats_kernel, dim3(1), dim3(kBig), 0, s, tot, P.T, blk, P.G_d, P.cap, n, ranges,
-                     stats);
+                     stats, deferred);
   GS_LAUNCH_CHECK("tile_scan_stats_kernel");
   // the deferred sweep usually exits at once: a smaller grid (its loop covers every chunk)
   const int write_blocks = deferred ? std::min(pass_blocks, 1024) : pass_blocks;
@@ -1278,7 +1280,6 @@ int superblock_lists(int64_t n, int width, int height, int64_t capacity, const v
   out->n_chunks = P.cmax;
   out->n_words = P.pcap;
   out->SX = P.SX;
-  out->cap = P.cap;
   out->stats = stats;
   return GS_OK;
 }

@@ -56,7 +56,6 @@ struct SBLists {
   int64_t n_chunks;             // chunks the masks have room for
   int64_t n_words;              // length of words
   int SX;                       // superblocks per row
-  int64_t cap;                  // entry capacity of the binning
   const int32_t* stats;         // the binning's stats
 };
 
@@ -66,14 +65,16 @@ struct SBLists {
 // costs more than the write sweep saves (cfg1: 124 -> 194 us against 93 -> 80 us).
 constexpr int kDeferMinTiles = 2048;
 
-// True when the deferred binning left the entry list unwritten: the image has at least
-// kDeferMinTiles tiles, every entry fits the capacity and no chunk of the default path
-// reads the clamped window.  The binning's write sweep and the compositing forward decide
-// by this same test.
-__device__ inline bool entries_deferred(const int32_t* __restrict__ tile_ranges, int T, int64_t cap,
-                                        const int32_t* __restrict__ stats) {
-  const int32_t total = tile_ranges[T];
-  return T >= kDeferMinTiles && total >= 0 && (int64_t)total <= cap && stats[GS_STAT_WINDOW_CLAMPED] == 0;
+// Whether a deferred binning leaves the entry list unwritten: the image has at least
+// kDeferMinTiles tiles, every entry fits the capacity and no chunk of the default path reads
+// the clamped window.  The tile scan decides and records it in the stats
+// (GS_STAT_ENTRIES_DEFERRED, 0 from every other binning); the write sweep and the compositing
+// forward read the flag.
+__host__ __device__ inline bool defer_entries(int T, int64_t entries, int64_t cap, bool clamped) {
+  return T >= kDeferMinTiles && entries >= 0 && entries <= cap && !clamped;
+}
+__device__ inline bool entries_deferred(const int32_t* __restrict__ stats) {
+  return stats[GS_STAT_ENTRIES_DEFERRED] != 0;
 }
 
 // The superblock lists inside a gs_bin_deferred workspace (the same n, image size and

@@ -555,7 +555,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
   };
 
   bool deferred = false;
-  if constexpr (SB) deferred = entries_deferred(ranges, T, sbl.cap, sbl.stats);
+  if constexpr (SB) deferred = entries_deferred(sbl.stats);
   if (!deferred) {
     const int64_t thr = WIN ? win->thr : 0;
     // The batch's probe records were requested a batch ago; the next batch's go out after

@@ -20,7 +20,7 @@ GS_NUM_STATS = 16
 GS_WINDOW_BYTES = 16 + 4 * 512  # sizeof(gs_window_t): int64 thr, 2 reserved int32, 512 ids
 STAT = dict(n_interactions=0, max_interactions_per_tile=1, overflow_tiles=2, overflow_interactions=3,
             truncated_tiles=4, truncated_interactions=5, radius_cap_violations=6, negative_depth=7,
-            capacity_exceeded=8, mean_per_tile=9, tile_entries=10, window_clamped=11)
+            capacity_exceeded=8, mean_per_tile=9, tile_entries=10, window_clamped=11, entries_deferred=12)
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
