@@ -701,32 +701,28 @@ __device__ inline void preprocess_bwd_gauss(int64_t i, int K, const GaussIn& in,
 }
 
 // Zero cotangents of Gaussian i's five arrays (KC = 3 K floats of SH).
-__device__ inline void zero_grads(int64_t i, int KC, bool aligned, float* __restrict__ g_means,
-                                  float* __restrict__ g_scales, float* __restrict__ g_quats,
-                                  float* __restrict__ g_opac, float* __restrict__ g_sh) {
-#pragma unroll
-  for (int k = 0; k < 3; ++k) {
-    g_means[3 * i + k] = 0.0f;
-    g_scales[3 * i + k] = 0.0f;
-  }
-#pragma unroll
-  for (int k = 0; k < 4; ++k) g_quats[4 * i + k] = 0.0f;
-  g_opac[i] = 0.0f;
-  float* __restrict__ dst = g_sh + i * KC;
-  if (aligned) {
-    for (int t = 0; t < KC / 4; ++t) reinterpret_cast<float4*>(dst)[t] = make_float4(0.f, 0.f, 0.f, 0.f);
-  } else {
-    for (int t = 0; t < KC; ++t) dst[t] = 0.0f;
-  }
+// Zeros floats [begin, end) of p with the block's threads (NT of them), consecutive threads on
+// consecutive 16-byte words: scalar stores up to the first 16-byte boundary and after the last.
+template <int NT>
+__device__ inline void zero_block(float* __restrict__ p, int64_t begin, int64_t end, int t) {
+  if (begin >= end) return;
+  int64_t a = begin;
+  while (a < end && ((reinterpret_cast<uintptr_t>(p + a) & 15) != 0)) ++a;  // <= 3 floats
+  const int64_t nv = (end - a) / 4;
+  if (t < a - begin) p[begin + t] = 0.0f;
+  float4* __restrict__ v = reinterpret_cast<float4*>(p + a);
+  for (int64_t j = t; j < nv; j += NT) v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int64_t tail = a + 4 * nv;
+  if (t < end - tail) p[tail + t] = 0.0f;
 }
 
 // The preprocessing VJP.  A Gaussian that no pixel's cotangent reached (off-screen, masked,
 // or occluded -- in a dense scene most are: 96 % of configuration 2's million, 77 % of
 // configuration 1's) has an all-zero gradient record, and its VJP is then exactly zero
 // (every term is a product with a record value; the parameters only need to be finite).
-// A workgroup takes SPAN consecutive Gaussians: its threads read the span's records,
-// write zero rows for the unreached Gaussians without reading their parameters or SH rows,
-// and list the reached ones in LDS; the list is then processed one Gaussian per thread, so
+// A workgroup takes SPAN consecutive Gaussians: its threads read the span's records, zero the
+// span's gradient rows (coalesced; no parameter or SH row is read for it) and list the reached
+// Gaussians in LDS; the list is then processed one Gaussian per thread, so
 // the arithmetic runs in full waves of reached Gaussians (with one thread per Gaussian
 // every wave holding a reached one would run it whole).  A reached Gaussian's SH row and
 // gradient record are loaded straight into registers and its SH cotangent row stored from
@@ -786,14 +782,20 @@ __global__ __launch_bounds__(kBwdThreads) void preprocess_bwd_kernel(
     total += wsum[w];
   }
 #pragma unroll
-  for (int r = 0; r < PER; ++r) {
-    const int64_t i = g0 + t + kBwdThreads * r;
-    if (hit[r]) {
-      reached_s[at++] = (uint16_t)(t + kBwdThreads * r);
-    } else if (i < n) {
-      zero_grads(i, KC, aligned, g_means, g_scales, g_quats, g_opac, g_sh);
-    }
+  for (int r = 0; r < PER; ++r)
+    if (hit[r]) reached_s[at++] = (uint16_t)(t + kBwdThreads * r);
+  // the span's gradient rows are zeroed whole, with coalesced 16-byte stores (a row per thread
+  // took one partial cache line per lane and store); the reached rows are overwritten below,
+  // after every zero store has completed
+  {
+    const int64_t g1 = g0 + SPAN < n ? g0 + SPAN : n;
+    zero_block<kBwdThreads>(g_means, 3 * g0, 3 * g1, t);
+    zero_block<kBwdThreads>(g_scales, 3 * g0, 3 * g1, t);
+    zero_block<kBwdThreads>(g_quats, 4 * g0, 4 * g1, t);
+    zero_block<kBwdThreads>(g_opac, g0, g1, t);
+    zero_block<kBwdThreads>(g_sh, (int64_t)KC * g0, (int64_t)KC * g1, t);
   }
+  __builtin_amdgcn_s_waitcnt(0);  // the zero stores performed before any wave writes a row
   __syncthreads();
   // 3. the reached Gaussians, one per thread
   float part[15];
