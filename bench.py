@@ -61,7 +61,7 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only (the multi-GPU path is design-only); "
                                    "run with --gpus 1"}))
         sys.exit(2)
-    from jax_gs_amd import _lib, render, scenes
+    from jax_gs_amd import _lib, render, render_l1, scenes
     from jax_gs_amd.renderer import rasterizer
     from jax_gs_amd.renderer.projection import preprocess
     from jax_gs_amd.training.losses import l1_loss
@@ -83,29 +83,33 @@ def main():
     stats_state = {"grad_accum": torch.zeros(N, device=dev), "denom": torch.zeros(N, dtype=torch.int32, device=dev),
                    "max_radii": torch.zeros(N, device=dev)}
 
-    def step():
+    def step(fused=True):
         if kind == "fwd":
             with torch.no_grad():
                 _, extras = render(g, cam, mask=mask, sh_degree=D)
             return extras
         for f in fields:
             getattr(g, f).grad = None
-        image, extras = render(g, cam, mask=mask, sh_degree=D)
-        loss = l1_loss(image, tgt)
+        if fused:
+            # render + L1 loss with the loss fused into the compositing launches
+            _, loss, extras = render_l1(g, cam, tgt, mask=mask, sh_degree=D)
+        else:
+            image, extras = render(g, cam, mask=mask, sh_degree=D)
+            loss = l1_loss(image, tgt)
         loss.backward()
         if kind == "fwdbwd_stats":
             accumulate_from_extras(stats_state, g.means.grad, g.means.detach(), cam, extras, active=mask)
         return extras
 
-    for _ in range(args.warmup):
-        extras = step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        extras = step()
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / args.steps
-    n_int = int(extras["n_interactions"])
+    def timed(fused):
+        for _ in range(args.warmup):
+            step(fused)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            ex = step(fused)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / args.steps, ex
 
     # ---- per-stage timing with HIP events on the launch stream (torch's current stream)
     st = torch.cuda.current_stream(dev)
@@ -119,8 +123,12 @@ def main():
 
     reps = max(3, args.steps)
     bg = torch.zeros(3, device=dev)
+    one = torch.ones((), device=dev)  # dL/dloss
     W, H = cam.W, cam.H
-    with torch.no_grad():
+
+    def stage_loop():
+        """One step's stages, `reps` times, an event between stages; returns the last
+        repetition's tensors."""
         for _ in range(reps):
             mark("t0")
             pre = preprocess(g, cam, mask=mask, sh_degree=D, projected=False)
@@ -129,26 +137,42 @@ def main():
                                          want_tiles=False, window=True, deferred=True)
             mark("t2")
             grec = torch.empty((N, _lib.GS_REC_STRIDE), device=dev)  # cleared by the forward launch
-            image, fT, nc, order = rasterizer.composite(pre["records"], b["sorted_gids"], b["ranges"], H, W, bg,
-                                                        clear_records=grec, window=b["window"], bins=b)
+            # the compositing forward with the L1 loss fused (its partial sums, and the
+            # launch that orders the tiles for the backward finishes the loss)
+            image, fT, nc, order, loss = rasterizer.composite(pre["records"], b["sorted_gids"], b["ranges"], H, W,
+                                                              bg, clear_records=grec, window=b["window"], bins=b,
+                                                              l1_target=tgt)
             mark("t3")
-            loss = torch.empty((), device=dev)
-            gimg = torch.empty_like(image)
-            _lib.call("gs_l1_loss", s_, image.numel(), _lib.ptr(image), _lib.ptr(tgt), _lib.ptr(loss), _lib.ptr(gimg))
+            _lib.call("gs_composite_bwd_l1", s_, N, _lib.ptr(pre["records"]), _lib.ptr(b["sorted_gids"]),
+                      b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), W, H, _lib.ptr(bg), None, _lib.ptr(image),
+                      _lib.ptr(tgt), _lib.ptr(one), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec),
+                      None, 1, _lib.ptr(b["window"]))
             mark("t4")
-            _lib.call("gs_composite_bwd", s_, N, _lib.ptr(pre["records"]), _lib.ptr(b["sorted_gids"]),
-                      b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), W, H, _lib.ptr(bg), _lib.ptr(gimg), _lib.ptr(fT), _lib.ptr(nc),
-                      _lib.ptr(order), _lib.ptr(grec), None, 1, _lib.ptr(b["window"]))
-            mark("t5")
             outs = [torch.empty_like(getattr(g, f)) for f in fields]
             _lib.call("gs_preprocess_bwd", s_, N, g.sh_coeffs.shape[1], D, *[_lib.ptr(getattr(g, f).detach())
                                                                              for f in fields],
                       _lib.ptr(cam.W2C.contiguous()), W, H, float(cam.fx), float(cam.fy), float(cam.cx),
                       float(cam.cy), _lib.ptr(grec), *[_lib.ptr(o) for o in outs])
-            mark("t6")
+            mark("t5")
             accumulate_from_extras(stats_state, outs[0], g.means.detach(), cam,
                                    {"valid_mask": pre["valid"], "radii": pre["radii"]}, active=mask)
-            mark("t7")
+            mark("t6")
+        return pre, b, grec, image, fT, nc, outs
+
+    with torch.no_grad():
+        # the stage tensors the side measurements below use (the stages are timed again
+        # after the headline, on a warm GPU)
+        pre, b, grec, image, fT, nc, outs = stage_loop()
+        # the L1 loss and its VJP as separate launches (gs_l1_loss, gs_l1_loss_bwd: the unfused
+        # path's loss stage) on the same image
+        for _ in range(reps):
+            mark("u0")
+            lo1 = torch.empty((), device=dev)
+            gimg = torch.empty_like(image)
+            _lib.call("gs_l1_loss", s_, image.numel(), _lib.ptr(image), _lib.ptr(tgt), _lib.ptr(lo1), None)
+            _lib.call("gs_l1_loss_bwd", s_, image.numel(), _lib.ptr(image), _lib.ptr(tgt), _lib.ptr(one),
+                      _lib.ptr(gimg))
+            mark("u1")
         # the trainer's other loss term (trainer.py:18-26): L1 + SSIM forward and VJP of
         # the same frame, timed beside the step (the headline step seeds L1 only)
         Hc, Wc, Cc = image.shape
@@ -220,9 +244,21 @@ def main():
         train_step(tstate, tgt, cam.W2C, cs, topt, sh_degree=D)
     torch.cuda.synchronize()
     train_step_ms = (time.perf_counter() - t_ts) / reps * 1e3
+    # The headline: W warm-up steps, then K timed steps.  It runs after the per-stage and
+    # side measurements above, so that the GPU has left its idle clocks (a cold start runs
+    # the first ~20 steps about 4 % slower).
+    dt, extras = timed(True)
+    # the same step with render and l1_loss as separate functions (the reference's call
+    # structure: the loss's own launches and the image gradient in memory), for comparison
+    dt_unfused = timed(False)[0] if kind != "fwd" else None
+    n_int = int(extras["n_interactions"])
+    for k in [k for k in ev if k.startswith("t")]:
+        del ev[k]
+    with torch.no_grad():
+        pre, b, grec, image, fT, nc, outs = stage_loop()
     extra_ms = {nm: float(np.median([ev[a][r].elapsed_time(ev[z][r]) for r in range(reps)]))
                 for nm, a, z in (("l1_ssim_fwd", "s0", "s1"), ("l1_ssim_bwd", "s1", "s2"), ("adam", "a0", "a1"),
-                                 ("densify_and_prune", "d0", "d1"))}
+                                 ("densify_and_prune", "d0", "d1"), ("l1_loss_unfused", "u0", "u1"))}
     if "p0" in ev:
         extra_ms["ply_pack"] = float(np.median([ev["p0"][r].elapsed_time(ev["p1"][r]) for r in range(reps)]))
     extra_ms["train_step"] = train_step_ms
@@ -243,8 +279,8 @@ def main():
     extra_gbs["densify_and_prune"] = den_bytes / (extra_ms["densify_and_prune"] * 1e-3) / 1e9
     if "ply_pack" in extra_ms:
         extra_gbs["ply_pack"] = (236 + 248) * N / (extra_ms["ply_pack"] * 1e-3) / 1e9
-    names = ["preprocess_fwd", "binning", "composite_fwd", "l1_loss", "composite_bwd", "preprocess_bwd",
-             "densify_stats"]
+    # composite_fwd and composite_bwd include the fused L1 loss and its VJP
+    names = ["preprocess_fwd", "binning", "composite_fwd", "composite_bwd", "preprocess_bwd", "densify_stats"]
     stage_ms = {}
     for i, nm in enumerate(names):
         a, z = ev[f"t{i}"], ev[f"t{i + 1}"]
@@ -308,7 +344,7 @@ def main():
                   "reference_design_bytes": ks_bytes,
                   "reference_design_bytes_over_this_time_frac": ks_bytes / (hbm_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
     # the dominant kernel of the timed step's own stages
-    step_stages = {"fwd": names[:3], "fwdbwd": names[:6], "fwdbwd_stats": names}[kind]
+    step_stages = {"fwd": names[:3], "fwdbwd": names[:5], "fwdbwd_stats": names}[kind]
     dominant = max(step_stages, key=stage_ms.get)
     if args.stages:
         print(json.dumps({"stage_ms": stage_ms, "stage_GBps": stage_gbs, "stage_TFLOPs": stage_tflops,
@@ -352,6 +388,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": dt * 1e3,
+        "ms_per_step_unfused_loss": None if dt_unfused is None else dt_unfused * 1e3,
         "fwd_ms": stage_ms["preprocess_fwd"] + stage_ms["binning"] + stage_ms["composite_fwd"],
         "step": kind,
         "higher_is_better": True,

@@ -84,7 +84,9 @@ const char* gs_last_error(void);
  * gs_eval_sh_bwd.  8: gs_l1_ssim_window, gs_l1_ssim_window_bwd.  9: compositing records carry
  * a cap flag in slot 11.  10: that flag is no_cap (1.0 = proven below the cap, rounding
  * included; 0.0 = not proven), read by gs_composite_bwd; gs_composite_prep_bwd,
- * gs_project_bwd.  11: gs_bin_deferred, gs_composite_fwd_deferred. */
+ * gs_project_bwd.  11: gs_bin_deferred, gs_composite_fwd_deferred.  12: the L1 loss fused
+ * into compositing: gs_composite_l1_out_size, gs_composite_fwd_deferred_l1,
+ * gs_composite_bwd_l1. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -257,6 +259,25 @@ int gs_composite_fwd_deferred(void* stream, int64_t n, const float* records, int
                               const float* background, float* image, float* final_T, int32_t* n_contrib,
                               int32_t* tile_order, float* clear_records, const gs_window_t* window);
 
+/* The L1 photometric loss fused into compositing: jax_gs/training/losses.py:4-8
+ * (l1_loss(image, target) = mean |image - target|) applied to the rendered image, as
+ * jax_gs/training/trainer.py differentiates l1_loss(render(...)).  The forward adds each
+ * pixel's |image - target| over its channels as it writes the image (one partial sum per
+ * workgroup) and the launch that orders the tiles sums the partials in a fixed order; the
+ * backward forms the image cotangent sign(image - target) * dL/dloss / (3 H W) per pixel
+ * where it reads it, so no separate loss launch, clear or image-gradient array is needed.
+ *
+ * gs_composite_l1_out_size: floats of l1_out (the loss, then the partial sums).
+ * gs_composite_fwd_deferred_l1: gs_composite_fwd_deferred, plus l1_target[H,W,3] and
+ *   l1_out, whose element 0 receives the loss. */
+int64_t gs_composite_l1_out_size(int width, int height);
+int gs_composite_fwd_deferred_l1(void* stream, int64_t n, const float* records, int32_t* sorted_gids,
+                                 int64_t capacity, const int32_t* ranges, const int32_t* stats,
+                                 const void* bin_workspace, size_t bin_workspace_bytes, int width, int height,
+                                 const float* background, float* image, float* final_T, int32_t* n_contrib,
+                                 int32_t* tile_order, float* clear_records, const gs_window_t* window,
+                                 const float* l1_target, float* l1_out);
+
 /* Vector-Jacobian product of gs_composite_fwd (JAX autodiff of render_tiles).
  * tile_order is the forward's (NULL: a fixed order; results agree up to the order of
  * floating-point additions).  grad_records[N,GS_REC_STRIDE] receives the gradient
@@ -269,6 +290,16 @@ int gs_composite_bwd(void* stream, int64_t n, const float* records, const int32_
                      const float* grad_image, const float* final_T, const int32_t* n_contrib,
                      const int32_t* tile_order, float* grad_records, float* grad_background, int accumulate,
                      const gs_window_t* window);
+
+/* gs_composite_bwd of a render whose L1 loss was fused (gs_composite_fwd_deferred_l1): the
+ * image cotangent of each pixel is sign(image - l1_target) * l1_cot[0] / (3 H W) (the VJP of
+ * losses.py:4-8, sign(0) = 0, l1_cot = dL/dloss on the device), plus grad_image when it is
+ * not NULL (the image also used elsewhere).  image is the forward's. */
+int gs_composite_bwd_l1(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
+                        int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
+                        const float* grad_image, const float* image, const float* l1_target, const float* l1_cot,
+                        const float* final_T, const int32_t* n_contrib, const int32_t* tile_order,
+                        float* grad_records, float* grad_background, int accumulate, const gs_window_t* window);
 
 /* Vector-Jacobian product of gs_preprocess_fwd's compositing records with respect to
  * the five Gaussian parameter arrays (JAX autodiff of project_gaussians, eval_sh,

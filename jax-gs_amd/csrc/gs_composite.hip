@@ -77,6 +77,36 @@ __device__ inline float wave_sum(float v) {
   return bcast(x, 63);
 }
 
+// The image cotangent the backward reads per pixel: dL/dimage (gimg), and/or the VJP of the
+// L1 loss fused into the compositing (losses.py:4-8) when tgt is set: sign(image - target)
+// times (dL/dloss) / count, sign(0) = 0, formed as the separate loss VJP forms it.
+struct ImageCot {
+  const float* gimg;  // may be NULL when tgt is set
+  const float* img;   // the forward's image (fused L1)
+  const float* tgt;   // L1 target; NULL: no fused L1
+  const float* cot;   // dL/dloss, one float on the device
+};
+__device__ inline float l1_sign(float d) { return d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f); }
+__device__ inline float l1_scale(const ImageCot& c, int W, int H) {
+  return c.tgt != nullptr ? c.cot[0] / (float)(3 * (int64_t)W * H) : 0.0f;
+}
+__device__ inline void image_cot(const ImageCot& c, float sc, int64_t p, float& g0, float& g1, float& g2) {
+  if (c.tgt == nullptr) {
+    g0 = c.gimg[3 * p];
+    g1 = c.gimg[3 * p + 1];
+    g2 = c.gimg[3 * p + 2];
+    return;
+  }
+  g0 = l1_sign(c.img[3 * p] - c.tgt[3 * p]) * sc;
+  g1 = l1_sign(c.img[3 * p + 1] - c.tgt[3 * p + 1]) * sc;
+  g2 = l1_sign(c.img[3 * p + 2] - c.tgt[3 * p + 2]) * sc;
+  if (c.gimg != nullptr) {
+    g0 += c.gimg[3 * p];
+    g1 += c.gimg[3 * p + 1];
+    g2 += c.gimg[3 * p + 2];
+  }
+}
+
 // Reduce-scatter of per-lane values over the wave by recursive halving.  A level pairs
 // the values (2k, 2k+1); a lane keeps the member selected by one of its lane bits and
 // adds the partner lane's copy of it (partner = lane ^ distance).  The levels run in
@@ -348,7 +378,8 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
     float* __restrict__ img, float* __restrict__ finalT, int32_t* __restrict__ ncontrib,
     int32_t* __restrict__ tile_cost, float4* __restrict__ clear, int64_t n_clear,
-    const gs_window_t* __restrict__ win, const SBLists sbl, int32_t* __restrict__ gids_out) {
+    const gs_window_t* __restrict__ win, const SBLists sbl, int32_t* __restrict__ gids_out,
+    const float* __restrict__ l1_tgt, float* __restrict__ l1_part) {
   constexpr int WPT = 4 / PPT;  // waves per tile
   // Every workgroup clears its slice of the caller's array after its own outputs (stores
   // and loads share one wait counter, so stores issued before the walk would hold up its
@@ -363,6 +394,7 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
   const int b = blockIdx.x / WPT, part = blockIdx.x % WPT;
   const int tile = tile_of_block(b, TX, T / TX);
   if (tile < 0) {
+    if (l1_part != nullptr && threadIdx.x == 0) l1_part[blockIdx.x] = 0.0f;
     clear_slice();
     return;
   }
@@ -660,18 +692,28 @@ __global__ __launch_bounds__(64) void composite_fwd_kernel(
     }
   }
   const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];
+  // the L1 loss against l1_tgt (losses.py:4-8): the lane's sum of |image - target| over its
+  // pixels' channels, reduced over the wave into the workgroup's partial
+  float l1 = 0.0f;
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
     const int Y = Y0 + 4 * i;
     if (X < W && Y < H) {
       const int64_t p = (int64_t)Y * W + X;
-      img[3 * p] = c0[i] + Tr[i] * bg0;
-      img[3 * p + 1] = c1[i] + Tr[i] * bg1;
-      img[3 * p + 2] = c2[i] + Tr[i] * bg2;
+      const float o0 = c0[i] + Tr[i] * bg0, o1 = c1[i] + Tr[i] * bg1, o2 = c2[i] + Tr[i] * bg2;
+      img[3 * p] = o0;
+      img[3 * p + 1] = o1;
+      img[3 * p + 2] = o2;
       if (finalT) finalT[p] = Tr[i];
       // a pixel still open met every entry of the tile, culled ones included
       if (ncontrib) ncontrib[p] = Tr[i] > kTMin ? n : cnt[i];
+      if (l1_tgt != nullptr)
+        l1 += (fabsf(o0 - l1_tgt[3 * p]) + fabsf(o1 - l1_tgt[3 * p + 1])) + fabsf(o2 - l1_tgt[3 * p + 2]);
     }
+  }
+  if (l1_part != nullptr) {
+    l1 = wave_sum(l1);
+    if (lane == 0) l1_part[blockIdx.x] = l1;
   }
   // walk length of the tile (first wave of the tile): the backward's cost estimate
   // (two waves per tile: each stores its own length in one 16-bit half, the order takes
@@ -696,7 +738,7 @@ template <int PPT, bool WIN, bool NOCAP, bool O32>
 __device__ __forceinline__ void composite_bwd_body(
     const float4* __restrict__ rec, int num_g, const int32_t* __restrict__ gids, int64_t n_entries,
     const int32_t* __restrict__ ranges, int W, int H, int TX, int T, const float* __restrict__ bg,
-    const float* __restrict__ gimg, const float* __restrict__ finalT, const int32_t* __restrict__ ncontrib,
+    const ImageCot gc, const float* __restrict__ finalT, const int32_t* __restrict__ ncontrib,
     float* __restrict__ grec, const int32_t* __restrict__ order, const gs_window_t* __restrict__ win) {
   constexpr int WPT = 4 / PPT;
   const int b = blockIdx.x / WPT, part = blockIdx.x % WPT;
@@ -710,6 +752,7 @@ __device__ __forceinline__ void composite_bwd_body(
   int start, n;
   tile_span(ranges, tile, n_entries, num_g, start, n);
   const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];
+  const float l1sc = l1_scale(gc, W, H);
 
   float py[PPT], Tr[PPT], g0[PPT], g1[PPT], g2[PPT], Rg[PPT];
   int kp[PPT];
@@ -727,9 +770,7 @@ __device__ __forceinline__ void composite_bwd_body(
       Tr[i] = NOCAP ? 1.0f / fmaxf(finalT[p], 1e-30f) : finalT[p];  // finite for T = 0
       const int k = ncontrib[p];
       kp[i] = k < 0 ? 0 : (k > n ? n : k);  // entries beyond the tile's list never load
-      g0[i] = gimg[3 * p];
-      g1[i] = gimg[3 * p + 1];
-      g2[i] = gimg[3 * p + 2];
+      image_cot(gc, l1sc, p, g0[i], g1[i], g2[i]);
     }
     // colour behind the last entry is the background
     Rg[i] = fmaf(bg2, g2[i], fmaf(bg1, g1[i], bg0 * g0[i]));
@@ -941,9 +982,9 @@ __device__ __forceinline__ void composite_bwd_body(
 #define GS_BWD_PARAMS                                                                                       \
   const float4 *__restrict__ rec, int num_g, const int32_t *__restrict__ gids, int64_t n_entries,               \
       const int32_t *__restrict__ ranges, int W, int H, int TX, int T, const float *__restrict__ bg,            \
-      const float *__restrict__ gimg, const float *__restrict__ finalT, const int32_t *__restrict__ ncontrib, \
+      const ImageCot gc, const float *__restrict__ finalT, const int32_t *__restrict__ ncontrib,               \
       float *__restrict__ grec, const int32_t *__restrict__ order, const gs_window_t *__restrict__ win
-#define GS_BWD_ARGS rec, num_g, gids, n_entries, ranges, W, H, TX, T, bg, gimg, finalT, ncontrib, grec, order, win
+#define GS_BWD_ARGS rec, num_g, gids, n_entries, ranges, W, H, TX, T, bg, gc, finalT, ncontrib, grec, order, win
 
 // The backward's two builds.  One pixel per lane (images below 2048 tiles, four waves per
 // tile): 64 VGPRs, 8 waves per SIMD, the general body only (the no-cap path's per-entry test
@@ -979,16 +1020,19 @@ __global__ void zero_grads_kernel(float4* __restrict__ p, int64_t n4, float* __r
 
 // dL/dbackground = sum over pixels of T_final * g (rasterizer.py:244): grid-stride
 // partial sums, a block reduction and 3 atomics per block.
-__global__ __launch_bounds__(256) void background_grad_kernel(int64_t npix, const float* __restrict__ finalT,
-                                                              const float* __restrict__ gimg,
+__global__ __launch_bounds__(256) void background_grad_kernel(int64_t npix, int W, int H,
+                                                              const float* __restrict__ finalT, const ImageCot gc,
                                                               float* __restrict__ gbg) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const float sc = l1_scale(gc, W, H);
   float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f;
   for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < npix; p += stride) {
     const float t = finalT[p];
-    a0 = fmaf(t, gimg[3 * p], a0);
-    a1 = fmaf(t, gimg[3 * p + 1], a1);
-    a2 = fmaf(t, gimg[3 * p + 2], a2);
+    float g0, g1, g2;
+    image_cot(gc, sc, p, g0, g1, g2);
+    a0 = fmaf(t, g0, a0);
+    a1 = fmaf(t, g1, a1);
+    a2 = fmaf(t, g2, a2);
   }
   a0 = wave_sum(a0);
   a1 = wave_sum(a1);
@@ -1019,11 +1063,30 @@ __global__ __launch_bounds__(256) void background_grad_kernel(int64_t npix, cons
 constexpr int kOrderMaxTiles = 65536;
 constexpr int kOrderBuckets = 1024;  // walk lengths <= 4096 -> buckets <= 512
 
-__global__ __launch_bounds__(1024) void tile_order_kernel(int32_t* __restrict__ order, int T) {
+// The same workgroup finishes the fused L1 loss: loss = (sum of the forward's per-workgroup
+// partials) / count, the partials added in a fixed order (no atomics: the same value on
+// every run).
+__global__ __launch_bounds__(1024) void tile_order_kernel(int32_t* __restrict__ order, int T,
+                                                          const float* __restrict__ l1_part, int nparts,
+                                                          int64_t count, float* __restrict__ l1_loss) {
   __shared__ uint16_t bucket[kOrderMaxTiles];
   __shared__ int start[kOrderBuckets];
   __shared__ int wsum[16];
+  __shared__ float fsum[16];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  if (l1_part != nullptr) {
+    float a = 0.0f;
+    for (int i = tid; i < nparts; i += 1024) a += l1_part[i];
+    a = wave_sum(a);
+    if (lane == 0) fsum[wid] = a;
+    __syncthreads();
+    if (tid == 0) {
+      float t = 0.0f;
+      for (int w = 0; w < 16; ++w) t += fsum[w];
+      l1_loss[0] = t / (float)count;  // jnp.mean: the sum over the count
+    }
+  }
+  if (order == nullptr) return;
   if (T > kOrderMaxTiles) {
     for (int t = tid; t < T; t += 1024) order[t] = t;
     return;
@@ -1095,10 +1158,18 @@ extern "C" int gs_window_from_list(void* stream, const int32_t* sorted_gids, int
 }
 
 namespace {
+// Floats of the l1_out array of the fused L1 loss: the loss, then one partial sum per
+// compositing workgroup (at most four per tile cell of the launch grid).
+int64_t l1_out_floats(int width, int height) {
+  const int TX = (width + kTile - 1) / kTile, TY = (height + kTile - 1) / kTile;
+  return 1 + 4 * (int64_t)tile_blocks(TX, TY);
+}
+
 int composite_fwd_run(const char* name, void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                       int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
                       float* image, float* final_T, int32_t* n_contrib, int32_t* tile_order, float* clear_records,
-                      const gs_window_t* window, const SBLists* sbl, int32_t* gids_out) {
+                      const gs_window_t* window, const SBLists* sbl, int32_t* gids_out,
+                      const float* l1_target = nullptr, float* l1_out = nullptr) {
   GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "%s: n out of range", name);
   GS_REQUIRE(n_entries >= 0, "%s: n_entries must be >= 0", name);
   GS_REQUIRE(width > 0 && height > 0, "%s: bad image size %dx%d", name, width, height);
@@ -1111,12 +1182,14 @@ int composite_fwd_run(const char* name, void* stream, int64_t n, const float* re
   GS_REQUIRE(clear_records == nullptr || ((uintptr_t)clear_records & 15) == 0,
              "%s: clear_records must be 16-byte aligned", name);
   const int64_t n4_clear = clear_records ? n * kRec / 4 : 0;  // kRec = 12: whole float4s
+  GS_REQUIRE((l1_target == nullptr) == (l1_out == nullptr), "%s: l1_target and l1_out go together", name);
+  float* l1_part = l1_out ? l1_out + 1 : nullptr;
   const SBLists none{};
 #define GS_FWD_LAUNCH2(PPT, WPT, WIN, O32, SB)                                                                  \
   hipLaunchKernelGGL((composite_fwd_kernel<PPT, WIN, O32, SB>), dim3(nblk * (WPT)), dim3(64), 0, s,             \
                      (const float4*)records, (int)n, sorted_gids, n_entries, ranges, width, height, TX, T,        \
                      background, image, final_T, n_contrib, tile_order, (float4*)clear_records, n4_clear, window, \
-                     SB ? *sbl : none, gids_out)
+                     SB ? *sbl : none, gids_out, l1_target, l1_part)
 #define GS_FWD_LAUNCH1(PPT, WPT, WIN, O32) \
   if (sbl) GS_FWD_LAUNCH2(PPT, WPT, WIN, O32, true); else GS_FWD_LAUNCH2(PPT, WPT, WIN, O32, false)
 #define GS_FWD_LAUNCH(PPT, WPT, WIN) \
@@ -1133,8 +1206,10 @@ int composite_fwd_run(const char* name, void* stream, int64_t n, const float* re
 #undef GS_FWD_LAUNCH1
 #undef GS_FWD_LAUNCH2
   GS_LAUNCH_CHECK("composite_fwd_kernel");
-  if (tile_order) {
-    hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(1024), 0, s, tile_order, T);
+  if (tile_order || l1_out) {
+    const int wpt = pick_ppt(T) == 4 ? (T >= kFwdOneWaveTiles ? 1 : 2) : 4;
+    hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(1024), 0, s, tile_order, T, l1_part, nblk * wpt,
+                       (int64_t)width * height * 3, l1_out);
     GS_LAUNCH_CHECK("tile_order_kernel");
   }
   return GS_OK;
@@ -1165,17 +1240,40 @@ extern "C" int gs_composite_fwd_deferred(void* stream, int64_t n, const float* r
                            sorted_gids);
 }
 
-extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
-                                int64_t n_entries, const int32_t* ranges, int width, int height,
-                                const float* background, const float* grad_image, const float* final_T,
-                                const int32_t* n_contrib, const int32_t* tile_order, float* grad_records,
-                                float* grad_background, int accumulate, const gs_window_t* window) {
-  GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "gs_composite_bwd: n out of range");
-  GS_REQUIRE(n_entries >= 0, "gs_composite_bwd: n_entries must be >= 0");
-  GS_REQUIRE(width > 0 && height > 0, "gs_composite_bwd: bad image size %dx%d", width, height);
-  GS_REQUIRE(ranges && background && grad_image && final_T && n_contrib, "gs_composite_bwd: NULL argument");
-  GS_REQUIRE(n == 0 || n_entries == 0 || (records && sorted_gids && grad_records),
-             "gs_composite_bwd: NULL records/gids");
+extern "C" int64_t gs_composite_l1_out_size(int width, int height) {
+  return width > 0 && height > 0 ? l1_out_floats(width, height) : 0;
+}
+
+extern "C" int gs_composite_fwd_deferred_l1(void* stream, int64_t n, const float* records, int32_t* sorted_gids,
+                                            int64_t capacity, const int32_t* ranges, const int32_t* stats,
+                                            const void* bin_workspace, size_t bin_workspace_bytes, int width,
+                                            int height, const float* background, float* image, float* final_T,
+                                            int32_t* n_contrib, int32_t* tile_order, float* clear_records,
+                                            const gs_window_t* window, const float* l1_target, float* l1_out) {
+  GS_REQUIRE(capacity > 0, "gs_composite_fwd_deferred_l1: capacity must be > 0 (got %lld)", (long long)capacity);
+  GS_REQUIRE(stats != nullptr && (n == 0 || sorted_gids != nullptr), "gs_composite_fwd_deferred_l1: NULL argument");
+  GS_REQUIRE(l1_target != nullptr && l1_out != nullptr, "gs_composite_fwd_deferred_l1: NULL l1_target or l1_out");
+  SBLists sbl;
+  const int rc = superblock_lists(n, width, height, capacity, bin_workspace, bin_workspace_bytes, stats, &sbl);
+  if (rc != GS_OK) return rc;
+  return composite_fwd_run("gs_composite_fwd_deferred_l1", stream, n, records, sorted_gids, capacity, ranges, width,
+                           height, background, image, final_T, n_contrib, tile_order, clear_records, window, &sbl,
+                           sorted_gids, l1_target, l1_out);
+}
+
+namespace {
+int composite_bwd_run(const char* name, void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
+                      int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
+                      const ImageCot& gc, const float* final_T, const int32_t* n_contrib,
+                      const int32_t* tile_order, float* grad_records, float* grad_background, int accumulate,
+                      const gs_window_t* window) {
+  GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "%s: n out of range", name);
+  GS_REQUIRE(n_entries >= 0, "%s: n_entries must be >= 0", name);
+  GS_REQUIRE(width > 0 && height > 0, "%s: bad image size %dx%d", name, width, height);
+  GS_REQUIRE(ranges && background && final_T && n_contrib, "%s: NULL argument", name);
+  GS_REQUIRE(gc.tgt != nullptr ? (gc.img != nullptr && gc.cot != nullptr) : gc.gimg != nullptr,
+             "%s: NULL image cotangent", name);
+  GS_REQUIRE(n == 0 || n_entries == 0 || (records && sorted_gids && grad_records), "%s: NULL records/gids", name);
   hipStream_t s = (hipStream_t)stream;
   if ((n > 0 && !accumulate) || grad_background) {
     // clears the records unless accumulating, and the background cotangent
@@ -1186,7 +1284,7 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
   if (grad_background) {
     const int64_t npix = (int64_t)width * height;
     hipLaunchKernelGGL(background_grad_kernel, dim3(std::min<int64_t>(1024, div_up(npix, 256))), dim3(256), 0, s,
-                       npix, final_T, grad_image, grad_background);
+                       npix, width, height, final_T, gc, grad_background);
     GS_LAUNCH_CHECK("background_grad_kernel");
   }
   const int TX = (width + kTile - 1) / kTile, TY = (height + kTile - 1) / kTile;
@@ -1194,7 +1292,7 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
   const int nblk = tile_blocks(TX, TY);
 #define GS_BWD_LAUNCH(KERNEL, WPT)                                                                                  \
   hipLaunchKernelGGL(KERNEL, dim3(nblk * (WPT)), dim3(64), 0, s, (const float4*)records, (int)n, sorted_gids, n_entries, \
-                     ranges, width, height, TX, T, background, grad_image, final_T, n_contrib, grad_records,           \
+                     ranges, width, height, TX, T, background, gc, final_T, n_contrib, grad_records,                   \
                      tile_order, window)
   const bool win = window != nullptr, o32 = rec_offsets_fit(n);
   if (pick_ppt(T) == 4) {
@@ -1217,4 +1315,30 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
 #undef GS_BWD_LAUNCH
   GS_LAUNCH_CHECK("composite_bwd_kernel");
   return GS_OK;
+}
+}  // namespace
+
+extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
+                                int64_t n_entries, const int32_t* ranges, int width, int height,
+                                const float* background, const float* grad_image, const float* final_T,
+                                const int32_t* n_contrib, const int32_t* tile_order, float* grad_records,
+                                float* grad_background, int accumulate, const gs_window_t* window) {
+  const ImageCot gc{grad_image, nullptr, nullptr, nullptr};
+  return composite_bwd_run("gs_composite_bwd", stream, n, records, sorted_gids, n_entries, ranges, width, height,
+                           background, gc, final_T, n_contrib, tile_order, grad_records, grad_background, accumulate,
+                           window);
+}
+
+extern "C" int gs_composite_bwd_l1(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
+                                   int64_t n_entries, const int32_t* ranges, int width, int height,
+                                   const float* background, const float* grad_image, const float* image,
+                                   const float* l1_target, const float* l1_cot, const float* final_T,
+                                   const int32_t* n_contrib, const int32_t* tile_order, float* grad_records,
+                                   float* grad_background, int accumulate, const gs_window_t* window) {
+  GS_REQUIRE(image != nullptr && l1_target != nullptr && l1_cot != nullptr,
+             "gs_composite_bwd_l1: NULL image, l1_target or l1_cot");
+  const ImageCot gc{grad_image, image, l1_target, l1_cot};
+  return composite_bwd_run("gs_composite_bwd_l1", stream, n, records, sorted_gids, n_entries, ranges, width,
+                           height, background, gc, final_T, n_contrib, tile_order, grad_records, grad_background,
+                           accumulate, window);
 }

@@ -6,6 +6,6 @@ signature and ``extras``, backed by hand-written HIP kernels in libgsraster.so
 """
 from .core.camera import Camera
 from .core.gaussians import Gaussians, init_gaussians_from_pcd
-from .renderer.renderer import render
+from .renderer.renderer import render, render_l1
 
-__all__ = ["Camera", "Gaussians", "init_gaussians_from_pcd", "render"]
+__all__ = ["Camera", "Gaussians", "init_gaussians_from_pcd", "render", "render_l1"]

@@ -48,6 +48,10 @@ _SIGS = {
     "gs_composite_fwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "gs_composite_fwd_deferred": [_P, _I64, _P, _P, _I64, _P, _P, _P, _SZ, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P],
+    "gs_composite_l1_out_size": [_I, _I],
+    "gs_composite_fwd_deferred_l1": [_P, _I64, _P, _P, _I64, _P, _P, _P, _SZ, _I, _I, _P, _P, _P, _P, _P, _P, _P,
+                                     _P, _P],
+    "gs_composite_bwd_l1": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P],
     "gs_preprocess_bwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P, _P],
     "gs_preprocess_bwd_w2c_workspace_size": [_I64],
     "gs_preprocess_bwd_w2c": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P,
@@ -83,12 +87,12 @@ _RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_
             "gs_bin_deferred_workspace_size": _SZ,
             "gs_bin_reference_workspace_size": _SZ, "gs_preprocess_bwd_w2c_workspace_size": _SZ,
             "gs_l1_ssim_window_workspace_size": _SZ,
-            "gs_densify_workspace_size": _SZ}
+            "gs_densify_workspace_size": _SZ, "gs_composite_l1_out_size": _I64}
 
 _lib = None
 
 
-ABI_VERSION = 11  # gs_abi_version() of the signatures bound below
+ABI_VERSION = 12  # gs_abi_version() of the signatures bound below
 
 
 class NativeLibraryMissing(RuntimeError):

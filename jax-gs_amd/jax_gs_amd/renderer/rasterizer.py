@@ -156,7 +156,8 @@ def composite_records(means2D, cov2D, opacities, colors) -> torch.Tensor:
 
 def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Tensor, H: int, W: int,
               background: torch.Tensor, residuals: bool = True, clear_records: torch.Tensor | None = None,
-              window: torch.Tensor | None = None, bins: BinResult | None = None):
+              window: torch.Tensor | None = None, bins: BinResult | None = None,
+              l1_target: torch.Tensor | None = None):
     """Front-to-back compositing; returns (image [H,W,3], final_T [H,W], n_contrib [H,W],
     tile_order [T]), the last three the backward's residuals (None unless residuals):
     tile_order lists the tiles longest walk first, the backward's launch order.
@@ -167,7 +168,9 @@ def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Te
     which differ only for chunks that start within 512 slots of the end of the
     reference's arrays.  bins: the BinResult of a deferred binning whose sorted_gids and
     ranges these are (gs_composite_fwd_deferred); the results are the same as with the
-    full list."""
+    full list.  l1_target ([H,W,3], with a deferred binning's bins): the L1 loss
+    mean |image - target| (losses.py:4-8) is computed by the same launches
+    (gs_composite_fwd_deferred_l1) and returned as a fifth value, a 0-d tensor."""
     dev = records.device
     _, _, T = num_tiles(W, H)
     image = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
@@ -178,10 +181,19 @@ def composite(records: torch.Tensor, sorted_gids: torch.Tensor, ranges: torch.Te
         if sorted_gids is not bins["sorted_gids"] or ranges is not bins["ranges"] or records.shape[0] != bins["n"]:
             raise ValueError("composite: bins must be the deferred binning of these entries and records")
         ws = bins["workspace"]
-        _lib.call("gs_composite_fwd_deferred", _lib.stream_handle(dev), records.shape[0], _lib.ptr(records),
-                  _lib.ptr(sorted_gids), bins["capacity"], _lib.ptr(ranges), _lib.ptr(bins["stats"]), _lib.ptr(ws),
-                  ws.shape[0], int(W), int(H), _lib.ptr(background), _lib.ptr(image), _lib.ptr(fT), _lib.ptr(nc),
-                  _lib.ptr(order), _lib.ptr(clear_records), _lib.ptr(window))
+        args = (_lib.stream_handle(dev), records.shape[0], _lib.ptr(records), _lib.ptr(sorted_gids), bins["capacity"],
+                _lib.ptr(ranges), _lib.ptr(bins["stats"]), _lib.ptr(ws), ws.shape[0], int(W), int(H),
+                _lib.ptr(background), _lib.ptr(image), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order),
+                _lib.ptr(clear_records), _lib.ptr(window))
+        if l1_target is not None:
+            tgt = check_f32("l1_target", l1_target, (H, W, 3), dev)
+            l1_out = torch.empty((_lib.lib().gs_composite_l1_out_size(int(W), int(H)),), dtype=torch.float32,
+                                 device=dev)
+            _lib.call("gs_composite_fwd_deferred_l1", *args, _lib.ptr(tgt), _lib.ptr(l1_out))
+            return image, fT, nc, order, l1_out[0]
+        _lib.call("gs_composite_fwd_deferred", *args)
+    elif l1_target is not None:
+        raise ValueError("composite: the fused L1 loss needs a deferred binning's bins")
     else:
         _lib.call("gs_composite_fwd", _lib.stream_handle(dev), records.shape[0], _lib.ptr(records),
                   _lib.ptr(sorted_gids), sorted_gids.shape[0], _lib.ptr(ranges), int(W), int(H),

@@ -11,7 +11,7 @@ HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))
 def declared_functions():
     src = open(HEADER).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?(?:int|size_t|char\s*\*|void)\s*\*?\s*(gs_\w+)\s*\(", src, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?(?:int64_t|int|size_t|char\s*\*|void)\s*\*?\s*(gs_\w+)\s*\(", src, re.M)))
 
 
 def test_header_declares_entry_points():
@@ -32,7 +32,7 @@ def test_binding_covers_every_declared_symbol():
 
 def test_abi_version_and_workspace_query_without_gpu():
     L = _lib.lib()
-    assert L.gs_abi_version() == _lib.ABI_VERSION == 11
+    assert L.gs_abi_version() == _lib.ABI_VERSION == 12
     # size query: pure host arithmetic, grows with the number of Gaussians
     a = L.gs_bin_workspace_size(1000, 64, 64, 0)
     b = L.gs_bin_workspace_size(100000, 64, 64, 0)
@@ -103,6 +103,27 @@ def test_argument_errors_of_the_deferred_binning():
     assert rc == 1 and b"NULL" in L.gs_last_error()
     rc = L.gs_composite_fwd_deferred(None, 10, fake, *args, fake, need, 0, 64, *([fake] * 2), *([None] * 5))
     assert rc == 1 and b"bad sizes" in L.gs_last_error()
+
+
+def test_argument_errors_of_the_fused_l1_loss():
+    """gs_composite_fwd_deferred_l1 / gs_composite_bwd_l1 need their target, loss and
+    cotangent arrays; the loss array holds the loss and one partial per compositing
+    workgroup (at most four per tile)."""
+    L = _lib.lib()
+    fake = ctypes.c_void_p(256)
+    assert L.gs_composite_l1_out_size(0, 64) == 0
+    T = ((1920 + 15) // 16) * ((1080 + 15) // 16)
+    assert L.gs_composite_l1_out_size(1920, 1080) >= 1 + T
+    rc = L.gs_composite_fwd_deferred_l1(None, 10, fake, fake, 1000, fake, fake, fake, 1 << 20, 64, 64,
+                                        *([fake] * 2), *([None] * 5), None, fake)
+    assert rc == 1 and b"l1_target" in L.gs_last_error()
+    rc = L.gs_composite_bwd_l1(None, 10, fake, fake, 100, fake, 64, 64, fake, None, None, fake, fake, fake, fake,
+                               fake, fake, None, 1, None)
+    assert rc == 1 and b"gs_composite_bwd_l1" in L.gs_last_error()
+    # the unfused backward still needs its image cotangent
+    rc = L.gs_composite_bwd(None, 10, fake, fake, 100, fake, 64, 64, fake, None, fake, fake, fake, fake, None, 1,
+                            None)
+    assert rc == 1 and b"image cotangent" in L.gs_last_error()
 
 
 def test_load_ply_missing_file():
