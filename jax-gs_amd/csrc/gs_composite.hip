@@ -1074,9 +1074,27 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(int32_t* __restrict__ 
   __shared__ int wsum[16];
   __shared__ float fsum[16];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  // the workgroup is latency-bound: the first 8 walk lengths and the partials of each round
+  // of 8 are requested together, before anything waits for them
+  const bool ord = order != nullptr && T <= kOrderMaxTiles;
+  uint32_t w0[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int t = tid + 1024 * k;
+    w0[k] = ord && t < T ? (uint32_t)order[t] : 0u;
+  }
   if (l1_part != nullptr) {
     float a = 0.0f;
-    for (int i = tid; i < nparts; i += 1024) a += l1_part[i];
+    for (int i0 = 0; i0 < nparts; i0 += 8 * 1024) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int i = i0 + tid + 1024 * k;
+        v[k] = i < nparts ? l1_part[i] : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) a += v[k];
+    }
     a = wave_sum(a);
     if (lane == 0) fsum[wid] = a;
     __syncthreads();
@@ -1093,13 +1111,16 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(int32_t* __restrict__ 
   }
   start[tid] = 0;
   __syncthreads();
-  for (int t = tid; t < T; t += 1024) {
-    const uint32_t w = (uint32_t)order[t];
+  auto count_tile = [&](int t, uint32_t w) {
     const int c = (int)max(w & 0xFFFFu, w >> 16);  // the longer of the tile's (one or two) walks
     const int bk = min(c >> 3, kOrderBuckets - 1);
     bucket[t] = (uint16_t)bk;
     atomicAdd(&start[bk], 1);
-  }
+  };
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (tid + 1024 * k < T) count_tile(tid + 1024 * k, w0[k]);
+  for (int t = tid + 8 * 1024; t < T; t += 1024) count_tile(t, (uint32_t)order[t]);
   __syncthreads();
   // exclusive scan over buckets in descending order: thread j owns bucket 1023 - j
   const int own = start[kOrderBuckets - 1 - tid];
