@@ -86,7 +86,8 @@ const char* gs_last_error(void);
  * included; 0.0 = not proven), read by gs_composite_bwd; gs_composite_prep_bwd,
  * gs_project_bwd.  11: gs_bin_deferred, gs_composite_fwd_deferred.  12: the L1 loss fused
  * into compositing: gs_composite_l1_out_size, gs_composite_fwd_deferred_l1,
- * gs_composite_bwd_l1. */
+ * gs_composite_bwd_l1.  13: gs_bin and gs_bin_deferred take the chunk window (the binning
+ * builds it; gs_window_from_bins stays for lists binned without it). */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -114,6 +115,19 @@ int gs_preprocess_fwd(void* stream, int64_t n, int sh_k, int sh_degree,
 int gs_composite_prep(void* stream, int64_t n, const float* means2d, const float* cov2d,
                       const float* opacities, const float* colors, float* records);
 
+/* The 512 ids a clamped chunk of the reference's default compositing path reads.
+ * rasterizer.py:184-190 slices chunk c of tile t at min(start + 512 c, L - 512) of its
+ * L-slot arrays, L = max(256 n, 512) (get_tile_interactions, rasterizer.py:84-114); a
+ * chunk starting past L - 512 reads the arrays' last 512 slots, which may hold other
+ * tiles' entries, the empty slots of the Gaussians (tile T, in (depth quantum, id) order)
+ * or the slots of negative-depth Gaussians.  thr is L - 512 in the coordinates of the
+ * entry list the compositing launch is given; ids are the arrays' slots L-512..L-1. */
+typedef struct {
+  int64_t thr;
+  int32_t reserved[2];
+  int32_t ids[512];
+} gs_window_t;
+
 /* Workspace bytes gs_bin needs for n Gaussians, a width x height image and an
  * interaction capacity (capacity <= 0 means the static bound 256*n). */
 size_t gs_bin_workspace_size(int64_t n, int width, int height, int64_t capacity);
@@ -129,11 +143,14 @@ size_t gs_bin_workspace_size(int64_t n, int width, int height, int64_t capacity)
  *   stats[GS_NUM_STATS]     see GS_STAT_*
  * With k Gaussians whose depth has its sign bit set, the reference's arrays carry
  * 256*k extra entries in front (tile -1), so its boundaries equal ranges + 256*k.
- * capacity <= 0 selects the static bound 256*n. */
+ * capacity <= 0 selects the static bound 256*n.
+ * window (may be NULL) receives the default path's chunk window of this list, what
+ * gs_window_from_bins writes, built by the binning's last launch (its threshold, and when
+ * GS_STAT_WINDOW_CLAMPED is set, the ids rebuilt from the inputs and the written list). */
 int gs_bin(void* stream, int64_t n, const float* means2d, const float* radii,
            const uint8_t* valid, const float* depths, int width, int height,
            int64_t capacity, void* workspace, size_t workspace_bytes, int32_t* sorted_gids,
-           int32_t* sorted_tiles, int32_t* ranges, int32_t* stats);
+           int32_t* sorted_tiles, int32_t* ranges, int32_t* stats, gs_window_t* window);
 
 /* Workspace bytes of gs_bin_deferred (gs_bin's and the count sweep's tile masks, 2 KiB
  * per chunk of 256 superblock words). */
@@ -152,7 +169,7 @@ size_t gs_bin_deferred_workspace_size(int64_t n, int width, int height, int64_t 
 int gs_bin_deferred(void* stream, int64_t n, const float* means2d, const float* radii,
                     const uint8_t* valid, const float* depths, int width, int height,
                     int64_t capacity, void* workspace, size_t workspace_bytes, int32_t* sorted_gids,
-                    int32_t* ranges, int32_t* stats);
+                    int32_t* ranges, int32_t* stats, gs_window_t* window);
 
 /* gs_bin without a workspace argument and without any allocation: the workspace is a
  * library-owned device array of GS_BIN_STATIC_SCRATCH_BYTES (128 MiB) that every GPU
@@ -193,18 +210,6 @@ int gs_bin_reference(void* stream, int64_t n, const float* means2d, const float*
 int gs_tile_ranges(void* stream, const int32_t* sorted_tiles, int64_t length, int num_tiles,
                    int32_t* ranges);
 
-/* The 512 ids a clamped chunk of the reference's default compositing path reads.
- * rasterizer.py:184-190 slices chunk c of tile t at min(start + 512 c, L - 512) of its
- * L-slot arrays, L = max(256 n, 512) (get_tile_interactions, rasterizer.py:84-114); a
- * chunk starting past L - 512 reads the arrays' last 512 slots, which may hold other
- * tiles' entries, the empty slots of the Gaussians (tile T, in (depth quantum, id) order)
- * or the slots of negative-depth Gaussians.  thr is L - 512 in the coordinates of the
- * entry list the compositing launch is given; ids are the arrays' slots L-512..L-1. */
-typedef struct {
-  int64_t thr;
-  int32_t reserved[2];
-  int32_t ids[512];
-} gs_window_t;
 
 /* Window of a caller list in the reference's layout (sorted_gids of L = n_entries
  * slots, e.g. from get_tile_interactions or gs_bin_reference): thr = L - 512 and the last

@@ -731,11 +731,13 @@ __global__ __launch_bounds__(kBig) void tile_scan_stats_kernel(const uint32_t* _
                                                                const uint32_t* __restrict__ blkstat, int nblk,
                                                                int64_t cap, int64_t n_gauss,
                                                                int32_t* __restrict__ ranges,
-                                                               int32_t* __restrict__ stats, bool deferred) {
+                                                               int32_t* __restrict__ stats, bool deferred,
+                                                               uint32_t* __restrict__ ticket) {
   constexpr int kPer = 8, kRound = kBig * kPer;
   __shared__ uint32_t stage[kBig * (kPer + 1)];
   __shared__ int64_t red[9][kBig / 64];
   const int tid = threadIdx.x;
+  if (tid == 0) *ticket = 0u;  // the write sweep's count of finished workgroups
   // max, ovf tiles, ovf inter, trunc tiles, trunc inter, cap, neg, negative-depth entries,
   // last 512-entry chunk start over the tiles (-1: no entries)
   int64_t acc[9] = {0, 0, 0, 0, 0, 0, 0, 0, -1};
@@ -895,6 +897,143 @@ __global__ __launch_bounds__(kBig) void chunk_scan_kernel(const uint32_t* __rest
   }
 }
 
+// The window of gs_bin's compact list (gs_window_t): slots L-512..L-1 of the reference's
+// L = max(256 n, 512)-slot arrays, laid out as gs_bin_reference writes them (negative-depth
+// Gaussians' runs, the entries, the other Gaussians' empty slots in (dq, id) order,
+// padding).  A chunk of the default path reads them only when the binning's stats set
+// GS_STAT_WINDOW_CLAMPED, which needs fewer than 511 empty slots in all: then at most 510
+// Gaussians have any, and the window's negative-depth runs are those of the last two
+// negative-depth Gaussians in (dq, id) order.  One workgroup rebuilds them from the inputs.
+
+// the larger two of (a0 >= a1) and (b0 >= b1), keys offset by one (0: none)
+__device__ inline void top2_merge(uint64_t& a0, uint64_t& a1, uint64_t b0, uint64_t b1) {
+  const uint64_t hi = a0 > b0 ? a0 : b0, lo = a0 > b0 ? b0 : a0;
+  const uint64_t r1 = a1 > b1 ? a1 : b1;
+  a0 = hi;
+  a1 = lo > r1 ? lo : r1;
+}
+
+// The window, with the NT threads of one workgroup (every thread calls it): thr always, the
+// ids when the stats say a chunk is clamped.
+template <int NT>
+__device__ void window_build(int64_t n, const float* __restrict__ means2d, const float* __restrict__ radii,
+                             const uint8_t* __restrict__ valid, const float* __restrict__ depths, int W, int H,
+                             const int32_t* __restrict__ gids, int64_t capacity, const int32_t* __restrict__ stats,
+                             gs_window_t* __restrict__ win) {
+  __shared__ uint64_t key[kBlock];
+  __shared__ uint32_t cnt[kBlock], pre[kBlock];
+  __shared__ uint64_t top_s[2 * (NT / 64)];
+  __shared__ int n_tail;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t L = 256 * n > kBlock ? 256 * n : kBlock, lo = L - kBlock;
+  const int64_t n_neg = stats[GS_STAT_NEGATIVE_DEPTH], m = stats[GS_STAT_TILE_ENTRIES];
+  if (tid == 0) win->thr = lo - 256 * n_neg;
+  if (tid < 2) win->reserved[tid] = 0;
+  if (stats[GS_STAT_WINDOW_CLAMPED] == 0) return;  // no chunk reads the ids
+  if (tid == 0) n_tail = 0;
+  __syncthreads();
+  // Gaussians with empty slots (non-negative depth), and the top two negative-depth ones
+  uint64_t t0 = 0, t1 = 0;
+  for (int64_t i = tid; i < n; i += NT) {
+    const uint32_t zb = float_to_bits(depths[i]);
+    const uint64_t k = ((uint64_t)depth_key(zb) << 32) | (uint64_t)i;
+    if (zb >> 31) {
+      top2_merge(t0, t1, k + 1, 0);
+    } else {
+      const TileRect t = tile_rect(means2d[2 * i], means2d[2 * i + 1], radii[i], valid[i] != 0, W, H);
+      const uint32_t e = 256u - (uint32_t)t.count();
+      if (e > 0) {
+        const int at = atomicAdd(&n_tail, 1);
+        if (at < kBlock) {
+          key[at] = k;
+          cnt[at] = e;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t b0 = __shfl_xor(t0, o, 64), b1 = __shfl_xor(t1, o, 64);
+    top2_merge(t0, t1, b0, b1);
+  }
+  if (lane == 0) {
+    top_s[2 * wid] = t0;
+    top_s[2 * wid + 1] = t1;
+  }
+  __syncthreads();
+  const int nt = n_tail < kBlock ? n_tail : kBlock;
+  for (int i = tid; i < kBlock; i += NT)
+    if (i >= nt) {
+      key[i] = ~0ull;
+      cnt[i] = 0;
+    }
+  __syncthreads();
+  // bitonic sort of the (dq, id) keys, ascending
+  for (int k = 2; k <= kBlock; k <<= 1)
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < kBlock; i += NT) {  // pairs (i, i ^ j) are disjoint within a step
+        const int x = i ^ j;
+        if (x > i) {
+          const bool up = (i & k) == 0;
+          if ((key[i] > key[x]) == up) {
+            const uint64_t tk = key[i];
+            key[i] = key[x];
+            key[x] = tk;
+            const uint32_t tc = cnt[i];
+            cnt[i] = cnt[x];
+            cnt[x] = tc;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  if (tid == 0) {
+    uint32_t acc = 0;
+    for (int i = 0; i < kBlock; ++i) {
+      pre[i] = acc;
+      acc += cnt[i];
+    }
+    t0 = 0;
+    t1 = 0;
+    for (int w = 0; w < NT / 64; ++w) top2_merge(t0, t1, top_s[2 * w], top_s[2 * w + 1]);
+    top_s[0] = t0;
+    top_s[1] = t1;
+  }
+  __syncthreads();
+  for (int i = tid; i < kBlock; i += NT) {
+    const int64_t q = lo + i;
+    int32_t id = 0;
+    if (q < 256 * n_neg) {
+      // rank q / 256 of the n_neg runs; the last two are top_s[1], top_s[0]
+      const int64_t d = n_neg - 1 - q / 256;
+      const uint64_t k = d == 0 ? top_s[0] : (d == 1 ? top_s[1] : 0);
+      id = k ? (int32_t)(uint32_t)(k - 1) : 0;
+    } else if (q < 256 * n_neg + m) {
+      const int64_t e = q - 256 * n_neg;
+      id = e < capacity ? gids[e] : 0;
+    } else if (q < 256 * n) {
+      const uint32_t u = (uint32_t)(q - 256 * n_neg - m);
+      int a = 0, b = nt - 1;  // last sorted Gaussian whose run starts at or before u
+      while (a < b) {
+        const int c = (a + b + 1) >> 1;
+        if (pre[c] <= u) a = c; else b = c - 1;
+      }
+      id = nt > 0 ? (int32_t)(uint32_t)key[a] : 0;
+    }
+    win->ids[i] = id;
+  }
+}
+
+
+// gs_window_from_bins: the window on its own (one workgroup).
+constexpr int kWinThreads = 1024;
+__global__ __launch_bounds__(kWinThreads) void window_bins_kernel(
+    int64_t n, const float* __restrict__ means2d, const float* __restrict__ radii, const uint8_t* __restrict__ valid,
+    const float* __restrict__ depths, int W, int H, const int32_t* __restrict__ gids, int64_t capacity,
+    const int32_t* __restrict__ stats, gs_window_t* __restrict__ win) {
+  window_build<kWinThreads>(n, means2d, radii, valid, depths, W, H, gids, capacity, stats, win);
+}
+
 // 4d. write every entry: tile t's entries from chunk c start at ranges[t] plus the
 // counts of the superblock's earlier chunks; within a step the 64 tiles are visited
 // in an unrolled loop with wave-uniform masks (column & row ballots), and the lanes
@@ -967,11 +1106,27 @@ __device__ inline void write_chunk(const uint4& d, const uint64_t* __restrict__ 
                                     out_tile);
 }
 
+// The default path's chunk window of the list being written (NULL win: none), with the
+// binning's inputs its clamped form is rebuilt from.
+struct WinArgs {
+  gs_window_t* win;
+  const float* means2d;
+  const float* radii;
+  const uint8_t* valid;
+  const float* depths;
+  int W, H;
+  uint32_t* ticket;  // finished workgroups of the sweep (cleared by the tile scan)
+};
+
 // OFFSET: the entries go after the 256 slots of every negative-depth Gaussian (the
 // reference's full arrays): the outputs start at 256 * stats[GS_STAT_NEGATIVE_DEPTH],
 // which tile_scan_stats_kernel has written.
 // DEFER (gs_bin_deferred): nothing is written when entries_deferred holds; the compositing
 // forward then writes the entries it meets.
+// The window (wa.win): its threshold from workgroup 0 at the start; when a chunk is clamped
+// (never with a deferred list), its ids from the last workgroup to finish, once every entry
+// is written (each workgroup's entries made visible device-wide before it counts itself
+// finished), which saves the window its own launch.
 template <bool WITH_TILES, bool OFFSET, bool DEFER>
 __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restrict__ n_chunks, int64_t cmax,
                                                          const uint4* __restrict__ desc,
@@ -981,7 +1136,16 @@ __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restr
                                                          const int32_t* __restrict__ ranges, int T, int64_t cap,
                                                          int32_t* __restrict__ out_gid,
                                                          int32_t* __restrict__ out_tile,
-                                                         const int32_t* __restrict__ stats) {
+                                                         const int32_t* __restrict__ stats, const WinArgs wa) {
+  const int32_t* const gids_in = out_gid;  // the list as the window reads it (no offset)
+  const int64_t cap_in = cap;
+  bool clamped = false;
+  if constexpr (!OFFSET) {
+    clamped = wa.win != nullptr && stats[GS_STAT_WINDOW_CLAMPED] != 0;
+    if (wa.win != nullptr && !clamped && blockIdx.x == 0)  // the threshold only (no chunk reads ids)
+      window_build<256>(n_gauss, wa.means2d, wa.radii, wa.valid, wa.depths, wa.W, wa.H, gids_in, cap_in, stats,
+                        wa.win);
+  }
   if (DEFER && entries_deferred(stats)) return;
   const int lane = threadIdx.x & 63;
   const uint32_t nwaves = gridDim.x * (blockDim.x / 64);
@@ -1006,6 +1170,20 @@ __global__ __launch_bounds__(256) void tile_write_kernel(const uint32_t* __restr
       write_chunk<WITH_TILES, false>(d, pval, n_gauss, TX, TY, cnt_c, seg_pre, ranges, cap32, lane, out_gid, out_tile);
     else
       write_chunk<WITH_TILES, true>(d, pval, n_gauss, TX, TY, cnt_c, seg_pre, ranges, cap32, lane, out_gid, out_tile);
+  }
+  if constexpr (!OFFSET) {
+    if (clamped) {  // (uniform: every workgroup takes this branch or none)
+      __shared__ int last;
+      __threadfence();  // this thread's entries, visible device-wide
+      __syncthreads();
+      if (threadIdx.x == 0) last = atomicAdd(wa.ticket, 1u) == gridDim.x - 1;
+      __syncthreads();
+      if (last) {
+        __threadfence();  // and every other workgroup's, seen here
+        window_build<256>(n_gauss, wa.means2d, wa.radii, wa.valid, wa.depths, wa.W, wa.H, gids_in, cap_in, stats,
+                          wa.win);
+      }
+    }
   }
 }
 
@@ -1121,7 +1299,7 @@ namespace {
 int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, const uint8_t* valid,
             const float* depths, int width, int height, int64_t capacity, void* workspace, size_t workspace_bytes,
             int32_t* sorted_gids, int32_t* sorted_tiles, int32_t* ranges, int32_t* stats, bool ref_offset,
-            bool deferred = false) {
+            bool deferred = false, gs_window_t* window = nullptr) {
   GS_REQUIRE(n >= 0 && n <= ((int64_t)1 << 26), "gs_bin: n must be in [0, 2^26] (got %lld)", (long long)n);
   GS_REQUIRE(width > 0 && height > 0 && width <= 4096 * kTile && height <= 4096 * kTile,
              "gs_bin: bad image size %dx%d (each side at most 65536)", width, height);
@@ -1162,12 +1340,18 @@ int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, c
   uint32_t* n_chunks = scal + 1;
   uint32_t* n_segs = scal + 2;
   uint32_t* n_has = scal + 3;  // Gaussians that meet at least one tile
+  uint32_t* ticket = scal + 4;  // workgroups of the write sweep done (the window's last one builds it)
 
   if (n == 0) {
     hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, s, stats, (int64_t)GS_NUM_STATS, 0);
     GS_LAUNCH_CHECK("fill_i32_kernel");
     hipLaunchKernelGGL(fill_i32_kernel, dim3(div_up(P.T + 1, 256)), dim3(256), 0, s, ranges, (int64_t)P.T + 1, 0);
     GS_LAUNCH_CHECK("fill_i32_kernel");
+    if (window != nullptr) {
+      hipLaunchKernelGGL(window_bins_kernel, dim3(1), dim3(kWinThreads), 0, s, n, means2d, radii, valid, depths,
+                         width, height, sorted_gids, P.cap, stats, window);
+      GS_LAUNCH_CHECK("window_bins_kernel");
+    }
     return GS_OK;
   }
   // 1. prep (+ histogram of the first depth digit)
@@ -1223,14 +1407,15 @@ int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, c
   hipLaunchKernelGGL(chunk_scan_kernel, dim3(P.S), dim3(kBig), 0, s, gbase, P.gmax, P.SX, P.TX, P.TY, gsum, tot);
   GS_LAUNCH_CHECK("chunk_scan_kernel");
   hipLaunchKernelGGL(tile_scan_stats_kernel, dim3(1), dim3(kBig), 0, s, tot, P.T, blk, P.G_d, P.cap, n, ranges,
-                     stats, deferred);
+                     stats, deferred, ticket);
   GS_LAUNCH_CHECK("tile_scan_stats_kernel");
   // the deferred sweep usually exits at once: a smaller grid (its loop covers every chunk)
   const int write_blocks = deferred ? std::min(pass_blocks, 1024) : pass_blocks;
+  const WinArgs winargs{ref_offset ? nullptr : window, means2d, radii, valid, depths, width, height, ticket};
 #define GS_WRITE_LAUNCH(TILES, OFF, DEFER)                                                                      \
   hipLaunchKernelGGL((tile_write_kernel<TILES, OFF, DEFER>), dim3(write_blocks), dim3(256), 0, s, n_chunks, P.cmax, \
                      desc, sbval, (uint32_t)n, P.TX, P.TY, cnt, gsum, ranges, P.T, P.cap, sorted_gids, sorted_tiles, \
-                     stats)
+                     stats, winargs)
   if (ref_offset)
     GS_WRITE_LAUNCH(true, true, false);
   else if (sorted_tiles != nullptr)
@@ -1249,17 +1434,17 @@ int bin_run(void* stream, int64_t n, const float* means2d, const float* radii, c
 extern "C" int gs_bin(void* stream, int64_t n, const float* means2d, const float* radii, const uint8_t* valid,
                       const float* depths, int width, int height, int64_t capacity, void* workspace,
                       size_t workspace_bytes, int32_t* sorted_gids, int32_t* sorted_tiles, int32_t* ranges,
-                      int32_t* stats) {
+                      int32_t* stats, gs_window_t* window) {
   return bin_run(stream, n, means2d, radii, valid, depths, width, height, capacity, workspace, workspace_bytes,
-                 sorted_gids, sorted_tiles, ranges, stats, false);
+                 sorted_gids, sorted_tiles, ranges, stats, false, false, window);
 }
 
 extern "C" int gs_bin_deferred(void* stream, int64_t n, const float* means2d, const float* radii,
                                const uint8_t* valid, const float* depths, int width, int height, int64_t capacity,
                                void* workspace, size_t workspace_bytes, int32_t* sorted_gids, int32_t* ranges,
-                               int32_t* stats) {
+                               int32_t* stats, gs_window_t* window) {
   return bin_run(stream, n, means2d, radii, valid, depths, width, height, capacity, workspace, workspace_bytes,
-                 sorted_gids, nullptr, ranges, stats, false, true);
+                 sorted_gids, nullptr, ranges, stats, false, true, window);
 }
 
 namespace gs {
@@ -1363,7 +1548,7 @@ extern "C" int gs_bin_static(void* stream, int64_t n, const float* means2d, cons
   const int rc = scratch_on_current_device(&ws);
   if (rc != GS_OK) return rc;
   return gs_bin(stream, n, means2d, radii, valid, depths, width, height, capacity, ws,
-                (size_t)GS_BIN_STATIC_SCRATCH_BYTES, sorted_gids, sorted_tiles, ranges, stats);
+                (size_t)GS_BIN_STATIC_SCRATCH_BYTES, sorted_gids, sorted_tiles, ranges, stats, nullptr);
 }
 
 // ---------------------------------------------------------------------------------
@@ -1567,135 +1752,6 @@ extern "C" int gs_bin_reference(void* stream, int64_t n, const float* means2d, c
 }
 
 // ---------------------------------------------------------------------------------
-// The window of gs_bin's compact list (gs_window_t): slots L-512..L-1 of the reference's
-// L = max(256 n, 512)-slot arrays, laid out as gs_bin_reference writes them (negative-depth
-// Gaussians' runs, the entries, the other Gaussians' empty slots in (dq, id) order,
-// padding).  A chunk of the default path reads them only when the binning's stats set
-// GS_STAT_WINDOW_CLAMPED, which needs fewer than 511 empty slots in all: then at most 510
-// Gaussians have any, and the window's negative-depth runs are those of the last two
-// negative-depth Gaussians in (dq, id) order.  One workgroup rebuilds them from the inputs.
-namespace gs {
-namespace {
-constexpr int kWinThreads = 1024;
-
-// the larger two of (a0 >= a1) and (b0 >= b1), keys offset by one (0: none)
-__device__ inline void top2_merge(uint64_t& a0, uint64_t& a1, uint64_t b0, uint64_t b1) {
-  const uint64_t hi = a0 > b0 ? a0 : b0, lo = a0 > b0 ? b0 : a0;
-  const uint64_t r1 = a1 > b1 ? a1 : b1;
-  a0 = hi;
-  a1 = lo > r1 ? lo : r1;
-}
-
-__global__ __launch_bounds__(kWinThreads) void window_bins_kernel(
-    int64_t n, const float* __restrict__ means2d, const float* __restrict__ radii, const uint8_t* __restrict__ valid,
-    const float* __restrict__ depths, int W, int H, const int32_t* __restrict__ gids, int64_t capacity,
-    const int32_t* __restrict__ stats, gs_window_t* __restrict__ win) {
-  __shared__ uint64_t key[kBlock];
-  __shared__ uint32_t cnt[kBlock], pre[kBlock];
-  __shared__ uint64_t top_s[2 * (kWinThreads / 64)];
-  __shared__ int n_tail;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int64_t L = 256 * n > kBlock ? 256 * n : kBlock, lo = L - kBlock;
-  const int64_t n_neg = stats[GS_STAT_NEGATIVE_DEPTH], m = stats[GS_STAT_TILE_ENTRIES];
-  if (tid == 0) win->thr = lo - 256 * n_neg;
-  if (tid < 2) win->reserved[tid] = 0;
-  if (stats[GS_STAT_WINDOW_CLAMPED] == 0) return;  // no chunk reads the ids
-  if (tid == 0) n_tail = 0;
-  __syncthreads();
-  // Gaussians with empty slots (non-negative depth), and the top two negative-depth ones
-  uint64_t t0 = 0, t1 = 0;
-  for (int64_t i = tid; i < n; i += kWinThreads) {
-    const uint32_t zb = float_to_bits(depths[i]);
-    const uint64_t k = ((uint64_t)depth_key(zb) << 32) | (uint64_t)i;
-    if (zb >> 31) {
-      top2_merge(t0, t1, k + 1, 0);
-    } else {
-      const TileRect t = tile_rect(means2d[2 * i], means2d[2 * i + 1], radii[i], valid[i] != 0, W, H);
-      const uint32_t e = 256u - (uint32_t)t.count();
-      if (e > 0) {
-        const int at = atomicAdd(&n_tail, 1);
-        if (at < kBlock) {
-          key[at] = k;
-          cnt[at] = e;
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t b0 = __shfl_xor(t0, o, 64), b1 = __shfl_xor(t1, o, 64);
-    top2_merge(t0, t1, b0, b1);
-  }
-  if (lane == 0) {
-    top_s[2 * wid] = t0;
-    top_s[2 * wid + 1] = t1;
-  }
-  __syncthreads();
-  const int nt = n_tail < kBlock ? n_tail : kBlock;
-  for (int i = tid; i < kBlock; i += kWinThreads)
-    if (i >= nt) {
-      key[i] = ~0ull;
-      cnt[i] = 0;
-    }
-  __syncthreads();
-  // bitonic sort of the (dq, id) keys, ascending
-  for (int k = 2; k <= kBlock; k <<= 1)
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      if (tid < kBlock) {
-        const int x = tid ^ j;
-        if (x > tid) {
-          const bool up = (tid & k) == 0;
-          if ((key[tid] > key[x]) == up) {
-            const uint64_t tk = key[tid];
-            key[tid] = key[x];
-            key[x] = tk;
-            const uint32_t tc = cnt[tid];
-            cnt[tid] = cnt[x];
-            cnt[x] = tc;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  if (tid == 0) {
-    uint32_t acc = 0;
-    for (int i = 0; i < kBlock; ++i) {
-      pre[i] = acc;
-      acc += cnt[i];
-    }
-    t0 = 0;
-    t1 = 0;
-    for (int w = 0; w < kWinThreads / 64; ++w) top2_merge(t0, t1, top_s[2 * w], top_s[2 * w + 1]);
-    top_s[0] = t0;
-    top_s[1] = t1;
-  }
-  __syncthreads();
-  if (tid < kBlock) {
-    const int64_t q = lo + tid;
-    int32_t id = 0;
-    if (q < 256 * n_neg) {
-      // rank q / 256 of the n_neg runs; the last two are top_s[1], top_s[0]
-      const int64_t d = n_neg - 1 - q / 256;
-      const uint64_t k = d == 0 ? top_s[0] : (d == 1 ? top_s[1] : 0);
-      id = k ? (int32_t)(uint32_t)(k - 1) : 0;
-    } else if (q < 256 * n_neg + m) {
-      const int64_t e = q - 256 * n_neg;
-      id = e < capacity ? gids[e] : 0;
-    } else if (q < 256 * n) {
-      const uint32_t u = (uint32_t)(q - 256 * n_neg - m);
-      int a = 0, b = nt - 1;  // last sorted Gaussian whose run starts at or before u
-      while (a < b) {
-        const int c = (a + b + 1) >> 1;
-        if (pre[c] <= u) a = c; else b = c - 1;
-      }
-      id = nt > 0 ? (int32_t)(uint32_t)key[a] : 0;
-    }
-    win->ids[tid] = id;
-  }
-}
-}  // namespace
-}  // namespace gs
-
 extern "C" int gs_window_from_bins(void* stream, int64_t n, const float* means2d, const float* radii,
                                    const uint8_t* valid, const float* depths, int width, int height,
                                    const int32_t* sorted_gids, int64_t capacity, const int32_t* stats,

@@ -37,8 +37,8 @@ _SIGS = {
     "gs_composite_prep": [_P, _I64, _P, _P, _P, _P, _P],
     "gs_bin_workspace_size": [_I64, _I, _I, _I64],
     "gs_bin_deferred_workspace_size": [_I64, _I, _I, _I64],
-    "gs_bin": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _SZ, _P, _P, _P, _P],
-    "gs_bin_deferred": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _SZ, _P, _P, _P],
+    "gs_bin": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _SZ, _P, _P, _P, _P, _P],
+    "gs_bin_deferred": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _SZ, _P, _P, _P, _P],
     "gs_bin_static": [_P, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _P, _P, _P],
     "gs_bin_reference_workspace_size": [_I64, _I, _I],
     "gs_bin_reference": [_P, _I64, _P, _P, _P, _P, _I, _I, _P, _SZ, _P, _P, _P, _P],
@@ -92,7 +92,7 @@ _RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_
 _lib = None
 
 
-ABI_VERSION = 12  # gs_abi_version() of the signatures bound below
+ABI_VERSION = 13  # gs_abi_version() of the signatures bound below
 
 
 class NativeLibraryMissing(RuntimeError):

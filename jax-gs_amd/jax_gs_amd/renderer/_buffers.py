@@ -24,7 +24,14 @@ def as_mask(mask, n: int, device) -> torch.Tensor | None:
     m = torch.as_tensor(mask, device=device)
     if tuple(m.shape) != (n,):
         raise ValueError(f"mask has shape {tuple(m.shape)}, expected ({n},)")
-    return m.to(torch.uint8).contiguous()
+    return as_bytes(m)
+
+
+def as_bytes(m: torch.Tensor) -> torch.Tensor:
+    """A 0/1 byte view of a bool tensor (no cast kernel: torch stores bools as bytes), else
+    the tensor cast to uint8; contiguous."""
+    m = m.contiguous()
+    return m.view(torch.uint8) if m.dtype == torch.bool else m.to(torch.uint8)
 
 
 _BLACK: dict = {}

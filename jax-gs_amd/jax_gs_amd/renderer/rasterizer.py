@@ -9,7 +9,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from ._buffers import background_tensor, check_f32, num_tiles
+from ._buffers import as_bytes, background_tensor, check_f32, num_tiles
 
 TILE_SIZE = 16  # rasterizer.py:6
 OFFSET_SIZE = 16  # rasterizer.py:7
@@ -65,7 +65,8 @@ def bin_gaussians(means2d: torch.Tensor, radii: torch.Tensor, valid: torch.Tenso
                   deferred: bool = False) -> BinResult:
     """gs_bin: the entries in the reference's (tile, depth quantum, id) order, compact.
     window=True also builds the default path's chunk window of that list (the reference's
-    rasterizer.py:184-190 clamp, gs_window_from_bins).  deferred=True (gs_bin_deferred, no
+    rasterizer.py:184-190 clamp; the binning's last launch writes it, as gs_window_from_bins
+    would).  deferred=True (gs_bin_deferred, no
     sorted_tiles) leaves the entry list to composite(..., bins=result), which writes the
     entries its walk meets: the part gs_composite_bwd reads."""
     if deferred and want_tiles:
@@ -85,19 +86,15 @@ def bin_gaussians(means2d: torch.Tensor, radii: torch.Tensor, valid: torch.Tenso
     tiles = torch.empty((cap,), dtype=torch.int32, device=dev) if want_tiles else None
     ranges = torch.empty((T + 1,), dtype=torch.int32, device=dev)
     stats = torch.empty((_lib.GS_NUM_STATS,), dtype=torch.int32, device=dev)
+    win = new_window(dev) if window else None  # built by the binning's last launch
     if deferred:
         _lib.call("gs_bin_deferred", _lib.stream_handle(dev), n, _lib.ptr(means2d), _lib.ptr(radii), _lib.ptr(v),
                   _lib.ptr(depths), int(W), int(H), cap, _lib.ptr(ws), ws_bytes, _lib.ptr(gids), _lib.ptr(ranges),
-                  _lib.ptr(stats))
+                  _lib.ptr(stats), _lib.ptr(win))
     else:
         _lib.call("gs_bin", _lib.stream_handle(dev), n, _lib.ptr(means2d), _lib.ptr(radii), _lib.ptr(v),
                   _lib.ptr(depths), int(W), int(H), cap, _lib.ptr(ws), ws_bytes, _lib.ptr(gids), _lib.ptr(tiles),
-                  _lib.ptr(ranges), _lib.ptr(stats))
-    win = None
-    if window:
-        win = new_window(dev)
-        _lib.call("gs_window_from_bins", _lib.stream_handle(dev), n, _lib.ptr(means2d), _lib.ptr(radii), _lib.ptr(v),
-                  _lib.ptr(depths), int(W), int(H), _lib.ptr(gids), cap, _lib.ptr(stats), _lib.ptr(win))
+                  _lib.ptr(ranges), _lib.ptr(stats), _lib.ptr(win))
     return BinResult(sorted_gids=gids, sorted_tiles=tiles, ranges=ranges, stats=stats,
                      n_interactions=stats[_lib.STAT["n_interactions"]], capacity=cap, num_tiles=T, window=win,
                      deferred=deferred, workspace=ws if deferred else None, n=n)
@@ -117,7 +114,7 @@ def get_tile_interactions(means2D, radii, valid_mask, depths, H, W, tile_size: i
     m2 = check_f32("means2D", means2D, (n, 2), dev)
     r = check_f32("radii", torch.as_tensor(radii, device=dev).to(torch.float32), (n,), dev)
     z = check_f32("depths", depths, (n,), dev)
-    v = torch.as_tensor(valid_mask, device=dev).to(torch.uint8).contiguous()
+    v = as_bytes(torch.as_tensor(valid_mask, device=dev))
     L = max(256 * n, BLOCK_SIZE)
     _, _, T = num_tiles(W, H)
     nb = _lib.lib().gs_bin_reference_workspace_size(n, int(W), int(H))

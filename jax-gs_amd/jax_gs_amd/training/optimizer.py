@@ -17,6 +17,7 @@ import torch
 
 from .. import _lib
 from ..core.gaussians import Gaussians
+from ..renderer._buffers import as_bytes
 
 FIELDS = ("means", "scales", "quaternions", "opacities", "sh_coeffs")
 LearningRate = Union[float, Callable[[int], float]]
@@ -78,7 +79,7 @@ class Adam:
             arrays.append((p, g, m, v, p.numel(), p.numel() // max(n, 1), self.lr_at(f, state.count)))
         act = None
         if active_mask is not None:
-            act = torch.as_tensor(active_mask, device=dev).to(torch.uint8).contiguous()
+            act = as_bytes(torch.as_tensor(active_mask, device=dev))
             if act.numel() != n:
                 raise ValueError(f"Adam: active_mask has {act.numel()} entries for {n} Gaussians")
         k = len(arrays)

@@ -17,6 +17,7 @@ import torch
 from .. import _lib
 from ..core.camera import Camera
 from ..core.gaussians import Gaussians
+from ..renderer._buffers import as_bytes
 
 
 def accumulate_from_extras(state: dict, grad_means: torch.Tensor, means: torch.Tensor, camera, extras: dict,
@@ -27,8 +28,8 @@ def accumulate_from_extras(state: dict, grad_means: torch.Tensor, means: torch.T
     focal = float(np.float32((camera.fx + camera.fy) / 2.0))
     pixel_scale = float(np.float32(float(camera.W) * float(camera.H) * 3.0))
     w2c = torch.as_tensor(camera.W2C, dtype=torch.float32, device=dev).contiguous()
-    valid = extras["valid_mask"].to(torch.uint8).contiguous()
-    act = None if active is None else torch.as_tensor(active, device=dev).to(torch.uint8).contiguous()
+    valid = as_bytes(extras["valid_mask"])
+    act = None if active is None else as_bytes(torch.as_tensor(active, device=dev))
     radii = extras["radii"].contiguous()
     for k, dt in (("grad_accum", torch.float32), ("denom", torch.int32), ("max_radii", torch.float32)):
         t = state[k]

@@ -32,7 +32,7 @@ def test_binding_covers_every_declared_symbol():
 
 def test_abi_version_and_workspace_query_without_gpu():
     L = _lib.lib()
-    assert L.gs_abi_version() == _lib.ABI_VERSION == 12
+    assert L.gs_abi_version() == _lib.ABI_VERSION == 13
     # size query: pure host arithmetic, grows with the number of Gaussians
     a = L.gs_bin_workspace_size(1000, 64, 64, 0)
     b = L.gs_bin_workspace_size(100000, 64, 64, 0)
@@ -45,7 +45,7 @@ def test_argument_errors_are_reported_without_launching():
     rc = L.gs_preprocess_fwd(None, 10, 4, 3, *([None] * 7), 64, 64, 1.0, 1.0, 0.0, 0.0, *([None] * 7))
     assert rc == 1
     assert b"sh_coeffs has 4 coefficients" in L.gs_last_error()
-    rc = L.gs_bin(None, 10, None, None, None, None, 64, 64, 0, None, 0, None, None, None, None)
+    rc = L.gs_bin(None, 10, None, None, None, None, 64, 64, 0, None, 0, None, None, None, None, None)
     assert rc == 1
     assert b"workspace" in L.gs_last_error()
 
@@ -87,7 +87,7 @@ def test_argument_errors_of_the_deferred_binning():
     binning workspace (the superblock lists are found in it) before launching anything."""
     L = _lib.lib()
     fake = ctypes.c_void_p(256)
-    assert L.gs_bin_deferred(None, 10, *([None] * 4), 64, 64, 1000, None, 0, None, None, None) == 1
+    assert L.gs_bin_deferred(None, 10, *([None] * 4), 64, 64, 1000, None, 0, None, None, None, None) == 1
     assert b"workspace" in L.gs_last_error()
     args = (fake, 1000, fake, fake)  # sorted_gids, capacity, ranges, stats
     rc = L.gs_composite_fwd_deferred(None, 10, fake, fake, 0, fake, fake, fake, 1 << 20, 64, 64, *([fake] * 2),

@@ -42,7 +42,7 @@ def _bin(pre, W, H, cuda, static):
     else:
         nb = _lib.lib().gs_bin_workspace_size(n, W, H, cap)
         ws = torch.empty((nb,), dtype=torch.uint8, device=cuda)
-        _lib.call("gs_bin", s, *args, _lib.ptr(ws), nb, *[_lib.ptr(o) for o in out])
+        _lib.call("gs_bin", s, *args, _lib.ptr(ws), nb, *[_lib.ptr(o) for o in out], None)
     torch.cuda.synchronize()
     return [o.cpu().numpy() for o in out]
 
