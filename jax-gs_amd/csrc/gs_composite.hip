@@ -838,7 +838,7 @@ __device__ __forceinline__ void composite_bwd_body(
         // per-lane sums over the lane's pixels: P = sum dpower, Q = sum dpower*dy,
         // V = sum dpower*dy^2, colour cotangents (from -0, so that the first term is
         // the sum itself)
-        float P = -0.0f, Q = -0.0f, V = -0.0f, gc0 = -0.0f, gc1 = -0.0f, gc2 = -0.0f;
+        float P = -0.0f, Q = -0.0f, V = -0.0f, M1 = -0.0f, M2 = -0.0f, gc0 = -0.0f, gc1 = -0.0f, gc2 = -0.0f;
         if (live) {
         float dyv[PPT], qv[PPT];
 #pragma unroll
@@ -872,7 +872,6 @@ __device__ __forceinline__ void composite_bwd_body(
           // keep their values, the sums get +0): its sums need no clearing per entry.
 #pragma unroll
           for (int i = 0; i < PPT; ++i) {
-            const float dy = dyv[i];
             const bool blends = k < kp[i] && qv[i] > e.thr;
             if (i == 0 || blends) {
               any = any || blends;
@@ -885,17 +884,26 @@ __device__ __forceinline__ void composite_bwd_body(
               gc0 = fmaf(w, g0[i], gc0);
               gc1 = fmaf(w, g1[i], gc1);
               gc2 = fmaf(w, g2[i], gc2);
-              const float cg = fmaf(e.b, g2[i], fmaf(e.g, g1[i], e.r * g0[i]));
-              const float dR = cg - Rg[i];
+              // c.g - Rg in one fma chain started from -Rg
+              const float dR = fmaf(e.b, g2[i], fmaf(e.g, g1[i], fmaf(e.r, g0[i], -Rg[i])));
               const float dpw = w * dR;  // (alpha T) dR
               wdv[i] = dpw;
               Rg[i] = fmaf(al, dR, Rg[i]);
               Tr[i] = iTk;
+              // row moments: the lane's pixel i lies 4 i rows below its pixel 0, so
+              // dy_i = dy_0 + 4 i, and sum dpw dy, sum dpw dy^2 follow from P and
+              // M1 = sum 4 i dpw, M2 = sum 16 i^2 dpw after the rows (pixel 0 adds to P only)
               P += dpw;
-              const float dpy = dpw * dy;
-              Q += dpy;
-              V = fmaf(dpy, dy, V);
+              if (i > 0) {
+                M1 = fmaf(4.0f * i, dpw, M1);
+                M2 = fmaf(16.0f * i * i, dpw, M2);
+              }
             }
+          }
+          {
+            const float dy0 = dyv[0];
+            Q = fmaf(dy0, P, M1);
+            V = fmaf(dy0, Q + M1, M2);  // dy0^2 P + 2 dy0 M1 + M2
           }
           if (capw) {
             P = -0.0f;
@@ -932,8 +940,7 @@ __device__ __forceinline__ void composite_bwd_body(
             gc0 = fmaf(w, g0[i], gc0);
             gc1 = fmaf(w, g1[i], gc1);
             gc2 = fmaf(w, g2[i], gc2);
-            const float cg = fmaf(e.b, g2[i], fmaf(e.g, g1[i], e.r * g0[i]));
-            const float dR = cg - Rg[i];
+            const float dR = fmaf(e.b, g2[i], fmaf(e.g, g1[i], fmaf(e.r, g0[i], -Rg[i])));  // c.g - Rg
             // dL/dalpha = T dR; d alpha/d power = araw below the cap, where alpha = araw,
             // so dL/dpower = (alpha T) dR = w dR (one product instead of two)
             const float wd = w * dR;
