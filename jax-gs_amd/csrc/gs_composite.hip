@@ -838,7 +838,7 @@ __device__ __forceinline__ void composite_bwd_body(
         // per-lane sums over the lane's pixels: P = sum dpower, Q = sum dpower*dy,
         // V = sum dpower*dy^2, colour cotangents (from -0, so that the first term is
         // the sum itself)
-        float P = -0.0f, Q = -0.0f, V = -0.0f, M1 = -0.0f, M2 = -0.0f, gc0 = -0.0f, gc1 = -0.0f, gc2 = -0.0f;
+        float P = -0.0f, Q = -0.0f, V = -0.0f, gc0 = -0.0f, gc1 = -0.0f, gc2 = -0.0f;
         if (live) {
         float dyv[PPT], qv[PPT];
 #pragma unroll
@@ -890,20 +890,11 @@ __device__ __forceinline__ void composite_bwd_body(
               wdv[i] = dpw;
               Rg[i] = fmaf(al, dR, Rg[i]);
               Tr[i] = iTk;
-              // row moments: the lane's pixel i lies 4 i rows below its pixel 0, so
-              // dy_i = dy_0 + 4 i, and sum dpw dy, sum dpw dy^2 follow from P and
-              // M1 = sum 4 i dpw, M2 = sum 16 i^2 dpw after the rows (pixel 0 adds to P only)
               P += dpw;
-              if (i > 0) {
-                M1 = fmaf(4.0f * i, dpw, M1);
-                M2 = fmaf(16.0f * i * i, dpw, M2);
-              }
+              const float dpy = dpw * dyv[i];
+              Q += dpy;
+              V = fmaf(dpy, dyv[i], V);
             }
-          }
-          {
-            const float dy0 = dyv[0];
-            Q = fmaf(dy0, P, M1);
-            V = fmaf(dy0, Q + M1, M2);  // dy0^2 P + 2 dy0 M1 + M2
           }
           if (capw) {
             P = -0.0f;
