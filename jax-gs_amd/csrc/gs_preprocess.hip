@@ -710,8 +710,10 @@ __device__ inline void zero_block(float* __restrict__ p, int64_t begin, int64_t 
   while (a < end && ((reinterpret_cast<uintptr_t>(p + a) & 15) != 0)) ++a;  // <= 3 floats
   const int64_t nv = (end - a) / 4;
   if (t < a - begin) p[begin + t] = 0.0f;
-  float4* __restrict__ v = reinterpret_cast<float4*>(p + a);
-  for (int64_t j = t; j < nv; j += NT) v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  f4v* __restrict__ v = reinterpret_cast<f4v*>(p + a);
+  const f4v z = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t j = t; j < nv; j += NT) __builtin_nontemporal_store(z, v + j);
   const int64_t tail = a + 4 * nv;
   if (t < end - tail) p[tail + t] = 0.0f;
 }
