@@ -10,6 +10,7 @@ Prints ONE JSON line (rank 0, N=1 only: this build runs on a single GPU).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -143,16 +144,19 @@ def main():
                                                               bg, clear_records=grec, window=b["window"], bins=b,
                                                               l1_target=tgt)
             mark("t3")
+            # as in the step: the compositing VJP zeroes the five gradient arrays on the side
+            # and the preprocessing VJP writes only the reached Gaussians' rows
+            outs = [torch.empty_like(getattr(g, f)) for f in fields]
+            cl = _lib.clear_list(*outs)
             _lib.call("gs_composite_bwd_l1", s_, N, _lib.ptr(pre["records"]), _lib.ptr(b["sorted_gids"]),
                       b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), W, H, _lib.ptr(bg), None, _lib.ptr(image),
                       _lib.ptr(tgt), _lib.ptr(one), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec),
-                      None, 1, _lib.ptr(b["window"]))
+                      None, 1, _lib.ptr(b["window"]), ctypes.byref(cl))
             mark("t4")
-            outs = [torch.empty_like(getattr(g, f)) for f in fields]
             _lib.call("gs_preprocess_bwd", s_, N, g.sh_coeffs.shape[1], D, *[_lib.ptr(getattr(g, f).detach())
                                                                              for f in fields],
                       _lib.ptr(cam.W2C.contiguous()), W, H, float(cam.fx), float(cam.fy), float(cam.cx),
-                      float(cam.cy), _lib.ptr(grec), *[_lib.ptr(o) for o in outs])
+                      float(cam.cy), _lib.ptr(grec), *[_lib.ptr(o) for o in outs], 1)
             mark("t5")
             accumulate_from_extras(stats_state, outs[0], g.means.detach(), cam,
                                    {"valid_mask": pre["valid"], "radii": pre["radii"]}, active=mask)

@@ -87,7 +87,9 @@ const char* gs_last_error(void);
  * gs_project_bwd.  11: gs_bin_deferred, gs_composite_fwd_deferred.  12: the L1 loss fused
  * into compositing: gs_composite_l1_out_size, gs_composite_fwd_deferred_l1,
  * gs_composite_bwd_l1.  13: gs_bin and gs_bin_deferred take the chunk window (the binning
- * builds it; gs_window_from_bins stays for lists binned without it). */
+ * builds it; gs_window_from_bins stays for lists binned without it).  14: gs_composite_bwd
+ * and gs_composite_bwd_l1 take a gs_clear_list_t; gs_preprocess_bwd and
+ * gs_preprocess_bwd_w2c take zeroed. */
 int gs_abi_version(void);
 
 /* Projection + covariance + SH colour for every Gaussian.
@@ -127,6 +129,17 @@ typedef struct {
   int32_t reserved[2];
   int32_t ids[512];
 } gs_window_t;
+
+/* Float arrays a compositing backward launch sets to zero on the side, while its
+ * arithmetic-bound waves run (16-byte non-temporal stores): up to GS_CLEAR_MAX arrays,
+ * ptr[i] with count[i] floats; entries with a NULL ptr or a count of 0 are skipped.  The
+ * five gradient arrays of a later gs_preprocess_bwd(..., zeroed = 1) are the intended use:
+ * the VJP then writes only the rows of the Gaussians some pixel reached. */
+#define GS_CLEAR_MAX 8
+typedef struct {
+  float* ptr[GS_CLEAR_MAX];
+  int64_t count[GS_CLEAR_MAX];
+} gs_clear_list_t;
 
 /* Workspace bytes gs_bin needs for n Gaussians, a width x height image and an
  * interaction capacity (capacity <= 0 means the static bound 256*n). */
@@ -289,12 +302,13 @@ int gs_composite_fwd_deferred_l1(void* stream, int64_t n, const float* records, 
  * record (layout above): overwritten when accumulate = 0, added to what it holds when
  * accumulate = 1 (records cleared by gs_composite_fwd's clear_records, or gradients of
  * several views summed in one buffer); grad_background[3] (may be NULL) is overwritten
- * with dL/d(background).  window: the forward's (entry ids read by the same rule). */
+ * with dL/d(background).  window: the forward's (entry ids read by the same rule).
+ * clear (host pointer, may be NULL): arrays the launch sets to zero (gs_clear_list_t). */
 int gs_composite_bwd(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
                      int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
                      const float* grad_image, const float* final_T, const int32_t* n_contrib,
                      const int32_t* tile_order, float* grad_records, float* grad_background, int accumulate,
-                     const gs_window_t* window);
+                     const gs_window_t* window, const gs_clear_list_t* clear);
 
 /* gs_composite_bwd of a render whose L1 loss was fused (gs_composite_fwd_deferred_l1): the
  * image cotangent of each pixel is sign(image - l1_target) * l1_cot[0] / (3 H W) (the VJP of
@@ -304,19 +318,23 @@ int gs_composite_bwd_l1(void* stream, int64_t n, const float* records, const int
                         int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
                         const float* grad_image, const float* image, const float* l1_target, const float* l1_cot,
                         const float* final_T, const int32_t* n_contrib, const int32_t* tile_order,
-                        float* grad_records, float* grad_background, int accumulate, const gs_window_t* window);
+                        float* grad_records, float* grad_background, int accumulate, const gs_window_t* window,
+                        const gs_clear_list_t* clear);
 
 /* Vector-Jacobian product of gs_preprocess_fwd's compositing records with respect to
  * the five Gaussian parameter arrays (JAX autodiff of project_gaussians, eval_sh,
  * get_covariance_3d and the conic/sigmoid prologue).  Outputs are overwritten:
  * grad_means[N,3] grad_scales[N,3] grad_quats[N,4] grad_opacities[N,1]
- * grad_sh[N,K,3] (coefficients >= (sh_degree+1)^2 get 0). */
+ * grad_sh[N,K,3] (coefficients >= (sh_degree+1)^2 get 0).  A Gaussian whose gradient
+ * record is all zero (no pixel reached it) has zero cotangents; zeroed = 1 promises that
+ * the five arrays hold zeros on entry (gs_composite_bwd's clear list), and only the rows
+ * of the other Gaussians are written; zeroed = 0 writes every row. */
 int gs_preprocess_bwd(void* stream, int64_t n, int sh_k, int sh_degree, const float* means,
                       const float* scales, const float* quats, const float* opacities,
                       const float* sh_coeffs, const float* w2c, int width, int height,
                       float fx, float fy, float cx, float cy, const float* grad_records,
                       float* grad_means, float* grad_scales, float* grad_quats,
-                      float* grad_opacities, float* grad_sh);
+                      float* grad_opacities, float* grad_sh, int zeroed);
 
 /* Workspace bytes gs_preprocess_bwd_w2c needs (16 floats per 64 Gaussians). */
 size_t gs_preprocess_bwd_w2c_workspace_size(int64_t n);
@@ -332,7 +350,7 @@ int gs_preprocess_bwd_w2c(void* stream, int64_t n, int sh_k, int sh_degree, cons
                           float fx, float fy, float cx, float cy, const float* grad_records,
                           float* grad_means, float* grad_scales, float* grad_quats,
                           float* grad_opacities, float* grad_sh, float* grad_w2c, void* workspace,
-                          size_t workspace_bytes);
+                          size_t workspace_bytes, int zeroed);
 
 /* Vector-Jacobian product of gs_composite_prep on its own (JAX autodiff of the prologue of
  * jax_gs/renderer/rasterizer.py:119-156, render_tiles: det clamp, inverse covariance,

@@ -27,4 +27,4 @@ int launch_check(const char* what) { return hip_check(hipGetLastError(), what); 
 }  // namespace gs
 
 extern "C" const char* gs_last_error(void) { return gs::g_err; }
-extern "C" int gs_abi_version(void) { return 13; }
+extern "C" int gs_abi_version(void) { return 14; }

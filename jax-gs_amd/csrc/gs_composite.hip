@@ -977,6 +977,38 @@ __device__ __forceinline__ void composite_bwd_body(
   }
 }
 
+// The arrays of a gs_clear_list_t, passed by value.  Workgroup b of nb zeroes its contiguous
+// share of each array's 16-byte-aligned body with non-temporal stores (the lines go to HBM while
+// the launch's waves compute, rather than staying dirty in the caches until a later kernel's
+// traffic evicts them); workgroup 0 also zeroes the up to three floats before and after it.
+struct ClearList {
+  float* p[GS_CLEAR_MAX];
+  int64_t n[GS_CLEAR_MAX];
+};
+
+__device__ inline void clear_list_share(const ClearList& cl, int b, int nb, int t) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+  for (int r = 0; r < GS_CLEAR_MAX; ++r) {
+    float* const p = cl.p[r];
+    const int64_t n = cl.n[r];
+    if (p == nullptr || n <= 0) continue;
+    const int64_t lead = (int64_t)((16u - (uint32_t)(reinterpret_cast<uintptr_t>(p) & 15u)) & 15u) / 4;
+    const int64_t head = lead < n ? lead : n;
+    const int64_t n4 = (n - head) / 4;
+    const int64_t per = (n4 + nb - 1) / nb;
+    const int64_t c0 = per * b, c1 = c0 + per < n4 ? c0 + per : n4;
+    f4v* const v = reinterpret_cast<f4v*>(p + head);
+    for (int64_t c = c0 + t; c < c1; c += 64) __builtin_nontemporal_store(z, v + c);
+    if (b == 0) {
+      const int64_t tail0 = head + 4 * n4;
+      if (t < head) p[t] = 0.0f;
+      if (t < n - tail0) p[tail0 + t] = 0.0f;
+    }
+  }
+}
+
 #define GS_BWD_PARAMS                                                                                       \
   const float4 *__restrict__ rec, int num_g, const int32_t *__restrict__ gids, int64_t n_entries,               \
       const int32_t *__restrict__ ranges, int W, int H, int TX, int T, const float *__restrict__ bg,            \
@@ -997,13 +1029,19 @@ __device__ __forceinline__ void composite_bwd_body(
 // is scheduled for 5 waves per SIMD (at 6, 80 VGPRs, it spilled): cfg2 285 -> 273 us and
 // cfg4 223 -> 214 against two entries at 6 waves per SIMD.  WIN: the default path's chunk
 // windows, as the forward read them.
+// Each workgroup zeroes its share of the clear list after its walk (stores issued before it
+// would hold up its first loads: loads and stores share one wait counter).
 template <int PPT, bool WIN, bool O32>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void composite_bwd_kernel(GS_BWD_PARAMS) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) void composite_bwd_kernel(GS_BWD_PARAMS,
+                                                                                                     const ClearList cl) {
   composite_bwd_body<PPT, WIN, false, O32>(GS_BWD_ARGS);
+  clear_list_share(cl, blockIdx.x, gridDim.x, threadIdx.x);
 }
 template <bool WIN, bool O32>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5, 5))) void composite_bwd_wide_kernel(GS_BWD_PARAMS) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5, 5))) void composite_bwd_wide_kernel(
+    GS_BWD_PARAMS, const ClearList cl) {
   composite_bwd_body<4, WIN, true, O32>(GS_BWD_ARGS);
+  clear_list_share(cl, blockIdx.x, gridDim.x, threadIdx.x);
 }
 #undef GS_BWD_PARAMS
 #undef GS_BWD_ARGS
@@ -1285,8 +1323,17 @@ int composite_bwd_run(const char* name, void* stream, int64_t n, const float* re
                       int64_t n_entries, const int32_t* ranges, int width, int height, const float* background,
                       const ImageCot& gc, const float* final_T, const int32_t* n_contrib,
                       const int32_t* tile_order, float* grad_records, float* grad_background, int accumulate,
-                      const gs_window_t* window) {
+                      const gs_window_t* window, const gs_clear_list_t* clear) {
   GS_REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "%s: n out of range", name);
+  ClearList cl{};
+  if (clear != nullptr) {
+    for (int r = 0; r < GS_CLEAR_MAX; ++r) {
+      GS_REQUIRE(clear->count[r] >= 0, "%s: clear list entry %d has a negative count", name, r);
+      GS_REQUIRE(clear->count[r] == 0 || clear->ptr[r] != nullptr, "%s: clear list entry %d is NULL", name, r);
+      cl.p[r] = clear->count[r] > 0 ? clear->ptr[r] : nullptr;
+      cl.n[r] = clear->count[r];
+    }
+  }
   GS_REQUIRE(n_entries >= 0, "%s: n_entries must be >= 0", name);
   GS_REQUIRE(width > 0 && height > 0, "%s: bad image size %dx%d", name, width, height);
   GS_REQUIRE(ranges && background && final_T && n_contrib, "%s: NULL argument", name);
@@ -1312,7 +1359,7 @@ int composite_bwd_run(const char* name, void* stream, int64_t n, const float* re
 #define GS_BWD_LAUNCH(KERNEL, WPT)                                                                                  \
   hipLaunchKernelGGL(KERNEL, dim3(nblk * (WPT)), dim3(64), 0, s, (const float4*)records, (int)n, sorted_gids, n_entries, \
                      ranges, width, height, TX, T, background, gc, final_T, n_contrib, grad_records,                   \
-                     tile_order, window)
+                     tile_order, window, cl)
   const bool win = window != nullptr, o32 = rec_offsets_fit(n);
   if (pick_ppt(T) == 4) {
     if (o32) {
@@ -1341,11 +1388,12 @@ extern "C" int gs_composite_bwd(void* stream, int64_t n, const float* records, c
                                 int64_t n_entries, const int32_t* ranges, int width, int height,
                                 const float* background, const float* grad_image, const float* final_T,
                                 const int32_t* n_contrib, const int32_t* tile_order, float* grad_records,
-                                float* grad_background, int accumulate, const gs_window_t* window) {
+                                float* grad_background, int accumulate, const gs_window_t* window,
+                                const gs_clear_list_t* clear) {
   const ImageCot gc{grad_image, nullptr, nullptr, nullptr};
   return composite_bwd_run("gs_composite_bwd", stream, n, records, sorted_gids, n_entries, ranges, width, height,
                            background, gc, final_T, n_contrib, tile_order, grad_records, grad_background, accumulate,
-                           window);
+                           window, clear);
 }
 
 extern "C" int gs_composite_bwd_l1(void* stream, int64_t n, const float* records, const int32_t* sorted_gids,
@@ -1353,11 +1401,12 @@ extern "C" int gs_composite_bwd_l1(void* stream, int64_t n, const float* records
                                    const float* background, const float* grad_image, const float* image,
                                    const float* l1_target, const float* l1_cot, const float* final_T,
                                    const int32_t* n_contrib, const int32_t* tile_order, float* grad_records,
-                                   float* grad_background, int accumulate, const gs_window_t* window) {
+                                   float* grad_background, int accumulate, const gs_window_t* window,
+                                   const gs_clear_list_t* clear) {
   GS_REQUIRE(image != nullptr && l1_target != nullptr && l1_cot != nullptr,
              "gs_composite_bwd_l1: NULL image, l1_target or l1_cot");
   const ImageCot gc{grad_image, image, l1_target, l1_cot};
   return composite_bwd_run("gs_composite_bwd_l1", stream, n, records, sorted_gids, n_entries, ranges, width,
                            height, background, gc, final_T, n_contrib, tile_order, grad_records, grad_background,
-                           accumulate, window);
+                           accumulate, window, clear);
 }

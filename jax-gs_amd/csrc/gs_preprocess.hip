@@ -740,7 +740,7 @@ __global__ __launch_bounds__(kBwdThreads) void preprocess_bwd_kernel(
     const float* __restrict__ quats, const float* __restrict__ opac, const float* __restrict__ sh,
     const float* __restrict__ w2c, float fx, float fy, const float* __restrict__ grec,
     float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_quats,
-    float* __restrict__ g_opac, float* __restrict__ g_sh, float* __restrict__ w2c_part) {
+    float* __restrict__ g_opac, float* __restrict__ g_sh, float* __restrict__ w2c_part, int zeroed) {
   constexpr int NB = (DEG + 1) * (DEG + 1);
   constexpr int PER = SPAN / kBwdThreads;
   constexpr int NW = kBwdThreads / 64;
@@ -786,18 +786,19 @@ __global__ __launch_bounds__(kBwdThreads) void preprocess_bwd_kernel(
 #pragma unroll
   for (int r = 0; r < PER; ++r)
     if (hit[r]) reached_s[at++] = (uint16_t)(t + kBwdThreads * r);
-  // the span's gradient rows are zeroed whole, with coalesced 16-byte stores (a row per thread
+  // unless the caller zeroed the arrays (zeroed: a compositing backward's clear list), the
+  // span's gradient rows are zeroed whole, with coalesced 16-byte stores (a row per thread
   // took one partial cache line per lane and store); the reached rows are overwritten below,
   // after every zero store has completed
-  {
+  if (!zeroed) {
     const int64_t g1 = g0 + SPAN < n ? g0 + SPAN : n;
     zero_block<kBwdThreads>(g_means, 3 * g0, 3 * g1, t);
     zero_block<kBwdThreads>(g_scales, 3 * g0, 3 * g1, t);
     zero_block<kBwdThreads>(g_quats, 4 * g0, 4 * g1, t);
     zero_block<kBwdThreads>(g_opac, g0, g1, t);
     zero_block<kBwdThreads>(g_sh, (int64_t)KC * g0, (int64_t)KC * g1, t);
+    __builtin_amdgcn_s_waitcnt(0);  // the zero stores performed before any wave writes a row
   }
-  __builtin_amdgcn_s_waitcnt(0);  // the zero stores performed before any wave writes a row
   __syncthreads();
   // 3. the reached Gaussians, one per thread
   float part[15];
@@ -1150,7 +1151,7 @@ int preprocess_bwd_launch(void* stream, int64_t n, int sh_k, int sh_degree, cons
                           const float* scales, const float* quats, const float* opacities, const float* sh_coeffs,
                           const float* w2c, float fx, float fy, const float* grad_records, float* grad_means,
                           float* grad_scales, float* grad_quats, float* grad_opacities, float* grad_sh,
-                          float* w2c_part, const char* who) {
+                          float* w2c_part, int zeroed, const char* who) {
   GS_REQUIRE(n >= 0, "%s: n must be >= 0", who);
   GS_REQUIRE(sh_degree >= 0 && sh_degree <= 3, "%s: sh_degree must be in 0..3 (got %d)", who, sh_degree);
   GS_REQUIRE(sh_k >= (sh_degree + 1) * (sh_degree + 1) && sh_k <= 16,
@@ -1167,11 +1168,13 @@ int preprocess_bwd_launch(void* stream, int64_t n, int sh_k, int sh_degree, cons
     if (part)                                                                                                    \
       hipLaunchKernelGGL((preprocess_bwd_kernel<D, true, SP>), dim3(div_up(n, SP)), dim3(kBwdThreads), 0,        \
                          (hipStream_t)stream, n, sh_k, means, scales, quats, opacities, sh_coeffs, w2c, fx, fy,   \
-                         grad_records, grad_means, grad_scales, grad_quats, grad_opacities, grad_sh, w2c_part);  \
+                         grad_records, grad_means, grad_scales, grad_quats, grad_opacities, grad_sh, w2c_part,   \
+                         zeroed);                                                                                \
     else                                                                                                         \
       hipLaunchKernelGGL((preprocess_bwd_kernel<D, false, SP>), dim3(div_up(n, SP)), dim3(kBwdThreads), 0,       \
                          (hipStream_t)stream, n, sh_k, means, scales, quats, opacities, sh_coeffs, w2c, fx, fy,   \
-                         grad_records, grad_means, grad_scales, grad_quats, grad_opacities, grad_sh, nullptr);   \
+                         grad_records, grad_means, grad_scales, grad_quats, grad_opacities, grad_sh, nullptr,    \
+                         zeroed);                                                                                \
   } while (0)
 #define GS_PRE_BWD(D) \
   if (span == 1024) GS_PRE_BWD2(D, 1024); else GS_PRE_BWD2(D, 256)
@@ -1194,14 +1197,14 @@ extern "C" int gs_preprocess_bwd(void* stream, int64_t n, int sh_k, int sh_degre
                                  const float* sh_coeffs, const float* w2c, int width, int height,
                                  float fx, float fy, float cx, float cy, const float* grad_records,
                                  float* grad_means, float* grad_scales, float* grad_quats,
-                                 float* grad_opacities, float* grad_sh) {
+                                 float* grad_opacities, float* grad_sh, int zeroed) {
   (void)width;
   (void)height;
   (void)cx;
   (void)cy;
   return preprocess_bwd_launch(stream, n, sh_k, sh_degree, means, scales, quats, opacities, sh_coeffs, w2c, fx, fy,
                                grad_records, grad_means, grad_scales, grad_quats, grad_opacities, grad_sh, nullptr,
-                               "gs_preprocess_bwd");
+                               zeroed, "gs_preprocess_bwd");
 }
 
 extern "C" size_t gs_preprocess_bwd_w2c_workspace_size(int64_t n) {
@@ -1213,7 +1216,7 @@ extern "C" int gs_preprocess_bwd_w2c(void* stream, int64_t n, int sh_k, int sh_d
                                      const float* sh_coeffs, const float* w2c, int width, int height, float fx,
                                      float fy, float cx, float cy, const float* grad_records, float* grad_means,
                                      float* grad_scales, float* grad_quats, float* grad_opacities, float* grad_sh,
-                                     float* grad_w2c, void* workspace, size_t workspace_bytes) {
+                                     float* grad_w2c, void* workspace, size_t workspace_bytes, int zeroed) {
   (void)width;
   (void)height;
   (void)cx;
@@ -1224,7 +1227,7 @@ extern "C" int gs_preprocess_bwd_w2c(void* stream, int64_t n, int sh_k, int sh_d
              gs_preprocess_bwd_w2c_workspace_size(n));
   const int rc = preprocess_bwd_launch(stream, n, sh_k, sh_degree, means, scales, quats, opacities, sh_coeffs, w2c,
                                        fx, fy, grad_records, grad_means, grad_scales, grad_quats, grad_opacities,
-                                       grad_sh, (float*)workspace, "gs_preprocess_bwd_w2c");
+                                       grad_sh, (float*)workspace, zeroed, "gs_preprocess_bwd_w2c");
   if (rc != GS_OK) return rc;
   hipLaunchKernelGGL(w2c_finish_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, (const float*)workspace,
                      n > 0 ? div_up(n, bwd_span(n)) : (int64_t)0, w2c, grad_w2c);

@@ -18,6 +18,25 @@ GS_OK = 0
 GS_REC_STRIDE = 12
 GS_NUM_STATS = 16
 GS_WINDOW_BYTES = 16 + 4 * 512  # sizeof(gs_window_t): int64 thr, 2 reserved int32, 512 ids
+GS_CLEAR_MAX = 8
+
+
+class ClearList(ctypes.Structure):
+    """gs_clear_list_t: float arrays a compositing backward launch sets to zero."""
+    _fields_ = [("ptr", ctypes.c_void_p * GS_CLEAR_MAX), ("count", ctypes.c_int64 * GS_CLEAR_MAX)]
+
+
+def clear_list(*tensors) -> ClearList:
+    """A gs_clear_list_t of contiguous float32 device tensors (kept alive by the caller)."""
+    if len(tensors) > GS_CLEAR_MAX:
+        raise ValueError(f"clear_list: at most {GS_CLEAR_MAX} arrays")
+    cl = ClearList()
+    for i, t in enumerate(tensors):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("clear_list: contiguous float32 tensors only")
+        cl.ptr[i] = t.data_ptr()
+        cl.count[i] = t.numel()
+    return cl
 STAT = dict(n_interactions=0, max_interactions_per_tile=1, overflow_tiles=2, overflow_interactions=3,
             truncated_tiles=4, truncated_interactions=5, radius_cap_violations=6, negative_depth=7,
             capacity_exceeded=8, mean_per_tile=9, tile_entries=10, window_clamped=11, entries_deferred=12)
@@ -47,15 +66,17 @@ _SIGS = {
     "gs_window_from_bins": [_P, _I64, _P, _P, _P, _P, _I, _I, _P, _I64, _P, _P],
     "gs_composite_fwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "gs_composite_fwd_deferred": [_P, _I64, _P, _P, _I64, _P, _P, _P, _SZ, _I, _I, _P, _P, _P, _P, _P, _P, _P],
-    "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P],
+    "gs_composite_bwd": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P],
     "gs_composite_l1_out_size": [_I, _I],
     "gs_composite_fwd_deferred_l1": [_P, _I64, _P, _P, _I64, _P, _P, _P, _SZ, _I, _I, _P, _P, _P, _P, _P, _P, _P,
                                      _P, _P],
-    "gs_composite_bwd_l1": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P],
-    "gs_preprocess_bwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P, _P],
+    "gs_composite_bwd_l1": [_P, _I64, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P,
+                            _P],
+    "gs_preprocess_bwd": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P, _P,
+                          _I],
     "gs_preprocess_bwd_w2c_workspace_size": [_I64],
     "gs_preprocess_bwd_w2c": [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P, _P, _P,
-                              _P, _P, _P, _SZ],
+                              _P, _P, _P, _SZ, _I],
     "gs_composite_prep_bwd": [_P, _I64, _P, _P, _P, _P, _P, _P, _P],
     "gs_project_bwd": [_P, _I64, _P, _P, _P, _P, _F, _F, _P, _P, _P, _P, _P, _P, _P, _P, _SZ],
     "gs_eval_sh": [_P, _I64, _I, _I, _P, _P, _P],
@@ -92,7 +113,7 @@ _RESTYPE = {"gs_last_error": ctypes.c_char_p, "gs_bin_workspace_size": _SZ, "gs_
 _lib = None
 
 
-ABI_VERSION = 13  # gs_abi_version() of the signatures bound below
+ABI_VERSION = 14  # gs_abi_version() of the signatures bound below
 
 
 class NativeLibraryMissing(RuntimeError):

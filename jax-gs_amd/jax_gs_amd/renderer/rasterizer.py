@@ -226,7 +226,7 @@ class _RenderTiles(torch.autograd.Function):
         gbg = torch.empty((3,), dtype=torch.float32, device=dev) if ctx.needs_input_grad[4] else None
         _lib.call("gs_composite_bwd", s, n, _lib.ptr(rec), _lib.ptr(gids), gids.shape[0], _lib.ptr(ranges), int(W),
                   int(H), _lib.ptr(bg), _lib.ptr(g_image), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order),
-                  _lib.ptr(grec), _lib.ptr(gbg), 0, _lib.ptr(win))
+                  _lib.ptr(grec), _lib.ptr(gbg), 0, _lib.ptr(win), None)
         gm = torch.empty((n, 2), dtype=torch.float32, device=dev)
         gc = torch.empty((n, 2, 2), dtype=torch.float32, device=dev)
         go = torch.empty((n, 1), dtype=torch.float32, device=dev)

@@ -21,6 +21,8 @@ it for the chunks past its threshold.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from .. import _lib
@@ -80,19 +82,24 @@ def _render_backward(ctx, g_image, g_loss=None):
     # dL/dbackground only when the background is differentiated (the trainer's is not)
     gbg = torch.empty((3,), dtype=torch.float32, device=dev) if ctx.needs_input_grad[6] else None
     gi = None if g_image is None else g_image.contiguous()
+    # the five cotangent arrays are set to zero by the compositing VJP's arithmetic-bound waves
+    # (its clear list), so the preprocessing VJP writes only the rows of the Gaussians some
+    # pixel reached (zeroed = 1)
+    gm = torch.empty_like(means)
+    gs_ = torch.empty_like(scales)
+    gq = torch.empty_like(quats)
+    go = torch.empty_like(opac)
+    gsh = torch.empty_like(sh)
+    cl = _lib.clear_list(gm, gs_, gq, go, gsh)
     head = (s, n, _lib.ptr(rec), _lib.ptr(gids), gids.shape[0], _lib.ptr(ranges), int(W), int(H), _lib.ptr(bg))
-    tail = (_lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec), _lib.ptr(gbg), accumulate, _lib.ptr(win))
+    tail = (_lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec), _lib.ptr(gbg), accumulate, _lib.ptr(win),
+            ctypes.byref(cl))
     if g_loss is not None:
         # the fused L1 loss: its VJP is formed per pixel inside the compositing VJP
         gl = g_loss.to(device=dev, dtype=torch.float32).contiguous()
         _lib.call("gs_composite_bwd_l1", *head, _lib.ptr(gi), _lib.ptr(image), _lib.ptr(target), _lib.ptr(gl), *tail)
     else:
         _lib.call("gs_composite_bwd", *head, _lib.ptr(gi), *tail)
-    gm = torch.empty_like(means)
-    gs_ = torch.empty_like(scales)
-    gq = torch.empty_like(quats)
-    go = torch.empty_like(opac)
-    gsh = torch.empty_like(sh)
     args = (s, n, sh.shape[1], int(sh_degree), _lib.ptr(means), _lib.ptr(scales), _lib.ptr(quats), _lib.ptr(opac),
             _lib.ptr(sh), _lib.ptr(w2c), int(W), int(H), float(fx), float(fy), float(cx), float(cy), _lib.ptr(grec),
             _lib.ptr(gm), _lib.ptr(gs_), _lib.ptr(gq), _lib.ptr(go), _lib.ptr(gsh))
@@ -102,9 +109,9 @@ def _render_backward(ctx, g_image, g_loss=None):
         gw = torch.empty((4, 4), dtype=torch.float32, device=dev)
         nb = _lib.lib().gs_preprocess_bwd_w2c_workspace_size(n)
         ws = torch.empty((nb,), dtype=torch.uint8, device=dev)
-        _lib.call("gs_preprocess_bwd_w2c", *args, _lib.ptr(gw), _lib.ptr(ws), nb)
+        _lib.call("gs_preprocess_bwd_w2c", *args, _lib.ptr(gw), _lib.ptr(ws), nb, 1)
     else:
-        _lib.call("gs_preprocess_bwd", *args)
+        _lib.call("gs_preprocess_bwd", *args, 1)
     return gm, gs_, gq, go, gsh, gw, gbg
 
 

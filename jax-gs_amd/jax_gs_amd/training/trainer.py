@@ -133,7 +133,8 @@ def _train_step_fused(state, target_image, camera, optimizer, sh_degree, fast_tp
                   _lib.ptr(gimg))
         _lib.call("gs_composite_bwd", s, n, _lib.ptr(pre["records"]), _lib.ptr(b["sorted_gids"]),
                   b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), int(W), int(H), _lib.ptr(bg), _lib.ptr(gimg),
-                  _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec), None, 1, _lib.ptr(b["window"]))
+                  _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec), None, 1, _lib.ptr(b["window"]),
+                  None)
         # preprocessing VJP + statistics + masked Adam, in place
         ost = state.opt_state
         moments = [ost.mu[f] for f in _FIELDS] + [ost.nu[f] for f in _FIELDS]

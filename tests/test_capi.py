@@ -32,7 +32,7 @@ def test_binding_covers_every_declared_symbol():
 
 def test_abi_version_and_workspace_query_without_gpu():
     L = _lib.lib()
-    assert L.gs_abi_version() == _lib.ABI_VERSION == 13
+    assert L.gs_abi_version() == _lib.ABI_VERSION == 14
     # size query: pure host arithmetic, grows with the number of Gaussians
     a = L.gs_bin_workspace_size(1000, 64, 64, 0)
     b = L.gs_bin_workspace_size(100000, 64, 64, 0)
@@ -69,7 +69,8 @@ def test_argument_errors_of_the_window_sh_ssim_and_camera_entry_points():
     assert b"window_size" in L.gs_last_error()
     nb = L.gs_preprocess_bwd_w2c_workspace_size(1000)
     assert nb == 16 * 16 * 4
-    rc = L.gs_preprocess_bwd_w2c(None, 1000, 16, 3, *([None] * 6), 64, 64, 1.0, 1.0, 0.0, 0.0, *([None] * 7), None, 0)
+    rc = L.gs_preprocess_bwd_w2c(None, 1000, 16, 3, *([None] * 6), 64, 64, 1.0, 1.0, 0.0, 0.0, *([None] * 7), None, 0,
+                                 0)
     assert rc == 1 and b"gs_preprocess_bwd_w2c" in L.gs_last_error()
     # the module VJPs: a camera cotangent needs its workspace; NULL arrays are rejected
     rc = L.gs_project_bwd(None, 1000, None, None, None, ctypes.c_void_p(8), 1.0, 1.0, *([None] * 6),
@@ -118,11 +119,11 @@ def test_argument_errors_of_the_fused_l1_loss():
                                         *([fake] * 2), *([None] * 5), None, fake)
     assert rc == 1 and b"l1_target" in L.gs_last_error()
     rc = L.gs_composite_bwd_l1(None, 10, fake, fake, 100, fake, 64, 64, fake, None, None, fake, fake, fake, fake,
-                               fake, fake, None, 1, None)
+                               fake, fake, None, 1, None, None)
     assert rc == 1 and b"gs_composite_bwd_l1" in L.gs_last_error()
     # the unfused backward still needs its image cotangent
     rc = L.gs_composite_bwd(None, 10, fake, fake, 100, fake, 64, 64, fake, None, fake, fake, fake, fake, None, 1,
-                            None)
+                            None, None)
     assert rc == 1 and b"image cotangent" in L.gs_last_error()
 
 

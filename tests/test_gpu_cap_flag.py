@@ -84,7 +84,7 @@ def _bwd(rec, b, H, W, bg, seed, fT, nc, order, n):
     gbg = torch.empty((3,), dtype=torch.float32, device=dev)
     _lib.call("gs_composite_bwd", _lib.stream_handle(dev), n, _lib.ptr(rec), _lib.ptr(b["sorted_gids"]),
               b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), int(W), int(H), _lib.ptr(bg), _lib.ptr(seed),
-              _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec), _lib.ptr(gbg), 0, None)
+              _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec), _lib.ptr(gbg), 0, None, None)
     torch.cuda.synchronize()
     return np_(grec), np_(gbg)
 

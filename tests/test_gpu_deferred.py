@@ -113,7 +113,7 @@ def _compare(sc, cuda, window, capacity=None, expect_deferred=True):
         _lib.call("gs_composite_bwd", _lib.stream_handle(cuda), n, _lib.ptr(pre["records"]),
                   _lib.ptr(b["sorted_gids"]), b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), W, H, _lib.ptr(bg),
                   _lib.ptr(seed), _lib.ptr(out_f[1]), _lib.ptr(out_f[2]), _lib.ptr(out_f[3]), _lib.ptr(grec),
-                  _lib.ptr(gbg), 0, _lib.ptr(b["window"]))
+                  _lib.ptr(gbg), 0, _lib.ptr(b["window"]), None)
         grads.append((np_(grec), np_(gbg)))
     e, e_bg = rel(grads[1][0], grads[0][0]), rel(grads[1][1], grads[0][1])
     log(f"backward on the deferred list vs the full one: records {e:.1e}, background {e_bg:.1e}")

@@ -215,7 +215,7 @@ def test_backward_tile_order(cuda, cfg):
             gbg = torch.empty(3, device=cuda)
             _lib.call("gs_composite_bwd", _lib.stream_handle(cuda), n, _lib.ptr(pre["records"]),
                       _lib.ptr(b["sorted_gids"]), b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), W, H, _lib.ptr(bg),
-                      _lib.ptr(gimg), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(o), _lib.ptr(grec), _lib.ptr(gbg), 0, None)
+                      _lib.ptr(gimg), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(o), _lib.ptr(grec), _lib.ptr(gbg), 0, None, None)
             out.append((_np(grec), _np(gbg)))
         # records cleared by the forward, then accumulated into (twice: the sum doubles)
         grec = torch.full((n, _lib.GS_REC_STRIDE), float("nan"), device=cuda)
@@ -224,7 +224,7 @@ def test_backward_tile_order(cuda, cfg):
         for rep in range(2):
             _lib.call("gs_composite_bwd", _lib.stream_handle(cuda), n, _lib.ptr(pre["records"]),
                       _lib.ptr(b["sorted_gids"]), b["sorted_gids"].shape[0], _lib.ptr(b["ranges"]), W, H, _lib.ptr(bg),
-                      _lib.ptr(gimg), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec), None, 1, None)
+                      _lib.ptr(gimg), _lib.ptr(fT), _lib.ptr(nc), _lib.ptr(order), _lib.ptr(grec), None, 1, None, None)
             if rep == 0:
                 acc1 = _np(grec)
         acc2 = _np(grec)
@@ -271,7 +271,7 @@ def test_records_beyond_4gib(cuda, w, h):
             grec = torch.empty((nn, _lib.GS_REC_STRIDE), device=cuda)
             _lib.call("gs_composite_bwd", _lib.stream_handle(cuda), nn, _lib.ptr(rr), _lib.ptr(gg), gg.shape[0],
                       _lib.ptr(ranges), W, H, _lib.ptr(bg), _lib.ptr(gimg), _lib.ptr(fT), _lib.ptr(nc),
-                      _lib.ptr(order), _lib.ptr(grec), None, 0, None)
+                      _lib.ptr(order), _lib.ptr(grec), None, 0, None, None)
             grads.append(_np(grec[-n:]))
             assert nn == n or not grec[:shift].any()
         del rec_big, grec
