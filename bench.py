@@ -296,13 +296,14 @@ def main():
     #                   12 each; write means2d 8, radius 4, valid 1, depth 4 (binning's inputs)
     #                   and the compositing record 48 (conic and colour: the renderer writes no
     #                   separate cov2d and colour arrays).
-    #   preprocess bwd: read the gradient record 48; write 5 gradient arrays
-    #                   (12 + 12 + 16 + 4 + 12 K); read the parameters and SH rows (44 + 12
-    #                   (D+1)^2) of the Gaussians the compositing reached (a nonzero gradient
-    #                   record): the others' gradients are zero without them.
+    #   preprocess bwd: read the gradient record 48; for the Gaussians the compositing
+    #                   reached (a nonzero gradient record) read the parameters and SH rows
+    #                   (44 + 12 (D+1)^2) and write their rows of the 5 gradient arrays
+    #                   (12 + 12 + 16 + 4 + 12 K); the other rows are zero, set by the
+    #                   compositing backward's clear list while its waves compute.
     pre_fwd_bytes = N * (44 + 12 * nb) + N * (8 + 4 + 1 + 4 + 48)
     n_reached = int((grec[:, :9] != 0).any(dim=1).sum())
-    pre_bwd_bytes = N * 48 + N * (12 + 12 + 16 + 4 + 12 * K) + n_reached * (44 + 12 * nb)
+    pre_bwd_bytes = N * 48 + n_reached * (44 + 12 * nb + 12 + 12 + 16 + 4 + 12 * K)
     #   binning: read means2d 8 + radius 4 + valid 1 + depth 4 per Gaussian; write the tile
     #            ranges (4 B per tile), and the entry list (4 B per entry) when the binning
     #            writes it (the deferred binning leaves it to the compositing forward, which
