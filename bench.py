@@ -318,9 +318,13 @@ def main():
     ncp = torch.zeros((TYn * 16, TXn * 16), dtype=torch.int32, device=dev)
     ncp[:H, :W] = nc
     entries_met = int(ncp.view(TYn, 16, TXn, 16).amax(dim=(1, 3)).to(torch.int64).sum())
-    #   densify stats: read grad_means 12 + means 12 + valid 1 + active 1 + radius 4 + the three
-    #                  statistics 12; write the three statistics 12.
-    dens_bytes = N * (12 + 12 + 1 + (1 if mask is not None else 0) + 4 + 12 + 12)
+    #   densify stats: read grad_means 12 + valid 1 + active 1 + radius 4 and update the count
+    #                  (4 + 4) per Gaussian; update the largest radius (4 + 4) of the visible ones;
+    #                  read the mean 12 and update the gradient sum (4 + 4) of those with a
+    #                  nonzero mean cotangent (a zero one adds +0).
+    n_vis = int(pre["valid"].to(torch.bool).sum())
+    n_gm = int((outs[0] != 0).any(dim=1).sum())
+    dens_bytes = (N * (12 + 1 + (1 if mask is not None else 0) + 4 + 8) + n_vis * 8 + n_gm * (12 + 8))
     stage_gbs = {"preprocess_fwd": pre_fwd_bytes / (stage_ms["preprocess_fwd"] * 1e-3) / 1e9,
                  "binning": bin_bytes / (stage_ms["binning"] * 1e-3) / 1e9,
                  "preprocess_bwd": pre_bwd_bytes / (stage_ms["preprocess_bwd"] * 1e-3) / 1e9,

@@ -1076,14 +1076,17 @@ __global__ __launch_bounds__(256) void densify_kernel(int64_t n, const float* __
                                                       float* __restrict__ max_radii) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  // trainer.py:145-147
-  const float mx = means[3 * i], my = means[3 * i + 1], mz = means[3 * i + 2];
-  const float zc = ((mx * w2c[8] + my * w2c[9]) + mz * w2c[10]) + w2c[11];
-  const float z = jmax(zc, 0.01f);
-  // trainer.py:148-152
+  // trainer.py:148-152; a zero cotangent (a Gaussian no pixel reached: most of them) adds +0,
+  // which leaves the sum as it is, so its mean and sum are not read
   const float gx = g_means[3 * i], gy = g_means[3 * i + 1], gz = g_means[3 * i + 2];
-  const float gn = sqrtf((gx * gx + gy * gy) + gz * gz);
-  grad_accum[i] = grad_accum[i] + (gn * (z / focal)) * pixel_scale;
+  if (gx != 0.0f || gy != 0.0f || gz != 0.0f) {
+    // trainer.py:145-147
+    const float mx = means[3 * i], my = means[3 * i + 1], mz = means[3 * i + 2];
+    const float zc = ((mx * w2c[8] + my * w2c[9]) + mz * w2c[10]) + w2c[11];
+    const float z = jmax(zc, 0.01f);
+    const float gn = sqrtf((gx * gx + gy * gy) + gz * gz);
+    grad_accum[i] = grad_accum[i] + (gn * (z / focal)) * pixel_scale;
+  }
   // trainer.py:153-159
   const bool v = valid[i] != 0;
   const bool act = (active == nullptr) || active[i] != 0;
