@@ -3,6 +3,9 @@ import ctypes
 import os
 import re
 
+import pytest
+import torch
+
 from jax_gs_amd import _lib
 
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "gs_raster.h")
@@ -125,6 +128,27 @@ def test_argument_errors_of_the_fused_l1_loss():
     rc = L.gs_composite_bwd(None, 10, fake, fake, 100, fake, 64, 64, fake, None, fake, fake, fake, fake, None, 1,
                             None, None)
     assert rc == 1 and b"image cotangent" in L.gs_last_error()
+
+
+def test_clear_list_and_zeroed_arguments():
+    """gs_composite_bwd rejects a clear list with a negative count or a NULL array with a
+    count, before launching anything; clear_list() builds the gs_clear_list_t layout."""
+    L = _lib.lib()
+    fake = ctypes.c_void_p(256)
+    assert ctypes.sizeof(_lib.ClearList) == _lib.GS_CLEAR_MAX * 16
+    for k, count, ptr, msg in ((3, -1, None, b"negative count"), (7, 10, None, b"is NULL")):
+        cl = _lib.ClearList()
+        cl.count[k] = count
+        cl.ptr[k] = ptr
+        rc = L.gs_composite_bwd(None, 10, fake, fake, 100, fake, 64, 64, fake, fake, fake, fake, fake, fake, None, 1,
+                                None, ctypes.byref(cl))
+        assert rc == 1 and msg in L.gs_last_error() and f"entry {k}".encode() in L.gs_last_error()
+    with pytest.raises(ValueError):
+        _lib.clear_list(*([torch.zeros(4)] * (_lib.GS_CLEAR_MAX + 1)))
+    with pytest.raises(ValueError):
+        _lib.clear_list(torch.zeros(4, dtype=torch.float64))
+    cl = _lib.clear_list(torch.zeros(7), torch.zeros(3, 5))
+    assert list(cl.count) == [7, 15] + [0] * (_lib.GS_CLEAR_MAX - 2)
 
 
 def test_load_ply_missing_file():
