@@ -977,7 +977,8 @@ __device__ __forceinline__ void composite_bwd_body(
   }
 }
 
-// The arrays of a gs_clear_list_t, passed by value.  Workgroup b of nb zeroes its contiguous
+// The arrays of a gs_clear_list_t, passed by value.  Workgroup b of nb (64 threads, t the
+// thread) zeroes its contiguous
 // share of each array's 16-byte-aligned body with non-temporal stores (the lines go to HBM while
 // the launch's waves compute, rather than staying dirty in the caches until a later kernel's
 // traffic evicts them); workgroup 0 also zeroes the up to three floats before and after it.
