@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import gc
 import json
 import math
 import os
@@ -106,11 +107,21 @@ def main():
         for _ in range(args.warmup):
             step(fused)
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            ex = step(fused)
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) / args.steps, ex
+        # Python's cyclic garbage collector paused over the timed steps (as timeit does): a
+        # collection triggered inside them stalled the host, and with it the GPU, for tens of
+        # milliseconds (seen in a fresh process on a fresh GPU box, whose first imports
+        # allocate differently)
+        gc.collect()
+        gc.disable()
+        try:
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                ex = step(fused)
+            torch.cuda.synchronize()
+            t = (time.perf_counter() - t0) / args.steps
+        finally:
+            gc.enable()
+        return t, ex
 
     # ---- per-stage timing with HIP events on the launch stream (torch's current stream)
     st = torch.cuda.current_stream(dev)
@@ -377,6 +388,10 @@ def main():
                     # share of SIMD cycles the kernel issues VALU work on (SQ counters)
                     "nonpacked_peak": FP32_NONPACKED_PEAK_TFLOPS, "valu_busy": busy, "valu_busy_source": busy_src}
 
+    # after the headline (it does not disturb the timed steps), before the calibration copies
+    # (the profile summaries take the run's last three copy dispatches for those)
+    probe = hbm_probe(dev)
+
     if args.copy_calibration:
         src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
@@ -418,9 +433,37 @@ def main():
         "extra_counts": extra_counts,
         "roofline": roofline,
         "hbm_stages": hbm_stages,
+        "hbm_probe": probe,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
+
+
+def hbm_probe(dev, mib: int = 512, reps: int = 5) -> dict:
+    """This GPU's streaming rates with torch's own kernels on mib-MiB buffers (median of reps
+    runs, HIP events): a fill (writes), a sum (reads) and a copy (reads + writes), in GB/s of the
+    bytes each moves.  The ceiling the bandwidth-bound stages are compared with besides the
+    published 8 TB/s."""
+    n = mib * 2**20 // 4
+    a = torch.ones(n, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    st = torch.cuda.current_stream(dev)
+    res = {"buffer_MiB": mib}
+    for name, fn, nbytes in (("write", lambda: b.fill_(0.5), 4 * n), ("read", lambda: a.sum(), 4 * n),
+                             ("copy", lambda: b.copy_(a), 8 * n)):
+        ts = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            fn()
+            e1.record(st)
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        res[name + "_GBps"] = nbytes / (float(np.median(ts)) * 1e-3) / 1e9
+    del a, b
+    torch.cuda.empty_cache()
+    return res
 
 
 def measured_traffic(kernel, config):
