@@ -1001,7 +1001,16 @@ __device__ inline void clear_list_share(const ClearList& cl, int b, int nb, int 
     const int64_t per = (n4 + nb - 1) / nb;
     const int64_t c0 = per * b, c1 = c0 + per < n4 ? c0 + per : n4;
     f4v* const v = reinterpret_cast<f4v*>(p + head);
-    for (int64_t c = c0 + t; c < c1; c += 64) __builtin_nontemporal_store(z, v + c);
+    // four stores per iteration at immediate offsets of one address: the loop's own vector
+    // instructions (64-bit address, compare) compete with the launch's arithmetic
+    int64_t c = c0 + t;
+    for (; c + 192 < c1; c += 256) {
+      __builtin_nontemporal_store(z, v + c);
+      __builtin_nontemporal_store(z, v + c + 64);
+      __builtin_nontemporal_store(z, v + c + 128);
+      __builtin_nontemporal_store(z, v + c + 192);
+    }
+    for (; c < c1; c += 64) __builtin_nontemporal_store(z, v + c);
     if (b == 0) {
       const int64_t tail0 = head + 4 * n4;
       if (t < head) p[t] = 0.0f;
