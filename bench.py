@@ -110,8 +110,8 @@ def main():
         # Python's cyclic garbage collector paused over the timed steps (as timeit does): a
         # collection triggered inside them stalled the host, and with it the GPU, for tens of
         # milliseconds (seen in a fresh process on a fresh GPU box, whose first imports
-        # allocate differently)
-        gc.collect()
+        # allocate differently).  No collection is forced first: steps timed right after a
+        # gc.collect() ran 0.73-0.75 ms against 0.70 (measured; the cause was not found)
         gc.disable()
         try:
             t0 = time.perf_counter()
