@@ -273,6 +273,8 @@ __global__ __launch_bounds__(64) void radix_upsweep_kernel(const uint32_t* __res
 // Rows longer than one piece (the superblock pass above 2M Gaussians: 11,719 workgroups at
 // 3M) were scanned from global memory by the threads' runs, uncoalesced: 33 us at 3M.
 constexpr int kSpineMax = 8192;
+constexpr int kSpineBatch = 8;  // global loads (stores) per thread in flight at once
+static_assert(kSpineMax % (kSpineBatch * kScanBlock) == 0, "batches tile a piece");
 __device__ inline int spine_at(int k) { return k + (k >> 5); }
 __global__ __launch_bounds__(kScanBlock) void radix_spine_kernel(uint32_t* __restrict__ table, int G,
                                                                  uint32_t* __restrict__ digit_tot) {
@@ -282,22 +284,52 @@ __global__ __launch_bounds__(kScanBlock) void radix_spine_kernel(uint32_t* __res
   uint32_t carry = 0;
   for (int c0 = 0; c0 < G; c0 += kSpineMax) {
     const int len = G - c0 < kSpineMax ? G - c0 : kSpineMax;
-    for (int k = threadIdx.x; k < len; k += kScanBlock) row_s[spine_at(k)] = row[c0 + k];
+    // The piece into LDS, kSpineBatch loads per thread issued before any of them is stored
+    // (one load waited for at a time made each thread a chain of round trips: 23 us for the
+    // 11,719-entry rows of 3M Gaussians).  k0 steps by kSpineBatch * kScanBlock, which divides
+    // kSpineMax, so every k below is inside the LDS array.
+    for (int k0 = 0; k0 < len; k0 += kSpineBatch * kScanBlock) {
+      uint32_t v[kSpineBatch];
+#pragma unroll
+      for (int u = 0; u < kSpineBatch; ++u) {
+        const int k = k0 + u * kScanBlock + threadIdx.x;
+        v[u] = k < len ? row[c0 + k] : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < kSpineBatch; ++u) {
+        const int k = k0 + u * kScanBlock + threadIdx.x;
+        if (k < len) row_s[spine_at(k)] = v[u];
+      }
+    }
     __syncthreads();
+    // each thread's run, branch-free (per * kScanBlock <= kSpineMax: slots past len are inside
+    // the array; they are read as 0 and what is written there is never stored)
     const int per = (len + kScanBlock - 1) / kScanBlock;
     const int b0 = threadIdx.x * per;
     uint32_t s = 0, tot;
-    for (int k = 0; k < per; ++k)
-      if (b0 + k < len) s += row_s[spine_at(b0 + k)];
+#pragma unroll 8
+    for (int k = 0; k < per; ++k) {
+      const uint32_t x = row_s[spine_at(b0 + k)];
+      s += b0 + k < len ? x : 0u;
+    }
     uint32_t run = carry + block_excl_scan<kScanBlock>(s, &tot);
-    for (int k = 0; k < per; ++k)
-      if (b0 + k < len) {
-        const uint32_t v = row_s[spine_at(b0 + k)];
-        row_s[spine_at(b0 + k)] = run;
-        run += v;
-      }
+#pragma unroll 8
+    for (int k = 0; k < per; ++k) {
+      const uint32_t x = row_s[spine_at(b0 + k)];
+      row_s[spine_at(b0 + k)] = run;
+      run += x;
+    }
     __syncthreads();
-    for (int k = threadIdx.x; k < len; k += kScanBlock) row[c0 + k] = row_s[spine_at(k)];
+    for (int k0 = 0; k0 < len; k0 += kSpineBatch * kScanBlock) {
+      uint32_t v[kSpineBatch];
+#pragma unroll
+      for (int u = 0; u < kSpineBatch; ++u) v[u] = row_s[spine_at(k0 + u * kScanBlock + threadIdx.x)];
+#pragma unroll
+      for (int u = 0; u < kSpineBatch; ++u) {
+        const int k = k0 + u * kScanBlock + threadIdx.x;
+        if (k < len) row[c0 + k] = v[u];
+      }
+    }
     carry += tot;
     __syncthreads();  // the piece's stores read row_s before the next piece overwrites it
   }
