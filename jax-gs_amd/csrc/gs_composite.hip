@@ -60,6 +60,10 @@ __device__ inline float bcast(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 __device__ inline int bcast_i(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+template <bool B>
+struct BoolTag {
+  static constexpr bool value = B;
+};
 
 __device__ inline float dpp_add(float x, int t) { return x + __int_as_float(t); }
 
@@ -756,7 +760,7 @@ __device__ __forceinline__ void composite_bwd_body(
 
   float py[PPT], Tr[PPT], g0[PPT], g1[PPT], g2[PPT], Rg[PPT];
   int kp[PPT];
-  int kmax = 0;
+  int kmax = 0, kmin = 1 << 30;
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
     const int yl = part * 4 * PPT + (lane >> 4) + 4 * i;
@@ -775,11 +779,17 @@ __device__ __forceinline__ void composite_bwd_body(
     // colour behind the last entry is the background
     Rg[i] = fmaf(bg2, g2[i], fmaf(bg1, g1[i], bg0 * g0[i]));
     kmax = max(kmax, kp[i]);
+    kmin = min(kmin, X < W && Y0 + 4 * i < H ? kp[i] : 0);
   }
-  // wave-wide maximum entry count (uniform loop bound)
+  // wave-wide maximum entry count (uniform loop bound); the wave-wide minimum: below it
+  // every pixel of the wave is inside the image and still open (k < kp)
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, __shfl_xor(kmax, o, 64));
+  for (int o = 32; o > 0; o >>= 1) {
+    kmax = max(kmax, __shfl_xor(kmax, o, 64));
+    kmin = min(kmin, __shfl_xor(kmin, o, 64));
+  }
   kmax = bcast_i(kmax, 0);
+  kmin = bcast_i(kmin, 0);
 
   // entries kmax-1 .. 0 in batches of 64 from the top; surviving entries walked from
   // the highest down, ids from the testing lane, records by scalar loads, prefetched
@@ -807,6 +817,10 @@ __device__ __forceinline__ void composite_bwd_body(
       gn = bcast_i(gk, jn);
       ra = load_rec_key<O32>(rec, gn);
     }
+    // KT: whether the walk tests k < kp per pixel; the no-cap body drops the test for a
+    // batch whose entries all lie below every pixel's count (most batches of a tile)
+    auto walk = [&](auto kt_tag) {
+    constexpr bool KT = decltype(kt_tag)::value;
     while (m != 0ull) {
       constexpr int E = 4;  // walked entries per reduce-scatter
       float s6[E][6], dxh[E], p0[6];
@@ -872,7 +886,7 @@ __device__ __forceinline__ void composite_bwd_body(
           // keep their values, the sums get +0): its sums need no clearing per entry.
 #pragma unroll
           for (int i = 0; i < PPT; ++i) {
-            const bool blends = k < kp[i] && qv[i] > e.thr;
+            const bool blends = (!KT || k < kp[i]) && qv[i] > e.thr;
             if (i == 0 || blends) {
               any = any || blends;
               const float al = i == 0 ? (blends ? alv[0] : 0.0f) : alv[i];
@@ -902,7 +916,7 @@ __device__ __forceinline__ void composite_bwd_body(
             V = -0.0f;
 #pragma unroll
             for (int i = 0; i < PPT; ++i) {
-              if (k < kp[i] && qv[i] > e.thr) {
+              if ((!KT || k < kp[i]) && qv[i] > e.thr) {
                 // the alpha before the cap again (a fresh exp2: not kept live across the body)
                 float qi = qv[i];
                 asm volatile("" : "+v"(qi));
@@ -974,6 +988,11 @@ __device__ __forceinline__ void composite_bwd_body(
       const int gq = b4 ? g23 : g01;
       if (vi < 9 && mine != 0.0f) atomicAdd(grec_at<O32>(grec, gq, vi), mine);
     }
+    };
+    if (NOCAP && b0 + 63 < kmin)
+      walk(BoolTag<false>{});
+    else
+      walk(BoolTag<true>{});
   }
 }
 
