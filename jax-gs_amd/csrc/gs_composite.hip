@@ -807,7 +807,10 @@ __device__ __forceinline__ void composite_bwd_body(
     p_next = probe_load(rec, ahead_gid(g_ahead, num_g));
     g_ahead = probe_gid_ahead<WIN>(gids, start, b0 - 128 + lane, kmax, win, thr);
     const int gk = rec_key<O32>(pr.g);  // the lane's record key (read where the lane survives)
-    uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
+    // KT: whether the walk tests k < kp per pixel; the no-cap body drops the test for a
+    // batch whose entries all lie below every pixel's count (most batches of a tile)
+    auto walk = [&](auto kt_tag, uint64_t m) {
+    constexpr bool KT = decltype(kt_tag)::value;
     // the next survivor's record is requested one entry ahead, into ra for the first
     // half of a pair and rb for the second (used in turn: no copy per entry)
     Rec ra = zero_rec(), rb = zero_rec();
@@ -817,10 +820,6 @@ __device__ __forceinline__ void composite_bwd_body(
       gn = bcast_i(gk, jn);
       ra = load_rec_key<O32>(rec, gn);
     }
-    // KT: whether the walk tests k < kp per pixel; the no-cap body drops the test for a
-    // batch whose entries all lie below every pixel's count (most batches of a tile)
-    auto walk = [&](auto kt_tag) {
-    constexpr bool KT = decltype(kt_tag)::value;
     while (m != 0ull) {
       constexpr int E = 4;  // walked entries per reduce-scatter
       float s6[E][6], dxh[E], p0[6];
@@ -989,10 +988,11 @@ __device__ __forceinline__ void composite_bwd_body(
       if (vi < 9 && mine != 0.0f) atomicAdd(grec_at<O32>(grec, gq, vi), mine);
     }
     };
+    const uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
     if (NOCAP && b0 + 63 < kmin)
-      walk(BoolTag<false>{});
+      walk(BoolTag<false>{}, m);
     else
-      walk(BoolTag<true>{});
+      walk(BoolTag<true>{}, m);
   }
 }
 
