@@ -808,7 +808,9 @@ __device__ __forceinline__ void composite_bwd_body(
     g_ahead = probe_gid_ahead<WIN>(gids, start, b0 - 128 + lane, kmax, win, thr);
     const int gk = rec_key<O32>(pr.g);  // the lane's record key (read where the lane survives)
     // KT: whether the walk tests k < kp per pixel; the no-cap body drops the test for a
-    // batch whose entries all lie below every pixel's count (most batches of a tile)
+    // batch whose entries all lie below every pixel's count (most batches of a tile).  The
+    // survivor mask and the prefetch state are the walk's own (captured by reference, the
+    // one-pixel build kept wave-uniform values in vector registers: cfg1 211 -> 226 us).
     auto walk = [&](auto kt_tag, uint64_t m) {
     constexpr bool KT = decltype(kt_tag)::value;
     // the next survivor's record is requested one entry ahead, into ra for the first
