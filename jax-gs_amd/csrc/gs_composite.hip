@@ -991,10 +991,17 @@ __device__ __forceinline__ void composite_bwd_body(
     }
     };
     const uint64_t m = probe_test(pr, rx0, rx1, ry0, ry1);
-    if (NOCAP && b0 + 63 < kmin)
+    if (NOCAP && b0 + 63 < kmin) {
       walk(BoolTag<false>{}, m);
-    else
+    } else if (NOCAP && b0 < kmin) {
+      // the batch straddles the minimum: its entries from kmin up with the test, then (in
+      // the same descending order) the ones below without it
+      const uint64_t below = (1ull << (kmin - b0)) - 1ull;  // kmin - b0 in 1..63
+      walk(BoolTag<true>{}, m & ~below);
+      walk(BoolTag<false>{}, m & below);
+    } else {
       walk(BoolTag<true>{}, m);
+    }
   }
 }
 
